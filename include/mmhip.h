@@ -1,0 +1,110 @@
+/*
+ * mmhip.h - C-ABI of the MI355X (gfx950) kernels behind the ggml backend.
+ *
+ * Plain pointers, sizes and byte strides; every pointer argument named
+ * data / W / x / y / out / ws is DEVICE memory; `stream` is a hipStream_t (or
+ * NULL for the null stream).  Every entry point returns MMHIP_OK (0) or a
+ * negative MMHIP_ERR_* code and never aborts; mmhip_last_error() gives the
+ * message of the last failure on the calling thread.
+ *
+ * Each entry point names the reference interface it replaces.  In the
+ * reference those operations are ggml ops executed by a ggml backend's
+ * graph_compute; the ggml backend in ggml-mi355x.h dispatches them here.
+ */
+#ifndef MMHIP_H
+#define MMHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MMHIP_OK               0
+#define MMHIP_ERR_INVALID     -1  /* bad argument or shape */
+#define MMHIP_ERR_UNSUPPORTED -2  /* valid ggml op this library does not run */
+#define MMHIP_ERR_HIP         -3  /* HIP runtime error */
+#define MMHIP_ERR_WORKSPACE   -4  /* workspace smaller than required */
+
+/* GGUF-stable type ids used below. */
+#define MMHIP_TYPE_F32  0
+#define MMHIP_TYPE_F16  1
+#define MMHIP_TYPE_Q8_0 8
+#define MMHIP_TYPE_Q4_K 12
+#define MMHIP_TYPE_Q6_K 14
+#define MMHIP_TYPE_Q8_K 15
+
+/* A device tensor view in ggml's convention: ne[0] fastest, nb[] in bytes
+ * (same meaning as ggml_tensor::ne / ::nb). */
+typedef struct {
+    const void * data;
+    int64_t      ne[4];
+    int64_t      nb[4];
+} mmhip_view;
+
+const char * mmhip_last_error(void);
+int          mmhip_version(void);
+
+/* ---------------------------------------------------------------------
+ * Weight layout.  Quantized weights live on the device in a row-grouped
+ * layout of the same byte size as GGUF rows (ggml_row_size), so tensor sizes,
+ * row strides and row views are unchanged.  Replaces the raw upload of GGUF
+ * blocks: src/gguf-weights.h:161-203 (ggml_backend_tensor_set of the mmapped
+ * bytes) reaches the ggml backend's set_tensor, which calls repack; its
+ * get_tensor calls unpack, so host reads see GGUF bytes.
+ * ------------------------------------------------------------------- */
+int mmhip_repack_rows(int type, const void * src_gguf, void * dst, int64_t nrows, int64_t ne0, void * stream);
+int mmhip_unpack_rows(int type, const void * src, void * dst_gguf, int64_t nrows, int64_t ne0, void * stream);
+
+/* Dequantise nrows rows (row-grouped layout, or F16/F32) to f32, bit-exact
+ * with the GGUF to_float definitions.  Replaces
+ * ggml_get_type_traits(t)->to_float as used at src/gguf-weights.h:230-235 and
+ * src/pipeline.cpp:114-126.  dst is [nrows][ne0] contiguous. */
+int mmhip_dequantize_rows(int type, const void * w, int64_t nrows, int64_t ne0, int64_t row_stride, float * dst,
+                          void * stream);
+
+/* ---------------------------------------------------------------------
+ * Quantized matrix products: GGML_OP_MUL_MAT with src0 in {Q8_0, Q4_K,
+ * Q6_K} (row-grouped layout), src1 f32, as emitted by qwen3_linear
+ * (src/qwen3-enc.h:67-69), the DiT projections (src/dit.h:197-199, :228,
+ * :237, :243) and the depth decoder (src/depth-decoder.h:206-230).
+ *   y[m*ldy + n] = sum_k deq(W)[n,k] * x[m*ldx + k],  n < N, m < M
+ * W has N rows of K elements, row stride w_row_stride bytes.
+ * M <= 8: activation-quantised GEMV (ggml-CPU arithmetic: Q8_0 / Q8_K
+ * activations, integer block dots).  M > 8: MFMA GEMM on f16-rounded
+ * dequantised weights and f16-rounded activations, f32 accumulation.
+ * ------------------------------------------------------------------- */
+size_t mmhip_mul_mat_workspace(int type, int64_t N, int64_t K, int64_t M);
+int    mmhip_mul_mat(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const float * x, int64_t ldx,
+                     int64_t M, float * y, int64_t ldy, void * ws, size_t ws_bytes, void * stream);
+
+/* The two halves of the GEMV path, exposed for fusion and for testing:
+ * quantise M activation rows into the layout mmhip_mul_mat_q consumes
+ * (size from mmhip_act_bytes), then run the GEMV on them (M <= 8). */
+size_t mmhip_act_bytes(int type, int64_t K, int64_t M);
+int    mmhip_quantize_act(int type, const float * x, int64_t ldx, int64_t K, int64_t M, void * xq, void * stream);
+int    mmhip_mul_mat_q(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const void * xq, int64_t M,
+                       float * y, int64_t ldy, void * stream);
+
+/* ---------------------------------------------------------------------
+ * GGML_OP_FLASH_ATTN_EXT, replacing the ggml backend kernel behind
+ *   src/qwen3-lm.h:816-821 (batched CFG decode over the f16 4-D KV cache),
+ *   src/qwen3-lm.h:432-436 (causal prefill),
+ *   src/dit.h:221-222      (DiT bidirectional, mask NULL).
+ * q    f32 [D, n_q, Hq, B]      any strides (permuted views allowed)
+ * k, v f16 [D, n_kv, Hkv, Bk]   any row/head/batch strides, rows contiguous
+ * mask f16 [>=n_kv, >=n_q, M2, M3] or NULL (broadcast over heads / batch)
+ * out  f32 [D, Hq, n_q, B] contiguous
+ * Requires D in {64, 128, 256}, Hq % Hkv == 0, B % Bk == 0.  scale is
+ * op_params[0]; max_bias and softcap must be 0 (as in every call of the
+ * reference).  Accumulation is f32 (GGML_PREC_F32).
+ * ------------------------------------------------------------------- */
+size_t mmhip_flash_attn_workspace(const mmhip_view * q, const mmhip_view * k, const mmhip_view * v);
+int    mmhip_flash_attn_ext(const mmhip_view * q, const mmhip_view * k, const mmhip_view * v, const mmhip_view * mask,
+                            float scale, float * out, void * ws, size_t ws_bytes, void * stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,190 @@
+// mmhip_api.hip - C-ABI entry points: argument validation, error reporting,
+// workspace sizing and kernel selection for MUL_MAT and FLASH_ATTN_EXT.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "k_fa_common.h"
+#include "mmhip_device.h"
+#include "mmhip_internal.h"
+
+namespace mmhip {
+
+static thread_local char g_err[512];
+
+void clear_error() {
+    g_err[0] = 0;
+}
+
+int set_error(int code, const char * fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int check_launch(const char * what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        return set_error(MMHIP_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    }
+    return MMHIP_OK;
+}
+
+// MUL_MAT dispatch: GEMV for small M, MFMA GEMM beyond.
+constexpr int64_t GEMV_MAX_M = 8;
+
+static bool use_gemm(int type, int64_t M) {
+    (void) type;
+    return M > GEMV_MAX_M;
+}
+
+}  // namespace mmhip
+
+using namespace mmhip;
+
+extern "C" const char * mmhip_last_error(void) {
+    return g_err;
+}
+
+extern "C" int mmhip_version(void) {
+    return 1;
+}
+
+extern "C" size_t mmhip_mul_mat_workspace(int type, int64_t N, int64_t K, int64_t M) {
+    (void) N;
+    if (use_gemm(type, M)) {
+        return 0;
+    }
+    return act_layout(type, K, M).total;
+}
+
+extern "C" int mmhip_mul_mat(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const float * x,
+                             int64_t ldx, int64_t M, float * y, int64_t ldy, void * ws, size_t ws_bytes,
+                             void * stream) {
+    MMHIP_API_BEGIN();
+    if (!W || !x || !y || N <= 0 || K <= 0 || M <= 0 || ldx < K || ldy < N) {
+        return set_error(MMHIP_ERR_INVALID, "mul_mat: bad arguments N=%lld K=%lld M=%lld", (long long) N,
+                         (long long) K, (long long) M);
+    }
+    if (!is_repacked_type(type)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat: weight type %d", type);
+    }
+    hipStream_t st = (hipStream_t) stream;
+    if (use_gemm(type, M)) {
+        return gemm_q(type, W, N, K, w_row_stride, x, ldx, M, y, ldy, st);
+    }
+    const ActLayout L = act_layout(type, K, M);
+    if (L.total == 0 || !gemv_supported(type, N, K, w_row_stride, W)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat: type %d N=%lld K=%lld rs=%lld", type, (long long) N,
+                         (long long) K, (long long) w_row_stride);
+    }
+    if (!ws || ws_bytes < L.total) {
+        return set_error(MMHIP_ERR_WORKSPACE, "mul_mat: workspace %zu < %zu", ws_bytes, L.total);
+    }
+    int rc = quantize_act(type, x, ldx, K, M, ws, st);
+    if (rc != MMHIP_OK) {
+        return rc;
+    }
+    return gemv_q(type, W, N, K, w_row_stride, ActPtrs::from(L, ws), M, y, ldy, st);
+}
+
+// ---------------------------------------------------------------------
+// FLASH_ATTN_EXT
+
+static int fa_validate(const mmhip_view * q, const mmhip_view * k, const mmhip_view * v, const mmhip_view * mask,
+                       FaArgs & a, int & D) {
+    if (!q || !k || !v || !q->data || !k->data || !v->data) {
+        return set_error(MMHIP_ERR_INVALID, "flash_attn: null operand");
+    }
+    D = (int) q->ne[0];
+    if (!(D == 64 || D == 128 || D == 256) || k->ne[0] != D || v->ne[0] != D) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "flash_attn: head dims q=%lld k=%lld v=%lld", (long long) q->ne[0],
+                         (long long) k->ne[0], (long long) v->ne[0]);
+    }
+    if (q->nb[0] != 4 || k->nb[0] != 2 || v->nb[0] != 2) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "flash_attn: dim 0 must be contiguous (q f32, k/v f16)");
+    }
+    if (k->ne[1] != v->ne[1] || k->ne[2] != v->ne[2] || k->ne[3] != v->ne[3]) {
+        return set_error(MMHIP_ERR_INVALID, "flash_attn: k/v shape mismatch");
+    }
+    if (k->ne[1] <= 0 || q->ne[1] <= 0 || k->ne[2] <= 0 || q->ne[2] % k->ne[2] != 0 || q->ne[3] % k->ne[3] != 0) {
+        return set_error(MMHIP_ERR_INVALID, "flash_attn: head/batch broadcast mismatch");
+    }
+    const int64_t lim = (int64_t) 1 << 30;
+    if (q->ne[1] > lim || k->ne[1] > lim || q->ne[2] > 65535 || q->ne[3] > 65535) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "flash_attn: sizes out of range");
+    }
+    // 16-byte K/V row loads
+    const uintptr_t kv_align = (uintptr_t) k->data | (uintptr_t) v->data | (uintptr_t) k->nb[1] |
+                               (uintptr_t) k->nb[2] | (uintptr_t) k->nb[3] | (uintptr_t) v->nb[1] |
+                               (uintptr_t) v->nb[2] | (uintptr_t) v->nb[3];
+    if (kv_align % 16 != 0 || ((uintptr_t) q->data | (uintptr_t) q->nb[1] | (uintptr_t) q->nb[2] |
+                               (uintptr_t) q->nb[3]) % 4 != 0) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "flash_attn: misaligned operands");
+    }
+    memset(&a, 0, sizeof(a));
+    a.q    = (const char *) q->data;
+    a.qnb1 = q->nb[1];
+    a.qnb2 = q->nb[2];
+    a.qnb3 = q->nb[3];
+    a.k    = (const char *) k->data;
+    a.knb1 = k->nb[1];
+    a.knb2 = k->nb[2];
+    a.knb3 = k->nb[3];
+    a.v    = (const char *) v->data;
+    a.vnb1 = v->nb[1];
+    a.vnb2 = v->nb[2];
+    a.vnb3 = v->nb[3];
+    a.nq   = (int) q->ne[1];
+    a.Hq   = (int) q->ne[2];
+    a.B    = (int) q->ne[3];
+    a.nkv  = (int) k->ne[1];
+    a.Hkv  = (int) k->ne[2];
+    a.Bk   = (int) k->ne[3];
+    if (mask && mask->data) {
+        if (mask->nb[0] != 2 || mask->ne[0] < k->ne[1] || mask->ne[1] < q->ne[1] || mask->ne[2] <= 0 ||
+            mask->ne[3] <= 0 || q->ne[2] % mask->ne[2] != 0 || q->ne[3] % mask->ne[3] != 0) {
+            return set_error(MMHIP_ERR_INVALID, "flash_attn: mask shape [%lld,%lld,%lld,%lld] does not cover q/k",
+                             (long long) mask->ne[0], (long long) mask->ne[1], (long long) mask->ne[2],
+                             (long long) mask->ne[3]);
+        }
+        a.mask = (const char *) mask->data;
+        a.mnb1 = mask->nb[1];
+        a.mnb2 = mask->nb[2];
+        a.mnb3 = mask->nb[3];
+        a.mne2 = (int) mask->ne[2];
+        a.mne3 = (int) mask->ne[3];
+    } else {
+        a.mne2 = 1;
+        a.mne3 = 1;
+    }
+    return MMHIP_OK;
+}
+
+extern "C" size_t mmhip_flash_attn_workspace(const mmhip_view * q, const mmhip_view * k, const mmhip_view * v) {
+    FaArgs a;
+    int    D;
+    if (fa_validate(q, k, v, nullptr, a, D) != MMHIP_OK) {
+        return 0;
+    }
+    return fa_decode_workspace(a, D);
+}
+
+extern "C" int mmhip_flash_attn_ext(const mmhip_view * q, const mmhip_view * k, const mmhip_view * v,
+                                    const mmhip_view * mask, float scale, float * out, void * ws, size_t ws_bytes,
+                                    void * stream) {
+    MMHIP_API_BEGIN();
+    FaArgs a;
+    int    D;
+    int    rc = fa_validate(q, k, v, mask, a, D);
+    if (rc != MMHIP_OK) {
+        return rc;
+    }
+    if (!out) {
+        return set_error(MMHIP_ERR_INVALID, "flash_attn: null output");
+    }
+    a.scale = scale;
+    return fa_decode(a, D, out, ws, ws_bytes, (hipStream_t) stream);
+}

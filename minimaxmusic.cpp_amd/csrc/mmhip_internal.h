@@ -1,0 +1,83 @@
+// mmhip_internal.h - host-side helpers shared by the C-ABI translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include <algorithm>
+
+#include "mmhip.h"
+
+namespace mmhip {
+
+int  set_error(int code, const char * fmt, ...) __attribute__((format(printf, 2, 3)));
+int  check_launch(const char * what);
+void clear_error();
+
+inline bool is_repacked_type(int type) {
+    return type == 8 /*Q8_0*/ || type == 12 /*Q4_K*/ || type == 14 /*Q6_K*/;
+}
+
+// Quantised-activation buffer layout for M rows of K elements:
+//   qs [M][K] int8 | d [M][K/blk] f32 | bsums [M][K/16] int16 (Q8_K only)
+// with every field 256-byte aligned.
+struct ActLayout {
+    int    vec_type;  // 8 = Q8_0, 15 = Q8_K, 0 = unsupported
+    int    blk;
+    size_t qs_off, d_off, bs_off, total;
+};
+
+inline size_t align_up(size_t v, size_t a) {
+    return (v + a - 1) / a * a;
+}
+
+inline ActLayout act_layout(int wtype, int64_t K, int64_t M) {
+    ActLayout L{};
+    if (wtype == 8 && K % 32 == 0) {
+        L.vec_type = 8;
+        L.blk      = 32;
+    } else if ((wtype == 12 || wtype == 14) && K % 256 == 0) {
+        L.vec_type = 15;
+        L.blk      = 256;
+    } else {
+        return L;
+    }
+    L.qs_off = 0;
+    L.d_off  = align_up((size_t) (M * K), 256);
+    L.bs_off = align_up(L.d_off + sizeof(float) * (size_t) (M * (K / L.blk)), 256);
+    L.total  = L.vec_type == 15 ? align_up(L.bs_off + 2 * (size_t) (M * (K / 16)), 256) : L.bs_off;
+    return L;
+}
+
+int quantize_act(int wtype, const float * x, int64_t ldx, int64_t K, int64_t M, void * xq, hipStream_t stream);
+
+// Field pointers of a quantised-activation buffer.
+struct ActPtrs {
+    const int8_t *  qs;
+    const float *   d;
+    const int16_t * bs;
+    int             blk;
+
+    static ActPtrs from(const ActLayout & L, const void * base) {
+        const char * b = (const char *) base;
+        return { (const int8_t *) (b + L.qs_off), (const float *) (b + L.d_off),
+                 L.vec_type == 15 ? (const int16_t *) (b + L.bs_off) : nullptr, L.blk };
+    }
+    ActPtrs slice(int64_t c0, int64_t K) const {
+        return { qs + c0 * K, d + c0 * (K / blk), bs ? bs + c0 * (K / 16) : nullptr, blk };
+    }
+};
+
+// Quantized GEMV on pre-quantised activations (any M; column groups of <= 8).
+bool gemv_supported(int wtype, int64_t N, int64_t K, int64_t row_stride, const void * W);
+int  gemv_q(int wtype, const void * W, int64_t N, int64_t K, int64_t row_stride, const ActPtrs & x, int64_t M, float * y,
+            int64_t ldy, hipStream_t stream);
+
+// MFMA GEMM with in-LDS dequantisation (any M).
+int gemm_q(int wtype, const void * W, int64_t N, int64_t K, int64_t row_stride, const float * x, int64_t ldx, int64_t M,
+           float * y, int64_t ldy, hipStream_t stream);
+
+}  // namespace mmhip
+
+#define MMHIP_API_BEGIN() ::mmhip::clear_error()

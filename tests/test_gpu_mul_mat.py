@@ -1,0 +1,59 @@
+"""GPU: GGML_OP_MUL_MAT over Q8_0 / Q4_K / Q6_K weights against the oracle.
+
+Tolerances (stated): against the ggml-CPU-semantics oracle, which quantises
+activations the same way and differs only in f32 summation order,
+max|y - y_ggml| <= 2e-5 * max|y_ggml|; against the exact fp64 oracle,
+cosine >= 0.9999 (ggml-CPU's own activation-quantisation error)."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import cosine, rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def run(mm, orc, pkg, t, N, K, M, seed):
+    raw = pkg.synth.gguf_blocks_np(t, N, K, seed)
+    x = pkg.synth.normal_np((M, K), seed + 1)
+    W = mm.QuantWeight.from_gguf(t, raw, N, K)
+    y = mm.mul_mat(W, torch.from_numpy(x).cuda()).cpu().numpy()
+    return y, orc.mul_mat_ggml(t, raw, N, K, x), orc.mul_mat_f64(t, raw, N, K, x)
+
+
+@pytest.mark.parametrize("t", [8, 12, 14])
+@pytest.mark.parametrize("M", [1, 2, 3, 5, 8])
+def test_gemv_small(mm, orc, pkg, t, M):
+    y, yg, yf = run(mm, orc, pkg, t, 1000, 2048, M, 2000 + 10 * t + M)
+    assert rel_err(y, yg) < 2e-5
+    assert cosine(y, yf) > 0.9999
+
+
+@pytest.mark.parametrize("t", [8, 12, 14])
+@pytest.mark.parametrize("N,K", [(6144, 4096), (4096, 12288), (2048, 2304), (3, 256)])
+def test_gemv_decode_shapes(mm, orc, pkg, t, N, K):
+    y, yg, yf = run(mm, orc, pkg, t, N, K, 2, 3000 + t + N)
+    assert rel_err(y, yg) < 2e-5
+    assert cosine(y, yf) > 0.9999
+
+
+def test_gemv_q8_0_benchmark_shape(mm, orc, pkg):
+    """The Q8_0 decode GEMV workload at full size: W 12288 x 4096, x [2 x 4096]."""
+    y, yg, yf = run(mm, orc, pkg, 8, 12288, 4096, 2, 1002)
+    assert rel_err(y, yg) < 2e-5
+    assert cosine(y, yf) > 0.99999
+    # swapping the two CFG rows swaps the outputs exactly
+    raw = pkg.synth.gguf_blocks_np(8, 12288, 4096, 1002)
+    x = pkg.synth.normal_np((2, 4096), 1003)
+    W = mm.QuantWeight.from_gguf(8, raw, 12288, 4096)
+    a = mm.mul_mat(W, torch.from_numpy(x).cuda())
+    b = mm.mul_mat(W, torch.from_numpy(x[::-1].copy()).cuda())
+    assert torch.equal(a, b.flip(0))
+
+
+def test_gemv_rejects_bad_shapes(mm, pkg):
+    raw = pkg.synth.gguf_blocks_np(8, 4, 96, 1)
+    W = mm.QuantWeight.from_gguf(8, raw, 4, 96)
+    with pytest.raises(mm.MmhipError) as e:
+        mm.mul_mat(W, torch.zeros((2, 96), device="cuda"))
+    assert e.value.code == mm.ERR_UNSUPPORTED
