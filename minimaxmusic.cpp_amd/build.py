@@ -36,7 +36,7 @@ HIP_FLAGS = [
 ]
 
 LIBS = {
-    "libmmhip.so": ["k_quant.hip", "k_gemv.hip", "k_gemm.hip", "k_fa_decode.hip", "mmhip_api.hip"],
+    "libmmhip.so": ["k_quant.hip", "k_gemv.hip", "k_gemm.hip", "k_fa_decode.hip", "k_fa_mfma.hip", "mmhip_api.hip"],
 }
 
 

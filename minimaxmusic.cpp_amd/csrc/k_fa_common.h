@@ -25,4 +25,15 @@ struct FaArgs {
 size_t fa_decode_workspace(const FaArgs & a, int D);
 int    fa_decode(const FaArgs & a, int D, float * out, void * ws, size_t ws_bytes, hipStream_t stream);
 
+size_t fa_mfma_workspace(const FaArgs & a);
+bool   fa_mfma_supported(const FaArgs & a, int D);
+int    fa_mfma(const FaArgs & a, int D, float * out, void * ws, size_t ws_bytes, hipStream_t stream);
+
+// Kernel choice: the split-KV decode kernel while the query rows of one KV head
+// fit one workgroup (the LM decode, the depth decoder's few rows), the MFMA
+// kernel beyond (prefill, DiT).
+inline bool fa_use_mfma(const FaArgs & a, int D) {
+    return fa_mfma_supported(a, D) && (a.Hq / a.Hkv) * a.nq > 8;
+}
+
 }  // namespace mmhip

@@ -18,7 +18,7 @@
 
 namespace mmhip {
 
-template <int D, int QR>
+template <int D, int QR, int U>
 __global__ __launch_bounds__(256) void k_fa_decode(FaArgs a, int chunk, int nsplit, float * __restrict__ part_o,
                                                    float * __restrict__ part_ml, float * __restrict__ out) {
     constexpr int LPK = D / 8;
@@ -74,34 +74,45 @@ __global__ __launch_bounds__(256) void k_fa_decode(FaArgs a, int chunk, int nspl
     }
     const float log2e = 1.4426950408889634f;
 
-    for (int base = kbeg + wave * KPW; base < kend; base += 4 * KPW) {
-        const int     j  = base + ks;
-        const bool    jv = j < kend;
-        const int64_t jc = jv ? j : kend - 1;
-        const half8_t kk = *(const half8_t *) (kbase + jc * a.knb1);
-        const half8_t vv = *(const half8_t *) (vbase + jc * a.vnb1);
+    // U keys per lane in flight: all K/V loads of an iteration are issued
+    // before the first use.
+    for (int base = kbeg + wave * KPW; base < kend; base += 4 * KPW * U) {
+        half8_t kk[U], vv[U];
+        int64_t jc[U];
+        bool    jv[U];
 #pragma unroll
-        for (int r = 0; r < QR; r++) {
-            float dot = 0.0f;
-            dot       = __builtin_amdgcn_fdot2(half2_t{ kk[0], kk[1] }, half2_t{ qv[r][0], qv[r][1] }, dot, false);
-            dot       = __builtin_amdgcn_fdot2(half2_t{ kk[2], kk[3] }, half2_t{ qv[r][2], qv[r][3] }, dot, false);
-            dot       = __builtin_amdgcn_fdot2(half2_t{ kk[4], kk[5] }, half2_t{ qv[r][4], qv[r][5] }, dot, false);
-            dot       = __builtin_amdgcn_fdot2(half2_t{ kk[6], kk[7] }, half2_t{ qv[r][6], qv[r][7] }, dot, false);
-            dot       = group_sum<LPK>(dot);
-            const float mv = mrow[r] ? h2f(*(const uint16_t *) (mrow[r] + jc * 2)) : 0.0f;
-            const float s  = (jv && rvalid[r]) ? (dot * a.scale + mv) * log2e : -INFINITY;
-            const float mn = fmaxf(m[r], s);
-            float       alpha = 1.0f, p = 0.0f;
-            if (mn != -INFINITY) {
-                alpha = __builtin_amdgcn_exp2f(m[r] - mn);
-                p     = __builtin_amdgcn_exp2f(s - mn);
-            }
-            l[r] = l[r] * alpha + p;
+        for (int u = 0; u < U; u++) {
+            const int j = base + 4 * KPW * u + ks;
+            jv[u]       = j < kend;
+            jc[u]       = jv[u] ? j : kend - 1;
+            kk[u]       = *(const half8_t *) (kbase + jc[u] * a.knb1);
+            vv[u]       = *(const half8_t *) (vbase + jc[u] * a.vnb1);
+        }
 #pragma unroll
-            for (int d = 0; d < 8; d++) {
-                o[r][d] = o[r][d] * alpha + p * (float) vv[d];
+        for (int u = 0; u < U; u++) {
+#pragma unroll
+            for (int r = 0; r < QR; r++) {
+                float dot = 0.0f;
+                dot = __builtin_amdgcn_fdot2(half2_t{ kk[u][0], kk[u][1] }, half2_t{ qv[r][0], qv[r][1] }, dot, false);
+                dot = __builtin_amdgcn_fdot2(half2_t{ kk[u][2], kk[u][3] }, half2_t{ qv[r][2], qv[r][3] }, dot, false);
+                dot = __builtin_amdgcn_fdot2(half2_t{ kk[u][4], kk[u][5] }, half2_t{ qv[r][4], qv[r][5] }, dot, false);
+                dot = __builtin_amdgcn_fdot2(half2_t{ kk[u][6], kk[u][7] }, half2_t{ qv[r][6], qv[r][7] }, dot, false);
+                dot = group_sum<LPK>(dot);
+                const float mv = mrow[r] ? h2f(*(const uint16_t *) (mrow[r] + jc[u] * 2)) : 0.0f;
+                const float s  = (jv[u] && rvalid[r]) ? (dot * a.scale + mv) * log2e : -INFINITY;
+                const float mn = fmaxf(m[r], s);
+                float       alpha = 1.0f, p = 0.0f;
+                if (mn != -INFINITY) {
+                    alpha = __builtin_amdgcn_exp2f(m[r] - mn);
+                    p     = __builtin_amdgcn_exp2f(s - mn);
+                }
+                l[r] = l[r] * alpha + p;
+#pragma unroll
+                for (int d = 0; d < 8; d++) {
+                    o[r][d] = o[r][d] * alpha + p * (float) vv[u][d];
+                }
+                m[r] = mn;
             }
-            m[r] = mn;
         }
     }
 
@@ -175,43 +186,88 @@ __global__ __launch_bounds__(256) void k_fa_decode(FaArgs a, int chunk, int nspl
     }
 }
 
-// One workgroup of D threads per output row (b, hq, iq).
-__global__ void k_fa_combine(const float * __restrict__ part_o, const float * __restrict__ part_ml, int nsplit, int D,
-                             int nq, int Hq, float * __restrict__ out) {
-    const int hq = blockIdx.x / nq;
-    const int iq = blockIdx.x % nq;
-    const int b  = blockIdx.y;
-    const int d  = threadIdx.x;
+// One workgroup of D threads per output row (b, hq, iq): the split weights
+// exp2(m_s - M) / L are formed once in LDS, then every thread sums its dim.
+__global__ __launch_bounds__(256) void k_fa_combine(const float * __restrict__ part_o,
+                                                    const float * __restrict__ part_ml, int nsplit, int D, int nq,
+                                                    int Hq, float * __restrict__ out) {
+    __shared__ float s_w[256];
+    __shared__ float s_red[2];
+    const int     hq  = blockIdx.x / nq;
+    const int     iq  = blockIdx.x % nq;
+    const int     b   = blockIdx.y;
+    const int     t   = threadIdx.x;
     const int64_t pr0 = (((int64_t) b * Hq + hq) * nq + iq) * nsplit;
-    float         M   = -INFINITY;
-    for (int s = 0; s < nsplit; s++) {
-        M = fmaxf(M, part_ml[(pr0 + s) * 2]);
+    // blockDim.x == D >= 64 and nsplit <= D: thread t < nsplit owns split t
+    float ms = -INFINITY, ls = 0.0f;
+    if (t < nsplit) {
+        ms = part_ml[(pr0 + t) * 2];
+        ls = part_ml[(pr0 + t) * 2 + 1];
     }
-    float L = 0.0f, O = 0.0f;
-    if (M != -INFINITY) {
-        for (int s = 0; s < nsplit; s++) {
-            const float ms = part_ml[(pr0 + s) * 2];
-            const float sc = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
-            L += part_ml[(pr0 + s) * 2 + 1] * sc;
-            O += part_o[(pr0 + s) * D + d] * sc;
+    float M = wave_max(ms);
+    if (blockDim.x > 64) {
+        if ((t & 63) == 0) {
+            s_w[t >> 6] = M;
         }
+        __syncthreads();
+        for (int w = 0; w < (int) blockDim.x / 64; w++) {
+            M = fmaxf(M, s_w[w]);
+        }
+        __syncthreads();
     }
-    out[(((int64_t) b * nq + iq) * Hq + hq) * D + d] = L > 0.0f ? O / L : 0.0f;
+    const float sc = (ms == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
+    float       L  = wave_sum(ls * sc);
+    if (blockDim.x > 64) {
+        if ((t & 63) == 0) {
+            s_w[t >> 6] = L;
+        }
+        __syncthreads();
+        L = 0.0f;
+        for (int w = 0; w < (int) blockDim.x / 64; w++) {
+            L += s_w[w];
+        }
+        __syncthreads();
+    }
+    if (t == 0) {
+        s_red[0] = L;
+    }
+    if (t < nsplit) {
+        s_w[t] = sc;
+    }
+    __syncthreads();
+    const float inv = s_red[0] > 0.0f ? 1.0f / s_red[0] : 0.0f;
+    float       O   = 0.0f;
+    int         s   = 0;
+    for (; s + 4 <= nsplit; s += 4) {
+        const float o0 = part_o[(pr0 + s) * D + t], o1 = part_o[(pr0 + s + 1) * D + t];
+        const float o2 = part_o[(pr0 + s + 2) * D + t], o3 = part_o[(pr0 + s + 3) * D + t];
+        O += o0 * s_w[s] + o1 * s_w[s + 1] + o2 * s_w[s + 2] + o3 * s_w[s + 3];
+    }
+    for (; s < nsplit; s++) {
+        O += part_o[(pr0 + s) * D + t] * s_w[s];
+    }
+    out[(((int64_t) b * nq + iq) * Hq + hq) * D + t] = O * inv;
 }
 
 // ---------------------------------------------------------------------
 
-constexpr int DEC_QR = 8;
+constexpr int DEC_U = 4;
+
+static int dec_qr(const FaArgs & a) {
+    return (a.Hq / a.Hkv) * a.nq <= 4 ? 4 : 8;
+}
 
 static void decode_plan(const FaArgs & a, int D, int & nsplit, int & chunk, int & rowgroups) {
-    const int G   = a.Hq / a.Hkv;
-    rowgroups     = (G * a.nq + DEC_QR - 1) / DEC_QR;
-    const int kpw = 64 / (D / 8);
-    const int step = 4 * kpw;
+    const int G    = a.Hq / a.Hkv;
+    const int QR   = dec_qr(a);
+    rowgroups      = (G * a.nq + QR - 1) / QR;
+    const int kpw  = 64 / (D / 8);
+    const int step = 4 * kpw * DEC_U;  // keys one workgroup iteration covers
     const int base_wgs = a.Hkv * a.B * rowgroups;
-    const int target   = 1024;
+    const int target   = 512;
     int       ns       = (target + base_wgs - 1) / base_wgs;
-    const int max_ns   = std::max(1, (a.nkv + step - 1) / step);
+    // the combine kernel gives one thread per split: nsplit <= D
+    const int max_ns   = std::max(1, std::min(D, (a.nkv + step - 1) / step));
     ns                 = std::max(1, std::min(ns, max_ns));
     chunk              = ((a.nkv + ns - 1) / ns + step - 1) / step * step;
     nsplit             = (a.nkv + chunk - 1) / chunk;
@@ -225,6 +281,16 @@ size_t fa_decode_workspace(const FaArgs & a, int D) {
     }
     const size_t rows = (size_t) a.B * a.Hq * a.nq * nsplit;
     return align_up(rows * D * sizeof(float), 256) + align_up(rows * 2 * sizeof(float), 256);
+}
+
+template <int D>
+static void launch_decode(const FaArgs & a, int QR, dim3 grid, int chunk, int nsplit, float * po, float * pml,
+                          float * out, hipStream_t stream) {
+    if (QR == 4) {
+        hipLaunchKernelGGL((k_fa_decode<D, 4, DEC_U>), grid, dim3(256), 0, stream, a, chunk, nsplit, po, pml, out);
+    } else {
+        hipLaunchKernelGGL((k_fa_decode<D, 8, DEC_U>), grid, dim3(256), 0, stream, a, chunk, nsplit, po, pml, out);
+    }
 }
 
 int fa_decode(const FaArgs & a, int D, float * out, void * ws, size_t ws_bytes, hipStream_t stream) {
@@ -241,22 +307,16 @@ int fa_decode(const FaArgs & a, int D, float * out, void * ws, size_t ws_bytes, 
         part_o            = (float *) ws;
         part_ml           = (float *) ((char *) ws + align_up(rows * D * sizeof(float), 256));
     }
+    if ((int64_t) a.B * rg > 65535) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "flash_attn decode: B * row groups too large");
+    }
     const dim3 grid(nsplit, a.Hkv, a.B * rg);
+    const int  QR = dec_qr(a);
     switch (D) {
-        case 64:
-            hipLaunchKernelGGL((k_fa_decode<64, DEC_QR>), grid, dim3(256), 0, stream, a, chunk, nsplit, part_o, part_ml,
-                               out);
-            break;
-        case 128:
-            hipLaunchKernelGGL((k_fa_decode<128, DEC_QR>), grid, dim3(256), 0, stream, a, chunk, nsplit, part_o,
-                               part_ml, out);
-            break;
-        case 256:
-            hipLaunchKernelGGL((k_fa_decode<256, DEC_QR>), grid, dim3(256), 0, stream, a, chunk, nsplit, part_o,
-                               part_ml, out);
-            break;
-        default:
-            return set_error(MMHIP_ERR_UNSUPPORTED, "flash_attn decode: head dim %d", D);
+        case 64: launch_decode<64>(a, QR, grid, chunk, nsplit, part_o, part_ml, out, stream); break;
+        case 128: launch_decode<128>(a, QR, grid, chunk, nsplit, part_o, part_ml, out, stream); break;
+        case 256: launch_decode<256>(a, QR, grid, chunk, nsplit, part_o, part_ml, out, stream); break;
+        default: return set_error(MMHIP_ERR_UNSUPPORTED, "flash_attn decode: head dim %d", D);
     }
     int rc = check_launch("flash_attn decode");
     if (rc != MMHIP_OK || nsplit == 1) {

@@ -90,309 +90,321 @@ __device__ __forceinline__ void store_rows(float (&acc)[R][NC], int lane, int64_
     }
 }
 
-template <int NC>
-__device__ __forceinline__ void stage_act(uint8_t * lds, const uint8_t * xq, size_t qs_bytes, const float * xd,
-                                          int nd, const int16_t * xbs, int nbs) {
-    const int tid = threadIdx.x;
-    for (size_t i = (size_t) tid * 16; i < qs_bytes; i += 256 * 16) {
-        *(int4_t *) (lds + i) = ld16(xq + i);
+// 16-byte load from a 16-byte aligned address, or (AL = false) from a 2-byte
+// aligned one as eight 16-bit loads.
+template <bool AL> __device__ __forceinline__ int4_t ld16a(const uint8_t * p) {
+    if constexpr (AL) {
+        return *(const int4_t *) p;
+    } else {
+        const uint16_t * s = (const uint16_t *) p;
+        return int4_t{ (int) (s[0] | ((uint32_t) s[1] << 16)), (int) (s[2] | ((uint32_t) s[3] << 16)),
+                       (int) (s[4] | ((uint32_t) s[5] << 16)), (int) (s[6] | ((uint32_t) s[7] << 16)) };
     }
-    float * ld = (float *) (lds + qs_bytes);
-    for (int i = tid; i < nd; i += 256) {
-        ld[i] = xd[i];
-    }
-    if (xbs) {
-        int16_t * lb = (int16_t *) (lds + qs_bytes + 4 * (size_t) nd);
-        for (int i = tid; i < nbs; i += 256) {
-            lb[i] = xbs[i];
-        }
-    }
-    __syncthreads();
 }
 
-template <int NC, int R>
+template <bool AL> __device__ __forceinline__ uint2 ld8a(const uint8_t * p) {
+    if constexpr (AL) {
+        return *(const uint2 *) p;
+    } else {
+        const uint16_t * s = (const uint16_t *) p;
+        return uint2{ s[0] | ((uint32_t) s[1] << 16), s[2] | ((uint32_t) s[3] << 16) };
+    }
+}
+
+// Q8_0.  Wave-chunk = 1024 bytes of qs (32 blocks); lane l owns bytes
+// [16l, 16l+16) = half of block l/2.  U chunks are loaded before any use.
+template <int NC, int R, int U>
 __global__ __launch_bounds__(256) void k_gemv_q8_0(const uint8_t * __restrict__ W, int64_t N, int64_t K, int64_t rs,
-                                                    const uint8_t * __restrict__ xq, const float * __restrict__ xd,
+                                                    const int8_t * __restrict__ xq, const float * __restrict__ xd,
                                                     float * __restrict__ y, int64_t ldy) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    const int64_t qs_bytes = (int64_t) NC * K;
-    const int     nblk     = (int) (K / 32);
-    stage_act<NC>(lds, xq, qs_bytes, xd, NC * nblk, nullptr, 0);
-    const int8_t * lq = (const int8_t *) lds;
-    const float *  ld = (const float *) (lds + qs_bytes);
-
-    const int     wave    = threadIdx.x >> 6;
-    const int     lane    = threadIdx.x & 63;
-    const int64_t ngroups = (N + R - 1) / R;
-    for (int64_t g = (int64_t) blockIdx.x * 4 + wave; g < ngroups; g += (int64_t) gridDim.x * 4) {
-        const uint8_t * wr[R];
+    const int     lane = threadIdx.x & 63;
+    const int64_t g    = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (g * R >= N) {
+        return;
+    }
+    const int       nblk = (int) (K / 32);
+    const uint8_t * wr[R];
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            const int64_t row = g * R + r < N ? g * R + r : N - 1;
-            wr[r]             = W + row * rs;
+    for (int r = 0; r < R; r++) {
+        wr[r] = W + (g * R + r < N ? g * R + r : N - 1) * rs;
+    }
+    float acc[R][NC];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            acc[r][c] = 0.0f;
         }
-        float acc[R][NC];
+    }
+    for (int64_t base = 0; base < K; base += 1024 * U) {
+        int4_t wv[U][R], xv[U][NC];
+        float  dw[U][R], dx[U][NC];
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-#pragma unroll
-            for (int c = 0; c < NC; c++) {
-                acc[r][c] = 0.0f;
-            }
-        }
-        for (int64_t off = (int64_t) lane * 16; off < K; off += 1024) {
-            int4_t wv[R];
-            float  dw[R];
+        for (int u = 0; u < U; u++) {
+            const int64_t off = base + 1024 * u + lane * 16;
+            const bool    ok  = off < K;
+            const int64_t o   = ok ? off : 0;
 #pragma unroll
             for (int r = 0; r < R; r++) {
-                wv[r] = ld16(wr[r] + off);
-                dw[r] = h2f(*(const uint16_t *) (wr[r] + K + 2 * (off >> 5)));
+                wv[u][r] = ld16(wr[r] + o);
+                dw[u][r] = ok ? h2f(*(const uint16_t *) (wr[r] + K + 2 * (o >> 5))) : 0.0f;
             }
-            const int b = (int) (off >> 5);
 #pragma unroll
             for (int c = 0; c < NC; c++) {
-                const int4_t xv = *(const int4_t *) (lq + c * K + off);
-                const float  dx = ld[c * nblk + b];
+                xv[u][c] = ld16(xq + c * K + o);
+                dx[u][c] = xd[c * nblk + (o >> 5)];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
 #pragma unroll
                 for (int r = 0; r < R; r++) {
-                    acc[r][c] += (float) dot16(wv[r], xv) * (dw[r] * dx);
+                    acc[r][c] += (float) dot16(wv[u][r], xv[u][c]) * (dw[u][r] * dx[u][c]);
                 }
             }
         }
-        store_rows<NC, R>(acc, lane, g * R, N, y, ldy);
     }
+    store_rows<NC, R>(acc, lane, g * R, N, y, ldy);
 }
 
-template <int NC, int R>
+// Q4_K.  Wave-chunk = 1024 bytes of qs (8 super-blocks); lane l owns 16
+// bytes = elements e_lo..e_lo+15 (low nibbles, sub-block 2c) and
+// e_lo+32..e_lo+47 (high nibbles, sub-block 2c+1) of super-block sb.
+template <int NC, int R, int U>
 __global__ __launch_bounds__(256) void k_gemv_q4_K(const uint8_t * __restrict__ W, int64_t N, int64_t K, int64_t rs,
-                                                    const uint8_t * __restrict__ xq, const float * __restrict__ xd,
+                                                    const int8_t * __restrict__ xq, const float * __restrict__ xd,
                                                     const int16_t * __restrict__ xbs, float * __restrict__ y,
                                                     int64_t ldy) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    const int64_t qs_bytes = (int64_t) NC * K;
-    const int     nsb      = (int) (K / 256);
-    const int     ngrp     = (int) (K / 16);
-    stage_act<NC>(lds, xq, qs_bytes, xd, NC * nsb, xbs, NC * ngrp);
-    const int8_t *  lq = (const int8_t *) lds;
-    const float *   ld = (const float *) (lds + qs_bytes);
-    const int16_t * lb = (const int16_t *) (lds + qs_bytes + 4 * (size_t) (NC * nsb));
-
-    const int     wave    = threadIdx.x >> 6;
-    const int     lane    = threadIdx.x & 63;
-    const int64_t half_k  = K / 2;
-    const int64_t ngroups = (N + R - 1) / R;
-    for (int64_t g = (int64_t) blockIdx.x * 4 + wave; g < ngroups; g += (int64_t) gridDim.x * 4) {
-        const uint8_t * wr[R];
+    const int     lane = threadIdx.x & 63;
+    const int64_t g    = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (g * R >= N) {
+        return;
+    }
+    const int64_t   half_k = K / 2;
+    const int       nsb    = (int) (K / 256);
+    const int       ngrp   = (int) (K / 16);
+    const uint8_t * wr[R];
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            const int64_t row = g * R + r < N ? g * R + r : N - 1;
-            wr[r]             = W + row * rs;
+    for (int r = 0; r < R; r++) {
+        wr[r] = W + (g * R + r < N ? g * R + r : N - 1) * rs;
+    }
+    float acc[R][NC];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            acc[r][c] = 0.0f;
         }
-        float acc[R][NC];
+    }
+    for (int64_t base = 0; base < half_k; base += 1024 * U) {
+        int4_t   wv[U][R];
+        uint32_t s0[U][R], s1[U][R], s2[U][R], dm[U][R];
+        int4_t   xlo[U][NC], xhi[U][NC];
+        int      blo[U][NC], bhi[U][NC];
+        float    dx[U][NC];
+        bool     ok[U];
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-#pragma unroll
-            for (int c = 0; c < NC; c++) {
-                acc[r][c] = 0.0f;
-            }
-        }
-        for (int64_t off = (int64_t) lane * 16; off < half_k; off += 1024) {
-            const int sb   = (int) (off >> 7);
-            const int o    = (int) (off & 127);
-            const int c64  = o >> 5;
-            const int hf   = (o >> 4) & 1;
-            const int e_lo = sb * 256 + c64 * 64 + hf * 16;
-            const int e_hi = e_lo + 32;
-            int4_t    wv[R];
-            int       sc_lo[R], sc_hi[R], mn_lo[R], mn_hi[R];
-            float     d[R], dmin[R];
+        for (int u = 0; u < U; u++) {
+            const int64_t off = base + 1024 * u + lane * 16;
+            ok[u]             = off < half_k;
+            const int64_t o   = ok[u] ? off : 0;
+            const int     sb  = (int) (o >> 7);
+            const int     e   = sb * 256 + (int) ((o & 127) >> 5) * 64 + (int) ((o >> 4) & 1) * 16;
 #pragma unroll
             for (int r = 0; r < R; r++) {
-                wv[r]               = ld16(wr[r] + off);
+                wv[u][r]            = ld16(wr[r] + o);
                 const uint32_t * sw = (const uint32_t *) (wr[r] + half_k + 12 * sb);
-                const uint32_t   w0 = sw[0], w1 = sw[1], w2 = sw[2];
-                const uint32_t   dm = *(const uint32_t *) (wr[r] + half_k + 12 * (int64_t) nsb + 4 * sb);
-                q4k_scale_min_w(2 * c64, w0, w1, w2, sc_lo[r], mn_lo[r]);
-                q4k_scale_min_w(2 * c64 + 1, w0, w1, w2, sc_hi[r], mn_hi[r]);
-                d[r]    = h2f((uint16_t) (dm & 0xffff));
-                dmin[r] = h2f((uint16_t) (dm >> 16));
+                s0[u][r]            = sw[0];
+                s1[u][r]            = sw[1];
+                s2[u][r]            = sw[2];
+                dm[u][r]            = *(const uint32_t *) (wr[r] + half_k + 12 * (int64_t) nsb + 4 * sb);
             }
 #pragma unroll
             for (int c = 0; c < NC; c++) {
-                const int4_t xlo   = *(const int4_t *) (lq + c * K + e_lo);
-                const int4_t xhi   = *(const int4_t *) (lq + c * K + e_hi);
-                const float  dx    = ld[c * nsb + sb];
-                const int    bs_lo = lb[c * ngrp + (e_lo >> 4)];
-                const int    bs_hi = lb[c * ngrp + (e_hi >> 4)];
+                xlo[u][c] = ld16(xq + c * K + e);
+                xhi[u][c] = ld16(xq + c * K + e + 32);
+                blo[u][c] = xbs[c * ngrp + (e >> 4)];
+                bhi[u][c] = xbs[c * ngrp + (e >> 4) + 2];
+                dx[u][c]  = xd[c * nsb + sb];
+            }
+        }
 #pragma unroll
-                for (int r = 0; r < R; r++) {
-                    const int4_t lo = { wv[r].x & 0x0F0F0F0F, wv[r].y & 0x0F0F0F0F, wv[r].z & 0x0F0F0F0F,
-                                        wv[r].w & 0x0F0F0F0F };
-                    const int4_t hi = { (wv[r].x >> 4) & 0x0F0F0F0F, (wv[r].y >> 4) & 0x0F0F0F0F,
-                                        (wv[r].z >> 4) & 0x0F0F0F0F, (wv[r].w >> 4) & 0x0F0F0F0F };
-                    const int isum = sc_lo[r] * dot16(lo, xlo) + sc_hi[r] * dot16(hi, xhi);
-                    const int msum = mn_lo[r] * bs_lo + mn_hi[r] * bs_hi;
-                    acc[r][c] += (d[r] * dx) * (float) isum - (dmin[r] * dx) * (float) msum;
+        for (int u = 0; u < U; u++) {
+            if (!ok[u]) {
+                continue;
+            }
+            const int c64 = (int) (((base + 1024 * u + lane * 16) & 127) >> 5);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                int sc_lo, mn_lo, sc_hi, mn_hi;
+                q4k_scale_min_w(2 * c64, s0[u][r], s1[u][r], s2[u][r], sc_lo, mn_lo);
+                q4k_scale_min_w(2 * c64 + 1, s0[u][r], s1[u][r], s2[u][r], sc_hi, mn_hi);
+                const float  d    = h2f((uint16_t) (dm[u][r] & 0xffff));
+                const float  dmin = h2f((uint16_t) (dm[u][r] >> 16));
+                const int4_t w    = wv[u][r];
+                const int4_t lo = { w.x & 0x0F0F0F0F, w.y & 0x0F0F0F0F, w.z & 0x0F0F0F0F, w.w & 0x0F0F0F0F };
+                const int4_t hi = { (w.x >> 4) & 0x0F0F0F0F, (w.y >> 4) & 0x0F0F0F0F, (w.z >> 4) & 0x0F0F0F0F,
+                                    (w.w >> 4) & 0x0F0F0F0F };
+#pragma unroll
+                for (int c = 0; c < NC; c++) {
+                    const int isum = sc_lo * dot16(lo, xlo[u][c]) + sc_hi * dot16(hi, xhi[u][c]);
+                    const int msum = mn_lo * blo[u][c] + mn_hi * bhi[u][c];
+                    acc[r][c] += (d * dx[u][c]) * (float) isum - (dmin * dx[u][c]) * (float) msum;
                 }
             }
         }
-        store_rows<NC, R>(acc, lane, g * R, N, y, ldy);
     }
+    store_rows<NC, R>(acc, lane, g * R, N, y, ldy);
 }
 
-template <int NC, int R>
+// Q6_K.  Unit = (super-block sb, half h, 16 columns l0..l0+15): 48 weight
+// bytes covering elements 256sb + 128h + l0 + 32t + i (t = 0..3, i < 16),
+// whose 16-element scale groups are g0 + 2t.  64 units per wave-chunk.
+template <int NC, int R, int U, bool AL>
 __global__ __launch_bounds__(256) void k_gemv_q6_K(const uint8_t * __restrict__ W, int64_t N, int64_t K, int64_t rs,
-                                                    const uint8_t * __restrict__ xq, const float * __restrict__ xd,
+                                                    const int8_t * __restrict__ xq, const float * __restrict__ xd,
                                                     const int16_t * __restrict__ xbs, float * __restrict__ y,
                                                     int64_t ldy) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    const int64_t qs_bytes = (int64_t) NC * K;
-    const int     nsb      = (int) (K / 256);
-    const int     ngrp     = (int) (K / 16);
-    stage_act<NC>(lds, xq, qs_bytes, xd, NC * nsb, xbs, NC * ngrp);
-    const int8_t *  lq = (const int8_t *) lds;
-    const float *   ld = (const float *) (lds + qs_bytes);
-    const int16_t * lb = (const int16_t *) (lds + qs_bytes + 4 * (size_t) (NC * nsb));
-
-    const int     wave    = threadIdx.x >> 6;
-    const int     lane    = threadIdx.x & 63;
-    const int64_t qh_off  = K / 2;
-    const int64_t sc_off  = K / 2 + K / 4;
-    const int64_t d_off   = sc_off + K / 16;
-    const int     units   = (int) (K / 64);
-    const int64_t ngroups = (N + R - 1) / R;
-    for (int64_t g = (int64_t) blockIdx.x * 4 + wave; g < ngroups; g += (int64_t) gridDim.x * 4) {
-        const uint8_t * wr[R];
+    const int     lane = threadIdx.x & 63;
+    const int64_t g    = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (g * R >= N) {
+        return;
+    }
+    const int64_t   qh_off = K / 2;
+    const int64_t   sc_off = K / 2 + K / 4;
+    const int64_t   d_off  = sc_off + K / 16;
+    const int       units  = (int) (K / 64);
+    const int       nsb    = (int) (K / 256);
+    const int       ngrp   = (int) (K / 16);
+    const uint8_t * wr[R];
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            const int64_t row = g * R + r < N ? g * R + r : N - 1;
-            wr[r]             = W + row * rs;
+    for (int r = 0; r < R; r++) {
+        wr[r] = W + (g * R + r < N ? g * R + r : N - 1) * rs;
+    }
+    float acc[R][NC];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            acc[r][c] = 0.0f;
         }
-        float acc[R][NC];
+    }
+    for (int base = 0; base < units; base += 64 * U) {
+        int4_t qa[U][R], qb[U][R], qh[U][R];
+        uint2  sw[U][R];
+        float  dw[U][R];
+        int4_t xv[U][NC][4];
+        int    bs[U][NC][4];
+        float  dx[U][NC];
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-#pragma unroll
-            for (int c = 0; c < NC; c++) {
-                acc[r][c] = 0.0f;
-            }
-        }
-        for (int u = lane; u < units; u += 64) {
-            const int sb  = u >> 2;
-            const int h   = (u >> 1) & 1;
-            const int l0  = (u & 1) * 16;
-            const int g0  = sb * 16 + h * 8 + (l0 >> 4);  // 16-element group of t = 0
-            const int eb  = sb * 256 + h * 128 + l0;      // element of t = 0, i = 0
-            int4_t    qa[R], qb[R], qh[R];
-            int       sc[R][4];
-            float     d[R];
+        for (int u = 0; u < U; u++) {
+            const int  uu = base + 64 * u + lane;
+            const bool ok = uu < units;
+            const int  un = ok ? uu : 0;
+            const int  sb = un >> 2, h = (un >> 1) & 1, l0 = (un & 1) * 16;
+            const int  g0 = sb * 16 + h * 8 + (l0 >> 4);
+            const int  eb = sb * 256 + h * 128 + l0;
 #pragma unroll
             for (int r = 0; r < R; r++) {
-                qa[r] = ld16(wr[r] + sb * 128 + h * 64 + l0);
-                qb[r] = ld16(wr[r] + sb * 128 + h * 64 + 32 + l0);
-                qh[r] = ld16(wr[r] + qh_off + sb * 64 + h * 32 + l0);
-                const uint8_t * s8 = wr[r] + sc_off + sb * 16 + h * 8;
-                const uint2     sw = *(const uint2 *) s8;
-#pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    const int      bi = (l0 >> 4) + 2 * t;
-                    const uint32_t wd = bi < 4 ? sw.x : sw.y;
-                    sc[r][t]          = (int) (int8_t) ((wd >> (8 * (bi & 3))) & 0xff);
-                }
-                d[r] = h2f(*(const uint16_t *) (wr[r] + d_off + 2 * sb));
+                qa[u][r] = ld16a<AL>(wr[r] + sb * 128 + h * 64 + l0);
+                qb[u][r] = ld16a<AL>(wr[r] + sb * 128 + h * 64 + 32 + l0);
+                qh[u][r] = ld16a<AL>(wr[r] + qh_off + sb * 64 + h * 32 + l0);
+                sw[u][r] = ld8a<AL>(wr[r] + sc_off + sb * 16 + h * 8);
+                dw[u][r] = ok ? h2f(*(const uint16_t *) (wr[r] + d_off + 2 * sb)) : 0.0f;
             }
 #pragma unroll
             for (int c = 0; c < NC; c++) {
-                const float dx = ld[c * nsb + sb];
-                int4_t      xv[4];
-                int         bs[4];
 #pragma unroll
                 for (int t = 0; t < 4; t++) {
-                    xv[t] = *(const int4_t *) (lq + c * K + eb + 32 * t);
-                    bs[t] = lb[c * ngrp + g0 + 2 * t];
+                    xv[u][c][t] = ld16(xq + c * K + eb + 32 * t);
+                    bs[u][c][t] = xbs[c * ngrp + g0 + 2 * t];
+                }
+                dx[u][c] = xd[c * nsb + sb];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int l0 = ((base + 64 * u + lane) & 1) * 16;
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                int4_t q[4];
+                int    sc[4];
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const int4_t src = (t & 1) ? qb[u][r] : qa[u][r];
+                    const int    sh  = (t < 2) ? 0 : 4;
+                    q[t].x = ((src.x >> sh) & 0x0F0F0F0F) | (((qh[u][r].x >> (2 * t)) & 0x03030303) << 4);
+                    q[t].y = ((src.y >> sh) & 0x0F0F0F0F) | (((qh[u][r].y >> (2 * t)) & 0x03030303) << 4);
+                    q[t].z = ((src.z >> sh) & 0x0F0F0F0F) | (((qh[u][r].z >> (2 * t)) & 0x03030303) << 4);
+                    q[t].w = ((src.w >> sh) & 0x0F0F0F0F) | (((qh[u][r].w >> (2 * t)) & 0x03030303) << 4);
+                    const int      bi = (l0 >> 4) + 2 * t;
+                    const uint32_t wd = bi < 4 ? sw[u][r].x : sw[u][r].y;
+                    sc[t]             = (int) (int8_t) ((wd >> (8 * (bi & 3))) & 0xff);
                 }
 #pragma unroll
-                for (int r = 0; r < R; r++) {
+                for (int c = 0; c < NC; c++) {
                     int isum = 0;
 #pragma unroll
                     for (int t = 0; t < 4; t++) {
-                        const int4_t src = (t & 1) ? qb[r] : qa[r];
-                        const int    sh  = (t < 2) ? 0 : 4;
-                        int4_t       q;
-                        q.x = ((src.x >> sh) & 0x0F0F0F0F) | (((qh[r].x >> (2 * t)) & 0x03030303) << 4);
-                        q.y = ((src.y >> sh) & 0x0F0F0F0F) | (((qh[r].y >> (2 * t)) & 0x03030303) << 4);
-                        q.z = ((src.z >> sh) & 0x0F0F0F0F) | (((qh[r].z >> (2 * t)) & 0x03030303) << 4);
-                        q.w = ((src.w >> sh) & 0x0F0F0F0F) | (((qh[r].w >> (2 * t)) & 0x03030303) << 4);
-                        isum += sc[r][t] * (dot16(q, xv[t]) - 32 * bs[t]);
+                        isum += sc[t] * (dot16(q[t], xv[u][c][t]) - 32 * bs[u][c][t]);
                     }
-                    acc[r][c] += (d[r] * dx) * (float) isum;
+                    acc[r][c] += (dw[u][r] * dx[u][c]) * (float) isum;
                 }
             }
         }
-        store_rows<NC, R>(acc, lane, g * R, N, y, ldy);
     }
+    store_rows<NC, R>(acc, lane, g * R, N, y, ldy);
 }
 
 // ---------------------------------------------------------------------
 // host dispatch
 
-constexpr int GEMV_R = 2;
-
-static size_t gemv_lds_bytes(int wtype, int64_t K, int M) {
-    if (wtype == TYPE_Q8_0) {
-        return (size_t) M * K + 4 * (size_t) M * (K / 32);
-    }
-    return (size_t) M * K + 4 * (size_t) M * (K / 256) + 2 * (size_t) M * (K / 16);
-}
-
 template <typename F, typename... Args>
-static int launch_gemv(F kern, size_t lds, int64_t N, hipStream_t stream, Args... args) {
-    static thread_local const void * raised[64] = {};
-    if (lds > 64 * 1024) {
-        // opt in to the large-LDS limit once per kernel instance
-        bool seen = false;
-        for (const void * p : raised) {
-            if (p == (const void *) kern) {
-                seen = true;
-                break;
-            }
-        }
-        if (!seen) {
-            if (hipFuncSetAttribute((const void *) kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds) !=
-                hipSuccess) {
-                return set_error(MMHIP_ERR_HIP, "gemv: cannot raise LDS limit to %zu", lds);
-            }
-            for (auto & p : raised) {
-                if (!p) {
-                    p = (const void *) kern;
-                    break;
-                }
-            }
-        }
+static int launch_gemv(F kern, int R, int64_t N, hipStream_t stream, Args... args) {
+    const int64_t waves = (N + R - 1) / R;
+    const int64_t wgs   = (waves + 3) / 4;
+    if (wgs > 0x7fffffff) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "gemv: N=%lld too large", (long long) N);
     }
-    const int64_t groups = (N + GEMV_R - 1) / GEMV_R;
-    const int64_t wgs    = (groups + 3) / 4;
-    const int     grid   = (int) std::min<int64_t>(wgs, 1024);
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, stream, args...);
+    hipLaunchKernelGGL(kern, dim3((unsigned) wgs), dim3(256), 0, stream, args...);
     return check_launch("gemv");
 }
+
+// Rows per wave and chunks in flight per lane, by activation count.
+template <int NC> struct GemvShape {
+    static constexpr int R = NC <= 2 ? 4 : 2;
+    static constexpr int U = NC <= 2 ? 4 : NC <= 4 ? 2 : 1;
+};
 
 template <int NC>
 static int gemv_dispatch(int wtype, const uint8_t * W, int64_t N, int64_t K, int64_t rs, const ActPtrs & x, float * y,
                          int64_t ldy, hipStream_t stream) {
-    const size_t    lds = gemv_lds_bytes(wtype, K, NC);
-    const uint8_t * xq  = (const uint8_t *) x.qs;
+    constexpr int R = GemvShape<NC>::R;
+    constexpr int U = GemvShape<NC>::U;
     if (wtype == TYPE_Q8_0) {
-        return launch_gemv(k_gemv_q8_0<NC, GEMV_R>, lds, N, stream, W, N, K, rs, xq, x.d, y, ldy);
+        return launch_gemv(k_gemv_q8_0<NC, R, U>, R, N, stream, W, N, K, rs, x.qs, x.d, y, ldy);
     }
     if (wtype == TYPE_Q4_K) {
-        return launch_gemv(k_gemv_q4_K<NC, GEMV_R>, lds, N, stream, W, N, K, rs, xq, x.d, x.bs, y, ldy);
+        constexpr int U4 = U > 2 ? 2 : U;
+        return launch_gemv(k_gemv_q4_K<NC, R, U4>, R, N, stream, W, N, K, rs, x.qs, x.d, x.bs, y, ldy);
     }
-    return launch_gemv(k_gemv_q6_K<NC, GEMV_R>, lds, N, stream, W, N, K, rs, xq, x.d, x.bs, y, ldy);
+    constexpr int U6 = 1;
+    if (rs % 16 == 0 && ((uintptr_t) W) % 16 == 0) {
+        return launch_gemv(k_gemv_q6_K<NC, R, U6, true>, R, N, stream, W, N, K, rs, x.qs, x.d, x.bs, y, ldy);
+    }
+    return launch_gemv(k_gemv_q6_K<NC, R, U6, false>, R, N, stream, W, N, K, rs, x.qs, x.d, x.bs, y, ldy);
 }
 
 bool gemv_supported(int wtype, int64_t N, int64_t K, int64_t rs, const void * W) {
-    return (wtype == TYPE_Q8_0 || wtype == TYPE_Q4_K || wtype == TYPE_Q6_K) && K % 256 == 0 && N > 0 &&
-           rs >= row_bytes(wtype, K) && rs % 16 == 0 && ((uintptr_t) W) % 16 == 0 &&
-           gemv_lds_bytes(wtype, K, 1) <= 160 * 1024;
+    if (!(wtype == TYPE_Q8_0 || wtype == TYPE_Q4_K || wtype == TYPE_Q6_K) || K % 256 != 0 || N <= 0 ||
+        rs < row_bytes(wtype, K)) {
+        return false;
+    }
+    // Q8_0 / Q4_K rows are read with 16-byte loads; Q6_K rows may be 2-byte aligned
+    const int64_t align = wtype == TYPE_Q6_K ? 2 : 16;
+    return rs % align == 0 && ((uintptr_t) W) % align == 0;
 }
 
 int gemv_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const ActPtrs & x, int64_t M, float * y,
@@ -401,11 +413,7 @@ int gemv_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const Ac
         return set_error(MMHIP_ERR_UNSUPPORTED, "gemv: type %d N=%lld K=%lld M=%lld rs=%lld not supported", wtype,
                          (long long) N, (long long) K, (long long) M, (long long) rs);
     }
-    // column groups of up to 8 that fit the LDS budget
-    int mc = 8;
-    while (mc > 1 && gemv_lds_bytes(wtype, K, mc) > 160 * 1024) {
-        mc--;
-    }
+    const int mc = 8;  // column groups of up to 8
     const uint8_t * wb = (const uint8_t *) W;
     for (int64_t c0 = 0; c0 < M; c0 += mc) {
         const int64_t nc = std::min<int64_t>(mc, M - c0);

@@ -169,7 +169,7 @@ extern "C" size_t mmhip_flash_attn_workspace(const mmhip_view * q, const mmhip_v
     if (fa_validate(q, k, v, nullptr, a, D) != MMHIP_OK) {
         return 0;
     }
-    return fa_decode_workspace(a, D);
+    return fa_use_mfma(a, D) ? fa_mfma_workspace(a) : fa_decode_workspace(a, D);
 }
 
 extern "C" int mmhip_flash_attn_ext(const mmhip_view * q, const mmhip_view * k, const mmhip_view * v,
@@ -186,5 +186,8 @@ extern "C" int mmhip_flash_attn_ext(const mmhip_view * q, const mmhip_view * k, 
         return set_error(MMHIP_ERR_INVALID, "flash_attn: null output");
     }
     a.scale = scale;
+    if (fa_use_mfma(a, D)) {
+        return fa_mfma(a, D, out, ws, ws_bytes, (hipStream_t) stream);
+    }
     return fa_decode(a, D, out, ws, ws_bytes, (hipStream_t) stream);
 }

@@ -63,10 +63,26 @@ def test_decode_shapes(mm, orc, B, Bk, Hq, Hkv, nq, nkv, D):
     k = rnd((Bk, Hkv, nkv, D), 22, np.float16)
     v = rnd((Bk, Hkv, nkv, D), 23, np.float16)
     mask = np.where(np.random.default_rng(24).random((1, 1, nq, nkv)) < 0.2, -np.inf, 0).astype(np.float16)
-    s = 0.3
+    s = float(np.float32(1 / np.sqrt(D)))  # the graphs' scale, src/qwen3-lm.h:785, src/dit.h:216
     out = mm.flash_attn_ext(torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
                             torch.from_numpy(mask).cuda(), s).cpu().numpy()
-    check(out, orc.flash_attn_ext(q, k, v, mask, s, "f64"))
+    check(out, orc.flash_attn_ext(q, k, v, mask, s, "f64"), orc.flash_attn_ext(q, k, v, mask, s, "ggml"))
+
+
+def test_decode_sharp_softmax(mm, orc):
+    """A larger scale sharpens the softmax; Q rounded to f16 (ggml's Q->f16
+    conversion) then dominates the error: bounded by 5e-3 against fp64."""
+    q = rnd((1, 8, 2, 128), 25)
+    k = rnd((1, 2, 500, 128), 26, np.float16)
+    v = rnd((1, 2, 500, 128), 27, np.float16)
+    out = mm.flash_attn_ext(torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                            None, 0.3).cpu().numpy()
+    ref = orc.flash_attn_ext(q, k, v, None, 0.3, "f64")
+    assert np.abs(out - ref).max() < 5e-3 and cosine(out, ref) > 0.9999
+    # the f16 V accumulator of the ggml-semantics oracle drifts further from
+    # fp64 than the f32 accumulation here: bound by its own error + 2e-3
+    refg = orc.flash_attn_ext(q, k, v, None, 0.3, "ggml")
+    assert np.abs(out - refg).max() < np.abs(refg - ref).max() + 2e-3
 
 
 def test_fully_masked_rows_are_zero(mm):
