@@ -107,3 +107,107 @@ def test_permuted_query_view(mm, orc):
                             q_view=qview).cpu().numpy()
     qn = np.ascontiguousarray(qs.transpose(0, 2, 1, 3))  # [B, H, S, D]
     check(out, orc.flash_attn_ext(qn, k, v, None, 0.125, "f64"))
+
+
+# ---------------------------------------------------------------------------
+# many query rows: the MFMA kernel (causal prefill, DiT bidirectional)
+
+def oracle_rows(orc, q, k, v, mask, scale, rows, flavour="f64"):
+    """Oracle on a subset of query rows (q [B, Hq, nq, D]); returns [B, len, Hq, D]."""
+    qs = np.ascontiguousarray(q[:, :, rows])
+    ms = None if mask is None else np.ascontiguousarray(mask[:, :, rows])
+    return orc.flash_attn_ext(qs, k, v, ms, scale, flavour)
+
+
+def test_dit_real_shape_permuted_views(mm, orc):
+    """DiT attention at its real shape (src/dit.h:54-55, T = 689 + 1): 32 heads
+    x 64 dims, 690 tokens, B = 2, no mask.  Q is the permuted view of the
+    [D, Nh, S, B] projection (src/dit.h:212); K/V are the contiguous f16 casts
+    (src/dit.h:219-220)."""
+    B, S, H, D = 2, 690, 32, 64
+    qst = rnd((B, S, H, D), 41)                      # ggml [D, H, S, B]
+    k = rnd((B, H, S, D), 42, np.float16)            # ggml [D, S, H, B]
+    v = rnd((B, H, S, D), 43, np.float16)
+    s = float(np.float32(1 / np.sqrt(D)))
+    qt = torch.from_numpy(qst).cuda()
+    qview = mm.view_of(qt, ne=[D, S, H, B], nb=[4, H * D * 4, D * 4, S * H * D * 4])
+    out = mm.flash_attn_ext(qt, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(), None, s,
+                            q_view=qview).cpu().numpy()
+    qn = np.ascontiguousarray(qst.transpose(0, 2, 1, 3))
+    check(out, orc.flash_attn_ext(qn, k, v, None, s, "f64"))
+
+
+def test_dit_benchmark_shape_sampled(mm, orc):
+    """B=2, 4096 latent tokens, 16 heads x 128, no mask; Q drawn N(0,1) and
+    rounded to f16 (passed as f32).  Checked on 48 sampled query rows."""
+    B, S, H, D = 2, 4096, 16, 128
+    q = rnd((B, H, S, D), 1004).astype(np.float16).astype(np.float32)
+    k = rnd((B, H, S, D), 1005, np.float16)
+    v = rnd((B, H, S, D), 1006, np.float16)
+    s = float(np.float32(1 / np.sqrt(D)))
+    out = mm.flash_attn_ext(torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                            None, s).cpu().numpy()
+    rows = np.array([0, 1, 127, 128, 129, 1000, 2047, 2048, 3071, 4094, 4095] +
+                    list(np.random.default_rng(7).choice(4096, 37, replace=False)))
+    ref = oracle_rows(orc, q, k, v, None, s, rows)
+    check(out[:, rows], ref)
+
+
+def causal_mask(S, n_kv):
+    m = np.full((S, n_kv), -np.inf, np.float32)
+    for i in range(S):
+        m[i, : i + 1] = 0
+    return m.astype(np.float16)[None, None]
+
+
+def test_causal_prefill_benchmark_shape_sampled(mm, orc):
+    """B=2 (CFG), 1024 tokens, 32 q / 8 KV heads, D=128, causal f16 mask."""
+    B, S, Hq, Hkv, D = 2, 1024, 32, 8, 128
+    q = rnd((B, Hq, S, D), 1003).astype(np.float16).astype(np.float32)
+    k = rnd((B, Hkv, S, D), 1013, np.float16)
+    v = rnd((B, Hkv, S, D), 1023, np.float16)
+    mask = causal_mask(S, S)
+    s = float(np.float32(1 / np.sqrt(D)))
+    out = mm.flash_attn_ext(torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                            torch.from_numpy(mask).cuda(), s).cpu().numpy()
+    rows = np.array([0, 1, 2, 63, 64, 127, 128, 129, 511, 512, 700, 1022, 1023])
+    ref = oracle_rows(orc, q, k, v, mask, s, rows)
+    check(out[:, rows], ref, oracle_rows(orc, q, k, v, mask, s, rows, "ggml"))
+
+
+def test_lm_prefill_real_path(mm, orc):
+    """qw3lm_build_attn (src/qwen3-lm.h:346-443): Q is the permuted view of
+    [D, Nh, S]; K/V are [0, n_kv_pad) windows of the [D, max_seq, Nkv] f16
+    cache; the mask is [n_kv_pad, S] with -inf above the diagonal and on the
+    padded tail."""
+    S, Hq, Hkv, D, max_seq, pad = 200, 32, 8, 128, 1024, 256
+    qst = rnd((S, Hq, D), 51)                               # ggml [D, Nh, S]
+    cache_k = torch.from_numpy(rnd((Hkv, max_seq, D), 52, np.float16)).cuda()
+    cache_v = torch.from_numpy(rnd((Hkv, max_seq, D), 53, np.float16)).cuda()
+    kw, vw = cache_k[:, :pad], cache_v[:, :pad]
+    mask = causal_mask(S, pad)
+    s = float(np.float32(1 / np.sqrt(D)))
+    qt = torch.from_numpy(qst).cuda()
+    qview = mm.view_of(qt, ne=[D, S, Hq, 1], nb=[4, Hq * D * 4, D * 4, S * Hq * D * 4])
+    out = mm.flash_attn_ext(qt, kw, vw, torch.from_numpy(mask).cuda(), s, q_view=qview).cpu().numpy()
+    qn = np.ascontiguousarray(qst.transpose(1, 0, 2))[None]
+    kn, vn = kw.cpu().numpy()[None], vw.cpu().numpy()[None]
+    check(out, orc.flash_attn_ext(qn, kn, vn, mask, s, "f64"), orc.flash_attn_ext(qn, kn, vn, mask, s, "ggml"))
+
+
+@pytest.mark.parametrize("B,Bk,Hq,Hkv,nq,nkv,D", [(2, 1, 8, 2, 130, 77, 64), (1, 1, 4, 1, 257, 300, 128),
+                                                 (2, 2, 2, 2, 33, 1, 128), (1, 1, 16, 16, 64, 640, 64)])
+def test_mfma_odd_shapes_with_mask(mm, orc, B, Bk, Hq, Hkv, nq, nkv, D):
+    q = rnd((B, Hq, nq, D), 61)
+    k = rnd((Bk, Hkv, nkv, D), 62, np.float16)
+    v = rnd((Bk, Hkv, nkv, D), 63, np.float16)
+    rng = np.random.default_rng(64)
+    mask = np.where(rng.random((B, 1, nq, nkv + 3)) < 0.3, -np.inf, rng.normal(0, 1, (B, 1, nq, nkv + 3)))
+    mask[:, :, 5] = -np.inf  # a fully masked query row -> 0
+    mask = mask.astype(np.float16)
+    s = float(np.float32(1 / np.sqrt(D)))
+    out = mm.flash_attn_ext(torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                            torch.from_numpy(mask).cuda(), s).cpu().numpy()
+    mk = np.ascontiguousarray(mask)
+    check(out, orc.flash_attn_ext(q, k, v, mk, s, "f64"))
+    assert not out[:, 5].any()

@@ -57,3 +57,50 @@ def test_gemv_rejects_bad_shapes(mm, pkg):
     with pytest.raises(mm.MmhipError) as e:
         mm.mul_mat(W, torch.zeros((2, 96), device="cuda"))
     assert e.value.code == mm.ERR_UNSUPPORTED
+
+
+# ---------------------------------------------------------------------------
+# token counts (M > 8): MFMA GEMM on f16-rounded dequantised weights and
+# f16-rounded activations with f32 accumulation.  Stated tolerance against
+# the exact fp64 oracle: relative RMS error <= 2e-3 and cosine >= 0.99999;
+# against the ggml-CPU-semantics oracle: cosine >= 0.9999.
+
+def rel_rms(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / np.linalg.norm(b))
+
+
+@pytest.mark.parametrize("t", [8, 12, 14])
+@pytest.mark.parametrize("N,K,M", [(384, 2048, 200), (100, 4096, 9), (130, 2048, 1380)])
+def test_gemm_shapes(mm, orc, pkg, t, N, K, M):
+    y, yg, yf = run(mm, orc, pkg, t, N, K, M, 5000 + t + M)
+    assert rel_rms(y, yf) < 2e-3
+    assert cosine(y, yf) > 0.99999
+    assert cosine(y, yg) > 0.9999
+
+
+def test_gemm_q4_K_benchmark_shape_sampled(mm, orc, pkg):
+    """DiT QKV projection workload: W 6144 x 2048 Q4_K, 8192 tokens; checked
+    on 40 sampled tokens."""
+    N, K, M = 6144, 2048, 8192
+    raw = pkg.synth.gguf_blocks_np(12, N, K, 1005)
+    x = pkg.synth.normal_np((M, K), 1006)
+    W = mm.QuantWeight.from_gguf(12, raw, N, K)
+    y = mm.mul_mat(W, torch.from_numpy(x).cuda()).cpu().numpy()
+    rows = np.array([0, 1, 127, 128, 4095, 8191] + list(np.random.default_rng(8).choice(M, 34, replace=False)))
+    yf = orc.mul_mat_f64(12, raw, N, K, x[rows])
+    assert rel_rms(y[rows], yf) < 2e-3
+    assert cosine(y[rows], yf) > 0.99999
+
+
+def test_gemm_matches_gemv_semantics_closely(mm, pkg):
+    """M = 8 (GEMV, activation-quantised) and M = 9 (GEMM, f16) agree on the
+    shared rows to the activation-quantisation error."""
+    N, K = 512, 2048
+    raw = pkg.synth.gguf_blocks_np(8, N, K, 77)
+    x = torch.from_numpy(pkg.synth.normal_np((9, K), 78)).cuda()
+    W = mm.QuantWeight.from_gguf(8, raw, N, K)
+    a = mm.mul_mat(W, x[:8].contiguous()).cpu().numpy()
+    b = mm.mul_mat(W, x).cpu().numpy()[:8]
+    assert cosine(a, b) > 0.9999
