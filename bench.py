@@ -37,7 +37,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="gemv_q8_0", choices=["gemv_q8_0", "fa_decode"])
+    ap.add_argument("--workload", default="gemv_q8_0",
+                    choices=["gemv_q8_0", "fa_decode", "fa_prefill", "fa_dit", "gemm_q4_k"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     return ap.parse_args()
@@ -206,6 +207,154 @@ def bench_fa(args, torch, pkg):
     }
 
 
+def _fa_common(args, torch, pkg, B, Hq, Hkv, S, D, causal, seed, copies):
+    mm, synth = pkg.mmhip, pkg.synth
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    qs = [torch.randn((B, Hq, S, D), device="cuda", generator=g).half().float() for _ in range(copies)]
+    ks = [torch.randn((B, Hkv, S, D), device="cuda", generator=g).half() for _ in range(copies)]
+    vs = [torch.randn((B, Hkv, S, D), device="cuda", generator=g).half() for _ in range(copies)]
+    mask = None
+    if causal:
+        mask = torch.full((S, S), float("-inf"), device="cuda").triu(1).half().view(1, 1, S, S)
+    out = torch.empty((B, S, Hq, D), device="cuda")
+    L = mm.load()
+    views = [(mm.view_of(q), mm.view_of(k), mm.view_of(v)) for q, k, v in zip(qs, ks, vs)]
+    mv = mm.view_of(mask) if mask is not None else None
+    need = L.mmhip_flash_attn_workspace(ctypes.byref(views[0][0]), ctypes.byref(views[0][1]),
+                                        ctypes.byref(views[0][2]))
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    scale = float(np.float32(1 / np.sqrt(D)))
+
+    def step(i):
+        qv, kv, vv = views[i % copies]
+        rc = L.mmhip_flash_attn_ext(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv),
+                                    ctypes.byref(mv) if mv is not None else None, scale,
+                                    ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(ws.data_ptr()), need, st)
+        assert rc == 0, L.mmhip_last_error()
+
+    return step
+
+
+def _timed(args, torch, step, copies):
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / args.steps * 1e3
+    avg_s, med_s = time_launches(torch, step, max(args.steps, 32), copies)
+    return ms, avg_s, med_s
+
+
+MFMA_PEAK_TFLOPS = 2500.0
+
+
+def bench_fa_mfma(args, torch, pkg, causal):
+    import oracle
+
+    if causal:
+        B, Hq, Hkv, S, D, seed = 2, 32, 8, 1024, 128, 1003
+        flops = 4.0 * B * Hq * D * S * (S + 1) / 2
+        name = "causal prefill attention B=2 S=1024 Hq=32 Hkv=8 D=128"
+    else:
+        B, Hq, Hkv, S, D, seed = 2, 16, 16, 4096, 128, 1004
+        flops = 4.0 * B * Hq * S * S * D
+        name = "DiT bidirectional attention B=2 S=4096 H=16 D=128"
+    copies = 2
+    step = _fa_common(args, torch, pkg, B, Hq, Hkv, S, D, causal, seed, copies)
+    ms, avg_s, med_s = _timed(args, torch, step, copies)
+    tf = flops / avg_s / 1e12
+    cpu = None
+    if not args.no_cpu:
+        rng = np.random.default_rng(seed)
+        rows = 16 if causal else 4  # bounded sample of query rows per head
+        q = rng.standard_normal((B, Hq, rows, D)).astype(np.float32)
+        k = rng.standard_normal((B, Hkv, S, D)).astype(np.float16)
+        v = rng.standard_normal((B, Hkv, S, D)).astype(np.float16)
+        n_thr = os.cpu_count() or 1
+        t0 = time.perf_counter()
+        it = 0
+        while time.perf_counter() - t0 < args.cpu_seconds:
+            oracle.flash_attn_ext(q, k, v, None, 1 / np.sqrt(D), "ggml", nthreads=n_thr)
+            it += 1
+        dt = (time.perf_counter() - t0) / it
+        cpu_flops = 4.0 * B * Hq * rows * S * D
+        cpu = {"value": round(cpu_flops / dt / 1e12, 5), "unit": "TFLOP/s", "cores": n_thr, "kind": "port",
+               "sample": f"ggml-CPU-semantics flash_attn_ext (oracle/oracle.c): {rows} query rows per head against "
+                         f"all {S} keys, {it} reps"}
+    return {
+        "metric": ("causal prefill" if causal else "DiT") + " attention TFLOP/s",
+        "value": round(flops / (ms * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "ms_per_step": round(ms, 4),
+        "dtype": "f16 MFMA, f32 accumulate",
+        "config": {"workload": name, "mask": "causal f16" if causal else "none"},
+        "roofline": {"bound": "mfma", "kernel": "k_fa_mfma<128>", "achieved": round(tf, 2),
+                     "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
+                     "avg_launch_us": round(avg_s * 1e6, 2), "median_launch_us": round(med_s * 1e6, 2),
+                     "alg_flops_per_launch": flops, "traffic": None},
+        "cpu_baseline": cpu,
+    }
+
+
+def bench_gemm(args, torch, pkg):
+    import oracle
+
+    mm, synth = pkg.mmhip, pkg.synth
+    N, K, M = 6144, 2048, 8192
+    copies = 2
+    Ws = [mm.QuantWeight.from_gguf(mm.Q4_K, synth.gguf_blocks_torch(mm.Q4_K, N, K, 1005 + c), N, K)
+          for c in range(copies)]
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1006)
+    xs = [torch.randn((M, K), device="cuda", generator=g) for _ in range(copies)]
+    y = torch.empty((M, N), device="cuda")
+    L = mm.load()
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def step(i):
+        W, x = Ws[i % copies], xs[i % copies]
+        rc = L.mmhip_mul_mat(mm.Q4_K, ctypes.c_void_p(W.data.data_ptr()), N, K, W.row_bytes,
+                             ctypes.c_void_p(x.data_ptr()), K, M, ctypes.c_void_p(y.data_ptr()), N, None, 0, st)
+        assert rc == 0, L.mmhip_last_error()
+
+    ms, avg_s, med_s = _timed(args, torch, step, copies)
+    flops = 2.0 * M * N * K
+    tf = flops / avg_s / 1e12
+    cpu = None
+    if not args.no_cpu:
+        rows = 64
+        raw = synth.gguf_blocks_np(mm.Q4_K, rows, K, 9)
+        x = synth.normal_np((64, K), 10)
+        n_thr = os.cpu_count() or 1
+        t0 = time.perf_counter()
+        it = 0
+        while time.perf_counter() - t0 < args.cpu_seconds:
+            oracle.mul_mat_ggml(mm.Q4_K, raw, rows, K, x, nthreads=n_thr)
+            it += 1
+        dt = (time.perf_counter() - t0) / it
+        cpu = {"value": round(2.0 * 64 * rows * K / dt / 1e12, 5), "unit": "TFLOP/s", "cores": n_thr,
+               "kind": "port", "sample": f"ggml-CPU-semantics Q4_K x Q8_K mul_mat (oracle/oracle.c): {rows} weight "
+                                         f"rows x 64 tokens, K={K}, {it} reps"}
+    return {
+        "metric": "Q4_K GEMM TFLOP/s (DiT QKV projection 2048->6144, 8192 tokens)",
+        "value": round(flops / (ms * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "ms_per_step": round(ms, 4),
+        "dtype": "f16 MFMA (Q4_K dequantised to f16), f32 accumulate",
+        "config": {"workload": "Q4_K GEMM W[6144x2048] x[8192x2048] f32 -> f32"},
+        "roofline": {"bound": "mfma", "kernel": "k_gemm_q<Q4_K>", "achieved": round(tf, 2),
+                     "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
+                     "avg_launch_us": round(avg_s * 1e6, 2), "median_launch_us": round(med_s * 1e6, 2),
+                     "alg_flops_per_launch": flops, "traffic": None},
+        "cpu_baseline": cpu,
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -217,7 +366,13 @@ def main():
 
     pkg = __graft_entry__.load_package()
     pkg.mmhip.load()
-    res = bench_gemv(args, torch, pkg) if args.workload == "gemv_q8_0" else bench_fa(args, torch, pkg)
+    res = {
+        "gemv_q8_0": lambda: bench_gemv(args, torch, pkg),
+        "fa_decode": lambda: bench_fa(args, torch, pkg),
+        "fa_prefill": lambda: bench_fa_mfma(args, torch, pkg, True),
+        "fa_dit": lambda: bench_fa_mfma(args, torch, pkg, False),
+        "gemm_q4_k": lambda: bench_gemm(args, torch, pkg),
+    }[args.workload]()
     line = {
         "metric": res["metric"],
         "value": res["value"],

@@ -2,7 +2,8 @@
 
 Tolerances (stated): against the fp64 oracle max-abs <= 2e-3 and cosine >=
 0.9999; against the ggml-CPU-semantics oracle (f16 V accumulator) max-abs
-<= 3e-3."""
+<= that oracle's own max-abs distance from fp64 + 1e-3 (the GPU accumulates
+in f32, so it sits closer to fp64 than ggml-CPU does)."""
 import numpy as np
 import pytest
 import torch
@@ -21,7 +22,7 @@ def check(out, ref64, refg=None):
     assert np.abs(out - ref64).max() < 2e-3
     assert cosine(out, ref64) > 0.9999
     if refg is not None:
-        assert np.abs(out - refg).max() < 3e-3
+        assert np.abs(out - refg).max() <= np.abs(refg - ref64).max() + 1e-3
 
 
 def test_decode_benchmark_shape(mm, orc):
