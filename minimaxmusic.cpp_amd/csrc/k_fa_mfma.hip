@@ -2,8 +2,8 @@
 // (src/qwen3-lm.h:432-436) and the DiT's bidirectional attention
 // (src/dit.h:221-222).
 //
-// Workgroup = 4 waves = 128 query rows of one (head, batch); each wave owns 32
-// query rows.  KV is walked in tiles of 64 keys staged in LDS (K as rows, V
+// Workgroup = NW waves = 32*NW query rows of one (head, batch); each wave owns
+// 32 query rows.  KV is walked in tiles of 64 keys staged in LDS (K as rows, V
 // transposed).  Per tile a wave computes S^T = K Q^T (keys x queries) with
 // v_mfma_f32_32x32x16_f16, so each lane owns one query column: the online
 // softmax (max, sum, rescale) is lane-local apart from one exchange with the
@@ -14,16 +14,16 @@
 //
 // Arithmetic: Q, K, V and P are f16 MFMA operands with f32 accumulation
 // (GGML_PREC_F32); the softmax runs in f32 base 2 with log2(e) folded into the
-// scale.  A prepass over the mask finds, per 128-query tile, the last key any
-// query of the tile can see, so fully masked KV tiles (the causal upper
-// triangle, the -inf padding of the cache window) are never read.
+// scale.  A prepass over the mask finds, per query row, the last key the row
+// can see; a workgroup stops at the last key any of its rows can see, so fully
+// masked KV tiles (the causal upper triangle, the -inf padding of the cache
+// window) are never read.
 #include "k_fa_common.h"
 #include "mmhip_device.h"
 #include "mmhip_internal.h"
 
 namespace mmhip {
 
-constexpr int FA_BQ = 128;
 constexpr int FA_BK = 64;
 
 __device__ __forceinline__ float16_t mfma32(half8_t a, half8_t b, float16_t c) {
@@ -35,28 +35,47 @@ __device__ __forceinline__ int vt_pos(int k) {
     return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
 }
 
-template <int D>
-__global__ __launch_bounds__(256) void k_fa_mfma(FaArgs a, const int * __restrict__ kv_end_tab, int n_qtiles,
-                                                 float * __restrict__ out) {
-    constexpr int KS = D + 8;       // K row stride (halves)
-    constexpr int VS = FA_BK + 8;   // V^T row stride (halves)
+// Work item of linear workgroup id `lin` out of `total`: workgroups are
+// dispatched round-robin over the 8 XCDs (id % 8), so consecutive work items
+// are dealt to one XCD at a time; all query tiles of a (head, batch) then
+// share that XCD's L2 for their K/V tiles.
+__device__ __forceinline__ int xcd_remap(int lin, int total) {
+    const int per = total / 8;
+    if (lin >= per * 8) {
+        return lin;  // the remainder keeps its own index
+    }
+    return (lin % 8) * per + lin / 8;
+}
+
+template <int D, int NW>
+__global__ __launch_bounds__(NW * 64) void k_fa_mfma(FaArgs a, const int * __restrict__ row_end, int n_qtiles,
+                                                     float * __restrict__ out) {
+    constexpr int NT  = NW * 64;
+    constexpr int BQ  = NW * 32;
+    constexpr int KS  = D + 8;      // K row stride (halves)
+    constexpr int VS  = FA_BK + 8;  // V^T row stride (halves)
     constexpr int NQK = D / 16;     // MFMA k-steps for Q.K
     constexpr int NDB = D / 32;     // 32-row blocks of O^T
+    constexpr int KCH = FA_BK * (D / 8) / NT;        // 16-byte K chunks per thread per tile
+    constexpr int VCH = (FA_BK / 2) * (D / 8) / NT;  // V key pairs x 8 dims per thread per tile
+    static_assert(KCH >= 1 && VCH >= 1, "tile too small for the workgroup");
     __shared__ __attribute__((aligned(16))) _Float16 sK[FA_BK * KS];
     __shared__ __attribute__((aligned(16))) _Float16 sV[D * VS];
 
-    const int qt   = n_qtiles - 1 - (int) blockIdx.x;  // longest (causal) tiles first
-    const int h    = blockIdx.y;
-    const int b    = blockIdx.z;
-    const int G    = a.Hq / a.Hkv;
-    const int hk   = h / G;
-    const int bk   = b / (a.B / a.Bk);
-    const int tid  = threadIdx.x;
-    const int wave = tid >> 6;
-    const int lane = tid & 63;
-    const int lq   = lane & 31;
-    const int hh   = lane >> 5;
-    const int my_q = qt * FA_BQ + wave * 32 + lq;
+    const int total = n_qtiles * a.Hq * a.B;
+    const int lin   = xcd_remap((int) (blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)), total);
+    const int qt    = n_qtiles - 1 - lin % n_qtiles;  // longest (causal) tiles first
+    const int h     = (lin / n_qtiles) % a.Hq;
+    const int b     = lin / (n_qtiles * a.Hq);
+    const int G     = a.Hq / a.Hkv;
+    const int hk    = h / G;
+    const int bk    = b / (a.B / a.Bk);
+    const int tid   = threadIdx.x;
+    const int wave  = tid >> 6;
+    const int lane  = tid & 63;
+    const int lq    = lane & 31;
+    const int hh    = lane >> 5;
+    const int my_q  = qt * BQ + wave * 32 + lq;
     const bool q_ok = my_q < a.nq;
 
     // Q^T operand: this lane's query, dims 16kk + 8hh + 0..7, rounded to f16
@@ -86,47 +105,68 @@ __global__ __launch_bounds__(256) void k_fa_mfma(FaArgs a, const int * __restric
     const float log2e = 1.4426950408889634f;
     const float sl2   = a.scale * log2e;
 
+    // last visible key of the tile: max over its rows of the per-row ends
     int kv_end = a.nkv;
-    if (kv_end_tab) {
-        const int plane = (b % a.mne3) * a.mne2 + (h % a.mne2);
-        kv_end          = min(kv_end, kv_end_tab[plane * n_qtiles + qt]);
+    if (row_end) {
+        __shared__ int s_end[NW];
+        const int      plane = (b % a.mne3) * a.mne2 + (h % a.mne2);
+        const int      e     = q_ok ? row_end[(int64_t) plane * a.nq + my_q] : 0;
+        const int      we    = (int) wave_max((float) e);
+        if (lane == 0) {
+            s_end[wave] = we;
+        }
+        __syncthreads();
+        int te = 0;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            te = max(te, s_end[w]);
+        }
+        kv_end = min(kv_end, te);
     }
 
     const char * kbase = a.k + hk * a.knb2 + bk * a.knb3;
     const char * vbase = a.v + hk * a.vnb2 + bk * a.vnb3;
 
+    // register stage of the next tile
+    half8_t rk[KCH], rv0[VCH], rv1[VCH];
+    auto    fetch = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < KCH; i++) {
+            const int c = tid + i * NT, key = c / (D / 8), seg = c % (D / 8), kg = k0 + key;
+            rk[i] = kg < a.nkv ? *(const half8_t *) (kbase + (int64_t) kg * a.knb1 + seg * 16) : half8_t{};
+        }
+#pragma unroll
+        for (int i = 0; i < VCH; i++) {
+            const int c = tid + i * NT, kp = c / (D / 8), seg = c % (D / 8), kg = k0 + 2 * kp;
+            rv0[i] = kg < a.nkv ? *(const half8_t *) (vbase + (int64_t) kg * a.vnb1 + seg * 16) : half8_t{};
+            rv1[i] = kg + 1 < a.nkv ? *(const half8_t *) (vbase + (int64_t) (kg + 1) * a.vnb1 + seg * 16)
+                                    : half8_t{};
+        }
+    };
+
+    if (kv_end > 0) {
+        fetch(0);
+    }
     for (int k0 = 0; k0 < kv_end; k0 += FA_BK) {
         __syncthreads();
-        // stage K rows
-        for (int c = tid; c < FA_BK * (D / 8); c += 256) {
-            const int key = c / (D / 8), seg = c % (D / 8);
-            const int kg  = k0 + key;
-            half8_t   v   = {};
-            if (kg < a.nkv) {
-                v = *(const half8_t *) (kbase + (int64_t) kg * a.knb1 + seg * 16);
-            }
-            *(half8_t *) &sK[key * KS + seg * 8] = v;
-        }
-        // stage V transposed, two keys per 32-bit LDS write
-        for (int c = tid; c < (FA_BK / 2) * (D / 8); c += 256) {
-            const int kp = c / (D / 8), seg = c % (D / 8);
-            const int key = 2 * kp;
-            const int kg  = k0 + key;
-            half8_t   v0 = {}, v1 = {};
-            if (kg < a.nkv) {
-                v0 = *(const half8_t *) (vbase + (int64_t) kg * a.vnb1 + seg * 16);
-            }
-            if (kg + 1 < a.nkv) {
-                v1 = *(const half8_t *) (vbase + (int64_t) (kg + 1) * a.vnb1 + seg * 16);
-            }
-            const int pos = vt_pos(key);
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                half2_t pr = { v0[i], v1[i] };
-                *(half2_t *) &sV[(seg * 8 + i) * VS + pos] = pr;
+        for (int i = 0; i < KCH; i++) {
+            const int c = tid + i * NT, key = c / (D / 8), seg = c % (D / 8);
+            *(half8_t *) &sK[key * KS + seg * 8] = rk[i];
+        }
+#pragma unroll
+        for (int i = 0; i < VCH; i++) {
+            const int c = tid + i * NT, kp = c / (D / 8), seg = c % (D / 8);
+            const int pos = vt_pos(2 * kp);
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                *(half2_t *) &sV[(seg * 8 + j) * VS + pos] = half2_t{ rv0[i][j], rv1[i][j] };
             }
         }
         __syncthreads();
+        if (k0 + FA_BK < kv_end) {
+            fetch(k0 + FA_BK);
+        }
 
         // S^T (64 keys x 32 queries) = K Q^T
         float16_t s[2];
@@ -175,34 +215,15 @@ __global__ __launch_bounds__(256) void k_fa_mfma(FaArgs a, const int * __restric
         }
         mx               = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
         const float mnew = fmaxf(m, mx);
-        float       alpha = 1.0f, rs = 0.0f;
-        half8_t     pb[2][2];
-        if (mnew == -INFINITY) {
-#pragma unroll
-            for (int kb = 0; kb < 2; kb++) {
-#pragma unroll
-                for (int t = 0; t < 2; t++) {
-                    pb[kb][t] = half8_t{};
-                }
-            }
-        } else {
-            alpha = __builtin_amdgcn_exp2f(m - mnew);
-#pragma unroll
-            for (int kb = 0; kb < 2; kb++) {
-#pragma unroll
-                for (int t = 0; t < 2; t++) {
-#pragma unroll
-                    for (int u = 0; u < 8; u++) {
-                        const float p = __builtin_amdgcn_exp2f(s[kb][8 * t + u] - mnew);
-                        rs += p;
-                        pb[kb][t][u] = (_Float16) p;
-                    }
-                }
-            }
-        }
-        rs = rs + __shfl_xor(rs, 32, WAVE);
-        l  = l * alpha + rs;
-        m  = mnew;
+        // No divergent control flow from here on: the MFMAs below combine the
+        // operands of all 64 lanes.  A query with nothing visible yet keeps
+        // its state (alpha = 1) and contributes p = exp2(-inf) = 0.
+        const bool  live  = mnew != -INFINITY;
+        const float mref  = live ? mnew : 0.0f;
+        const float alpha = live ? __builtin_amdgcn_exp2f(m - mnew) : 1.0f;
+        float       rs    = 0.0f;
+        l                 = l * alpha;
+        m                 = mnew;
 #pragma unroll
         for (int i = 0; i < NDB; i++) {
 #pragma unroll
@@ -210,18 +231,26 @@ __global__ __launch_bounds__(256) void k_fa_mfma(FaArgs a, const int * __restric
                 oacc[i][r] *= alpha;
             }
         }
-        // O^T (D x 32 queries) += V^T P^T
+        // P^T -> f16 B operands, then O^T (D x 32 queries) += V^T P^T
 #pragma unroll
-        for (int db = 0; db < NDB; db++) {
+        for (int kb = 0; kb < 2; kb++) {
 #pragma unroll
-            for (int kb = 0; kb < 2; kb++) {
+            for (int t = 0; t < 2; t++) {
+                half8_t pb;
 #pragma unroll
-                for (int t = 0; t < 2; t++) {
+                for (int u = 0; u < 8; u++) {
+                    const float p = __builtin_amdgcn_exp2f(s[kb][8 * t + u] - mref);
+                    rs += p;
+                    pb[u] = (_Float16) p;
+                }
+#pragma unroll
+                for (int db = 0; db < NDB; db++) {
                     const half8_t av = *(const half8_t *) &sV[(db * 32 + lq) * VS + kb * 32 + 16 * t + 8 * hh];
-                    oacc[db]         = mfma32(av, pb[kb][t], oacc[db]);
+                    oacc[db]         = mfma32(av, pb, oacc[db]);
                 }
             }
         }
+        l += rs + __shfl_xor(rs, 32, WAVE);
     }
 
     if (q_ok) {
@@ -240,69 +269,100 @@ __global__ __launch_bounds__(256) void k_fa_mfma(FaArgs a, const int * __restric
     }
 }
 
-// Mask prepass: for every mask plane (mask batch x mask head) and 128-query
-// tile, one past the last key with a finite mask value in any of the tile's
-// queries (0 if the whole tile is masked).
-__global__ __launch_bounds__(256) void k_fa_kv_end(FaArgs a, int n_qtiles, int * __restrict__ kv_end_tab) {
-    __shared__ int s_max[4];
-    const int      qt    = blockIdx.x;
-    const int      plane = blockIdx.y;
-    const int      m3    = plane / a.mne2;
-    const int      m2    = plane % a.mne2;
-    int            best  = -1;
-    const int      q_end = min(a.nq, (qt + 1) * FA_BQ);
-    for (int q = qt * FA_BQ; q < q_end; q++) {
-        const uint16_t * mr = (const uint16_t *) (a.mask + (int64_t) q * a.mnb1 + m2 * a.mnb2 + m3 * a.mnb3);
-        for (int k = a.nkv - 1 - (int) threadIdx.x; k > best; k -= 256) {
+// Mask prepass: for every mask plane (mask batch x mask head) and query row,
+// one past the last key whose mask value is not -inf (0 if the row is fully
+// masked).  One wave per row, 16-byte loads.
+__global__ __launch_bounds__(256) void k_fa_row_end(FaArgs a, int * __restrict__ row_end) {
+    const int64_t row   = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);  // plane * nq + q
+    const int     lane  = threadIdx.x & 63;
+    const int64_t nrows = (int64_t) a.nq * a.mne2 * a.mne3;
+    if (row >= nrows) {
+        return;
+    }
+    const int        q     = (int) (row % a.nq);
+    const int        plane = (int) (row / a.nq);
+    const uint16_t * mr    = (const uint16_t *) (a.mask + (int64_t) q * a.mnb1 + (plane % a.mne2) * a.mnb2 +
+                                                 (plane / a.mne2) * a.mnb3);
+    int best = -1;
+    if ((((uintptr_t) mr) & 15) == 0) {
+        const int nvec = a.nkv / 8;
+        for (int i = lane; i < nvec; i += 64) {
+            const int4_t w = *(const int4_t *) (mr + 8 * i);
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const uint32_t word = (uint32_t) w[j / 2];
+                const uint16_t hv   = (uint16_t) ((j & 1) ? (word >> 16) : (word & 0xffff));
+                if (hv != 0xfc00) {
+                    best = max(best, 8 * i + j);
+                }
+            }
+        }
+        for (int k = nvec * 8 + lane; k < a.nkv; k += 64) {
+            if (mr[k] != 0xfc00) {
+                best = max(best, k);
+            }
+        }
+    } else {
+        for (int k = lane; k < a.nkv; k += 64) {
             if (mr[k] != 0xfc00) {  // f16 -inf
                 best = max(best, k);
-                break;
             }
         }
     }
     best = (int) wave_max((float) best);
-    if ((threadIdx.x & 63) == 0) {
-        s_max[threadIdx.x >> 6] = best;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const int v = max(max(s_max[0], s_max[1]), max(s_max[2], s_max[3]));
-        kv_end_tab[plane * n_qtiles + qt] = v + 1;
+    if (lane == 0) {
+        row_end[row] = best + 1;
     }
 }
 
+// Query rows per workgroup: 256 (8 waves) for D = 128 when that still gives
+// every CU work, else 128 (4 waves).
+static int fa_mfma_waves(const FaArgs & a, int D) {
+    const int64_t tiles256 = (int64_t) ((a.nq + 255) / 256) * a.Hq * a.B;
+    return D == 128 && tiles256 >= 256 ? 8 : 4;
+}
+
 size_t fa_mfma_workspace(const FaArgs & a) {
-    const int n_qtiles = (a.nq + FA_BQ - 1) / FA_BQ;
-    return align_up((size_t) n_qtiles * a.Hq * a.B * sizeof(int), 256);
+    // per-row ends for up to Hq * B mask planes
+    return align_up((size_t) a.nq * a.Hq * a.B * sizeof(int), 256);
 }
 
 bool fa_mfma_supported(const FaArgs & a, int D) {
     return (D == 64 || D == 128) && a.nq >= 1;
 }
 
+template <int D, int NW>
+static void launch_fa_mfma(const FaArgs & a, const int * row_end, int n_qtiles, float * out, hipStream_t stream) {
+    const int64_t total = (int64_t) n_qtiles * a.Hq * a.B;
+    hipLaunchKernelGGL((k_fa_mfma<D, NW>), dim3((unsigned) total), dim3(NW * 64), 0, stream, a, row_end, n_qtiles, out);
+}
+
 int fa_mfma(const FaArgs & a, int D, float * out, void * ws, size_t ws_bytes, hipStream_t stream) {
-    const int n_qtiles = (a.nq + FA_BQ - 1) / FA_BQ;
-    if (a.Hq > 65535 || a.B > 65535) {
+    const int NW       = fa_mfma_waves(a, D);
+    const int BQ       = NW * 32;
+    const int n_qtiles = (a.nq + BQ - 1) / BQ;
+    if ((int64_t) n_qtiles * a.Hq * a.B > 0x7fffffff) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "flash_attn mfma: grid too large");
     }
-    int * kv_end = nullptr;
+    int * row_end = nullptr;
     if (a.mask) {
         const size_t need = fa_mfma_workspace(a);
         if (!ws || ws_bytes < need) {
             return set_error(MMHIP_ERR_WORKSPACE, "flash_attn mfma: workspace %zu < %zu", ws_bytes, need);
         }
-        kv_end = (int *) ws;
-        hipLaunchKernelGGL(k_fa_kv_end, dim3(n_qtiles, a.mne2 * a.mne3), dim3(256), 0, stream, a, n_qtiles, kv_end);
+        row_end             = (int *) ws;
+        const int64_t nrows = (int64_t) a.nq * a.mne2 * a.mne3;
+        hipLaunchKernelGGL(k_fa_row_end, dim3((unsigned) ((nrows + 3) / 4)), dim3(256), 0, stream, a, row_end);
         int rc = check_launch("flash_attn mask prepass");
         if (rc != MMHIP_OK) {
             return rc;
         }
     }
-    const dim3 grid(n_qtiles, a.Hq, a.B);
     if (D == 128) {
-        hipLaunchKernelGGL(k_fa_mfma<128>, grid, dim3(256), 0, stream, a, kv_end, n_qtiles, out);
+        NW == 8 ? launch_fa_mfma<128, 8>(a, row_end, n_qtiles, out, stream)
+                : launch_fa_mfma<128, 4>(a, row_end, n_qtiles, out, stream);
     } else if (D == 64) {
-        hipLaunchKernelGGL(k_fa_mfma<64>, grid, dim3(256), 0, stream, a, kv_end, n_qtiles, out);
+        launch_fa_mfma<64, 4>(a, row_end, n_qtiles, out, stream);
     } else {
         return set_error(MMHIP_ERR_UNSUPPORTED, "flash_attn mfma: head dim %d", D);
     }

@@ -3,9 +3,9 @@
 //
 //   y[m, n] = sum_k x[m, k] * deq(W)[n, k]
 //
-// Workgroup tile: 128 tokens x 128 weight rows, K step 64; 4 waves in a 2x2
-// arrangement, each computing 64 x 64 with four v_mfma_f32_32x32x16_f16
-// accumulators.  Per K step the x tile (f32) is rounded to f16 and the weight
+// Workgroup tile: 256 tokens x 256 weight rows (8 waves, each 128 x 64 with
+// eight v_mfma_f32_32x32x16_f16 accumulators) when the problem has at least
+// 256 such tiles, else 128 x 128 (4 waves, each 64 x 64); K step 64.  Per K step the x tile (f32) is rounded to f16 and the weight
 // tile is dequantised exactly as the GGUF definitions (f32, no contraction)
 // and then rounded to f16; both are stored row-major (k contiguous) in LDS,
 // which is the operand order of the MFMA A (tokens) and B (weight rows)
@@ -19,8 +19,6 @@
 
 namespace mmhip {
 
-constexpr int GM_BM = 128;
-constexpr int GM_BN = 128;
 constexpr int GM_BK = 64;
 constexpr int GM_LS = GM_BK + 8;  // LDS row stride in halves (144 bytes)
 
@@ -142,28 +140,43 @@ __device__ __forceinline__ void w_store(const WRaw & w, _Float16 * sW, const uin
     }
 }
 
-template <int WT>
-__global__ __launch_bounds__(256) void k_gemm_q(const uint8_t * __restrict__ W, int64_t N, int64_t K, int64_t rs,
-                                                 const float * __restrict__ x, int64_t ldx, int64_t M,
-                                                 float * __restrict__ y, int64_t ldy, int n_ntiles) {
-    __shared__ __attribute__((aligned(16))) _Float16 sX[GM_BM * GM_LS];
-    __shared__ __attribute__((aligned(16))) _Float16 sW[GM_BN * GM_LS];
+// Consecutive work items go to one XCD (workgroups are dealt round-robin over
+// the 8 XCDs), so the workgroups sharing an activation tile share an L2.
+__device__ __forceinline__ int64_t gm_xcd_remap(int64_t lin, int64_t total) {
+    const int64_t per = total / 8;
+    return lin >= per * 8 ? lin : (lin % 8) * per + lin / 8;
+}
 
-    // consecutive workgroups walk the token tiles of one weight tile, so a
-    // weight tile is dequantised by neighbouring workgroups while it is in L2
-    const int64_t nt   = blockIdx.x % n_ntiles;
-    const int64_t mt   = blockIdx.x / n_ntiles;
-    const int64_t m0   = mt * GM_BM;
-    const int64_t n0   = nt * GM_BN;
+// NW waves; tile BM x BN with BM = BN = 32 * NW (staging: thread t owns row
+// t / 2 of both tiles and half t % 2 of the K step); waves in a WM x (NW/WM)
+// grid, each computing MB x NB blocks of 32 x 32.
+template <int WT, int NW, int WM>
+__global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__ W, int64_t N, int64_t K, int64_t rs,
+                                                     const float * __restrict__ x, int64_t ldx, int64_t M,
+                                                     float * __restrict__ y, int64_t ldy, int64_t n_ntiles,
+                                                     int64_t n_tiles) {
+    constexpr int BM = 32 * NW;
+    constexpr int BN = 32 * NW;
+    constexpr int WN = NW / WM;
+    constexpr int MB = BM / WM / 32;
+    constexpr int NB = BN / WN / 32;
+    extern __shared__ __attribute__((aligned(16))) _Float16 g_lds[];
+    _Float16 * sX = g_lds;
+    _Float16 * sW = g_lds + BM * GM_LS;
+
+    const int64_t work = gm_xcd_remap(blockIdx.x, n_tiles);
+    const int64_t nt   = work % n_ntiles;
+    const int64_t mt   = work / n_ntiles;
+    const int64_t m0   = mt * BM;
+    const int64_t n0   = nt * BN;
     const int     tid  = threadIdx.x;
     const int     wave = tid >> 6;
     const int     lane = tid & 63;
-    const int     wm   = wave >> 1;
-    const int     wn   = wave & 1;
+    const int     wm   = wave / WN;
+    const int     wn   = wave % WN;
     const int     lq   = lane & 31;
     const int     hh   = lane >> 5;
 
-    // staging ownership: row tid/2 of each tile, half tid%2 of the K step
     const int       srow  = tid >> 1;
     const int       shalf = tid & 1;
     const int64_t   xm    = m0 + srow;
@@ -173,11 +186,11 @@ __global__ __launch_bounds__(256) void k_gemm_q(const uint8_t * __restrict__ W, 
     const bool      w_ok  = wn_ < N;
     const uint8_t * wrow  = W + (w_ok ? wn_ : 0) * rs;
 
-    float16_t acc[2][2];
+    float16_t acc[MB][NB];
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < MB; i++) {
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
+        for (int j = 0; j < NB; j++) {
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 acc[i][j][r] = 0.0f;
@@ -198,7 +211,6 @@ __global__ __launch_bounds__(256) void k_gemm_q(const uint8_t * __restrict__ W, 
     load(0);
     for (int k0 = 0; k0 < K; k0 += GM_BK) {
         __syncthreads();
-        // x tile: 32 f32 -> f16
         {
             half8_t o[4];
 #pragma unroll
@@ -227,16 +239,19 @@ __global__ __launch_bounds__(256) void k_gemm_q(const uint8_t * __restrict__ W, 
         }
 #pragma unroll
         for (int kk = 0; kk < GM_BK / 16; kk++) {
-            half8_t a[2], b[2];
+            half8_t a[MB], b[NB];
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
-                a[i] = *(const half8_t *) &sX[(wm * 64 + i * 32 + lq) * GM_LS + kk * 16 + 8 * hh];
-                b[i] = *(const half8_t *) &sW[(wn * 64 + i * 32 + lq) * GM_LS + kk * 16 + 8 * hh];
+            for (int i = 0; i < MB; i++) {
+                a[i] = *(const half8_t *) &sX[(wm * (BM / WM) + i * 32 + lq) * GM_LS + kk * 16 + 8 * hh];
             }
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
+            for (int j = 0; j < NB; j++) {
+                b[j] = *(const half8_t *) &sW[(wn * (BN / WN) + j * 32 + lq) * GM_LS + kk * 16 + 8 * hh];
+            }
 #pragma unroll
-                for (int j = 0; j < 2; j++) {
+            for (int i = 0; i < MB; i++) {
+#pragma unroll
+                for (int j = 0; j < NB; j++) {
                     acc[i][j] = gm_mfma(a[i], b[j], acc[i][j]);
                 }
             }
@@ -245,16 +260,16 @@ __global__ __launch_bounds__(256) void k_gemm_q(const uint8_t * __restrict__ W, 
 
     // C[i = token][j = weight row]: lane holds row j = lq, tokens 8(r/4) + 4hh + r%4
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < MB; i++) {
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int64_t n = n0 + wn * 64 + j * 32 + lq;
+        for (int j = 0; j < NB; j++) {
+            const int64_t n = n0 + wn * (BN / WN) + j * 32 + lq;
             if (n >= N) {
                 continue;
             }
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int64_t m = m0 + wm * 64 + i * 32 + 8 * (r / 4) + 4 * hh + (r % 4);
+                const int64_t m = m0 + wm * (BM / WM) + i * 32 + 8 * (r / 4) + 4 * hh + (r % 4);
                 if (m < M) {
                     y[m * ldy + n] = acc[i][j][r];
                 }
@@ -275,34 +290,44 @@ bool gemm_supported(int wtype, int64_t N, int64_t K, int64_t rs, const void * W,
     return rs % 16 == 0 && ((uintptr_t) W) % 16 == 0 && ((uintptr_t) x) % 16 == 0 && ldx % 4 == 0;
 }
 
+template <int NW, int WM>
+static int launch_gemm(int wtype, const uint8_t * W, int64_t N, int64_t K, int64_t rs, const float * x, int64_t ldx,
+                       int64_t M, float * y, int64_t ldy, hipStream_t stream) {
+    constexpr int BT   = 32 * NW;
+    const int64_t n_nt = (N + BT - 1) / BT;
+    const int64_t n_mt = (M + BT - 1) / BT;
+    const int64_t n    = n_nt * n_mt;
+    if (n > 0x7fffffff) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat gemm: too many tiles");
+    }
+    const size_t lds = (size_t) 2 * BT * GM_LS * sizeof(_Float16);
+    auto go = [&](auto kern) -> int {
+        if (lds > 64 * 1024 && !ensure_lds_limit((const void *) kern, lds)) {
+            return set_error(MMHIP_ERR_HIP, "mul_mat gemm: cannot raise LDS limit to %zu", lds);
+        }
+        hipLaunchKernelGGL(kern, dim3((unsigned) n), dim3(NW * 64), lds, stream, W, N, K, rs, x, ldx, M, y, ldy, n_nt,
+                           n);
+        return check_launch("mul_mat gemm");
+    };
+    switch (wtype) {
+        case TYPE_Q8_0: return go(k_gemm_q<TYPE_Q8_0, NW, WM>);
+        case TYPE_Q4_K: return go(k_gemm_q<TYPE_Q4_K, NW, WM>);
+        default: return go(k_gemm_q<TYPE_Q6_K, NW, WM>);
+    }
+}
+
 int gemm_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const float * x, int64_t ldx, int64_t M,
            float * y, int64_t ldy, hipStream_t stream) {
     if (!gemm_supported(wtype, N, K, rs, W, x, ldx)) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat gemm: type %d N=%lld K=%lld rs=%lld not supported", wtype,
                          (long long) N, (long long) K, (long long) rs);
     }
-    const int64_t n_nt = (N + GM_BN - 1) / GM_BN;
-    const int64_t n_mt = (M + GM_BM - 1) / GM_BM;
-    if (n_nt * n_mt > 0x7fffffff) {
-        return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat gemm: too many tiles");
+    const uint8_t * wb       = (const uint8_t *) W;
+    const int64_t   tiles256 = ((N + 255) / 256) * ((M + 255) / 256);
+    if (tiles256 >= 256) {
+        return launch_gemm<8, 2>(wtype, wb, N, K, rs, x, ldx, M, y, ldy, stream);
     }
-    const dim3 grid((unsigned) (n_nt * n_mt));
-    const uint8_t * wb = (const uint8_t *) W;
-    switch (wtype) {
-        case TYPE_Q8_0:
-            hipLaunchKernelGGL(k_gemm_q<TYPE_Q8_0>, grid, dim3(256), 0, stream, wb, N, K, rs, x, ldx, M, y, ldy,
-                               (int) n_nt);
-            break;
-        case TYPE_Q4_K:
-            hipLaunchKernelGGL(k_gemm_q<TYPE_Q4_K>, grid, dim3(256), 0, stream, wb, N, K, rs, x, ldx, M, y, ldy,
-                               (int) n_nt);
-            break;
-        default:
-            hipLaunchKernelGGL(k_gemm_q<TYPE_Q6_K>, grid, dim3(256), 0, stream, wb, N, K, rs, x, ldx, M, y, ldy,
-                               (int) n_nt);
-            break;
-    }
-    return check_launch("mul_mat gemm");
+    return launch_gemm<4, 2>(wtype, wb, N, K, rs, x, ldx, M, y, ldy, stream);
 }
 
 }  // namespace mmhip

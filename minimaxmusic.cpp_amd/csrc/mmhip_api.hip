@@ -4,6 +4,9 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+#include <unordered_map>
+
 #include "k_fa_common.h"
 #include "mmhip_device.h"
 #include "mmhip_internal.h"
@@ -22,6 +25,22 @@ int set_error(int code, const char * fmt, ...) {
     vsnprintf(g_err, sizeof(g_err), fmt, ap);
     va_end(ap);
     return code;
+}
+
+bool ensure_lds_limit(const void * kernel, size_t bytes) {
+    static std::mutex                               mu;
+    static std::unordered_map<const void *, size_t> raised;
+    std::lock_guard<std::mutex>                     lock(mu);
+    auto                                            it = raised.find(kernel);
+    if (it != raised.end() && it->second >= bytes) {
+        return true;
+    }
+    if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int) bytes) != hipSuccess) {
+        (void) hipGetLastError();
+        return false;
+    }
+    raised[kernel] = bytes;
+    return true;
 }
 
 int check_launch(const char * what) {

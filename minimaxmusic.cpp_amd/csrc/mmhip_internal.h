@@ -12,6 +12,10 @@
 namespace mmhip {
 
 int  set_error(int code, const char * fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Opt a kernel in to `bytes` of dynamic LDS (above the 64 KiB default) once
+// per process; thread-safe.  Returns false if the runtime refuses.
+bool ensure_lds_limit(const void * kernel, size_t bytes);
 int  check_launch(const char * what);
 void clear_error();
 
