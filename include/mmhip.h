@@ -104,6 +104,41 @@ size_t mmhip_flash_attn_workspace(const mmhip_view * q, const mmhip_view * k, co
 int    mmhip_flash_attn_ext(const mmhip_view * q, const mmhip_view * k, const mmhip_view * v, const mmhip_view * mask,
                             float scale, float * out, void * ws, size_t ws_bytes, void * stream);
 
+/* ---------------------------------------------------------------------
+ * Decode-step glue ops (the nodes between the hot-path ops in the LM
+ * batched decode graph, src/qwen3-lm.h:730-859).  Operands are ggml views;
+ * `dst` outputs are contiguous f32 unless a view is given.  A view passed as
+ * destination is written through its (non-const) data pointer.
+ * ------------------------------------------------------------------- */
+/* GGML_OP_ADD / SUB / MUL (op 0 / 1 / 2), b broadcast over a:
+ * residual adds src/qwen3-lm.h:827, :836; norm-weight MUL src/qwen3-enc.h:92. */
+int mmhip_binary(int op, const mmhip_view * a, const mmhip_view * b, float * dst, void * stream);
+/* GGML_OP_RMS_NORM over dim 0, optionally fused with the following MUL by w:
+ * qwen3_rms_norm src/qwen3-enc.h:87-93, qk-norm src/qwen3-lm.h:765-768. */
+int mmhip_rms_norm(const mmhip_view * x, const mmhip_view * w, float eps, float * dst, void * stream);
+/* GGML_OP_ROPE, NeoX mode (2), freq_scale 1, ext_factor 0, attn_factor 1:
+ * src/qwen3-lm.h:771-772, src/dit.h:206-209 (partial, n_dims < head_dim).
+ * x [head_dim, heads, tokens, B], pos int32 [tokens]; theta_scale =
+ * powf(freq_base, -2/n_dims) computed by the caller. */
+int mmhip_rope_neox(const mmhip_view * x, const int32_t * pos, int n_dims, float theta_scale, float * dst,
+                    void * stream);
+/* GGML_OP_CPY / GGML_OP_CONT between f32 and f16 views of equal element count:
+ * src/qwen3-lm.h:775-777, src/dit.h:219-220 (f32 -> f16 cast). */
+int mmhip_cpy(const mmhip_view * src, int src_type, const mmhip_view * dst, int dst_type, void * stream);
+/* GGML_OP_GET_ROWS (ids int32 [n, ne1, ne2]) from f32, f16 or quantized
+ * (row-grouped) rows: embedding lookup src/qwen3-lm.h:730. */
+int mmhip_get_rows(int src_type, const mmhip_view * src, const mmhip_view * ids, float * dst, void * stream);
+/* GGML_OP_SET_ROWS: f32 rows into an f16 / f32 destination at int32 / int64
+ * row ids (ids_type 26 / 27), broadcast over dims 2-3: KV-cache write
+ * src/qwen3-lm.h:803-804, :420-421. */
+int mmhip_set_rows(const mmhip_view * src, const mmhip_view * ids, int ids_type, const mmhip_view * dst,
+                   int dst_type, void * stream);
+/* GGML_OP_GLU SwiGLU: fused halves (b NULL; src/qwen3-enc.h:108) or split
+ * (src/dit.h:242). */
+int mmhip_swiglu(const mmhip_view * a, const mmhip_view * b, int swapped, float * dst, void * stream);
+/* GGML_OP_SCALE: dst = a * s + bias (src/depth-decoder.h:355). */
+int mmhip_scale(const mmhip_view * a, float s, float bias, float * dst, void * stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -2,9 +2,11 @@
 
     python -m build  (from this directory)   or   build.build_all()
 
-Compiles every csrc/*.hip with hipcc for gfx950 into _build/, links
-lib/libmmhip.so (the kernel C-ABI, include/mmhip.h) in-tree so that it
-travels with the source tree.
+Compiles the HIP sources with hipcc for gfx950 (and the host-only ggml core
+with clang++) into _build/ and links, in-tree under lib/:
+  libmmhip.so        the kernel C-ABI (include/mmhip.h)
+  libggml-base.so    the restated ggml-base subset (ggml/include/*.h)
+  libggml-mi355x.so  the MI355X ggml backend (include/ggml-mi355x.h)
 """
 import concurrent.futures as cf
 import os
@@ -20,7 +22,9 @@ BUILD = PKG / "_build"
 LIB = PKG / "lib"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+CLANGXX = os.environ.get("CLANGXX", "/opt/rocm/llvm/bin/clang++")
 ARCH = "gfx950"
+GGML_INC = PKG / "ggml" / "include"
 
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
@@ -33,48 +37,65 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{ROOT / 'include'}",
     f"-I{CSRC}",
+    f"-I{GGML_INC}",
 ]
 
-LIBS = {
-    "libmmhip.so": ["k_quant.hip", "k_gemv.hip", "k_gemm.hip", "k_fa_decode.hip", "k_fa_mfma.hip", "mmhip_api.hip"],
-}
+HOST_FLAGS = ["-O2", "-fPIC", "-std=c++17", "-Wall", f"-I{GGML_INC}", f"-I{ROOT / 'include'}"]
+
+# (library, compiler, sources, link flags)
+LIBS = [
+    ("libmmhip.so", "hip",
+     ["csrc/k_quant.hip", "csrc/k_gemv.hip", "csrc/k_gemm.hip", "csrc/k_fa_decode.hip", "csrc/k_fa_mfma.hip",
+      "csrc/k_glue.hip", "csrc/mmhip_api.hip"], []),
+    # stand-in for libggml-base (ggml is not vendored by the reference)
+    ("libggml-base.so", "host", ["ggml/src/ggml_core.cpp"], ["-ldl"]),
+    # the MI355X ggml backend, on top of the two above
+    ("libggml-mi355x.so", "hip", ["csrc/ggml-mi355x.cpp"],
+     ["-L{lib}", "-lmmhip", "-lggml-base", "-Wl,-rpath,$ORIGIN"]),
+]
 
 
-def _compile(src: pathlib.Path, obj: pathlib.Path, verbose: bool) -> None:
-    cmd = [HIPCC, *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+def _run(cmd, what, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     errs = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l)
     if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed on {src.name}:\n{errs}")
+        raise RuntimeError(f"{what} failed:\n{errs}")
     if errs.strip() and verbose:
         print(errs, file=sys.stderr)
+
+
+def _compile(kind, src, obj, verbose):
+    if kind == "hip":
+        cmd = [HIPCC, *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+    else:
+        cmd = [CLANGXX, *HOST_FLAGS, "-c", str(src), "-o", str(obj)]
+    _run(cmd, f"compile {src.name}", verbose)
 
 
 def build_all(verbose: bool = False, jobs: int = 8) -> list:
     BUILD.mkdir(exist_ok=True)
     LIB.mkdir(exist_ok=True)
+    jobs_list = []
+    for lib, kind, srcs, _ in LIBS:
+        for s in srcs:
+            src = PKG / s
+            jobs_list.append((kind, src, BUILD / (src.stem + ".o")))
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        for f in [ex.submit(_compile, k, s, o, verbose) for k, s, o in jobs_list]:
+            f.result()
     built = []
-    for lib, srcs in LIBS.items():
-        objs = []
-        with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-            futs = []
-            for s in srcs:
-                src = CSRC / s
-                obj = BUILD / (src.stem + ".o")
-                objs.append(obj)
-                futs.append(ex.submit(_compile, src, obj, verbose))
-            for f in futs:
-                f.result()
+    for lib, kind, srcs, ldflags in LIBS:
+        objs = [str(BUILD / (pathlib.Path(s).stem + ".o")) for s in srcs]
         out = LIB / lib
         tmp = LIB / (lib + ".tmp")
-        cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
-        if verbose:
-            print(" ".join(cmd), flush=True)
-        r = subprocess.run(cmd, capture_output=True, text=True)
-        if r.returncode != 0:
-            raise RuntimeError(f"link of {lib} failed:\n{r.stderr}")
+        flags = [f.replace("{lib}", str(LIB)) for f in ldflags]
+        if kind == "hip":
+            cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp), *flags]
+        else:
+            cmd = [CLANGXX, "-shared", "-fPIC", *objs, "-o", str(tmp), *flags]
+        _run(cmd, f"link {lib}", verbose)
         os.replace(tmp, out)
         built.append(out)
     return built
