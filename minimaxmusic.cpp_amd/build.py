@@ -7,6 +7,7 @@ with clang++) into _build/ and links, in-tree under lib/:
   libmmhip.so        the kernel C-ABI (include/mmhip.h)
   libggml-base.so    the restated ggml-base subset (ggml/include/*.h)
   libggml-mi355x.so  the MI355X ggml backend (include/ggml-mi355x.h)
+  libmm_lm.so        the LM batched decode step on that backend (include/mm_lm.h)
 """
 import concurrent.futures as cf
 import os
@@ -46,12 +47,15 @@ HOST_FLAGS = ["-O2", "-fPIC", "-std=c++17", "-Wall", f"-I{GGML_INC}", f"-I{ROOT 
 LIBS = [
     ("libmmhip.so", "hip",
      ["csrc/k_quant.hip", "csrc/k_gemv.hip", "csrc/k_gemm.hip", "csrc/k_fa_decode.hip", "csrc/k_fa_mfma.hip",
-      "csrc/k_glue.hip", "csrc/mmhip_api.hip"], []),
+      "csrc/k_glue.hip", "csrc/k_synth.hip", "csrc/mmhip_api.hip"], []),
     # stand-in for libggml-base (ggml is not vendored by the reference)
     ("libggml-base.so", "host", ["ggml/src/ggml_core.cpp"], ["-ldl"]),
     # the MI355X ggml backend, on top of the two above
     ("libggml-mi355x.so", "hip", ["csrc/ggml-mi355x.cpp"],
      ["-L{lib}", "-lmmhip", "-lggml-base", "-Wl,-rpath,$ORIGIN"]),
+    # Qwen3-shape LM batched decode step built with the ggml API (include/mm_lm.h)
+    ("libmm_lm.so", "hip", ["csrc/mm_lm.cpp"],
+     ["-L{lib}", "-lggml-mi355x", "-lggml-base", "-lmmhip", "-Wl,-rpath,$ORIGIN"]),
 ]
 
 
