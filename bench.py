@@ -38,7 +38,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="gemv_q8_0",
-                    choices=["gemv_q8_0", "fa_decode", "fa_prefill", "fa_dit", "gemm_q4_k"])
+                    choices=["lm_decode", "gemv_q8_0", "fa_decode", "fa_prefill", "fa_dit", "gemm_q4_k"])
+    ap.add_argument("--wtype", default="q8_0", choices=["q8_0", "q6_k"], help="lm_decode weight type")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     return ap.parse_args()
@@ -355,6 +356,119 @@ def bench_gemm(args, torch, pkg):
     }
 
 
+# Algorithmic HBM bytes of one Qwen3-8B-shape CFG decode step at KV 4096:
+# weights + KV read + norm weights + logits + KV write (per step, both rows).
+def lm_step_bytes(cfg, wtype):
+    be, bb = {8: (32, 34), 14: (256, 210), 12: (256, 144)}[wtype]
+    H, D, Nh, Nkv, F, V, L = (cfg["hidden"], cfg["head_dim"], cfg["n_heads"], cfg["n_kv_heads"], cfg["ffn"],
+                              cfg["vocab"], cfg["n_layers"])
+    per_layer_w = H * (Nh * D + 2 * Nkv * D) + Nh * D * H + H * 2 * F + F * H
+    weights = (per_layer_w * L + H * V) * bb // be
+    kv_len, sets = 4096, 2
+    kv_read = L * 2 * sets * Nkv * kv_len * D * 2
+    norms = (L * (2 * H + 2 * D) + H) * 4
+    logits = sets * V * 4
+    kv_write = L * 2 * sets * Nkv * D * 2
+    return weights + kv_read + norms + logits + kv_write
+
+
+def bench_lm(args, torch, pkg):
+    import importlib
+
+    lm_mod = importlib.import_module(pkg.__name__ + ".lm")
+    cfg = dict(lm_mod.QWEN3_8B)
+    cfg["wtype"] = 8 if args.wtype == "q8_0" else 14
+    lm = lm_mod.Lm(seed=1005, **cfg)
+    lm.fill_kv(0, 4095, seed=1)
+    lm.fill_kv(1, 4095, seed=2)
+    emb = np.random.default_rng(1005).standard_normal((2, cfg["hidden"])).astype(np.float32)
+
+    def step():
+        # every step attends over KV 4096 (positions reset to 4095)
+        lm.set_pos(0, 4095)
+        lm.set_pos(1, 4095)
+        lm.decode_device(emb, [0, 1])
+
+    for _ in range(max(args.warmup, 3)):
+        step()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    dt = (time.perf_counter() - t0) / args.steps
+    step_bytes = lm_step_bytes(cfg, cfg["wtype"])
+    achieved = step_bytes / dt / 1e9
+    replays, eager = lm.graph_stats()
+    nodes = lm.graph_nodes()
+    lm.close()
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_lm(args, lm_mod, cfg)
+    return {
+        "metric": "LM decode tok/s (CFG B=2, %s, KV 4096)" % args.wtype.upper(),
+        "value": round(2.0 / dt, 2),
+        "unit": "tok/s",
+        "ms_per_step": round(dt * 1e3, 4),
+        "dtype": args.wtype + " weights (int8-dot GEMV), f16 KV, f32 activations",
+        "config": {"workload": "Qwen3-8B-shape batched CFG decode step: 36 layers, hidden 4096, 32q/8kv d128, "
+                               "FFN 12288 SwiGLU, vocab 151936, KV 4096 x 2 sets",
+                   "weights": args.wtype, "graph_nodes": nodes, "graph_replays": replays, "eager_runs": eager,
+                   "tokens_per_step": 2},
+        "roofline": {"bound": "hbm", "kernel": "whole decode step (HIP-graph replay of %d ggml nodes)" % nodes,
+                     "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "alg_bytes_per_step": step_bytes,
+                     "step_us": round(dt * 1e6, 2), "traffic": None},
+        "cpu_baseline": cpu,
+    }
+
+
+def cpu_lm(args, lm_mod, cfg):
+    """One decoder layer and the lm_head at the full shape through the
+    ggml-CPU-semantics restatement, extrapolated to 36 layers."""
+    import oracle
+
+    sys.path.insert(0, str(ROOT / "tests"))
+    n_thr = os.cpu_count() or 1
+    H, D, Nh, Nkv, F, V = cfg["hidden"], cfg["head_dim"], cfg["n_heads"], cfg["n_kv_heads"], cfg["ffn"], cfg["vocab"]
+    t = cfg["wtype"]
+    rng = np.random.default_rng(7)
+    import importlib
+
+    synth = importlib.import_module(lm_mod.__name__.rsplit(".", 1)[0] + ".synth")
+    W = {n: synth.gguf_blocks_np(t, r, k, 50 + i) for i, (n, r, k) in enumerate(
+        [("qkv", Nh * D + 2 * Nkv * D, H), ("o", H, Nh * D), ("gu", 2 * F, H), ("down", H, F)])}
+    kc = rng.standard_normal((2, Nkv, 4096, D)).astype(np.float16)
+    vc = rng.standard_normal((2, Nkv, 4096, D)).astype(np.float16)
+    x = rng.standard_normal((2, H)).astype(np.float32)
+    wn = np.ones(H, np.float32)
+
+    def layer():
+        h = oracle.rms_norm_mul(x, wn, 1e-6)
+        qkv = oracle.mul_mat_ggml(t, W["qkv"], Nh * D + 2 * Nkv * D, H, h, nthreads=n_thr)
+        q = oracle.rope_neox(qkv[:, :Nh * D].reshape(2, Nh, D), np.array([4095, 4095], np.int32), D, 1e6)
+        o = oracle.flash_attn_ext(np.ascontiguousarray(q[:, :, None]), kc, vc, None, 1 / np.sqrt(D), "ggml",
+                                  nthreads=n_thr).reshape(2, Nh * D)
+        h2 = x + oracle.mul_mat_ggml(t, W["o"], H, Nh * D, np.asarray(o, np.float32), nthreads=n_thr)
+        gu = oracle.mul_mat_ggml(t, W["gu"], 2 * F, H, oracle.rms_norm_mul(h2, wn, 1e-6), nthreads=n_thr)
+        return h2 + oracle.mul_mat_ggml(t, W["down"], H, F, oracle.swiglu(gu), nthreads=n_thr)
+
+    t0 = time.perf_counter()
+    it = 0
+    while time.perf_counter() - t0 < args.cpu_seconds or it == 0:
+        layer()
+        it += 1
+    t_layer = (time.perf_counter() - t0) / it
+    rows = 8192  # lm_head sample: 8192 of the 151936 vocab rows
+    Wl = synth.gguf_blocks_np(t, rows, H, 99)
+    t0 = time.perf_counter()
+    oracle.mul_mat_ggml(t, Wl, rows, H, x, nthreads=n_thr)
+    t_head = (time.perf_counter() - t0) * V / rows
+    step = 36 * t_layer + t_head
+    return {"value": round(2.0 / step, 4), "unit": "tok/s", "cores": n_thr, "kind": "port",
+            "sample": f"ggml-CPU-semantics restatement (oracle/): {it} full-shape decoder layer(s) at KV 4096 "
+                      f"({t_layer * 1e3:.0f} ms each) and an 8192-row lm_head slice, extrapolated to 36 layers + "
+                      f"the 151936-row lm_head ({step:.2f} s per 2-token step)"}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -367,6 +481,7 @@ def main():
     pkg = __graft_entry__.load_package()
     pkg.mmhip.load()
     res = {
+        "lm_decode": lambda: bench_lm(args, torch, pkg),
         "gemv_q8_0": lambda: bench_gemv(args, torch, pkg),
         "fa_decode": lambda: bench_fa(args, torch, pkg),
         "fa_prefill": lambda: bench_fa_mfma(args, torch, pkg, True),

@@ -86,6 +86,11 @@ size_t mmhip_act_bytes(int type, int64_t K, int64_t M);
 int    mmhip_quantize_act(int type, const float * x, int64_t ldx, int64_t K, int64_t M, void * xq, void * stream);
 int    mmhip_mul_mat_q(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const void * xq, int64_t M,
                        float * y, int64_t ldy, void * stream);
+/* The GEMV with the residual GGML_OP_ADD that follows the output projections
+ * fused into its store: y[m*ldy + n] = mul_mat + r[m*ldr + n] (attention out
+ * src/qwen3-lm.h:826-828, MLP down src/qwen3-lm.h:835-836); r may alias y. */
+int    mmhip_mul_mat_q_add(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const void * xq,
+                           int64_t M, const float * r, int64_t ldr, float * y, int64_t ldy, void * stream);
 
 /* ---------------------------------------------------------------------
  * GGML_OP_FLASH_ATTN_EXT, replacing the ggml backend kernel behind
@@ -116,6 +121,48 @@ int mmhip_binary(int op, const mmhip_view * a, const mmhip_view * b, float * dst
 /* GGML_OP_RMS_NORM over dim 0, optionally fused with the following MUL by w:
  * qwen3_rms_norm src/qwen3-enc.h:87-93, qk-norm src/qwen3-lm.h:765-768. */
 int mmhip_rms_norm(const mmhip_view * x, const mmhip_view * w, float eps, float * dst, void * stream);
+/* The same RMS_NORM (+ MUL by w) with the normalised rows also quantised into
+ * the activation layout of mmhip_mul_mat_q for weights of `type` (the
+ * GEMV consuming the norm: QKV src/qwen3-lm.h:742-747, gate_up
+ * src/qwen3-enc.h:106-108, lm_head src/qwen3-lm.h:856), saving the separate
+ * quantisation pass.  dst may be NULL when the f32 rows are not needed.
+ * Rows must be contiguous with ne0 % 256 == 0. */
+int mmhip_rms_norm_quant(const mmhip_view * x, const mmhip_view * w, float eps, float * dst, int type, void * xq,
+                         void * stream);
+/* Per-head post-processing of the fused QKV projection in one launch: the
+ * node chain CONT(view of qkv) -> RESHAPE [D, H, T] -> [RMS_NORM -> MUL(w)]
+ * -> [ROPE NeoX] -> [CONT] -> [RESHAPE [D, 1, H, T] -> SET_ROWS] of the
+ * attention block (src/qwen3-lm.h:744-804 batched decode, src/qwen3-lm.h:
+ * 371-421 prefill).  Row (h, t) of D f32 elements is read at
+ * src + h*src_nb_h + t*src_nb_t.  norm != 0: RMS_NORM over D with eps, then
+ * times norm_w[D] when non-NULL.  pos != NULL: NeoX RoPE over all D dims at
+ * position pos[t], theta_i = pos * theta_scale^i.  ids == NULL: written as
+ * contiguous f32 dst[T][H][D]; else written as SET_ROWS into the dst view:
+ * row r = ids[(h % ids_ne1)*ids_nb1 + (t % ids_ne2)*ids_nb2] (i32 type 26 or
+ * i64 type 27) at dst + r*dst_nb1 + h*dst_nb2 + t*dst_nb3, as f32 or f16. */
+typedef struct {
+    const void *    src;
+    int64_t         src_nb_h, src_nb_t;
+    int             D, H, T;
+    int             norm;
+    const float *   norm_w;
+    float           eps;
+    const int32_t * pos;
+    float           theta_scale;
+    void *          dst;
+    int             dst_type;
+    const void *    ids;
+    int             ids_type;
+    int64_t         ids_nb1, ids_nb2, ids_ne1, ids_ne2;
+    int64_t         dst_nb1, dst_nb2, dst_nb3;
+} mmhip_head_rows_args;
+int mmhip_head_rows(const mmhip_head_rows_args * args, void * stream);
+/* GGML_OP_GLU SwiGLU (as mmhip_swiglu) with the result also quantised into
+ * the activation layout of mmhip_mul_mat_q for weights of `type` (the down
+ * projection, src/qwen3-enc.h:108-110).  dst may be NULL.  Rows contiguous,
+ * output width % 256 == 0. */
+int mmhip_swiglu_quant(const mmhip_view * a, const mmhip_view * b, int swapped, float * dst, int type, void * xq,
+                       void * stream);
 /* GGML_OP_ROPE, NeoX mode (2), freq_scale 1, ext_factor 0, attn_factor 1:
  * src/qwen3-lm.h:771-772, src/dit.h:206-209 (partial, n_dims < head_dim).
  * x [head_dim, heads, tokens, B], pos int32 [tokens]; theta_scale =

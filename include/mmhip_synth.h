@@ -9,7 +9,7 @@
  *   Q8_0: quants uniform in [-127, 127]; d = f16(|N(0, 0.02)| / 127)
  *   Q4_K: quant and 6-bit scale/min bytes uniform; d, dmin = f16(|N(0, 0.02)|)
  *   Q6_K: ql/qh bytes uniform; int8 scales uniform in [-64, 63];
- *         d = f16(|N(0, 0.02)| / 64)
+ *         d = f16(|N(0, 0.02)| / 1024)  (|w| ~ 0.01 like real weights)
  */
 #ifndef MMHIP_SYNTH_H
 #define MMHIP_SYNTH_H

@@ -304,6 +304,8 @@ struct mi_backend {
     hipStream_t    stream = nullptr;
     void *         ws     = nullptr;
     size_t         ws_size = 0;
+    void *         slot      = nullptr;  // quantised activation slots of the execution plan
+    size_t         slot_size = 0;
     bool           capturing = false;
     bool           use_graphs = true;
     mi_graph_cache cache;
@@ -323,6 +325,9 @@ void be_free(ggml_backend_t b) {
     }
     if (c->ws) {
         (void) hipFree(c->ws);
+    }
+    if (c->slot) {
+        (void) hipFree(c->slot);
     }
     (void) hipStreamDestroy(c->stream);
     delete c;
@@ -497,21 +502,20 @@ bool run_fa(mi_backend * c, const struct ggml_tensor * n) {
     return rc == MMHIP_OK || fail(n, rc);
 }
 
-int run_node(mi_backend * c, struct ggml_cgraph * g, int i, const std::vector<int> & uses) {
-    struct ggml_tensor * n = ggml_graph_node(g, i);
-    hipStream_t          s = c->stream;
-    int                  rc = MMHIP_OK;
+int run_node(mi_backend * c, const struct ggml_tensor * n) {
+    hipStream_t s  = c->stream;
+    int         rc = MMHIP_OK;
     switch (n->op) {
         case GGML_OP_NONE:
         case GGML_OP_RESHAPE:
         case GGML_OP_VIEW:
         case GGML_OP_PERMUTE:
         case GGML_OP_TRANSPOSE:
-            return 1;
+            return MMHIP_OK;
         case GGML_OP_MUL_MAT:
-            return run_mul_mat(c, n) ? 1 : -1;
+            return run_mul_mat(c, n) ? MMHIP_OK : -1;
         case GGML_OP_FLASH_ATTN_EXT:
-            return run_fa(c, n) ? 1 : -1;
+            return run_fa(c, n) ? MMHIP_OK : -1;
         case GGML_OP_ADD:
         case GGML_OP_SUB:
         case GGML_OP_MUL: {
@@ -523,18 +527,7 @@ int run_node(mi_backend * c, struct ggml_cgraph * g, int i, const std::vector<in
             float eps;
             memcpy(&eps, &n->op_params[0], sizeof(float));
             mmhip_view x = view_of(n->src[0]);
-            // fuse with the next node when it multiplies this result (only use)
-            if (i + 1 < ggml_graph_n_nodes(g)) {
-                struct ggml_tensor * nx = ggml_graph_node(g, i + 1);
-                if (nx->op == GGML_OP_MUL && nx->src[0] == n && uses[i] == 1 &&
-                    !(n->flags & GGML_TENSOR_FLAG_OUTPUT) && nx->src[1]->type == GGML_TYPE_F32 &&
-                    ggml_are_same_shape(nx, n)) {
-                    mmhip_view w = view_of(nx->src[1]);
-                    rc           = mmhip_rms_norm(&x, &w, eps, (float *) nx->data, s);
-                    return rc == MMHIP_OK ? 2 : (fail(n, rc), -1);
-                }
-            }
-            rc = mmhip_rms_norm(&x, nullptr, eps, (float *) n->data, s);
+            rc           = mmhip_rms_norm(&x, nullptr, eps, (float *) n->data, s);
             break;
         }
         case GGML_OP_ROPE: {
@@ -583,32 +576,486 @@ int run_node(mi_backend * c, struct ggml_cgraph * g, int i, const std::vector<in
             MI_LOG("unsupported node %s (%s)\n", n->name, ggml_op_name(n->op));
             return -1;
     }
-    return rc == MMHIP_OK ? 1 : (fail(n, rc), -1);
+    return rc == MMHIP_OK ? MMHIP_OK : (fail(n, rc), -1);
 }
 
-bool run_graph(mi_backend * c, struct ggml_cgraph * g) {
-    const int                                     nn = ggml_graph_n_nodes(g);
-    std::vector<int>                              uses(nn, 0);
+// ---- execution plan ----
+//
+// The graph's nodes in order, with these chains fused into single steps.
+// A fused step runs at the position of the chain's last node, so every input
+// it reads has been produced; the chain's other nodes must have exactly one
+// consumer (the next chain node) and not be graph outputs.
+//   NORM      RMS_NORM -> MUL(w): one row kernel; when every consumer is a
+//             GEMV MUL_MAT of one activation type, the rows are also
+//             quantised into an activation slot those MUL_MATs read.
+//   SWIGLU_Q  GLU SwiGLU whose consumers are GEMV MUL_MATs: quantised into a
+//             slot as well.
+//   HEAD      CONT(view) -> RESHAPE -> [RMS_NORM -> MUL] -> [ROPE] -> [CONT]
+//             -> [RESHAPE -> SET_ROWS]: the per-head Q / K / V rows of the
+//             attention block in one launch.
+//   MM_ADD    a GEMV MUL_MAT whose only consumer is an ADD with a same-shape
+//             residual: the ADD is done in the GEMV's store.
+// MUL_MATs reading a slot skip their activation quantisation.
+
+enum step_kind { ST_NODE, ST_NORM, ST_SWIGLU_Q, ST_HEAD, ST_MM };
+
+struct plan_step {
+    int                  kind = ST_NODE;
+    int                  node = -1;      // node executed / whose output is written
+    int                  src  = -1;      // NORM: the RMS_NORM node
+    int                  add  = -1;      // MM: the fused ADD node
+    int                  add_res = -1;   // MM: index 0/1 of the ADD's residual source
+    int64_t              slot_out = -1;  // byte offset of the quantised slot written (NORM / SWIGLU_Q)
+    int64_t              slot_in  = -1;  // byte offset of the slot read (MM)
+    int                  vec_wtype = 0;  // weight type the slot is quantised for
+    bool                 write_f32 = true;
+    mmhip_head_rows_args head{};
+};
+
+struct graph_info {
+    int                                          nn = 0;
+    std::vector<int>                             uses;
+    std::vector<int>                             cons;  // last consumer (the only one when uses == 1)
+    std::vector<std::vector<int>>                consumers;
     std::unordered_map<const ggml_tensor *, int> index;
-    index.reserve((size_t) nn * 2);
-    for (int i = 0; i < nn; i++) {
+};
+
+bool is_output(const struct ggml_tensor * t) {
+    return (t->flags & GGML_TENSOR_FLAG_OUTPUT) != 0;
+}
+
+// node index of t, or -1 for leafs / tensors outside the graph
+int node_index(const graph_info & gi, const struct ggml_tensor * t) {
+    auto it = gi.index.find(t);
+    return it == gi.index.end() ? -1 : it->second;
+}
+
+// Would mmhip_mul_mat run this MUL_MAT as an activation-quantised GEMV?
+bool mm_is_gemv(const struct ggml_tensor * n) {
+    const struct ggml_tensor * x = n->src[1];
+    const int64_t              M = x->ne[1] * x->ne[2] * x->ne[3];
+    return n->op == GGML_OP_MUL_MAT && M >= 1 && M <= 8 && mmhip_act_bytes(n->src[0]->type, n->src[0]->ne[0], M) > 0;
+}
+
+int act_vec_type(int wtype) {
+    return wtype == GGML_TYPE_Q8_0 ? GGML_TYPE_Q8_0 : GGML_TYPE_Q8_K;
+}
+
+// All consumers of node p are GEMV MUL_MATs reading p as src1 with weights
+// of one activation type; returns that weight type (0 if not).
+int gemv_consumer_type(struct ggml_cgraph * g, const graph_info & gi, int p) {
+    if (gi.consumers[(size_t) p].empty()) {
+        return 0;
+    }
+    int wt = 0;
+    for (int ci : gi.consumers[(size_t) p]) {
+        const struct ggml_tensor * m = ggml_graph_node(g, ci);
+        if (m->op != GGML_OP_MUL_MAT || m->src[1] != ggml_graph_node(g, p) || m->src[0] == m->src[1] ||
+            !mm_is_gemv(m)) {
+            return 0;
+        }
+        if (wt && act_vec_type(wt) != act_vec_type(m->src[0]->type)) {
+            return 0;
+        }
+        wt = m->src[0]->type;
+    }
+    return wt;
+}
+
+bool is_f32_vector(const struct ggml_tensor * w, int64_t n) {
+    return w->type == GGML_TYPE_F32 && w->ne[0] == n && w->ne[1] == 1 && w->ne[2] == 1 && w->ne[3] == 1 &&
+           w->nb[0] == sizeof(float);
+}
+
+bool rows_contiguous_f32(const struct ggml_tensor * t) {
+    return t->type == GGML_TYPE_F32 && ggml_is_contiguous(t) && ((uintptr_t) t->data) % 16 == 0;
+}
+
+// Try the HEAD chain starting at CONT node i; fills st and marks absorbed nodes.
+bool plan_head(struct ggml_cgraph * g, const graph_info & gi, int i, plan_step & st, std::vector<char> & absorbed) {
+    const struct ggml_tensor * n0 = ggml_graph_node(g, i);
+    const struct ggml_tensor * v  = n0->src[0];
+    if (n0->op != GGML_OP_CONT || n0->type != GGML_TYPE_F32 || v->type != GGML_TYPE_F32 || v->nb[0] != 4 ||
+        v->ne[2] != 1 || v->ne[3] != 1 || v->nb[1] % 4 != 0) {
+        return false;
+    }
+    std::vector<int> chain{ i };
+    auto             next = [&](int k) -> int {
+        if (gi.uses[(size_t) k] != 1 || is_output(ggml_graph_node(g, k))) {
+            return -1;
+        }
+        return gi.cons[(size_t) k];
+    };
+    int j = next(i);
+    if (j < 0) {
+        return false;
+    }
+    const struct ggml_tensor * r1 = ggml_graph_node(g, j);
+    const int64_t              D  = r1->ne[0], H = r1->ne[1], T = r1->ne[2];
+    if (r1->op != GGML_OP_RESHAPE || r1->src[0] != n0 || r1->ne[3] != 1 || D * H != v->ne[0] || T != v->ne[1] ||
+        !(D == 64 || D == 128 || D == 256)) {
+        return false;
+    }
+    chain.push_back(j);
+    mmhip_head_rows_args a{};
+    a.src      = v->data;
+    a.src_nb_h = D * 4;
+    a.src_nb_t = (int64_t) v->nb[1];
+    a.D        = (int) D;
+    a.H        = (int) H;
+    a.T        = (int) T;
+    a.dst_type = 0;
+    int cur    = j;  // last node of the chain so far
+    int end    = -1;
+    auto input_ok = [&](const struct ggml_tensor * t) { return node_index(gi, t) < i; };
+
+    int k = next(cur);
+    if (k >= 0 && ggml_graph_node(g, k)->op == GGML_OP_RMS_NORM && ggml_graph_node(g, k)->src[0] ==
+                                                                         ggml_graph_node(g, cur)) {
+        memcpy(&a.eps, &ggml_graph_node(g, k)->op_params[0], sizeof(float));
+        a.norm = 1;
+        chain.push_back(k);
+        cur = end = k;
+        k         = next(cur);
+        if (k >= 0) {
+            const struct ggml_tensor * m = ggml_graph_node(g, k);
+            if (m->op == GGML_OP_MUL && m->src[0] == ggml_graph_node(g, cur) && is_f32_vector(m->src[1], D) &&
+                input_ok(m->src[1])) {
+                a.norm_w = (const float *) m->src[1]->data;
+                chain.push_back(k);
+                cur = end = k;
+                k         = next(cur);
+            }
+        }
+    }
+    if (k >= 0) {
+        const struct ggml_tensor * r = ggml_graph_node(g, k);
+        if (r->op == GGML_OP_ROPE && r->src[0] == ggml_graph_node(g, cur) && supports_rope(r) && r->op_params[1] == D &&
+            r->src[1]->ne[0] == T && input_ok(r->src[1])) {
+            float base;
+            memcpy(&base, &r->op_params[5], sizeof(float));
+            a.pos         = (const int32_t *) r->src[1]->data;
+            a.theta_scale = powf(base, -2.0f / (float) D);
+            chain.push_back(k);
+            cur = end = k;
+            k         = next(cur);
+        }
+    }
+    if (k >= 0) {
+        const struct ggml_tensor * c2 = ggml_graph_node(g, k);
+        if (c2->op == GGML_OP_CONT && c2->type == GGML_TYPE_F32 && c2->src[0] == ggml_graph_node(g, cur)) {
+            chain.push_back(k);
+            cur = end = k;
+            k         = next(cur);
+        }
+    }
+    // [RESHAPE [D, 1, H, T] -> SET_ROWS]
+    if (k >= 0) {
+        const struct ggml_tensor * r2 = ggml_graph_node(g, k);
+        const int                  sk = r2->op == GGML_OP_RESHAPE ? next(k) : -1;
+        if (sk >= 0 && r2->src[0] == ggml_graph_node(g, cur) && r2->ne[0] == D && r2->ne[1] == 1 && r2->ne[2] == H &&
+            r2->ne[3] == T) {
+            const struct ggml_tensor * sr  = ggml_graph_node(g, sk);
+            const struct ggml_tensor * ids = sr->src[1];
+            const size_t               es  = sr->type == GGML_TYPE_F16 ? 2 : 4;
+            if (sr->op == GGML_OP_SET_ROWS && sr->src[0] == r2 && (sr->type == GGML_TYPE_F16 || sr->type == GGML_TYPE_F32) &&
+                (ids->type == GGML_TYPE_I64 || ids->type == GGML_TYPE_I32) && ids->ne[0] == 1 && ids->ne[3] == 1 &&
+                H % ids->ne[1] == 0 && T % ids->ne[2] == 0 && sr->ne[0] == D && sr->nb[0] == es && sr->ne[2] == H &&
+                sr->ne[3] == T && input_ok(ids)) {
+                a.ids       = ids->data;
+                a.ids_type  = ids->type;
+                a.ids_nb1   = (int64_t) ids->nb[1];
+                a.ids_nb2   = (int64_t) ids->nb[2];
+                a.ids_ne1   = ids->ne[1];
+                a.ids_ne2   = ids->ne[2];
+                a.dst       = sr->data;
+                a.dst_type  = sr->type == GGML_TYPE_F16 ? 1 : 0;
+                a.dst_nb1   = (int64_t) sr->nb[1];
+                a.dst_nb2   = (int64_t) sr->nb[2];
+                a.dst_nb3   = (int64_t) sr->nb[3];
+                chain.push_back(k);
+                chain.push_back(sk);
+                end = sk;
+            }
+        }
+    }
+    if (end < 0) {
+        return false;  // nothing but a copy: the plain CONT is as good
+    }
+    const struct ggml_tensor * e = ggml_graph_node(g, end);
+    if (!a.ids) {
+        if (!rows_contiguous_f32(e) || e->ne[0] != D || e->ne[1] != H || e->ne[2] != T) {
+            return false;
+        }
+        a.dst = e->data;
+    }
+    st.kind = ST_HEAD;
+    st.node = end;
+    st.head = a;
+    for (int x : chain) {
+        absorbed[(size_t) x] = 1;
+    }
+    return true;
+}
+
+struct graph_plan {
+    std::vector<plan_step> steps;
+    size_t                 slot_bytes = 0;
+};
+
+graph_plan build_plan(struct ggml_cgraph * g) {
+    graph_info gi;
+    gi.nn = ggml_graph_n_nodes(g);
+    gi.uses.assign((size_t) gi.nn, 0);
+    gi.cons.assign((size_t) gi.nn, -1);
+    gi.consumers.assign((size_t) gi.nn, {});
+    gi.index.reserve((size_t) gi.nn * 2);
+    for (int i = 0; i < gi.nn; i++) {
         struct ggml_tensor * n = ggml_graph_node(g, i);
         for (int s = 0; s < GGML_MAX_SRC; s++) {
             if (n->src[s]) {
-                auto it = index.find(n->src[s]);
-                if (it != index.end()) {
-                    uses[it->second]++;
+                auto it = gi.index.find(n->src[s]);
+                if (it != gi.index.end()) {
+                    gi.uses[(size_t) it->second]++;
+                    gi.cons[(size_t) it->second] = i;
+                    gi.consumers[(size_t) it->second].push_back(i);
                 }
             }
         }
-        index[n] = i;
+        gi.index[n] = i;
     }
-    for (int i = 0; i < nn;) {
-        const int step = run_node(c, g, i, uses);
-        if (step < 0) {
+    const bool no_fuse = getenv("GGML_MI355X_DISABLE_FUSION") != nullptr;
+
+    graph_plan               plan;
+    std::vector<char>        absorbed((size_t) gi.nn, 0);
+    std::vector<plan_step>   pending;                      // fused steps keyed by their execution node
+    std::vector<int>         step_at((size_t) gi.nn, -1);  // index into pending
+    std::vector<int64_t>     slot_of((size_t) gi.nn, -1);  // node -> quantised slot of its output
+    std::vector<int>         slot_wtype((size_t) gi.nn, 0);
+    auto add_pending = [&](const plan_step & st) {
+        step_at[(size_t) st.node] = (int) pending.size();
+        pending.push_back(st);
+    };
+    auto new_slot = [&](int wtype, int64_t K, int64_t M) -> int64_t {
+        const size_t  bytes = mmhip_act_bytes(wtype, K, M);
+        const int64_t off   = (int64_t) plan.slot_bytes;
+        plan.slot_bytes += (bytes + 255) / 256 * 256;
+        return off;
+    };
+
+    for (int i = 0; i < gi.nn && !no_fuse; i++) {
+        if (absorbed[(size_t) i]) {
+            continue;
+        }
+        struct ggml_tensor * n = ggml_graph_node(g, i);
+        if (n->op == GGML_OP_RMS_NORM && gi.uses[(size_t) i] == 1 && !is_output(n)) {
+            const int j = gi.cons[(size_t) i];
+            const struct ggml_tensor * m = ggml_graph_node(g, j);
+            if (m->op == GGML_OP_MUL && m->src[0] == n && m->src[1]->type == GGML_TYPE_F32 &&
+                ggml_are_same_shape(m, n) && node_index(gi, m->src[1]) < j) {
+                plan_step st;
+                st.kind = ST_NORM;
+                st.node = j;
+                st.src  = i;
+                const struct ggml_tensor * x  = n->src[0];
+                const int                  wt = gemv_consumer_type(g, gi, j);
+                const bool row_ok = x->nb[0] == 4 && x->ne[0] % 256 == 0 && x->ne[0] <= 16384 &&
+                                    is_f32_vector(m->src[1], x->ne[0]) && rows_contiguous_f32(m) &&
+                                    ((uintptr_t) x->data | x->nb[1] | x->nb[2] | x->nb[3]) % 16 == 0;
+                if (wt && row_ok) {
+                    st.vec_wtype = wt;
+                    st.slot_out  = new_slot(wt, x->ne[0], ggml_nrows(x));
+                    st.write_f32 = is_output(m);
+                    slot_of[(size_t) j]    = st.slot_out;
+                    slot_wtype[(size_t) j] = wt;
+                }
+                absorbed[(size_t) i] = 1;
+                absorbed[(size_t) j] = 1;
+                add_pending(st);
+                continue;
+            }
+        }
+        if (n->op == GGML_OP_GLU && n->op_params[0] == GGML_GLU_OP_SWIGLU && rows_contiguous_f32(n)) {
+            const struct ggml_tensor * a  = n->src[0];
+            const int                  wt = gemv_consumer_type(g, gi, i);
+            const int64_t              F  = n->ne[0];
+            const bool a_ok = a->nb[0] == 4 && a->nb[2] == a->nb[1] * (size_t) a->ne[1] &&
+                              a->nb[3] == a->nb[2] * (size_t) a->ne[2] && a->nb[1] % 16 == 0 &&
+                              ((uintptr_t) a->data) % 16 == 0;
+            const struct ggml_tensor * b    = n->src[1];
+            const bool                 b_ok = !b || (b->nb[0] == 4 && ggml_is_contiguous(b) && ((uintptr_t) b->data) % 16 == 0);
+            if (wt && F % 256 == 0 && a_ok && b_ok) {
+                plan_step st;
+                st.kind      = ST_SWIGLU_Q;
+                st.node      = i;
+                st.vec_wtype = wt;
+                st.slot_out  = new_slot(wt, F, ggml_nrows(n));
+                st.write_f32 = is_output(n);
+                slot_of[(size_t) i]    = st.slot_out;
+                slot_wtype[(size_t) i] = wt;
+                absorbed[(size_t) i]   = 1;
+                add_pending(st);
+                continue;
+            }
+        }
+        if (n->op == GGML_OP_CONT) {
+            plan_step st;
+            if (plan_head(g, gi, i, st, absorbed)) {
+                add_pending(st);
+                continue;
+            }
+        }
+        if (n->op == GGML_OP_MUL_MAT && mm_is_gemv(n)) {
+            plan_step st;
+            st.kind = ST_MM;
+            st.node = i;
+            const int p = node_index(gi, n->src[1]);
+            if (p >= 0 && slot_of[(size_t) p] >= 0) {
+                st.slot_in   = slot_of[(size_t) p];
+                st.vec_wtype = slot_wtype[(size_t) p];
+            }
+            // residual ADD in the store
+            if (gi.uses[(size_t) i] == 1 && !is_output(n)) {
+                const int                  j   = gi.cons[(size_t) i];
+                const struct ggml_tensor * ad  = ggml_graph_node(g, j);
+                const int                  oth = ad->op == GGML_OP_ADD ? (ad->src[0] == n ? 1 : ad->src[1] == n ? 0 : -1) : -1;
+                if (oth >= 0 && ad->src[oth] != n) {
+                    const struct ggml_tensor * r = ad->src[oth];
+                    if (r->type == GGML_TYPE_F32 && ggml_are_same_shape(r, n) && ggml_are_same_shape(ad, n) &&
+                        rows_contiguous_f32(ad) && r->nb[0] == 4 && r->ne[2] == 1 && r->ne[3] == 1 &&
+                        r->nb[1] % 4 == 0 && n->ne[2] == 1 && n->ne[3] == 1 && node_index(gi, r) < j) {
+                        st.add     = j;
+                        st.add_res = oth;
+                        st.node    = j;
+                        absorbed[(size_t) j] = 1;
+                    }
+                }
+            }
+            if (st.slot_in < 0 && st.add >= 0) {
+                // quantise the activations into a slot of their own
+                st.vec_wtype = n->src[0]->type;
+                st.slot_in   = new_slot(st.vec_wtype, n->src[0]->ne[0], n->src[1]->ne[1]);
+                st.src       = -2;  // marks "quantise first"
+                if (!mm_collapsible(n->src[1])) {
+                    st.add = -1, st.node = i, st.slot_in = -1, st.src = -1;
+                    absorbed[(size_t) gi.cons[(size_t) i]] = 0;
+                }
+            }
+            if (st.slot_in >= 0 || st.add >= 0) {
+                absorbed[(size_t) i] = 1;
+                add_pending(st);
+                continue;
+            }
+        }
+    }
+    for (int i = 0; i < gi.nn; i++) {
+        if (step_at[(size_t) i] >= 0) {
+            plan.steps.push_back(pending[(size_t) step_at[(size_t) i]]);
+        } else if (!absorbed[(size_t) i]) {
+            plan_step st;
+            st.node = i;
+            plan.steps.push_back(st);
+        }
+    }
+    return plan;
+}
+
+// Activation slots: device memory of the plan's quantised activations, kept
+// by the backend (separate from the per-op workspace).
+void * slots(mi_backend * c, size_t need) {
+    if (need <= c->slot_size) {
+        return c->slot;
+    }
+    if (c->capturing) {
+        return nullptr;
+    }
+    HIP_OK(hipStreamSynchronize(c->stream));
+    if (c->slot) {
+        (void) hipFree(c->slot);
+    }
+    c->slot      = nullptr;
+    c->slot_size = 0;
+    if (!HIP_OK(hipMalloc(&c->slot, need))) {
+        return nullptr;
+    }
+    c->slot_size = need;
+    return c->slot;
+}
+
+int run_step(mi_backend * c, struct ggml_cgraph * g, const plan_step & st, char * slot) {
+    hipStream_t          s = c->stream;
+    struct ggml_tensor * n = ggml_graph_node(g, st.node);
+    int                  rc;
+    switch (st.kind) {
+        case ST_NODE:
+            return run_node(c, n);
+        case ST_NORM: {
+            const struct ggml_tensor * rn = ggml_graph_node(g, st.src);
+            float                      eps;
+            memcpy(&eps, &rn->op_params[0], sizeof(float));
+            mmhip_view x = view_of(rn->src[0]), w = view_of(n->src[1]);
+            if (st.slot_out >= 0) {
+                rc = mmhip_rms_norm_quant(&x, &w, eps, st.write_f32 ? (float *) n->data : nullptr, st.vec_wtype,
+                                          slot + st.slot_out, s);
+            } else {
+                rc = mmhip_rms_norm(&x, &w, eps, (float *) n->data, s);
+            }
+            break;
+        }
+        case ST_SWIGLU_Q: {
+            mmhip_view a = view_of(n->src[0]);
+            mmhip_view b;
+            if (n->src[1]) {
+                b = view_of(n->src[1]);
+            }
+            rc = mmhip_swiglu_quant(&a, n->src[1] ? &b : nullptr, n->op_params[1],
+                                    st.write_f32 ? (float *) n->data : nullptr, st.vec_wtype, slot + st.slot_out, s);
+            break;
+        }
+        case ST_HEAD:
+            rc = mmhip_head_rows(&st.head, s);
+            break;
+        case ST_MM: {
+            const struct ggml_tensor * mm = st.add >= 0 ? ggml_graph_node(g, st.add)->src[1 - st.add_res] : n;
+            const struct ggml_tensor * w  = mm->src[0];
+            const struct ggml_tensor * x  = mm->src[1];
+            const int64_t              N = w->ne[1], K = w->ne[0], M = x->ne[1] * x->ne[2] * x->ne[3];
+            if (st.src == -2) {
+                rc = mmhip_quantize_act(w->type, (const float *) x->data, (int64_t) (x->nb[1] / 4), K, M,
+                                        slot + st.slot_in, s);
+                if (rc != MMHIP_OK) {
+                    break;
+                }
+            }
+            if (st.add >= 0) {
+                const struct ggml_tensor * r = ggml_graph_node(g, st.add)->src[st.add_res];
+                rc = mmhip_mul_mat_q_add(w->type, w->data, N, K, (int64_t) w->nb[1], slot + st.slot_in, M,
+                                         (const float *) r->data, (int64_t) (r->nb[1] / 4), (float *) n->data, N, s);
+            } else {
+                rc = mmhip_mul_mat_q(w->type, w->data, N, K, (int64_t) w->nb[1], slot + st.slot_in, M,
+                                     (float *) n->data, N, s);
+            }
+            break;
+        }
+        default:
+            return -1;
+    }
+    return rc == MMHIP_OK ? MMHIP_OK : (fail(n, rc), -1);
+}
+
+bool run_graph(mi_backend * c, struct ggml_cgraph * g) {
+    const graph_plan plan = build_plan(g);
+    char *           slot = nullptr;
+    if (plan.slot_bytes) {
+        slot = (char *) slots(c, plan.slot_bytes);
+        if (!slot) {
             return false;
         }
-        i += step;
+    }
+    for (const plan_step & st : plan.steps) {
+        if (run_step(c, g, st, slot) != MMHIP_OK) {
+            return false;
+        }
     }
     return true;
 }

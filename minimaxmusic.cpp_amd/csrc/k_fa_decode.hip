@@ -41,8 +41,8 @@ __global__ __launch_bounds__(256) void k_fa_decode(FaArgs a, int chunk, int nspl
     const int kbeg  = split * chunk;
     const int kend  = min(a.nkv, kbeg + chunk);
 
-    half8_t      qv[QR];
     const char * mrow[QR];
+    const float * qrow[QR];
     bool         rvalid[QR];
 #pragma unroll
     for (int r = 0; r < QR; r++) {
@@ -51,16 +51,55 @@ __global__ __launch_bounds__(256) void k_fa_decode(FaArgs a, int chunk, int nspl
         const int rrc = rvalid[r] ? rr : r0;
         const int hq  = g * G + rrc % G;
         const int iq  = rrc / G;
-        const float * qp = (const float *) (a.q + iq * a.qnb1 + hq * a.qnb2 + b * a.qnb3) + seg * 8;
-#pragma unroll
-        for (int d = 0; d < 8; d++) {
-            qv[r][d] = (_Float16) qp[d];
-        }
+        qrow[r]       = (const float *) (a.q + iq * a.qnb1 + hq * a.qnb2 + b * a.qnb3) + seg * 8;
         mrow[r] = a.mask ? a.mask + iq * a.mnb1 + (hq % a.mne2) * a.mnb2 + (b % a.mne3) * a.mnb3 : nullptr;
     }
 
     const char * kbase = a.k + g * a.knb2 + bk * a.knb3 + seg * 16;
     const char * vbase = a.v + g * a.vnb2 + bk * a.vnb3 + seg * 16;
+
+    // mask rows shared by every query row of the group (the LM's causal /
+    // padding mask is one row per token): one mask load per key
+    bool mask_shared = true;
+#pragma unroll
+    for (int r = 1; r < QR; r++) {
+        mask_shared = mask_shared && (!rvalid[r] || mrow[r] == mrow[0]);
+    }
+    // without a mask, the loads read K's first bytes (in bounds: 2 * nkv <=
+    // the K rows) and the value is dropped, keeping every load unconditional
+    const char * mbase = mrow[0] ? mrow[0] : a.k;
+    const bool   has_m = mrow[0] != nullptr;
+
+    // One pass = U keys per lane.  All K / V / mask loads of a pass are issued
+    // together (those of the first pass even before Q's), then all scores,
+    // one running-max update per row, and the exp2-weighted V sums.
+    half8_t  kk[U], vv[U];
+    int      jc[U];
+    uint16_t mk[U];  // raw f16 mask bits: converted at use, so no load waits here
+    auto     load_pass = [&](int base) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int j = base + 4 * KPW * u + ks;
+            jc[u]       = j < kend ? j : kend - 1;
+            kk[u]       = *(const half8_t *) (kbase + (int64_t) jc[u] * a.knb1);
+            vv[u]       = *(const half8_t *) (vbase + (int64_t) jc[u] * a.vnb1);
+            mk[u]       = *(const uint16_t *) (mbase + jc[u] * 2);
+        }
+    };
+    const int step = 4 * KPW * U;
+    int       base = kbeg + wave * KPW;
+    if (base < kend) {
+        load_pass(base);
+    }
+
+    half8_t qv[QR];
+#pragma unroll
+    for (int r = 0; r < QR; r++) {
+#pragma unroll
+        for (int d = 0; d < 8; d++) {
+            qv[r][d] = (_Float16) qrow[r][d];  // q is only 4-byte aligned
+        }
+    }
 
     float m[QR], l[QR], o[QR][8];
 #pragma unroll
@@ -74,20 +113,8 @@ __global__ __launch_bounds__(256) void k_fa_decode(FaArgs a, int chunk, int nspl
     }
     const float log2e = 1.4426950408889634f;
 
-    // U keys per lane in flight: all K/V loads of an iteration are issued
-    // before the first use.
-    for (int base = kbeg + wave * KPW; base < kend; base += 4 * KPW * U) {
-        half8_t kk[U], vv[U];
-        int64_t jc[U];
-        bool    jv[U];
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int j = base + 4 * KPW * u + ks;
-            jv[u]       = j < kend;
-            jc[u]       = jv[u] ? j : kend - 1;
-            kk[u]       = *(const half8_t *) (kbase + jc[u] * a.knb1);
-            vv[u]       = *(const half8_t *) (vbase + jc[u] * a.vnb1);
-        }
+    for (; base < kend; base += step) {
+        float sc[QR][U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
 #pragma unroll
@@ -98,21 +125,53 @@ __global__ __launch_bounds__(256) void k_fa_decode(FaArgs a, int chunk, int nspl
                 dot = __builtin_amdgcn_fdot2(half2_t{ kk[u][4], kk[u][5] }, half2_t{ qv[r][4], qv[r][5] }, dot, false);
                 dot = __builtin_amdgcn_fdot2(half2_t{ kk[u][6], kk[u][7] }, half2_t{ qv[r][6], qv[r][7] }, dot, false);
                 dot = group_sum<LPK>(dot);
-                const float mv = mrow[r] ? h2f(*(const uint16_t *) (mrow[r] + jc[u] * 2)) : 0.0f;
-                const float s  = (jv[u] && rvalid[r]) ? (dot * a.scale + mv) * log2e : -INFINITY;
-                const float mn = fmaxf(m[r], s);
-                float       alpha = 1.0f, p = 0.0f;
-                if (mn != -INFINITY) {
-                    alpha = __builtin_amdgcn_exp2f(m[r] - mn);
-                    p     = __builtin_amdgcn_exp2f(s - mn);
-                }
-                l[r] = l[r] * alpha + p;
+                const float mv = !has_m ? 0.0f
+                                 : (mask_shared || r == 0) ? h2f(mk[u])
+                                                           : h2f(*(const uint16_t *) (mrow[r] + jc[u] * 2));
+                const bool kv = base + 4 * KPW * u + ks < kend;
+                sc[r][u]      = (kv && rvalid[r]) ? (dot * a.scale + mv) * log2e : -INFINITY;
+            }
+        }
+        half8_t vcur[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            vcur[u] = vv[u];
+        }
+        if (base + step < kend) {
+            load_pass(base + step);  // next pass's loads overlap this pass's softmax
+        }
+#pragma unroll
+        for (int r = 0; r < QR; r++) {
+            float mn = m[r];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                mn = fmaxf(mn, sc[r][u]);
+            }
+            if (mn == -INFINITY) {
+                continue;  // nothing finite yet for this row (per-lane state, no cross-lane op below)
+            }
+            const float alpha = __builtin_amdgcn_exp2f(m[r] - mn);
+            float       psum  = 0.0f;
+            float       pv[8];
+#pragma unroll
+            for (int d = 0; d < 8; d++) {
+                pv[d] = 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const float p = __builtin_amdgcn_exp2f(sc[r][u] - mn);
+                psum += p;
 #pragma unroll
                 for (int d = 0; d < 8; d++) {
-                    o[r][d] = o[r][d] * alpha + p * (float) vv[u][d];
+                    pv[d] += p * (float) vcur[u][d];
                 }
-                m[r] = mn;
             }
+            l[r] = l[r] * alpha + psum;
+#pragma unroll
+            for (int d = 0; d < 8; d++) {
+                o[r][d] = o[r][d] * alpha + pv[d];
+            }
+            m[r] = mn;
         }
     }
 
@@ -177,6 +236,225 @@ __global__ __launch_bounds__(256) void k_fa_decode(FaArgs a, int chunk, int nspl
             out[(((int64_t) b * a.nq + iq) * a.Hq + hq) * D + d] = L > 0.0f ? O / L : 0.0f;
         } else {
             const int64_t pr = (((int64_t) b * a.Hq + hq) * a.nq + iq) * nsplit + split;
+            part_o[pr * D + d] = O;
+            if (d == 0) {
+                part_ml[pr * 2 + 0] = M;
+                part_ml[pr * 2 + 1] = L;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------
+// MFMA decode: the G * nq (<= 16) query rows of one KV head are the columns
+// of 16 x 16 MFMA tiles.  Workgroup = (split, KV head, batch), 4 waves; the
+// split's keys are dealt to the waves in 16-key tiles (wave w: tiles w,
+// w + 4, ...), each wave keeping its own online-softmax state.
+//   S^T (16 keys x 16 cols) = K Q^T with mfma_f32_16x16x32_f16: lane l owns
+//     key l % 16 and dims 32s + 8(l / 16) .. +7 of the A operand, a 16-byte
+//     load straight from the cache; Q^T is the B operand, held in registers.
+//   The S^T accumulator (lane l: keys 4(l / 16) + i, column l % 16) is
+//     exactly the B-operand layout of mfma_f32_16x16x16f16, so P^T feeds
+//     O^T (dims x cols) = V^T P^T without leaving registers.
+//   V^T (the A operand: lane l needs dim l % 16 of keys 4(l / 16) .. +3) goes
+//     through a per-wave LDS tile written transposed.
+// Scores, softmax and the partial format are those of k_fa_decode, and the
+// same combine kernel merges the splits.
+
+template <int D>
+__global__ __launch_bounds__(256) void k_fa_dec_mfma(FaArgs a, int chunk, int nsplit, float * __restrict__ part_o,
+                                                     float * __restrict__ part_ml, float * __restrict__ out) {
+    constexpr int NS  = D / 32;  // k-steps of Q.K (32 dims each)
+    constexpr int NDB = D / 16;  // 16-dim blocks of O^T
+    constexpr int VTS = 16 + 4;  // V^T row stride (halves): 16 keys + pad
+    constexpr int TP  = 2;       // tiles per wave per load round
+    constexpr int SVT = 4 * D * VTS;            // halves of the 4 waves' V^T tiles
+    constexpr int SO  = 4 * 16 * D * 2;         // halves of the merge buffer (floats)
+    __shared__ __attribute__((aligned(16))) _Float16 s_buf[SVT > SO ? SVT : SO];
+    __shared__ float s_m[4][16], s_l[4][16];
+
+    const int split = blockIdx.x;
+    const int g     = blockIdx.y;
+    const int b     = blockIdx.z;
+    const int G     = a.Hq / a.Hkv;
+    const int ncol  = G * a.nq;
+    const int bk    = b / (a.B / a.Bk);
+    const int wave  = threadIdx.x >> 6;
+    const int lane  = threadIdx.x & 63;
+    const int col   = lane & 15;
+    const int kq    = lane >> 4;
+    const int kbeg  = split * chunk;
+    const int kend  = min(a.nkv, kbeg + chunk);
+    const int ntile = (kend - kbeg + 15) / 16;
+
+    const bool   cvalid = col < ncol;
+    const int    cc     = cvalid ? col : 0;
+    const int    hq     = g * G + cc % G;
+    const int    iq     = cc / G;
+    const char * mrow   = a.mask ? a.mask + iq * a.mnb1 + (hq % a.mne2) * a.mnb2 + (b % a.mne3) * a.mnb3 : nullptr;
+
+    const char * kbase = a.k + g * a.knb2 + bk * a.knb3 + 16 * kq;
+    const char * vbase = a.v + g * a.vnb2 + bk * a.vnb3 + 16 * kq;
+    _Float16 *   svt   = s_buf + wave * D * VTS;
+
+    // without a mask the mask loads read the cache's first bytes (in bounds:
+    // 2 * nkv <= the K rows) and are dropped, so every load is unconditional
+    const char * mbase = mrow ? mrow : a.k;
+
+    // loads of TP tiles: K and V fragments (lane: key l % 16, dims 32s + 8kq
+    // ..) and the raw mask bits of the lane's score keys 4kq .. 4kq+3
+    half8_t  kf[TP][NS], vf[TP][NS];
+    uint16_t mk[TP][4];
+    auto     load_tiles = [&](int t0) {
+#pragma unroll
+        for (int p = 0; p < TP; p++) {
+            const int t   = t0 + 4 * p;
+            const int key = min(kbeg + 16 * t + col, kend - 1);
+#pragma unroll
+            for (int s = 0; s < NS; s++) {
+                kf[p][s] = *(const half8_t *) (kbase + (int64_t) key * a.knb1 + 64 * s);
+                vf[p][s] = *(const half8_t *) (vbase + (int64_t) key * a.vnb1 + 64 * s);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                mk[p][i] = *(const uint16_t *) (mbase + (int64_t) min(kbeg + 16 * t + 4 * kq + i, kend - 1) * 2);
+            }
+        }
+    };
+    int t0 = wave;
+    if (t0 < ntile) {
+        load_tiles(t0);
+    }
+
+    // Q^T B operand: column col, dims 32s + 8kq .. +7 (zero for unused columns)
+    half8_t       qb[NS];
+    const float * qp = (const float *) (a.q + iq * a.qnb1 + hq * a.qnb2 + b * a.qnb3) + 8 * kq;
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            qb[s][i] = cvalid ? (_Float16) qp[32 * s + i] : (_Float16) 0.0f;
+        }
+    }
+
+    float4_t oacc[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; i++) {
+        oacc[i] = float4_t{ 0.0f, 0.0f, 0.0f, 0.0f };
+    }
+    float       m     = -INFINITY;
+    float       l     = 0.0f;
+    const float log2e = 1.4426950408889634f;
+    const float sl2   = a.scale * log2e;
+
+    for (; t0 < ntile; t0 += 4 * TP) {
+#pragma unroll
+        for (int p = 0; p < TP; p++) {
+            const int t = t0 + 4 * p;
+            if (t >= ntile) {
+                break;  // uniform over the wave
+            }
+            // S^T tile
+            float4_t sacc = { 0.0f, 0.0f, 0.0f, 0.0f };
+#pragma unroll
+            for (int s = 0; s < NS; s++) {
+                sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[p][s], qb[s], sacc, 0, 0, 0);
+            }
+            // V^T tile into LDS: dim 32s + 8kq + j, key col
+#pragma unroll
+            for (int s = 0; s < NS; s++) {
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    svt[(32 * s + 8 * kq + j) * VTS + col] = vf[p][s][j];
+                }
+            }
+            // scores of keys 4kq + i for this lane's column
+            const int key0 = kbeg + 16 * t + 4 * kq;
+            float     sc[4];
+            float     mx = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int   key = key0 + i;
+                const bool  ok  = key < kend && cvalid;
+                const float mv  = mrow ? h2f(mk[p][i]) : 0.0f;
+                sc[i]           = ok ? sacc[i] * sl2 + mv * log2e : -INFINITY;
+                mx              = fmaxf(mx, sc[i]);
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
+            // no divergent control flow around the MFMAs: a column with
+            // nothing visible yet keeps alpha = 1 and p = exp2(-inf) = 0
+            const float mnew  = fmaxf(m, mx);
+            const bool  live  = mnew != -INFINITY;
+            const float mref  = live ? mnew : 0.0f;
+            const float alpha = live ? __builtin_amdgcn_exp2f(m - mnew) : 1.0f;
+            half4_t     pb;
+            float       rs = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float pv = __builtin_amdgcn_exp2f(sc[i] - mref);
+                rs += pv;
+                pb[i] = (_Float16) pv;
+            }
+            rs += __shfl_xor(rs, 16, WAVE);
+            rs += __shfl_xor(rs, 32, WAVE);
+            l = l * alpha + rs;
+            m = mnew;
+            // the transposed V tile written above by this wave's lanes
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int db = 0; db < NDB; db++) {
+                const half4_t av = *(const half4_t *) &svt[(16 * db + col) * VTS + 4 * kq];
+                oacc[db]         = oacc[db] * alpha;
+                oacc[db]         = __builtin_amdgcn_mfma_f32_16x16x16f16(av, pb, oacc[db], 0, 0, 0);
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+        if (t0 + 4 * TP < ntile) {
+            load_tiles(t0 + 4 * TP);
+        }
+    }
+
+    // merge the 4 waves (LDS reused: V^T tiles are done)
+    __syncthreads();
+    float * s_o = (float *) s_buf;  // [4][16][D]
+    if (kq == 0) {
+        s_m[wave][col] = m;
+        s_l[wave][col] = l;
+    }
+#pragma unroll
+    for (int db = 0; db < NDB; db++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            s_o[(wave * 16 + col) * D + 16 * db + 4 * kq + i] = oacc[db][i];
+        }
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < ncol * D; idx += 256) {
+        const int c = idx / D;
+        const int d = idx % D;
+        float     M = s_m[0][c];
+#pragma unroll
+        for (int w = 1; w < 4; w++) {
+            M = fmaxf(M, s_m[w][c]);
+        }
+        float L = 0.0f, O = 0.0f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const float f = s_m[w][c] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s_m[w][c] - M);
+                L += s_l[w][c] * f;
+                O += s_o[(w * 16 + c) * D + d] * f;
+            }
+        }
+        const int h  = g * G + c % G;
+        const int qi = c / G;
+        if (nsplit == 1) {
+            out[(((int64_t) b * a.nq + qi) * a.Hq + h) * D + d] = L > 0.0f ? O / L : 0.0f;
+        } else {
+            const int64_t pr = (((int64_t) b * a.Hq + h) * a.nq + qi) * nsplit + split;
             part_o[pr * D + d] = O;
             if (d == 0) {
                 part_ml[pr * 2 + 0] = M;
@@ -251,18 +529,24 @@ __global__ __launch_bounds__(256) void k_fa_combine(const float * __restrict__ p
 
 // ---------------------------------------------------------------------
 
-constexpr int DEC_U = 4;
+// keys per lane per pass (D = 128, QR = 4: 128 keys per workgroup pass)
+constexpr int dec_u(int QR) {
+    return QR <= 4 ? 8 : 4;
+}
 
 static int dec_qr(const FaArgs & a) {
     return (a.Hq / a.Hkv) * a.nq <= 4 ? 4 : 8;
 }
 
+static bool dec_mfma(const FaArgs & a);
+
 static void decode_plan(const FaArgs & a, int D, int & nsplit, int & chunk, int & rowgroups) {
     const int G    = a.Hq / a.Hkv;
     const int QR   = dec_qr(a);
-    rowgroups      = (G * a.nq + QR - 1) / QR;
+    rowgroups      = dec_mfma(a) ? 1 : (G * a.nq + QR - 1) / QR;
     const int kpw  = 64 / (D / 8);
-    const int step = 4 * kpw * DEC_U;  // keys one workgroup iteration covers
+    // keys one workgroup pass covers (MFMA kernel: 4 waves x 16-key tiles)
+    const int step = dec_mfma(a) ? 64 : 4 * kpw * dec_u(QR);
     const int base_wgs = a.Hkv * a.B * rowgroups;
     const int target   = 512;
     int       ns       = (target + base_wgs - 1) / base_wgs;
@@ -287,10 +571,15 @@ template <int D>
 static void launch_decode(const FaArgs & a, int QR, dim3 grid, int chunk, int nsplit, float * po, float * pml,
                           float * out, hipStream_t stream) {
     if (QR == 4) {
-        hipLaunchKernelGGL((k_fa_decode<D, 4, DEC_U>), grid, dim3(256), 0, stream, a, chunk, nsplit, po, pml, out);
+        hipLaunchKernelGGL((k_fa_decode<D, 4, dec_u(4)>), grid, dim3(256), 0, stream, a, chunk, nsplit, po, pml, out);
     } else {
-        hipLaunchKernelGGL((k_fa_decode<D, 8, DEC_U>), grid, dim3(256), 0, stream, a, chunk, nsplit, po, pml, out);
+        hipLaunchKernelGGL((k_fa_decode<D, 8, dec_u(8)>), grid, dim3(256), 0, stream, a, chunk, nsplit, po, pml, out);
     }
+}
+
+// The MFMA decode kernel serves up to 16 query rows per KV head.
+static bool dec_mfma(const FaArgs & a) {
+    return (a.Hq / a.Hkv) * a.nq <= 16;
 }
 
 int fa_decode(const FaArgs & a, int D, float * out, void * ws, size_t ws_bytes, hipStream_t stream) {
@@ -310,6 +599,15 @@ int fa_decode(const FaArgs & a, int D, float * out, void * ws, size_t ws_bytes, 
     if ((int64_t) a.B * rg > 65535) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "flash_attn decode: B * row groups too large");
     }
+    if (dec_mfma(a)) {
+        const dim3 g3(nsplit, a.Hkv, a.B);
+        switch (D) {
+            case 64: hipLaunchKernelGGL(k_fa_dec_mfma<64>, g3, dim3(256), 0, stream, a, chunk, nsplit, part_o, part_ml, out); break;
+            case 128: hipLaunchKernelGGL(k_fa_dec_mfma<128>, g3, dim3(256), 0, stream, a, chunk, nsplit, part_o, part_ml, out); break;
+            case 256: hipLaunchKernelGGL(k_fa_dec_mfma<256>, g3, dim3(256), 0, stream, a, chunk, nsplit, part_o, part_ml, out); break;
+            default: return set_error(MMHIP_ERR_UNSUPPORTED, "flash_attn decode: head dim %d", D);
+        }
+    } else {
     const dim3 grid(nsplit, a.Hkv, a.B * rg);
     const int  QR = dec_qr(a);
     switch (D) {
@@ -317,6 +615,7 @@ int fa_decode(const FaArgs & a, int D, float * out, void * ws, size_t ws_bytes, 
         case 128: launch_decode<128>(a, QR, grid, chunk, nsplit, part_o, part_ml, out, stream); break;
         case 256: launch_decode<256>(a, QR, grid, chunk, nsplit, part_o, part_ml, out, stream); break;
         default: return set_error(MMHIP_ERR_UNSUPPORTED, "flash_attn decode: head dim %d", D);
+    }
     }
     int rc = check_launch("flash_attn decode");
     if (rc != MMHIP_OK || nsplit == 1) {

@@ -9,8 +9,8 @@
 // Mapping: 256 threads = 4 waves; each wave owns R weight rows at a time and
 // streams them with 16-byte loads, 64 lanes covering 1024 contiguous bytes of
 // a field per step (every field of the row-grouped layout is contiguous).
-// The quantised activations of all M columns are staged once per workgroup
-// in LDS and re-read there, so HBM carries only the weights.
+// The quantised activations of the M columns (a few KB) are read through the
+// L1/L2 caches by every wave, so HBM carries essentially only the weights.
 #include "mmhip_device.h"
 #include "mmhip_internal.h"
 
@@ -67,9 +67,11 @@ template <int V> __device__ __forceinline__ int reduce_index(int lane) {
 }
 
 // Store R x NC reduced sums: value index v = r*NC + c.
+// With res != nullptr the stored value is total + res[c*ldr + row] (the residual
+// ADD of the graph, one f32 rounding as ggml's separate ADD node gives).
 template <int NC, int R>
 __device__ __forceinline__ void store_rows(float (&acc)[R][NC], int lane, int64_t row0, int64_t N, float * y,
-                                           int64_t ldy) {
+                                           int64_t ldy, const float * res, int64_t ldr) {
     constexpr int V  = R * NC;
     constexpr int VP = V <= 1 ? 1 : V <= 2 ? 2 : V <= 4 ? 4 : V <= 8 ? 8 : V <= 16 ? 16 : 32;
     float         a[VP];
@@ -85,7 +87,7 @@ __device__ __forceinline__ void store_rows(float (&acc)[R][NC], int lane, int64_
         const int     c   = idx % NC;
         const int64_t row = row0 + r;
         if (row < N) {
-            y[c * ldy + row] = total;
+            y[c * ldy + row] = res ? total + res[c * ldr + row] : total;
         }
     }
 }
@@ -111,12 +113,17 @@ template <bool AL> __device__ __forceinline__ uint2 ld8a(const uint8_t * p) {
     }
 }
 
-// Q8_0.  Wave-chunk = 1024 bytes of qs (32 blocks); lane l owns bytes
-// [16l, 16l+16) = half of block l/2.  U chunks are loaded before any use.
-template <int NC, int R, int U>
+// Q8_0.  One wave per R consecutive rows.  A row's qs is read in 1024-byte
+// chunks (32 blocks; lane l owns bytes 16l .. 16l+15 = half of block l/2);
+// the wave issues the loads of CH chunks x R rows before using any, so for
+// K <= 1024 * CH one memory round trip covers its whole share (measured on
+// the decode shapes: this beats both a per-chunk loop and a split of K over
+// the workgroup's waves, which adds a barrier and an LDS reduction).  The
+// activation chunks come through L1/L2 (a few KB shared by every wave).
+template <int NC, int R, int CH, bool ONE>  // ONE: K <= 1024 * CH, a single pass
 __global__ __launch_bounds__(256) void k_gemv_q8_0(const uint8_t * __restrict__ W, int64_t N, int64_t K, int64_t rs,
                                                     const int8_t * __restrict__ xq, const float * __restrict__ xd,
-                                                    float * __restrict__ y, int64_t ldy) {
+                                                    float * y, int64_t ldy, const float * res, int64_t ldr) {
     const int     lane = threadIdx.x & 63;
     const int64_t g    = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
     if (g * R >= N) {
@@ -136,37 +143,43 @@ __global__ __launch_bounds__(256) void k_gemv_q8_0(const uint8_t * __restrict__ 
             acc[r][c] = 0.0f;
         }
     }
-    for (int64_t base = 0; base < K; base += 1024 * U) {
-        int4_t wv[U][R], xv[U][NC];
-        float  dw[U][R], dx[U][NC];
+    const int k32   = (int) K;
+    const int npass = ONE ? 1 : (k32 + 1024 * CH - 1) / (1024 * CH);
+    for (int pass = 0; pass < npass; pass++) {
+        const int base = pass * 1024 * CH;
+        // every load unconditional (offsets clamped into the row, the lanes
+        // past K weighted by zero) so that all of them issue before any use
+        int4_t   wq[CH][R], xv[CH][NC];
+        uint16_t sw[CH][R];
+        float    dx[CH][NC];
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int64_t off = base + 1024 * u + lane * 16;
-            const bool    ok  = off < K;
-            const int64_t o   = ok ? off : 0;
+        for (int u = 0; u < CH; u++) {
+            const int o = min(base + 1024 * u + lane * 16, k32 - 16);
 #pragma unroll
             for (int r = 0; r < R; r++) {
-                wv[u][r] = ld16(wr[r] + o);
-                dw[u][r] = ok ? h2f(*(const uint16_t *) (wr[r] + K + 2 * (o >> 5))) : 0.0f;
+                wq[u][r] = ld16(wr[r] + o);
+                sw[u][r] = *(const uint16_t *) (wr[r] + k32 + 2 * (o >> 5));
             }
 #pragma unroll
             for (int c = 0; c < NC; c++) {
-                xv[u][c] = ld16(xq + c * K + o);
+                xv[u][c] = ld16(xq + c * k32 + o);
                 dx[u][c] = xd[c * nblk + (o >> 5)];
             }
         }
 #pragma unroll
-        for (int u = 0; u < U; u++) {
+        for (int u = 0; u < CH; u++) {
+            const bool ok = base + 1024 * u + lane * 16 < k32;
 #pragma unroll
-            for (int c = 0; c < NC; c++) {
+            for (int r = 0; r < R; r++) {
+                const float dw = ok ? h2f(sw[u][r]) : 0.0f;
 #pragma unroll
-                for (int r = 0; r < R; r++) {
-                    acc[r][c] += (float) dot16(wv[u][r], xv[u][c]) * (dw[u][r] * dx[u][c]);
+                for (int c = 0; c < NC; c++) {
+                    acc[r][c] += (float) dot16(wq[u][r], xv[u][c]) * (dw * dx[u][c]);
                 }
             }
         }
     }
-    store_rows<NC, R>(acc, lane, g * R, N, y, ldy);
+    store_rows<NC, R>(acc, lane, g * R, N, y, ldy, res, ldr);
 }
 
 // Q4_K.  Wave-chunk = 1024 bytes of qs (8 super-blocks); lane l owns 16
@@ -175,8 +188,8 @@ __global__ __launch_bounds__(256) void k_gemv_q8_0(const uint8_t * __restrict__ 
 template <int NC, int R, int U>
 __global__ __launch_bounds__(256) void k_gemv_q4_K(const uint8_t * __restrict__ W, int64_t N, int64_t K, int64_t rs,
                                                     const int8_t * __restrict__ xq, const float * __restrict__ xd,
-                                                    const int16_t * __restrict__ xbs, float * __restrict__ y,
-                                                    int64_t ldy) {
+                                                    const int16_t * __restrict__ xbs, float * y,
+                                                    int64_t ldy, const float * res, int64_t ldr) {
     const int     lane = threadIdx.x & 63;
     const int64_t g    = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
     if (g * R >= N) {
@@ -256,7 +269,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4_K(const uint8_t * __restrict__ 
             }
         }
     }
-    store_rows<NC, R>(acc, lane, g * R, N, y, ldy);
+    store_rows<NC, R>(acc, lane, g * R, N, y, ldy, res, ldr);
 }
 
 // Q6_K.  Unit = (super-block sb, half h, 16 columns l0..l0+15): 48 weight
@@ -265,8 +278,8 @@ __global__ __launch_bounds__(256) void k_gemv_q4_K(const uint8_t * __restrict__ 
 template <int NC, int R, int U, bool AL>
 __global__ __launch_bounds__(256) void k_gemv_q6_K(const uint8_t * __restrict__ W, int64_t N, int64_t K, int64_t rs,
                                                     const int8_t * __restrict__ xq, const float * __restrict__ xd,
-                                                    const int16_t * __restrict__ xbs, float * __restrict__ y,
-                                                    int64_t ldy) {
+                                                    const int16_t * __restrict__ xbs, float * y,
+                                                    int64_t ldy, const float * res, int64_t ldr) {
     const int     lane = threadIdx.x & 63;
     const int64_t g    = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
     if (g * R >= N) {
@@ -355,7 +368,7 @@ __global__ __launch_bounds__(256) void k_gemv_q6_K(const uint8_t * __restrict__ 
             }
         }
     }
-    store_rows<NC, R>(acc, lane, g * R, N, y, ldy);
+    store_rows<NC, R>(acc, lane, g * R, N, y, ldy, res, ldr);
 }
 
 // ---------------------------------------------------------------------
@@ -381,28 +394,64 @@ template <int NC> struct GemvShape {
     static constexpr int U = NC <= 4 ? 2 : 1;
 };
 
+// Q8_0 launch: rows per wave R by matrix height (more waves for the short
+// matrices, fewer activation re-reads for the tall ones), chunks per load
+// pass CH covering K up to 12288 in one pass for one or two columns.
+template <int NC, int R, int CH>
+static int launch_q8_0(const uint8_t * W, int64_t N, int64_t K, int64_t rs, const ActPtrs & x, float * y, int64_t ldy,
+                       const float * r, int64_t ldr, hipStream_t stream) {
+    if (K <= 1024 * CH) {
+        auto kern = k_gemv_q8_0<NC, R, CH, true>;
+        return launch_gemv(kern, R, N, stream, W, N, K, rs, x.qs, x.d, y, ldy, r, ldr);
+    }
+    auto kern = k_gemv_q8_0<NC, R, CH, false>;
+    return launch_gemv(kern, R, N, stream, W, N, K, rs, x.qs, x.d, y, ldy, r, ldr);
+}
+
+template <int NC, int R>
+static int launch_q8_0_k(const uint8_t * W, int64_t N, int64_t K, int64_t rs, const ActPtrs & x, float * y,
+                         int64_t ldy, const float * r, int64_t ldr, hipStream_t stream) {
+    const int64_t nch = (K + 1023) / 1024;
+    if constexpr (NC > 4) {
+        return launch_q8_0<NC, R, 2>(W, N, K, rs, x, y, ldy, r, ldr, stream);
+    } else if constexpr (NC > 2) {
+        return launch_q8_0<NC, R, 4>(W, N, K, rs, x, y, ldy, r, ldr, stream);
+    } else {
+        if (nch <= 4) {
+            return launch_q8_0<NC, R, 4>(W, N, K, rs, x, y, ldy, r, ldr, stream);
+        }
+        if (nch <= 12) {
+            return launch_q8_0<NC, R, 12>(W, N, K, rs, x, y, ldy, r, ldr, stream);
+        }
+        return launch_q8_0<NC, R, 8>(W, N, K, rs, x, y, ldy, r, ldr, stream);
+    }
+}
+
 template <int NC>
 static int gemv_dispatch(int wtype, const uint8_t * W, int64_t N, int64_t K, int64_t rs, const ActPtrs & x, float * y,
-                         int64_t ldy, hipStream_t stream) {
+                         int64_t ldy, const float * r, int64_t ldr, hipStream_t stream) {
     constexpr int R = GemvShape<NC>::R;
     constexpr int U = GemvShape<NC>::U;
     if (wtype == TYPE_Q8_0) {
-        return launch_gemv(k_gemv_q8_0<NC, R, U>, R, N, stream, W, N, K, rs, x.qs, x.d, y, ldy);
+        if (N <= 8192 && K <= 4096) {
+            return launch_q8_0_k<NC, 1>(W, N, K, rs, x, y, ldy, r, ldr, stream);
+        }
+        return launch_q8_0_k<NC, 2>(W, N, K, rs, x, y, ldy, r, ldr, stream);
     }
     if (wtype == TYPE_Q4_K) {
         constexpr int U4 = U > 2 ? 2 : U;
-        return launch_gemv(k_gemv_q4_K<NC, R, U4>, R, N, stream, W, N, K, rs, x.qs, x.d, x.bs, y, ldy);
+        return launch_gemv(k_gemv_q4_K<NC, R, U4>, R, N, stream, W, N, K, rs, x.qs, x.d, x.bs, y, ldy, r, ldr);
     }
     constexpr int U6 = 1;
     if (rs % 16 == 0 && ((uintptr_t) W) % 16 == 0) {
-        return launch_gemv(k_gemv_q6_K<NC, R, U6, true>, R, N, stream, W, N, K, rs, x.qs, x.d, x.bs, y, ldy);
+        return launch_gemv(k_gemv_q6_K<NC, R, U6, true>, R, N, stream, W, N, K, rs, x.qs, x.d, x.bs, y, ldy, r, ldr);
     }
-    return launch_gemv(k_gemv_q6_K<NC, R, U6, false>, R, N, stream, W, N, K, rs, x.qs, x.d, x.bs, y, ldy);
+    return launch_gemv(k_gemv_q6_K<NC, R, U6, false>, R, N, stream, W, N, K, rs, x.qs, x.d, x.bs, y, ldy, r, ldr);
 }
 
 bool gemv_supported(int wtype, int64_t N, int64_t K, int64_t rs, const void * W) {
     if (!(wtype == TYPE_Q8_0 || wtype == TYPE_Q4_K || wtype == TYPE_Q6_K) || K % 256 != 0 || N <= 0 ||
-        rs < row_bytes(wtype, K)) {
+        K > ((int64_t) 1 << 30) || rs < row_bytes(wtype, K)) {
         return false;
     }
     // Q8_0 / Q4_K rows are read with 16-byte loads; Q6_K rows may be 2-byte aligned
@@ -411,7 +460,7 @@ bool gemv_supported(int wtype, int64_t N, int64_t K, int64_t rs, const void * W)
 }
 
 int gemv_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const ActPtrs & x, int64_t M, float * y,
-           int64_t ldy, hipStream_t stream) {
+           int64_t ldy, hipStream_t stream, const float * r, int64_t ldr) {
     if (!gemv_supported(wtype, N, K, rs, W) || M < 1 || ldy < N) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "gemv: type %d N=%lld K=%lld M=%lld rs=%lld not supported", wtype,
                          (long long) N, (long long) K, (long long) M, (long long) rs);
@@ -422,16 +471,17 @@ int gemv_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const Ac
         const int64_t nc = std::min<int64_t>(mc, M - c0);
         ActPtrs       xs = x.slice(c0, K);
         float *       ys = y + c0 * ldy;
+        const float * rsl = r ? r + c0 * ldr : nullptr;
         int           rc;
         switch (nc) {
-            case 1: rc = gemv_dispatch<1>(wtype, wb, N, K, rs, xs, ys, ldy, stream); break;
-            case 2: rc = gemv_dispatch<2>(wtype, wb, N, K, rs, xs, ys, ldy, stream); break;
-            case 3: rc = gemv_dispatch<3>(wtype, wb, N, K, rs, xs, ys, ldy, stream); break;
-            case 4: rc = gemv_dispatch<4>(wtype, wb, N, K, rs, xs, ys, ldy, stream); break;
-            case 5: rc = gemv_dispatch<5>(wtype, wb, N, K, rs, xs, ys, ldy, stream); break;
-            case 6: rc = gemv_dispatch<6>(wtype, wb, N, K, rs, xs, ys, ldy, stream); break;
-            case 7: rc = gemv_dispatch<7>(wtype, wb, N, K, rs, xs, ys, ldy, stream); break;
-            default: rc = gemv_dispatch<8>(wtype, wb, N, K, rs, xs, ys, ldy, stream); break;
+            case 1: rc = gemv_dispatch<1>(wtype, wb, N, K, rs, xs, ys, ldy, rsl, ldr, stream); break;
+            case 2: rc = gemv_dispatch<2>(wtype, wb, N, K, rs, xs, ys, ldy, rsl, ldr, stream); break;
+            case 3: rc = gemv_dispatch<3>(wtype, wb, N, K, rs, xs, ys, ldy, rsl, ldr, stream); break;
+            case 4: rc = gemv_dispatch<4>(wtype, wb, N, K, rs, xs, ys, ldy, rsl, ldr, stream); break;
+            case 5: rc = gemv_dispatch<5>(wtype, wb, N, K, rs, xs, ys, ldy, rsl, ldr, stream); break;
+            case 6: rc = gemv_dispatch<6>(wtype, wb, N, K, rs, xs, ys, ldy, rsl, ldr, stream); break;
+            case 7: rc = gemv_dispatch<7>(wtype, wb, N, K, rs, xs, ys, ldy, rsl, ldr, stream); break;
+            default: rc = gemv_dispatch<8>(wtype, wb, N, K, rs, xs, ys, ldy, rsl, ldr, stream); break;
         }
         if (rc != MMHIP_OK) {
             return rc;
@@ -452,4 +502,15 @@ extern "C" int mmhip_mul_mat_q(int type, const void * W, int64_t N, int64_t K, i
         return set_error(MMHIP_ERR_INVALID, "mul_mat_q: bad arguments (type %d, K=%lld)", type, (long long) K);
     }
     return gemv_q(type, W, N, K, w_row_stride, ActPtrs::from(L, xq), M, y, ldy, (hipStream_t) stream);
+}
+
+extern "C" int mmhip_mul_mat_q_add(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride,
+                                   const void * xq, int64_t M, const float * r, int64_t ldr, float * y, int64_t ldy,
+                                   void * stream) {
+    MMHIP_API_BEGIN();
+    const ActLayout L = act_layout(type, K, M);
+    if (L.total == 0 || !xq || !W || !y || !r || ldr < N) {
+        return set_error(MMHIP_ERR_INVALID, "mul_mat_q_add: bad arguments (type %d, K=%lld)", type, (long long) K);
+    }
+    return gemv_q(type, W, N, K, w_row_stride, ActPtrs::from(L, xq), M, y, ldy, (hipStream_t) stream, r, ldr);
 }

@@ -29,14 +29,18 @@ static TV tv(const mmhip_view * v) {
     return t;
 }
 
-__device__ __forceinline__ void unravel(int64_t i, const int64_t * ne, int64_t & i0, int64_t & i1, int64_t & i2,
+// Element index -> (i0, i1, i2, i3).  Glue tensors are far below 2^31
+// elements (the API checks), so the divisions are 32-bit.
+__device__ __forceinline__ void unravel(int64_t i64, const int64_t * ne, int64_t & i0, int64_t & i1, int64_t & i2,
                                         int64_t & i3) {
-    i0 = i % ne[0];
-    i /= ne[0];
-    i1 = i % ne[1];
-    i /= ne[1];
-    i2 = i % ne[2];
-    i3 = i / ne[2];
+    uint32_t       i  = (uint32_t) i64;
+    const uint32_t n0 = (uint32_t) ne[0], n1 = (uint32_t) ne[1], n2 = (uint32_t) ne[2];
+    i0                = i % n0;
+    i /= n0;
+    i1 = i % n1;
+    i /= n1;
+    i2 = i % n2;
+    i3 = i / n2;
 }
 
 __device__ __forceinline__ char * at(const TV & t, int64_t i0, int64_t i1, int64_t i2, int64_t i3) {
@@ -54,6 +58,18 @@ static unsigned grid_for(int64_t n, int block) {
 // ---------------------------------------------------------------------------
 // binary ops, b broadcast over a (ggml_can_repeat(b, a))
 
+// contiguous a and b with b broadcast over whole rows of ne0 elements
+template <int OP>
+__global__ void k_binary_rows(const float * __restrict__ a, const float * __restrict__ b, float * __restrict__ dst,
+                              uint32_t n, uint32_t ne0, uint32_t b_rows) {
+#pragma clang fp contract(off)
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        const float x = a[i];
+        const float y = b[(i / ne0) % b_rows * ne0 + i % ne0];
+        dst[i]        = OP == 0 ? x + y : OP == 1 ? x - y : x * y;
+    }
+}
+
 template <int OP>
 __global__ void k_binary(TV a, TV b, float * __restrict__ dst, int64_t n) {
 #pragma clang fp contract(off)
@@ -67,27 +83,200 @@ __global__ void k_binary(TV a, TV b, float * __restrict__ dst, int64_t n) {
 }
 
 // ---------------------------------------------------------------------------
-// rms_norm (+ mul): one workgroup per row
+// Activation quantisation of a 256-element chunk held in registers, lane l
+// owning elements 4l .. 4l+3, with exactly the arithmetic of k_quant.hip
+// (ggml quantize_row_q8_0_ref / quantize_row_q8_K_ref):
+//   Q8_0: eight blocks of 32 (8 lanes each); d = amax/127 rounded to f16,
+//         q = roundf(x / d)
+//   Q8_K: one super-block; the first element of largest |x| gives
+//         iscale = -127 / x_max, q = min(127, nearest-even(iscale * x)),
+//         d = 1 / iscale, plus the sixteen 16-element sums of q.
+// qs, d, bs point at the chunk's first element / scale / sum.
 
+__device__ __forceinline__ void quant_chunk256(const float (&v)[4], int lane, int qtype, int8_t * __restrict__ qs,
+                                               float * __restrict__ d, int16_t * __restrict__ bs) {
+#pragma clang fp contract(off)
+    char4 q4;
+    if (qtype == TYPE_Q8_0) {
+        float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+        a       = fmaxf(a, __shfl_xor(a, 1, WAVE));
+        a       = fmaxf(a, __shfl_xor(a, 2, WAVE));
+        a       = fmaxf(a, __shfl_xor(a, 4, WAVE));
+        const float dd = a / 127.0f;
+        const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+        q4.x           = (signed char) roundf(v[0] * id);
+        q4.y           = (signed char) roundf(v[1] * id);
+        q4.z           = (signed char) roundf(v[2] * id);
+        q4.w           = (signed char) roundf(v[3] * id);
+        if ((lane & 7) == 0) {
+            d[lane >> 3] = h2f(f2h(dd));
+        }
+    } else {
+        float a = 0.0f, vm = 0.0f;
+        int   ix = 4 * lane;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float t = fabsf(v[k]);
+            if (t > a) {
+                a  = t;
+                vm = v[k];
+                ix = 4 * lane + k;
+            }
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            const float a2  = __shfl_xor(a, o, WAVE);
+            const float vm2 = __shfl_xor(vm, o, WAVE);
+            const int   ix2 = __shfl_xor(ix, o, WAVE);
+            if (a2 > a || (a2 == a && ix2 < ix)) {
+                a  = a2;
+                vm = vm2;
+                ix = ix2;
+            }
+        }
+        int   qv[4] = { 0, 0, 0, 0 };
+        float dd    = 0.0f;
+        if (a != 0.0f) {
+            const float iscale = -127.0f / vm;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int q = (int) rintf(iscale * v[k]);
+                qv[k]       = q > 127 ? 127 : q;
+            }
+            dd = 1.0f / iscale;
+        }
+        q4.x   = (signed char) qv[0];
+        q4.y   = (signed char) qv[1];
+        q4.z   = (signed char) qv[2];
+        q4.w   = (signed char) qv[3];
+        int sb = qv[0] + qv[1] + qv[2] + qv[3];
+        sb += __shfl_xor(sb, 1, WAVE);
+        sb += __shfl_xor(sb, 2, WAVE);
+        if ((lane & 3) == 0) {
+            bs[lane >> 2] = (int16_t) sb;
+        }
+        if (lane == 0) {
+            d[0] = dd;
+        }
+    }
+    *(char4 *) (qs + 4 * lane) = q4;
+}
+
+// Pointers of one quantised activation row (layout of act_layout()).
+struct QRow {
+    int8_t *  qs;
+    float *   d;
+    int16_t * bs;
+    int       qtype;
+    int       spb;  // scales per 256-element chunk: 8 (Q8_0) or 1 (Q8_K)
+
+    __device__ void chunk(const float (&v)[4], int lane, int c) const {
+        quant_chunk256(v, lane, qtype, qs + 256 * c, d + spb * c, bs ? bs + 16 * c : nullptr);
+    }
+};
+
+__device__ __forceinline__ QRow qrow(int qtype, int8_t * qs, float * d, int16_t * bs, int64_t row, int n) {
+    QRow r;
+    r.qtype = qtype;
+    r.spb   = qtype == TYPE_Q8_0 ? 8 : 1;
+    r.qs    = qs + row * n;
+    r.d     = d + row * (n / (qtype == TYPE_Q8_0 ? 32 : 256));
+    r.bs    = bs ? bs + row * (n / 16) : nullptr;
+    return r;
+}
+
+// ---------------------------------------------------------------------------
+// rms_norm (+ mul) (+ activation quantisation): one workgroup (4 waves) per
+// row of n f32 elements, n % 256 == 0, n <= 1024 * CPW.  The row splits into
+// 256-element chunks; wave w owns chunks w, w + 4, ..., lane l elements
+// 4l .. 4l+3 of each, so a chunk is exactly the quantisation unit of
+// quant_chunk256.  Every load of x and of the norm weight w (contiguous
+// vector of n) is issued before the reduction.  Squares are summed in double
+// and mean = sum / n rounded to f32, as ggml-CPU's RMS_NORM does.  With
+// xq_qs != nullptr the normalised row is also quantised for the GEMV that
+// consumes it.
+
+template <int CPW>  // chunks per wave
+__global__ __launch_bounds__(256) void k_rms_norm_row(const char * __restrict__ x, int64_t xs1, int64_t xs2,
+                                                      int64_t xs3, int ne1, int ne2, int n,
+                                                      const float * __restrict__ w, float eps,
+                                                      float * __restrict__ dst, int qtype, int8_t * __restrict__ xq_qs,
+                                                      float * __restrict__ xq_d, int16_t * __restrict__ xq_bs) {
+#pragma clang fp contract(off)
+    __shared__ double s_part[4];
+    const int     row  = (int) blockIdx.x;
+    const int     lane = threadIdx.x & 63;
+    const int     wv   = threadIdx.x >> 6;
+    const int     nch  = n / 256;
+    const int     i1 = row % ne1, i2 = (row / ne1) % ne2, i3 = row / (ne1 * ne2);
+    const float * xr = (const float *) (x + i1 * xs1 + i2 * xs2 + i3 * xs3);
+    float4_t      v[CPW], wq[CPW];
+#pragma unroll
+    for (int j = 0; j < CPW; j++) {
+        // chunks past the row end re-read the last chunk and are masked below
+        const int c = min(4 * j + wv, nch - 1);
+        v[j]        = *(const float4_t *) (xr + 256 * c + 4 * lane);
+        wq[j]       = w ? *(const float4_t *) (w + 256 * c + 4 * lane) : float4_t{ 1.0f, 1.0f, 1.0f, 1.0f };
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < CPW; j++) {
+        if (4 * j + wv < nch) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                ss += (double) (v[j][k] * v[j][k]);
+            }
+        }
+    }
+    ss = wave_sum_d(ss);
+    if (lane == 0) {
+        s_part[wv] = ss;
+    }
+    __syncthreads();
+    ss               = s_part[0] + s_part[1] + s_part[2] + s_part[3];
+    const float mean = (float) (ss / (double) n);
+    const float sc   = 1.0f / sqrtf(mean + eps);
+    const QRow  q    = xq_qs ? qrow(qtype, xq_qs, xq_d, xq_bs, row, n) : QRow{};
+#pragma unroll
+    for (int j = 0; j < CPW; j++) {
+        const int c = 4 * j + wv;
+        if (c < nch) {
+            float o[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const float t = v[j][k] * sc;
+                o[k]          = w ? t * wq[j][k] : t;
+            }
+            if (dst) {
+                *(float4_t *) (dst + (int64_t) row * n + 256 * c + 4 * lane) = float4_t{ o[0], o[1], o[2], o[3] };
+            }
+            if (xq_qs) {
+                q.chunk(o, lane, c);
+            }
+        }
+    }
+}
+
+// generic fallback: any strides and any broadcast of w (one workgroup per row)
 __global__ __launch_bounds__(256) void k_rms_norm(TV x, TV w, int has_w, float eps, float * __restrict__ dst) {
 #pragma clang fp contract(off)
-    __shared__ float s_part[4];
-    const int64_t    row = blockIdx.x;
-    const int64_t    i1 = row % x.ne[1], i2 = (row / x.ne[1]) % x.ne[2], i3 = row / (x.ne[1] * x.ne[2]);
-    const int64_t    n  = x.ne[0];
-    const char *     xr = at(x, 0, i1, i2, i3);
-    float            ss = 0.0f;
+    __shared__ double s_part[4];
+    const int64_t     row = blockIdx.x;
+    const int64_t     i1 = row % x.ne[1], i2 = (row / x.ne[1]) % x.ne[2], i3 = row / (x.ne[1] * x.ne[2]);
+    const int64_t     n  = x.ne[0];
+    const char *      xr = at(x, 0, i1, i2, i3);
+    double            ss = 0.0;
     for (int64_t i = threadIdx.x; i < n; i += 256) {
         const float v = *(const float *) (xr + i * x.nb[0]);
-        ss += v * v;
+        ss += (double) (v * v);
     }
-    ss = wave_sum(ss);
+    ss = wave_sum_d(ss);
     if ((threadIdx.x & 63) == 0) {
         s_part[threadIdx.x >> 6] = ss;
     }
     __syncthreads();
     ss               = s_part[0] + s_part[1] + s_part[2] + s_part[3];
-    const float mean = ss / (float) n;
+    const float mean = (float) (ss / (double) n);
     const float sc   = 1.0f / sqrtf(mean + eps);
     float *     dr   = dst + row * n;
     for (int64_t i = threadIdx.x; i < n; i += 256) {
@@ -97,6 +286,89 @@ __global__ __launch_bounds__(256) void k_rms_norm(TV x, TV w, int has_w, float e
             dr[i]          = t * wv;
         } else {
             dr[i] = t;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Per-head rows of the QKV projection (the CONT / RMS_NORM / MUL / ROPE /
+// SET_ROWS chain of the attention block): one wave per row (h, t) of D = 64 *
+// EPL f32 elements, lane l owning elements EPL*l .. EPL*l + EPL-1, so the NeoX
+// partner of element i < D/2 (i + D/2) sits in lane l ^ 32.
+
+template <int EPL>
+__global__ __launch_bounds__(256) void k_head_rows(mmhip_head_rows_args a) {
+#pragma clang fp contract(off)
+    constexpr int D    = 64 * EPL;
+    const int     row  = (int) blockIdx.x * 4 + ((int) threadIdx.x >> 6);
+    const int     lane = threadIdx.x & 63;
+    if (row >= a.H * a.T) {
+        return;
+    }
+    const int     h  = row % a.H;
+    const int     t  = row / a.H;
+    const float * xr = (const float *) ((const char *) a.src + h * a.src_nb_h + t * a.src_nb_t);
+    // every load up front (absent operands read a valid stand-in and are unused)
+    const float *   wp = a.norm_w ? a.norm_w : xr;
+    const int32_t * pp = a.pos ? a.pos + t : (const int32_t *) xr;
+    const char *    ip = a.ids ? (const char *) a.ids + (h % a.ids_ne1) * a.ids_nb1 + (t % a.ids_ne2) * a.ids_nb2
+                               : (const char *) xr;
+    float v[EPL], wv[EPL];
+#pragma unroll
+    for (int k = 0; k < EPL; k++) {
+        v[k]  = xr[EPL * lane + k];
+        wv[k] = wp[EPL * lane + k];
+    }
+    const int32_t p_t    = *pp;
+    const int64_t id_raw = a.ids_type == 27 ? *(const int64_t *) ip : (int64_t) *(const int32_t *) ip;
+    if (a.norm) {
+        double ss = 0.0;
+#pragma unroll
+        for (int k = 0; k < EPL; k++) {
+            ss += (double) (v[k] * v[k]);
+        }
+        ss               = wave_sum_d(ss);
+        const float mean = (float) (ss / (double) D);
+        const float sc   = 1.0f / sqrtf(mean + a.eps);
+#pragma unroll
+        for (int k = 0; k < EPL; k++) {
+            const float y = v[k] * sc;
+            v[k]          = a.norm_w ? y * wv[k] : y;
+        }
+    }
+    if (a.pos) {
+        // theta_i = pos * theta_scale^i, the power taken by repeated f32
+        // multiplication as ggml-CPU's rope cache does
+        const int   i0    = EPL * (lane & 31);
+        float       theta = (float) p_t;
+        for (int k = 0; k < i0; k++) {
+            theta *= a.theta_scale;
+        }
+        const bool upper = lane >= 32;
+#pragma unroll
+        for (int k = 0; k < EPL; k++) {
+            const float other = __shfl_xor(v[k], 32, WAVE);
+            const float c = cosf(theta), s = sinf(theta);
+            // lower lane holds x0 (element i), upper lane x1 (element i + D/2)
+            v[k]  = upper ? other * s + v[k] * c : v[k] * c - other * s;
+            theta *= a.theta_scale;
+        }
+    }
+    if (!a.ids) {
+        float * dr = (float *) a.dst + (int64_t) row * D;
+#pragma unroll
+        for (int k = 0; k < EPL; k++) {
+            dr[EPL * lane + k] = v[k];
+        }
+        return;
+    }
+    char * dp = (char *) a.dst + id_raw * a.dst_nb1 + h * a.dst_nb2 + t * a.dst_nb3;
+#pragma unroll
+    for (int k = 0; k < EPL; k++) {
+        if (a.dst_type == TYPE_F32) {
+            ((float *) dp)[EPL * lane + k] = v[k];
+        } else {
+            ((uint16_t *) dp)[EPL * lane + k] = f2h(v[k]);
         }
     }
 }
@@ -140,6 +412,17 @@ __global__ void k_rope_neox(TV x, const int32_t * __restrict__ pos, int n_dims, 
 
 // ---------------------------------------------------------------------------
 // copy with conversion between f32 / f16 (any strides on both sides)
+
+__global__ void k_cpy_linear(const char * __restrict__ src, int st, char * __restrict__ dst, int dt, uint32_t n) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        const float v = st == TYPE_F32 ? ((const float *) src)[i] : h2f(((const uint16_t *) src)[i]);
+        if (dt == TYPE_F32) {
+            ((float *) dst)[i] = v;
+        } else {
+            ((uint16_t *) dst)[i] = f2h(v);
+        }
+    }
+}
 
 __global__ void k_cpy(TV src, int st, TV dst, int dt, int64_t n) {
     for (int64_t i = blockIdx.x * (int64_t) blockDim.x + threadIdx.x; i < n; i += (int64_t) gridDim.x * blockDim.x) {
@@ -260,6 +543,44 @@ __global__ void k_swiglu(TV a, TV b, int split, int swapped, float * __restrict_
     }
 }
 
+// SwiGLU of contiguous f32 rows with the result also quantised for the down
+// projection's GEMV: one wave per 256-element chunk of an output row.
+__global__ __launch_bounds__(256) void k_swiglu_quant(const char * __restrict__ a, int64_t a_nb1,
+                                                      const char * __restrict__ b, int64_t b_nb1, int F, int T,
+                                                      int swapped, float * __restrict__ dst, int qtype,
+                                                      int8_t * __restrict__ xq_qs, float * __restrict__ xq_d,
+                                                      int16_t * __restrict__ xq_bs) {
+#pragma clang fp contract(off)
+    const int chunks = F / 256;
+    const int wid    = (int) blockIdx.x * 4 + ((int) threadIdx.x >> 6);
+    const int lane   = threadIdx.x & 63;
+    if (wid >= chunks * T) {
+        return;
+    }
+    const int     row = wid / chunks;
+    const int     c   = wid % chunks;
+    const int     e   = 256 * c + 4 * lane;
+    const float * ar  = (const float *) (a + (int64_t) row * a_nb1);
+    float4_t      g, u;
+    if (b) {
+        g = *(const float4_t *) (ar + e);
+        u = *(const float4_t *) ((const float *) (b + (int64_t) row * b_nb1) + e);
+    } else {
+        g = *(const float4_t *) (ar + (swapped ? e + F : e));
+        u = *(const float4_t *) (ar + (swapped ? e : e + F));
+    }
+    float v[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float silu = g[k] / (1.0f + expf(-g[k]));
+        v[k]             = silu * u[k];
+    }
+    if (dst) {
+        *(float4_t *) (dst + (int64_t) row * F + e) = float4_t{ v[0], v[1], v[2], v[3] };
+    }
+    qrow(qtype, xq_qs, xq_d, xq_bs, row, F).chunk(v, lane, c);
+}
+
 __global__ void k_scale(TV a, float s, float bias, float * __restrict__ dst, int64_t n) {
 #pragma clang fp contract(off)
     for (int64_t i = blockIdx.x * (int64_t) blockDim.x + threadIdx.x; i < n; i += (int64_t) gridDim.x * blockDim.x) {
@@ -267,6 +588,18 @@ __global__ void k_scale(TV a, float s, float bias, float * __restrict__ dst, int
         unravel(i, a.ne, i0, i1, i2, i3);
         dst[i] = *(const float *) at(a, i0, i1, i2, i3) * s + bias;
     }
+}
+
+// contiguous view of elements of `es` bytes
+static bool is_contig(const mmhip_view * v, int64_t es) {
+    int64_t expect = es;
+    for (int i = 0; i < 4; i++) {
+        if (v->ne[i] != 1 && v->nb[i] != expect) {
+            return false;
+        }
+        expect *= v->ne[i];
+    }
+    return true;
 }
 
 static bool broadcasts(const mmhip_view * b, const mmhip_view * a) {
@@ -291,7 +624,30 @@ extern "C" int mmhip_binary(int op, const mmhip_view * a, const mmhip_view * b, 
     if (n == 0) {
         return MMHIP_OK;
     }
+    if (n >= ((int64_t) 1 << 31)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "binary: too many elements");
+    }
     const dim3 g(grid_for(n, 256));
+    if (is_contig(a, 4) && is_contig(b, 4) && b->ne[0] == a->ne[0]) {
+        const uint32_t b_rows = (uint32_t) (nel(b) / b->ne[0]);
+        const uint32_t a_rows = (uint32_t) (n / a->ne[0]);
+        if (b_rows == 1 || (b->ne[1] == a->ne[1] && b->ne[2] == a->ne[2] && a_rows % b_rows == 0)) {
+            const float * ap = (const float *) a->data;
+            const float * bp = (const float *) b->data;
+            const uint32_t ne0 = (uint32_t) a->ne[0];
+            if (op == 0) {
+                hipLaunchKernelGGL(k_binary_rows<0>, g, dim3(256), 0, (hipStream_t) stream, ap, bp, dst, (uint32_t) n,
+                                   ne0, b_rows);
+            } else if (op == 1) {
+                hipLaunchKernelGGL(k_binary_rows<1>, g, dim3(256), 0, (hipStream_t) stream, ap, bp, dst, (uint32_t) n,
+                                   ne0, b_rows);
+            } else {
+                hipLaunchKernelGGL(k_binary_rows<2>, g, dim3(256), 0, (hipStream_t) stream, ap, bp, dst, (uint32_t) n,
+                                   ne0, b_rows);
+            }
+            return check_launch("binary");
+        }
+    }
     if (op == 0) {
         hipLaunchKernelGGL(k_binary<0>, g, dim3(256), 0, (hipStream_t) stream, tv(a), tv(b), dst, n);
     } else if (op == 1) {
@@ -302,22 +658,82 @@ extern "C" int mmhip_binary(int op, const mmhip_view * a, const mmhip_view * b, 
     return check_launch("binary");
 }
 
+namespace mmhip {
+// Row kernel when rows are contiguous and w (if any) is a plain vector of the
+// row length; launches the quantising variant when xq is given.
+static int rms_norm_launch(const mmhip_view * x, const mmhip_view * w, float eps, float * dst, int qtype,
+                           void * xq, hipStream_t stream) {
+    const int64_t rows = x->ne[1] * x->ne[2] * x->ne[3];
+    const int64_t n    = x->ne[0];
+    if (rows == 0 || n == 0) {
+        return MMHIP_OK;
+    }
+    const bool w_vec = !w || (is_contig(w, 4) && w->ne[0] == n && w->ne[1] * w->ne[2] * w->ne[3] == 1 &&
+                              ((uintptr_t) w->data) % 16 == 0);
+    const bool fast  = x->nb[0] == 4 && n % 256 == 0 && n <= 16384 && w_vec && rows < (1 << 30) &&
+                      ((uintptr_t) x->data | (uintptr_t) x->nb[1] | (uintptr_t) x->nb[2] | (uintptr_t) x->nb[3]) % 16 == 0 &&
+                      (!dst || ((uintptr_t) dst) % 16 == 0);
+    if (xq && !fast) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "rms_norm_quant: row layout not supported");
+    }
+    if (!fast) {
+        if (!dst) {
+            return set_error(MMHIP_ERR_INVALID, "rms_norm: no destination");
+        }
+        TV wv = w ? tv(w) : TV{};
+        hipLaunchKernelGGL(k_rms_norm, dim3((unsigned) rows), dim3(256), 0, stream, tv(x), wv, w ? 1 : 0, eps, dst);
+        return check_launch("rms_norm");
+    }
+    int8_t *  qs = nullptr;
+    float *   qd = nullptr;
+    int16_t * qb = nullptr;
+    if (xq) {
+        const ActLayout L = act_layout(qtype, n, rows);
+        if (L.total == 0) {
+            return set_error(MMHIP_ERR_UNSUPPORTED, "rms_norm_quant: weight type %d", qtype);
+        }
+        qs    = (int8_t *) xq + L.qs_off;
+        qd    = (float *) ((char *) xq + L.d_off);
+        qb    = L.vec_type == TYPE_Q8_K ? (int16_t *) ((char *) xq + L.bs_off) : nullptr;
+        qtype = L.vec_type;
+    }
+    const dim3    grid((unsigned) rows);
+    const float * wp = w ? (const float *) w->data : nullptr;
+    const int     ne1 = (int) x->ne[1], ne2 = (int) x->ne[2];
+#define MM_RMS(CPW)                                                                                              \
+    hipLaunchKernelGGL(k_rms_norm_row<CPW>, grid, dim3(256), 0, stream, (const char *) x->data, x->nb[1], x->nb[2], \
+                       x->nb[3], ne1, ne2, (int) n, wp, eps, dst, qtype, qs, qd, qb)
+    if (n <= 1024) {
+        MM_RMS(1);
+    } else if (n <= 2048) {
+        MM_RMS(2);
+    } else if (n <= 4096) {
+        MM_RMS(4);
+    } else if (n <= 8192) {
+        MM_RMS(8);
+    } else {
+        MM_RMS(16);
+    }
+#undef MM_RMS
+    return check_launch("rms_norm");
+}
+}  // namespace mmhip
+
 extern "C" int mmhip_rms_norm(const mmhip_view * x, const mmhip_view * w, float eps, float * dst, void * stream) {
     MMHIP_API_BEGIN();
     if (!x || !dst || (w && !broadcasts(w, x))) {
         return set_error(MMHIP_ERR_INVALID, "rms_norm: bad arguments");
     }
-    const int64_t rows = x->ne[1] * x->ne[2] * x->ne[3];
-    if (rows == 0 || x->ne[0] == 0) {
-        return MMHIP_OK;
+    return rms_norm_launch(x, w, eps, dst, 0, nullptr, (hipStream_t) stream);
+}
+
+extern "C" int mmhip_rms_norm_quant(const mmhip_view * x, const mmhip_view * w, float eps, float * dst, int type,
+                                    void * xq, void * stream) {
+    MMHIP_API_BEGIN();
+    if (!x || !xq || (w && !broadcasts(w, x))) {
+        return set_error(MMHIP_ERR_INVALID, "rms_norm_quant: bad arguments");
     }
-    if (rows > 0x7fffffff) {
-        return set_error(MMHIP_ERR_UNSUPPORTED, "rms_norm: too many rows");
-    }
-    TV wv = w ? tv(w) : TV{};
-    hipLaunchKernelGGL(k_rms_norm, dim3((unsigned) rows), dim3(256), 0, (hipStream_t) stream, tv(x), wv, w ? 1 : 0, eps,
-                       dst);
-    return check_launch("rms_norm");
+    return rms_norm_launch(x, w, eps, dst, type, xq, (hipStream_t) stream);
 }
 
 extern "C" int mmhip_rope_neox(const mmhip_view * x, const int32_t * pos, int n_dims, float theta_scale, float * dst,
@@ -345,6 +761,15 @@ extern "C" int mmhip_cpy(const mmhip_view * src, int src_type, const mmhip_view 
     const int64_t n = nel(src);
     if (n == 0) {
         return MMHIP_OK;
+    }
+    if (n >= ((int64_t) 1 << 31)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "cpy: too many elements");
+    }
+    const int64_t ss = src_type == TYPE_F32 ? 4 : 2, ds = dst_type == TYPE_F32 ? 4 : 2;
+    if (is_contig(src, ss) && is_contig(dst, ds)) {
+        hipLaunchKernelGGL(k_cpy_linear, dim3(grid_for(n, 256)), dim3(256), 0, (hipStream_t) stream,
+                           (const char *) src->data, src_type, (char *) dst->data, dst_type, (uint32_t) n);
+        return check_launch("cpy");
     }
     hipLaunchKernelGGL(k_cpy, dim3(grid_for(n, 256)), dim3(256), 0, (hipStream_t) stream, tv(src), src_type, tv(dst),
                        dst_type, n);
@@ -414,4 +839,65 @@ extern "C" int mmhip_scale(const mmhip_view * a, float s, float bias, float * ds
     }
     hipLaunchKernelGGL(k_scale, dim3(grid_for(n, 256)), dim3(256), 0, (hipStream_t) stream, tv(a), s, bias, dst, n);
     return check_launch("scale");
+}
+
+extern "C" int mmhip_swiglu_quant(const mmhip_view * a, const mmhip_view * b, int swapped, float * dst, int type,
+                                  void * xq, void * stream) {
+    MMHIP_API_BEGIN();
+    if (!a || !xq) {
+        return set_error(MMHIP_ERR_INVALID, "swiglu_quant: bad arguments");
+    }
+    const int64_t F = b ? a->ne[0] : a->ne[0] / 2;
+    const int64_t T = a->ne[1] * a->ne[2] * a->ne[3];
+    const bool rows_ok = a->nb[0] == 4 && a->nb[2] == a->nb[1] * a->ne[1] && a->nb[3] == a->nb[2] * a->ne[2] &&
+                         (b ? true : a->ne[0] % 2 == 0) && a->nb[1] % 16 == 0 && ((uintptr_t) a->data) % 16 == 0;
+    const bool b_ok = !b || (b->ne[0] == a->ne[0] && b->ne[1] * b->ne[2] * b->ne[3] == T && b->nb[0] == 4 &&
+                             b->nb[2] == b->nb[1] * b->ne[1] && b->nb[3] == b->nb[2] * b->ne[2] &&
+                             b->nb[1] % 16 == 0 && ((uintptr_t) b->data) % 16 == 0);
+    if (!rows_ok || !b_ok || F % 256 != 0 || T * F >= ((int64_t) 1 << 31) || (dst && ((uintptr_t) dst) % 16 != 0)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "swiglu_quant: layout not supported");
+    }
+    const ActLayout L = act_layout(type, F, T);
+    if (L.total == 0) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "swiglu_quant: weight type %d", type);
+    }
+    if (T == 0) {
+        return MMHIP_OK;
+    }
+    const int64_t waves = T * (F / 256);
+    hipLaunchKernelGGL(k_swiglu_quant, dim3((unsigned) ((waves + 3) / 4)), dim3(256), 0, (hipStream_t) stream,
+                       (const char *) a->data, a->nb[1], b ? (const char *) b->data : nullptr, b ? b->nb[1] : 0,
+                       (int) F, (int) T, swapped, dst, L.vec_type, (int8_t *) xq + L.qs_off,
+                       (float *) ((char *) xq + L.d_off),
+                       L.vec_type == TYPE_Q8_K ? (int16_t *) ((char *) xq + L.bs_off) : nullptr);
+    return check_launch("swiglu_quant");
+}
+
+extern "C" int mmhip_head_rows(const mmhip_head_rows_args * a, void * stream) {
+    MMHIP_API_BEGIN();
+    if (!a || !a->src || !a->dst || a->H <= 0 || a->T < 0) {
+        return set_error(MMHIP_ERR_INVALID, "head_rows: bad arguments");
+    }
+    if (!(a->D == 64 || a->D == 128 || a->D == 256) || (int64_t) a->H * a->T >= ((int64_t) 1 << 30)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "head_rows: D=%d H=%d T=%d not supported", a->D, a->H, a->T);
+    }
+    if (a->ids && (a->ids_ne1 <= 0 || a->ids_ne2 <= 0 || !(a->ids_type == 26 || a->ids_type == 27) ||
+                   !(a->dst_type == TYPE_F32 || a->dst_type == TYPE_F16))) {
+        return set_error(MMHIP_ERR_INVALID, "head_rows: bad row ids / destination type");
+    }
+    if (!a->ids && a->dst_type != TYPE_F32) {
+        return set_error(MMHIP_ERR_INVALID, "head_rows: contiguous output is f32");
+    }
+    if (a->T == 0) {
+        return MMHIP_OK;
+    }
+    const dim3 grid((unsigned) (((int64_t) a->H * a->T + 3) / 4));
+    if (a->D == 64) {
+        hipLaunchKernelGGL(k_head_rows<1>, grid, dim3(256), 0, (hipStream_t) stream, *a);
+    } else if (a->D == 128) {
+        hipLaunchKernelGGL(k_head_rows<2>, grid, dim3(256), 0, (hipStream_t) stream, *a);
+    } else {
+        hipLaunchKernelGGL(k_head_rows<4>, grid, dim3(256), 0, (hipStream_t) stream, *a);
+    }
+    return check_launch("head_rows");
 }

@@ -61,7 +61,7 @@ __global__ void k_synth_gguf(int type, uint8_t * __restrict__ dst, int64_t nbloc
                 const uint64_t h = hash2(seed ^ 0x5c5cull, base + (uint64_t) j);
                 p[192 + j]       = (uint8_t) (int8_t) ((int) (h % 128u) - 64);
             }
-            const uint16_t d = f2h(fabsf(normal01(seed ^ 0xd0d0ull, (uint64_t) b)) * 0.02f / 64.0f);
+            const uint16_t d = f2h(fabsf(normal01(seed ^ 0xd0d0ull, (uint64_t) b)) * 0.02f / 1024.0f);
             p[208]           = (uint8_t) (d & 0xff);
             p[209]           = (uint8_t) (d >> 8);
         }

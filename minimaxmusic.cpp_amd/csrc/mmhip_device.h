@@ -63,6 +63,15 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// double-precision wave sum (ggml-CPU accumulates RMS_NORM's squares in double)
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        v += __shfl_xor(v, o, WAVE);
+    }
+    return v;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {

@@ -76,7 +76,7 @@ struct ActPtrs {
 // Quantized GEMV on pre-quantised activations (any M; column groups of <= 8).
 bool gemv_supported(int wtype, int64_t N, int64_t K, int64_t row_stride, const void * W);
 int  gemv_q(int wtype, const void * W, int64_t N, int64_t K, int64_t row_stride, const ActPtrs & x, int64_t M, float * y,
-            int64_t ldy, hipStream_t stream);
+            int64_t ldy, hipStream_t stream, const float * r = nullptr, int64_t ldr = 0);
 
 // MFMA GEMM with in-LDS dequantisation (any M).
 int gemm_q(int wtype, const void * W, int64_t N, int64_t K, int64_t row_stride, const float * x, int64_t ldx, int64_t M,

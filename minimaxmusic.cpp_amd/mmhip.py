@@ -38,6 +38,17 @@ class MmhipView(ctypes.Structure):
     _fields_ = [("data", ctypes.c_void_p), ("ne", ctypes.c_int64 * 4), ("nb", ctypes.c_int64 * 4)]
 
 
+class HeadRowsArgs(ctypes.Structure):
+    """mmhip_head_rows_args (include/mmhip.h)."""
+    _fields_ = [("src", ctypes.c_void_p), ("src_nb_h", ctypes.c_int64), ("src_nb_t", ctypes.c_int64),
+                ("D", ctypes.c_int), ("H", ctypes.c_int), ("T", ctypes.c_int), ("norm", ctypes.c_int),
+                ("norm_w", ctypes.c_void_p), ("eps", ctypes.c_float), ("pos", ctypes.c_void_p),
+                ("theta_scale", ctypes.c_float), ("dst", ctypes.c_void_p), ("dst_type", ctypes.c_int),
+                ("ids", ctypes.c_void_p), ("ids_type", ctypes.c_int), ("ids_nb1", ctypes.c_int64),
+                ("ids_nb2", ctypes.c_int64), ("ids_ne1", ctypes.c_int64), ("ids_ne2", ctypes.c_int64),
+                ("dst_nb1", ctypes.c_int64), ("dst_nb2", ctypes.c_int64), ("dst_nb3", ctypes.c_int64)]
+
+
 # Every symbol include/mmhip.h declares, with (restype, argtypes).
 _vp, _i64, _i32, _f32, _sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
 _VP = ctypes.POINTER(MmhipView)
@@ -52,8 +63,23 @@ SIGNATURES = {
     "mmhip_act_bytes": (_sz, [_i32, _i64, _i64]),
     "mmhip_quantize_act": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _vp]),
     "mmhip_mul_mat_q": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp]),
+    "mmhip_mul_mat_q_add": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp]),
     "mmhip_flash_attn_workspace": (_sz, [_VP, _VP, _VP]),
     "mmhip_flash_attn_ext": (_i32, [_VP, _VP, _VP, _VP, _f32, _vp, _vp, _sz, _vp]),
+    "mmhip_binary": (_i32, [_i32, _VP, _VP, _vp, _vp]),
+    "mmhip_rms_norm": (_i32, [_VP, _VP, _f32, _vp, _vp]),
+    "mmhip_rms_norm_quant": (_i32, [_VP, _VP, _f32, _vp, _i32, _vp, _vp]),
+    "mmhip_head_rows": (_i32, [ctypes.c_void_p, _vp]),
+    "mmhip_swiglu_quant": (_i32, [_VP, _VP, _i32, _vp, _i32, _vp, _vp]),
+    "mmhip_rope_neox": (_i32, [_VP, _vp, _i32, _f32, _vp, _vp]),
+    "mmhip_cpy": (_i32, [_VP, _i32, _VP, _i32, _vp]),
+    "mmhip_get_rows": (_i32, [_i32, _VP, _VP, _vp, _vp]),
+    "mmhip_set_rows": (_i32, [_VP, _VP, _i32, _VP, _i32, _vp]),
+    "mmhip_swiglu": (_i32, [_VP, _VP, _i32, _vp, _vp]),
+    "mmhip_scale": (_i32, [_VP, _f32, _f32, _vp, _vp]),
+    # include/mmhip_synth.h
+    "mmhip_synth_gguf": (_i32, [_i32, _vp, _i64, ctypes.c_uint64, _vp]),
+    "mmhip_synth_normal": (_i32, [_i32, _vp, _i64, ctypes.c_uint64, _f32, _f32, _vp]),
 }
 
 _lib = None

@@ -7,7 +7,7 @@ distributions used for every measurement here:
 * Q4_K: 4-bit quants and 6-bit (scale, min) pairs uniform (random bytes);
   d, dmin = f16(|N(0, 0.02)|).
 * Q6_K: low/high quant bits uniform (random bytes); int8 scales uniform in
-  [-64, 63]; d = f16(|N(0, 0.02)| / 64).
+  [-64, 63]; d = f16(|N(0, 0.02)| / 1024), so |w| ~ 0.01 like real weights.
 
 ``*_np`` build host numpy bytes (parity tests); ``gguf_blocks_torch`` builds
 the same distributions directly in device memory (large benchmarks).
@@ -41,7 +41,7 @@ def gguf_blocks_np(qtype, N, K, seed):
     elif qtype == Q6_K:
         sc = rng.integers(-64, 64, size=(nb, 16), dtype=np.int16).astype(np.int8)
         blk[:, 192:208] = sc.view(np.uint8)
-        blk[:, 208:210] = _scale_bits(rng, nb, 64.0).view(np.uint8).reshape(nb, 2)
+        blk[:, 208:210] = _scale_bits(rng, nb, 1024.0).view(np.uint8).reshape(nb, 2)
     return blk.reshape(-1)
 
 
@@ -69,7 +69,7 @@ def gguf_blocks_torch(qtype, N, K, seed, device="cuda"):
     elif qtype == Q6_K:
         sc = torch.randint(-64, 64, (nb, 16), dtype=torch.int8, device=device, generator=g)
         blk[:, 192:208] = sc.view(torch.uint8)
-        blk[:, 208:210] = scale(64.0)
+        blk[:, 208:210] = scale(1024.0)
     return blk.view(-1)
 
 

@@ -13,6 +13,12 @@ def declared_functions(header):
     return sorted(set(re.findall(r"\b(mmhip_[a-z0-9_]+)\s*\(", text)))
 
 
+def declared(header, prefix):
+    text = re.sub(r"/\*.*?\*/", "", (ROOT / "include" / header).read_text(), flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    return sorted(set(re.findall(r"\b(" + prefix + r"[a-z0-9_]+)\s*\(", text)))
+
+
 def test_header_symbols_exported(pkg):
     import __graft_entry__
 
@@ -20,11 +26,29 @@ def test_header_symbols_exported(pkg):
     if not lib.exists():
         __graft_entry__.build()
     L = ctypes.CDLL(str(lib))
-    names = declared_functions(ROOT / "include" / "mmhip.h")
-    assert len(names) >= 12
+    names = declared_functions(ROOT / "include" / "mmhip.h") + declared("mmhip_synth.h", "mmhip_")
+    assert len(names) >= 20
     for n in names:
         assert hasattr(L, n), n
         assert n in pkg.mmhip.SIGNATURES, f"{n} missing from the Python binding"
+
+
+def test_backend_and_lm_symbols_exported(pkg):
+    libdir = pkg.mmhip.LIB_PATH.parent
+    base = ctypes.CDLL(str(libdir / "libggml-base.so"), mode=ctypes.RTLD_GLOBAL)
+    be = ctypes.CDLL(str(libdir / "libggml-mi355x.so"))
+    for n in declared("ggml-mi355x.h", "ggml_backend_"):
+        assert hasattr(be, n), n
+    # dynamic-loading entry points of a ggml backend
+    assert hasattr(be, "ggml_backend_init") and hasattr(be, "ggml_backend_score")
+    for n in ("ggml_backend_graph_compute", "ggml_backend_tensor_set", "ggml_gallocr_alloc_graph",
+              "ggml_flash_attn_ext", "ggml_mul_mat", "ggml_backend_load_all"):
+        assert hasattr(base, n), n
+    lm = ctypes.CDLL(str(libdir / "libmm_lm.so"))
+    names = declared("mm_lm.h", "mm_lm_")
+    assert len(names) >= 12
+    for n in names:
+        assert hasattr(lm, n), n
 
 
 def test_error_reporting_without_gpu(pkg):

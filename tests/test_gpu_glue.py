@@ -1,0 +1,292 @@
+"""GPU: decode-step glue kernels against the oracle / closed forms.
+
+Tolerances (stated): binary ops, copies, set_rows, get_rows bit-exact;
+rms_norm and swiglu max-rel 1e-5 (f32 reduction order, libm expf vs device
+expf); rope max-abs 2e-5 at positions up to 5000 (libm vs device cosf/sinf of
+the same f32 angle)."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def st():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def ptr(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def test_binary_broadcast(mm):
+    L = mm.load()
+    rng = np.random.default_rng(1)
+    a = rng.standard_normal((2, 3, 5, 64)).astype(np.float32)
+    b = rng.standard_normal((1, 3, 1, 64)).astype(np.float32)
+    ta, tb = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+    for op, ref in ((0, a + b), (1, a - b), (2, a * b)):
+        out = torch.empty_like(ta)
+        assert L.mmhip_binary(op, ctypes.byref(mm.view_of(ta)), ctypes.byref(mm.view_of(tb)), ptr(out), st()) == 0
+        assert np.array_equal(out.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("with_w", [False, True])
+def test_rms_norm(mm, orc, with_w):
+    L = mm.load()
+    rng = np.random.default_rng(2)
+    x = (rng.standard_normal((2, 32, 128)) * 3).astype(np.float32)
+    w = (1 + 0.02 * rng.standard_normal(128)).astype(np.float32)
+    tx, tw = torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda()
+    out = torch.empty_like(tx)
+    wv = ctypes.byref(mm.view_of(tw)) if with_w else None
+    assert L.mmhip_rms_norm(ctypes.byref(mm.view_of(tx)), wv, 1e-6, ptr(out), st()) == 0
+    ref = orc.rms_norm_mul(x, w if with_w else None, 1e-6)
+    assert rel_err(out.cpu().numpy(), ref) < 1e-5
+
+
+def test_rope_neox(mm, orc):
+    L = mm.load()
+    rng = np.random.default_rng(3)
+    T, H, D = 4, 8, 128
+    x = rng.standard_normal((T, H, D)).astype(np.float32)
+    pos = np.array([0, 1, 4095, 5000], np.int32)
+    tx, tp = torch.from_numpy(x).cuda(), torch.from_numpy(pos).cuda()
+    out = torch.empty_like(tx)
+    # the backend computes powf(base, -2/n_dims) on the host, as ggml-CPU does
+    theta_scale = float(np.power(np.float32(1e6), np.float32(-2.0) / np.float32(D)))
+    assert L.mmhip_rope_neox(ctypes.byref(mm.view_of(tx)), ptr(tp), D, ctypes.c_float(theta_scale), ptr(out), st()) == 0
+    ref = orc.rope_neox(x, pos, D, 1e6)
+    assert np.abs(out.cpu().numpy() - ref).max() < 2e-5
+    # partial rotation (DiT: 32 of 64 dims) leaves the tail unchanged
+    x2 = rng.standard_normal((3, 4, 64)).astype(np.float32)
+    t2 = torch.from_numpy(x2).cuda()
+    o2 = torch.empty_like(t2)
+    p2 = torch.tensor([5, 6, 7], dtype=torch.int32, device="cuda")
+    ts2 = float(np.power(np.float32(1e4), np.float32(-2.0) / np.float32(32)))
+    assert L.mmhip_rope_neox(ctypes.byref(mm.view_of(t2)), ptr(p2), 32, ctypes.c_float(ts2), ptr(o2), st()) == 0
+    r2 = orc.rope_neox(x2, np.array([5, 6, 7], np.int32), 32, 1e4)
+    assert np.abs(o2.cpu().numpy() - r2).max() < 2e-5
+    assert np.array_equal(o2.cpu().numpy()[..., 32:], x2[..., 32:])
+
+
+@pytest.mark.parametrize("split", [False, True])
+def test_swiglu(mm, orc, split):
+    L = mm.load()
+    rng = np.random.default_rng(4)
+    a = (rng.standard_normal((2, 1024)) * 4).astype(np.float32)
+    ta = torch.from_numpy(a).cuda()
+    if split:
+        out = torch.empty((2, 512), device="cuda")
+        g, u = ta[:, :512].contiguous(), ta[:, 512:].contiguous()
+        assert L.mmhip_swiglu(ctypes.byref(mm.view_of(g)), ctypes.byref(mm.view_of(u)), 0, ptr(out), st()) == 0
+    else:
+        out = torch.empty((2, 512), device="cuda")
+        assert L.mmhip_swiglu(ctypes.byref(mm.view_of(ta)), None, 0, ptr(out), st()) == 0
+    assert rel_err(out.cpu().numpy(), orc.swiglu(a)) < 1e-5
+
+
+def test_set_rows_into_f16_cache(mm):
+    """KV write of src/qwen3-lm.h:803-804: rows [D, 1, Nkv, N] into the
+    [D, max_seq, Nkv, N] f16 cache at per-set positions (int64)."""
+    L = mm.load()
+    D, S, Nkv, N = 128, 64, 8, 2
+    cache = torch.zeros((N, Nkv, S, D), dtype=torch.float16, device="cuda")
+    src = torch.randn((N, Nkv, 1, D), device="cuda")
+    ids = torch.tensor([[[5]], [[17]]], dtype=torch.int64, device="cuda").view(N, 1, 1)
+    sv = mm.view_of(src)
+    iv = mm.view_of(ids, ne=[1, 1, N, 1], nb=[8, 8, 8, 8 * N])
+    dv = mm.view_of(cache)
+    assert L.mmhip_set_rows(ctypes.byref(sv), ctypes.byref(iv), 27, ctypes.byref(dv), 1, st()) == 0
+    c = cache.cpu()
+    assert torch.equal(c[0, :, 5], src[0, :, 0].half().cpu()) and torch.equal(c[1, :, 17], src[1, :, 0].half().cpu())
+    c[0, :, 5] = 0
+    c[1, :, 17] = 0
+    assert not c.any()
+
+
+@pytest.mark.parametrize("t", [8, 12, 14])
+def test_get_rows_quantized(mm, orc, pkg, t):
+    L = mm.load()
+    V, K = 50, 512
+    raw = pkg.synth.gguf_blocks_np(t, V, K, 30 + t)
+    W = mm.QuantWeight.from_gguf(t, raw, V, K)
+    ids = torch.tensor([3, 49, 0, 3], dtype=torch.int32, device="cuda")
+    out = torch.empty((4, K), device="cuda")
+    rs = W.row_bytes
+    wv = mm.view_of(W.data, ne=[K, V, 1, 1], nb=[1, rs, rs * V, rs * V])
+    assert L.mmhip_get_rows(t, ctypes.byref(wv), ctypes.byref(mm.view_of(ids)), ptr(out), st()) == 0
+    ref = orc.dequantize(t, raw, K, V)[[3, 49, 0, 3]]
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+
+
+def test_cpy_strided_to_f16(mm):
+    L = mm.load()
+    a = torch.randn((3, 40, 64), device="cuda")
+    src = a.permute(1, 0, 2)  # strided view
+    dst = torch.empty((40, 3, 64), dtype=torch.float16, device="cuda")
+    assert L.mmhip_cpy(ctypes.byref(mm.view_of(src)), 0, ctypes.byref(mm.view_of(dst)), 1, st()) == 0
+    assert torch.equal(dst, src.half())
+
+
+def _act(mm, L, wt, x):
+    """Separate-pass activation quantisation of x [M, K] (reference for the fused forms)."""
+    M, K = x.shape
+    n = L.mmhip_act_bytes(wt, K, M)
+    buf = torch.zeros(n, dtype=torch.uint8, device="cuda")
+    assert L.mmhip_quantize_act(wt, ptr(x), K, K, M, ptr(buf), st()) == 0
+    return buf
+
+
+@pytest.mark.parametrize("shape", [(3, 4096), (2, 2, 1024), (1, 256)])
+def test_rms_norm_rows(mm, orc, shape):
+    """Row kernel (n % 256 == 0), also on rows read through a strided view."""
+    L = mm.load()
+    rng = np.random.default_rng(20)
+    n = shape[-1]
+    big = (rng.standard_normal(shape[:-1] + (n + 64,)) * 2).astype(np.float32)
+    w = (1 + 0.02 * rng.standard_normal(n)).astype(np.float32)
+    tb, tw = torch.from_numpy(big).cuda(), torch.from_numpy(w).cuda()
+    tx = tb[..., 32:32 + n]  # row stride n + 64, 16-byte aligned start
+    out = torch.empty(shape, dtype=torch.float32, device="cuda")
+    assert L.mmhip_rms_norm(ctypes.byref(mm.view_of(tx)), ctypes.byref(mm.view_of(tw)), 1e-6, ptr(out), st()) == 0
+    ref = orc.rms_norm_mul(np.ascontiguousarray(big[..., 32:32 + n]), w, 1e-6)
+    assert rel_err(out.cpu().numpy(), ref) < 1e-5
+
+
+@pytest.mark.parametrize("wt", [8, 12, 14])
+def test_rms_norm_quant_equals_two_pass(mm, wt):
+    """Fused norm + quantisation is byte-identical to norm then quantize_act."""
+    L = mm.load()
+    rng = np.random.default_rng(21)
+    M, K = 2, 4096
+    x = torch.from_numpy((rng.standard_normal((M, K)) * 3).astype(np.float32)).cuda()
+    w = torch.from_numpy((1 + 0.02 * rng.standard_normal(K)).astype(np.float32)).cuda()
+    y1 = torch.empty_like(x)
+    assert L.mmhip_rms_norm(ctypes.byref(mm.view_of(x)), ctypes.byref(mm.view_of(w)), 1e-6, ptr(y1), st()) == 0
+    ref_q = _act(mm, L, wt, y1)
+    y2 = torch.empty_like(x)
+    q2 = torch.zeros_like(ref_q)
+    assert L.mmhip_rms_norm_quant(ctypes.byref(mm.view_of(x)), ctypes.byref(mm.view_of(w)), 1e-6, ptr(y2), wt,
+                                  ptr(q2), st()) == 0
+    q3 = torch.zeros_like(ref_q)
+    assert L.mmhip_rms_norm_quant(ctypes.byref(mm.view_of(x)), ctypes.byref(mm.view_of(w)), 1e-6, None, wt,
+                                  ptr(q3), st()) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    assert torch.equal(q2, ref_q) and torch.equal(q3, ref_q)
+
+
+@pytest.mark.parametrize("wt", [8, 14])
+def test_swiglu_quant_equals_two_pass(mm, wt):
+    L = mm.load()
+    rng = np.random.default_rng(22)
+    M, F = 2, 1024
+    a = torch.from_numpy((rng.standard_normal((M, 2 * F)) * 2).astype(np.float32)).cuda()
+    y1 = torch.empty((M, F), dtype=torch.float32, device="cuda")
+    assert L.mmhip_swiglu(ctypes.byref(mm.view_of(a)), None, 0, ptr(y1), st()) == 0
+    ref_q = _act(mm, L, wt, y1)
+    y2 = torch.empty_like(y1)
+    q2 = torch.zeros_like(ref_q)
+    assert L.mmhip_swiglu_quant(ctypes.byref(mm.view_of(a)), None, 0, ptr(y2), wt, ptr(q2), st()) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2) and torch.equal(q2, ref_q)
+
+
+def _head_args(mm, src, D, H, T, nb_t, norm_w=None, eps=1e-6, pos=None, theta=1e6, dst=None, ids=None,
+               cache=None):
+    a = mm.HeadRowsArgs()
+    a.src = src.data_ptr()
+    a.src_nb_h, a.src_nb_t = D * 4, nb_t
+    a.D, a.H, a.T = D, H, T
+    a.norm = 1 if norm_w is not None else 0
+    a.norm_w = norm_w.data_ptr() if norm_w is not None else None
+    a.eps = eps
+    a.pos = pos.data_ptr() if pos is not None else None
+    a.theta_scale = float(np.power(np.float32(theta), np.float32(-2.0) / np.float32(D)))
+    if ids is None:
+        a.dst, a.dst_type = dst.data_ptr(), 0
+    else:
+        # cache [T(sets), H, S, D] f16; ids [T] i64: row ids[t] of set t
+        a.dst, a.dst_type = cache.data_ptr(), 1
+        a.ids, a.ids_type = ids.data_ptr(), 27
+        a.ids_nb1, a.ids_nb2, a.ids_ne1, a.ids_ne2 = 8, 8, 1, T
+        a.dst_nb1, a.dst_nb2, a.dst_nb3 = D * 2, cache.stride(1) * 2, cache.stride(0) * 2
+    return a
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_head_rows_q_and_k(mm, orc, D):
+    """QK-norm + NeoX RoPE of the heads of a fused QKV row (src/qwen3-lm.h:
+    764-772), then Q as contiguous f32 and K stored into an f16 cache."""
+    L = mm.load()
+    rng = np.random.default_rng(23)
+    T, Hq, Hk, S = 2, 8, 2, 64
+    C = (Hq + 2 * Hk) * D
+    qkv = (rng.standard_normal((T, C)) * 2).astype(np.float32)
+    wq = (1 + 0.02 * rng.standard_normal(D)).astype(np.float32)
+    wk = (1 + 0.02 * rng.standard_normal(D)).astype(np.float32)
+    pos = np.array([17, 4095], np.int32)
+    tqkv, twq, twk, tpos = (torch.from_numpy(v).cuda() for v in (qkv, wq, wk, pos))
+    qout = torch.empty((T, Hq, D), dtype=torch.float32, device="cuda")
+    a = _head_args(mm, tqkv, D, Hq, T, C * 4, norm_w=twq, pos=tpos, dst=qout)
+    assert L.mmhip_head_rows(ctypes.byref(a), st()) == 0
+    cache = torch.zeros((T, Hk, S, D), dtype=torch.float16, device="cuda")
+    ids = torch.tensor([5, 40], dtype=torch.int64, device="cuda")
+    kview = tqkv[:, Hq * D:]
+    a = _head_args(mm, kview, D, Hk, T, C * 4, norm_w=twk, pos=tpos, ids=ids, cache=cache)
+    assert L.mmhip_head_rows(ctypes.byref(a), st()) == 0
+    torch.cuda.synchronize()
+    qr = orc.rope_neox(orc.rms_norm_mul(qkv[:, :Hq * D].reshape(T * Hq, D), wq, 1e-6).reshape(T, Hq, D), pos, D, 1e6)
+    assert np.abs(qout.cpu().numpy() - qr).max() < 5e-5
+    kr = orc.rope_neox(orc.rms_norm_mul(qkv[:, Hq * D:(Hq + Hk) * D].reshape(T * Hk, D), wk, 1e-6).reshape(T, Hk, D),
+                       pos, D, 1e6)
+    c = cache.cpu().numpy().astype(np.float32)
+    for t, r in enumerate((5, 40)):
+        got = c[t, :, r, :]
+        assert np.abs(got - kr[t]).max() <= 2e-3 * np.abs(kr[t]).max()
+        # every other row untouched
+        assert not np.any(np.delete(c[t], r, axis=1))
+
+
+def test_head_rows_v_store(mm):
+    """V rows: no norm, no rope, f32 -> f16 into the cache rows (bit-exact)."""
+    L = mm.load()
+    rng = np.random.default_rng(24)
+    T, Hk, D, S = 2, 8, 128, 16
+    C = 48 * D
+    qkv = torch.from_numpy(rng.standard_normal((T, C)).astype(np.float32)).cuda()
+    vview = qkv[:, 40 * D:]
+    cache = torch.zeros((T, Hk, S, D), dtype=torch.float16, device="cuda")
+    ids = torch.tensor([3, 9], dtype=torch.int64, device="cuda")
+    a = _head_args(mm, vview, D, Hk, T, C * 4, ids=ids, cache=cache)
+    assert L.mmhip_head_rows(ctypes.byref(a), st()) == 0
+    torch.cuda.synchronize()
+    want = vview.reshape(T, Hk, D).half()
+    assert torch.equal(cache[0, :, 3], want[0]) and torch.equal(cache[1, :, 9], want[1])
+
+
+@pytest.mark.parametrize("wt", [8, 12, 14])
+def test_mul_mat_q_add(mm, pkg, wt):
+    """GEMV with the residual ADD in its store equals GEMV then a separate f32 add."""
+    L = mm.load()
+    synth = pkg.synth
+    N, K, M = 1000, 4096, 2
+    Wq = mm.QuantWeight.from_gguf(wt, synth.gguf_blocks_np(wt, N, K, 3), N, K)
+    rng = np.random.default_rng(25)
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).cuda()
+    r = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float32)).cuda()
+    xq = _act(mm, L, wt, x)
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    assert L.mmhip_mul_mat_q(wt, ptr(Wq.data), N, K, Wq.row_bytes, ptr(xq), M, ptr(y), N, st()) == 0
+    y2 = torch.empty_like(y)
+    assert L.mmhip_mul_mat_q_add(wt, ptr(Wq.data), N, K, Wq.row_bytes, ptr(xq), M, ptr(r), N, ptr(y2), N, st()) == 0
+    # in place: r and y the same buffer
+    r3 = r.clone()
+    assert L.mmhip_mul_mat_q_add(wt, ptr(Wq.data), N, K, Wq.row_bytes, ptr(xq), M, ptr(r3), N, ptr(r3), N, st()) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(y2, y + r) and torch.equal(r3, y + r)

@@ -30,7 +30,8 @@ def test_gemv_small(mm, orc, pkg, t, M):
 
 
 @pytest.mark.parametrize("t", [8, 12, 14])
-@pytest.mark.parametrize("N,K", [(6144, 4096), (4096, 12288), (2048, 2304), (3, 256), (513, 1280)])
+@pytest.mark.parametrize("N,K", [(6144, 4096), (4096, 12288), (2048, 2304), (3, 256), (513, 1280), (256, 512),
+                                 (1000, 256), (1024, 256)])
 def test_gemv_decode_shapes(mm, orc, pkg, t, N, K):
     y, yg, yf = run(mm, orc, pkg, t, N, K, 2, 3000 + t + N)
     assert rel_err(y, yg) < 2e-5
