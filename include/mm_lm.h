@@ -68,6 +68,9 @@ int     mm_lm_set_tensor(void * lm, const char * name, const void * src, size_t 
  * runs of the backend so far. */
 int  mm_lm_graph_nodes(void * lm);
 void mm_lm_graph_stats(void * lm, int64_t * replays, int64_t * eager);
+/* Mean GPU time (ms) of the decode graph executions since the last reset,
+ * from HIP events on the backend stream; reset != 0 starts a new window. */
+double mm_lm_gpu_ms(void * lm, int reset);
 
 #ifdef __cplusplus
 }

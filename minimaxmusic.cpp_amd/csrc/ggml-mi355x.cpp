@@ -311,7 +311,26 @@ struct mi_backend {
     mi_graph_cache cache;
     int64_t        n_replays = 0;
     int64_t        n_eager   = 0;
+    // GPU time of graph_compute calls: events recorded on the stream around
+    // each call, read back at the next call (or on query)
+    hipEvent_t     ev0 = nullptr, ev1 = nullptr;
+    bool           ev_pending = false;
+    double         gpu_ms     = 0.0;
+    int64_t        gpu_n      = 0;
 };
+
+// Fold the previous call's event pair into the totals (waits for it).
+void collect_time(mi_backend * c) {
+    if (!c->ev_pending) {
+        return;
+    }
+    c->ev_pending = false;
+    float ms      = 0.0f;
+    if (HIP_OK(hipEventSynchronize(c->ev1)) && HIP_OK(hipEventElapsedTime(&ms, c->ev0, c->ev1))) {
+        c->gpu_ms += ms;
+        c->gpu_n++;
+    }
+}
 
 const char * be_name(ggml_backend_t b) {
     return ((mi_backend *) b->context)->dev->name.c_str();
@@ -328,6 +347,10 @@ void be_free(ggml_backend_t b) {
     }
     if (c->slot) {
         (void) hipFree(c->slot);
+    }
+    if (c->ev0) {
+        (void) hipEventDestroy(c->ev0);
+        (void) hipEventDestroy(c->ev1);
     }
     (void) hipStreamDestroy(c->stream);
     delete c;
@@ -1081,7 +1104,7 @@ std::vector<uint64_t> signature(struct ggml_cgraph * g) {
     return sig;
 }
 
-enum ggml_status be_graph_compute(ggml_backend_t b, struct ggml_cgraph * g) {
+enum ggml_status graph_compute_inner(ggml_backend_t b, struct ggml_cgraph * g) {
     mi_backend * c = (mi_backend *) b->context;
     hipSetDevice(c->dev->id);
     for (int i = 0; i < ggml_graph_n_nodes(g); i++) {
@@ -1138,6 +1161,23 @@ enum ggml_status be_graph_compute(ggml_backend_t b, struct ggml_cgraph * g) {
     c->cache.sig = c->cache.seen_sig;
     c->n_replays++;
     return HIP_OK(hipGraphLaunch(c->cache.exec, c->stream)) ? GGML_STATUS_SUCCESS : GGML_STATUS_FAILED;
+}
+
+enum ggml_status be_graph_compute(ggml_backend_t b, struct ggml_cgraph * g) {
+    mi_backend * c = (mi_backend *) b->context;
+    hipSetDevice(c->dev->id);
+    collect_time(c);
+    if (!c->ev0 && !(HIP_OK(hipEventCreate(&c->ev0)) && HIP_OK(hipEventCreate(&c->ev1)))) {
+        return GGML_STATUS_FAILED;
+    }
+    if (!HIP_OK(hipEventRecord(c->ev0, c->stream))) {
+        return GGML_STATUS_FAILED;
+    }
+    const enum ggml_status st = graph_compute_inner(b, g);
+    if (st == GGML_STATUS_SUCCESS && HIP_OK(hipEventRecord(c->ev1, c->stream))) {
+        c->ev_pending = true;
+    }
+    return st;
 }
 
 void be_set_async(ggml_backend_t b, struct ggml_tensor * t, const void * data, size_t off, size_t size) {
@@ -1274,6 +1314,9 @@ void * reg_proc(ggml_backend_reg_t, const char * name) {
     if (strcmp(name, "ggml_backend_mi355x_graph_stats") == 0) {
         return (void *) ggml_backend_mi355x_graph_stats;
     }
+    if (strcmp(name, "ggml_backend_mi355x_gpu_time") == 0) {
+        return (void *) ggml_backend_mi355x_gpu_time;
+    }
     return nullptr;
 }
 
@@ -1355,6 +1398,18 @@ extern "C" void ggml_backend_mi355x_graph_stats(ggml_backend_t backend, int64_t 
     mi_backend * c = (mi_backend *) backend->context;
     *replays       = c->n_replays;
     *eager         = c->n_eager;
+}
+
+extern "C" void ggml_backend_mi355x_gpu_time(ggml_backend_t backend, double * total_ms, int64_t * n_calls, int reset) {
+    mi_backend * c = (mi_backend *) backend->context;
+    hipSetDevice(c->dev->id);
+    collect_time(c);
+    *total_ms = c->gpu_ms;
+    *n_calls  = c->gpu_n;
+    if (reset) {
+        c->gpu_ms = 0.0;
+        c->gpu_n  = 0;
+    }
 }
 
 // dynamic-loading entry points

@@ -484,6 +484,17 @@ extern "C" int mm_lm_graph_nodes(void * h) {
     return (m && m->gf) ? ggml_graph_n_nodes(m->gf) : 0;
 }
 
+extern "C" double mm_lm_gpu_ms(void * h, int reset) {
+    Lm *    m     = (Lm *) h;
+    double  total = 0.0;
+    int64_t n     = 0;
+    if (!m) {
+        return -1.0;
+    }
+    ggml_backend_mi355x_gpu_time(m->backend, &total, &n, reset);
+    return n ? total / (double) n : 0.0;
+}
+
 extern "C" void mm_lm_graph_stats(void * h, int64_t * replays, int64_t * eager) {
     Lm * m = (Lm *) h;
     ggml_backend_mi355x_graph_stats(m->backend, replays, eager);

@@ -45,6 +45,8 @@ def load():
         L.mm_lm_set_tensor.argtypes = [vp, ctypes.c_char_p, vp, ctypes.c_size_t]
         L.mm_lm_graph_nodes.argtypes = [vp]
         L.mm_lm_graph_stats.argtypes = [vp, ctypes.POINTER(i64), ctypes.POINTER(i64)]
+        L.mm_lm_gpu_ms.restype = ctypes.c_double
+        L.mm_lm_gpu_ms.argtypes = [vp, ctypes.c_int]
         _lib = L
     return _lib
 
@@ -115,6 +117,10 @@ class Lm:
 
     def graph_nodes(self):
         return load().mm_lm_graph_nodes(self.h)
+
+    def gpu_ms(self, reset=False):
+        """Mean GPU time per decode graph (ms) since the last reset."""
+        return load().mm_lm_gpu_ms(self.h, 1 if reset else 0)
 
     def graph_stats(self):
         r, e = ctypes.c_int64(), ctypes.c_int64()
