@@ -108,6 +108,13 @@ int    mmhip_mul_mat_q_add(int type, const void * W, int64_t N, int64_t K, int64
 size_t mmhip_flash_attn_workspace(const mmhip_view * q, const mmhip_view * k, const mmhip_view * v);
 int    mmhip_flash_attn_ext(const mmhip_view * q, const mmhip_view * k, const mmhip_view * v, const mmhip_view * mask,
                             float scale, float * out, void * ws, size_t ws_bytes, void * stream);
+/* The same attention with its output rows (b, iq) of Hq * D f32 also
+ * quantised into the activation layout of mmhip_mul_mat_q for weights of
+ * `type`: the input of the attention output projection (src/qwen3-lm.h:
+ * 823-826), quantised by the split combine instead of a separate pass. */
+int    mmhip_flash_attn_ext_q(const mmhip_view * q, const mmhip_view * k, const mmhip_view * v,
+                              const mmhip_view * mask, float scale, float * out, void * ws, size_t ws_bytes, int type,
+                              void * xq, void * stream);
 
 /* ---------------------------------------------------------------------
  * Decode-step glue ops (the nodes between the hot-path ops in the LM
@@ -157,6 +164,9 @@ typedef struct {
     int64_t         dst_nb1, dst_nb2, dst_nb3;
 } mmhip_head_rows_args;
 int mmhip_head_rows(const mmhip_head_rows_args * args, void * stream);
+/* n (1..4) such chains with a common D in one launch (the Q, K and V chains
+ * of one attention block). */
+int mmhip_head_rows_n(const mmhip_head_rows_args * args, int n, void * stream);
 /* GGML_OP_GLU SwiGLU (as mmhip_swiglu) with the result also quantised into
  * the activation layout of mmhip_mul_mat_q for weights of `type` (the down
  * projection, src/qwen3-enc.h:108-110).  dst may be NULL.  Rows contiguous,

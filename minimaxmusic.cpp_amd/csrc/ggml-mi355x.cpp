@@ -620,7 +620,7 @@ int run_node(mi_backend * c, const struct ggml_tensor * n) {
 //             residual: the ADD is done in the GEMV's store.
 // MUL_MATs reading a slot skip their activation quantisation.
 
-enum step_kind { ST_NODE, ST_NORM, ST_SWIGLU_Q, ST_HEAD, ST_MM };
+enum step_kind { ST_NODE, ST_NORM, ST_SWIGLU_Q, ST_HEAD, ST_MM, ST_FA_Q };
 
 struct plan_step {
     int                  kind = ST_NODE;
@@ -632,7 +632,8 @@ struct plan_step {
     int64_t              slot_in  = -1;  // byte offset of the slot read (MM)
     int                  vec_wtype = 0;  // weight type the slot is quantised for
     bool                 write_f32 = true;
-    mmhip_head_rows_args head{};
+    mmhip_head_rows_args head[4]{};  // HEAD: the chains run by this step
+    int                  n_head = 0;
 };
 
 struct graph_info {
@@ -642,6 +643,11 @@ struct graph_info {
     std::vector<std::vector<int>>                consumers;
     std::unordered_map<const ggml_tensor *, int> index;
 };
+
+bool is_noop(enum ggml_op op) {
+    return op == GGML_OP_NONE || op == GGML_OP_RESHAPE || op == GGML_OP_VIEW || op == GGML_OP_PERMUTE ||
+           op == GGML_OP_TRANSPOSE;
+}
 
 bool is_output(const struct ggml_tensor * t) {
     return (t->flags & GGML_TENSOR_FLAG_OUTPUT) != 0;
@@ -812,9 +818,10 @@ bool plan_head(struct ggml_cgraph * g, const graph_info & gi, int i, plan_step &
         }
         a.dst = e->data;
     }
-    st.kind = ST_HEAD;
-    st.node = end;
-    st.head = a;
+    st.kind    = ST_HEAD;
+    st.node    = end;
+    st.head[0] = a;
+    st.n_head  = 1;
     for (int x : chain) {
         absorbed[(size_t) x] = 1;
     }
@@ -964,6 +971,25 @@ graph_plan build_plan(struct ggml_cgraph * g) {
                     absorbed[(size_t) gi.cons[(size_t) i]] = 0;
                 }
             }
+            if (st.src == -2) {
+                // activations straight from an attention output (through a
+                // reshape): the attention's split combine quantises them
+                const struct ggml_tensor * x  = n->src[1];
+                const struct ggml_tensor * fa = x->op == GGML_OP_RESHAPE ? x->src[0] : x;
+                const int                  fi = node_index(gi, fa);
+                if (fa->op == GGML_OP_FLASH_ATTN_EXT && fi >= 0 && fi < i && step_at[(size_t) fi] < 0 &&
+                    !absorbed[(size_t) fi] && ggml_is_contiguous(fa) && ggml_is_contiguous(x) &&
+                    fa->ne[0] * fa->ne[1] == x->ne[0] && fa->ne[2] * fa->ne[3] == x->ne[1] * x->ne[2] * x->ne[3] &&
+                    supports_fa(fa)) {
+                    plan_step fs;
+                    fs.kind      = ST_FA_Q;
+                    fs.node      = fi;
+                    fs.slot_out  = st.slot_in;
+                    fs.vec_wtype = st.vec_wtype;
+                    add_pending(fs);
+                    st.src = -1;
+                }
+            }
             if (st.slot_in >= 0 || st.add >= 0) {
                 absorbed[(size_t) i] = 1;
                 add_pending(st);
@@ -980,6 +1006,33 @@ graph_plan build_plan(struct ggml_cgraph * g) {
             plan.steps.push_back(st);
         }
     }
+    // HEAD steps separated only by no-op nodes (views) run as one launch, at
+    // the later step's position: nothing in between reads their outputs
+    std::vector<plan_step> merged;
+    merged.reserve(plan.steps.size());
+    int last_head = -1;  // index in `merged` of the open HEAD step
+    for (const plan_step & st : plan.steps) {
+        const bool noop = st.kind == ST_NODE && is_noop(ggml_graph_node(g, st.node)->op);
+        if (st.kind == ST_HEAD && last_head >= 0 && merged[(size_t) last_head].n_head + st.n_head <= 4 &&
+            merged[(size_t) last_head].head[0].D == st.head[0].D) {
+            plan_step m = merged[(size_t) last_head];
+            for (int k = 0; k < st.n_head; k++) {
+                m.head[m.n_head++] = st.head[k];
+            }
+            m.node = st.node;
+            merged.erase(merged.begin() + last_head);
+            merged.push_back(m);
+            last_head = (int) merged.size() - 1;
+            continue;
+        }
+        merged.push_back(st);
+        if (st.kind == ST_HEAD) {
+            last_head = (int) merged.size() - 1;
+        } else if (!noop) {
+            last_head = -1;
+        }
+    }
+    plan.steps.swap(merged);
     return plan;
 }
 
@@ -1036,8 +1089,26 @@ int run_step(mi_backend * c, struct ggml_cgraph * g, const plan_step & st, char 
             break;
         }
         case ST_HEAD:
-            rc = mmhip_head_rows(&st.head, s);
+            rc = mmhip_head_rows_n(st.head, st.n_head, s);
             break;
+        case ST_FA_Q: {
+            mmhip_view q = view_of(n->src[0]), k = view_of(n->src[1]), v = view_of(n->src[2]);
+            mmhip_view m;
+            const bool has_m = n->src[3] != nullptr;
+            if (has_m) {
+                m = view_of(n->src[3]);
+            }
+            float scale;
+            memcpy(&scale, &n->op_params[0], sizeof(float));
+            const size_t ws = mmhip_flash_attn_workspace(&q, &k, &v);
+            void *       wp = ws ? workspace(c, ws) : nullptr;
+            if (ws && !wp) {
+                return -1;
+            }
+            rc = mmhip_flash_attn_ext_q(&q, &k, &v, has_m ? &m : nullptr, scale, (float *) n->data, wp, ws,
+                                        st.vec_wtype, slot + st.slot_out, s);
+            break;
+        }
         case ST_MM: {
             const struct ggml_tensor * mm = st.add >= 0 ? ggml_graph_node(g, st.add)->src[1 - st.add_res] : n;
             const struct ggml_tensor * w  = mm->src[0];

@@ -23,7 +23,11 @@ struct FaArgs {
 };
 
 size_t fa_decode_workspace(const FaArgs & a, int D);
-int    fa_decode(const FaArgs & a, int D, float * out, void * ws, size_t ws_bytes, hipStream_t stream);
+// With xq != nullptr the split combine also quantises the output rows into
+// the activation layout for weights of qtype; *quantised reports whether it
+// did (it does not when the decode runs in one split).
+int    fa_decode(const FaArgs & a, int D, float * out, void * ws, size_t ws_bytes, hipStream_t stream,
+                 int qtype = 0, void * xq = nullptr, bool * quantised = nullptr);
 
 size_t fa_mfma_workspace(const FaArgs & a);
 bool   fa_mfma_supported(const FaArgs & a, int D);

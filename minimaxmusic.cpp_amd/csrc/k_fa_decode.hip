@@ -527,6 +527,125 @@ __global__ __launch_bounds__(256) void k_fa_combine(const float * __restrict__ p
     out[(((int64_t) b * nq + iq) * Hq + hq) * D + t] = O * inv;
 }
 
+// Split combine that also quantises the output rows for the GEMV that
+// consumes them (the attention output projection): one 256-thread workgroup
+// per 256-element chunk of an output row (b, iq), thread t owning element t
+// (head e / D, dim e % D), so a workgroup holds whole Q8_0 blocks and a whole
+// Q8_K super-block.  The quantisation arithmetic is k_quant.hip's.
+__global__ __launch_bounds__(256) void k_fa_combine_q(const float * __restrict__ part_o,
+                                                      const float * __restrict__ part_ml, int nsplit, int D, int nq,
+                                                      int Hq, float * __restrict__ out, int qtype,
+                                                      int8_t * __restrict__ xq_qs, float * __restrict__ xq_d,
+                                                      int16_t * __restrict__ xq_bs) {
+#pragma clang fp contract(off)
+    __shared__ float s_m[4][128], s_l[4][128];
+    __shared__ float s_red[4], s_amax[4];
+    __shared__ int   s_idx[4];
+    const int t    = threadIdx.x;
+    const int lane = t & 63;
+    const int e    = 256 * blockIdx.x + t;  // element of the output row
+    const int iq   = blockIdx.y;
+    const int b    = blockIdx.z;
+    const int hq   = e / D;
+    const int d    = e % D;
+    const int hl   = t / D;                 // head within the workgroup (256 / D heads)
+    const int64_t pr0 = (((int64_t) b * Hq + hq) * nq + iq) * nsplit;
+    // split maxima and sums of this workgroup's heads into LDS
+    for (int sidx = d; sidx < nsplit; sidx += D) {
+        s_m[hl][sidx] = part_ml[(pr0 + sidx) * 2];
+        s_l[hl][sidx] = part_ml[(pr0 + sidx) * 2 + 1];
+    }
+    __syncthreads();
+    float M = -INFINITY;
+    for (int sidx = 0; sidx < nsplit; sidx++) {
+        M = fmaxf(M, s_m[hl][sidx]);
+    }
+    float L = 0.0f, O = 0.0f;
+    if (M != -INFINITY) {
+#pragma unroll 8
+        for (int sidx = 0; sidx < nsplit; sidx++) {
+            const float ms = s_m[hl][sidx];
+            const float f  = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
+            L += s_l[hl][sidx] * f;
+            O += part_o[(pr0 + sidx) * D + d] * f;
+        }
+    }
+    const float v   = L > 0.0f ? O / L : 0.0f;
+    const int64_t row = (int64_t) b * nq + iq;
+    const int     K   = Hq * D;
+    out[row * K + e]  = v;
+    if (!xq_qs) {
+        return;
+    }
+    int8_t * qs = xq_qs + row * K + e;
+    if (qtype == TYPE_Q8_0) {
+        // blocks of 32 = half a wave
+        float a = fabsf(v);
+#pragma unroll
+        for (int o = 16; o >= 1; o >>= 1) {
+            a = fmaxf(a, __shfl_xor(a, o, WAVE));
+        }
+        const float dd = a / 127.0f;
+        const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+        *qs            = (int8_t) roundf(v * id);
+        if ((t & 31) == 0) {
+            xq_d[row * (K / 32) + e / 32] = h2f(f2h(dd));
+        }
+        return;
+    }
+    // Q8_K super-block of 256: the first element of largest |x|
+    float a  = fabsf(v);
+    float vm = v;
+    int   ix = t;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float a2  = __shfl_xor(a, o, WAVE);
+        const float vm2 = __shfl_xor(vm, o, WAVE);
+        const int   ix2 = __shfl_xor(ix, o, WAVE);
+        if (a2 > a || (a2 == a && ix2 < ix)) {
+            a  = a2;
+            vm = vm2;
+            ix = ix2;
+        }
+    }
+    if (lane == 0) {
+        s_red[t >> 6]  = vm;
+        s_idx[t >> 6]  = ix;
+        s_amax[t >> 6] = a;
+    }
+    __syncthreads();
+    float bestA = s_amax[0], bestV = s_red[0];
+    int   bestI = s_idx[0];
+    for (int w = 1; w < 4; w++) {
+        const float aw = s_amax[w];
+        if (aw > bestA || (aw == bestA && s_idx[w] < bestI)) {
+            bestA = aw;
+            bestV = s_red[w];
+            bestI = s_idx[w];
+        }
+    }
+    int   q  = 0;
+    float dd = 0.0f;
+    if (bestA != 0.0f) {
+        const float iscale = -127.0f / bestV;
+        const int   qi     = (int) rintf(iscale * v);
+        q                  = qi > 127 ? 127 : qi;
+        dd                 = 1.0f / iscale;
+    }
+    *qs    = (int8_t) q;
+    int sb = q;
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) {
+        sb += __shfl_xor(sb, o, WAVE);
+    }
+    if ((t & 15) == 0) {
+        xq_bs[row * (K / 16) + e / 16] = (int16_t) sb;
+    }
+    if (t == 0) {
+        xq_d[row * (K / 256) + e / 256] = dd;
+    }
+}
+
 // ---------------------------------------------------------------------
 
 // keys per lane per pass (D = 128, QR = 4: 128 keys per workgroup pass)
@@ -582,7 +701,11 @@ static bool dec_mfma(const FaArgs & a) {
     return (a.Hq / a.Hkv) * a.nq <= 16;
 }
 
-int fa_decode(const FaArgs & a, int D, float * out, void * ws, size_t ws_bytes, hipStream_t stream) {
+int fa_decode(const FaArgs & a, int D, float * out, void * ws, size_t ws_bytes, hipStream_t stream, int qtype,
+              void * xq, bool * quantised) {
+    if (quantised) {
+        *quantised = false;
+    }
     int nsplit, chunk, rg;
     decode_plan(a, D, nsplit, chunk, rg);
     float * part_o  = nullptr;
@@ -620,6 +743,18 @@ int fa_decode(const FaArgs & a, int D, float * out, void * ws, size_t ws_bytes, 
     int rc = check_launch("flash_attn decode");
     if (rc != MMHIP_OK || nsplit == 1) {
         return rc;
+    }
+    const int64_t   K = (int64_t) a.Hq * D;
+    const ActLayout L = xq ? act_layout(qtype, K, (int64_t) a.B * a.nq) : ActLayout{};
+    if (xq && L.total != 0 && K % 256 == 0 && nsplit <= 128) {
+        hipLaunchKernelGGL(k_fa_combine_q, dim3((unsigned) (K / 256), a.nq, a.B), dim3(256), 0, stream, part_o, part_ml,
+                           nsplit, D, a.nq, a.Hq, out, L.vec_type, (int8_t *) xq + L.qs_off,
+                           (float *) ((char *) xq + L.d_off),
+                           L.vec_type == TYPE_Q8_K ? (int16_t *) ((char *) xq + L.bs_off) : nullptr);
+        if (quantised) {
+            *quantised = true;
+        }
+        return check_launch("flash_attn combine");
     }
     hipLaunchKernelGGL(k_fa_combine, dim3(a.Hq * a.nq, a.B), dim3(D), 0, stream, part_o, part_ml, nsplit, D, a.nq, a.Hq,
                        out);

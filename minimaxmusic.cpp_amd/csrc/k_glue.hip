@@ -296,15 +296,19 @@ __global__ __launch_bounds__(256) void k_rms_norm(TV x, TV w, int has_w, float e
 // EPL f32 elements, lane l owning elements EPL*l .. EPL*l + EPL-1, so the NeoX
 // partner of element i < D/2 (i + D/2) sits in lane l ^ 32.
 
+// Up to 4 chains in one launch (the attention block's Q, K and V chains):
+// rows of segment i are row indices start[i] .. start[i+1]-1.
+constexpr int HEAD_MAX_SEGS = 4;
+struct HeadSegs {
+    mmhip_head_rows_args seg[HEAD_MAX_SEGS];
+    int                  start[HEAD_MAX_SEGS + 1];
+    int                  n;
+};
+
 template <int EPL>
-__global__ __launch_bounds__(256) void k_head_rows(mmhip_head_rows_args a) {
+__device__ __forceinline__ void head_row(const mmhip_head_rows_args & a, int row, int lane) {
 #pragma clang fp contract(off)
-    constexpr int D    = 64 * EPL;
-    const int     row  = (int) blockIdx.x * 4 + ((int) threadIdx.x >> 6);
-    const int     lane = threadIdx.x & 63;
-    if (row >= a.H * a.T) {
-        return;
-    }
+    constexpr int D  = 64 * EPL;
     const int     h  = row % a.H;
     const int     t  = row / a.H;
     const float * xr = (const float *) ((const char *) a.src + h * a.src_nb_h + t * a.src_nb_t);
@@ -370,6 +374,25 @@ __global__ __launch_bounds__(256) void k_head_rows(mmhip_head_rows_args a) {
         } else {
             ((uint16_t *) dp)[EPL * lane + k] = f2h(v[k]);
         }
+    }
+}
+
+template <int EPL>
+__global__ __launch_bounds__(256) void k_head_rows(HeadSegs hs) {
+    const int row  = (int) blockIdx.x * 4 + ((int) threadIdx.x >> 6);  // one wave per row
+    const int lane = threadIdx.x & 63;
+    if (row >= hs.start[hs.n]) {
+        return;
+    }
+    // constant indices keep the kernel-argument struct out of scratch memory
+    if (hs.n > 3 && row >= hs.start[3]) {
+        head_row<EPL>(hs.seg[3], row - hs.start[3], lane);
+    } else if (hs.n > 2 && row >= hs.start[2]) {
+        head_row<EPL>(hs.seg[2], row - hs.start[2], lane);
+    } else if (hs.n > 1 && row >= hs.start[1]) {
+        head_row<EPL>(hs.seg[1], row - hs.start[1], lane);
+    } else {
+        head_row<EPL>(hs.seg[0], row, lane);
     }
 }
 
@@ -873,31 +896,51 @@ extern "C" int mmhip_swiglu_quant(const mmhip_view * a, const mmhip_view * b, in
     return check_launch("swiglu_quant");
 }
 
-extern "C" int mmhip_head_rows(const mmhip_head_rows_args * a, void * stream) {
+extern "C" int mmhip_head_rows_n(const mmhip_head_rows_args * args, int n, void * stream) {
     MMHIP_API_BEGIN();
-    if (!a || !a->src || !a->dst || a->H <= 0 || a->T < 0) {
-        return set_error(MMHIP_ERR_INVALID, "head_rows: bad arguments");
+    if (!args || n < 1 || n > HEAD_MAX_SEGS) {
+        return set_error(MMHIP_ERR_INVALID, "head_rows: %d chains (1..%d)", n, HEAD_MAX_SEGS);
     }
-    if (!(a->D == 64 || a->D == 128 || a->D == 256) || (int64_t) a->H * a->T >= ((int64_t) 1 << 30)) {
-        return set_error(MMHIP_ERR_UNSUPPORTED, "head_rows: D=%d H=%d T=%d not supported", a->D, a->H, a->T);
+    HeadSegs hs{};
+    hs.n     = n;
+    int64_t rows = 0;
+    for (int i = 0; i < n; i++) {
+        const mmhip_head_rows_args * a = &args[i];
+        if (!a->src || !a->dst || a->H <= 0 || a->T < 0) {
+            return set_error(MMHIP_ERR_INVALID, "head_rows: bad arguments (chain %d)", i);
+        }
+        if (!(a->D == 64 || a->D == 128 || a->D == 256) || a->D != args[0].D) {
+            return set_error(MMHIP_ERR_UNSUPPORTED, "head_rows: D=%d not supported (chains share D)", a->D);
+        }
+        if (a->ids && (a->ids_ne1 <= 0 || a->ids_ne2 <= 0 || !(a->ids_type == 26 || a->ids_type == 27) ||
+                       !(a->dst_type == TYPE_F32 || a->dst_type == TYPE_F16))) {
+            return set_error(MMHIP_ERR_INVALID, "head_rows: bad row ids / destination type (chain %d)", i);
+        }
+        if (!a->ids && a->dst_type != TYPE_F32) {
+            return set_error(MMHIP_ERR_INVALID, "head_rows: contiguous output is f32 (chain %d)", i);
+        }
+        hs.seg[i]   = *a;
+        hs.start[i] = (int) rows;
+        rows += (int64_t) a->H * a->T;
+        if (rows >= ((int64_t) 1 << 30)) {
+            return set_error(MMHIP_ERR_UNSUPPORTED, "head_rows: too many rows");
+        }
     }
-    if (a->ids && (a->ids_ne1 <= 0 || a->ids_ne2 <= 0 || !(a->ids_type == 26 || a->ids_type == 27) ||
-                   !(a->dst_type == TYPE_F32 || a->dst_type == TYPE_F16))) {
-        return set_error(MMHIP_ERR_INVALID, "head_rows: bad row ids / destination type");
-    }
-    if (!a->ids && a->dst_type != TYPE_F32) {
-        return set_error(MMHIP_ERR_INVALID, "head_rows: contiguous output is f32");
-    }
-    if (a->T == 0) {
+    hs.start[n] = (int) rows;
+    if (rows == 0) {
         return MMHIP_OK;
     }
-    const dim3 grid((unsigned) (((int64_t) a->H * a->T + 3) / 4));
-    if (a->D == 64) {
-        hipLaunchKernelGGL(k_head_rows<1>, grid, dim3(256), 0, (hipStream_t) stream, *a);
-    } else if (a->D == 128) {
-        hipLaunchKernelGGL(k_head_rows<2>, grid, dim3(256), 0, (hipStream_t) stream, *a);
+    const dim3 grid((unsigned) ((rows + 3) / 4));
+    if (args[0].D == 64) {
+        hipLaunchKernelGGL(k_head_rows<1>, grid, dim3(256), 0, (hipStream_t) stream, hs);
+    } else if (args[0].D == 128) {
+        hipLaunchKernelGGL(k_head_rows<2>, grid, dim3(256), 0, (hipStream_t) stream, hs);
     } else {
-        hipLaunchKernelGGL(k_head_rows<4>, grid, dim3(256), 0, (hipStream_t) stream, *a);
+        hipLaunchKernelGGL(k_head_rows<4>, grid, dim3(256), 0, (hipStream_t) stream, hs);
     }
     return check_launch("head_rows");
+}
+
+extern "C" int mmhip_head_rows(const mmhip_head_rows_args * a, void * stream) {
+    return mmhip_head_rows_n(a, 1, stream);
 }

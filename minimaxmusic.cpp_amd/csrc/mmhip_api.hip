@@ -210,3 +210,32 @@ extern "C" int mmhip_flash_attn_ext(const mmhip_view * q, const mmhip_view * k, 
     }
     return fa_decode(a, D, out, ws, ws_bytes, (hipStream_t) stream);
 }
+
+extern "C" int mmhip_flash_attn_ext_q(const mmhip_view * q, const mmhip_view * k, const mmhip_view * v,
+                                      const mmhip_view * mask, float scale, float * out, void * ws, size_t ws_bytes,
+                                      int type, void * xq, void * stream) {
+    MMHIP_API_BEGIN();
+    FaArgs a;
+    int    D;
+    int    rc = fa_validate(q, k, v, mask, a, D);
+    if (rc != MMHIP_OK) {
+        return rc;
+    }
+    const int64_t K = (int64_t) a.Hq * D, M = (int64_t) a.B * a.nq;
+    if (!out || !xq || act_layout(type, K, M).total == 0) {
+        return set_error(MMHIP_ERR_INVALID, "flash_attn_q: bad output / activation type %d for K=%lld", type,
+                         (long long) K);
+    }
+    a.scale        = scale;
+    bool quantised = false;
+    if (fa_use_mfma(a, D)) {
+        rc = fa_mfma(a, D, out, ws, ws_bytes, (hipStream_t) stream);
+    } else {
+        rc = fa_decode(a, D, out, ws, ws_bytes, (hipStream_t) stream, type, xq, &quantised);
+    }
+    if (rc != MMHIP_OK || quantised) {
+        return rc;
+    }
+    // output rows (b, iq) of Hq * D contiguous f32: quantise them separately
+    return quantize_act(type, out, K, K, M, xq, (hipStream_t) stream);
+}

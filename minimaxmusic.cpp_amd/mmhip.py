@@ -66,10 +66,12 @@ SIGNATURES = {
     "mmhip_mul_mat_q_add": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp]),
     "mmhip_flash_attn_workspace": (_sz, [_VP, _VP, _VP]),
     "mmhip_flash_attn_ext": (_i32, [_VP, _VP, _VP, _VP, _f32, _vp, _vp, _sz, _vp]),
+    "mmhip_flash_attn_ext_q": (_i32, [_VP, _VP, _VP, _VP, _f32, _vp, _vp, _sz, _i32, _vp, _vp]),
     "mmhip_binary": (_i32, [_i32, _VP, _VP, _vp, _vp]),
     "mmhip_rms_norm": (_i32, [_VP, _VP, _f32, _vp, _vp]),
     "mmhip_rms_norm_quant": (_i32, [_VP, _VP, _f32, _vp, _i32, _vp, _vp]),
     "mmhip_head_rows": (_i32, [ctypes.c_void_p, _vp]),
+    "mmhip_head_rows_n": (_i32, [ctypes.c_void_p, _i32, _vp]),
     "mmhip_swiglu_quant": (_i32, [_VP, _VP, _i32, _vp, _i32, _vp, _vp]),
     "mmhip_rope_neox": (_i32, [_VP, _vp, _i32, _f32, _vp, _vp]),
     "mmhip_cpy": (_i32, [_VP, _i32, _VP, _i32, _vp]),

@@ -212,3 +212,41 @@ def test_mfma_odd_shapes_with_mask(mm, orc, B, Bk, Hq, Hkv, nq, nkv, D):
     mk = np.ascontiguousarray(mask)
     check(out, orc.flash_attn_ext(q, k, v, mk, s, "f64"))
     assert not out[:, 5].any()
+
+
+@pytest.mark.parametrize("wt", [8, 14])
+def test_decode_with_quantised_output(mm, orc, wt):
+    """mmhip_flash_attn_ext_q (the attention feeding the output projection,
+    src/qwen3-lm.h:816-826): the output matches the oracle, and its quantised
+    copy is byte-identical to quantize_act of that output."""
+    import ctypes
+
+    L = mm.load()
+    D, Hq, Hkv, sets, max_seq, pad = 128, 32, 8, 2, 4096, 2304
+    kv_len = [2049, 2111]
+    cache_k = torch.from_numpy(rnd((sets, Hkv, max_seq, D), 31, np.float16)).cuda()
+    cache_v = torch.from_numpy(rnd((sets, Hkv, max_seq, D), 32, np.float16)).cuda()
+    kw, vw = cache_k[:, :, :pad], cache_v[:, :, :pad]
+    q = rnd((sets, Hq, 1, D), 33)
+    mask = np.zeros((sets, 1, 1, pad), np.float16)
+    for i, n in enumerate(kv_len):
+        mask[i, ..., n:] = -np.inf
+    s = float(np.float32(1 / np.sqrt(D)))
+    tq, tm = torch.from_numpy(q).cuda(), torch.from_numpy(mask).cuda()
+    qv, kv, vv, mv = mm.view_of(tq), mm.view_of(kw), mm.view_of(vw), mm.view_of(tm)
+    out = torch.empty((sets, 1, Hq, D), dtype=torch.float32, device="cuda")
+    need = L.mmhip_flash_attn_workspace(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv))
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
+    K, M = Hq * D, sets
+    xq = torch.zeros(L.mmhip_act_bytes(wt, K, M), dtype=torch.uint8, device="cuda")
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert L.mmhip_flash_attn_ext_q(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), ctypes.byref(mv), s,
+                                    ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(ws.data_ptr()), need, wt,
+                                    ctypes.c_void_p(xq.data_ptr()), st) == 0
+    ref_q = torch.zeros_like(xq)
+    assert L.mmhip_quantize_act(wt, ctypes.c_void_p(out.data_ptr()), K, K, M, ctypes.c_void_p(ref_q.data_ptr()),
+                                st) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(xq, ref_q)
+    kn, vn = kw.cpu().numpy(), vw.cpu().numpy()
+    check(out.cpu().numpy(), orc.flash_attn_ext(q, kn, vn, mask, s, "f64"), orc.flash_attn_ext(q, kn, vn, mask, s, "ggml"))

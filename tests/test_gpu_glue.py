@@ -290,3 +290,35 @@ def test_mul_mat_q_add(mm, pkg, wt):
     assert L.mmhip_mul_mat_q_add(wt, ptr(Wq.data), N, K, Wq.row_bytes, ptr(xq), M, ptr(r3), N, ptr(r3), N, st()) == 0
     torch.cuda.synchronize()
     assert torch.equal(y2, y + r) and torch.equal(r3, y + r)
+
+
+def test_head_rows_three_chains_one_launch(mm, orc):
+    """mmhip_head_rows_n with the Q, K and V chains of one attention block gives
+    exactly what three separate calls give."""
+    L = mm.load()
+    rng = np.random.default_rng(26)
+    T, Hq, Hk, D, S = 2, 32, 8, 128, 32
+    C = (Hq + 2 * Hk) * D
+    qkv = torch.from_numpy((rng.standard_normal((T, C)) * 2).astype(np.float32)).cuda()
+    wq = torch.from_numpy((1 + 0.02 * rng.standard_normal(D)).astype(np.float32)).cuda()
+    wk = torch.from_numpy((1 + 0.02 * rng.standard_normal(D)).astype(np.float32)).cuda()
+    pos = torch.tensor([7, 1234], dtype=torch.int32, device="cuda")
+    ids = torch.tensor([3, 17], dtype=torch.int64, device="cuda")
+    outs = []
+    for merged in (False, True):
+        qout = torch.zeros((T, Hq, D), dtype=torch.float32, device="cuda")
+        kc = torch.zeros((T, Hk, S, D), dtype=torch.float16, device="cuda")
+        vc = torch.zeros((T, Hk, S, D), dtype=torch.float16, device="cuda")
+        a = [_head_args(mm, qkv, D, Hq, T, C * 4, norm_w=wq, pos=pos, dst=qout),
+             _head_args(mm, qkv[:, Hq * D:], D, Hk, T, C * 4, norm_w=wk, pos=pos, ids=ids, cache=kc),
+             _head_args(mm, qkv[:, (Hq + Hk) * D:], D, Hk, T, C * 4, ids=ids, cache=vc)]
+        if merged:
+            arr = (mm.HeadRowsArgs * 3)(*a)
+            assert L.mmhip_head_rows_n(ctypes.byref(arr), 3, st()) == 0
+        else:
+            for x in a:
+                assert L.mmhip_head_rows(ctypes.byref(x), st()) == 0
+        torch.cuda.synchronize()
+        outs.append((qout, kc, vc))
+    for x, y in zip(outs[0], outs[1]):
+        assert torch.equal(x, y)
