@@ -433,7 +433,9 @@ static int gemv_dispatch(int wtype, const uint8_t * W, int64_t N, int64_t K, int
     constexpr int R = GemvShape<NC>::R;
     constexpr int U = GemvShape<NC>::U;
     if (wtype == TYPE_Q8_0) {
-        if (N <= 8192 && K <= 4096) {
+        // one row per wave for the short matrices (more waves in flight; with
+        // two rows a 12-chunk pass needs 256 VGPRs and one wave per SIMD)
+        if (N <= 8192) {
             return launch_q8_0_k<NC, 1>(W, N, K, rs, x, y, ldy, r, ldr, stream);
         }
         return launch_q8_0_k<NC, 2>(W, N, K, rs, x, y, ldy, r, ldr, stream);
