@@ -35,6 +35,13 @@ __device__ __forceinline__ int vt_pos(int k) {
     return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
 }
 
+// Bank swizzle of V^T row r: the 8-key groups of the row are XOR-permuted by
+// (r / 8) % 8, so the staging writes of 16 lanes to rows 8 apart fall in
+// different banks; reads of 8 consecutive positions stay contiguous.
+__device__ __forceinline__ int vt_swz(int r) {
+    return ((r >> 3) & 7) << 3;
+}
+
 // Work item of linear workgroup id `lin` out of `total`: workgroups are
 // dispatched round-robin over the 8 XCDs (id % 8), so consecutive work items
 // are dealt to one XCD at a time; all query tiles of a (head, batch) then
@@ -160,7 +167,8 @@ __global__ __launch_bounds__(NW * 64) void k_fa_mfma(FaArgs a, const int * __res
             const int pos = vt_pos(2 * kp);
 #pragma unroll
             for (int j = 0; j < 8; j++) {
-                *(half2_t *) &sV[(seg * 8 + j) * VS + pos] = half2_t{ rv0[i][j], rv1[i][j] };
+                const int r = seg * 8 + j;
+                *(half2_t *) &sV[r * VS + (pos ^ vt_swz(r))] = half2_t{ rv0[i][j], rv1[i][j] };
             }
         }
         __syncthreads();
@@ -182,8 +190,21 @@ __global__ __launch_bounds__(NW * 64) void k_fa_mfma(FaArgs a, const int * __res
                 s[kb]            = mfma32(ak, qreg[kk], s[kb]);
             }
         }
-        // scale, mask, out-of-range keys; tile max for this lane's query
-        float mx = -INFINITY;
+        // scale, mask, out-of-range keys; tile max for this lane's query.
+        // Without a mask on a full tile the raw scores are kept: their max
+        // is scaled once, and the scale folds into the exp2 argument below.
+        const bool fast = !mrow && k0 + FA_BK <= a.nkv;
+        float      mx   = -INFINITY;
+        if (fast) {
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    mx = fmaxf(mx, s[kb][r]);
+                }
+            }
+            mx *= sl2;
+        } else {
 #pragma unroll
         for (int kb = 0; kb < 2; kb++) {
 #pragma unroll
@@ -213,6 +234,7 @@ __global__ __launch_bounds__(NW * 64) void k_fa_mfma(FaArgs a, const int * __res
                 }
             }
         }
+        }
         mx               = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
         const float mnew = fmaxf(m, mx);
         // No divergent control flow from here on: the MFMAs below combine the
@@ -224,11 +246,13 @@ __global__ __launch_bounds__(NW * 64) void k_fa_mfma(FaArgs a, const int * __res
         float       rs    = 0.0f;
         l                 = l * alpha;
         m                 = mnew;
+        if (__any(alpha != 1.0f)) {  // wave-uniform: no lane's running max moved -> nothing to rescale
 #pragma unroll
-        for (int i = 0; i < NDB; i++) {
+            for (int i = 0; i < NDB; i++) {
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                oacc[i][r] *= alpha;
+                for (int r = 0; r < 16; r++) {
+                    oacc[i][r] *= alpha;
+                }
             }
         }
         // P^T -> f16 B operands, then O^T (D x 32 queries) += V^T P^T
@@ -239,13 +263,15 @@ __global__ __launch_bounds__(NW * 64) void k_fa_mfma(FaArgs a, const int * __res
                 half8_t pb;
 #pragma unroll
                 for (int u = 0; u < 8; u++) {
-                    const float p = __builtin_amdgcn_exp2f(s[kb][8 * t + u] - mref);
+                    const float p = fast ? __builtin_amdgcn_exp2f(fmaf(s[kb][8 * t + u], sl2, -mref))
+                                         : __builtin_amdgcn_exp2f(s[kb][8 * t + u] - mref);
                     rs += p;
                     pb[u] = (_Float16) p;
                 }
 #pragma unroll
                 for (int db = 0; db < NDB; db++) {
-                    const half8_t av = *(const half8_t *) &sV[(db * 32 + lq) * VS + kb * 32 + 16 * t + 8 * hh];
+                    const int     r  = db * 32 + lq;
+                    const half8_t av = *(const half8_t *) &sV[r * VS + ((kb * 32 + 16 * t + 8 * hh) ^ vt_swz(r))];
                     oacc[db]         = mfma32(av, pb, oacc[db]);
                 }
             }
