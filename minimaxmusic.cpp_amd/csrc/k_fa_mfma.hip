@@ -176,7 +176,10 @@ __global__ __launch_bounds__(NW * 64) void k_fa_mfma(FaArgs a, const int * __res
             fetch(k0 + FA_BK);
         }
 
-        // S^T (64 keys x 32 queries) = K Q^T
+        // S^T (64 keys x 32 queries) = K Q^T.  Raised wave priority while
+        // issuing MFMAs: of two waves on a SIMD, the one with matrix work
+        // goes first and the other's softmax fills the gaps.
+        __builtin_amdgcn_s_setprio(1);
         float16_t s[2];
 #pragma unroll
         for (int kb = 0; kb < 2; kb++) {
@@ -190,6 +193,7 @@ __global__ __launch_bounds__(NW * 64) void k_fa_mfma(FaArgs a, const int * __res
                 s[kb]            = mfma32(ak, qreg[kk], s[kb]);
             }
         }
+        __builtin_amdgcn_s_setprio(0);
         // scale, mask, out-of-range keys; tile max for this lane's query.
         // Without a mask on a full tile the raw scores are kept: their max
         // is scaled once, and the scale folds into the exp2 argument below.
@@ -242,6 +246,7 @@ __global__ __launch_bounds__(NW * 64) void k_fa_mfma(FaArgs a, const int * __res
         // its state (alpha = 1) and contributes p = exp2(-inf) = 0.
         const bool  live  = mnew != -INFINITY;
         const float mref  = live ? mnew : 0.0f;
+        const float smul  = fast ? sl2 : 1.0f;
         const float alpha = live ? __builtin_amdgcn_exp2f(m - mnew) : 1.0f;
         float       rs    = 0.0f;
         l                 = l * alpha;
@@ -256,6 +261,7 @@ __global__ __launch_bounds__(NW * 64) void k_fa_mfma(FaArgs a, const int * __res
             }
         }
         // P^T -> f16 B operands, then O^T (D x 32 queries) += V^T P^T
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int kb = 0; kb < 2; kb++) {
 #pragma unroll
@@ -263,8 +269,9 @@ __global__ __launch_bounds__(NW * 64) void k_fa_mfma(FaArgs a, const int * __res
                 half8_t pb;
 #pragma unroll
                 for (int u = 0; u < 8; u++) {
-                    const float p = fast ? __builtin_amdgcn_exp2f(fmaf(s[kb][8 * t + u], sl2, -mref))
-                                         : __builtin_amdgcn_exp2f(s[kb][8 * t + u] - mref);
+                    // fast path: raw score * scale - max in one rounding; masked
+                    // path: already scaled, s * 1 - max == s - max exactly
+                    const float p = __builtin_amdgcn_exp2f(fmaf(s[kb][8 * t + u], smul, -mref));
                     rs += p;
                     pb[u] = (_Float16) p;
                 }
@@ -276,6 +283,7 @@ __global__ __launch_bounds__(NW * 64) void k_fa_mfma(FaArgs a, const int * __res
                 }
             }
         }
+        __builtin_amdgcn_s_setprio(0);
         l += rs + __shfl_xor(rs, 32, WAVE);
     }
 

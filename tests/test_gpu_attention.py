@@ -214,6 +214,21 @@ def test_mfma_odd_shapes_with_mask(mm, orc, B, Bk, Hq, Hkv, nq, nkv, D):
     assert not out[:, 5].any()
 
 
+@pytest.mark.parametrize("B,Bk,Hq,Hkv,nq,nkv,D", [(2, 1, 8, 2, 130, 77, 64), (1, 1, 4, 1, 257, 300, 128),
+                                                 (2, 2, 2, 2, 33, 1, 128), (1, 1, 16, 16, 64, 640, 64),
+                                                 (1, 1, 8, 2, 96, 31, 128), (1, 1, 2, 2, 40, 33, 64)])
+def test_mfma_odd_shapes_no_mask(mm, orc, B, Bk, Hq, Hkv, nq, nkv, D):
+    """Unmasked attention (the DiT path) with partial key tiles (nkv % 32 != 0),
+    a single key, GQA and both head sizes."""
+    q = rnd((B, Hq, nq, D), 71)
+    k = rnd((Bk, Hkv, nkv, D), 72, np.float16)
+    v = rnd((Bk, Hkv, nkv, D), 73, np.float16)
+    s = float(np.float32(1 / np.sqrt(D)))
+    out = mm.flash_attn_ext(torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                            None, s).cpu().numpy()
+    check(out, orc.flash_attn_ext(q, k, v, None, s, "f64"))
+
+
 @pytest.mark.parametrize("wt", [8, 14])
 def test_decode_with_quantised_output(mm, orc, wt):
     """mmhip_flash_attn_ext_q (the attention feeding the output projection,
