@@ -45,11 +45,28 @@ namespace {
 // ---------------------------------------------------------------------------
 // device / registry state
 
+// Pinned staging for small host -> device tensor writes (per-step inputs of
+// the decode graph): the data is copied into a slot on the host and sent with
+// an asynchronous copy on the null stream, which the backends' blocking
+// streams order after; a slot is reused only once its copy has completed.
+// The caller sees ggml's synchronous tensor_set: its buffer is free on return.
+struct mi_staging {
+    static constexpr int    SLOTS     = 32;
+    static constexpr size_t SLOT_SIZE = 256 << 10;
+    std::mutex              mu;
+    char *                  host = nullptr;
+    hipEvent_t              ev[SLOTS]{};
+    bool                    used[SLOTS]{};
+    int                     next = 0;
+    bool                    failed = false;
+};
+
 struct mi_device {
     int                             id;
     std::string                     name;
     std::string                     desc;
     struct ggml_backend_buffer_type buft;
+    mi_staging                      staging;
 };
 
 struct mi_registry {
@@ -155,6 +172,47 @@ bool quant_rows_io(const struct ggml_tensor * t, size_t offset, size_t size, con
     return ok;
 }
 
+mi_device * device_by_id(int id);
+
+// Small write through the device's pinned staging ring; false when not taken.
+bool staged_write(int device, void * dst, const void * src, size_t size) {
+    mi_device * d = device_by_id(device);
+    if (!d || size > mi_staging::SLOT_SIZE) {
+        return false;
+    }
+    mi_staging &                g = d->staging;
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (g.failed) {
+        return false;
+    }
+    if (!g.host) {
+        if (!HIP_OK(hipHostMalloc((void **) &g.host, (size_t) mi_staging::SLOTS * mi_staging::SLOT_SIZE, 0))) {
+            g.failed = true;
+            g.host   = nullptr;
+            return false;
+        }
+        for (int i = 0; i < mi_staging::SLOTS; i++) {
+            if (!HIP_OK(hipEventCreateWithFlags(&g.ev[i], hipEventDisableTiming))) {
+                g.failed = true;
+                return false;
+            }
+        }
+    }
+    const int i = g.next;
+    g.next      = (g.next + 1) % mi_staging::SLOTS;
+    if (g.used[i] && !HIP_OK(hipEventSynchronize(g.ev[i]))) {
+        return false;
+    }
+    char * slot = g.host + (size_t) i * mi_staging::SLOT_SIZE;
+    memcpy(slot, src, size);
+    if (!HIP_OK(hipMemcpyAsync(dst, slot, size, hipMemcpyHostToDevice, nullptr)) ||
+        !HIP_OK(hipEventRecord(g.ev[i], nullptr))) {
+        return false;
+    }
+    g.used[i] = true;
+    return true;
+}
+
 void buf_set_tensor(ggml_backend_buffer_t b, struct ggml_tensor * t, const void * data, size_t offset, size_t size) {
     mi_buffer * c = (mi_buffer *) b->context;
     hipSetDevice(c->device);
@@ -162,6 +220,9 @@ void buf_set_tensor(ggml_backend_buffer_t b, struct ggml_tensor * t, const void 
         if (!quant_rows_io(t, offset, size, data, nullptr)) {
             abort();
         }
+        return;
+    }
+    if (staged_write(c->device, (char *) t->data + offset, data, size)) {
         return;
     }
     HIP_OK(hipMemcpy((char *) t->data + offset, data, size, hipMemcpyHostToDevice));
@@ -1292,6 +1353,18 @@ const struct ggml_backend_i k_be_iface = {
 };
 
 // ---- device iface ----
+
+mi_device * device_by_id(int id) {
+    if (!g_reg) {
+        return nullptr;
+    }
+    for (mi_device * d : g_reg->devs) {
+        if (d->id == id) {
+            return d;
+        }
+    }
+    return nullptr;
+}
 
 mi_device * devctx(ggml_backend_dev_t d) {
     return (mi_device *) d->context;
