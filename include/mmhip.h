@@ -91,6 +91,21 @@ int    mmhip_mul_mat_q(int type, const void * W, int64_t N, int64_t K, int64_t w
  * src/qwen3-lm.h:826-828, MLP down src/qwen3-lm.h:835-836); r may alias y. */
 int    mmhip_mul_mat_q_add(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const void * xq,
                            int64_t M, const float * r, int64_t ldr, float * y, int64_t ldy, void * stream);
+/* The GEMV that follows an RMS norm, with the norm in its prologue: the
+ * GGML_OP_RMS_NORM + GGML_OP_MUL by the norm weight of qwen3_rms_norm
+ * (src/qwen3-lm.h:736, :834, :843) feeding the Q/K/V, gate/up and lm_head
+ * GGML_OP_MUL_MATs (src/qwen3-lm.h:742-757, :835, :856).  x holds the M raw
+ * rows (row stride ldx floats); each workgroup recomputes the norm and the
+ * activation quantisation of mmhip_rms_norm_quant in LDS, with identical
+ * arithmetic, so y equals rms_norm_quant + mul_mat_q(_add) bit for bit.
+ * xn_out (optional) receives the f32 normalised rows [M, K]; r (optional) is
+ * the residual of mmhip_mul_mat_q_add.  Q8_0 weights, M <= 2, K a multiple of
+ * 256 up to 4096: mmhip_rms_norm_mul_mat_supported says whether a shape is
+ * taken.  y must not overlap x. */
+int mmhip_rms_norm_mul_mat_supported(int type, int64_t N, int64_t K, int64_t M);
+int mmhip_rms_norm_mul_mat(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const float * x,
+                           int64_t ldx, int64_t M, const float * norm_w, float eps, float * xn_out, const float * r,
+                           int64_t ldr, float * y, int64_t ldy, void * stream);
 
 /* ---------------------------------------------------------------------
  * GGML_OP_FLASH_ATTN_EXT, replacing the ggml backend kernel behind

@@ -689,6 +689,8 @@ struct plan_step {
     int                  src  = -1;      // NORM: the RMS_NORM node
     int                  add  = -1;      // MM: the fused ADD node
     int                  add_res = -1;   // MM: index 0/1 of the ADD's residual source
+    int                  norm    = -1;   // MM: the RMS_NORM node whose norm runs in the GEMV's prologue
+    int                  norm_mul = -1;  // MM: the MUL by the norm weight (the GEMV's src1)
     int64_t              slot_out = -1;  // byte offset of the quantised slot written (NORM / SWIGLU_Q)
     int64_t              slot_in  = -1;  // byte offset of the slot read (MM)
     int                  vec_wtype = 0;  // weight type the slot is quantised for
@@ -759,6 +761,43 @@ bool is_f32_vector(const struct ggml_tensor * w, int64_t n) {
 
 bool rows_contiguous_f32(const struct ggml_tensor * t) {
     return t->type == GGML_TYPE_F32 && ggml_is_contiguous(t) && ((uintptr_t) t->data) % 16 == 0;
+}
+
+bool overlaps(const struct ggml_tensor * a, const struct ggml_tensor * b) {
+    const uintptr_t a0 = (uintptr_t) a->data, b0 = (uintptr_t) b->data;
+    return a0 && b0 && a0 < b0 + ggml_nbytes(b) && b0 < a0 + ggml_nbytes(a);
+}
+
+// Can every consumer of the norm-weight MUL j (after RMS_NORM i) be a GEMV
+// that recomputes the norm itself (mmhip_rms_norm_mul_mat)?  The raw rows
+// must then stay intact until the last of them ran: no node executed in
+// between (or an ADD fused into one of them) may write over them.
+bool norm_into_gemvs(struct ggml_cgraph * g, const graph_info & gi, int i, int j) {
+    const struct ggml_tensor * n = ggml_graph_node(g, i);
+    const struct ggml_tensor * m = ggml_graph_node(g, j);
+    const struct ggml_tensor * x = n->src[0];
+    const int64_t              K = x->ne[0], M = ggml_nrows(x);
+    if (is_output(m) || gi.consumers[(size_t) j].empty() || x->type != GGML_TYPE_F32 || !mm_collapsible(x) ||
+        ((uintptr_t) x->data | x->nb[1]) % 16 != 0 || !is_f32_vector(m->src[1], K) ||
+        ((uintptr_t) m->src[1]->data) % 16 != 0) {
+        return false;
+    }
+    int last = j;
+    for (int ci : gi.consumers[(size_t) j]) {
+        const struct ggml_tensor * mm = ggml_graph_node(g, ci);
+        if (mm->op != GGML_OP_MUL_MAT || mm->src[1] != m || mm->src[0] == m || !mm_is_gemv(mm) ||
+            !mmhip_rms_norm_mul_mat_supported(mm->src[0]->type, mm->src[0]->ne[1], K, M)) {
+            return false;
+        }
+        last = std::max(last, gi.uses[(size_t) ci] == 1 ? std::max(ci, gi.cons[(size_t) ci]) : ci);
+    }
+    for (int t = j + 1; t <= last; t++) {
+        const struct ggml_tensor * nt = ggml_graph_node(g, t);
+        if (!is_noop(nt->op) && overlaps(nt, x)) {
+            return false;
+        }
+    }
+    return true;
 }
 
 // Try the HEAD chain starting at CONT node i; fills st and marks absorbed nodes.
@@ -923,6 +962,8 @@ graph_plan build_plan(struct ggml_cgraph * g) {
     std::vector<int>         step_at((size_t) gi.nn, -1);  // index into pending
     std::vector<int64_t>     slot_of((size_t) gi.nn, -1);  // node -> quantised slot of its output
     std::vector<int>         slot_wtype((size_t) gi.nn, 0);
+    std::vector<int>         norm_of((size_t) gi.nn, -1);  // MUL node -> its RMS_NORM, norm done by the GEMVs
+    const bool               no_norm_mm = getenv("GGML_MI355X_DISABLE_NORM_GEMV") != nullptr;
     auto add_pending = [&](const plan_step & st) {
         step_at[(size_t) st.node] = (int) pending.size();
         pending.push_back(st);
@@ -944,6 +985,12 @@ graph_plan build_plan(struct ggml_cgraph * g) {
             const struct ggml_tensor * m = ggml_graph_node(g, j);
             if (m->op == GGML_OP_MUL && m->src[0] == n && m->src[1]->type == GGML_TYPE_F32 &&
                 ggml_are_same_shape(m, n) && node_index(gi, m->src[1]) < j) {
+                if (!no_norm_mm && norm_into_gemvs(g, gi, i, j)) {
+                    norm_of[(size_t) j]  = i;
+                    absorbed[(size_t) i] = 1;
+                    absorbed[(size_t) j] = 1;
+                    continue;
+                }
                 plan_step st;
                 st.kind = ST_NORM;
                 st.node = j;
@@ -1005,6 +1052,10 @@ graph_plan build_plan(struct ggml_cgraph * g) {
                 st.slot_in   = slot_of[(size_t) p];
                 st.vec_wtype = slot_wtype[(size_t) p];
             }
+            if (p >= 0 && norm_of[(size_t) p] >= 0) {
+                st.norm     = norm_of[(size_t) p];
+                st.norm_mul = p;
+            }
             // residual ADD in the store
             if (gi.uses[(size_t) i] == 1 && !is_output(n)) {
                 const int                  j   = gi.cons[(size_t) i];
@@ -1022,7 +1073,7 @@ graph_plan build_plan(struct ggml_cgraph * g) {
                     }
                 }
             }
-            if (st.slot_in < 0 && st.add >= 0) {
+            if (st.slot_in < 0 && st.norm < 0 && st.add >= 0) {
                 // quantise the activations into a slot of their own
                 st.vec_wtype = n->src[0]->type;
                 st.slot_in   = new_slot(st.vec_wtype, n->src[0]->ne[0], n->src[1]->ne[1]);
@@ -1051,7 +1102,7 @@ graph_plan build_plan(struct ggml_cgraph * g) {
                     st.src = -1;
                 }
             }
-            if (st.slot_in >= 0 || st.add >= 0) {
+            if (st.slot_in >= 0 || st.add >= 0 || st.norm >= 0) {
                 absorbed[(size_t) i] = 1;
                 add_pending(st);
                 continue;
@@ -1175,6 +1226,19 @@ int run_step(mi_backend * c, struct ggml_cgraph * g, const plan_step & st, char 
             const struct ggml_tensor * w  = mm->src[0];
             const struct ggml_tensor * x  = mm->src[1];
             const int64_t              N = w->ne[1], K = w->ne[0], M = x->ne[1] * x->ne[2] * x->ne[3];
+            if (st.norm >= 0) {
+                const struct ggml_tensor * rn  = ggml_graph_node(g, st.norm);
+                const struct ggml_tensor * xr  = rn->src[0];
+                const struct ggml_tensor * nwt = ggml_graph_node(g, st.norm_mul)->src[1];
+                const struct ggml_tensor * r   = st.add >= 0 ? ggml_graph_node(g, st.add)->src[st.add_res] : nullptr;
+                float                      eps;
+                memcpy(&eps, &rn->op_params[0], sizeof(float));
+                rc = mmhip_rms_norm_mul_mat(w->type, w->data, N, K, (int64_t) w->nb[1], (const float *) xr->data,
+                                            (int64_t) (xr->nb[1] / 4), M, (const float *) nwt->data, eps, nullptr,
+                                            r ? (const float *) r->data : nullptr, r ? (int64_t) (r->nb[1] / 4) : 0,
+                                            (float *) n->data, N, s);
+                break;
+            }
             if (st.src == -2) {
                 rc = mmhip_quantize_act(w->type, (const float *) x->data, (int64_t) (x->nb[1] / 4), K, M,
                                         slot + st.slot_in, s);

@@ -667,7 +667,7 @@ static void decode_plan(const FaArgs & a, int D, int & nsplit, int & chunk, int 
     // keys one workgroup pass covers (MFMA kernel: 4 waves x 16-key tiles)
     const int step = dec_mfma(a) ? 64 : 4 * kpw * dec_u(QR);
     const int base_wgs = a.Hkv * a.B * rowgroups;
-    const int target   = 512;
+    const int target   = 256;  // workgroups (measured: 256 vs 512 splits, a few % on the decode step)
     int       ns       = (target + base_wgs - 1) / base_wgs;
     // the combine kernel gives one thread per split: nsplit <= D
     const int max_ns   = std::max(1, std::min(D, (a.nkv + step - 1) / step));

@@ -182,6 +182,191 @@ __global__ __launch_bounds__(256) void k_gemv_q8_0(const uint8_t * __restrict__ 
     store_rows<NC, R>(acc, lane, g * R, N, y, ldy, res, ldr);
 }
 
+// Q8_0 GEMV that takes the raw activation rows of an RMS_NORM (+ MUL by the
+// norm weight) and does the norm and the Q8_0 activation quantisation in its
+// prologue.  Persistent: one 16-wave workgroup per CU.  Each wave streams the
+// weight rows (it * TW + wave) * P .. + P - 1 (TW waves in the grid) through
+// two register buffers, the next iteration's loads in flight while the
+// current one is reduced.  The first two iterations' loads are issued before
+// the prologue: the workgroup reads the M <= 8 rows (K <= 4096, from L2),
+// sums the squares in double, normalises, quantises into LDS (the arithmetic
+// of k_rms_norm_row + quant_chunk256) while the weights are in flight.  This
+// removes the separate norm kernel of the decode graph.
+constexpr int NQ_MAXK  = 4096;
+constexpr int NQ_WAVES = 16;  // waves per workgroup
+
+template <int P> struct NqBuf {
+    int4_t   w[P][NQ_MAXK / 1024];
+    uint16_t s[P][NQ_MAXK / 1024];
+};
+
+template <int P>
+__device__ __forceinline__ void nq_load(NqBuf<P> & b, const uint8_t * __restrict__ W, int64_t N, int K, int64_t rs,
+                                        int64_t row0, int lane) {
+#pragma unroll
+    for (int p = 0; p < P; p++) {
+        const uint8_t * wr = W + (row0 + p < N ? row0 + p : N - 1) * rs;
+#pragma unroll
+        for (int u = 0; u < NQ_MAXK / 1024; u++) {
+            const unsigned o = min(1024u * u + 16u * lane, (unsigned) K - 16u);
+            b.w[p][u]        = ld16(wr + o);
+            b.s[p][u]        = *(const uint16_t *) (wr + K + 2 * (o >> 5));
+        }
+    }
+}
+
+template <int NC, int P>
+__device__ __forceinline__ void nq_dot(const NqBuf<P> & b, const int8_t (*s_q)[NQ_MAXK], const float (*s_d)[NQ_MAXK / 32],
+                                       int K, int lane, int64_t row0, int64_t N, float * y, int64_t ldy,
+                                       const float * res, int64_t ldr) {
+    float acc[P][NC];
+#pragma unroll
+    for (int p = 0; p < P; p++) {
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            acc[p][c] = 0.0f;
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < NQ_MAXK / 1024; u++) {
+        const int  o  = min(1024 * u + lane * 16, K - 16);
+        const bool ok = 1024 * u + lane * 16 < K;
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const int4_t xq = *(const int4_t *) &s_q[c][o];
+            const float  dx = s_d[c][o >> 5];
+#pragma unroll
+            for (int p = 0; p < P; p++) {
+                const float dw = ok ? h2f(b.s[p][u]) : 0.0f;
+                acc[p][c] += (float) dot16(b.w[p][u], xq) * (dw * dx);
+            }
+        }
+    }
+    store_rows<NC, P>(acc, lane, row0, N, y, ldy, res, ldr);
+}
+
+template <int NC, int P>
+__global__ __launch_bounds__(64 * NQ_WAVES) void k_gemv_q8_0_nq(const uint8_t * __restrict__ W, int64_t N, int K,
+                                                                int64_t rs, const float * __restrict__ x, int64_t ldx,
+                                                                const float * __restrict__ nw, float eps,
+                                                                float * __restrict__ xn_out, float * y, int64_t ldy,
+                                                                const float * res, int64_t ldr, int nit) {
+    constexpr int J = NQ_MAXK / (256 * NQ_WAVES);  // float4 activation chunks per thread
+    __shared__ __attribute__((aligned(16))) int8_t s_q[NC][NQ_MAXK];
+    __shared__ float  s_d[NC][NQ_MAXK / 32];
+    __shared__ double s_ss[NC][NQ_WAVES];
+    const int     lane = threadIdx.x & 63;
+    const int     wv   = threadIdx.x >> 6;
+    const int64_t gw   = (int64_t) blockIdx.x * NQ_WAVES + wv;
+    const int64_t TW   = (int64_t) gridDim.x * NQ_WAVES;
+    // 1. the activation rows and the norm weight: chunk j of thread t holds
+    // elements e = 4 t + 256 NQ_WAVES j .. e + 3 (a 32-block is 8 adjacent
+    // lanes).  Issued first: loads return in order, so the prologue waits
+    // for these and not for the weights behind them.
+    float4_t xv[J][NC], wn[J];
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const unsigned e = min(4u * threadIdx.x + 256u * NQ_WAVES * j, (unsigned) K - 4u);
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            xv[j][c] = *(const float4_t *) (x + c * ldx + e);
+        }
+        wn[j] = *(const float4_t *) (nw + e);
+    }
+    // 2. the first two iterations' weight loads (unconditional: a row past
+    // N re-reads row N - 1 and is not stored)
+    NqBuf<P> ba, bb;
+    nq_load<P>(ba, W, N, K, rs, gw * P, lane);
+    nq_load<P>(bb, W, N, K, rs, (TW + gw) * P, lane);
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        if (4 * (int) threadIdx.x + 256 * NQ_WAVES * j >= K) {
+            xv[j][0] = float4_t{ 0.0f, 0.0f, 0.0f, 0.0f };
+#pragma unroll
+            for (int c = 1; c < NC; c++) {
+                xv[j][c] = xv[j][0];
+            }
+        }
+    }
+    // 3. sum of squares per row in double, then 4. normalise, times the norm
+    // weight, quantise per 32-block: the separate norm kernel's unfused f32
+    // arithmetic (the dot products keep the plain GEMV's FMAs)
+    {
+#pragma clang fp contract(off)
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            double ss = 0.0;
+#pragma unroll
+            for (int j = 0; j < J; j++) {
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    ss += (double) (xv[j][c][k] * xv[j][c][k]);
+                }
+            }
+            ss = wave_sum_d(ss);
+            if (lane == 0) {
+                s_ss[c][wv] = ss;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            double tot = 0.0;
+#pragma unroll
+            for (int w = 0; w < NQ_WAVES; w++) {
+                tot += s_ss[c][w];
+            }
+            const float mean = (float) (tot / (double) K);
+            const float sc   = 1.0f / sqrtf(mean + eps);
+#pragma unroll
+            for (int j = 0; j < J; j++) {
+                const int e = 4 * (int) threadIdx.x + 256 * NQ_WAVES * j;
+                float     o[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const float t = xv[j][c][k] * sc;
+                    o[k]          = t * wn[j][k];
+                }
+                float a = fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3])));
+                a       = fmaxf(a, __shfl_xor(a, 1, WAVE));
+                a       = fmaxf(a, __shfl_xor(a, 2, WAVE));
+                a       = fmaxf(a, __shfl_xor(a, 4, WAVE));
+                const float dd = a / 127.0f;
+                const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+                if (e < K) {
+                    char4 q;
+                    q.x                   = (signed char) roundf(o[0] * id);
+                    q.y                   = (signed char) roundf(o[1] * id);
+                    q.z                   = (signed char) roundf(o[2] * id);
+                    q.w                   = (signed char) roundf(o[3] * id);
+                    *(char4 *) &s_q[c][e] = q;
+                    if ((lane & 7) == 0) {
+                        s_d[c][e / 32] = h2f(f2h(dd));
+                    }
+                    if (xn_out && blockIdx.x == 0) {
+                        *(float4_t *) (xn_out + (int64_t) c * K + e) = float4_t{ o[0], o[1], o[2], o[3] };
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+    // 5. stream the rows: reduce one buffer while the other's loads fly.  The
+    // steady-state loop's loads are unconditional so that each reduction
+    // waits for its own buffer only.
+    int it = 0;
+    for (; it + 2 < nit; it += 2) {
+        nq_dot<NC, P>(ba, s_q, s_d, K, lane, (it * TW + gw) * P, N, y, ldy, res, ldr);
+        nq_load<P>(ba, W, N, K, rs, ((it + 2) * TW + gw) * P, lane);
+        nq_dot<NC, P>(bb, s_q, s_d, K, lane, ((it + 1) * TW + gw) * P, N, y, ldy, res, ldr);
+        nq_load<P>(bb, W, N, K, rs, ((it + 3) * TW + gw) * P, lane);
+    }
+    nq_dot<NC, P>(ba, s_q, s_d, K, lane, (it * TW + gw) * P, N, y, ldy, res, ldr);
+    if (it + 1 < nit) {
+        nq_dot<NC, P>(bb, s_q, s_d, K, lane, ((it + 1) * TW + gw) * P, N, y, ldy, res, ldr);
+    }
+}
+
 // Q4_K.  Wave-chunk = 1024 bytes of qs (8 super-blocks); lane l owns 16
 // bytes = elements e_lo..e_lo+15 (low nibbles, sub-block 2c) and
 // e_lo+32..e_lo+47 (high nibbles, sub-block 2c+1) of super-block sb.
@@ -515,4 +700,84 @@ extern "C" int mmhip_mul_mat_q_add(int type, const void * W, int64_t N, int64_t 
         return set_error(MMHIP_ERR_INVALID, "mul_mat_q_add: bad arguments (type %d, K=%lld)", type, (long long) K);
     }
     return gemv_q(type, W, N, K, w_row_stride, ActPtrs::from(L, xq), M, y, ldy, (hipStream_t) stream, r, ldr);
+}
+
+namespace mmhip {
+// compute units of the current device (the persistent grid's size)
+static int64_t nq_cus() {
+    static int cached[64] = {};
+    int        dev        = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        return 256;
+    }
+    if (!cached[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+            n = 256;
+        }
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+struct NqArgs {
+    const uint8_t * W;
+    int64_t         N;
+    int             K;
+    int64_t         rs;
+    const float *   x;
+    int64_t         ldx;
+    const float *   nw;
+    float           eps;
+    float *         xn;
+    float *         y;
+    int64_t         ldy;
+    const float *   res;
+    int64_t         ldr;
+};
+
+template <int NC, int P>
+static int launch_nq(const NqArgs & a, hipStream_t stream) {
+    // one resident workgroup per CU; the rows split evenly over the iterations
+    const int64_t per_wg = (int64_t) NQ_WAVES * P;
+    const int64_t need   = (a.N + per_wg - 1) / per_wg;  // workgroups for one iteration
+    const int64_t nit    = (need + nq_cus() - 1) / nq_cus();
+    const int64_t wgs    = (need + nit - 1) / nit;
+    if (nit > 0x7fffffff) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "rms_norm_mul_mat: N=%lld too large", (long long) a.N);
+    }
+    auto kern = k_gemv_q8_0_nq<NC, P>;
+    hipLaunchKernelGGL(kern, dim3((unsigned) wgs), dim3(64 * NQ_WAVES), 0, stream, a.W, a.N, a.K, a.rs, a.x, a.ldx,
+                       a.nw, a.eps, a.xn, a.y, a.ldy, a.res, a.ldr, (int) nit);
+    return check_launch("rms_norm_mul_mat");
+}
+
+template <int NC>
+static int dispatch_nq(const NqArgs & a, hipStream_t stream) {
+    return launch_nq<NC, 1>(a, stream);
+}
+}  // namespace mmhip
+
+extern "C" int mmhip_rms_norm_mul_mat_supported(int type, int64_t N, int64_t K, int64_t M) {
+    // M <= 2: the quantised rows stay in registers across the row loop
+    return type == TYPE_Q8_0 && N > 0 && M >= 1 && M <= 2 && K >= 256 && K <= NQ_MAXK && K % 256 == 0;
+}
+
+extern "C" int mmhip_rms_norm_mul_mat(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride,
+                                      const float * x, int64_t ldx, int64_t M, const float * norm_w, float eps,
+                                      float * xn_out, const float * res, int64_t ldr, float * y, int64_t ldy,
+                                      void * stream) {
+    MMHIP_API_BEGIN();
+    if (!mmhip_rms_norm_mul_mat_supported(type, N, K, M)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "rms_norm_mul_mat: type %d N=%lld K=%lld M=%lld", type, (long long) N,
+                         (long long) K, (long long) M);
+    }
+    if (!W || !x || !norm_w || !y || ldx < K || ldy < N || (res && ldr < N) ||
+        !gemv_supported(type, N, K, w_row_stride, W) ||
+        ((uintptr_t) x | (uintptr_t) norm_w | (uintptr_t) xn_out) % 16 != 0 || (ldx % 4) != 0) {
+        return set_error(MMHIP_ERR_INVALID, "rms_norm_mul_mat: bad arguments / alignment");
+    }
+    const NqArgs a{ (const uint8_t *) W, N, (int) K, w_row_stride, x, ldx, norm_w, eps, xn_out, y, ldy, res, ldr };
+    hipStream_t  st = (hipStream_t) stream;
+    return M == 1 ? dispatch_nq<1>(a, st) : dispatch_nq<2>(a, st);
 }

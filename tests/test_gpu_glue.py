@@ -322,3 +322,49 @@ def test_head_rows_three_chains_one_launch(mm, orc):
         outs.append((qout, kc, vc))
     for x, y in zip(outs[0], outs[1]):
         assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("M,K,N,ldx", [(2, 4096, 6144, 4096), (1, 1024, 300, 1088), (2, 2048, 9000, 2048),
+                                       (2, 4096, 30000, 4096), (1, 256, 77, 320), (2, 1024, 70001, 1024)])
+def test_rms_norm_mul_mat_equals_two_pass(mm, pkg, M, K, N, ldx):
+    """GEMV with the RMS norm + quantisation in its prologue is bit-identical
+    to rms_norm_quant then mul_mat_q (and mul_mat_q_add with a residual);
+    N from one to eight row iterations of the persistent grid, odd tails."""
+    L = mm.load()
+    Wq = mm.QuantWeight.from_gguf(8, pkg.synth.gguf_blocks_np(8, N, K, 5), N, K)
+    rng = np.random.default_rng(26)
+    xb = torch.from_numpy((rng.standard_normal((M, ldx)) * 3).astype(np.float32)).cuda()
+    x = xb[:, :K]
+    w = torch.from_numpy((1 + 0.05 * rng.standard_normal(K)).astype(np.float32)).cuda()
+    r = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float32)).cuda()
+    assert L.mmhip_rms_norm_mul_mat_supported(8, N, K, M) == 1
+    xn = torch.empty((M, K), dtype=torch.float32, device="cuda")
+    xq = torch.zeros(L.mmhip_act_bytes(8, K, M), dtype=torch.uint8, device="cuda")
+    assert L.mmhip_rms_norm_quant(ctypes.byref(mm.view_of(x)), ctypes.byref(mm.view_of(w)), 1e-6, ptr(xn), 8,
+                                  ptr(xq), st()) == 0
+    y1 = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    assert L.mmhip_mul_mat_q(8, ptr(Wq.data), N, K, Wq.row_bytes, ptr(xq), M, ptr(y1), N, st()) == 0
+    y2 = torch.full((M, N), float("nan"), device="cuda")
+    xn2 = torch.full((M, K), float("nan"), device="cuda")
+    assert L.mmhip_rms_norm_mul_mat(8, ptr(Wq.data), N, K, Wq.row_bytes, ptr(x), ldx, M, ptr(w), 1e-6, ptr(xn2),
+                                    None, 0, ptr(y2), N, st()) == 0
+    y3 = torch.empty_like(y1)
+    assert L.mmhip_rms_norm_mul_mat(8, ptr(Wq.data), N, K, Wq.row_bytes, ptr(x), ldx, M, ptr(w), 1e-6, None,
+                                    ptr(r), N, ptr(y3), N, st()) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(y2, y1)
+    assert torch.equal(xn2, xn)
+    assert torch.equal(y3, y1 + r)
+
+
+def test_rms_norm_mul_mat_rejects_unsupported(mm):
+    """Shapes outside the fused kernel's limits are refused before any launch."""
+    L = mm.load()
+    assert L.mmhip_rms_norm_mul_mat_supported(8, 4096, 4352, 2) == 0   # K > 4096
+    assert L.mmhip_rms_norm_mul_mat_supported(8, 4096, 4096, 3) == 0   # M > 2
+    assert L.mmhip_rms_norm_mul_mat_supported(12, 4096, 4096, 2) == 0  # Q4_K weights
+    assert L.mmhip_rms_norm_mul_mat_supported(8, 4096, 1000, 2) == 0   # K % 256
+    dummy = torch.zeros(16, dtype=torch.float32, device="cuda")
+    rc = L.mmhip_rms_norm_mul_mat(8, ptr(dummy), 4096, 4352, 4624, ptr(dummy), 4352, 2, ptr(dummy), 1e-6, None,
+                                  None, 0, ptr(dummy), 4096, st())
+    assert rc != 0
