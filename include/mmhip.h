@@ -106,6 +106,19 @@ int mmhip_rms_norm_mul_mat_supported(int type, int64_t N, int64_t K, int64_t M);
 int mmhip_rms_norm_mul_mat(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const float * x,
                            int64_t ldx, int64_t M, const float * norm_w, float eps, float * xn_out, const float * r,
                            int64_t ldr, float * y, int64_t ldy, void * stream);
+/* The GEMV that follows a SwiGLU, with the SwiGLU in its prologue: the
+ * GGML_OP_GLU (swiglu / swiglu_split, src/qwen3-enc.h:106-113) feeding the
+ * MLP down GGML_OP_MUL_MAT (src/qwen3-enc.h:114) whose residual GGML_OP_ADD
+ * follows (src/qwen3-lm.h:835-836).  g and u hold the M gate and up rows
+ * (row strides ldg / ldu floats); each workgroup recomputes silu(g) * u and
+ * its activation quantisation with the arithmetic of mmhip_swiglu_quant, so
+ * y equals swiglu_quant + mul_mat_q(_add) bit for bit.  h_out (optional)
+ * receives the f32 SwiGLU rows [M, K]; r (optional) is the residual.  Q8_0
+ * weights, M <= 2, K a multiple of 256 up to 12288.  y must not overlap g/u. */
+int mmhip_swiglu_mul_mat_supported(int type, int64_t N, int64_t K, int64_t M);
+int mmhip_swiglu_mul_mat(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const float * g,
+                         int64_t ldg, const float * u, int64_t ldu, int64_t M, float * h_out, const float * r,
+                         int64_t ldr, float * y, int64_t ldy, void * stream);
 
 /* ---------------------------------------------------------------------
  * GGML_OP_FLASH_ATTN_EXT, replacing the ggml backend kernel behind

@@ -19,6 +19,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -691,6 +692,7 @@ struct plan_step {
     int                  add_res = -1;   // MM: index 0/1 of the ADD's residual source
     int                  norm    = -1;   // MM: the RMS_NORM node whose norm runs in the GEMV's prologue
     int                  norm_mul = -1;  // MM: the MUL by the norm weight (the GEMV's src1)
+    int                  glu      = -1;  // MM: the SWIGLU node whose SwiGLU runs in the GEMV's prologue
     int64_t              slot_out = -1;  // byte offset of the quantised slot written (NORM / SWIGLU_Q)
     int64_t              slot_in  = -1;  // byte offset of the slot read (MM)
     int                  vec_wtype = 0;  // weight type the slot is quantised for
@@ -794,6 +796,58 @@ bool norm_into_gemvs(struct ggml_cgraph * g, const graph_info & gi, int i, int j
     for (int t = j + 1; t <= last; t++) {
         const struct ggml_tensor * nt = ggml_graph_node(g, t);
         if (!is_noop(nt->op) && overlaps(nt, x)) {
+            return false;
+        }
+    }
+    return true;
+}
+
+// The gate and up rows of a SWIGLU node (fused: the two halves of src0,
+// swapped by op_params[1]; split: src0 and src1), each M rows of a uniform
+// stride.  False when the layout is not one the SwiGLU GEMV reads.
+bool glu_rows(const struct ggml_tensor * n, const float *& gate, int64_t & ldg, const float *& up, int64_t & ldu) {
+    const struct ggml_tensor * a = n->src[0];
+    const struct ggml_tensor * b = n->src[1];
+    const int64_t              F = n->ne[0];
+    auto rows_ok = [&](const struct ggml_tensor * t) {
+        return t->type == GGML_TYPE_F32 && mm_collapsible(t) && ggml_nrows(t) == ggml_nrows(n) &&
+               ((uintptr_t) t->data | t->nb[1]) % 16 == 0;
+    };
+    if (!rows_ok(a) || (b && (!rows_ok(b) || b->ne[0] != F)) || (!b && a->ne[0] != 2 * F)) {
+        return false;
+    }
+    const bool swapped = n->op_params[1] != 0;
+    gate = (const float *) a->data + (!b && swapped ? F : 0);
+    up   = b ? (const float *) b->data : (const float *) a->data + (swapped ? 0 : F);
+    ldg  = (int64_t) (a->nb[1] / 4);
+    ldu  = b ? (int64_t) (b->nb[1] / 4) : ldg;
+    return true;
+}
+
+// Can every consumer of SWIGLU node i be a GEMV that recomputes the SwiGLU
+// itself (mmhip_swiglu_mul_mat)?  Its inputs must then stay intact until the
+// last of them ran.
+bool glu_into_gemvs(struct ggml_cgraph * g, const graph_info & gi, int i) {
+    const struct ggml_tensor * n = ggml_graph_node(g, i);
+    const float *              gp;
+    const float *              up;
+    int64_t                    ldg, ldu;
+    if (is_output(n) || gi.consumers[(size_t) i].empty() || !glu_rows(n, gp, ldg, up, ldu)) {
+        return false;
+    }
+    const int64_t K = n->ne[0], M = ggml_nrows(n);
+    int           last = i;
+    for (int ci : gi.consumers[(size_t) i]) {
+        const struct ggml_tensor * mm = ggml_graph_node(g, ci);
+        if (mm->op != GGML_OP_MUL_MAT || mm->src[1] != n || mm->src[0] == n || !mm_is_gemv(mm) ||
+            !mmhip_swiglu_mul_mat_supported(mm->src[0]->type, mm->src[0]->ne[1], K, M)) {
+            return false;
+        }
+        last = std::max(last, gi.uses[(size_t) ci] == 1 ? std::max(ci, gi.cons[(size_t) ci]) : ci);
+    }
+    for (int t = i + 1; t <= last; t++) {
+        const struct ggml_tensor * nt = ggml_graph_node(g, t);
+        if (!is_noop(nt->op) && (overlaps(nt, n->src[0]) || (n->src[1] && overlaps(nt, n->src[1])))) {
             return false;
         }
     }
@@ -964,6 +1018,8 @@ graph_plan build_plan(struct ggml_cgraph * g) {
     std::vector<int>         slot_wtype((size_t) gi.nn, 0);
     std::vector<int>         norm_of((size_t) gi.nn, -1);  // MUL node -> its RMS_NORM, norm done by the GEMVs
     const bool               no_norm_mm = getenv("GGML_MI355X_DISABLE_NORM_GEMV") != nullptr;
+    std::vector<char>        glu_mm((size_t) gi.nn, 0);  // SWIGLU node done by its GEMVs
+    const bool               no_glu_mm = getenv("GGML_MI355X_DISABLE_SWIGLU_GEMV") != nullptr;
     auto add_pending = [&](const plan_step & st) {
         step_at[(size_t) st.node] = (int) pending.size();
         pending.push_back(st);
@@ -1013,6 +1069,12 @@ graph_plan build_plan(struct ggml_cgraph * g) {
                 continue;
             }
         }
+        if (n->op == GGML_OP_GLU && n->op_params[0] == GGML_GLU_OP_SWIGLU && rows_contiguous_f32(n) && !no_glu_mm &&
+            glu_into_gemvs(g, gi, i)) {
+            glu_mm[(size_t) i]   = 1;
+            absorbed[(size_t) i] = 1;
+            continue;
+        }
         if (n->op == GGML_OP_GLU && n->op_params[0] == GGML_GLU_OP_SWIGLU && rows_contiguous_f32(n)) {
             const struct ggml_tensor * a  = n->src[0];
             const int                  wt = gemv_consumer_type(g, gi, i);
@@ -1056,6 +1118,9 @@ graph_plan build_plan(struct ggml_cgraph * g) {
                 st.norm     = norm_of[(size_t) p];
                 st.norm_mul = p;
             }
+            if (p >= 0 && glu_mm[(size_t) p]) {
+                st.glu = p;
+            }
             // residual ADD in the store
             if (gi.uses[(size_t) i] == 1 && !is_output(n)) {
                 const int                  j   = gi.cons[(size_t) i];
@@ -1073,7 +1138,7 @@ graph_plan build_plan(struct ggml_cgraph * g) {
                     }
                 }
             }
-            if (st.slot_in < 0 && st.norm < 0 && st.add >= 0) {
+            if (st.slot_in < 0 && st.norm < 0 && st.glu < 0 && st.add >= 0) {
                 // quantise the activations into a slot of their own
                 st.vec_wtype = n->src[0]->type;
                 st.slot_in   = new_slot(st.vec_wtype, n->src[0]->ne[0], n->src[1]->ne[1]);
@@ -1102,7 +1167,7 @@ graph_plan build_plan(struct ggml_cgraph * g) {
                     st.src = -1;
                 }
             }
-            if (st.slot_in >= 0 || st.add >= 0 || st.norm >= 0) {
+            if (st.slot_in >= 0 || st.add >= 0 || st.norm >= 0 || st.glu >= 0) {
                 absorbed[(size_t) i] = 1;
                 add_pending(st);
                 continue;
@@ -1237,6 +1302,21 @@ int run_step(mi_backend * c, struct ggml_cgraph * g, const plan_step & st, char 
                                             (int64_t) (xr->nb[1] / 4), M, (const float *) nwt->data, eps, nullptr,
                                             r ? (const float *) r->data : nullptr, r ? (int64_t) (r->nb[1] / 4) : 0,
                                             (float *) n->data, N, s);
+                break;
+            }
+            if (st.glu >= 0) {
+                const struct ggml_tensor * gn = ggml_graph_node(g, st.glu);
+                const struct ggml_tensor * r  = st.add >= 0 ? ggml_graph_node(g, st.add)->src[st.add_res] : nullptr;
+                const float *              gp = nullptr;
+                const float *              up = nullptr;
+                int64_t                    ldg = 0, ldu = 0;
+                if (!glu_rows(gn, gp, ldg, up, ldu)) {
+                    rc = MMHIP_ERR_INVALID;
+                    break;
+                }
+                rc = mmhip_swiglu_mul_mat(w->type, w->data, N, K, (int64_t) w->nb[1], gp, ldg, up, ldu, M, nullptr,
+                                          r ? (const float *) r->data : nullptr, r ? (int64_t) (r->nb[1] / 4) : 0,
+                                          (float *) n->data, N, s);
                 break;
             }
             if (st.src == -2) {

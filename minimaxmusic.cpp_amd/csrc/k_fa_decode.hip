@@ -247,9 +247,11 @@ __global__ __launch_bounds__(256) void k_fa_decode(FaArgs a, int chunk, int nspl
 
 // ---------------------------------------------------------------------
 // MFMA decode: the G * nq (<= 16) query rows of one KV head are the columns
-// of 16 x 16 MFMA tiles.  Workgroup = (split, KV head, batch), 4 waves; the
+// of 16 x 16 MFMA tiles.  Workgroup = (split, KV head, batch), NW waves; the
 // split's keys are dealt to the waves in 16-key tiles (wave w: tiles w,
-// w + 4, ...), each wave keeping its own online-softmax state.
+// w + NW, ...), each wave keeping its own online-softmax state.  A wave
+// issues the loads of TP tiles at once: with the split sized to NW * TP
+// tiles every load of the workgroup is in flight before the first use.
 //   S^T (16 keys x 16 cols) = K Q^T with mfma_f32_16x16x32_f16: lane l owns
 //     key l % 16 and dims 32s + 8(l / 16) .. +7 of the A operand, a 16-byte
 //     load straight from the cache; Q^T is the B operand, held in registers.
@@ -261,17 +263,25 @@ __global__ __launch_bounds__(256) void k_fa_decode(FaArgs a, int chunk, int nspl
 // Scores, softmax and the partial format are those of k_fa_decode, and the
 // same combine kernel merges the splits.
 
-template <int D>
-__global__ __launch_bounds__(256) void k_fa_dec_mfma(FaArgs a, int chunk, int nsplit, float * __restrict__ part_o,
-                                                     float * __restrict__ part_ml, float * __restrict__ out) {
+#ifndef DEC_NW
+#define DEC_NW 8  // waves per MFMA decode workgroup
+#endif
+// waves per workgroup at head size D (the merge buffer is NW * 16 * D floats)
+constexpr int dec_nw(int D) {
+    return D >= 256 && DEC_NW > 8 ? 8 : DEC_NW;
+}
+
+template <int D, int NW, int TP>
+__global__ __launch_bounds__(64 * NW) void k_fa_dec_mfma(FaArgs a, int chunk, int nsplit, float * __restrict__ part_o,
+                                                         float * __restrict__ part_ml, float * __restrict__ out) {
     constexpr int NS  = D / 32;  // k-steps of Q.K (32 dims each)
     constexpr int NDB = D / 16;  // 16-dim blocks of O^T
     constexpr int VTS = 16 + 4;  // V^T row stride (halves): 16 keys + pad
-    constexpr int TP  = 2;       // tiles per wave per load round
-    constexpr int SVT = 4 * D * VTS;            // halves of the 4 waves' V^T tiles
-    constexpr int SO  = 4 * 16 * D * 2;         // halves of the merge buffer (floats)
+    constexpr int SVT = NW * D * VTS;     // halves of the waves' V^T tiles
+    constexpr int OS  = D + 4;             // merge-buffer row stride (floats): rows 4 banks apart
+    constexpr int SO  = NW * 16 * OS * 2;  // halves of the merge buffer (floats)
     __shared__ __attribute__((aligned(16))) _Float16 s_buf[SVT > SO ? SVT : SO];
-    __shared__ float s_m[4][16], s_l[4][16];
+    __shared__ float s_m[NW][16], s_l[NW][16];
 
     const int split = blockIdx.x;
     const int g     = blockIdx.y;
@@ -308,7 +318,7 @@ __global__ __launch_bounds__(256) void k_fa_dec_mfma(FaArgs a, int chunk, int ns
     auto     load_tiles = [&](int t0) {
 #pragma unroll
         for (int p = 0; p < TP; p++) {
-            const int t   = t0 + 4 * p;
+            const int t   = t0 + NW * p;
             const int key = min(kbeg + 16 * t + col, kend - 1);
 #pragma unroll
             for (int s = 0; s < NS; s++) {
@@ -321,19 +331,42 @@ __global__ __launch_bounds__(256) void k_fa_dec_mfma(FaArgs a, int chunk, int ns
             }
         }
     };
+    // the first tiles, unconditionally (keys are clamped into the split):
+    // loads return in order, and a load under a condition makes the compiler
+    // wait for everything issued before it
     int t0 = wave;
-    if (t0 < ntile) {
-        load_tiles(t0);
+    load_tiles(t0);
+    // Q^T B operand: column col, dims 32s + 8kq .. +7 (zero for unused
+    // columns; an unused column reads column 0's row)
+    float         qf[NS][8];
+    const float * qp  = (const float *) (a.q + iq * a.qnb1 + hq * a.qnb2 + b * a.qnb3) + 8 * kq;
+    const bool    q16 = (((uintptr_t) a.q | (uintptr_t) a.qnb1 | (uintptr_t) a.qnb2 | (uintptr_t) a.qnb3) & 15) == 0;
+    if (q16) {  // uniform
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            const float4_t lo = *(const float4_t *) (qp + 32 * s);
+            const float4_t hi = *(const float4_t *) (qp + 32 * s + 4);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                qf[s][i]     = lo[i];
+                qf[s][4 + i] = hi[i];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                qf[s][i] = qp[32 * s + i];
+            }
+        }
     }
-
-    // Q^T B operand: column col, dims 32s + 8kq .. +7 (zero for unused columns)
-    half8_t       qb[NS];
-    const float * qp = (const float *) (a.q + iq * a.qnb1 + hq * a.qnb2 + b * a.qnb3) + 8 * kq;
+    half8_t qb[NS];
 #pragma unroll
     for (int s = 0; s < NS; s++) {
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            qb[s][i] = cvalid ? (_Float16) qp[32 * s + i] : (_Float16) 0.0f;
+            qb[s][i] = cvalid ? (_Float16) qf[s][i] : (_Float16) 0.0f;
         }
     }
 
@@ -347,10 +380,10 @@ __global__ __launch_bounds__(256) void k_fa_dec_mfma(FaArgs a, int chunk, int ns
     const float log2e = 1.4426950408889634f;
     const float sl2   = a.scale * log2e;
 
-    for (; t0 < ntile; t0 += 4 * TP) {
+    for (; t0 < ntile; t0 += NW * TP) {
 #pragma unroll
         for (int p = 0; p < TP; p++) {
-            const int t = t0 + 4 * p;
+            const int t = t0 + NW * p;
             if (t >= ntile) {
                 break;  // uniform over the wave
             }
@@ -412,41 +445,43 @@ __global__ __launch_bounds__(256) void k_fa_dec_mfma(FaArgs a, int chunk, int ns
             }
             __builtin_amdgcn_wave_barrier();
         }
-        if (t0 + 4 * TP < ntile) {
-            load_tiles(t0 + 4 * TP);
+        if (t0 + NW * TP < ntile) {
+            load_tiles(t0 + NW * TP);
         }
     }
 
-    // merge the 4 waves (LDS reused: V^T tiles are done)
+    // merge the NW waves (LDS reused: V^T tiles are done)
     __syncthreads();
-    float * s_o = (float *) s_buf;  // [4][16][D]
+    float * s_o = (float *) s_buf;  // [NW][16][OS]
     if (kq == 0) {
         s_m[wave][col] = m;
         s_l[wave][col] = l;
     }
+    if (cvalid) {  // the merge reads the ncol used columns only
 #pragma unroll
-    for (int db = 0; db < NDB; db++) {
+        for (int db = 0; db < NDB; db++) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            s_o[(wave * 16 + col) * D + 16 * db + 4 * kq + i] = oacc[db][i];
+            for (int i = 0; i < 4; i++) {
+                s_o[(wave * 16 + col) * OS + 16 * db + 4 * kq + i] = oacc[db][i];
+            }
         }
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < ncol * D; idx += 256) {
+    for (int idx = threadIdx.x; idx < ncol * D; idx += 64 * NW) {
         const int c = idx / D;
         const int d = idx % D;
         float     M = s_m[0][c];
 #pragma unroll
-        for (int w = 1; w < 4; w++) {
+        for (int w = 1; w < NW; w++) {
             M = fmaxf(M, s_m[w][c]);
         }
         float L = 0.0f, O = 0.0f;
         if (M != -INFINITY) {
 #pragma unroll
-            for (int w = 0; w < 4; w++) {
+            for (int w = 0; w < NW; w++) {
                 const float f = s_m[w][c] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s_m[w][c] - M);
                 L += s_l[w][c] * f;
-                O += s_o[(w * 16 + c) * D + d] * f;
+                O += s_o[(w * 16 + c) * OS + d] * f;
             }
         }
         const int h  = g * G + c % G;
@@ -664,8 +699,8 @@ static void decode_plan(const FaArgs & a, int D, int & nsplit, int & chunk, int 
     const int QR   = dec_qr(a);
     rowgroups      = dec_mfma(a) ? 1 : (G * a.nq + QR - 1) / QR;
     const int kpw  = 64 / (D / 8);
-    // keys one workgroup pass covers (MFMA kernel: 4 waves x 16-key tiles)
-    const int step = dec_mfma(a) ? 64 : 4 * kpw * dec_u(QR);
+    // keys one workgroup pass covers (MFMA kernel: one 16-key tile per wave)
+    const int step = dec_mfma(a) ? 16 * dec_nw(D) : 4 * kpw * dec_u(QR);
     const int base_wgs = a.Hkv * a.B * rowgroups;
     const int target   = 256;  // workgroups (measured: 256 vs 512 splits, a few % on the decode step)
     int       ns       = (target + base_wgs - 1) / base_wgs;
@@ -696,6 +731,21 @@ static void launch_decode(const FaArgs & a, int QR, dim3 grid, int chunk, int ns
     }
 }
 
+template <int D>
+static int launch_dec_mfma(dim3 g3, int tiles, const FaArgs & a, int chunk, int nsplit, float * po, float * pml,
+                           float * out, hipStream_t stream) {
+    // D = 256 holds twice the fragments per tile: one tile per load round
+    constexpr int NW = dec_nw(D);
+    if constexpr (D <= 128) {
+        if (tiles >= 2) {
+            hipLaunchKernelGGL((k_fa_dec_mfma<D, NW, 2>), g3, dim3(64 * NW), 0, stream, a, chunk, nsplit, po, pml, out);
+            return check_launch("flash_attn decode");
+        }
+    }
+    hipLaunchKernelGGL((k_fa_dec_mfma<D, NW, 1>), g3, dim3(64 * NW), 0, stream, a, chunk, nsplit, po, pml, out);
+    return check_launch("flash_attn decode");
+}
+
 // The MFMA decode kernel serves up to 16 query rows per KV head.
 static bool dec_mfma(const FaArgs & a) {
     return (a.Hq / a.Hkv) * a.nq <= 16;
@@ -724,11 +774,17 @@ int fa_decode(const FaArgs & a, int D, float * out, void * ws, size_t ws_bytes, 
     }
     if (dec_mfma(a)) {
         const dim3 g3(nsplit, a.Hkv, a.B);
+        // tiles per wave: the split's tiles in one load round where that fits
+        const int tiles = (chunk / 16 + dec_nw(D) - 1) / dec_nw(D);
+        int       rc    = MMHIP_OK;
         switch (D) {
-            case 64: hipLaunchKernelGGL(k_fa_dec_mfma<64>, g3, dim3(256), 0, stream, a, chunk, nsplit, part_o, part_ml, out); break;
-            case 128: hipLaunchKernelGGL(k_fa_dec_mfma<128>, g3, dim3(256), 0, stream, a, chunk, nsplit, part_o, part_ml, out); break;
-            case 256: hipLaunchKernelGGL(k_fa_dec_mfma<256>, g3, dim3(256), 0, stream, a, chunk, nsplit, part_o, part_ml, out); break;
+            case 64: rc = launch_dec_mfma<64>(g3, tiles, a, chunk, nsplit, part_o, part_ml, out, stream); break;
+            case 128: rc = launch_dec_mfma<128>(g3, tiles, a, chunk, nsplit, part_o, part_ml, out, stream); break;
+            case 256: rc = launch_dec_mfma<256>(g3, tiles, a, chunk, nsplit, part_o, part_ml, out, stream); break;
             default: return set_error(MMHIP_ERR_UNSUPPORTED, "flash_attn decode: head dim %d", D);
+        }
+        if (rc != MMHIP_OK) {
+            return rc;
         }
     } else {
     const dim3 grid(nsplit, a.Hkv, a.B * rg);

@@ -182,188 +182,240 @@ __global__ __launch_bounds__(256) void k_gemv_q8_0(const uint8_t * __restrict__ 
     store_rows<NC, R>(acc, lane, g * R, N, y, ldy, res, ldr);
 }
 
-// Q8_0 GEMV that takes the raw activation rows of an RMS_NORM (+ MUL by the
-// norm weight) and does the norm and the Q8_0 activation quantisation in its
-// prologue.  Persistent: one 16-wave workgroup per CU.  Each wave streams the
-// weight rows (it * TW + wave) * P .. + P - 1 (TW waves in the grid) through
-// two register buffers, the next iteration's loads in flight while the
-// current one is reduced.  The first two iterations' loads are issued before
-// the prologue: the workgroup reads the M <= 8 rows (K <= 4096, from L2),
-// sums the squares in double, normalises, quantises into LDS (the arithmetic
-// of k_rms_norm_row + quant_chunk256) while the weights are in flight.  This
-// removes the separate norm kernel of the decode graph.
-constexpr int NQ_MAXK  = 4096;
-constexpr int NQ_WAVES = 16;  // waves per workgroup
+// Persistent Q8_0 GEMVs whose activation rows are made in their prologue:
+//   PRO_NORM    the raw rows of an RMS_NORM (+ MUL by the norm weight): sum of
+//               squares in double, normalise, times the weight (the arithmetic
+//               of k_rms_norm_row);
+//   PRO_SWIGLU  silu(gate) * up (the arithmetic of k_swiglu_quant);
+// then the Q8_0 activation quantisation of quant_chunk256 into LDS.  This
+// removes the separate norm / SwiGLU kernel of the decode graph.
+// One 16-wave workgroup per CU.  Each wave streams the weight rows
+// it * TW + wave (TW waves in the grid); for K <= 4096 through two register
+// buffers, the next iteration's loads in flight while the current one is
+// reduced.  Activations are loaded first, then the first weight rows: loads
+// return in order, so the prologue runs while the weights are in flight.
+constexpr int PG_WAVES   = 16;  // waves per workgroup
+constexpr int PRO_NORM   = 0;
+constexpr int PRO_SWIGLU = 1;
 
-template <int P> struct NqBuf {
-    int4_t   w[P][NQ_MAXK / 1024];
-    uint16_t s[P][NQ_MAXK / 1024];
+struct PgArgs {
+    const uint8_t * W;
+    int64_t         N;
+    int             K;
+    int64_t         rs;
+    const float *   x;  // NORM: raw rows; SWIGLU: gate rows
+    int64_t         ldx;
+    const float *   u;  // SWIGLU: up rows
+    int64_t         ldu;
+    const float *   nw;  // NORM: norm weight
+    float           eps;
+    float *         xo;  // optional f32 activation rows [M, K] (written by workgroup 0)
+    float *         y;
+    int64_t         ldy;
+    const float *   res;
+    int64_t         ldr;
+    int             nit;  // row iterations (uniform)
 };
 
-template <int P>
-__device__ __forceinline__ void nq_load(NqBuf<P> & b, const uint8_t * __restrict__ W, int64_t N, int K, int64_t rs,
-                                        int64_t row0, int lane) {
+template <int CH> struct PgBuf {
+    int4_t   w[CH];
+    uint16_t s[CH];
+};
+
+// chunks U0 .. U1 - 1 of a row into b: buffer loads off the row's (uniform)
+// base, so each chunk costs one 32-bit offset register; lanes past K re-read
+// the row's last 16 bytes and are weighted by zero
+template <int CH, int U0 = 0, int U1 = CH>
+__device__ __forceinline__ void pg_load(PgBuf<CH> & b, const PgArgs & a, int64_t row, int lane) {
+    const uint8_t *              wr = a.W + (row < a.N ? row : a.N - 1) * a.rs;
+    const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc((void *) wr, (short) 0, a.K + a.K / 16,
+                                                                        0x00020000);
 #pragma unroll
-    for (int p = 0; p < P; p++) {
-        const uint8_t * wr = W + (row0 + p < N ? row0 + p : N - 1) * rs;
-#pragma unroll
-        for (int u = 0; u < NQ_MAXK / 1024; u++) {
-            const unsigned o = min(1024u * u + 16u * lane, (unsigned) K - 16u);
-            b.w[p][u]        = ld16(wr + o);
-            b.s[p][u]        = *(const uint16_t *) (wr + K + 2 * (o >> 5));
-        }
+    for (int u = U0; u < U1; u++) {
+        const unsigned o = min(1024u * u + 16u * lane, (unsigned) a.K - 16u);
+        b.w[u]           = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(rr, (int) o, 0, 0));
+        b.s[u]           = __builtin_amdgcn_raw_buffer_load_b16(rr, a.K + 2 * (int) (o >> 5), 0, 0);
     }
 }
 
-template <int NC, int P>
-__device__ __forceinline__ void nq_dot(const NqBuf<P> & b, const int8_t (*s_q)[NQ_MAXK], const float (*s_d)[NQ_MAXK / 32],
-                                       int K, int lane, int64_t row0, int64_t N, float * y, int64_t ldy,
-                                       const float * res, int64_t ldr) {
-    float acc[P][NC];
+// one row against the NC quantised rows in LDS (sq: [NC][1024 CH], sd:
+// [NC][32 CH]); off is added to the LDS indices (an opaque zero keeps the
+// reads inside a loop where the rows do not fit in registers)
+template <int NC, int CH>
+__device__ __forceinline__ void pg_dot(const PgBuf<CH> & b, const int8_t * sq, const float * sd, int off,
+                                       const PgArgs & a, int lane, int64_t row) {
+    float acc[1][NC];
 #pragma unroll
-    for (int p = 0; p < P; p++) {
-#pragma unroll
-        for (int c = 0; c < NC; c++) {
-            acc[p][c] = 0.0f;
-        }
+    for (int c = 0; c < NC; c++) {
+        acc[0][c] = 0.0f;
     }
 #pragma unroll
-    for (int u = 0; u < NQ_MAXK / 1024; u++) {
-        const int  o  = min(1024 * u + lane * 16, K - 16);
-        const bool ok = 1024 * u + lane * 16 < K;
+    for (int u = 0; u < CH; u++) {
+        const int  o  = min(1024 * u + lane * 16, a.K - 16);
+        const bool ok = 1024 * u + lane * 16 < a.K;
+        const float dw = ok ? h2f(b.s[u]) : 0.0f;
 #pragma unroll
         for (int c = 0; c < NC; c++) {
-            const int4_t xq = *(const int4_t *) &s_q[c][o];
-            const float  dx = s_d[c][o >> 5];
-#pragma unroll
-            for (int p = 0; p < P; p++) {
-                const float dw = ok ? h2f(b.s[p][u]) : 0.0f;
-                acc[p][c] += (float) dot16(b.w[p][u], xq) * (dw * dx);
+            const int4_t xq = *(const int4_t *) &sq[c * 1024 * CH + o + off];
+            const float  dx = sd[c * 32 * CH + (o >> 5) + off];
+            acc[0][c] += (float) dot16(b.w[u], xq) * (dw * dx);
+        }
+        if constexpr (CH > 4) {
+            if (u % 4 == 3) {
+                __builtin_amdgcn_sched_barrier(0);  // bounds the LDS reads in flight (registers)
             }
         }
     }
-    store_rows<NC, P>(acc, lane, row0, N, y, ldy, res, ldr);
+    store_rows<NC, 1>(acc, lane, row, a.N, a.y, a.ldy, a.res, a.ldr);
 }
 
-template <int NC, int P>
-__global__ __launch_bounds__(64 * NQ_WAVES) void k_gemv_q8_0_nq(const uint8_t * __restrict__ W, int64_t N, int K,
-                                                                int64_t rs, const float * __restrict__ x, int64_t ldx,
-                                                                const float * __restrict__ nw, float eps,
-                                                                float * __restrict__ xn_out, float * y, int64_t ldy,
-                                                                const float * res, int64_t ldr, int nit) {
-    constexpr int J = NQ_MAXK / (256 * NQ_WAVES);  // float4 activation chunks per thread
-    __shared__ __attribute__((aligned(16))) int8_t s_q[NC][NQ_MAXK];
-    __shared__ float  s_d[NC][NQ_MAXK / 32];
-    __shared__ double s_ss[NC][NQ_WAVES];
+template <int NC, int CH, int PRO>
+__global__ __launch_bounds__(64 * PG_WAVES) void k_gemv_q8_0_pro(PgArgs a) {
+    constexpr int  MAXK = 1024 * CH;
+    constexpr int  J    = MAXK / (256 * PG_WAVES);  // float4 activation chunks per thread
+    constexpr bool DB   = CH <= 4;                  // double-buffered row loop
+    __shared__ __attribute__((aligned(16))) int8_t s_q[NC * MAXK];
+    __shared__ float  s_d[NC * MAXK / 32];
+    __shared__ double s_ss[NC][PG_WAVES];
     const int     lane = threadIdx.x & 63;
-    const int     wv   = threadIdx.x >> 6;
-    const int64_t gw   = (int64_t) blockIdx.x * NQ_WAVES + wv;
-    const int64_t TW   = (int64_t) gridDim.x * NQ_WAVES;
-    // 1. the activation rows and the norm weight: chunk j of thread t holds
-    // elements e = 4 t + 256 NQ_WAVES j .. e + 3 (a 32-block is 8 adjacent
-    // lanes).  Issued first: loads return in order, so the prologue waits
-    // for these and not for the weights behind them.
-    float4_t xv[J][NC], wn[J];
+    const int     wv   = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: row bases in SGPRs
+    const int64_t gw   = (int64_t) blockIdx.x * PG_WAVES + wv;
+    const int64_t TW   = (int64_t) gridDim.x * PG_WAVES;
+    const int     K    = a.K;
+    // 1. activations: chunk j of thread t holds elements e = 4 t + 4096 j ..
+    // e + 3 (a 32-block is 8 adjacent lanes); past K re-read the row's end
+    float4_t xv[J][NC], xw[J][PRO == PRO_NORM ? 1 : NC];
 #pragma unroll
     for (int j = 0; j < J; j++) {
-        const unsigned e = min(4u * threadIdx.x + 256u * NQ_WAVES * j, (unsigned) K - 4u);
+        const unsigned e = min(4u * threadIdx.x + 256u * PG_WAVES * j, (unsigned) K - 4u);
 #pragma unroll
         for (int c = 0; c < NC; c++) {
-            xv[j][c] = *(const float4_t *) (x + c * ldx + e);
-        }
-        wn[j] = *(const float4_t *) (nw + e);
-    }
-    // 2. the first two iterations' weight loads (unconditional: a row past
-    // N re-reads row N - 1 and is not stored)
-    NqBuf<P> ba, bb;
-    nq_load<P>(ba, W, N, K, rs, gw * P, lane);
-    nq_load<P>(bb, W, N, K, rs, (TW + gw) * P, lane);
-#pragma unroll
-    for (int j = 0; j < J; j++) {
-        if (4 * (int) threadIdx.x + 256 * NQ_WAVES * j >= K) {
-            xv[j][0] = float4_t{ 0.0f, 0.0f, 0.0f, 0.0f };
-#pragma unroll
-            for (int c = 1; c < NC; c++) {
-                xv[j][c] = xv[j][0];
+            xv[j][c] = *(const float4_t *) (a.x + c * a.ldx + e);
+            if constexpr (PRO == PRO_SWIGLU) {
+                xw[j][c] = *(const float4_t *) (a.u + c * a.ldu + e);
             }
         }
+        if constexpr (PRO == PRO_NORM) {
+            xw[j][0] = *(const float4_t *) (a.nw + e);
+        }
     }
-    // 3. sum of squares per row in double, then 4. normalise, times the norm
-    // weight, quantise per 32-block: the separate norm kernel's unfused f32
-    // arithmetic (the dot products keep the plain GEMV's FMAs)
+    // 2. the first weight rows, unconditionally (a row past N re-reads row
+    // N - 1 and is not stored); a long row's last chunks after the prologue,
+    // whose activation values would not fit in registers beside them
+    constexpr int      PRE = DB ? CH : 8;
+    PgBuf<CH>          ba;
+    PgBuf<DB ? CH : 1> bb;
+    pg_load<CH, 0, PRE>(ba, a, gw, lane);
+    if constexpr (DB) {
+        pg_load<CH>(bb, a, TW + gw, lane);
+    }
+    // 3. the activation values (separate kernels' unfused f32 arithmetic;
+    // the dot products keep the plain GEMV's FMAs), quantised into LDS
     {
 #pragma clang fp contract(off)
+        float sc[NC];
+        if constexpr (PRO == PRO_NORM) {
 #pragma unroll
-        for (int c = 0; c < NC; c++) {
-            double ss = 0.0;
+            for (int c = 0; c < NC; c++) {
+                double ss = 0.0;
 #pragma unroll
-            for (int j = 0; j < J; j++) {
+                for (int j = 0; j < J; j++) {
+                    if (4 * (int) threadIdx.x + 256 * PG_WAVES * j < K) {
 #pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    ss += (double) (xv[j][c][k] * xv[j][c][k]);
+                        for (int k = 0; k < 4; k++) {
+                            ss += (double) (xv[j][c][k] * xv[j][c][k]);
+                        }
+                    }
+                }
+                ss = wave_sum_d(ss);
+                if (lane == 0) {
+                    s_ss[c][wv] = ss;
                 }
             }
-            ss = wave_sum_d(ss);
-            if (lane == 0) {
-                s_ss[c][wv] = ss;
+            __syncthreads();
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                double tot = 0.0;
+#pragma unroll
+                for (int w = 0; w < PG_WAVES; w++) {
+                    tot += s_ss[c][w];
+                }
+                const float mean = (float) (tot / (double) K);
+                sc[c]            = 1.0f / sqrtf(mean + a.eps);
             }
         }
-        __syncthreads();
 #pragma unroll
         for (int c = 0; c < NC; c++) {
-            double tot = 0.0;
-#pragma unroll
-            for (int w = 0; w < NQ_WAVES; w++) {
-                tot += s_ss[c][w];
-            }
-            const float mean = (float) (tot / (double) K);
-            const float sc   = 1.0f / sqrtf(mean + eps);
 #pragma unroll
             for (int j = 0; j < J; j++) {
-                const int e = 4 * (int) threadIdx.x + 256 * NQ_WAVES * j;
+                const int e = 4 * (int) threadIdx.x + 256 * PG_WAVES * j;
                 float     o[4];
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
-                    const float t = xv[j][c][k] * sc;
-                    o[k]          = t * wn[j][k];
+                    if constexpr (PRO == PRO_NORM) {
+                        const float t = xv[j][c][k] * sc[c];
+                        o[k]          = t * xw[j][0][k];
+                    } else {
+                        const float g    = xv[j][c][k];
+                        const float silu = g / (1.0f + expf(-g));
+                        o[k]             = silu * xw[j][c][k];
+                    }
                 }
-                float a = fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3])));
-                a       = fmaxf(a, __shfl_xor(a, 1, WAVE));
-                a       = fmaxf(a, __shfl_xor(a, 2, WAVE));
-                a       = fmaxf(a, __shfl_xor(a, 4, WAVE));
-                const float dd = a / 127.0f;
+                float m = fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3])));
+                m       = fmaxf(m, __shfl_xor(m, 1, WAVE));
+                m       = fmaxf(m, __shfl_xor(m, 2, WAVE));
+                m       = fmaxf(m, __shfl_xor(m, 4, WAVE));
+                const float dd = m / 127.0f;
                 const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
                 if (e < K) {
                     char4 q;
-                    q.x                   = (signed char) roundf(o[0] * id);
-                    q.y                   = (signed char) roundf(o[1] * id);
-                    q.z                   = (signed char) roundf(o[2] * id);
-                    q.w                   = (signed char) roundf(o[3] * id);
-                    *(char4 *) &s_q[c][e] = q;
+                    q.x                          = (signed char) roundf(o[0] * id);
+                    q.y                          = (signed char) roundf(o[1] * id);
+                    q.z                          = (signed char) roundf(o[2] * id);
+                    q.w                          = (signed char) roundf(o[3] * id);
+                    *(char4 *) &s_q[c * MAXK + e] = q;
                     if ((lane & 7) == 0) {
-                        s_d[c][e / 32] = h2f(f2h(dd));
+                        s_d[c * (MAXK / 32) + e / 32] = h2f(f2h(dd));
                     }
-                    if (xn_out && blockIdx.x == 0) {
-                        *(float4_t *) (xn_out + (int64_t) c * K + e) = float4_t{ o[0], o[1], o[2], o[3] };
+                    if (a.xo && blockIdx.x == 0) {
+                        *(float4_t *) (a.xo + (int64_t) c * K + e) = float4_t{ o[0], o[1], o[2], o[3] };
                     }
                 }
             }
         }
     }
-    __syncthreads();
-    // 5. stream the rows: reduce one buffer while the other's loads fly.  The
-    // steady-state loop's loads are unconditional so that each reduction
-    // waits for its own buffer only.
-    int it = 0;
-    for (; it + 2 < nit; it += 2) {
-        nq_dot<NC, P>(ba, s_q, s_d, K, lane, (it * TW + gw) * P, N, y, ldy, res, ldr);
-        nq_load<P>(ba, W, N, K, rs, ((it + 2) * TW + gw) * P, lane);
-        nq_dot<NC, P>(bb, s_q, s_d, K, lane, ((it + 1) * TW + gw) * P, N, y, ldy, res, ldr);
-        nq_load<P>(bb, W, N, K, rs, ((it + 3) * TW + gw) * P, lane);
+    if constexpr (PRE < CH) {
+        pg_load<CH, PRE, CH>(ba, a, gw, lane);
     }
-    nq_dot<NC, P>(ba, s_q, s_d, K, lane, (it * TW + gw) * P, N, y, ldy, res, ldr);
-    if (it + 1 < nit) {
-        nq_dot<NC, P>(bb, s_q, s_d, K, lane, ((it + 1) * TW + gw) * P, N, y, ldy, res, ldr);
+    __syncthreads();
+    // 4. stream the rows
+    const int nit = a.nit;
+    if constexpr (DB) {
+        // reduce one buffer while the other's loads fly; the steady-state
+        // loads are unconditional so that each reduction waits for its own
+        int it = 0;
+        for (; it + 2 < nit; it += 2) {
+            pg_dot<NC, CH>(ba, s_q, s_d, 0, a, lane, it * TW + gw);
+            pg_load<CH>(ba, a, (it + 2) * TW + gw, lane);
+            pg_dot<NC, CH>(bb, s_q, s_d, 0, a, lane, (it + 1) * TW + gw);
+            pg_load<CH>(bb, a, (it + 3) * TW + gw, lane);
+        }
+        pg_dot<NC, CH>(ba, s_q, s_d, 0, a, lane, it * TW + gw);
+        if (it + 1 < nit) {
+            pg_dot<NC, CH>(bb, s_q, s_d, 0, a, lane, (it + 1) * TW + gw);
+        }
+    } else {
+        // one buffer (a long row fills the registers): load the next row
+        // after reducing the current one
+        for (int it = 0;;) {
+            int off = 0;
+            asm volatile("" : "+v"(off));  // the LDS rows are re-read per row
+            pg_dot<NC, CH>(ba, s_q, s_d, off, a, lane, it * TW + gw);
+            if (++it >= nit) {
+                break;
+            }
+            pg_load<CH>(ba, a, it * TW + gw, lane);
+        }
     }
 }
 
@@ -704,7 +756,7 @@ extern "C" int mmhip_mul_mat_q_add(int type, const void * W, int64_t N, int64_t 
 
 namespace mmhip {
 // compute units of the current device (the persistent grid's size)
-static int64_t nq_cus() {
+static int64_t pg_cus() {
     static int cached[64] = {};
     int        dev        = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
@@ -720,47 +772,40 @@ static int64_t nq_cus() {
     return cached[dev];
 }
 
-struct NqArgs {
-    const uint8_t * W;
-    int64_t         N;
-    int             K;
-    int64_t         rs;
-    const float *   x;
-    int64_t         ldx;
-    const float *   nw;
-    float           eps;
-    float *         xn;
-    float *         y;
-    int64_t         ldy;
-    const float *   res;
-    int64_t         ldr;
-};
-
-template <int NC, int P>
-static int launch_nq(const NqArgs & a, hipStream_t stream) {
+template <int NC, int CH, int PRO> static int launch_pro(PgArgs a, hipStream_t stream, const char * what) {
     // one resident workgroup per CU; the rows split evenly over the iterations
-    const int64_t per_wg = (int64_t) NQ_WAVES * P;
-    const int64_t need   = (a.N + per_wg - 1) / per_wg;  // workgroups for one iteration
-    const int64_t nit    = (need + nq_cus() - 1) / nq_cus();
-    const int64_t wgs    = (need + nit - 1) / nit;
+    const int64_t need = (a.N + PG_WAVES - 1) / PG_WAVES;  // workgroups for one iteration
+    const int64_t nit  = (need + pg_cus() - 1) / pg_cus();
+    const int64_t wgs  = (need + nit - 1) / nit;
     if (nit > 0x7fffffff) {
-        return set_error(MMHIP_ERR_UNSUPPORTED, "rms_norm_mul_mat: N=%lld too large", (long long) a.N);
+        return set_error(MMHIP_ERR_UNSUPPORTED, "%s: N=%lld too large", what, (long long) a.N);
     }
-    auto kern = k_gemv_q8_0_nq<NC, P>;
-    hipLaunchKernelGGL(kern, dim3((unsigned) wgs), dim3(64 * NQ_WAVES), 0, stream, a.W, a.N, a.K, a.rs, a.x, a.ldx,
-                       a.nw, a.eps, a.xn, a.y, a.ldy, a.res, a.ldr, (int) nit);
-    return check_launch("rms_norm_mul_mat");
+    a.nit     = (int) nit;
+    auto kern = k_gemv_q8_0_pro<NC, CH, PRO>;
+    hipLaunchKernelGGL(kern, dim3((unsigned) wgs), dim3(64 * PG_WAVES), 0, stream, a);
+    return check_launch(what);
 }
 
-template <int NC>
-static int dispatch_nq(const NqArgs & a, hipStream_t stream) {
-    return launch_nq<NC, 1>(a, stream);
+template <int PRO> static int dispatch_pro(const PgArgs & a, int64_t M, hipStream_t stream, const char * what) {
+    if (a.K <= 4096) {
+        return M == 1 ? launch_pro<1, 4, PRO>(a, stream, what) : launch_pro<2, 4, PRO>(a, stream, what);
+    }
+    if constexpr (PRO == PRO_SWIGLU) {
+        return M == 1 ? launch_pro<1, 12, PRO>(a, stream, what) : launch_pro<2, 12, PRO>(a, stream, what);
+    }
+    return set_error(MMHIP_ERR_UNSUPPORTED, "%s: K=%d", what, a.K);
+}
+
+// M <= 2 (two activation columns in registers); the norm over K <= 4096 (the
+// model widths), the SwiGLU over K <= 12288 (the FFN widths)
+static bool pro_supported(int pro, int type, int64_t N, int64_t K, int64_t M) {
+    return type == TYPE_Q8_0 && N > 0 && M >= 1 && M <= 2 && K >= 256 && K <= (pro == PRO_NORM ? 4096 : 12288) &&
+           K % 256 == 0;
 }
 }  // namespace mmhip
 
 extern "C" int mmhip_rms_norm_mul_mat_supported(int type, int64_t N, int64_t K, int64_t M) {
-    // M <= 2: the quantised rows stay in registers across the row loop
-    return type == TYPE_Q8_0 && N > 0 && M >= 1 && M <= 2 && K >= 256 && K <= NQ_MAXK && K % 256 == 0;
+    return pro_supported(PRO_NORM, type, N, K, M);
 }
 
 extern "C" int mmhip_rms_norm_mul_mat(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride,
@@ -768,7 +813,7 @@ extern "C" int mmhip_rms_norm_mul_mat(int type, const void * W, int64_t N, int64
                                       float * xn_out, const float * res, int64_t ldr, float * y, int64_t ldy,
                                       void * stream) {
     MMHIP_API_BEGIN();
-    if (!mmhip_rms_norm_mul_mat_supported(type, N, K, M)) {
+    if (!pro_supported(PRO_NORM, type, N, K, M)) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "rms_norm_mul_mat: type %d N=%lld K=%lld M=%lld", type, (long long) N,
                          (long long) K, (long long) M);
     }
@@ -777,7 +822,30 @@ extern "C" int mmhip_rms_norm_mul_mat(int type, const void * W, int64_t N, int64
         ((uintptr_t) x | (uintptr_t) norm_w | (uintptr_t) xn_out) % 16 != 0 || (ldx % 4) != 0) {
         return set_error(MMHIP_ERR_INVALID, "rms_norm_mul_mat: bad arguments / alignment");
     }
-    const NqArgs a{ (const uint8_t *) W, N, (int) K, w_row_stride, x, ldx, norm_w, eps, xn_out, y, ldy, res, ldr };
-    hipStream_t  st = (hipStream_t) stream;
-    return M == 1 ? dispatch_nq<1>(a, st) : dispatch_nq<2>(a, st);
+    const PgArgs a{ (const uint8_t *) W, N, (int) K, w_row_stride, x, ldx, nullptr, 0, norm_w, eps, xn_out, y, ldy,
+                    res, ldr, 1 };
+    return dispatch_pro<PRO_NORM>(a, M, (hipStream_t) stream, "rms_norm_mul_mat");
+}
+
+extern "C" int mmhip_swiglu_mul_mat_supported(int type, int64_t N, int64_t K, int64_t M) {
+    return pro_supported(PRO_SWIGLU, type, N, K, M);
+}
+
+extern "C" int mmhip_swiglu_mul_mat(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride,
+                                    const float * g, int64_t ldg, const float * u, int64_t ldu, int64_t M,
+                                    float * h_out, const float * res, int64_t ldr, float * y, int64_t ldy,
+                                    void * stream) {
+    MMHIP_API_BEGIN();
+    if (!pro_supported(PRO_SWIGLU, type, N, K, M)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "swiglu_mul_mat: type %d N=%lld K=%lld M=%lld", type, (long long) N,
+                         (long long) K, (long long) M);
+    }
+    if (!W || !g || !u || !y || ldg < K || ldu < K || ldy < N || (res && ldr < N) ||
+        !gemv_supported(type, N, K, w_row_stride, W) ||
+        ((uintptr_t) g | (uintptr_t) u | (uintptr_t) h_out) % 16 != 0 || (ldg % 4) != 0 || (ldu % 4) != 0) {
+        return set_error(MMHIP_ERR_INVALID, "swiglu_mul_mat: bad arguments / alignment");
+    }
+    const PgArgs a{ (const uint8_t *) W, N, (int) K, w_row_stride, g, ldg, u, ldu, nullptr, 0.0f, h_out, y, ldy,
+                    res, ldr, 1 };
+    return dispatch_pro<PRO_SWIGLU>(a, M, (hipStream_t) stream, "swiglu_mul_mat");
 }

@@ -368,3 +368,53 @@ def test_rms_norm_mul_mat_rejects_unsupported(mm):
     rc = L.mmhip_rms_norm_mul_mat(8, ptr(dummy), 4096, 4352, 4624, ptr(dummy), 4352, 2, ptr(dummy), 1e-6, None,
                                   None, 0, ptr(dummy), 4096, st())
     assert rc != 0
+
+
+@pytest.mark.parametrize("M,F,N,mode", [(2, 12288, 4096, "fused"), (1, 3072, 1000, "split"), (2, 2048, 9001, "swapped"),
+                                        (2, 12288, 5000, "fused"), (1, 256, 77, "fused")])
+def test_swiglu_mul_mat_equals_two_pass(mm, pkg, M, F, N, mode):
+    """GEMV with the SwiGLU + quantisation in its prologue is bit-identical to
+    swiglu_quant then mul_mat_q / mul_mat_q_add: fused gate|up rows (also
+    swapped) and split gate / up tensors; one and two row iterations of the
+    persistent grid for the long (K = 12288) rows."""
+    L = mm.load()
+    Wq = mm.QuantWeight.from_gguf(8, pkg.synth.gguf_blocks_np(8, N, F, 6), N, F)
+    rng = np.random.default_rng(27)
+    a = torch.from_numpy((rng.standard_normal((M, 2 * F)) * 2).astype(np.float32)).cuda()
+    r = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float32)).cuda()
+    swapped = 1 if mode == "swapped" else 0
+    if mode == "split":
+        g, u = a[:, :F].contiguous(), a[:, F:].contiguous()
+        b_view = ctypes.byref(mm.view_of(u))
+        a_view = ctypes.byref(mm.view_of(g))
+        gp, ldg, up, ldu = g, F, u, F
+    else:
+        a_view, b_view = ctypes.byref(mm.view_of(a)), None
+        first, second = a[:, :F], a[:, F:]
+        gp, up = (second, first) if swapped else (first, second)
+        ldg = ldu = 2 * F
+    assert L.mmhip_swiglu_mul_mat_supported(8, N, F, M) == 1
+    h = torch.empty((M, F), dtype=torch.float32, device="cuda")
+    xq = torch.zeros(L.mmhip_act_bytes(8, F, M), dtype=torch.uint8, device="cuda")
+    assert L.mmhip_swiglu_quant(a_view, b_view, swapped, ptr(h), 8, ptr(xq), st()) == 0
+    y1 = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    assert L.mmhip_mul_mat_q(8, ptr(Wq.data), N, F, Wq.row_bytes, ptr(xq), M, ptr(y1), N, st()) == 0
+    y2 = torch.full((M, N), float("nan"), device="cuda")
+    h2 = torch.full((M, F), float("nan"), device="cuda")
+    assert L.mmhip_swiglu_mul_mat(8, ptr(Wq.data), N, F, Wq.row_bytes, ptr(gp), ldg, ptr(up), ldu, M, ptr(h2), None, 0,
+                                  ptr(y2), N, st()) == 0
+    y3 = torch.empty_like(y1)
+    assert L.mmhip_swiglu_mul_mat(8, ptr(Wq.data), N, F, Wq.row_bytes, ptr(gp), ldg, ptr(up), ldu, M, None, ptr(r), N,
+                                  ptr(y3), N, st()) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(h2, h)
+    assert torch.equal(y2, y1)
+    assert torch.equal(y3, y1 + r)
+
+
+def test_swiglu_mul_mat_rejects_unsupported(mm):
+    L = mm.load()
+    assert L.mmhip_swiglu_mul_mat_supported(8, 4096, 12544, 2) == 0  # K > 12288
+    assert L.mmhip_swiglu_mul_mat_supported(8, 4096, 12288, 3) == 0  # M > 2
+    assert L.mmhip_swiglu_mul_mat_supported(14, 4096, 12288, 2) == 0  # Q6_K weights
+    assert L.mmhip_rms_norm_mul_mat_supported(8, 4096, 8192, 2) == 0  # the norm: K <= 4096
