@@ -195,6 +195,21 @@ int mmhip_head_rows(const mmhip_head_rows_args * args, void * stream);
 /* n (1..4) such chains with a common D in one launch (the Q, K and V chains
  * of one attention block). */
 int mmhip_head_rows_n(const mmhip_head_rows_args * args, int n, void * stream);
+/* Batched decode attention with the head chains of its block in the prologue
+ * (src/qwen3-lm.h:764-821: the QKV views' RMS_NORM + MUL q/k norm, NeoX
+ * ROPE, SET_ROWS of the new key / value rows into the f16 caches, then
+ * GGML_OP_FLASH_ATTN_EXT).  heads[0] is the query chain (ids NULL; q is a
+ * view of its dst, which is not written), heads[1] / heads[2] the key and
+ * value chains whose dst are the caches k / v view (same base and strides,
+ * same ids); all three as mmhip_head_rows_n would run them.  The new rows are
+ * written to the caches and used by the attention of this call; results equal
+ * mmhip_head_rows_n + mmhip_flash_attn_ext(_q) (xq NULL: no quantised
+ * output).  Decode shapes only: (Hq / Hkv) * nq + 2 <= 8, one cache set per
+ * batch: mmhip_flash_attn_ext_head_supported says whether q, k, v qualify. */
+int mmhip_flash_attn_ext_head_supported(const mmhip_view * q, const mmhip_view * k, const mmhip_view * v);
+int mmhip_flash_attn_ext_head(const mmhip_view * q, const mmhip_view * k, const mmhip_view * v,
+                              const mmhip_view * mask, float scale, float * out, void * ws, size_t ws_bytes, int type,
+                              void * xq, const mmhip_head_rows_args * heads, void * stream);
 /* GGML_OP_GLU SwiGLU (as mmhip_swiglu) with the result also quantised into
  * the activation layout of mmhip_mul_mat_q for weights of `type` (the down
  * projection, src/qwen3-enc.h:108-110).  dst may be NULL.  Rows contiguous,

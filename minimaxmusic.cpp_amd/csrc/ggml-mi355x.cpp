@@ -697,7 +697,8 @@ struct plan_step {
     int64_t              slot_in  = -1;  // byte offset of the slot read (MM)
     int                  vec_wtype = 0;  // weight type the slot is quantised for
     bool                 write_f32 = true;
-    mmhip_head_rows_args head[4]{};  // HEAD: the chains run by this step
+    mmhip_head_rows_args head[4]{};  // HEAD: the chains run by this step (FA_Q: the fused Q, K, V chains)
+    int                  head_end[4]{ -1, -1, -1, -1 };  // the chains' last nodes
     int                  n_head = 0;
 };
 
@@ -974,11 +975,63 @@ bool plan_head(struct ggml_cgraph * g, const graph_info & gi, int i, plan_step &
     }
     st.kind    = ST_HEAD;
     st.node    = end;
-    st.head[0] = a;
-    st.n_head  = 1;
+    st.head[0]     = a;
+    st.head_end[0] = end;
+    st.n_head      = 1;
     for (int x : chain) {
         absorbed[(size_t) x] = 1;
     }
+    return true;
+}
+
+// Does node e feed only node fa, through no-op views?
+bool feeds_only(struct ggml_cgraph * g, const graph_info & gi, int e, int fa, int depth = 0) {
+    if (depth > 8 || is_output(ggml_graph_node(g, e)) || gi.consumers[(size_t) e].empty()) {
+        return false;
+    }
+    for (int c : gi.consumers[(size_t) e]) {
+        if (c != fa && !(is_noop(ggml_graph_node(g, c)->op) && feeds_only(g, gi, c, fa, depth + 1))) {
+            return false;
+        }
+    }
+    return true;
+}
+
+// HEAD step h (three chains) + attention step a -> one FA_Q step f whose
+// attention runs the chains in its prologue (mmhip_flash_attn_ext_head)
+bool fa_head_fuse(struct ggml_cgraph * g, const graph_info & gi, const plan_step & h, const plan_step & a,
+                  plan_step & f) {
+    const int                  fi = a.node;
+    const struct ggml_tensor * n  = ggml_graph_node(g, fi);
+    if (n->op != GGML_OP_FLASH_ATTN_EXT || !(a.kind == ST_FA_Q || a.kind == ST_NODE) || !n->src[1] || !n->src[2]) {
+        return false;
+    }
+    int qc = -1, kc = -1, vc = -1;
+    for (int c = 0; c < 3; c++) {
+        if (!h.head[c].ids) {
+            qc = c;
+        } else if (h.head[c].dst == n->src[1]->data) {
+            kc = c;
+        } else if (h.head[c].dst == n->src[2]->data) {
+            vc = c;
+        }
+    }
+    if (qc < 0 || kc < 0 || vc < 0 || h.head_end[qc] < 0 || !feeds_only(g, gi, h.head_end[qc], fi)) {
+        return false;
+    }
+    const mmhip_view q = view_of(n->src[0]), k = view_of(n->src[1]), v = view_of(n->src[2]);
+    if (!mmhip_flash_attn_ext_head_supported(&q, &k, &v)) {
+        return false;
+    }
+    f = a;
+    if (f.kind == ST_NODE) {
+        f.kind     = ST_FA_Q;
+        f.slot_out = -1;
+    }
+    f.head[0]     = h.head[qc];
+    f.head[1]     = h.head[kc];
+    f.head[2]     = h.head[vc];
+    f.n_head      = 3;
     return true;
 }
 
@@ -1194,7 +1247,8 @@ graph_plan build_plan(struct ggml_cgraph * g) {
             merged[(size_t) last_head].head[0].D == st.head[0].D) {
             plan_step m = merged[(size_t) last_head];
             for (int k = 0; k < st.n_head; k++) {
-                m.head[m.n_head++] = st.head[k];
+                m.head_end[m.n_head] = st.head_end[k];
+                m.head[m.n_head++]   = st.head[k];
             }
             m.node = st.node;
             merged.erase(merged.begin() + last_head);
@@ -1210,6 +1264,31 @@ graph_plan build_plan(struct ggml_cgraph * g) {
         }
     }
     plan.steps.swap(merged);
+    // a HEAD step of Q, K and V chains followed (past views only) by the
+    // decode attention they feed: one launch, the chains in its prologue
+    if (getenv("GGML_MI355X_DISABLE_FA_HEAD") == nullptr && !no_fuse) {
+        std::vector<plan_step> fused;
+        fused.reserve(plan.steps.size());
+        for (size_t x = 0; x < plan.steps.size(); x++) {
+            const plan_step & st = plan.steps[x];
+            size_t            y  = x + 1;
+            while (y < plan.steps.size() && plan.steps[y].kind == ST_NODE &&
+                   is_noop(ggml_graph_node(g, plan.steps[y].node)->op)) {
+                y++;
+            }
+            plan_step f;
+            if (st.kind == ST_HEAD && st.n_head == 3 && y < plan.steps.size() && fa_head_fuse(g, gi, st, plan.steps[y], f)) {
+                for (size_t z = x + 1; z < y; z++) {
+                    fused.push_back(plan.steps[z]);
+                }
+                fused.push_back(f);
+                x = y;
+                continue;
+            }
+            fused.push_back(st);
+        }
+        plan.steps.swap(fused);
+    }
     return plan;
 }
 
@@ -1282,8 +1361,14 @@ int run_step(mi_backend * c, struct ggml_cgraph * g, const plan_step & st, char 
             if (ws && !wp) {
                 return -1;
             }
-            rc = mmhip_flash_attn_ext_q(&q, &k, &v, has_m ? &m : nullptr, scale, (float *) n->data, wp, ws,
-                                        st.vec_wtype, slot + st.slot_out, s);
+            if (st.n_head == 3) {
+                rc = mmhip_flash_attn_ext_head(&q, &k, &v, has_m ? &m : nullptr, scale, (float *) n->data, wp, ws,
+                                               st.slot_out >= 0 ? st.vec_wtype : 0,
+                                               st.slot_out >= 0 ? slot + st.slot_out : nullptr, st.head, s);
+            } else {
+                rc = mmhip_flash_attn_ext_q(&q, &k, &v, has_m ? &m : nullptr, scale, (float *) n->data, wp, ws,
+                                            st.vec_wtype, slot + st.slot_out, s);
+            }
             break;
         }
         case ST_MM: {

@@ -271,9 +271,50 @@ constexpr int dec_nw(int D) {
     return D >= 256 && DEC_NW > 8 ? 8 : DEC_NW;
 }
 
-template <int D, int NW, int TP>
-__global__ __launch_bounds__(64 * NW) void k_fa_dec_mfma(FaArgs a, int chunk, int nsplit, float * __restrict__ part_o,
-                                                         float * __restrict__ part_ml, float * __restrict__ out) {
+// One row of the fused head prologue (HD): the RMS norm, weight and NeoX
+// RoPE of k_head_rows' head_row, lane l holding elements EPL l .. (the rotate
+// pairs lanes l and l ^ 32).
+template <int D>
+__device__ __forceinline__ void fa_head_row(float (&v)[D / 64], const float (&w)[D / 64], bool norm, bool has_w,
+                                            float eps, bool rope, int32_t pos, float ts, int lane) {
+#pragma clang fp contract(off)
+    constexpr int EPL = D / 64;
+    if (norm) {
+        double ss = 0.0;
+#pragma unroll
+        for (int k = 0; k < EPL; k++) {
+            ss += (double) (v[k] * v[k]);
+        }
+        ss               = wave_sum_d(ss);
+        const float mean = (float) (ss / (double) D);
+        const float sc   = 1.0f / sqrtf(mean + eps);
+#pragma unroll
+        for (int k = 0; k < EPL; k++) {
+            const float y = v[k] * sc;
+            v[k]          = has_w ? y * w[k] : y;
+        }
+    }
+    if (rope) {
+        const int i0    = EPL * (lane & 31);
+        float     theta = (float) pos;
+        for (int k = 0; k < i0; k++) {
+            theta *= ts;
+        }
+        const bool upper = lane >= 32;
+#pragma unroll
+        for (int k = 0; k < EPL; k++) {
+            const float other = __shfl_xor(v[k], 32, WAVE);
+            const float c = cosf(theta), sn = sinf(theta);
+            v[k]  = upper ? other * sn + v[k] * c : v[k] * c - other * sn;
+            theta *= ts;
+        }
+    }
+}
+
+template <int D, int NW, int TP, bool HD>
+__global__ __launch_bounds__(64 * NW) void k_fa_dec_mfma(FaArgs a, FaHead h, int chunk, int nsplit,
+                                                         float * __restrict__ part_o, float * __restrict__ part_ml,
+                                                         float * __restrict__ out) {
     constexpr int NS  = D / 32;  // k-steps of Q.K (32 dims each)
     constexpr int NDB = D / 16;  // 16-dim blocks of O^T
     constexpr int VTS = 16 + 4;  // V^T row stride (halves): 16 keys + pad
@@ -282,6 +323,9 @@ __global__ __launch_bounds__(64 * NW) void k_fa_dec_mfma(FaArgs a, int chunk, in
     constexpr int SO  = NW * 16 * OS * 2;  // halves of the merge buffer (floats)
     __shared__ __attribute__((aligned(16))) _Float16 s_buf[SVT > SO ? SVT : SO];
     __shared__ float s_m[NW][16], s_l[NW][16];
+    // HD: the processed query rows (f32) and the new key / value rows (f16)
+    __shared__ __attribute__((aligned(16))) float    s_qrow[HD ? 16 : 1][HD ? D : 4];
+    __shared__ __attribute__((aligned(16))) _Float16 s_new[2][HD ? D : 8];
 
     const int split = blockIdx.x;
     const int g     = blockIdx.y;
@@ -331,13 +375,95 @@ __global__ __launch_bounds__(64 * NW) void k_fa_dec_mfma(FaArgs a, int chunk, in
             }
         }
     };
+    // HD: wave w < ncol processes query column w, wave ncol the new key row,
+    // wave ncol + 1 the new value row (further waves redo the value row and
+    // drop it).  Their loads go first, ahead of the tiles: loads return in
+    // order, so the prologue runs while the tiles are in flight.
+    constexpr int EPL  = D / 64;
+    const int     task = min(wave, ncol + 1);
+    float         tv[EPL], tw[EPL];
+    int32_t       tpos = 0;
+    int64_t       id   = -1;  // the new rows' cache row
+    if constexpr (HD) {
+        const char *    src;
+        const float *   wp;
+        const int32_t * pp;
+        if (task < ncol) {
+            const int     hq_t = g * G + task % G;
+            const int     iq_t = task / G;
+            const int64_t r    = h.qr0 + iq_t * h.qr1 + hq_t * h.qr2 + b * h.qr3;
+            src                = h.q_src + (r / h.q_H) * h.q_nbt + (r % h.q_H) * h.q_nbh;
+            wp                 = h.q_w ? h.q_w : (const float *) src;
+            pp                 = h.q_pos ? h.q_pos + r / h.q_H : (const int32_t *) src;
+        } else if (task == ncol) {
+            src = h.k_src + b * h.k_nbt + g * h.k_nbh;
+            wp  = h.k_w ? h.k_w : (const float *) src;
+            pp  = h.k_pos ? h.k_pos + b : (const int32_t *) src;
+        } else {
+            src = h.v_src + b * h.v_nbt + g * h.v_nbh;
+            wp  = (const float *) src;
+            pp  = (const int32_t *) src;
+        }
+#pragma unroll
+        for (int k = 0; k < EPL; k++) {
+            tv[k] = ((const float *) src)[EPL * lane + k];
+            tw[k] = wp[EPL * lane + k];
+        }
+        tpos             = *pp;
+        const char * ip  = h.ids + (g % h.ids_ne1) * h.ids_nb1 + (b % h.ids_ne2) * h.ids_nb2;
+        id               = h.ids_type == 27 ? *(const int64_t *) ip : (int64_t) *(const int32_t *) ip;
+    }
     // the first tiles, unconditionally (keys are clamped into the split):
-    // loads return in order, and a load under a condition makes the compiler
-    // wait for everything issued before it
+    // a load under a condition makes the compiler wait for everything
+    // issued before it
     int t0 = wave;
     load_tiles(t0);
     // Q^T B operand: column col, dims 32s + 8kq .. +7 (zero for unused
     // columns; an unused column reads column 0's row)
+    half8_t qb[NS];
+    // HD: the key tile / column holding the new row (tn = -1: not in this
+    // split); the writer is the split holding it (split 0 when none does)
+    int tn = -1, kc = 0;
+    if constexpr (HD) {
+        if (task <= ncol + 1) {
+            const bool is_q = task < ncol;
+            fa_head_row<D>(tv, tw, is_q ? h.q_norm != 0 : task == ncol && h.k_norm != 0,
+                           is_q ? h.q_w != nullptr : h.k_w != nullptr, is_q ? h.q_eps : h.k_eps,
+                           is_q ? h.q_pos != nullptr : task == ncol && h.k_pos != nullptr, tpos, is_q ? h.q_ts : h.k_ts,
+                           lane);
+            const bool writer = split == ((id >= 0 && id < a.nkv) ? (int) (id / chunk) : 0);
+            if (is_q) {
+#pragma unroll
+                for (int k = 0; k < EPL; k++) {
+                    s_qrow[task][EPL * lane + k] = tv[k];
+                }
+            } else if (wave == task) {
+                const int  nr = task - ncol;  // 0 key, 1 value
+                char *     dp = (char *) (nr == 0 ? a.k : a.v) + id * (nr == 0 ? a.knb1 : a.vnb1) +
+                            g * (nr == 0 ? a.knb2 : a.vnb2) + b * (nr == 0 ? a.knb3 : a.vnb3);
+#pragma unroll
+                for (int k = 0; k < EPL; k++) {
+                    const uint16_t hb = f2h(tv[k]);
+                    s_new[nr][EPL * lane + k] = __builtin_bit_cast(_Float16, hb);
+                    if (writer && id >= 0) {
+                        ((uint16_t *) dp)[EPL * lane + k] = hb;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                qb[s][i] = cvalid ? (_Float16) s_qrow[cc][32 * s + 8 * kq + i] : (_Float16) 0.0f;
+            }
+        }
+        if (id >= kbeg && id < kend) {
+            tn = (int) (id - kbeg) / 16;
+            kc = (int) (id - kbeg) % 16;
+        }
+    } else {
     float         qf[NS][8];
     const float * qp  = (const float *) (a.q + iq * a.qnb1 + hq * a.qnb2 + b * a.qnb3) + 8 * kq;
     const bool    q16 = (((uintptr_t) a.q | (uintptr_t) a.qnb1 | (uintptr_t) a.qnb2 | (uintptr_t) a.qnb3) & 15) == 0;
@@ -361,13 +487,13 @@ __global__ __launch_bounds__(64 * NW) void k_fa_dec_mfma(FaArgs a, int chunk, in
             }
         }
     }
-    half8_t qb[NS];
 #pragma unroll
     for (int s = 0; s < NS; s++) {
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             qb[s][i] = cvalid ? (_Float16) qf[s][i] : (_Float16) 0.0f;
         }
+    }
     }
 
     float4_t oacc[NDB];
@@ -386,6 +512,16 @@ __global__ __launch_bounds__(64 * NW) void k_fa_dec_mfma(FaArgs a, int chunk, in
             const int t = t0 + NW * p;
             if (t >= ntile) {
                 break;  // uniform over the wave
+            }
+            if constexpr (HD) {
+                // the new row replaces what the cache held at its position
+                if (t == tn && col == kc) {
+#pragma unroll
+                    for (int s = 0; s < NS; s++) {
+                        kf[p][s] = *(const half8_t *) &s_new[0][32 * s + 8 * kq];
+                        vf[p][s] = *(const half8_t *) &s_new[1][32 * s + 8 * kq];
+                    }
+                }
             }
             // S^T tile
             float4_t sacc = { 0.0f, 0.0f, 0.0f, 0.0f };
@@ -413,8 +549,7 @@ __global__ __launch_bounds__(64 * NW) void k_fa_dec_mfma(FaArgs a, int chunk, in
                 sc[i]           = ok ? sacc[i] * sl2 + mv * log2e : -INFINITY;
                 mx              = fmaxf(mx, sc[i]);
             }
-            mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
+            mx = max_xor32(max_xor16(mx));
             // no divergent control flow around the MFMAs: a column with
             // nothing visible yet keeps alpha = 1 and p = exp2(-inf) = 0
             const float mnew  = fmaxf(m, mx);
@@ -429,8 +564,7 @@ __global__ __launch_bounds__(64 * NW) void k_fa_dec_mfma(FaArgs a, int chunk, in
                 rs += pv;
                 pb[i] = (_Float16) pv;
             }
-            rs += __shfl_xor(rs, 16, WAVE);
-            rs += __shfl_xor(rs, 32, WAVE);
+            rs = sum_xor32(sum_xor16(rs));
             l = l * alpha + rs;
             m = mnew;
             // the transposed V tile written above by this wave's lanes
@@ -731,18 +865,19 @@ static void launch_decode(const FaArgs & a, int QR, dim3 grid, int chunk, int ns
     }
 }
 
-template <int D>
-static int launch_dec_mfma(dim3 g3, int tiles, const FaArgs & a, int chunk, int nsplit, float * po, float * pml,
-                           float * out, hipStream_t stream) {
+template <int D, bool HD>
+static int launch_dec_mfma(dim3 g3, int tiles, const FaArgs & a, const FaHead & h, int chunk, int nsplit, float * po,
+                           float * pml, float * out, hipStream_t stream) {
     // D = 256 holds twice the fragments per tile: one tile per load round
     constexpr int NW = dec_nw(D);
     if constexpr (D <= 128) {
         if (tiles >= 2) {
-            hipLaunchKernelGGL((k_fa_dec_mfma<D, NW, 2>), g3, dim3(64 * NW), 0, stream, a, chunk, nsplit, po, pml, out);
+            hipLaunchKernelGGL((k_fa_dec_mfma<D, NW, 2, HD>), g3, dim3(64 * NW), 0, stream, a, h, chunk, nsplit, po, pml,
+                               out);
             return check_launch("flash_attn decode");
         }
     }
-    hipLaunchKernelGGL((k_fa_dec_mfma<D, NW, 1>), g3, dim3(64 * NW), 0, stream, a, chunk, nsplit, po, pml, out);
+    hipLaunchKernelGGL((k_fa_dec_mfma<D, NW, 1, HD>), g3, dim3(64 * NW), 0, stream, a, h, chunk, nsplit, po, pml, out);
     return check_launch("flash_attn decode");
 }
 
@@ -751,10 +886,19 @@ static bool dec_mfma(const FaArgs & a) {
     return (a.Hq / a.Hkv) * a.nq <= 16;
 }
 
+bool fa_decode_head_supported(const FaArgs & a, int D) {
+    // the query columns and the two new rows one wave each; one cache set
+    // per attention batch
+    return dec_mfma(a) && (a.Hq / a.Hkv) * a.nq + 2 <= dec_nw(D) && a.Bk == a.B && (D == 64 || D == 128 || D == 256);
+}
+
 int fa_decode(const FaArgs & a, int D, float * out, void * ws, size_t ws_bytes, hipStream_t stream, int qtype,
-              void * xq, bool * quantised) {
+              void * xq, bool * quantised, const FaHead * hd) {
     if (quantised) {
         *quantised = false;
+    }
+    if (hd && !fa_decode_head_supported(a, D)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "flash_attn decode: fused head prologue does not fit these shapes");
     }
     int nsplit, chunk, rg;
     decode_plan(a, D, nsplit, chunk, rg);
@@ -776,13 +920,19 @@ int fa_decode(const FaArgs & a, int D, float * out, void * ws, size_t ws_bytes, 
         const dim3 g3(nsplit, a.Hkv, a.B);
         // tiles per wave: the split's tiles in one load round where that fits
         const int tiles = (chunk / 16 + dec_nw(D) - 1) / dec_nw(D);
-        int       rc    = MMHIP_OK;
+        int          rc    = MMHIP_OK;
+        const FaHead h0{};
+        const FaHead & h   = hd ? *hd : h0;
+#define MM_DEC(DD)                                                                                               \
+    rc = hd ? launch_dec_mfma<DD, true>(g3, tiles, a, h, chunk, nsplit, part_o, part_ml, out, stream)             \
+            : launch_dec_mfma<DD, false>(g3, tiles, a, h, chunk, nsplit, part_o, part_ml, out, stream)
         switch (D) {
-            case 64: rc = launch_dec_mfma<64>(g3, tiles, a, chunk, nsplit, part_o, part_ml, out, stream); break;
-            case 128: rc = launch_dec_mfma<128>(g3, tiles, a, chunk, nsplit, part_o, part_ml, out, stream); break;
-            case 256: rc = launch_dec_mfma<256>(g3, tiles, a, chunk, nsplit, part_o, part_ml, out, stream); break;
+            case 64: MM_DEC(64); break;
+            case 128: MM_DEC(128); break;
+            case 256: MM_DEC(256); break;
             default: return set_error(MMHIP_ERR_UNSUPPORTED, "flash_attn decode: head dim %d", D);
         }
+#undef MM_DEC
         if (rc != MMHIP_OK) {
             return rc;
         }

@@ -239,7 +239,7 @@ __global__ __launch_bounds__(NW * 64) void k_fa_mfma(FaArgs a, const int * __res
             }
         }
         }
-        mx               = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
+        mx               = max_xor32(mx);
         const float mnew = fmaxf(m, mx);
         // No divergent control flow from here on: the MFMAs below combine the
         // operands of all 64 lanes.  A query with nothing visible yet keeps
@@ -284,7 +284,7 @@ __global__ __launch_bounds__(NW * 64) void k_fa_mfma(FaArgs a, const int * __res
             }
         }
         __builtin_amdgcn_s_setprio(0);
-        l += rs + __shfl_xor(rs, 32, WAVE);
+        l += sum_xor32(rs);
     }
 
     if (q_ok) {

@@ -211,6 +211,104 @@ extern "C" int mmhip_flash_attn_ext(const mmhip_view * q, const mmhip_view * k, 
     return fa_decode(a, D, out, ws, ws_bytes, (hipStream_t) stream);
 }
 
+// The Q / K / V head chains (mmhip_head_rows_args) folded into the decode
+// attention: checks that they feed this attention exactly and builds FaHead.
+static int fa_head_args(const mmhip_view * q, const mmhip_view * k, const mmhip_view * v, const FaArgs & a, int D,
+                        const mmhip_head_rows_args * hr, FaHead & h) {
+    const mmhip_head_rows_args & hq = hr[0];
+    const mmhip_head_rows_args & hk = hr[1];
+    const mmhip_head_rows_args & hv = hr[2];
+    const int64_t                rb = (int64_t) D * 4;  // bytes of one processed query row
+    const int64_t                qoff = (const char *) q->data - (const char *) hq.dst;
+    const bool q_ok = hq.D == D && !hq.ids && hq.dst && hq.src && hq.H > 0 && hq.T > 0 && qoff >= 0 && qoff % rb == 0 &&
+                      q->nb[1] % rb == 0 && q->nb[2] % rb == 0 && q->nb[3] % rb == 0 &&
+                      qoff + (q->ne[1] - 1) * q->nb[1] + (q->ne[2] - 1) * q->nb[2] + (q->ne[3] - 1) * q->nb[3] + rb <=
+                          (int64_t) hq.H * hq.T * rb;
+    auto cache_ok = [&](const mmhip_head_rows_args & c, const mmhip_view * kv) {
+        return c.D == D && c.src && c.ids && c.dst == kv->data && c.dst_type == 1 && c.dst_nb1 == kv->nb[1] &&
+               c.dst_nb2 == kv->nb[2] && c.dst_nb3 == kv->nb[3] && c.H == a.Hkv && c.T == a.B &&
+               (c.ids_type == 26 || c.ids_type == 27) && c.ids_ne1 > 0 && c.ids_ne2 > 0;
+    };
+    const bool same_ids = hk.ids == hv.ids && hk.ids_type == hv.ids_type && hk.ids_nb1 == hv.ids_nb1 &&
+                          hk.ids_nb2 == hv.ids_nb2 && hk.ids_ne1 == hv.ids_ne1 && hk.ids_ne2 == hv.ids_ne2;
+    if (!q_ok || !cache_ok(hk, k) || !cache_ok(hv, v) || !same_ids || hv.norm || hv.pos) {
+        return set_error(MMHIP_ERR_INVALID, "flash_attn_head: the head chains do not feed this attention");
+    }
+    memset(&h, 0, sizeof(h));
+    h.q_src    = (const char *) hq.src;
+    h.q_nbh    = hq.src_nb_h;
+    h.q_nbt    = hq.src_nb_t;
+    h.q_H      = hq.H;
+    h.q_w      = hq.norm ? hq.norm_w : nullptr;
+    h.q_eps    = hq.eps;
+    h.q_norm   = hq.norm;
+    h.q_pos    = hq.pos;
+    h.q_ts     = hq.theta_scale;
+    h.qr0      = qoff / rb;
+    h.qr1      = q->nb[1] / rb;
+    h.qr2      = q->nb[2] / rb;
+    h.qr3      = q->nb[3] / rb;
+    h.k_src    = (const char *) hk.src;
+    h.k_nbh    = hk.src_nb_h;
+    h.k_nbt    = hk.src_nb_t;
+    h.k_w      = hk.norm ? hk.norm_w : nullptr;
+    h.k_eps    = hk.eps;
+    h.k_norm   = hk.norm;
+    h.k_pos    = hk.pos;
+    h.k_ts     = hk.theta_scale;
+    h.v_src    = (const char *) hv.src;
+    h.v_nbh    = hv.src_nb_h;
+    h.v_nbt    = hv.src_nb_t;
+    h.ids      = (const char *) hk.ids;
+    h.ids_type = hk.ids_type;
+    h.ids_nb1  = hk.ids_nb1;
+    h.ids_nb2  = hk.ids_nb2;
+    h.ids_ne1  = hk.ids_ne1;
+    h.ids_ne2  = hk.ids_ne2;
+    return MMHIP_OK;
+}
+
+extern "C" int mmhip_flash_attn_ext_head_supported(const mmhip_view * q, const mmhip_view * k, const mmhip_view * v) {
+    FaArgs a;
+    int    D;
+    if (fa_validate(q, k, v, nullptr, a, D) != MMHIP_OK) {
+        clear_error();
+        return 0;
+    }
+    return !fa_use_mfma(a, D) && fa_decode_head_supported(a, D);
+}
+
+extern "C" int mmhip_flash_attn_ext_head(const mmhip_view * q, const mmhip_view * k, const mmhip_view * v,
+                                         const mmhip_view * mask, float scale, float * out, void * ws, size_t ws_bytes,
+                                         int type, void * xq, const mmhip_head_rows_args * heads, void * stream) {
+    MMHIP_API_BEGIN();
+    FaArgs a;
+    int    D;
+    int    rc = fa_validate(q, k, v, mask, a, D);
+    if (rc != MMHIP_OK) {
+        return rc;
+    }
+    if (!out || !heads || fa_use_mfma(a, D) || !fa_decode_head_supported(a, D)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "flash_attn_head: not a decode shape the fused prologue takes");
+    }
+    const int64_t K = (int64_t) a.Hq * D, M = (int64_t) a.B * a.nq;
+    if (xq && act_layout(type, K, M).total == 0) {
+        return set_error(MMHIP_ERR_INVALID, "flash_attn_head: activation type %d for K=%lld", type, (long long) K);
+    }
+    FaHead h;
+    rc = fa_head_args(q, k, v, a, D, heads, h);
+    if (rc != MMHIP_OK) {
+        return rc;
+    }
+    a.scale        = scale;
+    bool quantised = false;
+    rc = fa_decode(a, D, out, ws, ws_bytes, (hipStream_t) stream, xq ? type : 0, xq, &quantised, &h);
+    if (rc != MMHIP_OK || !xq || quantised) {
+        return rc;
+    }
+    return quantize_act(type, out, K, K, M, xq, (hipStream_t) stream);
+}
+
 extern "C" int mmhip_flash_attn_ext_q(const mmhip_view * q, const mmhip_view * k, const mmhip_view * v,
                                       const mmhip_view * mask, float scale, float * out, void * ws, size_t ws_bytes,
                                       int type, void * xq, void * stream) {

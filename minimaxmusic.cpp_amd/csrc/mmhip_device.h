@@ -54,7 +54,43 @@ __device__ __forceinline__ int dot4(int a, int b, int c) {
     return __builtin_amdgcn_sdot4(a, b, c, false);
 }
 
-// Sum over all 64 lanes; every lane receives the total.
+// Reductions across the 16-lane rows of a wave with the gfx950 row swaps
+// (one VALU op instead of an LDS permute): v_permlane16_swap exchanges rows
+// 1 / 3 of its first operand with rows 0 / 2 of its second, v_permlane32_swap
+// rows 2-3 with rows 0-1; with the value in both operands each lane ends up
+// holding its own value and that of lane ^ 16 (^ 32), in some order, so a
+// symmetric op of the pair is the xor reduction (a + b == b + a in IEEE).
+__device__ __forceinline__ float2 lanes_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return float2{ __uint_as_float(r[0]), __uint_as_float(r[1]) };
+}
+
+__device__ __forceinline__ float2 lanes_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return float2{ __uint_as_float(r[0]), __uint_as_float(r[1]) };
+}
+
+__device__ __forceinline__ float max_xor16(float x) {
+    const float2 p = lanes_xor16(x);
+    return fmaxf(p.x, p.y);
+}
+
+__device__ __forceinline__ float max_xor32(float x) {
+    const float2 p = lanes_xor32(x);
+    return fmaxf(p.x, p.y);
+}
+
+__device__ __forceinline__ float sum_xor16(float x) {
+    const float2 p = lanes_xor16(x);
+    return p.x + p.y;
+}
+
+__device__ __forceinline__ float sum_xor32(float x) {
+    const float2 p = lanes_xor32(x);
+    return p.x + p.y;
+}
+
+// Sum over all 64 lanes; every lane receives the total.// Sum over all 64 lanes; every lane receives the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {

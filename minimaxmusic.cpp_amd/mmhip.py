@@ -64,6 +64,8 @@ SIGNATURES = {
     "mmhip_quantize_act": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _vp]),
     "mmhip_mul_mat_q": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp]),
     "mmhip_mul_mat_q_add": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp]),
+    "mmhip_flash_attn_ext_head_supported": (_i32, [_VP, _VP, _VP]),
+    "mmhip_flash_attn_ext_head": (_i32, [_VP, _VP, _VP, _VP, _f32, _vp, _vp, _sz, _i32, _vp, _vp, _vp]),
     "mmhip_rms_norm_mul_mat_supported": (_i32, [_i32, _i64, _i64, _i64]),
     "mmhip_rms_norm_mul_mat": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _f32, _vp, _vp, _i64, _vp,
                                       _i64, _vp]),

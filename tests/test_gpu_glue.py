@@ -324,6 +324,79 @@ def test_head_rows_three_chains_one_launch(mm, orc):
         assert torch.equal(x, y)
 
 
+@pytest.mark.parametrize("D,nkv,ids_", [(128, 512, (300, 45)), (128, 4096, (4095, 4095)), (64, 700, (699, 0)),
+                                        (128, 256, (900, 3))])
+@pytest.mark.parametrize("quant", [False, True])
+def test_flash_attn_head_equals_separate(mm, D, nkv, ids_, quant):
+    """Decode attention with the Q/K/V head chains in its prologue equals
+    mmhip_head_rows_n then the attention: the same caches (the new rows
+    written), the same output (and quantised output) bit for bit.  Cases: new
+    rows inside the window, at its last key, and past it (900 > nkv: written,
+    not attended)."""
+    L = mm.load()
+    rng = np.random.default_rng(31)
+    T, Hq, Hk, S = 2, 32, 8, 4608
+    C = (Hq + 2 * Hk) * D
+    qkv = torch.from_numpy((rng.standard_normal((T, C)) * 2).astype(np.float32)).cuda()
+    wq = torch.from_numpy((1 + 0.02 * rng.standard_normal(D)).astype(np.float32)).cuda()
+    wk = torch.from_numpy((1 + 0.02 * rng.standard_normal(D)).astype(np.float32)).cuda()
+    pos = torch.tensor(list(ids_), dtype=torch.int32, device="cuda")
+    ids = torch.tensor(list(ids_), dtype=torch.int64, device="cuda")
+    kc0 = torch.from_numpy(rng.standard_normal((T, Hk, S, D)).astype(np.float16)).cuda()
+    vc0 = torch.from_numpy(rng.standard_normal((T, Hk, S, D)).astype(np.float16)).cuda()
+    keys = np.arange(nkv)[None, :]
+    allow = keys <= np.minimum(np.array(ids_), nkv - 1)[:, None]
+    mask = torch.from_numpy(np.where(allow, 0, -np.inf).astype(np.float16).reshape(T, 1, 1, nkv)).cuda()
+    kvne, kvnb = [D, nkv, Hk, T], [2, 2 * D, 2 * D * S, 2 * D * S * Hk]
+    K = Hq * D
+    res = []
+    for fused in (False, True):
+        qout = torch.zeros((T, Hq, D), dtype=torch.float32, device="cuda")
+        kc, vc = kc0.clone(), vc0.clone()
+        a = (mm.HeadRowsArgs * 3)(
+            _head_args(mm, qkv, D, Hq, T, C * 4, norm_w=wq, pos=pos, dst=qout),
+            _head_args(mm, qkv[:, Hq * D:], D, Hk, T, C * 4, norm_w=wk, pos=pos, ids=ids, cache=kc),
+            _head_args(mm, qkv[:, (Hq + Hk) * D:], D, Hk, T, C * 4, ids=ids, cache=vc))
+        qv = mm.view_of(qout, [D, 1, Hq, T], [4, 4 * D * Hq, 4 * D, 4 * D * Hq])
+        kv, vv = mm.view_of(kc, kvne, kvnb), mm.view_of(vc, kvne, kvnb)
+        mv = mm.view_of(mask)
+        need = L.mmhip_flash_attn_workspace(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv))
+        ws = torch.empty(max(need, 256), dtype=torch.uint8, device="cuda")
+        out = torch.full((T, 1, Hq, D), float("nan"), device="cuda")
+        xq = torch.zeros(L.mmhip_act_bytes(8, K, T), dtype=torch.uint8, device="cuda") if quant else None
+        args = (ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), ctypes.byref(mv), float(1 / np.sqrt(D)),
+                ptr(out), ptr(ws), need)
+        if fused:
+            assert L.mmhip_flash_attn_ext_head_supported(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv)) == 1
+            assert L.mmhip_flash_attn_ext_head(*args, 8 if quant else 0, ptr(xq) if quant else None,
+                                               ctypes.byref(a), st()) == 0
+        else:
+            assert L.mmhip_head_rows_n(ctypes.byref(a), 3, st()) == 0
+            if quant:
+                assert L.mmhip_flash_attn_ext_q(*args, 8, ptr(xq), st()) == 0
+            else:
+                assert L.mmhip_flash_attn_ext(*args, st()) == 0
+        torch.cuda.synchronize()
+        res.append((out, kc, vc, xq))
+    (o1, k1, v1, x1), (o2, k2, v2, x2) = res
+    assert torch.equal(k1, k2) and torch.equal(v1, v2)
+    assert not torch.equal(k1, kc0)  # the new rows were written
+    assert torch.equal(o1, o2)
+    if quant:
+        assert torch.equal(x1, x2)
+
+
+def test_flash_attn_head_rejects_prefill_shapes(mm):
+    """Too many query columns per KV head for the prologue's waves (nq = 4
+    tokens x 4 heads): not taken, so the caller keeps the separate chains."""
+    L = mm.load()
+    D, nq, Hq, Hk, T, S = 128, 4, 32, 8, 2, 64
+    q = torch.zeros((T, Hq, nq, D), device="cuda")
+    kc = torch.zeros((T, Hk, S, D), dtype=torch.float16, device="cuda")
+    qv, kv = mm.view_of(q), mm.view_of(kc)
+    assert L.mmhip_flash_attn_ext_head_supported(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(kv)) == 0
+
+
 @pytest.mark.parametrize("M,K,N,ldx", [(2, 4096, 6144, 4096), (1, 1024, 300, 1088), (2, 2048, 9000, 2048),
                                        (2, 4096, 30000, 4096), (1, 256, 77, 320), (2, 1024, 70001, 1024)])
 def test_rms_norm_mul_mat_equals_two_pass(mm, pkg, M, K, N, ldx):
