@@ -8,10 +8,13 @@ random-init weights; all inputs resident in HBM before timing):
   lm_decode   (default) the full Qwen3-8B-shape batched CFG decode step on the
               ggml backend: 36 layers, hidden 4096, 32 q / 8 KV heads d128,
               FFN 12288, vocab 151936, Q8_0 weights (--wtype q6_k), f16 KV
-              cache at 4096 x 2 sets.  value = 2 tokens / wall-clock step time
-              (host input uploads + one HIP-graph replay); roofline = the
-              step's algorithmic bytes / its GPU time from HIP events on the
-              backend stream.
+              cache at 4096 x 2 sets.  value = 2 tokens / the GPU time of one
+              step's HIP-graph replay (HIP events on the backend stream; inputs
+              resident), wall_tok_s = the same with each step's host input
+              uploads and launch included; roofline = the
+              step's largest kernel (the MLP gate_up GEMV with its RMS-norm
+              prologue) alone; step_roofline = the step's algorithmic bytes /
+              its GPU time from HIP events on the backend stream.
   gemv_q8_0   Q8_0 decode GEMV: W 12288 x 4096 Q8_0, x [2 x 4096] f32 -> [2 x 12288]
               (one step = activation quantisation + GEMV).  8 weight copies
               (428 MB) rotate so the 256 MB Infinity Cache cannot hold them.
@@ -63,6 +66,50 @@ def time_launches(torch, fn, n, rotate):
     torch.cuda.synchronize()
     ts = [a.elapsed_time(b) for a, b in evs]
     return float(np.mean(ts)) * 1e-3, float(np.median(ts)) * 1e-3
+
+
+def graph_time(torch, fn, n, reps=10):
+    """Per-launch time of n launches of fn(i) captured into one HIP graph on a
+    side stream, replayed reps times between HIP events on that stream (the
+    launch gaps of a graph replay, as in the decode step)."""
+    hip = ctypes.CDLL("libamdhip64.so")
+    s = torch.cuda.Stream()
+    st = ctypes.c_void_p(s.cuda_stream)
+    with torch.cuda.stream(s):
+        fn(0, st)
+    torch.cuda.synchronize()
+    assert hip.hipStreamBeginCapture(st, 2) == 0
+    for i in range(n):
+        fn(i, st)
+    g = ctypes.c_void_p()
+    assert hip.hipStreamEndCapture(st, ctypes.byref(g)) == 0
+    ex = ctypes.c_void_p()
+    assert hip.hipGraphInstantiate(ctypes.byref(ex), g, None, None, ctypes.c_size_t(0)) == 0
+    assert hip.hipGraphLaunch(ex, st) == 0
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        assert hip.hipGraphLaunch(ex, st) == 0
+        e1.record(s)
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1) * 1e-3 / n)
+    hip.hipGraphExecDestroy(ex)
+    hip.hipGraphDestroy(g)
+    return float(np.mean(ts)), float(np.min(ts))
+
+
+def profile_traffic(name):
+    """HBM bytes per launch of a kernel, from the committed rocprofv3 PMC
+    summary profiles/<name>.md (its `traffic_bytes_per_launch:` line), or None."""
+    p = ROOT / "profiles" / (name + ".md")
+    if not p.exists():
+        return None
+    for line in p.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":")[1].strip())
+    return None
 
 
 def bench_gemv(args, torch, pkg):
@@ -126,7 +173,7 @@ def bench_gemv(args, torch, pkg):
         "roofline": {"bound": "hbm", "kernel": "k_gemv_q8_0<2,2>", "achieved": round(achieved, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "avg_launch_us": round(avg_s * 1e6, 3), "median_launch_us": round(med_s * 1e6, 3),
-                     "alg_bytes_per_launch": alg_bytes, "traffic": None},
+                     "alg_bytes_per_launch": alg_bytes, "traffic": profile_traffic("gemv_q8_0_12288x4096_m2")},
         "cpu_baseline": cpu,
     }
 
@@ -210,7 +257,7 @@ def bench_fa(args, torch, pkg):
         "roofline": {"bound": "hbm", "kernel": "k_fa_decode<128,8> + k_fa_combine", "achieved": round(achieved, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "avg_launch_us": round(avg_s * 1e6, 3), "median_launch_us": round(med_s * 1e6, 3),
-                     "alg_bytes_per_launch": alg_bytes, "traffic": None},
+                     "alg_bytes_per_launch": alg_bytes, "traffic": profile_traffic("fa_decode_gqa_b2_kv2048")},
         "cpu_baseline": cpu,
     }
 
@@ -304,7 +351,7 @@ def bench_fa_mfma(args, torch, pkg, causal):
         "roofline": {"bound": "mfma", "kernel": "k_fa_mfma<128>", "achieved": round(tf, 2),
                      "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
                      "avg_launch_us": round(avg_s * 1e6, 2), "median_launch_us": round(med_s * 1e6, 2),
-                     "alg_flops_per_launch": flops, "traffic": None},
+                     "alg_flops_per_launch": flops, "traffic": profile_traffic("fa_prefill_causal_b2_s1024_gqa" if causal else "fa_dit_b2_s4096_h16_d128")},
         "cpu_baseline": cpu,
     }
 
@@ -358,7 +405,7 @@ def bench_gemm(args, torch, pkg):
         "roofline": {"bound": "mfma", "kernel": "k_gemm_q<Q4_K>", "achieved": round(tf, 2),
                      "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
                      "avg_launch_us": round(avg_s * 1e6, 2), "median_launch_us": round(med_s * 1e6, 2),
-                     "alg_flops_per_launch": flops, "traffic": None},
+                     "alg_flops_per_launch": flops, "traffic": profile_traffic("gemm_q4_k_6144x2048_m8192")},
         "cpu_baseline": cpu,
     }
 
@@ -409,26 +456,68 @@ def bench_lm(args, torch, pkg):
     replays, eager = lm.graph_stats()
     nodes = lm.graph_nodes()
     lm.close()
+    dom = lm_dominant_kernel(torch, pkg, cfg)
     cpu = None
     if not args.no_cpu:
         cpu = cpu_lm(args, lm_mod, cfg)
     return {
         "metric": "LM decode tok/s (CFG B=2, %s, KV 4096)" % args.wtype.upper(),
-        "value": round(2.0 / dt, 2),
+        # inputs resident: the GPU time of the step's graph replay; the host
+        # input uploads of each step are in the wall-clock figures beside it
+        "value": round(2.0 / gpu_s, 2),
         "unit": "tok/s",
-        "ms_per_step": round(dt * 1e3, 4),
+        "ms_per_step": round(gpu_s * 1e3, 4),
+        "wall_tok_s": round(2.0 / dt, 2),
+        "wall_ms_per_step": round(dt * 1e3, 4),
         "dtype": args.wtype + " weights (int8-dot GEMV), f16 KV, f32 activations",
         "config": {"workload": "Qwen3-8B-shape batched CFG decode step: 36 layers, hidden 4096, 32q/8kv d128, "
                                "FFN 12288 SwiGLU, vocab 151936, KV 4096 x 2 sets",
                    "weights": args.wtype, "graph_nodes": nodes, "graph_replays": replays, "eager_runs": eager,
                    "tokens_per_step": 2},
-        "roofline": {"bound": "hbm", "kernel": "whole decode step (one HIP-graph replay of %d ggml nodes)" % nodes,
-                     "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "alg_bytes_per_step": step_bytes, "gpu_us_per_step": round(gpu_s * 1e6, 2),
-                     "wall_us_per_step": round(dt * 1e6, 2)},
+        "roofline": dom,
+        "step_roofline": {"bound": "hbm", "kernel": "whole decode step (one HIP-graph replay of %d ggml nodes)" % nodes,
+                          "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(achieved / HBM_PEAK_GBS, 4), "alg_bytes_per_step": step_bytes,
+                          "gpu_us_per_step": round(gpu_s * 1e6, 2), "wall_us_per_step": round(dt * 1e6, 2)},
         "cpu_baseline": cpu,
     }
+
+
+def lm_dominant_kernel(torch, pkg, cfg):
+    """The step's largest kernel alone: the MLP gate_up GEMV with the RMS norm
+    in its prologue (W [2 ffn x hidden] Q8_0, 2 columns), six weight copies
+    (642 MB) rotating past the 256 MB Infinity Cache, launches replayed as a
+    HIP graph like the step's."""
+    mm, synth = pkg.mmhip, pkg.synth
+    N, K, M = 2 * cfg["ffn"], cfg["hidden"], 2
+    wt = cfg["wtype"]
+    copies = 6
+    Ws = [mm.QuantWeight.from_gguf(wt, synth.gguf_blocks_torch(wt, N, K, 2001 + c), N, K) for c in range(copies)]
+    x = torch.from_numpy(synth.normal_np((M, K), 2011)).cuda()
+    nw = torch.ones(K, device="cuda")
+    y = torch.empty((M, N), device="cuda")
+    L = mm.load()
+    if not L.mmhip_rms_norm_mul_mat_supported(wt, N, K, M):
+        return None
+
+    def launch(i, st):
+        W = Ws[i % copies]
+        rc = L.mmhip_rms_norm_mul_mat(wt, ctypes.c_void_p(W.data.data_ptr()), N, K, W.row_bytes,
+                                      ctypes.c_void_p(x.data_ptr()), K, M, ctypes.c_void_p(nw.data_ptr()), 1e-6, None,
+                                      None, 0, ctypes.c_void_p(y.data_ptr()), N, st)
+        assert rc == 0, L.mmhip_last_error()
+
+    avg_s, min_s = graph_time(torch, launch, 36)
+    alg_bytes = Ws[0].data.numel() + M * K * 4 + K * 4 + M * N * 4  # weights + x + norm weight + y
+    achieved = alg_bytes / avg_s / 1e9
+    del Ws
+    torch.cuda.empty_cache()
+    return {"bound": "hbm", "kernel": "k_gemv_q8_0_pro<2,4,0>: RMS norm + gate_up GEMV %d x %d Q8_0, 2 columns "
+                                      "(the decode step's largest kernel)" % (N, K),
+            "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profile_traffic("gemv_norm_gate_up_24576x4096_m2"),
+            "avg_launch_us": round(avg_s * 1e6, 3), "min_launch_us": round(min_s * 1e6, 3),
+            "alg_bytes_per_launch": alg_bytes}
 
 
 def cpu_lm(args, lm_mod, cfg):
@@ -516,6 +605,9 @@ def main():
         "cpu_baseline": res["cpu_baseline"],
         "baseline_metric": METRIC,
     }
+    for k in ("step_roofline", "wall_tok_s", "wall_ms_per_step"):
+        if k in res:
+            line[k] = res[k]
     print(json.dumps(line), flush=True)
 
 
