@@ -36,10 +36,12 @@ __device__ __forceinline__ int vt_pos(int k) {
 }
 
 // Bank swizzle of V^T row r: the 8-key groups of the row are XOR-permuted by
-// (r / 8) % 8, so the staging writes of 16 lanes to rows 8 apart fall in
-// different banks; reads of 8 consecutive positions stay contiguous.
+// (r / 16) % 8.  Staging writes (4 bytes: 16 lanes on rows 8 apart x 4
+// lanes on adjacent key pairs) and A-operand reads (16 bytes: 16 lanes on
+// adjacent rows, one position) then both hit 64 distinct banks per pass;
+// reads of 8 consecutive positions stay contiguous.
 __device__ __forceinline__ int vt_swz(int r) {
-    return ((r >> 3) & 7) << 3;
+    return ((r >> 4) & 7) << 3;
 }
 
 // Work item of linear workgroup id `lin` out of `total`: workgroups are
@@ -144,7 +146,8 @@ __global__ __launch_bounds__(NW * 64) void k_fa_mfma(FaArgs a, const int * __res
         }
 #pragma unroll
         for (int i = 0; i < VCH; i++) {
-            const int c = tid + i * NT, kp = c / (D / 8), seg = c % (D / 8), kg = k0 + 2 * kp;
+            // the pair whose keys land at positions 2 kp, 2 kp + 1 of the V^T rows
+            const int c = tid + i * NT, kp = c / (D / 8), seg = c % (D / 8), kg = k0 + vt_pos(2 * kp);
             rv0[i] = kg < a.nkv ? *(const half8_t *) (vbase + (int64_t) kg * a.vnb1 + seg * 16) : half8_t{};
             rv1[i] = kg + 1 < a.nkv ? *(const half8_t *) (vbase + (int64_t) (kg + 1) * a.vnb1 + seg * 16)
                                     : half8_t{};
@@ -164,7 +167,7 @@ __global__ __launch_bounds__(NW * 64) void k_fa_mfma(FaArgs a, const int * __res
 #pragma unroll
         for (int i = 0; i < VCH; i++) {
             const int c = tid + i * NT, kp = c / (D / 8), seg = c % (D / 8);
-            const int pos = vt_pos(2 * kp);
+            const int pos = 2 * kp;
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 const int r = seg * 8 + j;
