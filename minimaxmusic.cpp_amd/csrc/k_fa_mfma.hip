@@ -57,7 +57,8 @@ __device__ __forceinline__ int xcd_remap(int lin, int total) {
 }
 
 template <int D, int NW>
-__global__ __launch_bounds__(NW * 64) void k_fa_mfma(FaArgs a, const int * __restrict__ row_end, int n_qtiles,
+__global__ __launch_bounds__(NW * 64) void k_fa_mfma(FaArgs a, const int * __restrict__ row_end,
+                                                     const int * __restrict__ zero_end, int n_qtiles,
                                                      float * __restrict__ out) {
     constexpr int NT  = NW * 64;
     constexpr int BQ  = NW * 32;
@@ -114,23 +115,29 @@ __global__ __launch_bounds__(NW * 64) void k_fa_mfma(FaArgs a, const int * __res
     const float log2e = 1.4426950408889634f;
     const float sl2   = a.scale * log2e;
 
-    // last visible key of the tile: max over its rows of the per-row ends
-    int kv_end = a.nkv;
+    // last visible key of the tile: max over its rows of the per-row ends;
+    // keys below every row's all-zero mask prefix take the unmasked path
+    int kv_end = a.nkv, zfast = a.nkv;
     if (row_end) {
-        __shared__ int s_end[NW];
+        __shared__ int s_end[NW], s_zero[NW];
         const int      plane = (b % a.mne3) * a.mne2 + (h % a.mne2);
         const int      e     = q_ok ? row_end[(int64_t) plane * a.nq + my_q] : 0;
+        const int      z     = q_ok ? zero_end[(int64_t) plane * a.nq + my_q] : a.nkv;
         const int      we    = (int) wave_max((float) e);
+        const int      wz    = -(int) wave_max((float) -z);
         if (lane == 0) {
-            s_end[wave] = we;
+            s_end[wave]  = we;
+            s_zero[wave] = wz;
         }
         __syncthreads();
-        int te = 0;
+        int te = 0, tz = a.nkv;
 #pragma unroll
         for (int w = 0; w < NW; w++) {
             te = max(te, s_end[w]);
+            tz = min(tz, s_zero[w]);
         }
         kv_end = min(kv_end, te);
+        zfast  = tz;
     }
 
     const char * kbase = a.k + hk * a.knb2 + bk * a.knb3;
@@ -200,7 +207,7 @@ __global__ __launch_bounds__(NW * 64) void k_fa_mfma(FaArgs a, const int * __res
         // scale, mask, out-of-range keys; tile max for this lane's query.
         // Without a mask on a full tile the raw scores are kept: their max
         // is scaled once, and the scale folds into the exp2 argument below.
-        const bool fast = !mrow && k0 + FA_BK <= a.nkv;
+        const bool fast = (!mrow || k0 + FA_BK <= zfast) && k0 + FA_BK <= a.nkv;
         float      mx   = -INFINITY;
         if (fast) {
 #pragma unroll
@@ -308,8 +315,9 @@ __global__ __launch_bounds__(NW * 64) void k_fa_mfma(FaArgs a, const int * __res
 
 // Mask prepass: for every mask plane (mask batch x mask head) and query row,
 // one past the last key whose mask value is not -inf (0 if the row is fully
-// masked).  One wave per row, 16-byte loads.
-__global__ __launch_bounds__(256) void k_fa_row_end(FaArgs a, int * __restrict__ row_end) {
+// masked), and the length of the row's leading run of exact zeros (+-0: no
+// bias, so those keys need no mask).  One wave per row, 16-byte loads.
+__global__ __launch_bounds__(256) void k_fa_row_end(FaArgs a, int * __restrict__ row_end, int * __restrict__ zero_end) {
     const int64_t row   = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);  // plane * nq + q
     const int     lane  = threadIdx.x & 63;
     const int64_t nrows = (int64_t) a.nq * a.mne2 * a.mne3;
@@ -320,7 +328,15 @@ __global__ __launch_bounds__(256) void k_fa_row_end(FaArgs a, int * __restrict__
     const int        plane = (int) (row / a.nq);
     const uint16_t * mr    = (const uint16_t *) (a.mask + (int64_t) q * a.mnb1 + (plane % a.mne2) * a.mnb2 +
                                                  (plane / a.mne2) * a.mnb3);
-    int best = -1;
+    int best = -1, first_nz = a.nkv;
+    auto see = [&](uint16_t hv, int k) {
+        if (hv != 0xfc00) {  // f16 -inf
+            best = max(best, k);
+        }
+        if ((hv & 0x7fff) != 0) {
+            first_nz = min(first_nz, k);
+        }
+    };
     if ((((uintptr_t) mr) & 15) == 0) {
         const int nvec = a.nkv / 8;
         for (int i = lane; i < nvec; i += 64) {
@@ -328,27 +344,22 @@ __global__ __launch_bounds__(256) void k_fa_row_end(FaArgs a, int * __restrict__
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 const uint32_t word = (uint32_t) w[j / 2];
-                const uint16_t hv   = (uint16_t) ((j & 1) ? (word >> 16) : (word & 0xffff));
-                if (hv != 0xfc00) {
-                    best = max(best, 8 * i + j);
-                }
+                see((uint16_t) ((j & 1) ? (word >> 16) : (word & 0xffff)), 8 * i + j);
             }
         }
         for (int k = nvec * 8 + lane; k < a.nkv; k += 64) {
-            if (mr[k] != 0xfc00) {
-                best = max(best, k);
-            }
+            see(mr[k], k);
         }
     } else {
         for (int k = lane; k < a.nkv; k += 64) {
-            if (mr[k] != 0xfc00) {  // f16 -inf
-                best = max(best, k);
-            }
+            see(mr[k], k);
         }
     }
-    best = (int) wave_max((float) best);
+    best     = (int) wave_max((float) best);
+    first_nz = -(int) wave_max((float) -first_nz);
     if (lane == 0) {
-        row_end[row] = best + 1;
+        row_end[row]  = best + 1;
+        zero_end[row] = first_nz;
     }
 }
 
@@ -360,8 +371,8 @@ static int fa_mfma_waves(const FaArgs & a, int D) {
 }
 
 size_t fa_mfma_workspace(const FaArgs & a) {
-    // per-row ends for up to Hq * B mask planes
-    return align_up((size_t) a.nq * a.Hq * a.B * sizeof(int), 256);
+    // per-row ends and zero-prefix lengths for up to Hq * B mask planes
+    return 2 * align_up((size_t) a.nq * a.Hq * a.B * sizeof(int), 256);
 }
 
 bool fa_mfma_supported(const FaArgs & a, int D) {
@@ -369,9 +380,11 @@ bool fa_mfma_supported(const FaArgs & a, int D) {
 }
 
 template <int D, int NW>
-static void launch_fa_mfma(const FaArgs & a, const int * row_end, int n_qtiles, float * out, hipStream_t stream) {
+static void launch_fa_mfma(const FaArgs & a, const int * row_end, const int * zero_end, int n_qtiles, float * out,
+                           hipStream_t stream) {
     const int64_t total = (int64_t) n_qtiles * a.Hq * a.B;
-    hipLaunchKernelGGL((k_fa_mfma<D, NW>), dim3((unsigned) total), dim3(NW * 64), 0, stream, a, row_end, n_qtiles, out);
+    hipLaunchKernelGGL((k_fa_mfma<D, NW>), dim3((unsigned) total), dim3(NW * 64), 0, stream, a, row_end, zero_end,
+                       n_qtiles, out);
 }
 
 int fa_mfma(const FaArgs & a, int D, float * out, void * ws, size_t ws_bytes, hipStream_t stream) {
@@ -381,25 +394,28 @@ int fa_mfma(const FaArgs & a, int D, float * out, void * ws, size_t ws_bytes, hi
     if ((int64_t) n_qtiles * a.Hq * a.B > 0x7fffffff) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "flash_attn mfma: grid too large");
     }
-    int * row_end = nullptr;
+    int * row_end  = nullptr;
+    int * zero_end = nullptr;
     if (a.mask) {
         const size_t need = fa_mfma_workspace(a);
         if (!ws || ws_bytes < need) {
             return set_error(MMHIP_ERR_WORKSPACE, "flash_attn mfma: workspace %zu < %zu", ws_bytes, need);
         }
         row_end             = (int *) ws;
+        zero_end            = (int *) ((char *) ws + need / 2);
         const int64_t nrows = (int64_t) a.nq * a.mne2 * a.mne3;
-        hipLaunchKernelGGL(k_fa_row_end, dim3((unsigned) ((nrows + 3) / 4)), dim3(256), 0, stream, a, row_end);
+        hipLaunchKernelGGL(k_fa_row_end, dim3((unsigned) ((nrows + 3) / 4)), dim3(256), 0, stream, a, row_end,
+                           zero_end);
         int rc = check_launch("flash_attn mask prepass");
         if (rc != MMHIP_OK) {
             return rc;
         }
     }
     if (D == 128) {
-        NW == 8 ? launch_fa_mfma<128, 8>(a, row_end, n_qtiles, out, stream)
-                : launch_fa_mfma<128, 4>(a, row_end, n_qtiles, out, stream);
+        NW == 8 ? launch_fa_mfma<128, 8>(a, row_end, zero_end, n_qtiles, out, stream)
+                : launch_fa_mfma<128, 4>(a, row_end, zero_end, n_qtiles, out, stream);
     } else if (D == 64) {
-        launch_fa_mfma<64, 4>(a, row_end, n_qtiles, out, stream);
+        launch_fa_mfma<64, 4>(a, row_end, zero_end, n_qtiles, out, stream);
     } else {
         return set_error(MMHIP_ERR_UNSUPPORTED, "flash_attn mfma: head dim %d", D);
     }
