@@ -412,18 +412,17 @@ __global__ __launch_bounds__(64 * NW) void k_fa_dec_mfma(FaArgs a, FaHead h, int
         tpos             = *pp;
         const char * ip  = h.ids + (g % h.ids_ne1) * h.ids_nb1 + (b % h.ids_ne2) * h.ids_nb2;
         id               = h.ids_type == 27 ? *(const int64_t *) ip : (int64_t) *(const int32_t *) ip;
+        // wait for them before the tile loads go out: issued together, these
+        // few small loads return behind the whole KV stream of the GPU
+#pragma unroll
+        for (int k = 0; k < EPL; k++) {
+            asm volatile("" ::"v"(tv[k]), "v"(tw[k]));
+        }
+        asm volatile("" ::"v"(tpos), "v"(id));
     }
-    // the first tiles, unconditionally (keys are clamped into the split):
-    // a load under a condition makes the compiler wait for everything
-    // issued before it
-    int t0 = wave;
-    load_tiles(t0);
-    // Q^T B operand: column col, dims 32s + 8kq .. +7 (zero for unused
-    // columns; an unused column reads column 0's row)
-    half8_t qb[NS];
-    // HD: the key tile / column holding the new row (tn = -1: not in this
-    // split); the writer is the split holding it (split 0 when none does)
-    int tn = -1, kc = 0;
+    // HD: the rows are processed before the tile loads go out as well: the
+    // sine / cosine argument reduction reads a constant table, and any load
+    // issued after the tiles returns behind them
     if constexpr (HD) {
         if (task <= ncol + 1) {
             const bool is_q = task < ncol;
@@ -451,6 +450,19 @@ __global__ __launch_bounds__(64 * NW) void k_fa_dec_mfma(FaArgs a, FaHead h, int
                 }
             }
         }
+    }
+    // the first tiles, unconditionally (keys are clamped into the split):
+    // a load under a condition makes the compiler wait for everything
+    // issued before it
+    int t0 = wave;
+    load_tiles(t0);
+    // Q^T B operand: column col, dims 32s + 8kq .. +7 (zero for unused
+    // columns; an unused column reads column 0's row)
+    half8_t qb[NS];
+    // HD: the key tile / column holding the new row (tn = -1: not in this
+    // split); the writer is the split holding it (split 0 when none does)
+    int tn = -1, kc = 0;
+    if constexpr (HD) {
         __syncthreads();
 #pragma unroll
         for (int s = 0; s < NS; s++) {
