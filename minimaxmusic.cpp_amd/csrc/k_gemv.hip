@@ -307,6 +307,16 @@ __global__ __launch_bounds__(64 * PG_WAVES) void k_gemv_q8_0_pro(PgArgs a) {
     PgBuf<DB ? CH : 1> bb;
     pg_load<CH, 0, PRE>(ba, a, gw, lane);
     if constexpr (DB) {
+        // the second row once the activations are in: a load returns behind
+        // every request the chip has queued before it, so the weights issued
+        // ahead of the activations delay them
+#pragma unroll
+        for (int j = 0; j < J; j++) {
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                asm volatile("" ::"v"(xv[j][c][0]), "v"(xw[j][PRO == PRO_NORM ? 0 : c][0]) : "memory");
+            }
+        }
         pg_load<CH>(bb, a, TW + gw, lane);
     }
     // 3. the activation values (separate kernels' unfused f32 arithmetic;
@@ -361,10 +371,7 @@ __global__ __launch_bounds__(64 * PG_WAVES) void k_gemv_q8_0_pro(PgArgs a) {
                         o[k]             = silu * xw[j][c][k];
                     }
                 }
-                float m = fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3])));
-                m       = fmaxf(m, __shfl_xor(m, 1, WAVE));
-                m       = fmaxf(m, __shfl_xor(m, 2, WAVE));
-                m       = fmaxf(m, __shfl_xor(m, 4, WAVE));
+                const float m = group8_max(fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3]))));
                 const float dd = m / 127.0f;
                 const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
                 if (e < K) {

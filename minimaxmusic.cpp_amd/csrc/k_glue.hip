@@ -98,10 +98,7 @@ __device__ __forceinline__ void quant_chunk256(const float (&v)[4], int lane, in
 #pragma clang fp contract(off)
     char4 q4;
     if (qtype == TYPE_Q8_0) {
-        float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-        a       = fmaxf(a, __shfl_xor(a, 1, WAVE));
-        a       = fmaxf(a, __shfl_xor(a, 2, WAVE));
-        a       = fmaxf(a, __shfl_xor(a, 4, WAVE));
+        const float a = group8_max(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
         const float dd = a / 127.0f;
         const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
         q4.x           = (signed char) roundf(v[0] * id);

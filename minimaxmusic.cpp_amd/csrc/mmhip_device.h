@@ -90,30 +90,74 @@ __device__ __forceinline__ float sum_xor32(float x) {
     return p.x + p.y;
 }
 
-// Sum over all 64 lanes; every lane receives the total.// Sum over all 64 lanes; every lane receives the total.
+// DPP row moves used below (all lanes of every row take part):
+// quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1] (lane ^ 2),
+// row_half_mirror (lane i of an 8-lane half <-> 7 - i: the other quad) and
+// row_mirror (lane i of a 16-lane row <-> 15 - i: the other half).  Once
+// every lane of a quad (half) holds the same value, the mirrors pair it
+// with the other quad (half), so a symmetric op reduces over 8 (16) lanes.
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
+
+template <int CTRL> __device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+template <int CTRL> __device__ __forceinline__ double dpp_d(double v) {
+    const int2 p = __builtin_bit_cast(int2, v);
+    return __builtin_bit_cast(double, int2{ __builtin_amdgcn_mov_dpp(p.x, CTRL, 0xF, 0xF, false),
+                                            __builtin_amdgcn_mov_dpp(p.y, CTRL, 0xF, 0xF, false) });
+}
+
+// both halves of a double through the row swaps: element k of the two
+// results comes from the same lane, so {lo[k], hi[k]} are that lane's double
+__device__ __forceinline__ double sum_xor16_d(double v) {
+    const int2 p  = __builtin_bit_cast(int2, v);
+    const auto lo = __builtin_amdgcn_permlane16_swap(p.x, p.x, false, false);
+    const auto hi = __builtin_amdgcn_permlane16_swap(p.y, p.y, false, false);
+    return __builtin_bit_cast(double, int2{ (int) lo[0], (int) hi[0] }) +
+           __builtin_bit_cast(double, int2{ (int) lo[1], (int) hi[1] });
+}
+
+__device__ __forceinline__ double sum_xor32_d(double v) {
+    const int2 p  = __builtin_bit_cast(int2, v);
+    const auto lo = __builtin_amdgcn_permlane32_swap(p.x, p.x, false, false);
+    const auto hi = __builtin_amdgcn_permlane32_swap(p.y, p.y, false, false);
+    return __builtin_bit_cast(double, int2{ (int) lo[0], (int) hi[0] }) +
+           __builtin_bit_cast(double, int2{ (int) lo[1], (int) hi[1] });
+}
+
+// Max over aligned groups of 8 lanes (a Q8_0 block of 4-value lanes);
+// every lane of the group receives it.
+__device__ __forceinline__ float group8_max(float v) {
+    v = fmaxf(v, dpp_f<DPP_XOR1>(v));
+    v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+    return fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
+}
+
+// Sum over all 64 lanes; every lane receives the total.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        v += __shfl_xor(v, o, WAVE);
-    }
-    return v;
+    v += dpp_f<DPP_XOR1>(v);
+    v += dpp_f<DPP_XOR2>(v);
+    v += dpp_f<DPP_HALF_MIRROR>(v);
+    v += dpp_f<DPP_MIRROR>(v);
+    return sum_xor32(sum_xor16(v));
 }
 
 // double-precision wave sum (ggml-CPU accumulates RMS_NORM's squares in double)
 __device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        v += __shfl_xor(v, o, WAVE);
-    }
-    return v;
+    v += dpp_d<DPP_XOR1>(v);
+    v += dpp_d<DPP_XOR2>(v);
+    v += dpp_d<DPP_HALF_MIRROR>(v);
+    v += dpp_d<DPP_MIRROR>(v);
+    return sum_xor32_d(sum_xor16_d(v));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        v = fmaxf(v, __shfl_xor(v, o, WAVE));
-    }
-    return v;
+    v = fmaxf(v, dpp_f<DPP_XOR1>(v));
+    v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+    v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_f<DPP_MIRROR>(v));
+    return max_xor32(max_xor16(v));
 }
 
 // Sum over aligned groups of G lanes (G a power of two <= 64), using
