@@ -3,7 +3,8 @@
 // (src/dit.h:221-222).
 //
 // Workgroup = NW waves = 32*NW query rows of one (head, batch); each wave owns
-// 32 query rows.  KV is walked in tiles of 64 keys staged in LDS (K as rows, V
+// 32 query rows (with 8 waves: two 128-row ranges from opposite ends of the
+// sequence, which evens out causal work).  KV is walked in tiles of 64 keys staged in LDS (K as rows, V
 // transposed).  Per tile a wave computes S^T = K Q^T (keys x queries) with
 // v_mfma_f32_32x32x16_f16, so each lane owns one query column: the online
 // softmax (max, sum, rescale) is lane-local apart from one exchange with the
@@ -85,7 +86,19 @@ __global__ __launch_bounds__(NW * 64) void k_fa_mfma(FaArgs a, const int * __res
     const int lane  = tid & 63;
     const int lq    = lane & 31;
     const int hh    = lane >> 5;
-    const int my_q  = qt * BQ + wave * 32 + lq;
+    // query rows: with 8 waves the workgroup pairs 128-row tile qt (waves 0-3)
+    // with tile n128 - 1 - qt (waves 4-7), so that under a causal mask every
+    // workgroup gets one short and one long row range (the middle tile of an
+    // odd count goes alone); otherwise 32 NW consecutive rows
+    int my_q;
+    if constexpr (NW == 8) {
+        const int n128 = (a.nq + 127) / 128;
+        const int half = wave >> 2;
+        const int t128 = half ? n128 - 1 - qt : qt;
+        my_q           = half && t128 <= qt ? a.nq : t128 * 128 + (wave & 3) * 32 + lq;
+    } else {
+        my_q = qt * BQ + wave * 32 + lq;
+    }
     const bool q_ok = my_q < a.nq;
 
     // Q^T operand: this lane's query, dims 16kk + 8hh + 0..7, rounded to f16
@@ -115,29 +128,28 @@ __global__ __launch_bounds__(NW * 64) void k_fa_mfma(FaArgs a, const int * __res
     const float log2e = 1.4426950408889634f;
     const float sl2   = a.scale * log2e;
 
-    // last visible key of the tile: max over its rows of the per-row ends;
-    // keys below every row's all-zero mask prefix take the unmasked path
-    int kv_end = a.nkv, zfast = a.nkv;
+    // last visible key of each wave's rows (max of the per-row ends) and of
+    // the workgroup's (max over waves: the K / V staging walks that far, a
+    // wave computes up to its own end); keys below every row's all-zero mask
+    // prefix take the unmasked path
+    int kv_end = a.nkv, w_end = __any(q_ok) ? a.nkv : 0, zfast = a.nkv;
     if (row_end) {
-        __shared__ int s_end[NW], s_zero[NW];
+        __shared__ int s_end[NW];
         const int      plane = (b % a.mne3) * a.mne2 + (h % a.mne2);
         const int      e     = q_ok ? row_end[(int64_t) plane * a.nq + my_q] : 0;
         const int      z     = q_ok ? zero_end[(int64_t) plane * a.nq + my_q] : a.nkv;
-        const int      we    = (int) wave_max((float) e);
-        const int      wz    = -(int) wave_max((float) -z);
+        w_end                = min(a.nkv, (int) wave_max((float) e));
+        zfast                = -(int) wave_max((float) -z);
         if (lane == 0) {
-            s_end[wave]  = we;
-            s_zero[wave] = wz;
+            s_end[wave] = w_end;
         }
         __syncthreads();
-        int te = 0, tz = a.nkv;
+        int te = 0;
 #pragma unroll
         for (int w = 0; w < NW; w++) {
             te = max(te, s_end[w]);
-            tz = min(tz, s_zero[w]);
         }
         kv_end = min(kv_end, te);
-        zfast  = tz;
     }
 
     const char * kbase = a.k + hk * a.knb2 + bk * a.knb3;
@@ -184,6 +196,9 @@ __global__ __launch_bounds__(NW * 64) void k_fa_mfma(FaArgs a, const int * __res
         __syncthreads();
         if (k0 + FA_BK < kv_end) {
             fetch(k0 + FA_BK);
+        }
+        if (k0 >= w_end) {
+            continue;  // past every key this wave's rows can see (it keeps staging)
         }
 
         // S^T (64 keys x 32 queries) = K Q^T.  Raised wave priority while
