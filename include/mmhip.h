@@ -119,6 +119,21 @@ int mmhip_swiglu_mul_mat_supported(int type, int64_t N, int64_t K, int64_t M);
 int mmhip_swiglu_mul_mat(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const float * g,
                          int64_t ldg, const float * u, int64_t ldu, int64_t M, float * h_out, const float * r,
                          int64_t ldr, float * y, int64_t ldy, void * stream);
+/* The MLP's gate_up GEMV with the RMS norm in its prologue and the SwiGLU
+ * that follows it in its epilogue: GGML_OP_RMS_NORM + GGML_OP_MUL
+ * (src/qwen3-lm.h:834) -> gate_up GGML_OP_MUL_MAT over the fused [gate | up]
+ * rows (src/qwen3-enc.h:106-108, src/gguf-weights.h:289-362) -> GGML_OP_GLU
+ * swiglu (src/qwen3-enc.h:108), whose output feeds the down projection
+ * (src/qwen3-enc.h:114).  W holds N = 2F rows (gate rows first, or up rows
+ * first when swapped); the result is the down GEMV's Q8_0 activation buffer
+ * xq (mmhip_act_bytes(8, F, M) bytes, as mmhip_swiglu_quant writes it) and,
+ * if h_out is given, the f32 SwiGLU rows [M, F].  Identical arithmetic:
+ * xq and h_out equal rms_norm_mul_mat followed by swiglu_quant bit for bit.
+ * Q8_0 weights, M <= 2, K a multiple of 256 up to 4096, N a multiple of 512. */
+int mmhip_rms_norm_mul_mat_glu_supported(int type, int64_t N, int64_t K, int64_t M);
+int mmhip_rms_norm_mul_mat_glu(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const float * x,
+                               int64_t ldx, int64_t M, const float * norm_w, float eps, int swapped, void * xq,
+                               float * h_out, void * stream);
 
 /* ---------------------------------------------------------------------
  * GGML_OP_FLASH_ATTN_EXT, replacing the ggml backend kernel behind

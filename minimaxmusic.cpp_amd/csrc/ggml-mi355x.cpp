@@ -678,6 +678,9 @@ int run_node(mi_backend * c, const struct ggml_tensor * n) {
 //   HEAD      CONT(view) -> RESHAPE -> [RMS_NORM -> MUL] -> [ROPE] -> [CONT]
 //             -> [RESHAPE -> SET_ROWS]: the per-head Q / K / V rows of the
 //             attention block in one launch.
+//   MM_GLU    a norm-fused gate_up GEMV MUL_MAT whose only consumer is a
+//             SwiGLU feeding Q8_0 GEMVs: the SwiGLU and its quantisation into
+//             those GEMVs' slot run in the gate_up GEMV's epilogue.
 //   MM_ADD    a GEMV MUL_MAT whose only consumer is an ADD with a same-shape
 //             residual: the ADD is done in the GEMV's store.
 // MUL_MATs reading a slot skip their activation quantisation.
@@ -693,6 +696,7 @@ struct plan_step {
     int                  norm    = -1;   // MM: the RMS_NORM node whose norm runs in the GEMV's prologue
     int                  norm_mul = -1;  // MM: the MUL by the norm weight (the GEMV's src1)
     int                  glu      = -1;  // MM: the SWIGLU node whose SwiGLU runs in the GEMV's prologue
+    int                  glu_epi  = -1;  // MM: the SWIGLU node computed in the (gate_up) GEMV's epilogue
     int64_t              slot_out = -1;  // byte offset of the quantised slot written (NORM / SWIGLU_Q)
     int64_t              slot_in  = -1;  // byte offset of the slot read (MM)
     int                  vec_wtype = 0;  // weight type the slot is quantised for
@@ -1072,7 +1076,8 @@ graph_plan build_plan(struct ggml_cgraph * g) {
     std::vector<int>         norm_of((size_t) gi.nn, -1);  // MUL node -> its RMS_NORM, norm done by the GEMVs
     const bool               no_norm_mm = getenv("GGML_MI355X_DISABLE_NORM_GEMV") != nullptr;
     std::vector<char>        glu_mm((size_t) gi.nn, 0);  // SWIGLU node done by its GEMVs
-    const bool               no_glu_mm = getenv("GGML_MI355X_DISABLE_SWIGLU_GEMV") != nullptr;
+    const bool               no_glu_mm  = getenv("GGML_MI355X_DISABLE_SWIGLU_GEMV") != nullptr;
+    const bool               no_glu_epi = getenv("GGML_MI355X_DISABLE_SWIGLU_EPILOGUE") != nullptr;
     auto add_pending = [&](const plan_step & st) {
         step_at[(size_t) st.node] = (int) pending.size();
         pending.push_back(st);
@@ -1120,6 +1125,32 @@ graph_plan build_plan(struct ggml_cgraph * g) {
                 absorbed[(size_t) j] = 1;
                 add_pending(st);
                 continue;
+            }
+        }
+        if (n->op == GGML_OP_GLU && n->op_params[0] == GGML_GLU_OP_SWIGLU && rows_contiguous_f32(n) && !no_glu_epi) {
+            // the SwiGLU (and the down GEMVs' activation quantisation) in the
+            // epilogue of the norm-fused gate_up GEMV that produces its input
+            const struct ggml_tensor * a = n->src[0];
+            const int                  p = node_index(gi, a);
+            const int64_t              F = n->ne[0], M = ggml_nrows(n);
+            bool only_views = p >= 0 && p < i;  // the fused step runs at p and writes the SwiGLU's outputs then
+            for (int t = p + 1; only_views && t < i; t++) {
+                only_views = is_noop(ggml_graph_node(g, t)->op);
+            }
+            if (!n->src[1] && only_views && step_at[(size_t) p] >= 0 && gi.uses[(size_t) p] == 1 &&
+                !is_output(a) && a->op == GGML_OP_MUL_MAT && a->ne[0] == 2 * F && ggml_nrows(a) == M &&
+                gemv_consumer_type(g, gi, i) == GGML_TYPE_Q8_0) {
+                plan_step & ms = pending[(size_t) step_at[(size_t) p]];
+                if (ms.kind == ST_MM && ms.node == p && ms.norm >= 0 && ms.add < 0 && ms.glu < 0 &&
+                    mmhip_rms_norm_mul_mat_glu_supported(a->src[0]->type, a->ne[0], a->src[0]->ne[0], M)) {
+                    ms.glu_epi             = i;
+                    ms.slot_out            = new_slot(GGML_TYPE_Q8_0, F, M);
+                    ms.write_f32           = is_output(n);
+                    slot_of[(size_t) i]    = ms.slot_out;
+                    slot_wtype[(size_t) i] = GGML_TYPE_Q8_0;
+                    absorbed[(size_t) i]   = 1;
+                    continue;
+                }
             }
         }
         if (n->op == GGML_OP_GLU && n->op_params[0] == GGML_GLU_OP_SWIGLU && rows_contiguous_f32(n) && !no_glu_mm &&
@@ -1383,6 +1414,14 @@ int run_step(mi_backend * c, struct ggml_cgraph * g, const plan_step & st, char 
                 const struct ggml_tensor * r   = st.add >= 0 ? ggml_graph_node(g, st.add)->src[st.add_res] : nullptr;
                 float                      eps;
                 memcpy(&eps, &rn->op_params[0], sizeof(float));
+                if (st.glu_epi >= 0) {
+                    const struct ggml_tensor * gn = ggml_graph_node(g, st.glu_epi);
+                    rc = mmhip_rms_norm_mul_mat_glu(w->type, w->data, N, K, (int64_t) w->nb[1], (const float *) xr->data,
+                                                    (int64_t) (xr->nb[1] / 4), M, (const float *) nwt->data, eps,
+                                                    gn->op_params[1] != 0, slot + st.slot_out,
+                                                    st.write_f32 ? (float *) gn->data : nullptr, s);
+                    break;
+                }
                 rc = mmhip_rms_norm_mul_mat(w->type, w->data, N, K, (int64_t) w->nb[1], (const float *) xr->data,
                                             (int64_t) (xr->nb[1] / 4), M, (const float *) nwt->data, eps, nullptr,
                                             r ? (const float *) r->data : nullptr, r ? (int64_t) (r->nb[1] / 4) : 0,

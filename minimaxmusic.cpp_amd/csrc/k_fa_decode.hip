@@ -421,8 +421,9 @@ __global__ __launch_bounds__(64 * NW) void k_fa_dec_mfma(FaArgs a, FaHead h, int
         asm volatile("" ::"v"(tpos), "v"(id));
     }
     // HD: the rows are processed before the tile loads go out as well: the
-    // sine / cosine argument reduction reads a constant table, and any load
-    // issued after the tiles returns behind them
+    // tile loads fill the memory request queues, so a wave issuing them
+    // stalls until earlier requests drain, and the rows are on the critical
+    // path (every wave needs the query rows before its first tile)
     if constexpr (HD) {
         if (task <= ncol + 1) {
             const bool is_q = task < ncol;

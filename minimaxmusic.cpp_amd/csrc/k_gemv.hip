@@ -242,9 +242,8 @@ __device__ __forceinline__ void pg_load(PgBuf<CH> & b, const PgArgs & a, int64_t
 // [NC][32 CH]); off is added to the LDS indices (an opaque zero keeps the
 // reads inside a loop where the rows do not fit in registers)
 template <int NC, int CH>
-__device__ __forceinline__ void pg_dot(const PgBuf<CH> & b, const int8_t * sq, const float * sd, int off,
-                                       const PgArgs & a, int lane, int64_t row) {
-    float acc[1][NC];
+__device__ __forceinline__ void pg_acc(const PgBuf<CH> & b, const int8_t * sq, const float * sd, int off,
+                                       const PgArgs & a, int lane, float (&acc)[1][NC]) {
 #pragma unroll
     for (int c = 0; c < NC; c++) {
         acc[0][c] = 0.0f;
@@ -266,7 +265,92 @@ __device__ __forceinline__ void pg_dot(const PgBuf<CH> & b, const int8_t * sq, c
             }
         }
     }
+}
+
+template <int NC, int CH>
+__device__ __forceinline__ void pg_dot(const PgBuf<CH> & b, const int8_t * sq, const float * sd, int off,
+                                       const PgArgs & a, int lane, int64_t row) {
+    float acc[1][NC];
+    pg_acc<NC, CH>(b, sq, sd, off, a, lane, acc);
     store_rows<NC, 1>(acc, lane, row, a.N, a.y, a.ldy, a.res, a.ldr);
+}
+
+// The activation values of the persistent GEMVs' prologue (the separate
+// kernels' unfused f32 arithmetic; the dot products keep the plain GEMV's
+// FMAs), quantised into LDS (s_q: [NC][MAXK] int8, s_d: [NC][MAXK / 32]).
+// xv / xw hold chunk j of thread t: elements 4 t + 4096 j .. + 3.
+template <int NC, int J, int MAXK, int PRO>
+__device__ __forceinline__ void pg_prologue(const float4_t (&xv)[J][NC], const float4_t (&xw)[J][PRO == PRO_NORM ? 1 : NC],
+                                            int8_t * s_q, float * s_d, double (*s_ss)[PG_WAVES], const PgArgs & a,
+                                            int lane, int wv, int K) {
+#pragma clang fp contract(off)
+    float sc[NC];
+    if constexpr (PRO == PRO_NORM) {
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            double ss = 0.0;
+#pragma unroll
+            for (int j = 0; j < J; j++) {
+                if (4 * (int) threadIdx.x + 256 * PG_WAVES * j < K) {
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        ss += (double) (xv[j][c][k] * xv[j][c][k]);
+                    }
+                }
+            }
+            ss = wave_sum_d(ss);
+            if (lane == 0) {
+                s_ss[c][wv] = ss;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            double tot = 0.0;
+#pragma unroll
+            for (int w = 0; w < PG_WAVES; w++) {
+                tot += s_ss[c][w];
+            }
+            const float mean = (float) (tot / (double) K);
+            sc[c]            = 1.0f / sqrtf(mean + a.eps);
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+#pragma unroll
+        for (int j = 0; j < J; j++) {
+            const int e = 4 * (int) threadIdx.x + 256 * PG_WAVES * j;
+            float     o[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                if constexpr (PRO == PRO_NORM) {
+                    const float t = xv[j][c][k] * sc[c];
+                    o[k]          = t * xw[j][0][k];
+                } else {
+                    const float g    = xv[j][c][k];
+                    const float silu = g / (1.0f + expf(-g));
+                    o[k]             = silu * xw[j][c][k];
+                }
+            }
+            const float m = group8_max(fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3]))));
+            const float dd = m / 127.0f;
+            const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+            if (e < K) {
+                char4 q;
+                q.x                          = (signed char) roundf(o[0] * id);
+                q.y                          = (signed char) roundf(o[1] * id);
+                q.z                          = (signed char) roundf(o[2] * id);
+                q.w                          = (signed char) roundf(o[3] * id);
+                *(char4 *) &s_q[c * MAXK + e] = q;
+                if ((lane & 7) == 0) {
+                    s_d[c * (MAXK / 32) + e / 32] = h2f(f2h(dd));
+                }
+                if (a.xo && blockIdx.x == 0) {
+                    *(float4_t *) (a.xo + (int64_t) c * K + e) = float4_t{ o[0], o[1], o[2], o[3] };
+                }
+            }
+        }
+    }
 }
 
 template <int NC, int CH, int PRO>
@@ -319,78 +403,8 @@ __global__ __launch_bounds__(64 * PG_WAVES) void k_gemv_q8_0_pro(PgArgs a) {
         }
         pg_load<CH>(bb, a, TW + gw, lane);
     }
-    // 3. the activation values (separate kernels' unfused f32 arithmetic;
-    // the dot products keep the plain GEMV's FMAs), quantised into LDS
-    {
-#pragma clang fp contract(off)
-        float sc[NC];
-        if constexpr (PRO == PRO_NORM) {
-#pragma unroll
-            for (int c = 0; c < NC; c++) {
-                double ss = 0.0;
-#pragma unroll
-                for (int j = 0; j < J; j++) {
-                    if (4 * (int) threadIdx.x + 256 * PG_WAVES * j < K) {
-#pragma unroll
-                        for (int k = 0; k < 4; k++) {
-                            ss += (double) (xv[j][c][k] * xv[j][c][k]);
-                        }
-                    }
-                }
-                ss = wave_sum_d(ss);
-                if (lane == 0) {
-                    s_ss[c][wv] = ss;
-                }
-            }
-            __syncthreads();
-#pragma unroll
-            for (int c = 0; c < NC; c++) {
-                double tot = 0.0;
-#pragma unroll
-                for (int w = 0; w < PG_WAVES; w++) {
-                    tot += s_ss[c][w];
-                }
-                const float mean = (float) (tot / (double) K);
-                sc[c]            = 1.0f / sqrtf(mean + a.eps);
-            }
-        }
-#pragma unroll
-        for (int c = 0; c < NC; c++) {
-#pragma unroll
-            for (int j = 0; j < J; j++) {
-                const int e = 4 * (int) threadIdx.x + 256 * PG_WAVES * j;
-                float     o[4];
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    if constexpr (PRO == PRO_NORM) {
-                        const float t = xv[j][c][k] * sc[c];
-                        o[k]          = t * xw[j][0][k];
-                    } else {
-                        const float g    = xv[j][c][k];
-                        const float silu = g / (1.0f + expf(-g));
-                        o[k]             = silu * xw[j][c][k];
-                    }
-                }
-                const float m = group8_max(fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3]))));
-                const float dd = m / 127.0f;
-                const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
-                if (e < K) {
-                    char4 q;
-                    q.x                          = (signed char) roundf(o[0] * id);
-                    q.y                          = (signed char) roundf(o[1] * id);
-                    q.z                          = (signed char) roundf(o[2] * id);
-                    q.w                          = (signed char) roundf(o[3] * id);
-                    *(char4 *) &s_q[c * MAXK + e] = q;
-                    if ((lane & 7) == 0) {
-                        s_d[c * (MAXK / 32) + e / 32] = h2f(f2h(dd));
-                    }
-                    if (a.xo && blockIdx.x == 0) {
-                        *(float4_t *) (a.xo + (int64_t) c * K + e) = float4_t{ o[0], o[1], o[2], o[3] };
-                    }
-                }
-            }
-        }
-    }
+    // 3. the activation values, quantised into LDS
+    pg_prologue<NC, J, MAXK, PRO>(xv, xw, s_q, s_d, s_ss, a, lane, wv, K);
     if constexpr (PRE < CH) {
         pg_load<CH, PRE, CH>(ba, a, gw, lane);
     }
@@ -422,6 +436,136 @@ __global__ __launch_bounds__(64 * PG_WAVES) void k_gemv_q8_0_pro(PgArgs a) {
                 break;
             }
             pg_load<CH>(ba, a, it * TW + gw, lane);
+        }
+    }
+}
+
+// The MLP's gate_up GEMV with the RMS norm in its prologue (as
+// k_gemv_q8_0_pro<PRO_NORM>) and the SwiGLU plus the down GEMV's Q8_0
+// activation quantisation in its epilogue: the arithmetic of
+// rms_norm_mul_mat followed by swiglu_quant, each SwiGLU value and each
+// quantisation block computed once in the grid instead of once per CU in the
+// down GEMV's prologue.  Workgroup w owns the Q8_0 blocks [w bpw, (w+1) bpw)
+// of the F = N / 2 SwiGLU outputs; per block two units of 16 outputs, wave v
+// taking output h = 32 block + 16 half + v, i.e. gate row h and up row F + h
+// (swapped halves: F + h and h).  The two rows' sums are reduced as
+// store_rows reduces them (same bits as the separate GEMV's y), the SwiGLU of
+// each column goes to LDS, and once every unit is done the workgroup
+// quantises its blocks, 8 lanes per (block, column) as quant_chunk256.
+constexpr int GLU_MAXB = 8;  // blocks per workgroup
+
+struct GluArgs {
+    int64_t  F;        // SwiGLU width (N / 2)
+    int      swapped;  // gate in the second half
+    int      bpw;      // blocks per workgroup
+    int8_t * qs;       // Q8_0 activations [NC][F]
+    float *  qd;       // their scales [NC][F / 32]
+    float *  h;        // optional f32 SwiGLU rows [NC][F]
+};
+
+// SwiGLU output of one unit from the gate and up rows' per-lane partial
+// sums: each reduced as store_rows<NC, 1> reduces a row, the SwiGLU of
+// column c stored at sh[32 c]
+template <int NC>
+__device__ __forceinline__ void glu_out(float (&ag)[1][NC], float (&au)[1][NC], int lane, float * sh) {
+    float vg[NC], vu[NC];
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        vg[c] = ag[0][c];
+        vu[c] = au[0][c];
+    }
+    const float g   = wave_reduce_scatter<NC>(vg, lane);
+    const float u   = wave_reduce_scatter<NC>(vu, lane);
+    const int   idx = reduce_index<NC>(lane);
+    if ((lane & ((64 / NC) - 1)) == 0) {
+#pragma clang fp contract(off)
+        const float silu = g / (1.0f + expf(-g));
+        sh[idx * 32]     = silu * u;
+    }
+}
+
+template <int NC>
+__global__ __launch_bounds__(64 * PG_WAVES) void k_gemv_q8_0_norm_glu(PgArgs a, GluArgs gl) {
+    constexpr int CH   = 4;
+    constexpr int MAXK = 1024 * CH;
+    constexpr int J    = MAXK / (256 * PG_WAVES);
+    __shared__ __attribute__((aligned(16))) int8_t s_q[NC * MAXK];
+    __shared__ float  s_d[NC * MAXK / 32];
+    __shared__ double s_ss[NC][PG_WAVES];
+    __shared__ __attribute__((aligned(16))) float s_h[GLU_MAXB][NC][32];
+    const int     lane = threadIdx.x & 63;
+    const int     wv   = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int     K    = a.K;
+    const int64_t nblk = gl.F / 32;
+    const int     blk0 = (int) blockIdx.x * gl.bpw;
+    const int     nu   = 2 * (int) min((int64_t) gl.bpw, nblk - blk0);  // units of this workgroup (even)
+    auto          out  = [&](int u) { return (int64_t) (blk0 + u / 2) * 32 + (u & 1) * 16 + wv; };
+    auto          grow = [&](int u) { return gl.swapped ? gl.F + out(u) : out(u); };
+    auto          urow = [&](int u) { return gl.swapped ? out(u) : gl.F + out(u); };
+    // 1. activations, then unit 0's gate row, then (once the activations are
+    // in) its up row; the prologue computes while the rows are in flight
+    float4_t xv[J][NC], xw[J][1];
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const unsigned e = min(4u * threadIdx.x + 256u * PG_WAVES * j, (unsigned) K - 4u);
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            xv[j][c] = *(const float4_t *) (a.x + c * a.ldx + e);
+        }
+        xw[j][0] = *(const float4_t *) (a.nw + e);
+    }
+    PgBuf<CH> ba, bb;  // gate rows, up rows
+    pg_load<CH>(ba, a, grow(0), lane);
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            asm volatile("" ::"v"(xv[j][c][0]), "v"(xw[j][0][0]) : "memory");
+        }
+    }
+    pg_load<CH>(bb, a, urow(0), lane);
+    pg_prologue<NC, J, MAXK, PRO_NORM>(xv, xw, s_q, s_d, s_ss, a, lane, wv, K);
+    __syncthreads();
+    // 2. the units: the gate row's partial sums wait (unreduced) while the up
+    // row is reduced; each buffer is reloaded as soon as it is consumed
+    auto slot = [&](int u) { return &s_h[u / 2][0][(u & 1) * 16 + wv]; };
+    float ag[1][NC], au[1][NC];
+    int   u = 0;
+    for (; u + 1 < nu; u++) {
+        pg_acc<NC, CH>(ba, s_q, s_d, 0, a, lane, ag);
+        pg_load<CH>(ba, a, grow(u + 1), lane);
+        pg_acc<NC, CH>(bb, s_q, s_d, 0, a, lane, au);
+        glu_out<NC>(ag, au, lane, slot(u));
+        pg_load<CH>(bb, a, urow(u + 1), lane);
+    }
+    pg_acc<NC, CH>(ba, s_q, s_d, 0, a, lane, ag);
+    pg_acc<NC, CH>(bb, s_q, s_d, 0, a, lane, au);
+    glu_out<NC>(ag, au, lane, slot(u));
+    __syncthreads();
+    // 3. quantise the workgroup's blocks: 8 lanes per (block, column)
+    {
+#pragma clang fp contract(off)
+        const int p  = wv * 8 + (lane >> 3);
+        const int l8 = lane & 7;
+        if (p < nu / 2 * NC) {
+            const int      b  = p / NC, c = p % NC;
+            const float4_t v  = *(const float4_t *) &s_h[b][c][4 * l8];
+            const float    m  = group8_max(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+            const float    dd = m / 127.0f;
+            const float    id = dd != 0.0f ? 1.0f / dd : 0.0f;
+            char4          q;
+            q.x                 = (signed char) roundf(v[0] * id);
+            q.y                 = (signed char) roundf(v[1] * id);
+            q.z                 = (signed char) roundf(v[2] * id);
+            q.w                 = (signed char) roundf(v[3] * id);
+            const int64_t e     = (int64_t) (blk0 + b) * 32 + 4 * l8;
+            *(char4 *) &gl.qs[c * gl.F + e] = q;
+            if (l8 == 0) {
+                gl.qd[c * (gl.F / 32) + blk0 + b] = h2f(f2h(dd));
+            }
+            if (gl.h) {
+                *(float4_t *) &gl.h[c * gl.F + e] = v;
+            }
         }
     }
 }
@@ -677,6 +821,15 @@ static int gemv_dispatch(int wtype, const uint8_t * W, int64_t N, int64_t K, int
     constexpr int R = GemvShape<NC>::R;
     constexpr int U = GemvShape<NC>::U;
     if (wtype == TYPE_Q8_0) {
+        if constexpr (NC <= 2) {
+            // long rows (the down projection, K = 12288): two rows per wave
+            // in passes of two 1 KB chunks (4096 x 12288, M = 2: 12.1 us
+            // against 13.6 us for one pass over twelve chunks of one row;
+            // the same sums in the same order)
+            if (K > 4096) {
+                return launch_q8_0<NC, 2, 2>(W, N, K, rs, x, y, ldy, r, ldr, stream);
+            }
+        }
         // one row per wave for the short matrices (more waves in flight; with
         // two rows a 12-chunk pass needs 256 VGPRs and one wave per SIMD)
         if (N <= 8192) {
@@ -855,4 +1008,43 @@ extern "C" int mmhip_swiglu_mul_mat(int type, const void * W, int64_t N, int64_t
     const PgArgs a{ (const uint8_t *) W, N, (int) K, w_row_stride, g, ldg, u, ldu, nullptr, 0.0f, h_out, y, ldy,
                     res, ldr, 1 };
     return dispatch_pro<PRO_SWIGLU>(a, M, (hipStream_t) stream, "swiglu_mul_mat");
+}
+
+extern "C" int mmhip_rms_norm_mul_mat_glu_supported(int type, int64_t N, int64_t K, int64_t M) {
+    if (!(type == TYPE_Q8_0 && M >= 1 && M <= 2 && K >= 256 && K <= 4096 && K % 256 == 0 && N > 0 && N % 512 == 0)) {
+        return 0;
+    }
+    const int64_t nblk = N / 64;  // Q8_0 blocks of the N / 2 SwiGLU outputs
+    return (nblk + pg_cus() - 1) / pg_cus() <= GLU_MAXB;
+}
+
+extern "C" int mmhip_rms_norm_mul_mat_glu(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride,
+                                          const float * x, int64_t ldx, int64_t M, const float * norm_w, float eps,
+                                          int swapped, void * xq, float * h_out, void * stream) {
+    MMHIP_API_BEGIN();
+    if (!mmhip_rms_norm_mul_mat_glu_supported(type, N, K, M)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "rms_norm_mul_mat_glu: type %d N=%lld K=%lld M=%lld", type,
+                         (long long) N, (long long) K, (long long) M);
+    }
+    if (!W || !x || !norm_w || !xq || ldx < K || !gemv_supported(type, N, K, w_row_stride, W) ||
+        ((uintptr_t) x | (uintptr_t) norm_w | (uintptr_t) h_out | (uintptr_t) xq) % 16 != 0 || (ldx % 4) != 0) {
+        return set_error(MMHIP_ERR_INVALID, "rms_norm_mul_mat_glu: bad arguments / alignment");
+    }
+    const int64_t   F    = N / 2;
+    const ActLayout L    = act_layout(TYPE_Q8_0, F, M);
+    const int64_t   nblk = F / 32;
+    const int64_t   bpw  = (nblk + pg_cus() - 1) / pg_cus();
+    const int64_t   wgs  = (nblk + bpw - 1) / bpw;
+    const PgArgs    a{ (const uint8_t *) W, N, (int) K, w_row_stride, x, ldx, nullptr, 0, norm_w, eps, nullptr,
+                       nullptr, 0, nullptr, 0, 1 };
+    const GluArgs   gl{ F, swapped ? 1 : 0, (int) bpw, (int8_t *) xq + L.qs_off, (float *) ((char *) xq + L.d_off),
+                        h_out };
+    if (M == 1) {
+        hipLaunchKernelGGL(k_gemv_q8_0_norm_glu<1>, dim3((unsigned) wgs), dim3(64 * PG_WAVES), 0,
+                           (hipStream_t) stream, a, gl);
+    } else {
+        hipLaunchKernelGGL(k_gemv_q8_0_norm_glu<2>, dim3((unsigned) wgs), dim3(64 * PG_WAVES), 0,
+                           (hipStream_t) stream, a, gl);
+    }
+    return check_launch("rms_norm_mul_mat_glu");
 }

@@ -72,6 +72,9 @@ SIGNATURES = {
     "mmhip_swiglu_mul_mat_supported": (_i32, [_i32, _i64, _i64, _i64]),
     "mmhip_swiglu_mul_mat": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _vp,
                                     _i64, _vp]),
+    "mmhip_rms_norm_mul_mat_glu_supported": (_i32, [_i32, _i64, _i64, _i64]),
+    "mmhip_rms_norm_mul_mat_glu": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _f32, _i32, _vp, _vp,
+                                          _vp]),
     "mmhip_flash_attn_workspace": (_sz, [_VP, _VP, _VP]),
     "mmhip_flash_attn_ext": (_i32, [_VP, _VP, _VP, _VP, _f32, _vp, _vp, _sz, _vp]),
     "mmhip_flash_attn_ext_q": (_i32, [_VP, _VP, _VP, _VP, _f32, _vp, _vp, _sz, _i32, _vp, _vp]),

@@ -485,6 +485,58 @@ def test_swiglu_mul_mat_equals_two_pass(mm, pkg, M, F, N, mode):
     assert torch.equal(y3, y1 + r)
 
 
+@pytest.mark.parametrize("M,K,F,swapped", [(2, 4096, 12288, 0), (1, 1024, 512, 0), (2, 2048, 256 * 65, 1),
+                                           (1, 256, 256, 1), (2, 4096, 256 * 90, 0)])
+def test_rms_norm_mul_mat_glu_equals_two_pass(mm, pkg, M, K, F, swapped):
+    """gate_up GEMV with the RMS norm in its prologue and the SwiGLU + the
+    down GEMV's Q8_0 quantisation in its epilogue: the quantised activations
+    (bytes and scales) and the f32 SwiGLU rows equal rms_norm_mul_mat then
+    swiglu_quant bit for bit; one to three blocks per workgroup, a last
+    workgroup with one block (520 blocks over 256 CUs), gate / up halves in
+    either order."""
+    L = mm.load()
+    N = 2 * F
+    Wq = mm.QuantWeight.from_gguf(8, pkg.synth.gguf_blocks_np(8, N, K, 7), N, K)
+    rng = np.random.default_rng(28)
+    x = torch.from_numpy((rng.standard_normal((M, K)) * 3).astype(np.float32)).cuda()
+    w = torch.from_numpy((1 + 0.05 * rng.standard_normal(K)).astype(np.float32)).cuda()
+    assert L.mmhip_rms_norm_mul_mat_glu_supported(8, N, K, M) == 1
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    assert L.mmhip_rms_norm_mul_mat(8, ptr(Wq.data), N, K, Wq.row_bytes, ptr(x), K, M, ptr(w), 1e-6, None, None, 0,
+                                    ptr(y), N, st()) == 0
+    h1 = torch.empty((M, F), dtype=torch.float32, device="cuda")
+    xq1 = torch.zeros(L.mmhip_act_bytes(8, F, M), dtype=torch.uint8, device="cuda")
+    assert L.mmhip_swiglu_quant(ctypes.byref(mm.view_of(y)), None, swapped, ptr(h1), 8, ptr(xq1), st()) == 0
+    h2 = torch.full((M, F), float("nan"), device="cuda")
+    xq2 = torch.full_like(xq1, 0x5A)
+    assert L.mmhip_rms_norm_mul_mat_glu(8, ptr(Wq.data), N, K, Wq.row_bytes, ptr(x), K, M, ptr(w), 1e-6, swapped,
+                                        ptr(xq2), ptr(h2), st()) == 0
+    xq3 = torch.full_like(xq1, 0xA5)
+    assert L.mmhip_rms_norm_mul_mat_glu(8, ptr(Wq.data), N, K, Wq.row_bytes, ptr(x), K, M, ptr(w), 1e-6, swapped,
+                                        ptr(xq3), None, st()) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(h2, h1)
+    # the layout's padding bytes are never written: compare the qs and d fields
+    qs_n, d_off = M * F, (M * F + 255) // 256 * 256
+    for xq in (xq2, xq3):
+        assert torch.equal(xq[:qs_n], xq1[:qs_n])
+        assert torch.equal(xq[d_off:d_off + 4 * M * (F // 32)], xq1[d_off:d_off + 4 * M * (F // 32)])
+
+
+def test_rms_norm_mul_mat_glu_rejects_unsupported(mm):
+    L = mm.load()
+    assert L.mmhip_rms_norm_mul_mat_glu_supported(8, 24576, 4096, 2) == 1
+    assert L.mmhip_rms_norm_mul_mat_glu_supported(8, 24576, 8192, 2) == 0   # the norm: K <= 4096
+    assert L.mmhip_rms_norm_mul_mat_glu_supported(8, 24576, 4096, 3) == 0   # M > 2
+    assert L.mmhip_rms_norm_mul_mat_glu_supported(14, 24576, 4096, 2) == 0  # Q6_K weights
+    assert L.mmhip_rms_norm_mul_mat_glu_supported(8, 24320, 4096, 2) == 0   # N / 2 not whole 256-chunks
+    assert L.mmhip_rms_norm_mul_mat_glu_supported(8, 1 << 22, 4096, 2) == 0  # too many blocks per workgroup
+    dummy = torch.zeros(16, dtype=torch.float32, device="cuda")
+    rc = L.mmhip_rms_norm_mul_mat_glu(8, ptr(dummy), 24576, 8192, 8704, ptr(dummy), 8192, 2, ptr(dummy), 1e-6, 0,
+                                      ptr(dummy), None, st())
+    assert rc != 0
+
+
 def test_swiglu_mul_mat_rejects_unsupported(mm):
     L = mm.load()
     assert L.mmhip_swiglu_mul_mat_supported(8, 4096, 12544, 2) == 0  # K > 12288
