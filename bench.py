@@ -13,17 +13,19 @@ random-init weights; all inputs resident in HBM before timing):
               resident), wall_tok_s = the same with each step's host input
               uploads and launch included; roofline = the
               step's largest kernel (the MLP gate_up GEMV with its RMS-norm
-              prologue) alone; step_roofline = the step's algorithmic bytes /
+              prologue and SwiGLU epilogue) alone; step_roofline = the step's algorithmic bytes /
               its GPU time from HIP events on the backend stream.
   gemv_q8_0   Q8_0 decode GEMV: W 12288 x 4096 Q8_0, x [2 x 4096] f32 -> [2 x 12288]
               (one step = activation quantisation + GEMV).  8 weight copies
               (428 MB) rotate so the 256 MB Infinity Cache cannot hold them.
   fa_decode   GQA decode attention: B=2 (CFG), 32 q / 8 KV heads, D=128, KV 2048,
-              Q f32, K/V f16, no mask.  12 K/V copies rotate (202 MB... x 12).
+              Q f32, K/V f16, no mask.  16 K/V copies rotate (269 MB).
 
-The roofline object times the dominant kernel alone with HIP events on the
-stream it is launched on; the cpu_baseline object times the in-repo C
-restatement of ggml-CPU arithmetic (oracle/, "port") on a bounded sample.
+The roofline object times the dominant kernel (or the one call it belongs
+to) alone: its launches are captured into a HIP graph and replayed between
+HIP events on the stream they are launched on; the cpu_baseline object times
+the in-repo C restatement of ggml-CPU arithmetic (oracle/, "port") on a
+bounded sample.
 """
 import argparse
 import ctypes
@@ -53,19 +55,6 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     return ap.parse_args()
-
-
-def time_launches(torch, fn, n, rotate):
-    """Average duration of single launches, each bracketed by HIP events on the
-    current stream (the stream the kernels are launched on)."""
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
-    for i in range(n):
-        evs[i][0].record()
-        fn(i % rotate)
-        evs[i][1].record()
-    torch.cuda.synchronize()
-    ts = [a.elapsed_time(b) for a, b in evs]
-    return float(np.mean(ts)) * 1e-3, float(np.median(ts)) * 1e-3
 
 
 def graph_time(torch, fn, n, reps=10):
@@ -143,18 +132,17 @@ def bench_gemv(args, torch, pkg):
     dt = time.perf_counter() - t0
     ms = dt / args.steps * 1e3
 
-    # dominant kernel alone: the GEMV on pre-quantised activations
+    # dominant kernel alone: the GEMV on pre-quantised activations, launches
+    # replayed as a HIP graph (the kernel's own duration, as in a decode step)
     xq = mm.quantize_act(mm.Q8_0, x)
 
-    def gemv(i):
-        W = Ws[i]
+    def gemv(i, s):
+        W = Ws[i % copies]
         rc = L.mmhip_mul_mat_q(mm.Q8_0, ctypes.c_void_p(W.data.data_ptr()), N, K, W.row_bytes,
-                               ctypes.c_void_p(xq.data_ptr()), M, ctypes.c_void_p(y.data_ptr()), N, st)
+                               ctypes.c_void_p(xq.data_ptr()), M, ctypes.c_void_p(y.data_ptr()), N, s)
         assert rc == 0
 
-    for i in range(copies):
-        gemv(i)
-    avg_s, med_s = time_launches(torch, gemv, max(args.steps, 64), copies)
+    avg_s, med_s = graph_time(torch, gemv, 4 * copies)
     alg_bytes = N * K // 32 * 34 + M * K * 4 + M * N * 4  # weights + f32 x + f32 y
     achieved = alg_bytes / avg_s / 1e9
 
@@ -170,9 +158,9 @@ def bench_gemv(args, torch, pkg):
         "dtype": "q8_0xq8_0->f32 (int8 dot)",
         "config": {"workload": "Q8_0 decode GEMV W[12288x4096] x[2x4096] f32", "weight_copies_rotated": copies,
                    "step": "quantize_act + gemv"},
-        "roofline": {"bound": "hbm", "kernel": "k_gemv_q8_0<2,2>", "achieved": round(achieved, 2),
+        "roofline": {"bound": "hbm", "kernel": "k_gemv_q8_0<2,2,4,true>", "achieved": round(achieved, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "avg_launch_us": round(avg_s * 1e6, 3), "median_launch_us": round(med_s * 1e6, 3),
+                     "avg_launch_us": round(avg_s * 1e6, 3), "min_launch_us": round(med_s * 1e6, 3),
                      "alg_bytes_per_launch": alg_bytes, "traffic": profile_traffic("gemv_q8_0_12288x4096_m2")},
         "cpu_baseline": cpu,
     }
@@ -216,10 +204,11 @@ def bench_fa(args, torch, pkg):
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     scale = float(np.float32(1 / np.sqrt(D)))
 
-    def step(i):
+    def step(i, s=None):
         kv, vv = kvs[i % copies]
         rc = L.mmhip_flash_attn_ext(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), None, scale,
-                                    ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(ws.data_ptr()), need, st)
+                                    ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(ws.data_ptr()), need,
+                                    st if s is None else s)
         assert rc == 0, L.mmhip_last_error()
 
     for i in range(args.warmup):
@@ -230,7 +219,9 @@ def bench_fa(args, torch, pkg):
         step(i)
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) / args.steps * 1e3
-    avg_s, med_s = time_launches(torch, step, max(args.steps, 64), copies)
+    # one attention call = the split-KV kernel + the split combine, replayed
+    # as a HIP graph
+    avg_s, med_s = graph_time(torch, step, 4 * copies)
     alg_bytes = B * Hq * D * 4 * 2 + 2 * B * Hkv * nkv * D * 2
     achieved = alg_bytes / avg_s / 1e9
     cpu = None
@@ -254,9 +245,10 @@ def bench_fa(args, torch, pkg):
         "ms_per_step": round(ms, 5),
         "dtype": "f16 K/V, f32 accumulate",
         "config": {"workload": "GQA decode FA B=2 Hq=32 Hkv=8 D=128 KV=2048 no mask", "kv_copies_rotated": copies},
-        "roofline": {"bound": "hbm", "kernel": "k_fa_decode<128,8> + k_fa_combine", "achieved": round(achieved, 2),
+        "roofline": {"bound": "hbm", "kernel": "k_fa_dec_mfma<128,8,1,false> + k_fa_combine (one attention call)",
+                     "achieved": round(achieved, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "avg_launch_us": round(avg_s * 1e6, 3), "median_launch_us": round(med_s * 1e6, 3),
+                     "avg_launch_us": round(avg_s * 1e6, 3), "min_launch_us": round(med_s * 1e6, 3),
                      "alg_bytes_per_launch": alg_bytes, "traffic": profile_traffic("fa_decode_gqa_b2_kv2048")},
         "cpu_baseline": cpu,
     }
@@ -282,11 +274,12 @@ def _fa_common(args, torch, pkg, B, Hq, Hkv, S, D, causal, seed, copies):
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     scale = float(np.float32(1 / np.sqrt(D)))
 
-    def step(i):
+    def step(i, s=None):
         qv, kv, vv = views[i % copies]
         rc = L.mmhip_flash_attn_ext(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv),
                                     ctypes.byref(mv) if mv is not None else None, scale,
-                                    ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(ws.data_ptr()), need, st)
+                                    ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(ws.data_ptr()), need,
+                                    st if s is None else s)
         assert rc == 0, L.mmhip_last_error()
 
     return step
@@ -301,8 +294,10 @@ def _timed(args, torch, step, copies):
         step(i)
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) / args.steps * 1e3
-    avg_s, med_s = time_launches(torch, step, max(args.steps, 32), copies)
-    return ms, avg_s, med_s
+    # the roofline's launches replayed as a HIP graph (kernel durations
+    # without per-call host dispatch)
+    avg_s, min_s = graph_time(torch, step, 4 * copies)
+    return ms, avg_s, min_s
 
 
 MFMA_PEAK_TFLOPS = 2500.0
@@ -348,9 +343,11 @@ def bench_fa_mfma(args, torch, pkg, causal):
         "ms_per_step": round(ms, 4),
         "dtype": "f16 MFMA, f32 accumulate",
         "config": {"workload": name, "mask": "causal f16" if causal else "none"},
-        "roofline": {"bound": "mfma", "kernel": "k_fa_mfma<128>", "achieved": round(tf, 2),
+        "roofline": {"bound": "mfma",
+                     "kernel": "k_fa_mfma<128,8>" + (" + k_fa_row_end mask prepass (one attention call)" if causal else ""),
+                     "achieved": round(tf, 2),
                      "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
-                     "avg_launch_us": round(avg_s * 1e6, 2), "median_launch_us": round(med_s * 1e6, 2),
+                     "avg_launch_us": round(avg_s * 1e6, 2), "min_launch_us": round(med_s * 1e6, 2),
                      "alg_flops_per_launch": flops, "traffic": profile_traffic("fa_prefill_causal_b2_s1024_gqa" if causal else "fa_dit_b2_s4096_h16_d128")},
         "cpu_baseline": cpu,
     }
@@ -371,10 +368,11 @@ def bench_gemm(args, torch, pkg):
     L = mm.load()
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
-    def step(i):
+    def step(i, s=None):
         W, x = Ws[i % copies], xs[i % copies]
         rc = L.mmhip_mul_mat(mm.Q4_K, ctypes.c_void_p(W.data.data_ptr()), N, K, W.row_bytes,
-                             ctypes.c_void_p(x.data_ptr()), K, M, ctypes.c_void_p(y.data_ptr()), N, None, 0, st)
+                             ctypes.c_void_p(x.data_ptr()), K, M, ctypes.c_void_p(y.data_ptr()), N, None, 0,
+                             st if s is None else s)
         assert rc == 0, L.mmhip_last_error()
 
     ms, avg_s, med_s = _timed(args, torch, step, copies)
@@ -404,7 +402,7 @@ def bench_gemm(args, torch, pkg):
         "config": {"workload": "Q4_K GEMM W[6144x2048] x[8192x2048] f32 -> f32"},
         "roofline": {"bound": "mfma", "kernel": "k_gemm_q<Q4_K>", "achieved": round(tf, 2),
                      "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
-                     "avg_launch_us": round(avg_s * 1e6, 2), "median_launch_us": round(med_s * 1e6, 2),
+                     "avg_launch_us": round(avg_s * 1e6, 2), "min_launch_us": round(med_s * 1e6, 2),
                      "alg_flops_per_launch": flops, "traffic": profile_traffic("gemm_q4_k_6144x2048_m8192")},
         "cpu_baseline": cpu,
     }
@@ -485,37 +483,41 @@ def bench_lm(args, torch, pkg):
 
 def lm_dominant_kernel(torch, pkg, cfg):
     """The step's largest kernel alone: the MLP gate_up GEMV with the RMS norm
-    in its prologue (W [2 ffn x hidden] Q8_0, 2 columns), six weight copies
-    (642 MB) rotating past the 256 MB Infinity Cache, launches replayed as a
-    HIP graph like the step's."""
+    in its prologue and the SwiGLU + the down GEMV's Q8_0 quantisation in its
+    epilogue (W [2 ffn x hidden] Q8_0, 2 columns), six weight copies (642 MB)
+    rotating past the 256 MB Infinity Cache, launches replayed as a HIP graph
+    like the step's."""
     mm, synth = pkg.mmhip, pkg.synth
     N, K, M = 2 * cfg["ffn"], cfg["hidden"], 2
+    F = N // 2
     wt = cfg["wtype"]
     copies = 6
+    L = mm.load()
+    if not L.mmhip_rms_norm_mul_mat_glu_supported(wt, N, K, M):
+        return None
     Ws = [mm.QuantWeight.from_gguf(wt, synth.gguf_blocks_torch(wt, N, K, 2001 + c), N, K) for c in range(copies)]
     x = torch.from_numpy(synth.normal_np((M, K), 2011)).cuda()
     nw = torch.ones(K, device="cuda")
-    y = torch.empty((M, N), device="cuda")
-    L = mm.load()
-    if not L.mmhip_rms_norm_mul_mat_supported(wt, N, K, M):
-        return None
+    xq = torch.empty(L.mmhip_act_bytes(mm.Q8_0, F, M), dtype=torch.uint8, device="cuda")
 
     def launch(i, st):
         W = Ws[i % copies]
-        rc = L.mmhip_rms_norm_mul_mat(wt, ctypes.c_void_p(W.data.data_ptr()), N, K, W.row_bytes,
-                                      ctypes.c_void_p(x.data_ptr()), K, M, ctypes.c_void_p(nw.data_ptr()), 1e-6, None,
-                                      None, 0, ctypes.c_void_p(y.data_ptr()), N, st)
+        rc = L.mmhip_rms_norm_mul_mat_glu(wt, ctypes.c_void_p(W.data.data_ptr()), N, K, W.row_bytes,
+                                          ctypes.c_void_p(x.data_ptr()), K, M, ctypes.c_void_p(nw.data_ptr()), 1e-6, 0,
+                                          ctypes.c_void_p(xq.data_ptr()), None, st)
         assert rc == 0, L.mmhip_last_error()
 
     avg_s, min_s = graph_time(torch, launch, 36)
-    alg_bytes = Ws[0].data.numel() + M * K * 4 + K * 4 + M * N * 4  # weights + x + norm weight + y
+    # weights + x + norm weight + the Q8_0 SwiGLU rows written (int8 + f32 block scales)
+    alg_bytes = Ws[0].data.numel() + M * K * 4 + K * 4 + M * F + M * (F // 32) * 4
     achieved = alg_bytes / avg_s / 1e9
     del Ws
     torch.cuda.empty_cache()
-    return {"bound": "hbm", "kernel": "k_gemv_q8_0_pro<2,4,0>: RMS norm + gate_up GEMV %d x %d Q8_0, 2 columns "
-                                      "(the decode step's largest kernel)" % (N, K),
+    return {"bound": "hbm", "kernel": "k_gemv_q8_0_norm_glu<2>: RMS norm + gate_up GEMV %d x %d Q8_0 + SwiGLU, "
+                                      "2 columns (the decode step's largest kernel)" % (N, K),
             "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profile_traffic("gemv_norm_gate_up_24576x4096_m2"),
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": profile_traffic("gemv_norm_glu_gate_up_24576x4096_m2"),
             "avg_launch_us": round(avg_s * 1e6, 3), "min_launch_us": round(min_s * 1e6, 3),
             "alg_bytes_per_launch": alg_bytes}
 
