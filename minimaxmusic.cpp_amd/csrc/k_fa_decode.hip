@@ -762,11 +762,7 @@ __global__ __launch_bounds__(256) void k_fa_combine_q(const float * __restrict__
     int8_t * qs = xq_qs + row * K + e;
     if (qtype == TYPE_Q8_0) {
         // blocks of 32 = half a wave
-        float a = fabsf(v);
-#pragma unroll
-        for (int o = 16; o >= 1; o >>= 1) {
-            a = fmaxf(a, __shfl_xor(a, o, WAVE));
-        }
+        const float a = group32_max(fabsf(v));
         const float dd = a / 127.0f;
         const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
         *qs            = (int8_t) roundf(v * id);
@@ -779,17 +775,7 @@ __global__ __launch_bounds__(256) void k_fa_combine_q(const float * __restrict__
     float a  = fabsf(v);
     float vm = v;
     int   ix = t;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        const float a2  = __shfl_xor(a, o, WAVE);
-        const float vm2 = __shfl_xor(vm, o, WAVE);
-        const int   ix2 = __shfl_xor(ix, o, WAVE);
-        if (a2 > a || (a2 == a && ix2 < ix)) {
-            a  = a2;
-            vm = vm2;
-            ix = ix2;
-        }
-    }
+    wave_argmax_abs(a, vm, ix);
     if (lane == 0) {
         s_red[t >> 6]  = vm;
         s_idx[t >> 6]  = ix;
@@ -815,11 +801,7 @@ __global__ __launch_bounds__(256) void k_fa_combine_q(const float * __restrict__
         dd                 = 1.0f / iscale;
     }
     *qs    = (int8_t) q;
-    int sb = q;
-#pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) {
-        sb += __shfl_xor(sb, o, WAVE);
-    }
+    const int sb = group16_sum_i(q);
     if ((t & 15) == 0) {
         xq_bs[row * (K / 16) + e / 16] = (int16_t) sb;
     }

@@ -120,17 +120,7 @@ __device__ __forceinline__ void quant_chunk256(const float (&v)[4], int lane, in
                 ix = 4 * lane + k;
             }
         }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            const float a2  = __shfl_xor(a, o, WAVE);
-            const float vm2 = __shfl_xor(vm, o, WAVE);
-            const int   ix2 = __shfl_xor(ix, o, WAVE);
-            if (a2 > a || (a2 == a && ix2 < ix)) {
-                a  = a2;
-                vm = vm2;
-                ix = ix2;
-            }
-        }
+        wave_argmax_abs(a, vm, ix);
         int   qv[4] = { 0, 0, 0, 0 };
         float dd    = 0.0f;
         if (a != 0.0f) {
@@ -147,8 +137,8 @@ __device__ __forceinline__ void quant_chunk256(const float (&v)[4], int lane, in
         q4.z   = (signed char) qv[2];
         q4.w   = (signed char) qv[3];
         int sb = qv[0] + qv[1] + qv[2] + qv[3];
-        sb += __shfl_xor(sb, 1, WAVE);
-        sb += __shfl_xor(sb, 2, WAVE);
+        sb += dpp_i<DPP_XOR1>(sb);
+        sb += dpp_i<DPP_XOR2>(sb);
         if ((lane & 3) == 0) {
             bs[lane >> 2] = (int16_t) sb;
         }

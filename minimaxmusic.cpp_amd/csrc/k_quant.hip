@@ -126,11 +126,7 @@ __global__ __launch_bounds__(256) void k_quant_q8_0(const float * __restrict__ x
         const int64_t m  = blk / nblk;
         const int64_t b  = blk % nblk;
         const float   xv = x[m * ldx + b * 32 + lane];
-        float         a  = fabsf(xv);
-#pragma unroll
-        for (int o = 16; o >= 1; o >>= 1) {
-            a = fmaxf(a, __shfl_xor(a, o, 32));
-        }
+        const float   a  = group32_max(fabsf(xv));
         const float d  = a / 127.0f;
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
         qs[m * K + b * 32 + lane] = (int8_t) roundf(xv * id);
@@ -155,16 +151,9 @@ __global__ __launch_bounds__(256) void k_quant_q8_K(const float * __restrict__ x
         const float * xb = x + m * ldx + sb * 256;
         const float   xv = xb[tid];
         float         a  = fabsf(xv);
+        float         vm = xv;
         int           ix = tid;
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            const float a2 = __shfl_xor(a, o, WAVE);
-            const int   i2 = __shfl_xor(ix, o, WAVE);
-            if (a2 > a || (a2 == a && i2 < ix)) {
-                a  = a2;
-                ix = i2;
-            }
-        }
+        wave_argmax_abs(a, vm, ix);
         if ((tid & 63) == 0) {
             s_amax[tid >> 6] = a;
             s_idx[tid >> 6]  = ix;
@@ -188,11 +177,7 @@ __global__ __launch_bounds__(256) void k_quant_q8_K(const float * __restrict__ x
             d                  = 1.0f / iscale;
         }
         qs[m * K + sb * 256 + tid] = qv;
-        int s = qv;
-#pragma unroll
-        for (int o = 8; o >= 1; o >>= 1) {
-            s += __shfl_xor(s, o, 16);
-        }
+        const int s = group16_sum_i(qv);
         if ((tid & 15) == 0) {
             bsums[m * (K / 16) + sb * 16 + tid / 16] = (int16_t) s;
         }

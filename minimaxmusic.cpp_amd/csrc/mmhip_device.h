@@ -102,6 +102,10 @@ template <int CTRL> __device__ __forceinline__ float dpp_f(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
 
+template <int CTRL> __device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
+}
+
 template <int CTRL> __device__ __forceinline__ double dpp_d(double v) {
     const int2 p = __builtin_bit_cast(int2, v);
     return __builtin_bit_cast(double, int2{ __builtin_amdgcn_mov_dpp(p.x, CTRL, 0xF, 0xF, false),
@@ -132,6 +136,55 @@ __device__ __forceinline__ float group8_max(float v) {
     v = fmaxf(v, dpp_f<DPP_XOR1>(v));
     v = fmaxf(v, dpp_f<DPP_XOR2>(v));
     return fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
+}
+
+// Max over aligned groups of 32 lanes (a Q8_0 block of one value per lane).
+__device__ __forceinline__ float group32_max(float v) {
+    v = fmaxf(v, dpp_f<DPP_XOR1>(v));
+    v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+    v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_f<DPP_MIRROR>(v));
+    return max_xor16(v);
+}
+
+// Sum over aligned groups of 16 lanes (a Q8_K 16-element block sum).
+__device__ __forceinline__ int group16_sum_i(int v) {
+    v += dpp_i<DPP_XOR1>(v);
+    v += dpp_i<DPP_XOR2>(v);
+    v += dpp_i<DPP_HALF_MIRROR>(v);
+    return v + dpp_i<DPP_MIRROR>(v);
+}
+
+// The element of largest |x| over the wave, lowest index on ties: a (its
+// |x|), vm (its x) and ix (its index) hold each lane's candidate on entry and
+// the winner in every lane on return.  (largest a, lowest ix) is a total
+// order, so any reduction tree selects the same element.
+__device__ __forceinline__ void wave_argmax_abs(float & a, float & vm, int & ix) {
+    auto take = [&](float a2, float vm2, int ix2) {
+        if (a2 > a || (a2 == a && ix2 < ix)) {
+            a  = a2;
+            vm = vm2;
+            ix = ix2;
+        }
+    };
+    take(dpp_f<DPP_XOR1>(a), dpp_f<DPP_XOR1>(vm), dpp_i<DPP_XOR1>(ix));
+    take(dpp_f<DPP_XOR2>(a), dpp_f<DPP_XOR2>(vm), dpp_i<DPP_XOR2>(ix));
+    take(dpp_f<DPP_HALF_MIRROR>(a), dpp_f<DPP_HALF_MIRROR>(vm), dpp_i<DPP_HALF_MIRROR>(ix));
+    take(dpp_f<DPP_MIRROR>(a), dpp_f<DPP_MIRROR>(vm), dpp_i<DPP_MIRROR>(ix));
+    {
+        const auto pa = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+        const auto pv = __builtin_amdgcn_permlane16_swap(__float_as_uint(vm), __float_as_uint(vm), false, false);
+        const auto pi = __builtin_amdgcn_permlane16_swap((unsigned) ix, (unsigned) ix, false, false);
+        a = __uint_as_float(pa[0]), vm = __uint_as_float(pv[0]), ix = (int) pi[0];
+        take(__uint_as_float(pa[1]), __uint_as_float(pv[1]), (int) pi[1]);
+    }
+    {
+        const auto pa = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+        const auto pv = __builtin_amdgcn_permlane32_swap(__float_as_uint(vm), __float_as_uint(vm), false, false);
+        const auto pi = __builtin_amdgcn_permlane32_swap((unsigned) ix, (unsigned) ix, false, false);
+        a = __uint_as_float(pa[0]), vm = __uint_as_float(pv[0]), ix = (int) pi[0];
+        take(__uint_as_float(pa[1]), __uint_as_float(pv[1]), (int) pi[1]);
+    }
 }
 
 // Sum over all 64 lanes; every lane receives the total.
