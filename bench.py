@@ -101,6 +101,40 @@ def profile_traffic(name):
     return None
 
 
+def via_backend(pkg, make, reps=20):
+    """The same op through the ggml-backend boundary: a graph of n_ops
+    independent nodes of it (one per rotated input copy) built with the ggml
+    API and run by ggml_backend_graph_compute on the MI355X backend.  make(og)
+    creates the tensors and ops on the OpGraph og and returns (outputs, n_ops,
+    upload) where upload() sets the inputs after allocation.  Reported: GPU
+    time per op of the replayed graph (HIP events on the backend stream) and
+    the host wall clock per op of graph_compute + synchronize."""
+    import importlib
+
+    og_mod = importlib.import_module(pkg.__name__ + ".opgraph")
+    og = og_mod.OpGraph(n_tensors=256)
+    try:
+        outs, n_ops, upload = make(og)
+        og.build(outs)
+        upload()
+        for _ in range(3):  # eager, captured, first replay
+            og.compute()
+        og.synchronize()
+        og.gpu_time(reset=True)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            og.compute()
+        og.synchronize()
+        wall = (time.perf_counter() - t0) / reps
+        ms, n = og.gpu_time()
+        replays, eager = og.graph_stats()
+    finally:
+        og.close()
+    return {"path": "ggml_backend_graph_compute, MI355X backend, HIP-graph replay", "ops_per_graph": n_ops,
+            "gpu_us_per_op": round(ms / max(n, 1) * 1e3 / n_ops, 3), "wall_us_per_op": round(wall * 1e6 / n_ops, 3),
+            "replays": replays, "eager": eager}
+
+
 def bench_gemv(args, torch, pkg):
     import oracle
 
@@ -146,6 +180,22 @@ def bench_gemv(args, torch, pkg):
     alg_bytes = N * K // 32 * 34 + M * K * 4 + M * N * 4  # weights + f32 x + f32 y
     achieved = alg_bytes / avg_s / 1e9
 
+    del xq
+    raw = synth.gguf_blocks_np(mm.Q8_0, N, K, 1002)
+    xh = synth.normal_np((M, K), 1003)
+
+    def make(og):
+        x_t = og.tensor(mm.F32, [K, M])
+        ws_t = [og.tensor(mm.Q8_0, [K, N]) for _ in range(copies)]
+        outs = [og.mul_mat(w, x_t) for w in ws_t]
+
+        def upload():
+            og.set(x_t, xh)
+            for w in ws_t:
+                og.set(w, raw)
+        return outs, copies, upload
+
+    backend = via_backend(pkg, make)
     cpu = None
     if not args.no_cpu:
         cpu = cpu_gemv(oracle, synth, N, K, M, args.cpu_seconds)
@@ -158,6 +208,7 @@ def bench_gemv(args, torch, pkg):
         "dtype": "q8_0xq8_0->f32 (int8 dot)",
         "config": {"workload": "Q8_0 decode GEMV W[12288x4096] x[2x4096] f32", "weight_copies_rotated": copies,
                    "step": "quantize_act + gemv"},
+        "via_backend": backend,
         "roofline": {"bound": "hbm", "kernel": "k_gemv_q8_0<2,2,4,true>", "achieved": round(achieved, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "avg_launch_us": round(avg_s * 1e6, 3), "min_launch_us": round(med_s * 1e6, 3),
@@ -224,6 +275,22 @@ def bench_fa(args, torch, pkg):
     avg_s, med_s = graph_time(torch, step, 4 * copies)
     alg_bytes = B * Hq * D * 4 * 2 + 2 * B * Hkv * nkv * D * 2
     achieved = alg_bytes / avg_s / 1e9
+    qh = q.cpu().numpy()
+    kh = ks[0].cpu().numpy()
+
+    def make(og):
+        q_t = og.tensor(mm.F32, [D, 1, Hq, B])
+        kv_t = [(og.tensor(mm.F16, [D, nkv, Hkv, B]), og.tensor(mm.F16, [D, nkv, Hkv, B])) for _ in range(copies)]
+        outs = [og.flash_attn(q_t, k_t, v_t, None, scale) for k_t, v_t in kv_t]
+
+        def upload():
+            og.set(q_t, qh)
+            for k_t, v_t in kv_t:
+                og.set(k_t, kh)
+                og.set(v_t, kh)
+        return outs, copies, upload
+
+    backend = via_backend(pkg, make)
     cpu = None
     if not args.no_cpu:
         qn = q.cpu().numpy()
@@ -245,6 +312,7 @@ def bench_fa(args, torch, pkg):
         "ms_per_step": round(ms, 5),
         "dtype": "f16 K/V, f32 accumulate",
         "config": {"workload": "GQA decode FA B=2 Hq=32 Hkv=8 D=128 KV=2048 no mask", "kv_copies_rotated": copies},
+        "via_backend": backend,
         "roofline": {"bound": "hbm", "kernel": "k_fa_dec_mfma<128,8,1,false> + k_fa_combine (one attention call)",
                      "achieved": round(achieved, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
@@ -318,6 +386,32 @@ def bench_fa_mfma(args, torch, pkg, causal):
     step = _fa_common(args, torch, pkg, B, Hq, Hkv, S, D, causal, seed, copies)
     ms, avg_s, med_s = _timed(args, torch, step, copies)
     tf = flops / avg_s / 1e12
+    mm = pkg.mmhip
+    rng = np.random.default_rng(seed + 100)
+    qh = rng.standard_normal((B, Hq, S, D)).astype(np.float16).astype(np.float32)
+    kh = rng.standard_normal((B, Hkv, S, D)).astype(np.float16)
+    mh = np.triu(np.full((S, S), -np.inf, np.float32), 1).astype(np.float16) if causal else None
+    scale = float(np.float32(1 / np.sqrt(D)))
+
+    def make(og):
+        m_t = og.tensor(mm.F16, [S, S]) if causal else None
+        ops = [(og.tensor(mm.F32, [D, S, Hq, B]), og.tensor(mm.F16, [D, S, Hkv, B]), og.tensor(mm.F16, [D, S, Hkv, B]))
+               for _ in range(copies)]
+        outs = [og.flash_attn(q_t, k_t, v_t, m_t, scale) for q_t, k_t, v_t in ops]
+
+        def upload():
+            if causal:
+                og.set(m_t, mh)
+            for q_t, k_t, v_t in ops:
+                og.set(q_t, qh)
+                og.set(k_t, kh)
+                og.set(v_t, kh)
+        return outs, copies, upload
+
+    backend = via_backend(pkg, make, reps=5)
+    backend["tflops_per_op"] = round(flops / (backend["gpu_us_per_op"] * 1e-6) / 1e12, 2)
+    backend["note"] = ("measured after the C-ABI timings: the same kernel runs slower once the MFMA load has been "
+                       "sustained for a while (clock drop visible in the kernel trace)")
     cpu = None
     if not args.no_cpu:
         rng = np.random.default_rng(seed)
@@ -343,6 +437,7 @@ def bench_fa_mfma(args, torch, pkg, causal):
         "ms_per_step": round(ms, 4),
         "dtype": "f16 MFMA, f32 accumulate",
         "config": {"workload": name, "mask": "causal f16" if causal else "none"},
+        "via_backend": backend,
         "roofline": {"bound": "mfma",
                      "kernel": "k_fa_mfma<128,8>" + (" + k_fa_row_end mask prepass (one attention call)" if causal else ""),
                      "achieved": round(tf, 2),
@@ -378,6 +473,23 @@ def bench_gemm(args, torch, pkg):
     ms, avg_s, med_s = _timed(args, torch, step, copies)
     flops = 2.0 * M * N * K
     tf = flops / avg_s / 1e12
+    raw = synth.gguf_blocks_np(mm.Q4_K, N, K, 1005)
+    xh = np.random.default_rng(1006).standard_normal((M, K)).astype(np.float32)
+
+    def make(og):
+        ops = [(og.tensor(mm.Q4_K, [K, N]), og.tensor(mm.F32, [K, M])) for _ in range(copies)]
+        outs = [og.mul_mat(w_t, x_t) for w_t, x_t in ops]
+
+        def upload():
+            for w_t, x_t in ops:
+                og.set(w_t, raw)
+                og.set(x_t, xh)
+        return outs, copies, upload
+
+    backend = via_backend(pkg, make, reps=5)
+    backend["tflops_per_op"] = round(flops / (backend["gpu_us_per_op"] * 1e-6) / 1e12, 2)
+    backend["note"] = ("measured after the C-ABI timings: the same kernel runs slower once the MFMA load has been "
+                       "sustained for a while (clock drop visible in the kernel trace)")
     cpu = None
     if not args.no_cpu:
         rows = 64
@@ -400,6 +512,7 @@ def bench_gemm(args, torch, pkg):
         "ms_per_step": round(ms, 4),
         "dtype": "f16 MFMA (Q4_K dequantised to f16), f32 accumulate",
         "config": {"workload": "Q4_K GEMM W[6144x2048] x[8192x2048] f32 -> f32"},
+        "via_backend": backend,
         "roofline": {"bound": "mfma", "kernel": "k_gemm_q<Q4_K>", "achieved": round(tf, 2),
                      "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
                      "avg_launch_us": round(avg_s * 1e6, 2), "min_launch_us": round(med_s * 1e6, 2),
@@ -607,7 +720,7 @@ def main():
         "cpu_baseline": res["cpu_baseline"],
         "baseline_metric": METRIC,
     }
-    for k in ("step_roofline", "wall_tok_s", "wall_ms_per_step"):
+    for k in ("step_roofline", "wall_tok_s", "wall_ms_per_step", "via_backend"):
         if k in res:
             line[k] = res[k]
     print(json.dumps(line), flush=True)

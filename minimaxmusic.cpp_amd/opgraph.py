@@ -1,0 +1,166 @@
+"""Single-op ggml graphs run through the MI355X ggml backend (ctypes).
+
+The reference hands every op to a ggml backend inside a graph
+(ggml_backend_sched_graph_compute, src/qwen3-lm.h:620, src/dit.h:385, or
+ggml_backend_graph_compute, src/static-graph.h:58).  This module builds graphs
+of FLASH_ATTN_EXT / MUL_MAT nodes with the restated ggml API
+(libggml-base.so), allocates them in the backend's device buffer, uploads
+inputs with ggml_backend_tensor_set (quantized weights as GGUF blocks: the
+buffer repacks them) and runs ggml_backend_graph_compute on the MI355X backend
+(libggml-mi355x.so): the eager first call, then HIP-graph capture and replays.
+There is no CPU path: the backend library must load and find a GPU.
+"""
+import ctypes
+import pathlib
+
+import numpy as np
+
+LIBDIR = pathlib.Path(__file__).resolve().parent / "lib"
+GGML_MAX_NAME = 128
+F32, F16, Q8_0, Q4_K, Q6_K = 0, 1, 8, 12, 14
+PREC_F32 = 10
+
+
+class Tensor(ctypes.Structure):
+    pass
+
+
+Tensor._fields_ = [
+    ("type", ctypes.c_int), ("buffer", ctypes.c_void_p), ("ne", ctypes.c_int64 * 4), ("nb", ctypes.c_size_t * 4),
+    ("op", ctypes.c_int), ("op_params", ctypes.c_int32 * 16), ("flags", ctypes.c_int32),
+    ("src", ctypes.POINTER(Tensor) * 10), ("view_src", ctypes.POINTER(Tensor)), ("view_offs", ctypes.c_size_t),
+    ("data", ctypes.c_void_p), ("name", ctypes.c_char * GGML_MAX_NAME), ("extra", ctypes.c_void_p),
+    ("padding", ctypes.c_char * 8),
+]
+
+
+class _InitParams(ctypes.Structure):
+    _fields_ = [("mem_size", ctypes.c_size_t), ("mem_buffer", ctypes.c_void_p), ("no_alloc", ctypes.c_bool)]
+
+
+_T = ctypes.POINTER(Tensor)
+_libs = {}
+
+
+def _load():
+    if _libs:
+        return _libs["base"], _libs["mi"]
+    vp, i64, i32, f32, sz, b = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_size_t, ctypes.c_bool
+    base = ctypes.CDLL(str(LIBDIR / "libggml-base.so"), mode=ctypes.RTLD_GLOBAL)
+    mi = ctypes.CDLL(str(LIBDIR / "libggml-mi355x.so"), mode=ctypes.RTLD_GLOBAL)
+    sig = {
+        "ggml_init": (vp, [_InitParams]), "ggml_free": (None, [vp]),
+        "ggml_tensor_overhead": (sz, []), "ggml_graph_overhead_custom": (sz, [sz, b]),
+        "ggml_new_tensor_4d": (_T, [vp, i32, i64, i64, i64, i64]),
+        "ggml_mul_mat": (_T, [vp, _T, _T]),
+        "ggml_flash_attn_ext": (_T, [vp, _T, _T, _T, _T, f32, f32, f32]),
+        "ggml_flash_attn_ext_set_prec": (None, [_T, i32]),
+        "ggml_new_graph_custom": (vp, [vp, sz, b]), "ggml_build_forward_expand": (None, [vp, _T]),
+        "ggml_nbytes": (sz, [_T]),
+        "ggml_backend_alloc_ctx_tensors": (vp, [vp, vp]), "ggml_backend_buffer_free": (None, [vp]),
+        "ggml_backend_tensor_set": (None, [_T, vp, sz, sz]), "ggml_backend_tensor_get": (None, [_T, vp, sz, sz]),
+        "ggml_backend_graph_compute": (i32, [vp, vp]), "ggml_backend_synchronize": (None, [vp]),
+        "ggml_backend_free": (None, [vp]),
+    }
+    for n, (r, a) in sig.items():
+        fn = getattr(base, n)
+        fn.restype, fn.argtypes = r, a
+    misig = {
+        "ggml_backend_mi355x_init": (vp, [i32]),
+        "ggml_backend_mi355x_gpu_time": (None, [vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(i64), i32]),
+        "ggml_backend_mi355x_graph_stats": (None, [vp, ctypes.POINTER(i64), ctypes.POINTER(i64)]),
+    }
+    for n, (r, a) in misig.items():
+        fn = getattr(mi, n)
+        fn.restype, fn.argtypes = r, a
+    _libs["base"], _libs["mi"] = base, mi
+    return base, mi
+
+
+class OpGraph:
+    """A ggml context of graph tensors on the MI355X backend.  Create the
+    tensors and ops, call build(outputs), upload inputs with set(), then
+    compute() runs the graph through ggml_backend_graph_compute."""
+
+    def __init__(self, n_tensors=256, device=0):
+        self.G, self.MI = _load()
+        mem = n_tensors * self.G.ggml_tensor_overhead() + self.G.ggml_graph_overhead_custom(n_tensors, False)
+        self.ctx = self.G.ggml_init(_InitParams(mem, None, True))
+        if not self.ctx:
+            raise RuntimeError("ggml_init failed")
+        self.backend = self.MI.ggml_backend_mi355x_init(device)
+        if not self.backend:
+            raise RuntimeError("MI355X ggml backend: no device")
+        self.n_tensors = n_tensors
+        self.buf = None
+        self.graph = None
+
+    def tensor(self, type_, ne):
+        ne = list(ne) + [1] * (4 - len(ne))
+        return self.G.ggml_new_tensor_4d(self.ctx, type_, *ne)
+
+    def flash_attn(self, q, k, v, mask, scale):
+        t = self.G.ggml_flash_attn_ext(self.ctx, q, k, v, mask, scale, 0.0, 0.0)
+        self.G.ggml_flash_attn_ext_set_prec(t, PREC_F32)
+        return t
+
+    def mul_mat(self, w, x):
+        return self.G.ggml_mul_mat(self.ctx, w, x)
+
+    def build(self, outputs):
+        self.graph = self.G.ggml_new_graph_custom(self.ctx, self.n_tensors, False)
+        for t in outputs:
+            self.G.ggml_build_forward_expand(self.graph, t)
+        self.buf = self.G.ggml_backend_alloc_ctx_tensors(self.ctx, self.backend)
+        if not self.buf:
+            raise RuntimeError("ggml_backend_alloc_ctx_tensors failed")
+
+    def set(self, t, arr):
+        a = np.ascontiguousarray(arr)
+        n = self.G.ggml_nbytes(t)
+        if a.nbytes != n:
+            raise ValueError(f"tensor_set: {a.nbytes} bytes for a {n}-byte tensor")
+        self.G.ggml_backend_tensor_set(t, a.ctypes.data_as(ctypes.c_void_p), 0, n)
+
+    def get(self, t, dtype=np.float32):
+        n = self.G.ggml_nbytes(t)
+        out = np.empty(n // np.dtype(dtype).itemsize, dtype=dtype)
+        self.G.ggml_backend_tensor_get(t, out.ctypes.data_as(ctypes.c_void_p), 0, n)
+        return out
+
+    def compute(self):
+        rc = self.G.ggml_backend_graph_compute(self.backend, self.graph)
+        if rc != 0:
+            raise RuntimeError(f"ggml_backend_graph_compute: status {rc}")
+
+    def synchronize(self):
+        self.G.ggml_backend_synchronize(self.backend)
+
+    def gpu_time(self, reset=False):
+        """(total GPU ms, graph_compute calls) since the last reset: HIP
+        events on the backend stream around each graph_compute."""
+        ms, n = ctypes.c_double(0.0), ctypes.c_int64(0)
+        self.MI.ggml_backend_mi355x_gpu_time(self.backend, ctypes.byref(ms), ctypes.byref(n), 1 if reset else 0)
+        return ms.value, n.value
+
+    def graph_stats(self):
+        r, e = ctypes.c_int64(0), ctypes.c_int64(0)
+        self.MI.ggml_backend_mi355x_graph_stats(self.backend, ctypes.byref(r), ctypes.byref(e))
+        return r.value, e.value
+
+    def close(self):
+        if self.buf:
+            self.G.ggml_backend_buffer_free(self.buf)
+            self.buf = None
+        if self.backend:
+            self.G.ggml_backend_free(self.backend)
+            self.backend = None
+        if self.ctx:
+            self.G.ggml_free(self.ctx)
+            self.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
