@@ -101,6 +101,22 @@ def profile_traffic(name):
     return None
 
 
+def cpu_rate(fn, seconds):
+    """Seconds per call of fn() over about `seconds` of repeated calls."""
+    t0 = time.perf_counter()
+    it = 0
+    while time.perf_counter() - t0 < seconds or it == 0:
+        fn()
+        it += 1
+    return (time.perf_counter() - t0) / it, it
+
+
+def half_threads():
+    """The reference's default CPU thread count: hardware_concurrency() / 2
+    (src/backend.h:25-31)."""
+    return max(1, (os.cpu_count() or 2) // 2)
+
+
 def via_backend(pkg, make, reps=20):
     """The same op through the ggml-backend boundary: a graph of n_ops
     independent nodes of it (one per rotated input copy) built with the ggml
@@ -223,14 +239,13 @@ def cpu_gemv(oracle, synth, N, K, M, seconds):
     raw = synth.gguf_blocks_np(8, rows, K, 7)
     x = synth.normal_np((M, K), 8)
     oracle.mul_mat_ggml(8, raw, rows, K, x, nthreads=n_thr)
-    t0 = time.perf_counter()
-    it = 0
-    while time.perf_counter() - t0 < seconds:
-        oracle.mul_mat_ggml(8, raw, rows, K, x, nthreads=n_thr)
-        it += 1
-    dt = (time.perf_counter() - t0) / it
-    gbs = (rows * K // 32 * 34 + M * K * 4 + M * rows * 4) / dt / 1e9
+    nbytes = rows * K // 32 * 34 + M * K * 4 + M * rows * 4
+    dt, it = cpu_rate(lambda: oracle.mul_mat_ggml(8, raw, rows, K, x, nthreads=n_thr), seconds)
+    nh = half_threads()
+    dt_h, _ = cpu_rate(lambda: oracle.mul_mat_ggml(8, raw, rows, K, x, nthreads=nh), seconds / 2)
+    gbs = nbytes / dt / 1e9
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": n_thr, "kind": "port",
+            "half_threads": {"value": round(nbytes / dt_h / 1e9, 3), "cores": nh},
             "sample": f"ggml-CPU-semantics Q8_0 mul_mat (oracle/oracle.c) on {rows} of {N} rows, K={K}, M={M}, "
                       f"{it} reps in {seconds:.0f}s"}
 
@@ -297,13 +312,13 @@ def bench_fa(args, torch, pkg):
         kn = ks[0].cpu().numpy()
         vn = vs[0].cpu().numpy()
         n_thr = os.cpu_count() or 1
-        t0 = time.perf_counter()
-        it = 0
-        while time.perf_counter() - t0 < args.cpu_seconds:
-            oracle.flash_attn_ext(qn, kn, vn, None, scale, "ggml", nthreads=n_thr)
-            it += 1
-        dt = (time.perf_counter() - t0) / it
+        dt, it = cpu_rate(lambda: oracle.flash_attn_ext(qn, kn, vn, None, scale, "ggml", nthreads=n_thr),
+                          args.cpu_seconds)
+        nh = half_threads()
+        dt_h, _ = cpu_rate(lambda: oracle.flash_attn_ext(qn, kn, vn, None, scale, "ggml", nthreads=nh),
+                           args.cpu_seconds / 2)
         cpu = {"value": round(alg_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": n_thr, "kind": "port",
+               "half_threads": {"value": round(alg_bytes / dt_h / 1e9, 3), "cores": nh},
                "sample": f"ggml-CPU-semantics flash_attn_ext (oracle/oracle.c), full shape, {it} reps"}
     return {
         "metric": "GQA decode attention effective HBM GB/s (B=2, 32q/8kv, D128, KV 2048)",
@@ -420,14 +435,14 @@ def bench_fa_mfma(args, torch, pkg, causal):
         k = rng.standard_normal((B, Hkv, S, D)).astype(np.float16)
         v = rng.standard_normal((B, Hkv, S, D)).astype(np.float16)
         n_thr = os.cpu_count() or 1
-        t0 = time.perf_counter()
-        it = 0
-        while time.perf_counter() - t0 < args.cpu_seconds:
-            oracle.flash_attn_ext(q, k, v, None, 1 / np.sqrt(D), "ggml", nthreads=n_thr)
-            it += 1
-        dt = (time.perf_counter() - t0) / it
+        dt, it = cpu_rate(lambda: oracle.flash_attn_ext(q, k, v, None, 1 / np.sqrt(D), "ggml", nthreads=n_thr),
+                          args.cpu_seconds)
+        nh = half_threads()
+        dt_h, _ = cpu_rate(lambda: oracle.flash_attn_ext(q, k, v, None, 1 / np.sqrt(D), "ggml", nthreads=nh),
+                           args.cpu_seconds / 2)
         cpu_flops = 4.0 * B * Hq * rows * S * D
         cpu = {"value": round(cpu_flops / dt / 1e12, 5), "unit": "TFLOP/s", "cores": n_thr, "kind": "port",
+               "half_threads": {"value": round(cpu_flops / dt_h / 1e12, 5), "cores": nh},
                "sample": f"ggml-CPU-semantics flash_attn_ext (oracle/oracle.c): {rows} query rows per head against "
                          f"all {S} keys, {it} reps"}
     return {
@@ -496,13 +511,11 @@ def bench_gemm(args, torch, pkg):
         raw = synth.gguf_blocks_np(mm.Q4_K, rows, K, 9)
         x = synth.normal_np((64, K), 10)
         n_thr = os.cpu_count() or 1
-        t0 = time.perf_counter()
-        it = 0
-        while time.perf_counter() - t0 < args.cpu_seconds:
-            oracle.mul_mat_ggml(mm.Q4_K, raw, rows, K, x, nthreads=n_thr)
-            it += 1
-        dt = (time.perf_counter() - t0) / it
+        dt, it = cpu_rate(lambda: oracle.mul_mat_ggml(mm.Q4_K, raw, rows, K, x, nthreads=n_thr), args.cpu_seconds)
+        nh = half_threads()
+        dt_h, _ = cpu_rate(lambda: oracle.mul_mat_ggml(mm.Q4_K, raw, rows, K, x, nthreads=nh), args.cpu_seconds / 2)
         cpu = {"value": round(2.0 * 64 * rows * K / dt / 1e12, 5), "unit": "TFLOP/s", "cores": n_thr,
+               "half_threads": {"value": round(2.0 * 64 * rows * K / dt_h / 1e12, 5), "cores": nh},
                "kind": "port", "sample": f"ggml-CPU-semantics Q4_K x Q8_K mul_mat (oracle/oracle.c): {rows} weight "
                                          f"rows x 64 tokens, K={K}, {it} reps"}
     return {
@@ -655,29 +668,29 @@ def cpu_lm(args, lm_mod, cfg):
     x = rng.standard_normal((2, H)).astype(np.float32)
     wn = np.ones(H, np.float32)
 
-    def layer():
+    def layer(nt):
         h = oracle.rms_norm_mul(x, wn, 1e-6)
-        qkv = oracle.mul_mat_ggml(t, W["qkv"], Nh * D + 2 * Nkv * D, H, h, nthreads=n_thr)
+        qkv = oracle.mul_mat_ggml(t, W["qkv"], Nh * D + 2 * Nkv * D, H, h, nthreads=nt)
         q = oracle.rope_neox(qkv[:, :Nh * D].reshape(2, Nh, D), np.array([4095, 4095], np.int32), D, 1e6)
         o = oracle.flash_attn_ext(np.ascontiguousarray(q[:, :, None]), kc, vc, None, 1 / np.sqrt(D), "ggml",
-                                  nthreads=n_thr).reshape(2, Nh * D)
-        h2 = x + oracle.mul_mat_ggml(t, W["o"], H, Nh * D, np.asarray(o, np.float32), nthreads=n_thr)
-        gu = oracle.mul_mat_ggml(t, W["gu"], 2 * F, H, oracle.rms_norm_mul(h2, wn, 1e-6), nthreads=n_thr)
-        return h2 + oracle.mul_mat_ggml(t, W["down"], H, F, oracle.swiglu(gu), nthreads=n_thr)
+                                  nthreads=nt).reshape(2, Nh * D)
+        h2 = x + oracle.mul_mat_ggml(t, W["o"], H, Nh * D, np.asarray(o, np.float32), nthreads=nt)
+        gu = oracle.mul_mat_ggml(t, W["gu"], 2 * F, H, oracle.rms_norm_mul(h2, wn, 1e-6), nthreads=nt)
+        return h2 + oracle.mul_mat_ggml(t, W["down"], H, F, oracle.swiglu(gu), nthreads=nt)
 
-    t0 = time.perf_counter()
-    it = 0
-    while time.perf_counter() - t0 < args.cpu_seconds or it == 0:
-        layer()
-        it += 1
-    t_layer = (time.perf_counter() - t0) / it
     rows = 8192  # lm_head sample: 8192 of the 151936 vocab rows
     Wl = synth.gguf_blocks_np(t, rows, H, 99)
-    t0 = time.perf_counter()
-    oracle.mul_mat_ggml(t, Wl, rows, H, x, nthreads=n_thr)
-    t_head = (time.perf_counter() - t0) * V / rows
-    step = 36 * t_layer + t_head
+
+    def step_s(nt, seconds):
+        t_layer, it = cpu_rate(lambda: layer(nt), seconds)
+        t_head, _ = cpu_rate(lambda: oracle.mul_mat_ggml(t, Wl, rows, H, x, nthreads=nt), 0.0)
+        return 36 * t_layer + t_head * V / rows, t_layer, it
+
+    step, t_layer, it = step_s(n_thr, args.cpu_seconds)
+    nh = half_threads()
+    step_h, _, _ = step_s(nh, args.cpu_seconds / 2)
     return {"value": round(2.0 / step, 4), "unit": "tok/s", "cores": n_thr, "kind": "port",
+            "half_threads": {"value": round(2.0 / step_h, 4), "cores": nh},
             "sample": f"ggml-CPU-semantics restatement (oracle/): {it} full-shape decoder layer(s) at KV 4096 "
                       f"({t_layer * 1e3:.0f} ms each) and an 8192-row lm_head slice, extrapolated to 36 layers + "
                       f"the 151936-row lm_head ({step:.2f} s per 2-token step)"}
