@@ -264,8 +264,12 @@ __global__ __launch_bounds__(NW * 64) void k_fa_mfma(FaArgs a, const int * __res
             }
         }
         }
-        mx               = max_xor32(mx);
-        const float mnew = fmaxf(m, mx);
+        mx = max_xor32(mx);
+        // the reference max moves only when a score exceeds it by more than
+        // 8 (log2 units): p = exp2(s - m) then stays <= 2^8 (well inside f16
+        // and f32), O / l is unchanged in exact arithmetic, and most tiles
+        // need no rescale of the accumulators
+        const float mnew = mx > m + 8.0f ? mx : m;
         // No divergent control flow from here on: the MFMAs below combine the
         // operands of all 64 lanes.  A query with nothing visible yet keeps
         // its state (alpha = 1) and contributes p = exp2(-inf) = 0.
