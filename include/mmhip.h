@@ -253,6 +253,16 @@ int mmhip_set_rows(const mmhip_view * src, const mmhip_view * ids, int ids_type,
 int mmhip_swiglu(const mmhip_view * a, const mmhip_view * b, int swapped, float * dst, void * stream);
 /* GGML_OP_SCALE: dst = a * s + bias (src/depth-decoder.h:355). */
 int mmhip_scale(const mmhip_view * a, float s, float bias, float * dst, void * stream);
+/* GGML_OP_NORM: per-row LayerNorm without the affine part, eps as given
+ * (dit_layer_norm, src/dit.h:161-167, eps 1e-5); dst contiguous f32 rows.
+ * ggml-CPU's steps: mean and variance from double sums. */
+int mmhip_norm(const mmhip_view * x, float eps, float * dst, void * stream);
+/* GGML_OP_CONCAT of f32 a and b along dim 0..3 (the DiT input channel concat
+ * and the timestep token, src/dit.h:262-264, :273); dst contiguous. */
+int mmhip_concat(const mmhip_view * a, const mmhip_view * b, int dim, float * dst, void * stream);
+/* GGML_OP_CLAMP: dst = MAX(MIN(a, hi), lo) (the DiT's f16-range clamp,
+ * src/dit.h:276-278); dst may alias a contiguous a (ggml_clamp is in place). */
+int mmhip_clamp(const mmhip_view * a, float lo, float hi, float * dst, void * stream);
 
 #ifdef __cplusplus
 }

@@ -500,7 +500,7 @@ bool supports_rope(const struct ggml_tensor * op) {
     memcpy(&attn_factor, &op->op_params[8], sizeof(float));
     return mode == GGML_ROPE_TYPE_NEOX && freq_scale == 1.0f && ext_factor == 0.0f && attn_factor == 1.0f &&
            op->src[2] == nullptr && op->src[0]->type == GGML_TYPE_F32 && op->src[0]->nb[0] == 4 &&
-           op->src[1]->type == GGML_TYPE_I32 && ggml_is_contiguous(op->src[1]) && op->src[0]->ne[3] == 1;
+           op->src[1]->type == GGML_TYPE_I32 && ggml_is_contiguous(op->src[1]) && op->src[1]->ne[0] == op->src[0]->ne[2];
 }
 
 bool is_f32_or_f16(enum ggml_type t) {
@@ -542,6 +542,13 @@ bool supports(const struct ggml_tensor * op) {
                    ggml_is_contiguous(op);
         case GGML_OP_SCALE:
             return op->src[0]->type == GGML_TYPE_F32 && ggml_is_contiguous(op);
+        case GGML_OP_NORM:
+            return op->src[0]->type == GGML_TYPE_F32 && op->type == GGML_TYPE_F32 && ggml_is_contiguous(op);
+        case GGML_OP_CONCAT:
+            return op->src[0]->type == GGML_TYPE_F32 && op->src[1]->type == GGML_TYPE_F32 &&
+                   op->type == GGML_TYPE_F32 && ggml_is_contiguous(op);
+        case GGML_OP_CLAMP:
+            return op->src[0]->type == GGML_TYPE_F32 && ggml_is_contiguous(op->src[0]) && ggml_is_contiguous(op);
         default:
             return false;
     }
@@ -655,6 +662,27 @@ int run_node(mi_backend * c, const struct ggml_tensor * n) {
             memcpy(&bias, &n->op_params[1], sizeof(float));
             mmhip_view a = view_of(n->src[0]);
             rc           = mmhip_scale(&a, sc, bias, (float *) n->data, s);
+            break;
+        }
+        case GGML_OP_NORM: {
+            float eps;
+            memcpy(&eps, &n->op_params[0], sizeof(float));
+            mmhip_view x = view_of(n->src[0]);
+            rc           = mmhip_norm(&x, eps, (float *) n->data, s);
+            break;
+        }
+        case GGML_OP_CONCAT: {
+            mmhip_view a = view_of(n->src[0]);
+            mmhip_view b = view_of(n->src[1]);
+            rc           = mmhip_concat(&a, &b, n->op_params[0], (float *) n->data, s);
+            break;
+        }
+        case GGML_OP_CLAMP: {
+            float lo, hi;
+            memcpy(&lo, &n->op_params[0], sizeof(float));
+            memcpy(&hi, &n->op_params[1], sizeof(float));
+            mmhip_view a = view_of(n->src[0]);
+            rc           = mmhip_clamp(&a, lo, hi, (float *) n->data, s);
             break;
         }
         default:

@@ -277,6 +277,77 @@ __global__ __launch_bounds__(256) void k_rms_norm(TV x, TV w, int has_w, float e
     }
 }
 
+// GGML_OP_NORM (LayerNorm without affine part, src/dit.h:161-167): one
+// workgroup per row, ggml-CPU's steps -- mean from a double sum, y = x - mean,
+// variance from the double sum of y^2, y *= 1 / sqrtf(variance + eps).
+__global__ __launch_bounds__(256) void k_layer_norm(TV x, float eps, float * __restrict__ dst) {
+#pragma clang fp contract(off)
+    __shared__ double s_part[4];
+    const int64_t     row = blockIdx.x;
+    const int64_t     i1 = row % x.ne[1], i2 = (row / x.ne[1]) % x.ne[2], i3 = row / (x.ne[1] * x.ne[2]);
+    const int64_t     n  = x.ne[0];
+    const char *      xr = at(x, 0, i1, i2, i3);
+    float *           dr = dst + row * n;
+    double            sm = 0.0;
+    for (int64_t i = threadIdx.x; i < n; i += 256) {
+        sm += (double) *(const float *) (xr + i * x.nb[0]);
+    }
+    sm = wave_sum_d(sm);
+    if ((threadIdx.x & 63) == 0) {
+        s_part[threadIdx.x >> 6] = sm;
+    }
+    __syncthreads();
+    const float mean = (float) ((s_part[0] + s_part[1] + s_part[2] + s_part[3]) / (double) n);
+    __syncthreads();
+    double ss = 0.0;
+    for (int64_t i = threadIdx.x; i < n; i += 256) {
+        const float v = *(const float *) (xr + i * x.nb[0]) - mean;
+        dr[i]         = v;
+        ss += (double) (v * v);
+    }
+    ss = wave_sum_d(ss);
+    if ((threadIdx.x & 63) == 0) {
+        s_part[threadIdx.x >> 6] = ss;
+    }
+    __syncthreads();
+    const float var = (float) ((s_part[0] + s_part[1] + s_part[2] + s_part[3]) / (double) n);
+    const float sc  = 1.0f / sqrtf(var + eps);
+    for (int64_t i = threadIdx.x; i < n; i += 256) {
+        dr[i] = dr[i] * sc;  // each thread rescales the elements it wrote
+    }
+}
+
+// GGML_OP_CONCAT of two f32 tensors along dim (src/dit.h:262-273): dst is
+// contiguous; an index below a's extent along dim reads a, the rest b.
+__global__ void k_concat(TV a, TV b, int dim, int64_t n, float * __restrict__ dst) {
+    int64_t ne[4];
+    for (int i = 0; i < 4; i++) {
+        ne[i] = a.ne[i] + (i == dim ? b.ne[i] : 0);
+    }
+    for (int64_t i = blockIdx.x * (int64_t) blockDim.x + threadIdx.x; i < n; i += (int64_t) gridDim.x * blockDim.x) {
+        int64_t j[4];
+        unravel(i, ne, j[0], j[1], j[2], j[3]);
+        const int64_t na = a.ne[dim];
+        if (j[dim] < na) {
+            dst[i] = *(const float *) at(a, j[0], j[1], j[2], j[3]);
+        } else {
+            j[dim] -= na;
+            dst[i] = *(const float *) at(b, j[0], j[1], j[2], j[3]);
+        }
+    }
+}
+
+// GGML_OP_CLAMP (src/dit.h:276-278): ggml-CPU's MAX(MIN(x, hi), lo).
+__global__ void k_clamp(TV a, float lo, float hi, int64_t n, float * __restrict__ dst) {
+    for (int64_t i = blockIdx.x * (int64_t) blockDim.x + threadIdx.x; i < n; i += (int64_t) gridDim.x * blockDim.x) {
+        int64_t i0, i1, i2, i3;
+        unravel(i, a.ne, i0, i1, i2, i3);
+        const float x = *(const float *) at(a, i0, i1, i2, i3);
+        const float t = x < hi ? x : hi;
+        dst[i]        = t > lo ? t : lo;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Per-head rows of the QKV projection (the CONT / RMS_NORM / MUL / ROPE /
 // SET_ROWS chain of the attention block): one wave per row (h, t) of D = 64 *
@@ -836,6 +907,60 @@ extern "C" int mmhip_swiglu(const mmhip_view * a, const mmhip_view * b, int swap
     hipLaunchKernelGGL(k_swiglu, dim3(grid_for(n, 256)), dim3(256), 0, (hipStream_t) stream, tv(a), bv, b ? 1 : 0,
                        swapped, dst, n, nout0);
     return check_launch("swiglu");
+}
+
+extern "C" int mmhip_norm(const mmhip_view * x, float eps, float * dst, void * stream) {
+    MMHIP_API_BEGIN();
+    if (!x || !dst || x->ne[0] <= 0) {
+        return set_error(MMHIP_ERR_INVALID, "norm: bad arguments");
+    }
+    const int64_t rows = x->ne[1] * x->ne[2] * x->ne[3];
+    if (rows == 0) {
+        return MMHIP_OK;
+    }
+    if (rows >= ((int64_t) 1 << 31) || nel(x) >= ((int64_t) 1 << 31)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "norm: too many elements");
+    }
+    hipLaunchKernelGGL(k_layer_norm, dim3((unsigned) rows), dim3(256), 0, (hipStream_t) stream, tv(x), eps, dst);
+    return check_launch("norm");
+}
+
+extern "C" int mmhip_concat(const mmhip_view * a, const mmhip_view * b, int dim, float * dst, void * stream) {
+    MMHIP_API_BEGIN();
+    if (!a || !b || !dst || dim < 0 || dim > 3) {
+        return set_error(MMHIP_ERR_INVALID, "concat: bad arguments");
+    }
+    for (int i = 0; i < 4; i++) {
+        if (i != dim && a->ne[i] != b->ne[i]) {
+            return set_error(MMHIP_ERR_INVALID, "concat: shapes differ outside dim %d", dim);
+        }
+    }
+    const int64_t n = nel(a) + nel(b);
+    if (n == 0) {
+        return MMHIP_OK;
+    }
+    if (n >= ((int64_t) 1 << 31)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "concat: too many elements");
+    }
+    hipLaunchKernelGGL(k_concat, dim3(grid_for(n, 256)), dim3(256), 0, (hipStream_t) stream, tv(a), tv(b), dim, n,
+                       dst);
+    return check_launch("concat");
+}
+
+extern "C" int mmhip_clamp(const mmhip_view * a, float lo, float hi, float * dst, void * stream) {
+    MMHIP_API_BEGIN();
+    if (!a || !dst) {
+        return set_error(MMHIP_ERR_INVALID, "clamp: bad arguments");
+    }
+    const int64_t n = nel(a);
+    if (n == 0) {
+        return MMHIP_OK;
+    }
+    if (n >= ((int64_t) 1 << 31)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "clamp: too many elements");
+    }
+    hipLaunchKernelGGL(k_clamp, dim3(grid_for(n, 256)), dim3(256), 0, (hipStream_t) stream, tv(a), lo, hi, n, dst);
+    return check_launch("clamp");
 }
 
 extern "C" int mmhip_scale(const mmhip_view * a, float s, float bias, float * dst, void * stream) {

@@ -158,6 +158,7 @@ extern "C" const char * ggml_op_name(enum ggml_op op) {
         case GGML_OP_SCALE: return "SCALE";
         case GGML_OP_CLAMP: return "CLAMP";
         case GGML_OP_NORM: return "NORM";
+        case GGML_OP_CONCAT: return "CONCAT";
         case GGML_OP_RMS_NORM: return "RMS_NORM";
         case GGML_OP_MUL_MAT: return "MUL_MAT";
         case GGML_OP_CPY: return "CPY";
@@ -570,6 +571,24 @@ extern "C" struct ggml_tensor * ggml_clamp(struct ggml_context * ctx, struct ggm
     set_op_params(r, params, sizeof(params));
     r->op     = GGML_OP_CLAMP;
     r->src[0] = a;
+    return r;
+}
+
+// a and b joined along dim (equal extents elsewhere); op_params[0] = dim
+extern "C" struct ggml_tensor * ggml_concat(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b,
+                                            int dim) {
+    CORE_ASSERT(dim >= 0 && dim < 4 && a->type == b->type);
+    int64_t ne[4];
+    for (int i = 0; i < 4; i++) {
+        CORE_ASSERT(i == dim || a->ne[i] == b->ne[i]);
+        ne[i] = a->ne[i] + (i == dim ? b->ne[i] : 0);
+    }
+    struct ggml_tensor * r = ggml_new_tensor(ctx, a->type, 4, ne);
+    const int32_t        d = dim;
+    set_op_params(r, &d, sizeof(d));
+    r->op     = GGML_OP_CONCAT;
+    r->src[0] = a;
+    r->src[1] = b;
     return r;
 }
 

@@ -90,6 +90,9 @@ SIGNATURES = {
     "mmhip_set_rows": (_i32, [_VP, _VP, _i32, _VP, _i32, _vp]),
     "mmhip_swiglu": (_i32, [_VP, _VP, _i32, _vp, _vp]),
     "mmhip_scale": (_i32, [_VP, _f32, _f32, _vp, _vp]),
+    "mmhip_norm": (_i32, [_VP, _f32, _vp, _vp]),
+    "mmhip_concat": (_i32, [_VP, _VP, _i32, _vp, _vp]),
+    "mmhip_clamp": (_i32, [_VP, _f32, _f32, _vp, _vp]),
     # include/mmhip_synth.h
     "mmhip_synth_gguf": (_i32, [_i32, _vp, _i64, ctypes.c_uint64, _vp]),
     "mmhip_synth_normal": (_i32, [_i32, _vp, _i64, ctypes.c_uint64, _f32, _f32, _vp]),

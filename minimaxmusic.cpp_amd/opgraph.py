@@ -3,7 +3,7 @@
 The reference hands every op to a ggml backend inside a graph
 (ggml_backend_sched_graph_compute, src/qwen3-lm.h:620, src/dit.h:385, or
 ggml_backend_graph_compute, src/static-graph.h:58).  This module builds graphs
-of FLASH_ATTN_EXT / MUL_MAT nodes with the restated ggml API
+of FLASH_ATTN_EXT / MUL_MAT nodes and of the DiT block's glue ops with the restated ggml API
 (libggml-base.so), allocates them in the backend's device buffer, uploads
 inputs with ggml_backend_tensor_set (quantized weights as GGUF blocks: the
 buffer repacks them) and runs ggml_backend_graph_compute on the MI355X backend
@@ -19,6 +19,7 @@ LIBDIR = pathlib.Path(__file__).resolve().parent / "lib"
 GGML_MAX_NAME = 128
 F32, F16, Q8_0, Q4_K, Q6_K = 0, 1, 8, 12, 14
 PREC_F32 = 10
+ROPE_NEOX = 2
 
 
 class Tensor(ctypes.Structure):
@@ -53,6 +54,15 @@ def _load():
         "ggml_tensor_overhead": (sz, []), "ggml_graph_overhead_custom": (sz, [sz, b]),
         "ggml_new_tensor_4d": (_T, [vp, i32, i64, i64, i64, i64]),
         "ggml_mul_mat": (_T, [vp, _T, _T]),
+        "ggml_add": (_T, [vp, _T, _T]), "ggml_mul": (_T, [vp, _T, _T]),
+        "ggml_norm": (_T, [vp, _T, f32]), "ggml_scale": (_T, [vp, _T, f32]),
+        "ggml_clamp": (_T, [vp, _T, f32, f32]), "ggml_concat": (_T, [vp, _T, _T, i32]),
+        "ggml_rope_ext": (_T, [vp, _T, _T, _T, i32, i32, i32, f32, f32, f32, f32, f32, f32]),
+        "ggml_permute": (_T, [vp, _T, i32, i32, i32, i32]),
+        "ggml_reshape_3d": (_T, [vp, _T, i64, i64, i64]), "ggml_reshape_4d": (_T, [vp, _T, i64, i64, i64, i64]),
+        "ggml_view_3d": (_T, [vp, _T, i64, i64, i64, sz, sz, sz]),
+        "ggml_cast": (_T, [vp, _T, i32]), "ggml_cont": (_T, [vp, _T]),
+        "ggml_swiglu_split": (_T, [vp, _T, _T]),
         "ggml_flash_attn_ext": (_T, [vp, _T, _T, _T, _T, f32, f32, f32]),
         "ggml_flash_attn_ext_set_prec": (None, [_T, i32]),
         "ggml_new_graph_custom": (vp, [vp, sz, b]), "ggml_build_forward_expand": (None, [vp, _T]),
@@ -106,6 +116,48 @@ class OpGraph:
 
     def mul_mat(self, w, x):
         return self.G.ggml_mul_mat(self.ctx, w, x)
+
+    # the DiT block's other ops (src/dit.h:161-247, :255-268)
+    def add(self, a, b):
+        return self.G.ggml_add(self.ctx, a, b)
+
+    def mul(self, a, b):
+        return self.G.ggml_mul(self.ctx, a, b)
+
+    def norm(self, a, eps):
+        return self.G.ggml_norm(self.ctx, a, eps)
+
+    def scale(self, a, s):
+        return self.G.ggml_scale(self.ctx, a, s)
+
+    def clamp(self, a, lo, hi):
+        return self.G.ggml_clamp(self.ctx, a, lo, hi)
+
+    def concat(self, a, b, dim):
+        return self.G.ggml_concat(self.ctx, a, b, dim)
+
+    def rope_neox(self, a, pos, n_dims, freq_base):
+        return self.G.ggml_rope_ext(self.ctx, a, pos, None, n_dims, ROPE_NEOX, 0, freq_base, 1.0, 0.0, 1.0, 0.0, 0.0)
+
+    def permute(self, a, *axes):
+        return self.G.ggml_permute(self.ctx, a, *axes)
+
+    def reshape(self, a, ne):
+        if len(ne) == 3:
+            return self.G.ggml_reshape_3d(self.ctx, a, *ne)
+        return self.G.ggml_reshape_4d(self.ctx, a, *ne)
+
+    def view_3d(self, a, ne, nb1, nb2, offset):
+        return self.G.ggml_view_3d(self.ctx, a, ne[0], ne[1], ne[2], nb1, nb2, offset)
+
+    def cast(self, a, type_):
+        return self.G.ggml_cast(self.ctx, a, type_)
+
+    def cont(self, a):
+        return self.G.ggml_cont(self.ctx, a)
+
+    def swiglu_split(self, gate, value):
+        return self.G.ggml_swiglu_split(self.ctx, gate, value)
 
     def build(self, outputs):
         self.graph = self.G.ggml_new_graph_custom(self.ctx, self.n_tensors, False)

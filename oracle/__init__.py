@@ -72,6 +72,7 @@ def lib():
         L.orc_flash_attn_ext_ggml.argtypes = [T, T, T, T, f32, vp, i32]
         L.orc_flash_attn_ext_f64.argtypes = [T, T, T, T, f32, vp, i32]
         L.orc_rms_norm_mul.argtypes = [vp, vp, vp, i64, i64, f32]
+        L.orc_layer_norm.argtypes = [vp, vp, i64, i64, f32]
         L.orc_rope_neox.argtypes = [vp, vp, i64, i64, i64, i64, vp, f32]
         L.orc_swiglu.argtypes = [vp, vp, i64, i64]
         _lib = L
@@ -209,6 +210,15 @@ def rms_norm_mul(x, w, eps):
     y = np.empty_like(x)
     wp = _p(np.ascontiguousarray(w, dtype=np.float32)) if w is not None else None
     lib().orc_rms_norm_mul(_p(x), wp, _p(y), n, rows, eps)
+    return y
+
+
+def layer_norm(x, eps):
+    """GGML_OP_NORM over the last axis (oracle.c orc_layer_norm)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n = x.shape[-1]
+    y = np.empty_like(x)
+    lib().orc_layer_norm(_p(x), _p(y), n, x.size // n, eps)
     return y
 
 

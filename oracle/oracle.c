@@ -671,6 +671,29 @@ void orc_rms_norm_mul(const float * x, const float * w, float * y, int64_t n, in
     }
 }
 
+void orc_layer_norm(const float * x, float * y, int64_t n, int64_t rows, float eps) {
+    for (int64_t r = 0; r < rows; r++) {
+        const float * xr  = x + r * n;
+        float *       yr  = y + r * n;
+        double        sum = 0.0;
+        for (int64_t i = 0; i < n; i++) {
+            sum += (double) xr[i];
+        }
+        const float mean = (float) (sum / (double) n);
+        double      sum2 = 0.0;
+        for (int64_t i = 0; i < n; i++) {
+            const float v = xr[i] - mean;
+            yr[i]         = v;
+            sum2 += (double) (v * v);
+        }
+        const float variance = (float) (sum2 / (double) n);
+        const float scale    = 1.0f / sqrtf(variance + eps);
+        for (int64_t i = 0; i < n; i++) {
+            yr[i] *= scale;
+        }
+    }
+}
+
 /* NeoX RoPE: pair (i, i + n_dims/2) rotates by theta_i, with theta_0 = pos
  * and theta_{i+1} = theta_i * base^(-2/n_dims) accumulated in f32 (the
  * iterative cache of ggml's rope [ext]). */

@@ -117,6 +117,10 @@ void orc_flash_attn_ext_f64(const orc_tensor * q, const orc_tensor * k, const or
 /* ---- decode-step glue, closed-form definitions (qwen3-lm.h:730-859) ---- */
 /* y = x / sqrt(mean(x^2) + eps) * w, rows of n (w may be NULL). */
 void orc_rms_norm_mul(const float * x, const float * w, float * y, int64_t n, int64_t rows, float eps);
+/* LayerNorm without affine part (GGML_OP_NORM, src/dit.h:161-167): mean from
+ * a double sum, y = x - mean, variance from the double sum of y^2,
+ * y *= 1 / sqrtf(variance + eps) -- ggml-CPU's norm_f32 steps [ext]. */
+void orc_layer_norm(const float * x, float * y, int64_t n, int64_t rows, float eps);
 /* NeoX RoPE (mode 2) on rows of head_dim, rotating the first n_dims, with
  * positions[row / heads]; freq_base as ggml's theta, freq_scale 1. */
 void orc_rope_neox(const float * x, float * y, int64_t head_dim, int64_t n_dims, int64_t heads,

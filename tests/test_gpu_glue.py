@@ -543,3 +543,94 @@ def test_swiglu_mul_mat_rejects_unsupported(mm):
     assert L.mmhip_swiglu_mul_mat_supported(8, 4096, 12288, 3) == 0  # M > 2
     assert L.mmhip_swiglu_mul_mat_supported(14, 4096, 12288, 2) == 0  # Q6_K weights
     assert L.mmhip_rms_norm_mul_mat_supported(8, 4096, 8192, 2) == 0  # the norm: K <= 4096
+
+
+# ---- DiT glue: LayerNorm, CONCAT, CLAMP ----
+
+@pytest.mark.parametrize("shape", [(3, 2048), (2, 5, 300), (4, 1), (1, 4096 + 7)])
+def test_layer_norm(mm, orc, shape):
+    """GGML_OP_NORM vs the oracle: max-rel 1e-5 (f32 steps, double sums in
+    another order); a strided view reads the same rows."""
+    L = mm.load()
+    rng = np.random.default_rng(31)
+    x = (rng.standard_normal(shape) * 4 + 10).astype(np.float32)
+    tx = torch.from_numpy(x).cuda()
+    out = torch.empty_like(tx)
+    assert L.mmhip_norm(ctypes.byref(mm.view_of(tx)), 1e-6, ptr(out), st()) == 0
+    ref = orc.layer_norm(x, 1e-6)
+    assert rel_err(out.cpu().numpy(), ref) < 1e-5
+    # rows of a wider tensor (nb[1] = 2 * ne[0] * 4)
+    wide = torch.from_numpy(np.concatenate([x, -x], axis=-1)).cuda()
+    vw = wide[..., : shape[-1]]
+    out2 = torch.empty_like(tx)
+    assert L.mmhip_norm(ctypes.byref(mm.view_of(vw)), 1e-6, ptr(out2), st()) == 0
+    assert torch.equal(out2, out)
+
+
+def test_layer_norm_in_place_and_constant_rows(mm):
+    L = mm.load()
+    t = torch.full((3, 512), 2.5, device="cuda")
+    assert L.mmhip_norm(ctypes.byref(mm.view_of(t)), 1e-6, ptr(t), st()) == 0
+    assert torch.equal(t, torch.zeros_like(t))
+    a = torch.tensor([1.0, -1.0], device="cuda").repeat(2, 64) + 7.0
+    assert L.mmhip_norm(ctypes.byref(mm.view_of(a)), 3.0, ptr(a), st()) == 0
+    exp = torch.tensor([0.5, -0.5], device="cuda").repeat(2, 64)
+    assert torch.allclose(a, exp, rtol=1e-6, atol=0)
+
+
+@pytest.mark.parametrize("dim", [0, 1, 2])
+def test_concat(mm, dim):
+    """GGML_OP_CONCAT, bit-exact against torch.cat (ggml dim d is torch dim 2-d
+    for 3-d tensors)."""
+    L = mm.load()
+    g = torch.Generator().manual_seed(32 + dim)
+    base = [4, 6, 40]
+    sa, sb = list(base), list(base)
+    sb[2 - dim] = 3
+    a = torch.randn(sa, generator=g).cuda()
+    b = torch.randn(sb, generator=g).cuda()
+    ref = torch.cat([a, b], dim=2 - dim)
+    out = torch.empty_like(ref)
+    assert L.mmhip_concat(ctypes.byref(mm.view_of(a)), ctypes.byref(mm.view_of(b)), dim, ptr(out), st()) == 0
+    assert torch.equal(out, ref)
+    # a transposed (non-contiguous) first operand
+    at_ = torch.randn([sa[0], sa[2], sa[1]], generator=g).cuda().transpose(1, 2)
+    ref2 = torch.cat([at_, b], dim=2 - dim)
+    out2 = torch.empty_like(ref2)
+    assert L.mmhip_concat(ctypes.byref(mm.view_of(at_)), ctypes.byref(mm.view_of(b)), dim, ptr(out2), st()) == 0
+    assert torch.equal(out2, ref2)
+
+
+def test_concat_rejects_mismatched_shapes(mm):
+    L = mm.load()
+    a = torch.zeros(4, 8, device="cuda")
+    b = torch.zeros(5, 7, device="cuda")
+    out = torch.zeros(64, device="cuda")
+    assert L.mmhip_concat(ctypes.byref(mm.view_of(a)), ctypes.byref(mm.view_of(b)), 0, ptr(out), st()) != 0
+    assert L.mmhip_concat(ctypes.byref(mm.view_of(a)), ctypes.byref(mm.view_of(a)), 4, ptr(out), st()) != 0
+
+
+def test_clamp(mm):
+    """GGML_OP_CLAMP: MAX(MIN(x, hi), lo) with ggml's comparison macros,
+    bit-exact; NaN becomes hi (x < hi is false, then hi > lo)."""
+    L = mm.load()
+
+    def ref(a, lo, hi):
+        t = np.where(a < np.float32(hi), a, np.float32(hi))
+        return np.where(t > np.float32(lo), t, np.float32(lo))
+
+    rng = np.random.default_rng(33)
+    x = (rng.standard_normal((3, 7, 129)) * 10).astype(np.float32)
+    x[0, 0, :5] = [np.inf, -np.inf, 0.0, -0.0, np.nan]
+    tx = torch.from_numpy(x).cuda()
+    out = torch.empty_like(tx)
+    assert L.mmhip_clamp(ctypes.byref(mm.view_of(tx)), -3.5, 2.25, ptr(out), st()) == 0
+    o = out.cpu().numpy()
+    assert np.array_equal(o, ref(x, -3.5, 2.25)) and o[0, 0, 4] == np.float32(2.25)
+    # strided input; then in place on a contiguous tensor
+    tv = tx.transpose(1, 2)
+    o2 = torch.empty(tv.shape, device="cuda")
+    assert L.mmhip_clamp(ctypes.byref(mm.view_of(tv)), -1.0, 1.0, ptr(o2), st()) == 0
+    assert np.array_equal(o2.cpu().numpy(), ref(x.transpose(0, 2, 1), -1.0, 1.0))
+    assert L.mmhip_clamp(ctypes.byref(mm.view_of(tx)), -1.0, 1.0, ptr(tx), st()) == 0
+    assert np.array_equal(tx.cpu().numpy(), ref(x, -1.0, 1.0))
