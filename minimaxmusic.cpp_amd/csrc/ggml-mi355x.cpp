@@ -426,6 +426,16 @@ void be_sync(ggml_backend_t b) {
 
 // Workspace large enough for `need` bytes; returns nullptr when it would have
 // to grow during a capture (the caller then abandons the capture).
+// A captured graph holds the addresses of the workspace and the activation
+// slots: when either moves, the capture is dropped and the graph captured again.
+void drop_captured(mi_backend * c) {
+    if (c->cache.exec) {
+        (void) hipGraphExecDestroy(c->cache.exec);
+        c->cache.exec = nullptr;
+    }
+    c->cache.sig.clear();
+}
+
 void * workspace(mi_backend * c, size_t need) {
     if (need <= c->ws_size) {
         return c->ws;
@@ -436,6 +446,7 @@ void * workspace(mi_backend * c, size_t need) {
     HIP_OK(hipStreamSynchronize(c->stream));
     if (c->ws) {
         (void) hipFree(c->ws);
+        drop_captured(c);
     }
     c->ws      = nullptr;
     c->ws_size = 0;
@@ -1363,6 +1374,7 @@ void * slots(mi_backend * c, size_t need) {
     HIP_OK(hipStreamSynchronize(c->stream));
     if (c->slot) {
         (void) hipFree(c->slot);
+        drop_captured(c);
     }
     c->slot      = nullptr;
     c->slot_size = 0;

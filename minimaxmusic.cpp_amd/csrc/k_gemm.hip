@@ -3,17 +3,16 @@
 //
 //   y[m, n] = sum_k x[m, k] * deq(W)[n, k]
 //
-// Workgroup tile: 256 tokens x 256 weight rows (8 waves, each 128 x 64 with
-// eight v_mfma_f32_32x32x16_f16 accumulators) when the problem has at least
-// 256 such tiles, else 128 x 128 (4 waves, each 64 x 64); K step 64.  Per K step the x tile (f32) is rounded to f16 and the weight
-// tile is dequantised exactly as the GGUF definitions (f32, no contraction)
-// and then rounded to f16; both are stored row-major (k contiguous) in LDS,
-// which is the operand order of the MFMA A (tokens) and B (weight rows)
-// inputs.  The output accumulator layout gives each lane one weight row, so
-// stores of 32 lanes are 128 contiguous bytes of a y row.
-//
-// The next K step's global loads are issued before the current step's MFMAs
-// (register double buffering), so HBM/L2 latency overlaps the matrix work.
+// The activations are first rounded to f16 into a packed copy (workspace):
+// every workgroup along N reads them, so they are converted once and moved at
+// half the bytes.  Workgroup tile: 256 tokens x 256 weight rows (8 waves,
+// each 128 x 64 with eight v_mfma_f32_32x32x16_f16 accumulators) when the
+// problem has at least 256 such tiles, else 128 x 128 (4 waves, each 64 x
+// 64); K step 64.  The weight tile is dequantised exactly as the GGUF
+// definitions (f32, no contraction) and then rounded to f16; both tiles are
+// k-contiguous rows in LDS, the operand order of the MFMA A (tokens) and B
+// (weight rows) inputs.  The output accumulator layout gives each lane one
+// weight row, so stores of 32 lanes are 128 contiguous bytes of a y row.
 #include "mmhip_device.h"
 #include "mmhip_internal.h"
 
@@ -69,74 +68,84 @@ __device__ __forceinline__ void w_load(WRaw & w, const uint8_t * row, int64_t K,
     }
 }
 
-// Dequantise the thread's 32 weights (f32 exact, then f16) into LDS row
-// `wrow` of the tile at K columns [32*half, 32*half+32) (Q8_0) or the column
-// sets given by the format (Q4_K, Q6_K).
+// Byte e of a 16-byte load, as the format's signed / unsigned value.  The
+// bytes are taken from the 32-bit words with shifts at the point of use: a
+// byte-pointer view of the loaded vector makes the compiler unpack it right
+// after the load, which forces the wait for that load before the MFMA work
+// that should hide it.
+__device__ __forceinline__ int byte_s(const int4_t & v, int e) {
+    return (int) (int8_t) (v[e >> 2] >> (8 * (e & 3)));
+}
+
+__device__ __forceinline__ int byte_u(const int4_t & v, int e) {
+    return (v[e >> 2] >> (8 * (e & 3))) & 0xff;
+}
+
+__device__ __forceinline__ int byte_u32(const uint32_t (&w)[4], int e) {
+    return (int) ((w[e >> 2] >> (8 * (e & 3))) & 0xff);
+}
+
+// Dequantise the thread's 32 weights (f32 exact, then f16) into four 16-byte
+// chunks o[0..3] and name the chunk index (0..7) of the 64-wide K step each
+// one belongs to (Q8_0: 4*half + c; Q4_K / Q6_K: low nibbles or first
+// quarter at 2*half + {0,1}, high nibbles or second quarter at 4 + 2*half +
+// {0,1}).
 template <int WT>
-__device__ __forceinline__ void w_store(const WRaw & w, _Float16 * sW, const uint8_t * row, int64_t K, int k0,
-                                        int half) {
+__device__ __forceinline__ void w_dequant(const WRaw & w, const uint8_t * row, int64_t K, int k0, int half,
+                                          half8_t (&o)[4], int (&chunk)[4]) {
 #pragma clang fp contract(off)
     if constexpr (WT == TYPE_Q8_0) {
         const float d = h2f((uint16_t) w.dm);
-        half8_t     o[4];
-        const int8_t * q = (const int8_t *) &w.q0;
-        const int8_t * r = (const int8_t *) &w.q1;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            o[i / 8][i % 8]     = (_Float16) (d * (float) q[i]);
-            o[2 + i / 8][i % 8] = (_Float16) (d * (float) r[i]);
+            o[i / 8][i % 8]     = (_Float16) (d * (float) byte_s(w.q0, i));
+            o[2 + i / 8][i % 8] = (_Float16) (d * (float) byte_s(w.q1, i));
         }
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            *(half8_t *) &sW[32 * half + 8 * j] = o[j];
+            chunk[j] = 4 * half + j;
         }
     } else if constexpr (WT == TYPE_Q4_K) {
         const int c = (k0 & 255) >> 6;
         int       sc_lo, mn_lo, sc_hi, mn_hi;
         q4k_scale_min_w(2 * c, w.s0, w.s1, w.s2, sc_lo, mn_lo);
         q4k_scale_min_w(2 * c + 1, w.s0, w.s1, w.s2, sc_hi, mn_hi);
-        const float     d    = h2f((uint16_t) (w.dm & 0xffff));
-        const float     dmin = h2f((uint16_t) (w.dm >> 16));
-        const float     d1 = d * (float) sc_lo, m1 = dmin * (float) mn_lo;
-        const float     d2 = d * (float) sc_hi, m2 = dmin * (float) mn_hi;
-        const uint8_t * q  = (const uint8_t *) &w.q0;
-        half8_t         lo[2], hi[2];
+        const float d    = h2f((uint16_t) (w.dm & 0xffff));
+        const float dmin = h2f((uint16_t) (w.dm >> 16));
+        const float d1 = d * (float) sc_lo, m1 = dmin * (float) mn_lo;
+        const float d2 = d * (float) sc_hi, m2 = dmin * (float) mn_hi;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            lo[i / 8][i % 8] = (_Float16) (d1 * (float) (q[i] & 15) - m1);
-            hi[i / 8][i % 8] = (_Float16) (d2 * (float) (q[i] >> 4) - m2);
+            const int q         = byte_u(w.q0, i);
+            o[i / 8][i % 8]     = (_Float16) (d1 * (float) (q & 15) - m1);
+            o[2 + i / 8][i % 8] = (_Float16) (d2 * (float) (q >> 4) - m2);
         }
-        // low nibbles: columns 16*half + 0..15; high nibbles: 32 + 16*half + 0..15
-        *(half8_t *) &sW[16 * half]          = lo[0];
-        *(half8_t *) &sW[16 * half + 8]      = lo[1];
-        *(half8_t *) &sW[32 + 16 * half]     = hi[0];
-        *(half8_t *) &sW[32 + 16 * half + 8] = hi[1];
+        chunk[0] = 2 * half;
+        chunk[1] = 2 * half + 1;
+        chunk[2] = 4 + 2 * half;
+        chunk[3] = 4 + 2 * half + 1;
     } else {
         const int       sb = k0 >> 8, hf = (k0 & 255) >> 7, tq = (k0 & 127) >> 5;
         const float     d  = h2f(*(const uint16_t *) (row + K / 2 + K / 4 + K / 16 + 2 * sb));
         const int8_t *  sc = (const int8_t *) (row + K / 2 + K / 4) + sb * 16 + hf * 8;
-        const uint8_t * qa = (const uint8_t *) &w.q0;
-        const uint8_t * qb = (const uint8_t *) &w.q1;
         const uint32_t  qhw[4] = { w.s0, w.s1, w.s2, w.dm };
-        const uint8_t * qh = (const uint8_t *) qhw;
         // element l0 + i of quarter t has scale index 2t + (l0 + i) / 16 = 2t + half
         const float ds0 = d * (float) sc[2 * tq + half];
         const float ds1 = d * (float) sc[2 * (tq + 1) + half];
-        half8_t     o0[2], o1[2];
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const int lo0 = tq == 0 ? (qa[i] & 15) : (qa[i] >> 4);
-            const int lo1 = tq == 0 ? (qb[i] & 15) : (qb[i] >> 4);
-            const int h0  = (qh[i] >> (2 * tq)) & 3;
-            const int h1  = (qh[i] >> (2 * tq + 2)) & 3;
-            o0[i / 8][i % 8] = (_Float16) (ds0 * (float) ((lo0 | (h0 << 4)) - 32));
-            o1[i / 8][i % 8] = (_Float16) (ds1 * (float) ((lo1 | (h1 << 4)) - 32));
+            const int qa = byte_u(w.q0, i), qb = byte_u(w.q1, i), qh = byte_u32(qhw, i);
+            const int lo0 = tq == 0 ? (qa & 15) : (qa >> 4);
+            const int lo1 = tq == 0 ? (qb & 15) : (qb >> 4);
+            const int h0  = (qh >> (2 * tq)) & 3;
+            const int h1  = (qh >> (2 * tq + 2)) & 3;
+            o[i / 8][i % 8]     = (_Float16) (ds0 * (float) ((lo0 | (h0 << 4)) - 32));
+            o[2 + i / 8][i % 8] = (_Float16) (ds1 * (float) ((lo1 | (h1 << 4)) - 32));
         }
-        // quarter t -> columns 0..31, quarter t+1 -> 32..63 of the K step
-        *(half8_t *) &sW[16 * half]          = o0[0];
-        *(half8_t *) &sW[16 * half + 8]      = o0[1];
-        *(half8_t *) &sW[32 + 16 * half]     = o1[0];
-        *(half8_t *) &sW[32 + 16 * half + 8] = o1[1];
+        chunk[0] = 2 * half;
+        chunk[1] = 2 * half + 1;
+        chunk[2] = 4 + 2 * half;
+        chunk[3] = 4 + 2 * half + 1;
     }
 }
 
@@ -147,28 +156,51 @@ __device__ __forceinline__ int64_t gm_xcd_remap(int64_t lin, int64_t total) {
     return lin >= per * 8 ? lin : (lin % 8) * per + lin / 8;
 }
 
-// NW waves; tile BM x BN with BM = BN = 32 * NW (staging: thread t owns row
-// t / 2 of both tiles and half t % 2 of the K step); waves in a WM x (NW/WM)
-// grid, each computing MB x NB blocks of 32 x 32.
+// The activation tile reaches LDS without passing through registers:
+// global_load_lds_dwordx4 writes the 16 bytes of lane l at M0 + 16 l, so one
+// wave instruction fills 1 KB of LDS.  It is issued from inline asm so that
+// the compiler's wait-count bookkeeping (which would wait for every such load
+// before any LDS read it cannot prove disjoint) leaves the prefetch alone; the
+// kernel waits for it explicitly before the barrier that publishes a stage.
+typedef __attribute__((address_space(3))) _Float16 lds_half_t;
+
+__device__ __forceinline__ void dma16(const void * src, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr) : "memory", "m0");
+}
+
+// Tiles in LDS are unpadded rows of 64 halves (8 chunks of 16 bytes) with
+// chunk c of row r stored at chunk c ^ (r & 7): the 32 rows an MFMA operand
+// read touches then spread over all banks.
+__device__ __forceinline__ int swz(int r, int c) {
+    return r * 64 + 8 * (c ^ (r & 7));
+}
+
+// NW waves; tile BT x BT with BT = 32 * NW tokens x weight rows.  Waves in a
+// WM x (NW/WM) grid, each computing MB x NB blocks of 32 x 32.  Per 64-wide K
+// step: the activation tile (f16, from the converted copy) is DMA'd into one
+// of two LDS stages; thread t dequantises half (t % 2) of weight row t / 2
+// into one of two LDS weight buffers.  The next step's DMA and weight loads
+// are issued before the current step's MFMAs, so one step of MFMA work hides
+// their latency; one barrier per step.
 template <int WT, int NW, int WM>
 __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__ W, int64_t N, int64_t K, int64_t rs,
-                                                     const float * __restrict__ x, int64_t ldx, int64_t M,
+                                                     const _Float16 * __restrict__ xh, int64_t M,
                                                      float * __restrict__ y, int64_t ldy, int64_t n_ntiles,
                                                      int64_t n_tiles) {
-    constexpr int BM = 32 * NW;
-    constexpr int BN = 32 * NW;
-    constexpr int WN = NW / WM;
-    constexpr int MB = BM / WM / 32;
-    constexpr int NB = BN / WN / 32;
+    constexpr int BT  = 32 * NW;
+    constexpr int T   = NW * 64;
+    constexpr int WN  = NW / WM;
+    constexpr int MB  = BT / WM / 32;
+    constexpr int NB  = BT / WN / 32;
+    constexpr int XI  = BT * 8 / T;  // DMA instructions per thread per stage
+    constexpr int TIL = BT * 64;     // halves per tile
     extern __shared__ __attribute__((aligned(16))) _Float16 g_lds[];
-    _Float16 * sX = g_lds;
-    _Float16 * sW = g_lds + BM * GM_LS;
+    _Float16 * sX = g_lds;            // 2 stages
+    _Float16 * sW = g_lds + 2 * TIL;  // 2 buffers
 
     const int64_t work = gm_xcd_remap(blockIdx.x, n_tiles);
-    const int64_t nt   = work % n_ntiles;
-    const int64_t mt   = work / n_ntiles;
-    const int64_t m0   = mt * BM;
-    const int64_t n0   = nt * BN;
+    const int64_t m0   = (work / n_ntiles) * BT;
+    const int64_t n0   = (work % n_ntiles) * BT;
     const int     tid  = threadIdx.x;
     const int     wave = tid >> 6;
     const int     lane = tid & 63;
@@ -177,14 +209,37 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
     const int     lq   = lane & 31;
     const int     hh   = lane >> 5;
 
+    // DMA sources: instruction i of wave w fills stage chunks (w XI + i) 64 + lane
+    const int        wave_s = __builtin_amdgcn_readfirstlane(wave);
+    const _Float16 * xsrc[XI];
+#pragma unroll
+    for (int i = 0; i < XI; i++) {
+        const int     c = (wave * XI + i) * 64 + lane, r = c >> 3;
+        const int64_t m = m0 + r < M ? m0 + r : M - 1;  // rows past M: any valid row, never stored
+        xsrc[i]         = xh + m * K + 8 * ((c & 7) ^ (r & 7));
+    }
+    const uint32_t lds_x = (uint32_t) (uintptr_t) (lds_half_t *) sX;
+    auto           dma   = [&](int stage, int k0) {
+#pragma unroll
+        for (int i = 0; i < XI; i++) {
+            dma16(xsrc[i] + k0, lds_x + 2u * (uint32_t) (stage * TIL + (wave_s * XI + i) * 512));
+        }
+    };
+
     const int       srow  = tid >> 1;
     const int       shalf = tid & 1;
-    const int64_t   xm    = m0 + srow;
-    const bool      x_ok  = xm < M;
-    const float *   xrow  = x + (x_ok ? xm : 0) * ldx + shalf * 32;
-    const int64_t   wn_   = n0 + srow;
-    const bool      w_ok  = wn_ < N;
-    const uint8_t * wrow  = W + (w_ok ? wn_ : 0) * rs;
+    const bool      w_ok  = n0 + srow < N;
+    const uint8_t * wrow  = W + (w_ok ? n0 + srow : 0) * rs;
+    WRaw            wr;
+    auto            wstore = [&](int buf, int k0) {
+        half8_t o[4];
+        int     ch[4];
+        w_dequant<WT>(wr, wrow, K, k0, shalf, o, ch);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            *(half8_t *) &sW[buf * TIL + swz(srow, ch[j])] = w_ok ? o[j] : half8_t{};
+        }
+    };
 
     float16_t acc[MB][NB];
 #pragma unroll
@@ -197,56 +252,19 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
             }
         }
     }
-
-    float4_t xr[8];
-    WRaw     wr;
-    auto     load = [&](int k0) {
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            xr[i] = x_ok ? *(const float4_t *) (xrow + k0 + 4 * i) : float4_t{ 0.0f, 0.0f, 0.0f, 0.0f };
-        }
-        w_load<WT>(wr, wrow, K, k0, shalf);
-    };
-
-    load(0);
-    for (int k0 = 0; k0 < K; k0 += GM_BK) {
-        __syncthreads();
-        {
-            half8_t o[4];
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    o[i / 2][(i % 2) * 4 + j] = (_Float16) xr[i][j];
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                *(half8_t *) &sX[srow * GM_LS + shalf * 32 + 8 * j] = o[j];
-            }
-        }
-        if (w_ok) {
-            w_store<WT>(wr, &sW[srow * GM_LS], wrow, K, k0, shalf);
-        } else {
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                *(half8_t *) &sW[srow * GM_LS + shalf * 32 + 8 * j] = half8_t{};
-            }
-        }
-        __syncthreads();
-        if (k0 + GM_BK < K) {
-            load(k0 + GM_BK);
-        }
+    auto compute = [&](int buf) {
+        const _Float16 * bx = sX + buf * TIL;
+        const _Float16 * bw = sW + buf * TIL;
 #pragma unroll
         for (int kk = 0; kk < GM_BK / 16; kk++) {
             half8_t a[MB], b[NB];
 #pragma unroll
             for (int i = 0; i < MB; i++) {
-                a[i] = *(const half8_t *) &sX[(wm * (BM / WM) + i * 32 + lq) * GM_LS + kk * 16 + 8 * hh];
+                a[i] = *(const half8_t *) &bx[swz(wm * (BT / WM) + i * 32 + lq, 2 * kk + hh)];
             }
 #pragma unroll
             for (int j = 0; j < NB; j++) {
-                b[j] = *(const half8_t *) &sW[(wn * (BN / WN) + j * 32 + lq) * GM_LS + kk * 16 + 8 * hh];
+                b[j] = *(const half8_t *) &bw[swz(wn * (BT / WN) + j * 32 + lq, 2 * kk + hh)];
             }
 #pragma unroll
             for (int i = 0; i < MB; i++) {
@@ -256,6 +274,28 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
                 }
             }
         }
+    };
+
+    const int nk = (int) (K / GM_BK);
+    dma(0, 0);
+    w_load<WT>(wr, wrow, K, 0, shalf);
+    wstore(0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int ks = 0; ks < nk; ks++) {
+        const int nxt = (ks + 1) & 1;
+        if (ks + 1 < nk) {
+            dma(nxt, (ks + 1) * GM_BK);
+            __builtin_amdgcn_sched_barrier(0);
+            w_load<WT>(wr, wrow, K, (ks + 1) * GM_BK, shalf);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        compute(ks & 1);
+        if (ks + 1 < nk) {
+            wstore(nxt, (ks + 1) * GM_BK);
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // this thread's DMA and LDS writes
+        __syncthreads();
     }
 
     // C[i = token][j = weight row]: lane holds row j = lq, tokens 8(r/4) + 4hh + r%4
@@ -263,18 +303,36 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
     for (int i = 0; i < MB; i++) {
 #pragma unroll
         for (int j = 0; j < NB; j++) {
-            const int64_t n = n0 + wn * (BN / WN) + j * 32 + lq;
+            const int64_t n = n0 + wn * (BT / WN) + j * 32 + lq;
             if (n >= N) {
                 continue;
             }
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int64_t m = m0 + wm * (BM / WM) + i * 32 + 8 * (r / 4) + 4 * hh + (r % 4);
+                const int64_t m = m0 + wm * (BT / WM) + i * 32 + 8 * (r / 4) + 4 * hh + (r % 4);
                 if (m < M) {
                     y[m * ldy + n] = acc[i][j][r];
                 }
             }
         }
+    }
+}
+
+// Activations f32 -> f16 (round to nearest even), rows of K into a packed
+// [M, K] copy: 8 elements per thread per pass.
+__global__ void k_x_to_f16(const float * __restrict__ x, int64_t ldx, int64_t K, int64_t n8,
+                           _Float16 * __restrict__ xh) {
+    for (int64_t t = blockIdx.x * (int64_t) blockDim.x + threadIdx.x; t < n8; t += (int64_t) gridDim.x * blockDim.x) {
+        const int64_t  e = t * 8, m = e / K, k = e % K;
+        const float4_t a = *(const float4_t *) (x + m * ldx + k);
+        const float4_t b = *(const float4_t *) (x + m * ldx + k + 4);
+        half8_t        o;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            o[j]     = (_Float16) a[j];
+            o[4 + j] = (_Float16) b[j];
+        }
+        *(half8_t *) (xh + e) = o;
     }
 }
 
@@ -290,9 +348,13 @@ bool gemm_supported(int wtype, int64_t N, int64_t K, int64_t rs, const void * W,
     return rs % 16 == 0 && ((uintptr_t) W) % 16 == 0 && ((uintptr_t) x) % 16 == 0 && ldx % 4 == 0;
 }
 
+size_t gemm_workspace(int64_t K, int64_t M) {
+    return (size_t) M * (size_t) K * sizeof(_Float16);
+}
+
 template <int NW, int WM>
-static int launch_gemm(int wtype, const uint8_t * W, int64_t N, int64_t K, int64_t rs, const float * x, int64_t ldx,
-                       int64_t M, float * y, int64_t ldy, hipStream_t stream) {
+static int launch_gemm(int wtype, const uint8_t * W, int64_t N, int64_t K, int64_t rs, const _Float16 * xh, int64_t M,
+                       float * y, int64_t ldy, hipStream_t stream) {
     constexpr int BT   = 32 * NW;
     const int64_t n_nt = (N + BT - 1) / BT;
     const int64_t n_mt = (M + BT - 1) / BT;
@@ -300,13 +362,12 @@ static int launch_gemm(int wtype, const uint8_t * W, int64_t N, int64_t K, int64
     if (n > 0x7fffffff) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat gemm: too many tiles");
     }
-    const size_t lds = (size_t) 2 * BT * GM_LS * sizeof(_Float16);
-    auto go = [&](auto kern) -> int {
+    const size_t lds = (size_t) 4 * BT * 64 * sizeof(_Float16);
+    auto         go  = [&](auto kern) -> int {
         if (lds > 64 * 1024 && !ensure_lds_limit((const void *) kern, lds)) {
             return set_error(MMHIP_ERR_HIP, "mul_mat gemm: cannot raise LDS limit to %zu", lds);
         }
-        hipLaunchKernelGGL(kern, dim3((unsigned) n), dim3(NW * 64), lds, stream, W, N, K, rs, x, ldx, M, y, ldy, n_nt,
-                           n);
+        hipLaunchKernelGGL(kern, dim3((unsigned) n), dim3(NW * 64), lds, stream, W, N, K, rs, xh, M, y, ldy, n_nt, n);
         return check_launch("mul_mat gemm");
     };
     switch (wtype) {
@@ -317,17 +378,29 @@ static int launch_gemm(int wtype, const uint8_t * W, int64_t N, int64_t K, int64
 }
 
 int gemm_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const float * x, int64_t ldx, int64_t M,
-           float * y, int64_t ldy, hipStream_t stream) {
+           float * y, int64_t ldy, void * ws, size_t ws_bytes, hipStream_t stream) {
     if (!gemm_supported(wtype, N, K, rs, W, x, ldx)) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat gemm: type %d N=%lld K=%lld rs=%lld not supported", wtype,
                          (long long) N, (long long) K, (long long) rs);
     }
+    const size_t need = gemm_workspace(K, M);
+    if (!ws || ws_bytes < need || ((uintptr_t) ws) % 16 != 0) {
+        return set_error(MMHIP_ERR_WORKSPACE, "mul_mat gemm: workspace %zu < %zu (16-byte aligned)", ws_bytes, need);
+    }
+    _Float16 *    xh = (_Float16 *) ws;
+    const int64_t n8 = M * K / 8;
+    const int64_t nb = (n8 + 255) / 256;
+    hipLaunchKernelGGL(k_x_to_f16, dim3((unsigned) (nb < 8192 ? nb : 8192)), dim3(256), 0, stream, x, ldx, K, n8, xh);
+    int rc = check_launch("mul_mat gemm: convert");
+    if (rc != MMHIP_OK) {
+        return rc;
+    }
     const uint8_t * wb       = (const uint8_t *) W;
     const int64_t   tiles256 = ((N + 255) / 256) * ((M + 255) / 256);
     if (tiles256 >= 256) {
-        return launch_gemm<8, 2>(wtype, wb, N, K, rs, x, ldx, M, y, ldy, stream);
+        return launch_gemm<8, 2>(wtype, wb, N, K, rs, xh, M, y, ldy, stream);
     }
-    return launch_gemm<4, 2>(wtype, wb, N, K, rs, x, ldx, M, y, ldy, stream);
+    return launch_gemm<4, 2>(wtype, wb, N, K, rs, xh, M, y, ldy, stream);
 }
 
 }  // namespace mmhip

@@ -74,7 +74,7 @@ extern "C" int mmhip_version(void) {
 extern "C" size_t mmhip_mul_mat_workspace(int type, int64_t N, int64_t K, int64_t M) {
     (void) N;
     if (use_gemm(type, M)) {
-        return 0;
+        return gemm_workspace(K, M);
     }
     return act_layout(type, K, M).total;
 }
@@ -92,7 +92,7 @@ extern "C" int mmhip_mul_mat(int type, const void * W, int64_t N, int64_t K, int
     }
     hipStream_t st = (hipStream_t) stream;
     if (use_gemm(type, M)) {
-        return gemm_q(type, W, N, K, w_row_stride, x, ldx, M, y, ldy, st);
+        return gemm_q(type, W, N, K, w_row_stride, x, ldx, M, y, ldy, ws, ws_bytes, st);
     }
     const ActLayout L = act_layout(type, K, M);
     if (L.total == 0 || !gemv_supported(type, N, K, w_row_stride, W)) {

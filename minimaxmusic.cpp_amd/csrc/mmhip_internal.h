@@ -78,9 +78,11 @@ bool gemv_supported(int wtype, int64_t N, int64_t K, int64_t row_stride, const v
 int  gemv_q(int wtype, const void * W, int64_t N, int64_t K, int64_t row_stride, const ActPtrs & x, int64_t M, float * y,
             int64_t ldy, hipStream_t stream, const float * r = nullptr, int64_t ldr = 0);
 
-// MFMA GEMM with in-LDS dequantisation (any M).
-int gemm_q(int wtype, const void * W, int64_t N, int64_t K, int64_t row_stride, const float * x, int64_t ldx, int64_t M,
-           float * y, int64_t ldy, hipStream_t stream);
+// MFMA GEMM with in-LDS dequantisation (any M); the workspace holds the f16
+// copy of the activations (gemm_workspace bytes, 16-byte aligned).
+size_t gemm_workspace(int64_t K, int64_t M);
+int    gemm_q(int wtype, const void * W, int64_t N, int64_t K, int64_t row_stride, const float * x, int64_t ldx,
+              int64_t M, float * y, int64_t ldy, void * ws, size_t ws_bytes, hipStream_t stream);
 
 }  // namespace mmhip
 
