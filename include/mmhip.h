@@ -78,6 +78,13 @@ int mmhip_dequantize_rows(int type, const void * w, int64_t nrows, int64_t ne0, 
 size_t mmhip_mul_mat_workspace(int type, int64_t N, int64_t K, int64_t M);
 int    mmhip_mul_mat(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const float * x, int64_t ldx,
                      int64_t M, float * y, int64_t ldy, void * ws, size_t ws_bytes, void * stream);
+/* MUL_MAT at token counts (M > 8) with the ADDs that follow it fused into the
+ * store: y = (x W^T + bias[n]) + r[m*ldr + n], each ADD rounded as its op;
+ * bias and r may be NULL (r may alias y).  The DiT's projection biases and
+ * residuals (src/dit.h:228-229, :237-245).  Workspace as mmhip_mul_mat. */
+int    mmhip_mul_mat_bias_add(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const float * x,
+                              int64_t ldx, int64_t M, const float * bias, const float * r, int64_t ldr, float * y,
+                              int64_t ldy, void * ws, size_t ws_bytes, void * stream);
 
 /* The two halves of the GEMV path, exposed for fusion and for testing:
  * quantise M activation rows into the layout mmhip_mul_mat_q consumes
@@ -257,6 +264,10 @@ int mmhip_scale(const mmhip_view * a, float s, float bias, float * dst, void * s
  * (dit_layer_norm, src/dit.h:161-167, eps 1e-5); dst contiguous f32 rows.
  * ggml-CPU's steps: mean and variance from double sums. */
 int mmhip_norm(const mmhip_view * x, float eps, float * dst, void * stream);
+/* GGML_OP_NORM followed by the MUL by w[ne0] and the ADD of b[ne0] of
+ * dit_layer_norm (src/dit.h:161-167), fused: dst = (norm(x) * w) + b, each
+ * step rounded as in the three ops; w or b may be NULL. */
+int mmhip_norm_affine(const mmhip_view * x, float eps, const float * w, const float * b, float * dst, void * stream);
 /* GGML_OP_CONCAT of f32 a and b along dim 0..3 (the DiT input channel concat
  * and the timestep token, src/dit.h:262-264, :273); dst contiguous. */
 int mmhip_concat(const mmhip_view * a, const mmhip_view * b, int dim, float * dst, void * stream);

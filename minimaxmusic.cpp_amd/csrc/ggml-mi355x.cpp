@@ -724,7 +724,7 @@ int run_node(mi_backend * c, const struct ggml_tensor * n) {
 //             residual: the ADD is done in the GEMV's store.
 // MUL_MATs reading a slot skip their activation quantisation.
 
-enum step_kind { ST_NODE, ST_NORM, ST_SWIGLU_Q, ST_HEAD, ST_MM, ST_FA_Q };
+enum step_kind { ST_NODE, ST_NORM, ST_SWIGLU_Q, ST_HEAD, ST_MM, ST_FA_Q, ST_GEMM, ST_LN };
 
 struct plan_step {
     int                  kind = ST_NODE;
@@ -736,6 +736,10 @@ struct plan_step {
     int                  norm_mul = -1;  // MM: the MUL by the norm weight (the GEMV's src1)
     int                  glu      = -1;  // MM: the SWIGLU node whose SwiGLU runs in the GEMV's prologue
     int                  glu_epi  = -1;  // MM: the SWIGLU node computed in the (gate_up) GEMV's epilogue
+    int                  mm       = -1;  // GEMM: the MUL_MAT node
+    int                  bias     = -1;  // GEMM: the bias ADD node / LN: the ADD of the LayerNorm bias
+    int                  bias_src = -1;  // index 0/1 of that ADD's vector operand
+    int                  mul      = -1;  // LN: the MUL by the LayerNorm weight
     int64_t              slot_out = -1;  // byte offset of the quantised slot written (NORM / SWIGLU_Q)
     int64_t              slot_in  = -1;  // byte offset of the slot read (MM)
     int                  vec_wtype = 0;  // weight type the slot is quantised for
@@ -769,6 +773,22 @@ int node_index(const graph_info & gi, const struct ggml_tensor * t) {
 }
 
 // Would mmhip_mul_mat run this MUL_MAT as an activation-quantised GEMV?
+// The operand index (0/1) of `add` (an ADD reading n) that is an f32
+// contiguous vector of n->ne[0] elements broadcast over n's rows, else -1.
+int add_row_vector(const struct ggml_tensor * add, const struct ggml_tensor * n) {
+    if (add->op != GGML_OP_ADD && add->op != GGML_OP_MUL) {
+        return -1;
+    }
+    const int oth = add->src[0] == n ? 1 : add->src[1] == n ? 0 : -1;
+    if (oth < 0 || add->src[oth] == n) {
+        return -1;
+    }
+    const struct ggml_tensor * v = add->src[oth];
+    const bool ok = v->type == GGML_TYPE_F32 && ggml_is_contiguous(v) && v->ne[0] == n->ne[0] && v->ne[1] == 1 &&
+                    v->ne[2] == 1 && v->ne[3] == 1 && ggml_are_same_shape(add, n) && add->type == GGML_TYPE_F32;
+    return ok ? oth : -1;
+}
+
 bool mm_is_gemv(const struct ggml_tensor * n) {
     const struct ggml_tensor * x = n->src[1];
     const int64_t              M = x->ne[1] * x->ne[2] * x->ne[3];
@@ -1228,6 +1248,89 @@ graph_plan build_plan(struct ggml_cgraph * g) {
                 continue;
             }
         }
+        // Steps run at their last node: every node in between must be a view or
+        // absorbed, so no other node can reuse a buffer the step still reads.
+        auto quiet_between = [&](int a, int b, int s1, int s2) {
+            for (int t = a + 1; t < b; t++) {
+                if (t != s1 && t != s2 && !is_noop(ggml_graph_node(g, t)->op)) {
+                    return false;
+                }
+            }
+            return true;
+        };
+        // LayerNorm with its weight MUL and bias ADD (dit_layer_norm): one kernel
+        if (n->op == GGML_OP_NORM && gi.uses[(size_t) i] == 1 && !is_output(n) && rows_contiguous_f32(n)) {
+            const int                  j  = gi.cons[(size_t) i];
+            const struct ggml_tensor * m  = ggml_graph_node(g, j);
+            const int                  wi = m->op == GGML_OP_MUL ? add_row_vector(m, n) : -1;
+            if (wi >= 0 && node_index(gi, m->src[wi]) < j && gi.uses[(size_t) j] == 1 && !is_output(m)) {
+                const int                  k  = gi.cons[(size_t) j];
+                const struct ggml_tensor * a  = ggml_graph_node(g, k);
+                const int                  bi = a->op == GGML_OP_ADD ? add_row_vector(a, m) : -1;
+                if (bi >= 0 && node_index(gi, a->src[bi]) < k && ggml_is_contiguous(a) && quiet_between(i, k, j, -1)) {
+                    plan_step st;
+                    st.kind     = ST_LN;
+                    st.node     = k;
+                    st.src      = i;
+                    st.mul      = j;
+                    st.bias     = k;
+                    st.bias_src = bi;
+                    st.add_res  = wi;  // the MUL's weight operand
+                    absorbed[(size_t) i] = 1;
+                    absorbed[(size_t) j] = 1;
+                    absorbed[(size_t) k] = 1;
+                    add_pending(st);
+                    continue;
+                }
+            }
+        }
+        // GEMM with the bias ADD and / or residual ADD that follow it in its store
+        if (n->op == GGML_OP_MUL_MAT && !mm_is_gemv(n) && supports_mul_mat(n) && ggml_is_contiguous(n)) {
+            plan_step st;
+            st.kind  = ST_GEMM;
+            st.node  = i;
+            st.mm    = i;
+            int  cur = i;
+            auto single = [&](int t) { return gi.uses[(size_t) t] == 1 && !is_output(ggml_graph_node(g, t)); };
+            if (single(cur)) {
+                const int                  j  = gi.cons[(size_t) cur];
+                const struct ggml_tensor * ad = ggml_graph_node(g, j);
+                const int                  bi = ad->op == GGML_OP_ADD ? add_row_vector(ad, n) : -1;
+                if (bi >= 0 && node_index(gi, ad->src[bi]) < j && ggml_is_contiguous(ad) && quiet_between(i, j, -1, -1)) {
+                    st.bias     = j;
+                    st.bias_src = bi;
+                    cur         = j;
+                }
+            }
+            if (single(cur)) {
+                const int                  j   = gi.cons[(size_t) cur];
+                const struct ggml_tensor * c_  = ggml_graph_node(g, cur);
+                const struct ggml_tensor * ad  = ggml_graph_node(g, j);
+                const int                  oth = ad->op == GGML_OP_ADD ? (ad->src[0] == c_ ? 1 : ad->src[1] == c_ ? 0 : -1) : -1;
+                if (oth >= 0 && ad->src[oth] != c_) {
+                    const struct ggml_tensor * r = ad->src[oth];
+                    if (r->type == GGML_TYPE_F32 && ggml_are_same_shape(r, n) && ggml_are_same_shape(ad, n) &&
+                        ggml_is_contiguous(ad) && mm_collapsible(r) && node_index(gi, r) < j &&
+                        quiet_between(i, j, st.bias, -1)) {
+                        st.add     = j;
+                        st.add_res = oth;
+                        cur        = j;
+                    }
+                }
+            }
+            if (cur != i) {
+                st.node = cur;
+                absorbed[(size_t) i] = 1;
+                if (st.bias >= 0) {
+                    absorbed[(size_t) st.bias] = 1;
+                }
+                if (st.add >= 0) {
+                    absorbed[(size_t) st.add] = 1;
+                }
+                add_pending(st);
+                continue;
+            }
+        }
         if (n->op == GGML_OP_MUL_MAT && mm_is_gemv(n)) {
             plan_step st;
             st.kind = ST_MM;
@@ -1418,6 +1521,35 @@ int run_step(mi_backend * c, struct ggml_cgraph * g, const plan_step & st, char 
         case ST_HEAD:
             rc = mmhip_head_rows_n(st.head, st.n_head, s);
             break;
+        case ST_LN: {
+            const struct ggml_tensor * nn = ggml_graph_node(g, st.src);
+            const struct ggml_tensor * mu = ggml_graph_node(g, st.mul);
+            float                      eps;
+            memcpy(&eps, &nn->op_params[0], sizeof(float));
+            mmhip_view x = view_of(nn->src[0]);
+            rc = mmhip_norm_affine(&x, eps, (const float *) mu->src[st.add_res]->data,
+                                   (const float *) n->src[st.bias_src]->data, (float *) n->data, s);
+            break;
+        }
+        case ST_GEMM: {
+            const struct ggml_tensor * mm = ggml_graph_node(g, st.mm);
+            const struct ggml_tensor * w  = mm->src[0];
+            const struct ggml_tensor * x  = mm->src[1];
+            const int64_t              N = w->ne[1], K = w->ne[0], M = x->ne[1] * x->ne[2] * x->ne[3];
+            const float *              bias = st.bias >= 0 ? (const float *) ggml_graph_node(g, st.bias)->src[st.bias_src]->data
+                                                           : nullptr;
+            const struct ggml_tensor * r  = st.add >= 0 ? ggml_graph_node(g, st.add)->src[st.add_res] : nullptr;
+            const size_t               ws = mmhip_mul_mat_workspace(w->type, N, K, M);
+            void *                     wp = ws ? workspace(c, ws) : nullptr;
+            if (ws && !wp) {
+                return -1;
+            }
+            rc = mmhip_mul_mat_bias_add(w->type, w->data, N, K, (int64_t) w->nb[1], (const float *) x->data,
+                                        (int64_t) (x->nb[1] / sizeof(float)), M, bias,
+                                        r ? (const float *) r->data : nullptr, r ? (int64_t) (r->nb[1] / sizeof(float)) : 0,
+                                        (float *) n->data, N, wp, ws, s);
+            break;
+        }
         case ST_FA_Q: {
             mmhip_view q = view_of(n->src[0]), k = view_of(n->src[1]), v = view_of(n->src[2]);
             mmhip_view m;

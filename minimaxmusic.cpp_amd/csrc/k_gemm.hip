@@ -185,8 +185,10 @@ __device__ __forceinline__ int swz(int r, int c) {
 template <int WT, int NW, int WM>
 __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__ W, int64_t N, int64_t K, int64_t rs,
                                                      const _Float16 * __restrict__ xh, int64_t M,
-                                                     float * __restrict__ y, int64_t ldy, int64_t n_ntiles,
-                                                     int64_t n_tiles) {
+                                                     const float * __restrict__ bias, const float * res, int64_t ldr,
+                                                     float * y, int64_t ldy,
+                                                     int64_t n_ntiles, int64_t n_tiles) {
+#pragma clang fp contract(off)
     constexpr int BT  = 32 * NW;
     constexpr int T   = NW * 64;
     constexpr int WN  = NW / WM;
@@ -298,7 +300,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
         __syncthreads();
     }
 
-    // C[i = token][j = weight row]: lane holds row j = lq, tokens 8(r/4) + 4hh + r%4
+    // C[i = token][j = weight row]: lane holds row j = lq, tokens 8(r/4) + 4hh + r%4.
+    // Epilogue: the bias ADD, then the residual ADD, each rounded as its op.
 #pragma unroll
     for (int i = 0; i < MB; i++) {
 #pragma unroll
@@ -307,11 +310,19 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
             if (n >= N) {
                 continue;
             }
+            const float bn = bias ? bias[n] : 0.0f;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int64_t m = m0 + wm * (BT / WM) + i * 32 + 8 * (r / 4) + 4 * hh + (r % 4);
                 if (m < M) {
-                    y[m * ldy + n] = acc[i][j][r];
+                    float v = acc[i][j][r];
+                    if (bias) {
+                        v = v + bn;
+                    }
+                    if (res) {
+                        v = res[m * ldr + n] + v;
+                    }
+                    y[m * ldy + n] = v;
                 }
             }
         }
@@ -354,7 +365,7 @@ size_t gemm_workspace(int64_t K, int64_t M) {
 
 template <int NW, int WM>
 static int launch_gemm(int wtype, const uint8_t * W, int64_t N, int64_t K, int64_t rs, const _Float16 * xh, int64_t M,
-                       float * y, int64_t ldy, hipStream_t stream) {
+                       const float * bias, const float * res, int64_t ldr, float * y, int64_t ldy, hipStream_t stream) {
     constexpr int BT   = 32 * NW;
     const int64_t n_nt = (N + BT - 1) / BT;
     const int64_t n_mt = (M + BT - 1) / BT;
@@ -367,7 +378,8 @@ static int launch_gemm(int wtype, const uint8_t * W, int64_t N, int64_t K, int64
         if (lds > 64 * 1024 && !ensure_lds_limit((const void *) kern, lds)) {
             return set_error(MMHIP_ERR_HIP, "mul_mat gemm: cannot raise LDS limit to %zu", lds);
         }
-        hipLaunchKernelGGL(kern, dim3((unsigned) n), dim3(NW * 64), lds, stream, W, N, K, rs, xh, M, y, ldy, n_nt, n);
+        hipLaunchKernelGGL(kern, dim3((unsigned) n), dim3(NW * 64), lds, stream, W, N, K, rs, xh, M, bias, res, ldr, y,
+                           ldy, n_nt, n);
         return check_launch("mul_mat gemm");
     };
     switch (wtype) {
@@ -378,7 +390,8 @@ static int launch_gemm(int wtype, const uint8_t * W, int64_t N, int64_t K, int64
 }
 
 int gemm_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const float * x, int64_t ldx, int64_t M,
-           float * y, int64_t ldy, void * ws, size_t ws_bytes, hipStream_t stream) {
+           float * y, int64_t ldy, void * ws, size_t ws_bytes, hipStream_t stream, const float * bias,
+           const float * res, int64_t ldr) {
     if (!gemm_supported(wtype, N, K, rs, W, x, ldx)) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat gemm: type %d N=%lld K=%lld rs=%lld not supported", wtype,
                          (long long) N, (long long) K, (long long) rs);
@@ -398,9 +411,9 @@ int gemm_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const fl
     const uint8_t * wb       = (const uint8_t *) W;
     const int64_t   tiles256 = ((N + 255) / 256) * ((M + 255) / 256);
     if (tiles256 >= 256) {
-        return launch_gemm<8, 2>(wtype, wb, N, K, rs, xh, M, y, ldy, stream);
+        return launch_gemm<8, 2>(wtype, wb, N, K, rs, xh, M, bias, res, ldr, y, ldy, stream);
     }
-    return launch_gemm<4, 2>(wtype, wb, N, K, rs, xh, M, y, ldy, stream);
+    return launch_gemm<4, 2>(wtype, wb, N, K, rs, xh, M, bias, res, ldr, y, ldy, stream);
 }
 
 }  // namespace mmhip

@@ -279,8 +279,11 @@ __global__ __launch_bounds__(256) void k_rms_norm(TV x, TV w, int has_w, float e
 
 // GGML_OP_NORM (LayerNorm without affine part, src/dit.h:161-167): one
 // workgroup per row, ggml-CPU's steps -- mean from a double sum, y = x - mean,
-// variance from the double sum of y^2, y *= 1 / sqrtf(variance + eps).
-__global__ __launch_bounds__(256) void k_layer_norm(TV x, float eps, float * __restrict__ dst) {
+// variance from the double sum of y^2, y *= 1 / sqrtf(variance + eps).  With
+// w / b it also applies the MUL and ADD that follow it (dit_layer_norm),
+// each rounded as its own op: (y * w[i]) + b[i].
+__global__ __launch_bounds__(256) void k_layer_norm(TV x, float eps, const float * __restrict__ w,
+                                                     const float * __restrict__ b, float * __restrict__ dst) {
 #pragma clang fp contract(off)
     __shared__ double s_part[4];
     const int64_t     row = blockIdx.x;
@@ -313,7 +316,14 @@ __global__ __launch_bounds__(256) void k_layer_norm(TV x, float eps, float * __r
     const float var = (float) ((s_part[0] + s_part[1] + s_part[2] + s_part[3]) / (double) n);
     const float sc  = 1.0f / sqrtf(var + eps);
     for (int64_t i = threadIdx.x; i < n; i += 256) {
-        dr[i] = dr[i] * sc;  // each thread rescales the elements it wrote
+        float t = dr[i] * sc;  // each thread rescales the elements it wrote
+        if (w) {
+            t = t * w[i];
+        }
+        if (b) {
+            t = t + b[i];
+        }
+        dr[i] = t;
     }
 }
 
@@ -501,6 +511,33 @@ __global__ void k_cpy_linear(const char * __restrict__ src, int st, char * __res
             ((float *) dst)[i] = v;
         } else {
             ((uint16_t *) dst)[i] = f2h(v);
+        }
+    }
+}
+
+// Rows of ne0 contiguous source elements into a contiguous destination:
+// thread t converts elements 4j .. 4j+3 of row r = t / (ne0/4), with the row's
+// indices taken once per 4 elements and 16- / 8-byte accesses.
+__global__ void k_cpy_rows4(TV src, int st, char * __restrict__ dst, int dt, int64_t n4, int64_t q) {
+    for (int64_t t = blockIdx.x * (int64_t) blockDim.x + threadIdx.x; t < n4; t += (int64_t) gridDim.x * blockDim.x) {
+        const int64_t r = t / q, j = t % q;
+        const int64_t i1 = r % src.ne[1], i2 = (r / src.ne[1]) % src.ne[2], i3 = r / (src.ne[1] * src.ne[2]);
+        const char *  sp = at(src, 4 * j, i1, i2, i3);
+        float4_t      v;
+        if (st == TYPE_F32) {
+            v = *(const float4_t *) sp;
+        } else {
+            const uint2 h = *(const uint2 *) sp;
+            v = float4_t{ h2f((uint16_t) (h.x & 0xffff)), h2f((uint16_t) (h.x >> 16)), h2f((uint16_t) (h.y & 0xffff)),
+                          h2f((uint16_t) (h.y >> 16)) };
+        }
+        if (dt == TYPE_F32) {
+            *(float4_t *) (dst + 16 * t) = v;
+        } else {
+            uint2 h;
+            h.x = (uint32_t) f2h(v[0]) | ((uint32_t) f2h(v[1]) << 16);
+            h.y = (uint32_t) f2h(v[2]) | ((uint32_t) f2h(v[3]) << 16);
+            *(uint2 *) (dst + 8 * t) = h;
         }
     }
 }
@@ -852,6 +889,15 @@ extern "C" int mmhip_cpy(const mmhip_view * src, int src_type, const mmhip_view 
                            (const char *) src->data, src_type, (char *) dst->data, dst_type, (uint32_t) n);
         return check_launch("cpy");
     }
+    // inner rows contiguous, destination contiguous (element i of the source's
+    // row-major order lands at dst[i] whatever dst's shape), 4-element aligned
+    const int64_t sal = 4 * ss;
+    if (src->nb[0] == ss && is_contig(dst, ds) && src->ne[0] % 4 == 0 && ((uintptr_t) src->data) % sal == 0 &&
+        src->nb[1] % sal == 0 && src->nb[2] % sal == 0 && src->nb[3] % sal == 0 && ((uintptr_t) dst->data) % (4 * ds) == 0) {
+        hipLaunchKernelGGL(k_cpy_rows4, dim3(grid_for(n / 4, 256)), dim3(256), 0, (hipStream_t) stream, tv(src), src_type,
+                           (char *) dst->data, dst_type, n / 4, src->ne[0] / 4);
+        return check_launch("cpy");
+    }
     hipLaunchKernelGGL(k_cpy, dim3(grid_for(n, 256)), dim3(256), 0, (hipStream_t) stream, tv(src), src_type, tv(dst),
                        dst_type, n);
     return check_launch("cpy");
@@ -910,6 +956,11 @@ extern "C" int mmhip_swiglu(const mmhip_view * a, const mmhip_view * b, int swap
 }
 
 extern "C" int mmhip_norm(const mmhip_view * x, float eps, float * dst, void * stream) {
+    return mmhip_norm_affine(x, eps, nullptr, nullptr, dst, stream);
+}
+
+extern "C" int mmhip_norm_affine(const mmhip_view * x, float eps, const float * w, const float * b, float * dst,
+                                 void * stream) {
     MMHIP_API_BEGIN();
     if (!x || !dst || x->ne[0] <= 0) {
         return set_error(MMHIP_ERR_INVALID, "norm: bad arguments");
@@ -921,7 +972,7 @@ extern "C" int mmhip_norm(const mmhip_view * x, float eps, float * dst, void * s
     if (rows >= ((int64_t) 1 << 31) || nel(x) >= ((int64_t) 1 << 31)) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "norm: too many elements");
     }
-    hipLaunchKernelGGL(k_layer_norm, dim3((unsigned) rows), dim3(256), 0, (hipStream_t) stream, tv(x), eps, dst);
+    hipLaunchKernelGGL(k_layer_norm, dim3((unsigned) rows), dim3(256), 0, (hipStream_t) stream, tv(x), eps, w, b, dst);
     return check_launch("norm");
 }
 

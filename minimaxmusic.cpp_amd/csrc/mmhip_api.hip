@@ -109,6 +109,24 @@ extern "C" int mmhip_mul_mat(int type, const void * W, int64_t N, int64_t K, int
     return gemv_q(type, W, N, K, w_row_stride, ActPtrs::from(L, ws), M, y, ldy, st);
 }
 
+extern "C" int mmhip_mul_mat_bias_add(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride,
+                                      const float * x, int64_t ldx, int64_t M, const float * bias, const float * r,
+                                      int64_t ldr, float * y, int64_t ldy, void * ws, size_t ws_bytes, void * stream) {
+    MMHIP_API_BEGIN();
+    if (!W || !x || !y || N <= 0 || K <= 0 || M <= 0 || ldx < K || ldy < N || (r && ldr < N)) {
+        return set_error(MMHIP_ERR_INVALID, "mul_mat_bias_add: bad arguments N=%lld K=%lld M=%lld", (long long) N,
+                         (long long) K, (long long) M);
+    }
+    if (!is_repacked_type(type)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat_bias_add: weight type %d", type);
+    }
+    if (!use_gemm(type, M)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat_bias_add: token count %lld takes the GEMV path",
+                         (long long) M);
+    }
+    return gemm_q(type, W, N, K, w_row_stride, x, ldx, M, y, ldy, ws, ws_bytes, (hipStream_t) stream, bias, r, ldr);
+}
+
 // ---------------------------------------------------------------------
 // FLASH_ATTN_EXT
 

@@ -81,8 +81,10 @@ int  gemv_q(int wtype, const void * W, int64_t N, int64_t K, int64_t row_stride,
 // MFMA GEMM with in-LDS dequantisation (any M); the workspace holds the f16
 // copy of the activations (gemm_workspace bytes, 16-byte aligned).
 size_t gemm_workspace(int64_t K, int64_t M);
+// The epilogue adds bias[n] (if given), then res[m * ldr + n] (if given).
 int    gemm_q(int wtype, const void * W, int64_t N, int64_t K, int64_t row_stride, const float * x, int64_t ldx,
-              int64_t M, float * y, int64_t ldy, void * ws, size_t ws_bytes, hipStream_t stream);
+              int64_t M, float * y, int64_t ldy, void * ws, size_t ws_bytes, hipStream_t stream,
+              const float * bias = nullptr, const float * res = nullptr, int64_t ldr = 0);
 
 }  // namespace mmhip
 

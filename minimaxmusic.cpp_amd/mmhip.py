@@ -60,6 +60,8 @@ SIGNATURES = {
     "mmhip_dequantize_rows": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _vp]),
     "mmhip_mul_mat_workspace": (_sz, [_i32, _i64, _i64, _i64]),
     "mmhip_mul_mat": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _sz, _vp]),
+    "mmhip_mul_mat_bias_add": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _vp,
+                                      _sz, _vp]),
     "mmhip_act_bytes": (_sz, [_i32, _i64, _i64]),
     "mmhip_quantize_act": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _vp]),
     "mmhip_mul_mat_q": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp]),
@@ -91,6 +93,7 @@ SIGNATURES = {
     "mmhip_swiglu": (_i32, [_VP, _VP, _i32, _vp, _vp]),
     "mmhip_scale": (_i32, [_VP, _f32, _f32, _vp, _vp]),
     "mmhip_norm": (_i32, [_VP, _f32, _vp, _vp]),
+    "mmhip_norm_affine": (_i32, [_VP, _f32, _vp, _vp, _vp, _vp]),
     "mmhip_concat": (_i32, [_VP, _VP, _i32, _vp, _vp]),
     "mmhip_clamp": (_i32, [_VP, _f32, _f32, _vp, _vp]),
     # include/mmhip_synth.h

@@ -634,3 +634,44 @@ def test_clamp(mm):
     assert np.array_equal(o2.cpu().numpy(), ref(x.transpose(0, 2, 1), -1.0, 1.0))
     assert L.mmhip_clamp(ctypes.byref(mm.view_of(tx)), -1.0, 1.0, ptr(tx), st()) == 0
     assert np.array_equal(tx.cpu().numpy(), ref(x, -1.0, 1.0))
+
+
+def test_norm_affine_equals_three_ops(mm, orc):
+    """mmhip_norm_affine (dit_layer_norm fused) is bit-identical to
+    mmhip_norm followed by the MUL by w and the ADD of b in f32."""
+    L = mm.load()
+    rng = np.random.default_rng(34)
+    x = (rng.standard_normal((5, 2048)) * 3 + 1).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(2048)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(2048)).astype(np.float32)
+    tx, tw, tb = (torch.from_numpy(a).cuda() for a in (x, w, b))
+    n = torch.empty_like(tx)
+    assert L.mmhip_norm(ctypes.byref(mm.view_of(tx)), 1e-5, ptr(n), st()) == 0
+    out = torch.empty_like(tx)
+    assert L.mmhip_norm_affine(ctypes.byref(mm.view_of(tx)), 1e-5, ptr(tw), ptr(tb), ptr(out), st()) == 0
+    assert torch.equal(out, n * tw + tb)
+    assert rel_err(out.cpu().numpy(), orc.layer_norm(x, 1e-5) * w + b) < 1e-5
+
+
+@pytest.mark.parametrize("case", ["dit_kv_cast", "f16_to_f32", "odd_inner", "misaligned"])
+def test_cpy_row_paths(mm, case):
+    """CPY / CONT over views with contiguous inner rows (the DiT's K/V cast of
+    the permuted projections, src/dit.h:219-220, and the value / gate conts,
+    :239-241): bit-exact against torch, including the generic fallback cases
+    (inner size not a multiple of 4, misaligned start)."""
+    L = mm.load()
+    g = torch.Generator().manual_seed(35)
+    if case == "dit_kv_cast":
+        k = torch.randn((2, 37, 32, 64), generator=g).cuda()      # [B, S, H, D]
+        src, dt = k.permute(0, 2, 1, 3), torch.float16            # [B, H, S, D] view
+    elif case == "f16_to_f32":
+        src, dt = torch.randn((5, 6, 128), generator=g).half().cuda().transpose(0, 1), torch.float32
+    elif case == "odd_inner":
+        src, dt = torch.randn((7, 9, 30), generator=g).cuda().transpose(0, 1), torch.float16
+    else:
+        src, dt = torch.randn((4, 6, 65), generator=g).cuda()[:, :, 1:], torch.float32
+    dst = torch.empty(src.shape, dtype=dt, device="cuda")
+    stype = 0 if src.dtype == torch.float32 else 1
+    dtype_ = 0 if dt == torch.float32 else 1
+    assert L.mmhip_cpy(ctypes.byref(mm.view_of(src)), stype, ctypes.byref(mm.view_of(dst)), dtype_, st()) == 0
+    assert torch.equal(dst, src.to(dt))

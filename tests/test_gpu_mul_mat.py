@@ -105,3 +105,42 @@ def test_gemm_matches_gemv_semantics_closely(mm, pkg):
     a = mm.mul_mat(W, x[:8].contiguous()).cpu().numpy()
     b = mm.mul_mat(W, x).cpu().numpy()[:8]
     assert cosine(a, b) > 0.9999
+
+
+@pytest.mark.parametrize("t", [8, 12, 14])
+@pytest.mark.parametrize("bias,res", [(True, False), (False, True), (True, True)])
+def test_gemm_bias_add_equals_separate_ops(mm, pkg, t, bias, res):
+    """mmhip_mul_mat_bias_add (the DiT's projection + bias, + residual) is
+    bit-identical to mmhip_mul_mat followed by the two ADDs in f32; the
+    residual may be the output buffer itself."""
+    import ctypes
+
+    N, K, M = 300, 2048, 77  # Q6_K rows of 2048 are 16-byte multiples (GEMM loads)
+    raw = pkg.synth.gguf_blocks_np(t, N, K, 4100 + t)
+    W = mm.QuantWeight.from_gguf(t, raw, N, K)
+    x = torch.from_numpy(pkg.synth.normal_np((M, K), 4200 + t)).cuda()
+    b = torch.randn(N, device="cuda") if bias else None
+    r = torch.randn(M, N, device="cuda") if res else None
+    y0 = mm.mul_mat(W, x)
+    ref = y0 + b if bias else y0
+    ref = r + ref if res else ref
+    L = mm.load()
+    need = L.mmhip_mul_mat_workspace(t, N, K, M)
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    P = lambda a: ctypes.c_void_p(a.data_ptr()) if a is not None else None
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    out = r.clone() if res else torch.empty(M, N, device="cuda")
+    rc = L.mmhip_mul_mat_bias_add(t, P(W.data), N, K, W.row_bytes, P(x), K, M, P(b), P(out) if res else None,
+                                  N, P(out), N, P(ws), need, st)
+    assert rc == 0, L.mmhip_last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+
+
+def test_gemm_bias_add_rejects_gemv_token_counts(mm):
+    import ctypes
+
+    L = mm.load()
+    d = torch.zeros(1 << 16, device="cuda")
+    P = ctypes.c_void_p(d.data_ptr())
+    assert L.mmhip_mul_mat_bias_add(8, P, 64, 256, 272, P, 256, 8, P, None, 0, P, 64, P, 1 << 18, None) != 0
