@@ -50,7 +50,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="lm_decode",
-                    choices=["lm_decode", "gemv_q8_0", "fa_decode", "fa_prefill", "fa_dit", "gemm_q4_k"])
+                    choices=["lm_decode", "gemv_q8_0", "fa_decode", "fa_prefill", "fa_dit", "gemm_q4_k",
+                             "dit_block"])
     ap.add_argument("--wtype", default="q8_0", choices=["q8_0", "q6_k"], help="lm_decode weight type")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -536,6 +537,132 @@ def bench_gemm(args, torch, pkg):
     }
 
 
+def dit_block_flops(S, B, dim=2048, ff=8192, heads=32, hd=64):
+    """FLOPs of one DiT block: the six projections (q, k, v, o, ff_in emitting
+    2 ff, ff_out) and bidirectional attention (QK^T and PV)."""
+    M = S * B
+    return 2.0 * M * (4 * dim * dim + dim * 2 * ff + ff * dim) + 4.0 * B * heads * S * S * hd
+
+
+def cpu_dit_block(oracle, dg, w, x, pos):
+    """One DiT block (src/dit.h:183-247) composed from the oracle's
+    ggml-CPU-semantics restatements; x [B, S, dim] f32."""
+    B, S, dim = x.shape
+    H, D, ff = dg.N_HEADS, dg.HEAD_DIM, dg.FF_INNER
+    Q8 = 8
+
+    def mm(name, a, n_out):
+        return oracle.mul_mat_ggml(Q8, w[name], n_out, a.shape[-1], a.reshape(-1, a.shape[-1])).reshape(B, S, n_out)
+
+    def ln(a, g_, b_):
+        return oracle.layer_norm(a, dg.LN_EPS) * g_ + b_
+
+    h = ln(x, w["norm1_w"], w["norm1_b"])
+    q, k, v = (mm(n, h, dim).reshape(B * S, H, D) for n in ("wq", "wk", "wv"))
+    pos_b = np.tile(pos, B)
+    q = oracle.rope_neox(q, pos_b, dg.ROTARY_DIM, dg.ROPE_BASE).reshape(B, S, H, D).transpose(0, 2, 1, 3)
+    k = oracle.rope_neox(k, pos_b, dg.ROTARY_DIM, dg.ROPE_BASE).reshape(B, S, H, D).transpose(0, 2, 1, 3)
+    v = v.reshape(B, S, H, D).transpose(0, 2, 1, 3)
+    a = oracle.flash_attn_ext(np.ascontiguousarray(q), np.ascontiguousarray(k).astype(np.float16),
+                              np.ascontiguousarray(v).astype(np.float16), None, float(np.float32(1 / np.sqrt(D))))
+    x = x + mm("wo", a.reshape(B, S, H * D), dim)
+    h = ln(x, w["norm2_w"], w["norm2_b"])
+    f = mm("ff_in_w", h, 2 * ff) + w["ff_in_b"]
+    act = oracle.swiglu(np.concatenate([f[..., ff:], f[..., :ff]], axis=-1))
+    return x + (mm("ff_out_w", act, dim) + w["ff_out_b"])
+
+
+def bench_dit_block(args, torch, pkg):
+    """The DiT block (src/dit.h:183-247) at the model's shape, S = 690 tokens
+    (T = 689 latent frames + the timestep token), CFG B = 2, Q8_0 weights:
+    a graph of NB chained blocks (distinct weights) through
+    ggml_backend_graph_compute on the MI355X backend, HIP-graph replay."""
+    import importlib
+
+    import oracle
+
+    og_mod = importlib.import_module(pkg.__name__ + ".opgraph")
+    dg = importlib.import_module(pkg.__name__ + ".ditgraph")
+    mm = pkg.mmhip
+    S, B, NB = 690, 2, 4
+    ws = [dg.synth_block(3000 + i) for i in range(NB)]
+    x0 = np.random.default_rng(3100).standard_normal((B, S, dg.DIM)).astype(np.float32)
+    pos = np.arange(S, dtype=np.int32)
+    g = og_mod.OpGraph(n_tensors=64 * NB)
+    try:
+        blks = [dg.Block(g) for _ in range(NB)]
+        tx = g.tensor(og_mod.F32, [dg.DIM, S, B])
+        tp = g.tensor(26, [S])  # GGML_TYPE_I32
+        out = tx
+        for b in blks:
+            out = dg.build_block(g, b, out, tp, S, B)
+        g.build([out])
+        for b, w in zip(blks, ws):
+            b.upload(g, w)
+        g.set(tx, x0)
+        g.set(tp, pos)
+        for _ in range(args.warmup + 2):
+            g.compute()
+        g.synchronize()
+        g.gpu_time(reset=True)
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            g.compute()
+        g.synchronize()
+        wall = (time.perf_counter() - t0) / args.steps
+        gms, n = g.gpu_time()
+        replays, eager = g.graph_stats()
+    finally:
+        g.close()
+    us_block = gms / max(n, 1) * 1e3 / NB
+    flops = dit_block_flops(S, B)
+    # dominant kernel: the ff_in projection with its bias (2048 -> 16384, 1380 tokens), C-ABI, graph replay
+    M, N, K = S * B, 2 * dg.FF_INNER, dg.DIM
+    W = mm.QuantWeight.from_gguf(mm.Q8_0, ws[0]["ff_in_w"], N, K)
+    xs = torch.randn((M, K), device="cuda")
+    bias = torch.from_numpy(ws[0]["ff_in_b"]).cuda()
+    y = torch.empty((M, N), device="cuda")
+    L = mm.load()
+    ws_n = L.mmhip_mul_mat_workspace(mm.Q8_0, N, K, M)
+    wsb = torch.empty(ws_n, dtype=torch.uint8, device="cuda")
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+
+    def step(i, s):
+        rc = L.mmhip_mul_mat_bias_add(mm.Q8_0, P(W.data), N, K, W.row_bytes, P(xs), K, M, P(bias), None, 0, P(y), N,
+                                      P(wsb), ws_n, s)
+        assert rc == 0, L.mmhip_last_error()
+
+    avg_s, min_s = graph_time(torch, step, 10)
+    gf = 2.0 * M * N * K
+    tf = gf / avg_s / 1e12
+    cpu = None
+    if not args.no_cpu:
+        Sc = 32
+        xc = x0[:, :Sc].copy()
+        dt, it = cpu_rate(lambda: cpu_dit_block(oracle, dg, ws[0], xc, np.arange(Sc, dtype=np.int32)), args.cpu_seconds)
+        cpu = {"value": round(dit_block_flops(Sc, B) / dt / 1e12, 5), "unit": "TFLOP/s",
+               "cores": oracle.default_threads(), "kind": "port",
+               "sample": f"one DiT block from the oracle's ggml-CPU-semantics restatements (Q8_0 mul_mat, LayerNorm, "
+                         f"NeoX RoPE, flash_attn_ext, SwiGLU): S={Sc} tokens x B={B}, {it} reps"}
+    return {
+        "metric": "DiT block TFLOP/s (S=690 tokens, CFG B=2, Q8_0, dim 2048, 32x64 heads, FF 8192)",
+        "value": round(flops / (us_block * 1e-6) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "ms_per_step": round(us_block * 1e-3, 4),
+        "dtype": "f16 MFMA (Q8_0 dequantised to f16), f32 glue",
+        "config": {"workload": f"DiT block x{NB} chained through ggml_backend_graph_compute, S={S}, B={B}, Q8_0"},
+        "via_backend": {"path": "ggml_backend_graph_compute, MI355X backend, HIP-graph replay", "blocks_per_graph": NB,
+                        "gpu_us_per_block": round(us_block, 2), "wall_us_per_block": round(wall * 1e6 / NB, 2),
+                        "replays": replays, "eager": eager},
+        "roofline": {"bound": "mfma", "kernel": "k_x_to_f16 + k_gemm_q<Q8_0> + bias (ff_in 2048->16384, 1380 tokens)",
+                     "achieved": round(tf, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tf / MFMA_PEAK_TFLOPS, 4), "avg_launch_us": round(avg_s * 1e6, 2),
+                     "min_launch_us": round(min_s * 1e6, 2), "alg_flops_per_launch": gf,
+                     "traffic": profile_traffic("dit_block_s690_b2_q8_0")},
+        "cpu_baseline": cpu,
+    }
+
+
 # Algorithmic HBM bytes of one Qwen3-8B-shape CFG decode step at KV 4096:
 # weights + KV read + norm weights + logits + KV write (per step, both rows).
 def lm_step_bytes(cfg, wtype):
@@ -716,6 +843,7 @@ def main():
         "fa_prefill": lambda: bench_fa_mfma(args, torch, pkg, True),
         "fa_dit": lambda: bench_fa_mfma(args, torch, pkg, False),
         "gemm_q4_k": lambda: bench_gemm(args, torch, pkg),
+        "dit_block": lambda: bench_dit_block(args, torch, pkg),
     }[args.workload]()
     line = {
         "metric": res["metric"],

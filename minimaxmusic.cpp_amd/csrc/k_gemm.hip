@@ -171,8 +171,9 @@ __device__ __forceinline__ void dma16(const void * src, uint32_t lds_addr) {
 // Tiles in LDS are unpadded rows of 64 halves (8 chunks of 16 bytes) with
 // chunk c of row r stored at chunk c ^ (r & 7): the 32 rows an MFMA operand
 // read touches then spread over all banks.
+template <int BK>
 __device__ __forceinline__ int swz(int r, int c) {
-    return r * 64 + 8 * (c ^ (r & 7));
+    return r * BK + 8 * (c ^ (r & 7));
 }
 
 // NW waves; tile BT x BT with BT = 32 * NW tokens x weight rows.  Waves in a
@@ -182,7 +183,7 @@ __device__ __forceinline__ int swz(int r, int c) {
 // into one of two LDS weight buffers.  The next step's DMA and weight loads
 // are issued before the current step's MFMAs, so one step of MFMA work hides
 // their latency; one barrier per step.
-template <int WT, int NW, int WM>
+template <int WT, int NW, int WM, int BK>
 __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__ W, int64_t N, int64_t K, int64_t rs,
                                                      const _Float16 * __restrict__ xh, int64_t M,
                                                      const float * __restrict__ bias, const float * res, int64_t ldr,
@@ -194,15 +195,22 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
     constexpr int WN  = NW / WM;
     constexpr int MB  = BT / WM / 32;
     constexpr int NB  = BT / WN / 32;
-    constexpr int XI  = BT * 8 / T;  // DMA instructions per thread per stage
-    constexpr int TIL = BT * 64;     // halves per tile
+    constexpr int CPR = BK / 8;        // 16-byte chunks per tile row
+    constexpr int SUB = BK / GM_BK;    // 64-wide weight sub-steps per K step
+    constexpr int XI  = BT * CPR / T;  // DMA instructions per thread per stage
+    constexpr int TIL = BT * BK;       // halves per tile
     extern __shared__ __attribute__((aligned(16))) _Float16 g_lds[];
     _Float16 * sX = g_lds;            // 2 stages
     _Float16 * sW = g_lds + 2 * TIL;  // 2 buffers
 
-    const int64_t work = gm_xcd_remap(blockIdx.x, n_tiles);
-    const int64_t m0   = (work / n_ntiles) * BT;
-    const int64_t n0   = (work % n_ntiles) * BT;
+    // consecutive work items (one XCD, one L2) share the operand that is
+    // re-read most: the weight tile when there are more weight tiles than
+    // token tiles (m_fast), else the activation tile
+    const int64_t work    = gm_xcd_remap(blockIdx.x, n_tiles);
+    const int64_t n_mt    = n_tiles / n_ntiles;
+    const bool    m_fast  = n_ntiles > n_mt;
+    const int64_t m0      = (m_fast ? work % n_mt : work / n_ntiles) * BT;
+    const int64_t n0      = (m_fast ? work / n_mt : work % n_ntiles) * BT;
     const int     tid  = threadIdx.x;
     const int     wave = tid >> 6;
     const int     lane = tid & 63;
@@ -216,9 +224,9 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
     const _Float16 * xsrc[XI];
 #pragma unroll
     for (int i = 0; i < XI; i++) {
-        const int     c = (wave * XI + i) * 64 + lane, r = c >> 3;
+        const int     c = (wave * XI + i) * 64 + lane, r = c / CPR;
         const int64_t m = m0 + r < M ? m0 + r : M - 1;  // rows past M: any valid row, never stored
-        xsrc[i]         = xh + m * K + 8 * ((c & 7) ^ (r & 7));
+        xsrc[i]         = xh + m * K + 8 * ((c % CPR) ^ (r & 7));
     }
     const uint32_t lds_x = (uint32_t) (uintptr_t) (lds_half_t *) sX;
     auto           dma   = [&](int stage, int k0) {
@@ -232,14 +240,23 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
     const int       shalf = tid & 1;
     const bool      w_ok  = n0 + srow < N;
     const uint8_t * wrow  = W + (w_ok ? n0 + srow : 0) * rs;
-    WRaw            wr;
-    auto            wstore = [&](int buf, int k0) {
-        half8_t o[4];
-        int     ch[4];
-        w_dequant<WT>(wr, wrow, K, k0, shalf, o, ch);
+    WRaw            wr[SUB];
+    auto            wload = [&](int k0) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            *(half8_t *) &sW[buf * TIL + swz(srow, ch[j])] = w_ok ? o[j] : half8_t{};
+        for (int u = 0; u < SUB; u++) {
+            w_load<WT>(wr[u], wrow, K, k0 + GM_BK * u, shalf);
+        }
+    };
+    auto wstore = [&](int buf, int k0) {
+#pragma unroll
+        for (int u = 0; u < SUB; u++) {
+            half8_t o[4];
+            int     ch[4];
+            w_dequant<WT>(wr[u], wrow, K, k0 + GM_BK * u, shalf, o, ch);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                *(half8_t *) &sW[buf * TIL + swz<BK>(srow, ch[j] + 8 * u)] = w_ok ? o[j] : half8_t{};
+            }
         }
     };
 
@@ -258,15 +275,15 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
         const _Float16 * bx = sX + buf * TIL;
         const _Float16 * bw = sW + buf * TIL;
 #pragma unroll
-        for (int kk = 0; kk < GM_BK / 16; kk++) {
+        for (int kk = 0; kk < BK / 16; kk++) {
             half8_t a[MB], b[NB];
 #pragma unroll
             for (int i = 0; i < MB; i++) {
-                a[i] = *(const half8_t *) &bx[swz(wm * (BT / WM) + i * 32 + lq, 2 * kk + hh)];
+                a[i] = *(const half8_t *) &bx[swz<BK>(wm * (BT / WM) + i * 32 + lq, 2 * kk + hh)];
             }
 #pragma unroll
             for (int j = 0; j < NB; j++) {
-                b[j] = *(const half8_t *) &bw[swz(wn * (BT / WN) + j * 32 + lq, 2 * kk + hh)];
+                b[j] = *(const half8_t *) &bw[swz<BK>(wn * (BT / WN) + j * 32 + lq, 2 * kk + hh)];
             }
 #pragma unroll
             for (int i = 0; i < MB; i++) {
@@ -278,23 +295,23 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
         }
     };
 
-    const int nk = (int) (K / GM_BK);
+    const int nk = (int) (K / BK);
     dma(0, 0);
-    w_load<WT>(wr, wrow, K, 0, shalf);
+    wload(0);
     wstore(0, 0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     for (int ks = 0; ks < nk; ks++) {
         const int nxt = (ks + 1) & 1;
         if (ks + 1 < nk) {
-            dma(nxt, (ks + 1) * GM_BK);
+            dma(nxt, (ks + 1) * BK);
             __builtin_amdgcn_sched_barrier(0);
-            w_load<WT>(wr, wrow, K, (ks + 1) * GM_BK, shalf);
+            wload((ks + 1) * BK);
             __builtin_amdgcn_sched_barrier(0);
         }
         compute(ks & 1);
         if (ks + 1 < nk) {
-            wstore(nxt, (ks + 1) * GM_BK);
+            wstore(nxt, (ks + 1) * BK);
         }
         __builtin_amdgcn_s_waitcnt(0);  // this thread's DMA and LDS writes
         __syncthreads();
@@ -363,7 +380,7 @@ size_t gemm_workspace(int64_t K, int64_t M) {
     return (size_t) M * (size_t) K * sizeof(_Float16);
 }
 
-template <int NW, int WM>
+template <int NW, int WM, int BK>
 static int launch_gemm(int wtype, const uint8_t * W, int64_t N, int64_t K, int64_t rs, const _Float16 * xh, int64_t M,
                        const float * bias, const float * res, int64_t ldr, float * y, int64_t ldy, hipStream_t stream) {
     constexpr int BT   = 32 * NW;
@@ -373,7 +390,7 @@ static int launch_gemm(int wtype, const uint8_t * W, int64_t N, int64_t K, int64
     if (n > 0x7fffffff) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat gemm: too many tiles");
     }
-    const size_t lds = (size_t) 4 * BT * 64 * sizeof(_Float16);
+    const size_t lds = (size_t) 4 * BT * BK * sizeof(_Float16);
     auto         go  = [&](auto kern) -> int {
         if (lds > 64 * 1024 && !ensure_lds_limit((const void *) kern, lds)) {
             return set_error(MMHIP_ERR_HIP, "mul_mat gemm: cannot raise LDS limit to %zu", lds);
@@ -383,9 +400,9 @@ static int launch_gemm(int wtype, const uint8_t * W, int64_t N, int64_t K, int64
         return check_launch("mul_mat gemm");
     };
     switch (wtype) {
-        case TYPE_Q8_0: return go(k_gemm_q<TYPE_Q8_0, NW, WM>);
-        case TYPE_Q4_K: return go(k_gemm_q<TYPE_Q4_K, NW, WM>);
-        default: return go(k_gemm_q<TYPE_Q6_K, NW, WM>);
+        case TYPE_Q8_0: return go(k_gemm_q<TYPE_Q8_0, NW, WM, BK>);
+        case TYPE_Q4_K: return go(k_gemm_q<TYPE_Q4_K, NW, WM, BK>);
+        default: return go(k_gemm_q<TYPE_Q6_K, NW, WM, BK>);
     }
 }
 
@@ -411,9 +428,13 @@ int gemm_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const fl
     const uint8_t * wb       = (const uint8_t *) W;
     const int64_t   tiles256 = ((N + 255) / 256) * ((M + 255) / 256);
     if (tiles256 >= 256) {
-        return launch_gemm<8, 2>(wtype, wb, N, K, rs, xh, M, bias, res, ldr, y, ldy, stream);
+        return launch_gemm<8, 2, 64>(wtype, wb, N, K, rs, xh, M, bias, res, ldr, y, ldy, stream);
     }
-    return launch_gemm<4, 2>(wtype, wb, N, K, rs, xh, M, bias, res, ldr, y, ldy, stream);
+    // small grids: 128-wide K steps, twice the MFMA work per load round trip
+    if (K % 128 == 0) {
+        return launch_gemm<4, 2, 128>(wtype, wb, N, K, rs, xh, M, bias, res, ldr, y, ldy, stream);
+    }
+    return launch_gemm<4, 2, 64>(wtype, wb, N, K, rs, xh, M, bias, res, ldr, y, ldy, stream);
 }
 
 }  // namespace mmhip

@@ -81,6 +81,17 @@ def test_gemm_shapes(mm, orc, pkg, t, N, K, M):
     assert cosine(y, yg) > 0.9999
 
 
+@pytest.mark.parametrize("N,K,M", [(96, 2304, 40), (300, 768, 600), (2048, 2048, 1380)])
+def test_gemm_q8_0_k_steps(mm, orc, pkg, N, K, M):
+    """Q8_0 GEMMs on small grids (128-wide K steps): the DiT preprocess K,
+    a short K and the DiT projection shape.  (16-byte weight rows make K a
+    multiple of 256 on this path.)"""
+    y, yg, yf = run(mm, orc, pkg, 8, N, K, M, 5100 + K + M)
+    assert rel_rms(y, yf) < 2e-3
+    assert cosine(y, yf) > 0.99999
+    assert cosine(y, yg) > 0.9999
+
+
 def test_gemm_q4_K_benchmark_shape_sampled(mm, orc, pkg):
     """DiT QKV projection workload: W 6144 x 2048 Q4_K, 8192 tokens; checked
     on 40 sampled tokens."""
