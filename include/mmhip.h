@@ -268,6 +268,18 @@ int mmhip_norm(const mmhip_view * x, float eps, float * dst, void * stream);
  * dit_layer_norm (src/dit.h:161-167), fused: dst = (norm(x) * w) + b, each
  * step rounded as in the three ops; w or b may be NULL. */
 int mmhip_norm_affine(const mmhip_view * x, float eps, const float * w, const float * b, float * dst, void * stream);
+/* GGML_OP_MUL_MAT of two f32 tensors (activation x activation: the depth
+ * decoder's manual attention scores and P.V, src/depth-decoder.h:214-219):
+ * dst[i, j, i2, i3] = sum_k a[k, i, i2/r2, i3/r3] * b[k, j, i2, i3], any
+ * strides with contiguous dim 0, a broadcast over dims 2/3; dst contiguous
+ * [a->ne[1], b->ne[1], b->ne[2], b->ne[3]]. */
+int mmhip_mul_mat_f32(const mmhip_view * a, const mmhip_view * b, float * dst, void * stream);
+/* GGML_OP_DIAG_MASK_INF (src/depth-decoder.h:216): elements with i0 > n_past
+ * + i1 become -inf; dst contiguous. */
+int mmhip_diag_mask_inf(const mmhip_view * a, int n_past, float * dst, void * stream);
+/* GGML_OP_SOFT_MAX without mask, scale 1 (src/depth-decoder.h:217, :348):
+ * row softmax with ggml-CPU's steps (f32 exp, double sum); dst contiguous. */
+int mmhip_soft_max(const mmhip_view * a, float * dst, void * stream);
 /* GGML_OP_CONCAT of f32 a and b along dim 0..3 (the DiT input channel concat
  * and the timestep token, src/dit.h:262-264, :273); dst contiguous. */
 int mmhip_concat(const mmhip_view * a, const mmhip_view * b, int dim, float * dst, void * stream);

@@ -527,9 +527,22 @@ bool supports(const struct ggml_tensor * op) {
         case GGML_OP_TRANSPOSE:
             return true;
         case GGML_OP_MUL_MAT:
+            if (op->src[0]->type == GGML_TYPE_F32) {  // activation x activation
+                return op->src[1]->type == GGML_TYPE_F32 && op->src[0]->nb[0] == 4 && op->src[1]->nb[0] == 4 &&
+                       op->type == GGML_TYPE_F32 && ggml_is_contiguous(op);
+            }
             return supports_mul_mat(op);
         case GGML_OP_FLASH_ATTN_EXT:
             return supports_fa(op);
+        case GGML_OP_SOFT_MAX: {
+            float scale, max_bias;
+            memcpy(&scale, &op->op_params[0], sizeof(float));
+            memcpy(&max_bias, &op->op_params[1], sizeof(float));
+            return op->src[1] == nullptr && scale == 1.0f && max_bias == 0.0f && op->src[0]->type == GGML_TYPE_F32 &&
+                   op->type == GGML_TYPE_F32 && ggml_is_contiguous(op);
+        }
+        case GGML_OP_DIAG_MASK_INF:
+            return op->src[0]->type == GGML_TYPE_F32 && op->type == GGML_TYPE_F32 && ggml_is_contiguous(op);
         case GGML_OP_ADD:
         case GGML_OP_SUB:
         case GGML_OP_MUL:
@@ -616,6 +629,11 @@ int run_node(mi_backend * c, const struct ggml_tensor * n) {
         case GGML_OP_TRANSPOSE:
             return MMHIP_OK;
         case GGML_OP_MUL_MAT:
+            if (n->src[0]->type == GGML_TYPE_F32) {
+                mmhip_view a = view_of(n->src[0]), b = view_of(n->src[1]);
+                rc           = mmhip_mul_mat_f32(&a, &b, (float *) n->data, s);
+                break;
+            }
             return run_mul_mat(c, n) ? MMHIP_OK : -1;
         case GGML_OP_FLASH_ATTN_EXT:
             return run_fa(c, n) ? MMHIP_OK : -1;
@@ -694,6 +712,16 @@ int run_node(mi_backend * c, const struct ggml_tensor * n) {
             memcpy(&hi, &n->op_params[1], sizeof(float));
             mmhip_view a = view_of(n->src[0]);
             rc           = mmhip_clamp(&a, lo, hi, (float *) n->data, s);
+            break;
+        }
+        case GGML_OP_SOFT_MAX: {
+            mmhip_view a = view_of(n->src[0]);
+            rc           = mmhip_soft_max(&a, (float *) n->data, s);
+            break;
+        }
+        case GGML_OP_DIAG_MASK_INF: {
+            mmhip_view a = view_of(n->src[0]);
+            rc           = mmhip_diag_mask_inf(&a, n->op_params[0], (float *) n->data, s);
             break;
         }
         default:

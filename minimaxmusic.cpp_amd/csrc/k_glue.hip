@@ -358,6 +358,68 @@ __global__ void k_clamp(TV a, float lo, float hi, int64_t n, float * __restrict_
     }
 }
 
+// GGML_OP_MUL_MAT of two f32 tensors (activation x activation: the depth
+// decoder's manual attention, src/depth-decoder.h:214-219): dst[i, j, i2, i3]
+// = sum_k a[k, i, i2 / r2, i3 / r3] * b[k, j, i2, i3] over any strides, f32
+// products summed in double.  One thread per output element.
+__global__ void k_mul_mat_f32(TV a, TV b, float * __restrict__ dst, int64_t ne0, int64_t ne1, int64_t ne2,
+                              int64_t K, int64_t r2, int64_t r3, int64_t n) {
+    for (int64_t t = blockIdx.x * (int64_t) blockDim.x + threadIdx.x; t < n; t += (int64_t) gridDim.x * blockDim.x) {
+        const int64_t i = t % ne0, j = (t / ne0) % ne1, i2 = (t / (ne0 * ne1)) % ne2, i3 = t / (ne0 * ne1 * ne2);
+        const char *  pa = at(a, 0, i, i2 / r2, i3 / r3);
+        const char *  pb = at(b, 0, j, i2, i3);
+        double        acc = 0.0;
+        for (int64_t k = 0; k < K; k++) {
+            acc += (double) (*(const float *) (pa + k * a.nb[0]) * *(const float *) (pb + k * b.nb[0]));
+        }
+        dst[t] = (float) acc;
+    }
+}
+
+// GGML_OP_DIAG_MASK_INF (src/depth-decoder.h:216): element (i0, i1, ..) of a
+// with i0 > n_past + i1 becomes -inf; dst contiguous.
+__global__ void k_diag_mask_inf(TV a, int n_past, int64_t n, float * __restrict__ dst) {
+    for (int64_t t = blockIdx.x * (int64_t) blockDim.x + threadIdx.x; t < n; t += (int64_t) gridDim.x * blockDim.x) {
+        int64_t i0, i1, i2, i3;
+        unravel(t, a.ne, i0, i1, i2, i3);
+        const float v = *(const float *) at(a, i0, i1, i2, i3);
+        dst[t]        = i0 > n_past + i1 ? -INFINITY : v;
+    }
+}
+
+// GGML_OP_SOFT_MAX without mask, scale 1 (src/depth-decoder.h:217, the
+// sampler's softmax :348): one wave per row, ggml-CPU's steps -- the row max,
+// e = expf(x - max), the sum of e in double, y = e * (float) (1 / sum).
+__global__ __launch_bounds__(256) void k_soft_max_rows(TV a, int64_t rows, float * __restrict__ dst) {
+#pragma clang fp contract(off)
+    const int64_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int     l   = threadIdx.x & 63;
+    if (row >= rows) {
+        return;
+    }
+    const int64_t n  = a.ne[0];
+    const int64_t i1 = row % a.ne[1], i2 = (row / a.ne[1]) % a.ne[2], i3 = row / (a.ne[1] * a.ne[2]);
+    const char *  xr = at(a, 0, i1, i2, i3);
+    float *       dr = dst + row * n;
+    float         mx = -INFINITY;
+    for (int64_t i = l; i < n; i += 64) {
+        const float v = *(const float *) (xr + i * a.nb[0]);
+        mx            = v > mx ? v : mx;
+    }
+    mx         = wave_max(mx);
+    double sum = 0.0;
+    for (int64_t i = l; i < n; i += 64) {
+        const float e = expf(*(const float *) (xr + i * a.nb[0]) - mx);
+        dr[i]         = e;
+        sum += (double) e;
+    }
+    sum            = wave_sum_d(sum);
+    const float is = (float) (1.0 / sum);
+    for (int64_t i = l; i < n; i += 64) {
+        dr[i] = dr[i] * is;  // each lane rescales the elements it wrote
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Per-head rows of the QKV projection (the CONT / RMS_NORM / MUL / ROPE /
 // SET_ROWS chain of the attention block): one wave per row (h, t) of D = 64 *
@@ -974,6 +1036,58 @@ extern "C" int mmhip_norm_affine(const mmhip_view * x, float eps, const float * 
     }
     hipLaunchKernelGGL(k_layer_norm, dim3((unsigned) rows), dim3(256), 0, (hipStream_t) stream, tv(x), eps, w, b, dst);
     return check_launch("norm");
+}
+
+extern "C" int mmhip_mul_mat_f32(const mmhip_view * a, const mmhip_view * b, float * dst, void * stream) {
+    MMHIP_API_BEGIN();
+    if (!a || !b || !dst || a->ne[0] != b->ne[0] || a->ne[2] <= 0 || a->ne[3] <= 0 || b->ne[2] % a->ne[2] != 0 ||
+        b->ne[3] % a->ne[3] != 0 || a->nb[0] != 4 || b->nb[0] != 4) {
+        return set_error(MMHIP_ERR_INVALID, "mul_mat_f32: bad arguments");
+    }
+    const int64_t n = a->ne[1] * b->ne[1] * b->ne[2] * b->ne[3];
+    if (n == 0) {
+        return MMHIP_OK;
+    }
+    if (n >= ((int64_t) 1 << 31)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat_f32: too many outputs");
+    }
+    hipLaunchKernelGGL(k_mul_mat_f32, dim3(grid_for(n, 256)), dim3(256), 0, (hipStream_t) stream, tv(a), tv(b), dst,
+                       a->ne[1], b->ne[1], b->ne[2], a->ne[0], b->ne[2] / a->ne[2], b->ne[3] / a->ne[3], n);
+    return check_launch("mul_mat_f32");
+}
+
+extern "C" int mmhip_diag_mask_inf(const mmhip_view * a, int n_past, float * dst, void * stream) {
+    MMHIP_API_BEGIN();
+    if (!a || !dst) {
+        return set_error(MMHIP_ERR_INVALID, "diag_mask_inf: bad arguments");
+    }
+    const int64_t n = nel(a);
+    if (n == 0) {
+        return MMHIP_OK;
+    }
+    if (n >= ((int64_t) 1 << 31)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "diag_mask_inf: too many elements");
+    }
+    hipLaunchKernelGGL(k_diag_mask_inf, dim3(grid_for(n, 256)), dim3(256), 0, (hipStream_t) stream, tv(a), n_past, n,
+                       dst);
+    return check_launch("diag_mask_inf");
+}
+
+extern "C" int mmhip_soft_max(const mmhip_view * a, float * dst, void * stream) {
+    MMHIP_API_BEGIN();
+    if (!a || !dst || a->ne[0] <= 0) {
+        return set_error(MMHIP_ERR_INVALID, "soft_max: bad arguments");
+    }
+    const int64_t rows = a->ne[1] * a->ne[2] * a->ne[3];
+    if (rows == 0) {
+        return MMHIP_OK;
+    }
+    if (rows >= ((int64_t) 1 << 31)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "soft_max: too many rows");
+    }
+    hipLaunchKernelGGL(k_soft_max_rows, dim3((unsigned) ((rows + 3) / 4)), dim3(256), 0, (hipStream_t) stream, tv(a),
+                       rows, dst);
+    return check_launch("soft_max");
 }
 
 extern "C" int mmhip_concat(const mmhip_view * a, const mmhip_view * b, int dim, float * dst, void * stream) {

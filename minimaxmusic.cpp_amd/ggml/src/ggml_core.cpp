@@ -157,6 +157,8 @@ extern "C" const char * ggml_op_name(enum ggml_op op) {
         case GGML_OP_MUL: return "MUL";
         case GGML_OP_SCALE: return "SCALE";
         case GGML_OP_CLAMP: return "CLAMP";
+        case GGML_OP_SOFT_MAX: return "SOFT_MAX";
+        case GGML_OP_DIAG_MASK_INF: return "DIAG_MASK_INF";
         case GGML_OP_NORM: return "NORM";
         case GGML_OP_CONCAT: return "CONCAT";
         case GGML_OP_RMS_NORM: return "RMS_NORM";
@@ -570,6 +572,26 @@ extern "C" struct ggml_tensor * ggml_clamp(struct ggml_context * ctx, struct ggm
     const float          params[2] = { min, max };
     set_op_params(r, params, sizeof(params));
     r->op     = GGML_OP_CLAMP;
+    r->src[0] = a;
+    return r;
+}
+
+// softmax over rows (no mask, scale 1, no ALiBi): op_params = {scale, max_bias}
+extern "C" struct ggml_tensor * ggml_soft_max(struct ggml_context * ctx, struct ggml_tensor * a) {
+    struct ggml_tensor * r         = ggml_dup_tensor(ctx, a);
+    const float          params[2] = { 1.0f, 0.0f };
+    set_op_params(r, params, sizeof(params));
+    r->op     = GGML_OP_SOFT_MAX;
+    r->src[0] = a;
+    return r;
+}
+
+// elements (i0, i1) with i0 > n_past + i1 set to -inf; op_params[0] = n_past
+extern "C" struct ggml_tensor * ggml_diag_mask_inf(struct ggml_context * ctx, struct ggml_tensor * a, int n_past) {
+    struct ggml_tensor * r        = ggml_dup_tensor(ctx, a);
+    const int32_t        params[1] = { n_past };
+    set_op_params(r, params, sizeof(params));
+    r->op     = GGML_OP_DIAG_MASK_INF;
     r->src[0] = a;
     return r;
 }

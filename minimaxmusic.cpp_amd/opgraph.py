@@ -63,6 +63,8 @@ def _load():
         "ggml_view_3d": (_T, [vp, _T, i64, i64, i64, sz, sz, sz]),
         "ggml_cast": (_T, [vp, _T, i32]), "ggml_cont": (_T, [vp, _T]),
         "ggml_swiglu_split": (_T, [vp, _T, _T]),
+        "ggml_rms_norm": (_T, [vp, _T, f32]), "ggml_transpose": (_T, [vp, _T]),
+        "ggml_soft_max": (_T, [vp, _T]), "ggml_diag_mask_inf": (_T, [vp, _T, i32]),
         "ggml_flash_attn_ext": (_T, [vp, _T, _T, _T, _T, f32, f32, f32]),
         "ggml_flash_attn_ext_set_prec": (None, [_T, i32]),
         "ggml_new_graph_custom": (vp, [vp, sz, b]), "ggml_build_forward_expand": (None, [vp, _T]),
@@ -158,6 +160,19 @@ class OpGraph:
 
     def swiglu_split(self, gate, value):
         return self.G.ggml_swiglu_split(self.ctx, gate, value)
+
+    # the depth decoder's layer (src/depth-decoder.h:192-236)
+    def rms_norm(self, a, eps):
+        return self.G.ggml_rms_norm(self.ctx, a, eps)
+
+    def transpose(self, a):
+        return self.G.ggml_transpose(self.ctx, a)
+
+    def soft_max(self, a):
+        return self.G.ggml_soft_max(self.ctx, a)
+
+    def diag_mask_inf(self, a, n_past):
+        return self.G.ggml_diag_mask_inf(self.ctx, a, n_past)
 
     def build(self, outputs):
         self.graph = self.G.ggml_new_graph_custom(self.ctx, self.n_tensors, False)
