@@ -51,7 +51,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="lm_decode",
                     choices=["lm_decode", "gemv_q8_0", "fa_decode", "fa_prefill", "fa_dit", "gemm_q4_k",
-                             "dit_block"])
+                             "dit_block", "depth"])
     ap.add_argument("--wtype", default="q8_0", choices=["q8_0", "q6_k"], help="lm_decode weight type")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -663,6 +663,90 @@ def bench_dit_block(args, torch, pkg):
     }
 
 
+def bench_depth(args, torch, pkg):
+    """The RVQ depth decoder's 4-layer transformer stack (src/depth-decoder.h:
+    196-236) at its last step, S = 8 positions x the CFG pair (B = 2, 16
+    tokens), Q8_0 weights, through ggml_backend_graph_compute on the MI355X
+    backend (HIP-graph replay).  The roofline call is the gate projection
+    (6144 x 4096) at 16 tokens through the C-ABI (two 8-column GEMV groups)."""
+    import importlib
+
+    import oracle
+
+    og_mod = importlib.import_module(pkg.__name__ + ".opgraph")
+    dg = importlib.import_module(pkg.__name__ + ".depthgraph")
+    mm = pkg.mmhip
+    S, B, NL = 8, 2, 4
+    ws = [dg.synth_layer(3200 + i) for i in range(NL)]
+    x0 = np.random.default_rng(3300).standard_normal((B, S, dg.DIM)).astype(np.float32)
+    g = og_mod.OpGraph(n_tensors=100 * NL)
+    try:
+        ls = [dg.Layer(g) for _ in range(NL)]
+        tx = g.tensor(og_mod.F32, [dg.DIM, S, B])
+        out = tx
+        for lw in ls:
+            out = dg.build_layer(g, lw, out, S, B)
+        g.build([out])
+        for lw, w in zip(ls, ws):
+            lw.upload(g, w)
+        g.set(tx, x0)
+        for _ in range(args.warmup + 2):
+            g.compute()
+        g.synchronize()
+        g.gpu_time(reset=True)
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            g.compute()
+        g.synchronize()
+        wall = (time.perf_counter() - t0) / args.steps
+        gms, n = g.gpu_time()
+        replays, eager = g.graph_stats()
+    finally:
+        g.close()
+    us = gms / max(n, 1) * 1e3
+    wbytes = NL * (4 * dg.DIM * dg.DIM + 3 * dg.DIM * dg.FF_INNER) * 34 // 32
+    M, N, K = S * B, dg.FF_INNER, dg.DIM
+    W = mm.QuantWeight.from_gguf(mm.Q8_0, ws[0]["w_gate"], N, K)
+    xs = torch.randn((M, K), device="cuda")
+    y = torch.empty((M, N), device="cuda")
+    L = mm.load()
+    ws_n = L.mmhip_mul_mat_workspace(mm.Q8_0, N, K, M)
+    wsb = torch.empty(ws_n, dtype=torch.uint8, device="cuda")
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+
+    def step(i, s):
+        rc = L.mmhip_mul_mat(mm.Q8_0, P(W.data), N, K, W.row_bytes, P(xs), K, M, P(y), N, P(wsb), ws_n, s)
+        assert rc == 0, L.mmhip_last_error()
+
+    avg_s, min_s = graph_time(torch, step, 10)
+    alg = N * K * 34 // 32 + M * K * 4 + M * N * 4
+    cpu = None
+    if not args.no_cpu:
+        raw = ws[0]["w_gate"][:512]
+        xc = x0.reshape(-1, dg.DIM)
+        n_thr = os.cpu_count() or 1
+        dt, it = cpu_rate(lambda: oracle.mul_mat_ggml(mm.Q8_0, raw, 512, K, xc, nthreads=n_thr), args.cpu_seconds)
+        cpu = {"value": round(512 * K * 34 / 32 / dt / 1e9, 3), "unit": "GB/s (weight bytes streamed)", "cores": n_thr,
+               "kind": "port", "sample": f"ggml-CPU-semantics Q8_0 mul_mat (oracle/oracle.c): 512 gate rows x {M} "
+                                         f"tokens, K={K}, {it} reps"}
+    return {
+        "metric": "Depth decoder 4-layer stack weight GB/s (S=8 steps, CFG B=2, Q8_0, 16 x 256 heads, FF 6144)",
+        "value": round(wbytes / (us * 1e-6) / 1e9, 2),
+        "unit": "GB/s",
+        "ms_per_step": round(us * 1e-3, 4),
+        "dtype": "int8 dots on Q8_0-quantised activations (GEMV), f32 attention",
+        "config": {"workload": f"depth decoder layers x{NL} through ggml_backend_graph_compute, S={S}, B={B}, Q8_0"},
+        "via_backend": {"path": "ggml_backend_graph_compute, MI355X backend, HIP-graph replay", "layers_per_graph": NL,
+                        "gpu_us_per_stack": round(us, 2), "wall_us_per_stack": round(wall * 1e6, 2),
+                        "replays": replays, "eager": eager},
+        "roofline": {"bound": "hbm", "kernel": "k_quant_q8_0 + 2 x k_gemv_q8_0<8> (gate 6144x4096, 16 tokens)",
+                     "achieved": round(alg / avg_s / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(alg / avg_s / 1e9 / HBM_PEAK_GBS, 4), "avg_launch_us": round(avg_s * 1e6, 2),
+                     "min_launch_us": round(min_s * 1e6, 2), "alg_bytes_per_launch": alg, "traffic": None},
+        "cpu_baseline": cpu,
+    }
+
+
 # Algorithmic HBM bytes of one Qwen3-8B-shape CFG decode step at KV 4096:
 # weights + KV read + norm weights + logits + KV write (per step, both rows).
 def lm_step_bytes(cfg, wtype):
@@ -844,6 +928,7 @@ def main():
         "fa_dit": lambda: bench_fa_mfma(args, torch, pkg, False),
         "gemm_q4_k": lambda: bench_gemm(args, torch, pkg),
         "dit_block": lambda: bench_dit_block(args, torch, pkg),
+        "depth": lambda: bench_depth(args, torch, pkg),
     }[args.workload]()
     line = {
         "metric": res["metric"],

@@ -71,14 +71,14 @@ int mmhip_dequantize_rows(int type, const void * w, int64_t nrows, int64_t ne0, 
  * :237, :243) and the depth decoder (src/depth-decoder.h:206-230).
  *   y[m*ldy + n] = sum_k deq(W)[n,k] * x[m*ldx + k],  n < N, m < M
  * W has N rows of K elements, row stride w_row_stride bytes.
- * M <= 8: activation-quantised GEMV (ggml-CPU arithmetic: Q8_0 / Q8_K
- * activations, integer block dots).  M > 8: MFMA GEMM on f16-rounded
+ * M <= 16: activation-quantised GEMV (ggml-CPU arithmetic: Q8_0 / Q8_K
+ * activations, integer block dots).  M > 16: MFMA GEMM on f16-rounded
  * dequantised weights and f16-rounded activations, f32 accumulation.
  * ------------------------------------------------------------------- */
 size_t mmhip_mul_mat_workspace(int type, int64_t N, int64_t K, int64_t M);
 int    mmhip_mul_mat(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const float * x, int64_t ldx,
                      int64_t M, float * y, int64_t ldy, void * ws, size_t ws_bytes, void * stream);
-/* MUL_MAT at token counts (M > 8) with the ADDs that follow it fused into the
+/* MUL_MAT at token counts (M > 16) with the ADDs that follow it fused into the
  * store: y = (x W^T + bias[n]) + r[m*ldr + n], each ADD rounded as its op;
  * bias and r may be NULL (r may alias y).  The DiT's projection biases and
  * residuals (src/dit.h:228-229, :237-245).  Workspace as mmhip_mul_mat. */
@@ -88,7 +88,8 @@ int    mmhip_mul_mat_bias_add(int type, const void * W, int64_t N, int64_t K, in
 
 /* The two halves of the GEMV path, exposed for fusion and for testing:
  * quantise M activation rows into the layout mmhip_mul_mat_q consumes
- * (size from mmhip_act_bytes), then run the GEMV on them (M <= 8). */
+ * (size from mmhip_act_bytes), then run the GEMV on them (any M, in groups
+ * of 8 activation rows). */
 size_t mmhip_act_bytes(int type, int64_t K, int64_t M);
 int    mmhip_quantize_act(int type, const float * x, int64_t ldx, int64_t K, int64_t M, void * xq, void * stream);
 int    mmhip_mul_mat_q(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const void * xq, int64_t M,

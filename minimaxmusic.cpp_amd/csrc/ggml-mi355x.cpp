@@ -820,7 +820,7 @@ int add_row_vector(const struct ggml_tensor * add, const struct ggml_tensor * n)
 bool mm_is_gemv(const struct ggml_tensor * n) {
     const struct ggml_tensor * x = n->src[1];
     const int64_t              M = x->ne[1] * x->ne[2] * x->ne[3];
-    return n->op == GGML_OP_MUL_MAT && M >= 1 && M <= 8 && mmhip_act_bytes(n->src[0]->type, n->src[0]->ne[0], M) > 0;
+    return n->op == GGML_OP_MUL_MAT && M >= 1 && M <= 16 && mmhip_act_bytes(n->src[0]->type, n->src[0]->ne[0], M) > 0;
 }
 
 int act_vec_type(int wtype) {

@@ -1,4 +1,4 @@
-// k_gemm.hip - MUL_MAT at token counts (M > 8): MFMA GEMM with the weight
+// k_gemm.hip - MUL_MAT at token counts (M > 16): MFMA GEMM with the weight
 // tile dequantised into LDS.
 //
 //   y[m, n] = sum_k x[m, k] * deq(W)[n, k]

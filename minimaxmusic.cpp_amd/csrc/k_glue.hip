@@ -376,6 +376,30 @@ __global__ void k_mul_mat_f32(TV a, TV b, float * __restrict__ dst, int64_t ne0,
     }
 }
 
+// The same with one wave per output (long K: the attention scores, K = head
+// dim 256): lanes stride over K (coalesced), double partial sums reduced
+// symmetrically across the wave.
+__global__ __launch_bounds__(256) void k_mul_mat_f32_wave(TV a, TV b, float * __restrict__ dst, int64_t ne0,
+                                                          int64_t ne1, int64_t ne2, int64_t K, int64_t r2, int64_t r3,
+                                                          int64_t n) {
+    const int64_t t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int     l = threadIdx.x & 63;
+    if (t >= n) {
+        return;
+    }
+    const int64_t i = t % ne0, j = (t / ne0) % ne1, i2 = (t / (ne0 * ne1)) % ne2, i3 = t / (ne0 * ne1 * ne2);
+    const char *  pa = at(a, 0, i, i2 / r2, i3 / r3);
+    const char *  pb = at(b, 0, j, i2, i3);
+    double        acc = 0.0;
+    for (int64_t k = l; k < K; k += 64) {
+        acc += (double) (*(const float *) (pa + k * a.nb[0]) * *(const float *) (pb + k * b.nb[0]));
+    }
+    acc = wave_sum_d(acc);
+    if (l == 0) {
+        dst[t] = (float) acc;
+    }
+}
+
 // GGML_OP_DIAG_MASK_INF (src/depth-decoder.h:216): element (i0, i1, ..) of a
 // with i0 > n_past + i1 becomes -inf; dst contiguous.
 __global__ void k_diag_mask_inf(TV a, int n_past, int64_t n, float * __restrict__ dst) {
@@ -1050,6 +1074,11 @@ extern "C" int mmhip_mul_mat_f32(const mmhip_view * a, const mmhip_view * b, flo
     }
     if (n >= ((int64_t) 1 << 31)) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat_f32: too many outputs");
+    }
+    if (a->ne[0] >= 128 && n <= ((int64_t) 1 << 24)) {
+        hipLaunchKernelGGL(k_mul_mat_f32_wave, dim3((unsigned) ((n + 3) / 4)), dim3(256), 0, (hipStream_t) stream, tv(a),
+                           tv(b), dst, a->ne[1], b->ne[1], b->ne[2], a->ne[0], b->ne[2] / a->ne[2], b->ne[3] / a->ne[3], n);
+        return check_launch("mul_mat_f32");
     }
     hipLaunchKernelGGL(k_mul_mat_f32, dim3(grid_for(n, 256)), dim3(256), 0, (hipStream_t) stream, tv(a), tv(b), dst,
                        a->ne[1], b->ne[1], b->ne[2], a->ne[0], b->ne[2] / a->ne[2], b->ne[3] / a->ne[3], n);

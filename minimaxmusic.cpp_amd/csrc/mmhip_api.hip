@@ -51,8 +51,10 @@ int check_launch(const char * what) {
     return MMHIP_OK;
 }
 
-// MUL_MAT dispatch: GEMV for small M, MFMA GEMM beyond.
-constexpr int64_t GEMV_MAX_M = 8;
+// MUL_MAT dispatch: GEMV for small M (column groups of 8, each streaming the
+// weights; the second group's rows come back from the Infinity Cache), MFMA
+// GEMM beyond: at 9..16 tokens a GEMM has too few tiles to cover the CUs.
+constexpr int64_t GEMV_MAX_M = 16;
 
 static bool use_gemm(int type, int64_t M) {
     (void) type;

@@ -22,7 +22,7 @@ def run(mm, orc, pkg, t, N, K, M, seed):
 
 
 @pytest.mark.parametrize("t", [8, 12, 14])
-@pytest.mark.parametrize("M", [1, 2, 3, 5, 8])
+@pytest.mark.parametrize("M", [1, 2, 3, 5, 8, 12, 16])
 def test_gemv_small(mm, orc, pkg, t, M):
     y, yg, yf = run(mm, orc, pkg, t, 1000, 2048, M, 2000 + 10 * t + M)
     assert rel_err(y, yg) < 2e-5
@@ -61,7 +61,7 @@ def test_gemv_rejects_bad_shapes(mm, pkg):
 
 
 # ---------------------------------------------------------------------------
-# token counts (M > 8): MFMA GEMM on f16-rounded dequantised weights and
+# token counts (M > 16): MFMA GEMM on f16-rounded dequantised weights and
 # f16-rounded activations with f32 accumulation.  Stated tolerance against
 # the exact fp64 oracle: relative RMS error <= 2e-3 and cosine >= 0.99999;
 # against the ggml-CPU-semantics oracle: cosine >= 0.9999.
@@ -73,7 +73,7 @@ def rel_rms(a, b):
 
 
 @pytest.mark.parametrize("t", [8, 12, 14])
-@pytest.mark.parametrize("N,K,M", [(384, 2048, 200), (100, 4096, 9), (130, 2048, 1380)])
+@pytest.mark.parametrize("N,K,M", [(384, 2048, 200), (100, 4096, 17), (130, 2048, 1380)])
 def test_gemm_shapes(mm, orc, pkg, t, N, K, M):
     y, yg, yf = run(mm, orc, pkg, t, N, K, M, 5000 + t + M)
     assert rel_rms(y, yf) < 2e-3
@@ -107,14 +107,15 @@ def test_gemm_q4_K_benchmark_shape_sampled(mm, orc, pkg):
 
 
 def test_gemm_matches_gemv_semantics_closely(mm, pkg):
-    """M = 8 (GEMV, activation-quantised) and M = 9 (GEMM, f16) agree on the
-    shared rows to the activation-quantisation error."""
+    """M = 16 (GEMV in two column groups, activation-quantised) and M = 17
+    (GEMM, f16) agree on the shared rows to the activation-quantisation
+    error."""
     N, K = 512, 2048
     raw = pkg.synth.gguf_blocks_np(8, N, K, 77)
-    x = torch.from_numpy(pkg.synth.normal_np((9, K), 78)).cuda()
+    x = torch.from_numpy(pkg.synth.normal_np((17, K), 78)).cuda()
     W = mm.QuantWeight.from_gguf(8, raw, N, K)
-    a = mm.mul_mat(W, x[:8].contiguous()).cpu().numpy()
-    b = mm.mul_mat(W, x).cpu().numpy()[:8]
+    a = mm.mul_mat(W, x[:16].contiguous()).cpu().numpy()
+    b = mm.mul_mat(W, x).cpu().numpy()[:16]
     assert cosine(a, b) > 0.9999
 
 
@@ -154,4 +155,4 @@ def test_gemm_bias_add_rejects_gemv_token_counts(mm):
     L = mm.load()
     d = torch.zeros(1 << 16, device="cuda")
     P = ctypes.c_void_p(d.data_ptr())
-    assert L.mmhip_mul_mat_bias_add(8, P, 64, 256, 272, P, 256, 8, P, None, 0, P, 64, P, 1 << 18, None) != 0
+    assert L.mmhip_mul_mat_bias_add(8, P, 64, 256, 272, P, 256, 16, P, None, 0, P, 64, P, 1 << 18, None) != 0
