@@ -742,7 +742,8 @@ def bench_depth(args, torch, pkg):
         "roofline": {"bound": "hbm", "kernel": "k_quant_q8_0 + 2 x k_gemv_q8_0<8> (gate 6144x4096, 16 tokens)",
                      "achieved": round(alg / avg_s / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(alg / avg_s / 1e9 / HBM_PEAK_GBS, 4), "avg_launch_us": round(avg_s * 1e6, 2),
-                     "min_launch_us": round(min_s * 1e6, 2), "alg_bytes_per_launch": alg, "traffic": None},
+                     "min_launch_us": round(min_s * 1e6, 2), "alg_bytes_per_launch": alg,
+                     "traffic": profile_traffic("depth_stack_s8_b2_q8_0")},
         "cpu_baseline": cpu,
     }
 
