@@ -752,7 +752,7 @@ int run_node(mi_backend * c, const struct ggml_tensor * n) {
 //             residual: the ADD is done in the GEMV's store.
 // MUL_MATs reading a slot skip their activation quantisation.
 
-enum step_kind { ST_NODE, ST_NORM, ST_SWIGLU_Q, ST_HEAD, ST_MM, ST_FA_Q, ST_GEMM, ST_LN };
+enum step_kind { ST_NODE, ST_NORM, ST_SWIGLU_Q, ST_HEAD, ST_MM, ST_FA_Q, ST_GEMM, ST_LN, ST_GLU_V };
 
 struct plan_step {
     int                  kind = ST_NODE;
@@ -1181,6 +1181,16 @@ graph_plan build_plan(struct ggml_cgraph * g) {
             continue;
         }
         struct ggml_tensor * n = ggml_graph_node(g, i);
+        // Steps run at their last node: every node in between must be a view or
+        // absorbed, so no other node can reuse a buffer the step still reads.
+        auto quiet_between = [&](int a, int b, int s1, int s2) {
+            for (int t = a + 1; t < b; t++) {
+                if (t != s1 && t != s2 && !is_noop(ggml_graph_node(g, t)->op)) {
+                    return false;
+                }
+            }
+            return true;
+        };
         if (n->op == GGML_OP_RMS_NORM && gi.uses[(size_t) i] == 1 && !is_output(n)) {
             const int j = gi.cons[(size_t) i];
             const struct ggml_tensor * m = ggml_graph_node(g, j);
@@ -1269,6 +1279,35 @@ graph_plan build_plan(struct ggml_cgraph * g) {
                 continue;
             }
         }
+        // SWIGLU reading its gate / value straight from the views the CONTs
+        // before it copy (the DiT's value / gate halves of ff_in, src/dit.h:
+        // 239-242): the CONTs are not run
+        if (n->op == GGML_OP_GLU && n->op_params[0] == GGML_GLU_OP_SWIGLU && n->src[1] && ggml_is_contiguous(n)) {
+            int cont_of[2] = { -1, -1 };
+            for (int k = 0; k < 2; k++) {
+                const struct ggml_tensor * c  = n->src[k];
+                const int                  ci = node_index(gi, c);
+                if (ci >= 0 && c->op == GGML_OP_CONT && gi.uses[(size_t) ci] == 1 && !is_output(c) &&
+                    c->src[0]->type == GGML_TYPE_F32 && c->src[0]->nb[0] == 4 && !overlaps(n, c->src[0])) {
+                    cont_of[k] = ci;
+                }
+            }
+            const int lo = std::min(cont_of[0] >= 0 ? cont_of[0] : i, cont_of[1] >= 0 ? cont_of[1] : i);
+            if ((cont_of[0] >= 0 || cont_of[1] >= 0) && quiet_between(lo, i, cont_of[0], cont_of[1])) {
+                plan_step st;
+                st.kind = ST_GLU_V;
+                st.node = i;
+                st.src  = cont_of[0];
+                st.mul  = cont_of[1];
+                for (int k = 0; k < 2; k++) {
+                    if (cont_of[k] >= 0) {
+                        absorbed[(size_t) cont_of[k]] = 1;
+                    }
+                }
+                add_pending(st);
+                continue;
+            }
+        }
         if (n->op == GGML_OP_CONT) {
             plan_step st;
             if (plan_head(g, gi, i, st, absorbed)) {
@@ -1276,16 +1315,6 @@ graph_plan build_plan(struct ggml_cgraph * g) {
                 continue;
             }
         }
-        // Steps run at their last node: every node in between must be a view or
-        // absorbed, so no other node can reuse a buffer the step still reads.
-        auto quiet_between = [&](int a, int b, int s1, int s2) {
-            for (int t = a + 1; t < b; t++) {
-                if (t != s1 && t != s2 && !is_noop(ggml_graph_node(g, t)->op)) {
-                    return false;
-                }
-            }
-            return true;
-        };
         // LayerNorm with its weight MUL and bias ADD (dit_layer_norm): one kernel
         if (n->op == GGML_OP_NORM && gi.uses[(size_t) i] == 1 && !is_output(n) && rows_contiguous_f32(n)) {
             const int                  j  = gi.cons[(size_t) i];
@@ -1549,6 +1578,13 @@ int run_step(mi_backend * c, struct ggml_cgraph * g, const plan_step & st, char 
         case ST_HEAD:
             rc = mmhip_head_rows_n(st.head, st.n_head, s);
             break;
+        case ST_GLU_V: {
+            const struct ggml_tensor * ga = st.src >= 0 ? ggml_graph_node(g, st.src)->src[0] : n->src[0];
+            const struct ggml_tensor * gb = st.mul >= 0 ? ggml_graph_node(g, st.mul)->src[0] : n->src[1];
+            mmhip_view                 a = view_of(ga), b = view_of(gb);
+            rc = mmhip_swiglu(&a, &b, n->op_params[1], (float *) n->data, s);
+            break;
+        }
         case ST_LN: {
             const struct ggml_tensor * nn = ggml_graph_node(g, st.src);
             const struct ggml_tensor * mu = ggml_graph_node(g, st.mul);
