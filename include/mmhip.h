@@ -85,6 +85,12 @@ int    mmhip_mul_mat(int type, const void * W, int64_t N, int64_t K, int64_t w_r
 int    mmhip_mul_mat_bias_add(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const float * x,
                               int64_t ldx, int64_t M, const float * bias, const float * r, int64_t ldr, float * y,
                               int64_t ldy, void * ws, size_t ws_bytes, void * stream);
+/* The same on activations already rounded to f16 (xh: M rows of K halves,
+ * contiguous, 16-byte aligned; as mmhip_norm_affine_h writes them): no
+ * workspace.  Used when a LayerNorm feeds only GEMMs (src/dit.h:193-199, :236). */
+int    mmhip_mul_mat_bias_add_h(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const void * xh,
+                                int64_t M, const float * bias, const float * r, int64_t ldr, float * y, int64_t ldy,
+                                void * stream);
 
 /* The two halves of the GEMV path, exposed for fusion and for testing:
  * quantise M activation rows into the layout mmhip_mul_mat_q consumes
@@ -269,6 +275,10 @@ int mmhip_norm(const mmhip_view * x, float eps, float * dst, void * stream);
  * dit_layer_norm (src/dit.h:161-167), fused: dst = (norm(x) * w) + b, each
  * step rounded as in the three ops; w or b may be NULL. */
 int mmhip_norm_affine(const mmhip_view * x, float eps, const float * w, const float * b, float * dst, void * stream);
+/* The same writing the rows also (or only: dst NULL) rounded to f16 into dsth,
+ * contiguous, the activation copy mmhip_mul_mat_bias_add_h consumes. */
+int mmhip_norm_affine_h(const mmhip_view * x, float eps, const float * w, const float * b, float * dst, void * dsth,
+                        void * stream);
 /* GGML_OP_MUL_MAT of two f32 tensors (activation x activation: the depth
  * decoder's manual attention scores and P.V, src/depth-decoder.h:214-219):
  * dst[i, j, i2, i3] = sum_k a[k, i, i2/r2, i3/r3] * b[k, j, i2, i3], any

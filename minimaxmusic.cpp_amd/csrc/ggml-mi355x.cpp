@@ -1160,6 +1160,7 @@ graph_plan build_plan(struct ggml_cgraph * g) {
     std::vector<int>         step_at((size_t) gi.nn, -1);  // index into pending
     std::vector<int64_t>     slot_of((size_t) gi.nn, -1);  // node -> quantised slot of its output
     std::vector<int>         slot_wtype((size_t) gi.nn, 0);
+    std::vector<int64_t>     f16_slot_of((size_t) gi.nn, -1);  // node -> slot holding its rows in f16
     std::vector<int>         norm_of((size_t) gi.nn, -1);  // MUL node -> its RMS_NORM, norm done by the GEMVs
     const bool               no_norm_mm = getenv("GGML_MI355X_DISABLE_NORM_GEMV") != nullptr;
     std::vector<char>        glu_mm((size_t) gi.nn, 0);  // SWIGLU node done by its GEMVs
@@ -1333,6 +1334,20 @@ graph_plan build_plan(struct ggml_cgraph * g) {
                     st.bias     = k;
                     st.bias_src = bi;
                     st.add_res  = wi;  // the MUL's weight operand
+                    // feeding only GEMMs (the DiT's Q/K/V and ff_in projections): the
+                    // rows go out in f16, the GEMMs' activation format, and not in f32
+                    bool only_gemm = !is_output(a) && !gi.consumers[(size_t) k].empty() && (a->ne[0] % 64) == 0;
+                    for (int c : gi.consumers[(size_t) k]) {
+                        const struct ggml_tensor * mm = ggml_graph_node(g, c);
+                        only_gemm = only_gemm && mm->op == GGML_OP_MUL_MAT && mm->src[1] == a && mm->src[0] != a &&
+                                    !mm_is_gemv(mm) && supports_mul_mat(mm) && ggml_is_contiguous(mm);
+                    }
+                    if (only_gemm) {
+                        st.slot_out  = (int64_t) plan.slot_bytes;
+                        plan.slot_bytes += (ggml_nelements(a) * 2 + 255) / 256 * 256;
+                        st.write_f32 = false;
+                        f16_slot_of[(size_t) k] = st.slot_out;
+                    }
                     absorbed[(size_t) i] = 1;
                     absorbed[(size_t) j] = 1;
                     absorbed[(size_t) k] = 1;
@@ -1348,6 +1363,10 @@ graph_plan build_plan(struct ggml_cgraph * g) {
             st.node  = i;
             st.mm    = i;
             int  cur = i;
+            const int xp = node_index(gi, n->src[1]);
+            if (xp >= 0 && f16_slot_of[(size_t) xp] >= 0) {
+                st.slot_in = f16_slot_of[(size_t) xp];  // activations already in f16
+            }
             auto single = [&](int t) { return gi.uses[(size_t) t] == 1 && !is_output(ggml_graph_node(g, t)); };
             if (single(cur)) {
                 const int                  j  = gi.cons[(size_t) cur];
@@ -1375,7 +1394,7 @@ graph_plan build_plan(struct ggml_cgraph * g) {
                     }
                 }
             }
-            if (cur != i) {
+            if (cur != i || st.slot_in >= 0) {
                 st.node = cur;
                 absorbed[(size_t) i] = 1;
                 if (st.bias >= 0) {
@@ -1591,8 +1610,10 @@ int run_step(mi_backend * c, struct ggml_cgraph * g, const plan_step & st, char 
             float                      eps;
             memcpy(&eps, &nn->op_params[0], sizeof(float));
             mmhip_view x = view_of(nn->src[0]);
-            rc = mmhip_norm_affine(&x, eps, (const float *) mu->src[st.add_res]->data,
-                                   (const float *) n->src[st.bias_src]->data, (float *) n->data, s);
+            rc = mmhip_norm_affine_h(&x, eps, (const float *) mu->src[st.add_res]->data,
+                                     (const float *) n->src[st.bias_src]->data,
+                                     st.write_f32 ? (float *) n->data : nullptr,
+                                     st.slot_out >= 0 ? (void *) (slot + st.slot_out) : nullptr, s);
             break;
         }
         case ST_GEMM: {
@@ -1603,6 +1624,12 @@ int run_step(mi_backend * c, struct ggml_cgraph * g, const plan_step & st, char 
             const float *              bias = st.bias >= 0 ? (const float *) ggml_graph_node(g, st.bias)->src[st.bias_src]->data
                                                            : nullptr;
             const struct ggml_tensor * r  = st.add >= 0 ? ggml_graph_node(g, st.add)->src[st.add_res] : nullptr;
+            if (st.slot_in >= 0) {
+                rc = mmhip_mul_mat_bias_add_h(w->type, w->data, N, K, (int64_t) w->nb[1], slot + st.slot_in, M, bias,
+                                              r ? (const float *) r->data : nullptr,
+                                              r ? (int64_t) (r->nb[1] / sizeof(float)) : 0, (float *) n->data, N, s);
+                break;
+            }
             const size_t               ws = mmhip_mul_mat_workspace(w->type, N, K, M);
             void *                     wp = ws ? workspace(c, ws) : nullptr;
             if (ws && !wp) {

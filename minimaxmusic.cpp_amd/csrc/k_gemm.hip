@@ -406,6 +406,29 @@ static int launch_gemm(int wtype, const uint8_t * W, int64_t N, int64_t K, int64
     }
 }
 
+// Tile configuration by shape (activations already f16, rows of K).
+static int gemm_launch(int wtype, const uint8_t * wb, int64_t N, int64_t K, int64_t rs, const _Float16 * xh, int64_t M,
+                       const float * bias, const float * res, int64_t ldr, float * y, int64_t ldy, hipStream_t stream) {
+    const int64_t tiles256 = ((N + 255) / 256) * ((M + 255) / 256);
+    if (tiles256 >= 256) {
+        return launch_gemm<8, 2, 64>(wtype, wb, N, K, rs, xh, M, bias, res, ldr, y, ldy, stream);
+    }
+    // small grids: 128-wide K steps, twice the MFMA work per load round trip
+    if (K % 128 == 0) {
+        return launch_gemm<4, 2, 128>(wtype, wb, N, K, rs, xh, M, bias, res, ldr, y, ldy, stream);
+    }
+    return launch_gemm<4, 2, 64>(wtype, wb, N, K, rs, xh, M, bias, res, ldr, y, ldy, stream);
+}
+
+int gemm_q_h(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const void * xh, int64_t M, float * y,
+             int64_t ldy, hipStream_t stream, const float * bias, const float * res, int64_t ldr) {
+    if (!gemm_supported(wtype, N, K, rs, W, (const float *) xh, K) || ((uintptr_t) xh) % 16 != 0) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat gemm (f16 activations): type %d N=%lld K=%lld rs=%lld not supported",
+                         wtype, (long long) N, (long long) K, (long long) rs);
+    }
+    return gemm_launch(wtype, (const uint8_t *) W, N, K, rs, (const _Float16 *) xh, M, bias, res, ldr, y, ldy, stream);
+}
+
 int gemm_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const float * x, int64_t ldx, int64_t M,
            float * y, int64_t ldy, void * ws, size_t ws_bytes, hipStream_t stream, const float * bias,
            const float * res, int64_t ldr) {
@@ -425,16 +448,7 @@ int gemm_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const fl
     if (rc != MMHIP_OK) {
         return rc;
     }
-    const uint8_t * wb       = (const uint8_t *) W;
-    const int64_t   tiles256 = ((N + 255) / 256) * ((M + 255) / 256);
-    if (tiles256 >= 256) {
-        return launch_gemm<8, 2, 64>(wtype, wb, N, K, rs, xh, M, bias, res, ldr, y, ldy, stream);
-    }
-    // small grids: 128-wide K steps, twice the MFMA work per load round trip
-    if (K % 128 == 0) {
-        return launch_gemm<4, 2, 128>(wtype, wb, N, K, rs, xh, M, bias, res, ldr, y, ldy, stream);
-    }
-    return launch_gemm<4, 2, 64>(wtype, wb, N, K, rs, xh, M, bias, res, ldr, y, ldy, stream);
+    return gemm_launch(wtype, (const uint8_t *) W, N, K, rs, xh, M, bias, res, ldr, y, ldy, stream);
 }
 
 }  // namespace mmhip

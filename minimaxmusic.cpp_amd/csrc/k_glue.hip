@@ -283,14 +283,14 @@ __global__ __launch_bounds__(256) void k_rms_norm(TV x, TV w, int has_w, float e
 // w / b it also applies the MUL and ADD that follow it (dit_layer_norm),
 // each rounded as its own op: (y * w[i]) + b[i].
 __global__ __launch_bounds__(256) void k_layer_norm(TV x, float eps, const float * __restrict__ w,
-                                                     const float * __restrict__ b, float * __restrict__ dst) {
+                                                     const float * __restrict__ b, float * dst,
+                                                     _Float16 * __restrict__ dsth) {
 #pragma clang fp contract(off)
     __shared__ double s_part[4];
     const int64_t     row = blockIdx.x;
     const int64_t     i1 = row % x.ne[1], i2 = (row / x.ne[1]) % x.ne[2], i3 = row / (x.ne[1] * x.ne[2]);
     const int64_t     n  = x.ne[0];
     const char *      xr = at(x, 0, i1, i2, i3);
-    float *           dr = dst + row * n;
     double            sm = 0.0;
     for (int64_t i = threadIdx.x; i < n; i += 256) {
         sm += (double) *(const float *) (xr + i * x.nb[0]);
@@ -305,7 +305,6 @@ __global__ __launch_bounds__(256) void k_layer_norm(TV x, float eps, const float
     double ss = 0.0;
     for (int64_t i = threadIdx.x; i < n; i += 256) {
         const float v = *(const float *) (xr + i * x.nb[0]) - mean;
-        dr[i]         = v;
         ss += (double) (v * v);
     }
     ss = wave_sum_d(ss);
@@ -316,14 +315,20 @@ __global__ __launch_bounds__(256) void k_layer_norm(TV x, float eps, const float
     const float var = (float) ((s_part[0] + s_part[1] + s_part[2] + s_part[3]) / (double) n);
     const float sc  = 1.0f / sqrtf(var + eps);
     for (int64_t i = threadIdx.x; i < n; i += 256) {
-        float t = dr[i] * sc;  // each thread rescales the elements it wrote
+        // x - mean again (the same f32 value), then the scale and the affine part
+        float t = (*(const float *) (xr + i * x.nb[0]) - mean) * sc;
         if (w) {
             t = t * w[i];
         }
         if (b) {
             t = t + b[i];
         }
-        dr[i] = t;
+        if (dst) {
+            dst[row * n + i] = t;
+        }
+        if (dsth) {
+            dsth[row * n + i] = (_Float16) t;
+        }
     }
 }
 
@@ -1047,8 +1052,17 @@ extern "C" int mmhip_norm(const mmhip_view * x, float eps, float * dst, void * s
 
 extern "C" int mmhip_norm_affine(const mmhip_view * x, float eps, const float * w, const float * b, float * dst,
                                  void * stream) {
+    if (!dst) {
+        MMHIP_API_BEGIN();
+        return set_error(MMHIP_ERR_INVALID, "norm: bad arguments");
+    }
+    return mmhip_norm_affine_h(x, eps, w, b, dst, nullptr, stream);
+}
+
+extern "C" int mmhip_norm_affine_h(const mmhip_view * x, float eps, const float * w, const float * b, float * dst,
+                                   void * dsth, void * stream) {
     MMHIP_API_BEGIN();
-    if (!x || !dst || x->ne[0] <= 0) {
+    if (!x || (!dst && !dsth) || x->ne[0] <= 0) {
         return set_error(MMHIP_ERR_INVALID, "norm: bad arguments");
     }
     const int64_t rows = x->ne[1] * x->ne[2] * x->ne[3];
@@ -1058,7 +1072,8 @@ extern "C" int mmhip_norm_affine(const mmhip_view * x, float eps, const float * 
     if (rows >= ((int64_t) 1 << 31) || nel(x) >= ((int64_t) 1 << 31)) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "norm: too many elements");
     }
-    hipLaunchKernelGGL(k_layer_norm, dim3((unsigned) rows), dim3(256), 0, (hipStream_t) stream, tv(x), eps, w, b, dst);
+    hipLaunchKernelGGL(k_layer_norm, dim3((unsigned) rows), dim3(256), 0, (hipStream_t) stream, tv(x), eps, w, b, dst,
+                       (_Float16 *) dsth);
     return check_launch("norm");
 }
 

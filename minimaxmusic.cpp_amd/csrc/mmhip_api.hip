@@ -129,6 +129,21 @@ extern "C" int mmhip_mul_mat_bias_add(int type, const void * W, int64_t N, int64
     return gemm_q(type, W, N, K, w_row_stride, x, ldx, M, y, ldy, ws, ws_bytes, (hipStream_t) stream, bias, r, ldr);
 }
 
+extern "C" int mmhip_mul_mat_bias_add_h(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride,
+                                        const void * xh, int64_t M, const float * bias, const float * r, int64_t ldr,
+                                        float * y, int64_t ldy, void * stream) {
+    MMHIP_API_BEGIN();
+    if (!W || !xh || !y || N <= 0 || K <= 0 || M <= 0 || ldy < N || (r && ldr < N)) {
+        return set_error(MMHIP_ERR_INVALID, "mul_mat_bias_add_h: bad arguments N=%lld K=%lld M=%lld", (long long) N,
+                         (long long) K, (long long) M);
+    }
+    if (!is_repacked_type(type) || !use_gemm(type, M)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat_bias_add_h: weight type %d at %lld tokens", type,
+                         (long long) M);
+    }
+    return gemm_q_h(type, W, N, K, w_row_stride, xh, M, y, ldy, (hipStream_t) stream, bias, r, ldr);
+}
+
 // ---------------------------------------------------------------------
 // FLASH_ATTN_EXT
 

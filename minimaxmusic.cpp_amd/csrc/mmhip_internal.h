@@ -85,6 +85,9 @@ size_t gemm_workspace(int64_t K, int64_t M);
 int    gemm_q(int wtype, const void * W, int64_t N, int64_t K, int64_t row_stride, const float * x, int64_t ldx,
               int64_t M, float * y, int64_t ldy, void * ws, size_t ws_bytes, hipStream_t stream,
               const float * bias = nullptr, const float * res = nullptr, int64_t ldr = 0);
+// The same on activations already rounded to f16 (rows of K halves, 16-byte aligned).
+int    gemm_q_h(int wtype, const void * W, int64_t N, int64_t K, int64_t row_stride, const void * xh, int64_t M,
+                float * y, int64_t ldy, hipStream_t stream, const float * bias, const float * res, int64_t ldr);
 
 }  // namespace mmhip
 

@@ -62,6 +62,7 @@ SIGNATURES = {
     "mmhip_mul_mat": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _sz, _vp]),
     "mmhip_mul_mat_bias_add": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _vp,
                                       _sz, _vp]),
+    "mmhip_mul_mat_bias_add_h": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _vp]),
     "mmhip_act_bytes": (_sz, [_i32, _i64, _i64]),
     "mmhip_quantize_act": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _vp]),
     "mmhip_mul_mat_q": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp]),
@@ -94,6 +95,7 @@ SIGNATURES = {
     "mmhip_scale": (_i32, [_VP, _f32, _f32, _vp, _vp]),
     "mmhip_norm": (_i32, [_VP, _f32, _vp, _vp]),
     "mmhip_norm_affine": (_i32, [_VP, _f32, _vp, _vp, _vp, _vp]),
+    "mmhip_norm_affine_h": (_i32, [_VP, _f32, _vp, _vp, _vp, _vp, _vp]),
     "mmhip_concat": (_i32, [_VP, _VP, _i32, _vp, _vp]),
     "mmhip_mul_mat_f32": (_i32, [_VP, _VP, _vp, _vp]),
     "mmhip_diag_mask_inf": (_i32, [_VP, _i32, _vp, _vp]),

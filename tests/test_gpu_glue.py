@@ -675,3 +675,35 @@ def test_cpy_row_paths(mm, case):
     dtype_ = 0 if dt == torch.float32 else 1
     assert L.mmhip_cpy(ctypes.byref(mm.view_of(src)), stype, ctypes.byref(mm.view_of(dst)), dtype_, st()) == 0
     assert torch.equal(dst, src.to(dt))
+
+
+def test_norm_affine_h_and_gemm_on_f16_rows(mm, pkg):
+    """mmhip_norm_affine_h writes the f32 rows' f16 rounding, and
+    mmhip_mul_mat_bias_add_h on those rows equals mmhip_mul_mat_bias_add on
+    the f32 rows (which rounds them to f16 itself), bit for bit."""
+    L = mm.load()
+    rng = np.random.default_rng(36)
+    M, K, N = 96, 2048, 384
+    x = (rng.standard_normal((M, K)) * 2).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(K)).astype(np.float32)
+    tx, tw, tb = (torch.from_numpy(a).cuda() for a in (x, w, b))
+    f32 = torch.empty_like(tx)
+    h16 = torch.empty((M, K), dtype=torch.float16, device="cuda")
+    assert L.mmhip_norm_affine_h(ctypes.byref(mm.view_of(tx)), 1e-5, ptr(tw), ptr(tb), ptr(f32), ptr(h16), st()) == 0
+    ref = torch.empty_like(tx)
+    assert L.mmhip_norm_affine(ctypes.byref(mm.view_of(tx)), 1e-5, ptr(tw), ptr(tb), ptr(ref), st()) == 0
+    assert torch.equal(f32, ref) and torch.equal(h16, ref.half())
+    raw = pkg.synth.gguf_blocks_np(8, N, K, 37)
+    W = mm.QuantWeight.from_gguf(8, raw, N, K)
+    bias = torch.randn(N, device="cuda")
+    y1 = torch.empty((M, N), device="cuda")
+    y2 = torch.empty((M, N), device="cuda")
+    need = L.mmhip_mul_mat_workspace(8, N, K, M)
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    assert L.mmhip_mul_mat_bias_add(8, ptr(W.data), N, K, W.row_bytes, ptr(f32), K, M, ptr(bias), None, 0, ptr(y1), N,
+                                    ptr(ws), need, st()) == 0
+    assert L.mmhip_mul_mat_bias_add_h(8, ptr(W.data), N, K, W.row_bytes, ptr(h16), M, ptr(bias), None, 0, ptr(y2), N,
+                                      st()) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
