@@ -7,8 +7,8 @@
 // every workgroup along N reads them, so they are converted once and moved at
 // half the bytes.  Workgroup tile: 256 tokens x 256 weight rows (8 waves,
 // each 128 x 64 with eight v_mfma_f32_32x32x16_f16 accumulators) when the
-// problem has at least 256 such tiles, else 128 x 128 (4 waves, each 64 x
-// 64); K step 64.  The weight tile is dequantised exactly as the GGUF
+// problem has at least 256 such tiles, else 64 tokens x 128 weight rows (4
+// waves, each 32 x 64); K step 64.  The weight tile is dequantised exactly as the GGUF
 // definitions (f32, no contraction) and then rounded to f16; both tiles are
 // k-contiguous rows in LDS, the operand order of the MFMA A (tokens) and B
 // (weight rows) inputs.  The output accumulator layout gives each lane one
@@ -183,25 +183,27 @@ __device__ __forceinline__ int swz(int r, int c) {
 // into one of two LDS weight buffers.  The next step's DMA and weight loads
 // are issued before the current step's MFMAs, so one step of MFMA work hides
 // their latency; one barrier per step.
-template <int WT, int NW, int WM, int BK>
+template <int WT, int NW, int WM, int BK, int BM>
 __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__ W, int64_t N, int64_t K, int64_t rs,
                                                      const _Float16 * __restrict__ xh, int64_t M,
                                                      const float * __restrict__ bias, const float * res, int64_t ldr,
                                                      float * y, int64_t ldy,
                                                      int64_t n_ntiles, int64_t n_tiles) {
 #pragma clang fp contract(off)
-    constexpr int BT  = 32 * NW;
+    constexpr int BT  = 32 * NW;       // weight rows per tile (thread t stages row t / 2)
     constexpr int T   = NW * 64;
     constexpr int WN  = NW / WM;
-    constexpr int MB  = BT / WM / 32;
+    constexpr int MB  = BM / WM / 32;
     constexpr int NB  = BT / WN / 32;
     constexpr int CPR = BK / 8;        // 16-byte chunks per tile row
     constexpr int SUB = BK / GM_BK;    // 64-wide weight sub-steps per K step
-    constexpr int XI  = BT * CPR / T;  // DMA instructions per thread per stage
-    constexpr int TIL = BT * BK;       // halves per tile
+    constexpr int XI  = BM * CPR / T;  // DMA instructions per thread per stage
+    constexpr int TIX = BM * BK;       // halves per activation tile
+    constexpr int TIL = BT * BK;       // halves per weight tile
+    static_assert(MB >= 1 && XI >= 1, "tile shape");
     extern __shared__ __attribute__((aligned(16))) _Float16 g_lds[];
     _Float16 * sX = g_lds;            // 2 stages
-    _Float16 * sW = g_lds + 2 * TIL;  // 2 buffers
+    _Float16 * sW = g_lds + 2 * TIX;  // 2 buffers
 
     // consecutive work items (one XCD, one L2) share the operand that is
     // re-read most: the weight tile when there are more weight tiles than
@@ -209,7 +211,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
     const int64_t work    = gm_xcd_remap(blockIdx.x, n_tiles);
     const int64_t n_mt    = n_tiles / n_ntiles;
     const bool    m_fast  = n_ntiles > n_mt;
-    const int64_t m0      = (m_fast ? work % n_mt : work / n_ntiles) * BT;
+    const int64_t m0      = (m_fast ? work % n_mt : work / n_ntiles) * BM;
     const int64_t n0      = (m_fast ? work / n_mt : work % n_ntiles) * BT;
     const int     tid  = threadIdx.x;
     const int     wave = tid >> 6;
@@ -232,7 +234,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
     auto           dma   = [&](int stage, int k0) {
 #pragma unroll
         for (int i = 0; i < XI; i++) {
-            dma16(xsrc[i] + k0, lds_x + 2u * (uint32_t) (stage * TIL + (wave_s * XI + i) * 512));
+            dma16(xsrc[i] + k0, lds_x + 2u * (uint32_t) (stage * TIX + (wave_s * XI + i) * 512));
         }
     };
 
@@ -272,14 +274,14 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
         }
     }
     auto compute = [&](int buf) {
-        const _Float16 * bx = sX + buf * TIL;
+        const _Float16 * bx = sX + buf * TIX;
         const _Float16 * bw = sW + buf * TIL;
 #pragma unroll
         for (int kk = 0; kk < BK / 16; kk++) {
             half8_t a[MB], b[NB];
 #pragma unroll
             for (int i = 0; i < MB; i++) {
-                a[i] = *(const half8_t *) &bx[swz<BK>(wm * (BT / WM) + i * 32 + lq, 2 * kk + hh)];
+                a[i] = *(const half8_t *) &bx[swz<BK>(wm * (BM / WM) + i * 32 + lq, 2 * kk + hh)];
             }
 #pragma unroll
             for (int j = 0; j < NB; j++) {
@@ -330,7 +332,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
             const float bn = bias ? bias[n] : 0.0f;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int64_t m = m0 + wm * (BT / WM) + i * 32 + 8 * (r / 4) + 4 * hh + (r % 4);
+                const int64_t m = m0 + wm * (BM / WM) + i * 32 + 8 * (r / 4) + 4 * hh + (r % 4);
                 if (m < M) {
                     float v = acc[i][j][r];
                     if (bias) {
@@ -380,17 +382,17 @@ size_t gemm_workspace(int64_t K, int64_t M) {
     return (size_t) M * (size_t) K * sizeof(_Float16);
 }
 
-template <int NW, int WM, int BK>
+template <int NW, int WM, int BK, int BM = 32 * NW>
 static int launch_gemm(int wtype, const uint8_t * W, int64_t N, int64_t K, int64_t rs, const _Float16 * xh, int64_t M,
                        const float * bias, const float * res, int64_t ldr, float * y, int64_t ldy, hipStream_t stream) {
     constexpr int BT   = 32 * NW;
     const int64_t n_nt = (N + BT - 1) / BT;
-    const int64_t n_mt = (M + BT - 1) / BT;
+    const int64_t n_mt = (M + BM - 1) / BM;
     const int64_t n    = n_nt * n_mt;
     if (n > 0x7fffffff) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat gemm: too many tiles");
     }
-    const size_t lds = (size_t) 4 * BT * BK * sizeof(_Float16);
+    const size_t lds = (size_t) 2 * (BM + BT) * BK * sizeof(_Float16);
     auto         go  = [&](auto kern) -> int {
         if (lds > 64 * 1024 && !ensure_lds_limit((const void *) kern, lds)) {
             return set_error(MMHIP_ERR_HIP, "mul_mat gemm: cannot raise LDS limit to %zu", lds);
@@ -400,9 +402,9 @@ static int launch_gemm(int wtype, const uint8_t * W, int64_t N, int64_t K, int64
         return check_launch("mul_mat gemm");
     };
     switch (wtype) {
-        case TYPE_Q8_0: return go(k_gemm_q<TYPE_Q8_0, NW, WM, BK>);
-        case TYPE_Q4_K: return go(k_gemm_q<TYPE_Q4_K, NW, WM, BK>);
-        default: return go(k_gemm_q<TYPE_Q6_K, NW, WM, BK>);
+        case TYPE_Q8_0: return go(k_gemm_q<TYPE_Q8_0, NW, WM, BK, BM>);
+        case TYPE_Q4_K: return go(k_gemm_q<TYPE_Q4_K, NW, WM, BK, BM>);
+        default: return go(k_gemm_q<TYPE_Q6_K, NW, WM, BK, BM>);
     }
 }
 
@@ -413,11 +415,11 @@ static int gemm_launch(int wtype, const uint8_t * wb, int64_t N, int64_t K, int6
     if (tiles256 >= 256) {
         return launch_gemm<8, 2, 64>(wtype, wb, N, K, rs, xh, M, bias, res, ldr, y, ldy, stream);
     }
-    // small grids: 128-wide K steps, twice the MFMA work per load round trip
-    if (K % 128 == 0) {
-        return launch_gemm<4, 2, 128>(wtype, wb, N, K, rs, xh, M, bias, res, ldr, y, ldy, stream);
-    }
-    return launch_gemm<4, 2, 64>(wtype, wb, N, K, rs, xh, M, bias, res, ldr, y, ldy, stream);
+    // small grids (the DiT's 2048-row projections at 1380 tokens: 176 tiles of
+    // 128 x 128): 64-token x 128-row tiles, twice the workgroups, three per CU
+    // in LDS (a 128-wide K step on 128 x 128 tiles: 2.6 % slower per DiT block;
+    // 32 x 128 and 128 x 256 tiles: 1 % and 25 % slower)
+    return launch_gemm<4, 2, 64, 64>(wtype, wb, N, K, rs, xh, M, bias, res, ldr, y, ldy, stream);
 }
 
 int gemm_q_h(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const void * xh, int64_t M, float * y,
