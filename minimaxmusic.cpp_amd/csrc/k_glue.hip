@@ -945,6 +945,41 @@ extern "C" int mmhip_rms_norm_quant(const mmhip_view * x, const mmhip_view * w, 
     return rms_norm_launch(x, w, eps, dst, type, xq, (hipStream_t) stream);
 }
 
+// The same with the angle of pair j at position i2 computed once for a group
+// of RH heads (the DiT's 32 heads, the prefill's 32 / 8): thread (j, head
+// group, i2, i3) rotates pair j of those heads and copies their tail
+// elements j, j + half, .. past n_dims.  Same theta recurrence, same cosf /
+// sinf, same products: bit-identical to k_rope_neox.
+constexpr int RH = 8;
+
+__global__ void k_rope_neox_heads(TV x, const int32_t * __restrict__ pos, int n_dims, float theta_scale,
+                                  float * __restrict__ dst, int64_t n_items) {
+#pragma clang fp contract(off)
+    const int64_t D = x.ne[0], half = n_dims / 2, ng = (x.ne[1] + RH - 1) / RH;
+    for (int64_t t = blockIdx.x * (int64_t) blockDim.x + threadIdx.x; t < n_items;
+         t += (int64_t) gridDim.x * blockDim.x) {
+        const int64_t j = t % half, hg = (t / half) % ng, i2 = (t / (half * ng)) % x.ne[2];
+        const int64_t i3 = t / (half * ng * x.ne[2]);
+        float         theta = (float) pos[i2];
+        for (int64_t k = 0; k < j; k++) {
+            theta *= theta_scale;
+        }
+        const float   c = cosf(theta), sn = sinf(theta);
+        const int64_t h1 = min((hg + 1) * RH, x.ne[1]);
+        for (int64_t i1 = hg * RH; i1 < h1; i1++) {
+            const char * xr = at(x, 0, i1, i2, i3);
+            float *      dr = dst + ((i3 * x.ne[2] + i2) * x.ne[1] + i1) * D;
+            const float  x0 = *(const float *) (xr + j * x.nb[0]);
+            const float  x1 = *(const float *) (xr + (j + half) * x.nb[0]);
+            dr[j]           = x0 * c - x1 * sn;
+            dr[j + half]    = x0 * sn + x1 * c;
+            for (int64_t i = n_dims + j; i < D; i += half) {
+                dr[i] = *(const float *) (xr + i * x.nb[0]);
+            }
+        }
+    }
+}
+
 extern "C" int mmhip_rope_neox(const mmhip_view * x, const int32_t * pos, int n_dims, float theta_scale, float * dst,
                                void * stream) {
     MMHIP_API_BEGIN();
@@ -955,6 +990,12 @@ extern "C" int mmhip_rope_neox(const mmhip_view * x, const int32_t * pos, int n_
     const int64_t total = rows * (n_dims / 2 + (x->ne[0] - n_dims));
     if (total == 0) {
         return MMHIP_OK;
+    }
+    if (x->ne[1] >= RH && n_dims >= 2) {
+        const int64_t items = (n_dims / 2) * ((x->ne[1] + RH - 1) / RH) * x->ne[2] * x->ne[3];
+        hipLaunchKernelGGL(k_rope_neox_heads, dim3(grid_for(items, 256)), dim3(256), 0, (hipStream_t) stream, tv(x), pos,
+                           n_dims, theta_scale, dst, items);
+        return check_launch("rope");
     }
     hipLaunchKernelGGL(k_rope_neox, dim3(grid_for(total, 256)), dim3(256), 0, (hipStream_t) stream, tv(x), pos, n_dims,
                        theta_scale, dst);
