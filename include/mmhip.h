@@ -82,6 +82,12 @@ int    mmhip_mul_mat(int type, const void * W, int64_t N, int64_t K, int64_t w_r
  * store: y = (x W^T + bias[n]) + r[m*ldr + n], each ADD rounded as its op;
  * bias and r may be NULL (r may alias y).  The DiT's projection biases and
  * residuals (src/dit.h:228-229, :237-245).  Workspace as mmhip_mul_mat. */
+/* MUL_MAT over BF16 weight rows (ldw elements apart) at 1..16 activation
+ * rows: ggml's BF16 dot (activations rounded to bf16, f32 products summed in
+ * f32); the BF16 files of the depth decoder and LM (src/depth-decoder.h:206-257,
+ * src/qwen3-lm.h:743-856).  K % 8 == 0, 16-byte aligned rows. */
+int    mmhip_mul_mat_bf16(const void * W, int64_t N, int64_t K, int64_t ldw, const float * x, int64_t ldx, int64_t M,
+                          float * y, int64_t ldy, void * stream);
 int    mmhip_mul_mat_bias_add(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const float * x,
                               int64_t ldx, int64_t M, const float * bias, const float * r, int64_t ldr, float * y,
                               int64_t ldy, void * ws, size_t ws_bytes, void * stream);

@@ -527,6 +527,13 @@ bool supports(const struct ggml_tensor * op) {
         case GGML_OP_TRANSPOSE:
             return true;
         case GGML_OP_MUL_MAT:
+            if (op->src[0]->type == GGML_TYPE_BF16) {  // BF16 weights at up to 16 tokens
+                const struct ggml_tensor * w = op->src[0];
+                const struct ggml_tensor * x = op->src[1];
+                return w->nb[0] == 2 && w->ne[2] == 1 && w->ne[3] == 1 && w->ne[0] % 8 == 0 && w->nb[1] % 16 == 0 &&
+                       x->type == GGML_TYPE_F32 && mm_collapsible(x) && x->ne[1] * x->ne[2] * x->ne[3] <= 16 &&
+                       op->type == GGML_TYPE_F32 && ggml_is_contiguous(op);
+            }
             if (op->src[0]->type == GGML_TYPE_F32) {  // activation x activation
                 return op->src[1]->type == GGML_TYPE_F32 && op->src[0]->nb[0] == 4 && op->src[1]->nb[0] == 4 &&
                        op->type == GGML_TYPE_F32 && ggml_is_contiguous(op);
@@ -629,6 +636,14 @@ int run_node(mi_backend * c, const struct ggml_tensor * n) {
         case GGML_OP_TRANSPOSE:
             return MMHIP_OK;
         case GGML_OP_MUL_MAT:
+            if (n->src[0]->type == GGML_TYPE_BF16) {
+                const struct ggml_tensor * w = n->src[0];
+                const struct ggml_tensor * x = n->src[1];
+                rc = mmhip_mul_mat_bf16(w->data, w->ne[1], w->ne[0], (int64_t) (w->nb[1] / 2), (const float *) x->data,
+                                        (int64_t) (x->nb[1] / 4), x->ne[1] * x->ne[2] * x->ne[3], (float *) n->data,
+                                        w->ne[1], s);
+                break;
+            }
             if (n->src[0]->type == GGML_TYPE_F32) {
                 mmhip_view a = view_of(n->src[0]), b = view_of(n->src[1]);
                 rc           = mmhip_mul_mat_f32(&a, &b, (float *) n->data, s);

@@ -858,6 +858,79 @@ bool gemv_supported(int wtype, int64_t N, int64_t K, int64_t rs, const void * W)
     return rs % align == 0 && ((uintptr_t) W) % align == 0;
 }
 
+// f32 -> bf16 as ggml rounds it: nearest-even on the upper 16 bits, NaN kept
+// quiet.
+__device__ __forceinline__ float round_bf16(float v) {
+    uint32_t u = __float_as_uint(v);
+    if ((u & 0x7fffffffu) > 0x7f800000u) {
+        u = (u | 0x00400000u) & 0xffff0000u;
+    } else {
+        u = (u + (0x7fffu + ((u >> 16) & 1u))) & 0xffff0000u;
+    }
+    return __uint_as_float(u);
+}
+
+// GGML_OP_MUL_MAT over BF16 weights at 1..16 activation rows (the BF16 files
+// of the depth decoder and the LM, src/depth-decoder.h:206-257): ggml's BF16
+// dot rounds the activations to bf16 and sums the f32 products of the pairs.
+// One wave per weight row; lane l takes the 8-element chunks l, l + 64, ..;
+// the activation chunks come from cache.  Sums: per-lane f32, then a
+// symmetric wave reduction.
+constexpr int BF16_MAXM = 16;
+
+__global__ __launch_bounds__(256) void k_gemv_bf16(const uint16_t * __restrict__ W, int64_t N, int64_t K, int64_t ldw,
+                                                   const float * __restrict__ x, int64_t ldx, int M,
+                                                   float * __restrict__ y, int64_t ldy) {
+#pragma clang fp contract(off)
+    const int64_t row  = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int     lane = threadIdx.x & 63;
+    if (row >= N) {
+        return;  // wave-uniform
+    }
+    const uint16_t * wr = W + row * ldw;
+    float            acc[BF16_MAXM];
+#pragma unroll
+    for (int c = 0; c < BF16_MAXM; c++) {
+        acc[c] = 0.0f;
+    }
+    for (int64_t k = (int64_t) lane * 8; k < K; k += 512) {
+        const uint4 wv = *(const uint4 *) (wr + k);
+        float       wf[8];
+        const uint32_t ww[4] = { wv.x, wv.y, wv.z, wv.w };
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            wf[2 * e]     = __uint_as_float(ww[e] << 16);
+            wf[2 * e + 1] = __uint_as_float(ww[e] & 0xffff0000u);
+        }
+#pragma unroll
+        for (int c = 0; c < BF16_MAXM; c++) {
+            if (c < M) {
+                const float4_t a = *(const float4_t *) (x + c * ldx + k);
+                const float4_t b = *(const float4_t *) (x + c * ldx + k + 4);
+                float          s = acc[c];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    s = s + wf[e] * round_bf16(a[e]);
+                }
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    s = s + wf[4 + e] * round_bf16(b[e]);
+                }
+                acc[c] = s;
+            }
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < BF16_MAXM; c++) {
+        if (c < M) {
+            const float v = wave_sum(acc[c]);
+            if (lane == 0) {
+                y[c * ldy + row] = v;
+            }
+        }
+    }
+}
+
 int gemv_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const ActPtrs & x, int64_t M, float * y,
            int64_t ldy, hipStream_t stream, const float * r, int64_t ldr) {
     if (!gemv_supported(wtype, N, K, rs, W) || M < 1 || ldy < N) {
@@ -892,6 +965,27 @@ int gemv_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const Ac
 }  // namespace mmhip
 
 using namespace mmhip;
+
+extern "C" int mmhip_mul_mat_bf16(const void * W, int64_t N, int64_t K, int64_t ldw, const float * x, int64_t ldx,
+                                  int64_t M, float * y, int64_t ldy, void * stream) {
+    MMHIP_API_BEGIN();
+    if (!W || !x || !y || N <= 0 || K <= 0 || M <= 0 || ldw < K || ldx < K || ldy < N) {
+        return set_error(MMHIP_ERR_INVALID, "mul_mat_bf16: bad arguments N=%lld K=%lld M=%lld", (long long) N,
+                         (long long) K, (long long) M);
+    }
+    if (M > BF16_MAXM || K % 8 != 0 || ldw % 8 != 0 || ldx % 4 != 0 || ((uintptr_t) W) % 16 != 0 ||
+        ((uintptr_t) x) % 16 != 0) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat_bf16: M=%lld K=%lld (M <= 16, K %% 8 == 0, aligned rows)",
+                         (long long) M, (long long) K);
+    }
+    const int64_t nwg = (N + 3) / 4;
+    if (nwg > 0x7fffffff) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat_bf16: too many rows");
+    }
+    hipLaunchKernelGGL(k_gemv_bf16, dim3((unsigned) nwg), dim3(256), 0, (hipStream_t) stream, (const uint16_t *) W, N,
+                       K, ldw, x, ldx, (int) M, y, ldy);
+    return check_launch("mul_mat_bf16");
+}
 
 extern "C" int mmhip_mul_mat_q(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const void * xq,
                                int64_t M, float * y, int64_t ldy, void * stream) {

@@ -156,3 +156,60 @@ def test_gemm_bias_add_rejects_gemv_token_counts(mm):
     d = torch.zeros(1 << 16, device="cuda")
     P = ctypes.c_void_p(d.data_ptr())
     assert L.mmhip_mul_mat_bias_add(8, P, 64, 256, 272, P, 256, 16, P, None, 0, P, 64, P, 1 << 18, None) != 0
+
+
+@pytest.mark.parametrize("N,K,M", [(4096, 4096, 2), (1000, 2048, 16), (37, 520, 5), (6144, 4096, 16), (300, 1024, 1)])
+def test_mul_mat_bf16_weights(mm, N, K, M):
+    """MUL_MAT over BF16 weights at 1..16 tokens (ggml's BF16 dot: the
+    activations rounded to bf16 -- torch's bfloat16 rounding, nearest-even
+    -- and the products summed in f32) against float64 of the same bf16
+    operands: max-rel 1e-5."""
+    import ctypes
+
+    g = torch.Generator().manual_seed(N + K + M)
+    W = (torch.randn((N, K), generator=g) * 0.02).bfloat16()
+    x = torch.randn((M, K), generator=g)
+    ref = x.bfloat16().double() @ W.double().T
+    L = mm.load()
+    tw, tx = W.cuda(), x.cuda()
+    y = torch.empty((M, N), device="cuda")
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert L.mmhip_mul_mat_bf16(P(tw), N, K, K, P(tx), K, M, P(y), N, st) == 0, L.mmhip_last_error()
+    torch.cuda.synchronize()
+    assert float((y.cpu().double() - ref).abs().max() / ref.abs().max()) < 1e-5
+
+
+def test_mul_mat_bf16_rejects_and_backend(mm, pkg):
+    """Over 16 tokens or K % 8 != 0 is refused; through the backend a BF16
+    MUL_MAT node gives the C-ABI result bit for bit."""
+    import ctypes
+    import importlib
+
+    L = mm.load()
+    d = torch.zeros(1 << 16, device="cuda")
+    P = ctypes.c_void_p(d.data_ptr())
+    assert L.mmhip_mul_mat_bf16(P, 64, 256, 256, P, 256, 17, P, 64, None) != 0
+    assert L.mmhip_mul_mat_bf16(P, 64, 250, 256, P, 256, 4, P, 64, None) != 0
+    og = importlib.import_module(pkg.__name__ + ".opgraph")
+    N, K, M = 512, 2048, 6
+    g = torch.Generator().manual_seed(5)
+    W = (torch.randn((N, K), generator=g) * 0.02).bfloat16()
+    x = torch.randn((M, K), generator=g)
+    gr = og.OpGraph()
+    try:
+        tw = gr.tensor(30, [K, N])  # GGML_TYPE_BF16
+        tx = gr.tensor(og.F32, [K, M])
+        out = gr.mul_mat(tw, tx)
+        gr.build([out])
+        gr.set(tw, W.view(torch.int16).numpy())
+        gr.set(tx, x.numpy())
+        gr.compute()
+        yb = gr.get(out).reshape(M, N)
+    finally:
+        gr.close()
+    y = torch.empty((M, N), device="cuda")
+    Q = lambda t: ctypes.c_void_p(t.data_ptr())
+    assert L.mmhip_mul_mat_bf16(Q(W.cuda()), N, K, K, Q(x.cuda()), K, M, Q(y), N, None) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(yb, y.cpu().numpy())
