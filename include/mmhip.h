@@ -297,6 +297,17 @@ int mmhip_diag_mask_inf(const mmhip_view * a, int n_past, float * dst, void * st
 /* GGML_OP_SOFT_MAX without mask, scale 1 (src/depth-decoder.h:217, :348):
  * row softmax with ggml-CPU's steps (f32 exp, double sum); dst contiguous. */
 int mmhip_soft_max(const mmhip_view * a, float * dst, void * stream);
+/* The depth decoder's in-graph CFG sampler (src/depth-decoder.h:345-361):
+ * GGML_OP_ARGSORT descending (I32 indices, rows of <= 4096; equal values in
+ * ascending index order), GGML_OP_CUMSUM along dim 0 (running f32 sum),
+ * GGML_OP_SUM of all elements (double accumulation, dst[0]), the STEP unary
+ * (x > 0 ? 1 : 0) and the casts to I32 (truncation) and back; dst contiguous. */
+int mmhip_argsort_desc(const mmhip_view * a, int32_t * dst, void * stream);
+int mmhip_cumsum(const mmhip_view * a, float * dst, void * stream);
+int mmhip_sum(const mmhip_view * a, float * dst, void * stream);
+int mmhip_step(const mmhip_view * a, float * dst, void * stream);
+int mmhip_cast_i32(const mmhip_view * a, int32_t * dst, void * stream);
+int mmhip_cast_f32_of_i32(const mmhip_view * a, float * dst, void * stream);
 /* GGML_OP_CONCAT of f32 a and b along dim 0..3 (the DiT input channel concat
  * and the timestep token, src/dit.h:262-264, :273); dst contiguous. */
 int mmhip_concat(const mmhip_view * a, const mmhip_view * b, int dim, float * dst, void * stream);

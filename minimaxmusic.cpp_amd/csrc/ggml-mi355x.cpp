@@ -550,6 +550,15 @@ bool supports(const struct ggml_tensor * op) {
         }
         case GGML_OP_DIAG_MASK_INF:
             return op->src[0]->type == GGML_TYPE_F32 && op->type == GGML_TYPE_F32 && ggml_is_contiguous(op);
+        case GGML_OP_ARGSORT:
+            return op->src[0]->type == GGML_TYPE_F32 && op->op_params[0] == GGML_SORT_ORDER_DESC &&
+                   op->src[0]->ne[0] <= 4096 && op->type == GGML_TYPE_I32 && ggml_is_contiguous(op);
+        case GGML_OP_CUMSUM:
+        case GGML_OP_SUM:
+            return op->src[0]->type == GGML_TYPE_F32 && op->type == GGML_TYPE_F32 && ggml_is_contiguous(op);
+        case GGML_OP_UNARY:
+            return op->op_params[0] == GGML_UNARY_OP_STEP && op->src[0]->type == GGML_TYPE_F32 &&
+                   op->type == GGML_TYPE_F32 && ggml_is_contiguous(op);
         case GGML_OP_ADD:
         case GGML_OP_SUB:
         case GGML_OP_MUL:
@@ -561,8 +570,18 @@ bool supports(const struct ggml_tensor * op) {
             return supports_rope(op);
         case GGML_OP_CPY:
         case GGML_OP_CONT:
+            if (op->type == GGML_TYPE_I32) {  // ggml_cast to I32 (the sampler's pick), CONT of the top-k view
+                return (op->src[0]->type == GGML_TYPE_F32 || op->src[0]->type == GGML_TYPE_I32) &&
+                       ggml_is_contiguous(op);
+            }
+            if (op->src[0]->type == GGML_TYPE_I32) {  // the top-k indices as F32
+                return op->type == GGML_TYPE_F32 && ggml_is_contiguous(op);
+            }
             return is_f32_or_f16(op->src[0]->type) && is_f32_or_f16(op->type);
         case GGML_OP_GET_ROWS:
+            if (op->src[0]->type == GGML_TYPE_I32) {  // rows of indices (the sampler's gathers)
+                return op->src[1]->type == GGML_TYPE_I32 && op->type == GGML_TYPE_I32 && ggml_is_contiguous(op);
+            }
             return (is_f32_or_f16(op->src[0]->type) || is_repacked(op->src[0]->type)) &&
                    op->src[1]->type == GGML_TYPE_I32 && op->type == GGML_TYPE_F32 && ggml_is_contiguous(op);
         case GGML_OP_SET_ROWS:
@@ -677,6 +696,22 @@ int run_node(mi_backend * c, const struct ggml_tensor * n) {
         }
         case GGML_OP_CPY:
         case GGML_OP_CONT: {
+            if (n->type == GGML_TYPE_I32 && n->src[0]->type == GGML_TYPE_I32) {
+                // 4-byte words moved as they are (the f32 copy path does no arithmetic)
+                mmhip_view src = view_of(n->src[0]), dst = view_of(n);
+                rc             = mmhip_cpy(&src, GGML_TYPE_F32, &dst, GGML_TYPE_F32, s);
+                break;
+            }
+            if (n->type == GGML_TYPE_I32) {
+                mmhip_view a = view_of(n->src[0]);
+                rc           = mmhip_cast_i32(&a, (int32_t *) n->data, s);
+                break;
+            }
+            if (n->src[0]->type == GGML_TYPE_I32) {
+                mmhip_view a = view_of(n->src[0]);
+                rc           = mmhip_cast_f32_of_i32(&a, (float *) n->data, s);
+                break;
+            }
             mmhip_view src = view_of(n->src[0]), dst = view_of(n);
             rc = mmhip_cpy(&src, n->src[0]->type, &dst, n->type, s);
             break;
@@ -732,6 +767,26 @@ int run_node(mi_backend * c, const struct ggml_tensor * n) {
         case GGML_OP_SOFT_MAX: {
             mmhip_view a = view_of(n->src[0]);
             rc           = mmhip_soft_max(&a, (float *) n->data, s);
+            break;
+        }
+        case GGML_OP_ARGSORT: {
+            mmhip_view a = view_of(n->src[0]);
+            rc           = mmhip_argsort_desc(&a, (int32_t *) n->data, s);
+            break;
+        }
+        case GGML_OP_CUMSUM: {
+            mmhip_view a = view_of(n->src[0]);
+            rc           = mmhip_cumsum(&a, (float *) n->data, s);
+            break;
+        }
+        case GGML_OP_SUM: {
+            mmhip_view a = view_of(n->src[0]);
+            rc           = mmhip_sum(&a, (float *) n->data, s);
+            break;
+        }
+        case GGML_OP_UNARY: {
+            mmhip_view a = view_of(n->src[0]);
+            rc           = mmhip_step(&a, (float *) n->data, s);
             break;
         }
         case GGML_OP_DIAG_MASK_INF: {

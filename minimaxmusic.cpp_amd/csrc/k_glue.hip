@@ -449,6 +449,115 @@ __global__ __launch_bounds__(256) void k_soft_max_rows(TV a, int64_t rows, float
     }
 }
 
+// The depth decoder's in-graph sampler (src/depth-decoder.h:345-361).
+// GGML_OP_ARGSORT, descending: one workgroup per row of n <= 4096 f32 values,
+// a bitonic sort of (value, index) pairs in LDS padded with -inf; equal values
+// keep ascending index order.  dst: contiguous I32 rows.
+constexpr int SORT_MAX = 4096;
+
+__global__ __launch_bounds__(256) void k_argsort_desc(TV a, int32_t * __restrict__ dst) {
+    __shared__ float   sv[SORT_MAX];
+    __shared__ int32_t si[SORT_MAX];
+    const int64_t      row = blockIdx.x;
+    const int64_t      n   = a.ne[0];
+    const int64_t      i1 = row % a.ne[1], i2 = (row / a.ne[1]) % a.ne[2], i3 = row / (a.ne[1] * a.ne[2]);
+    const char *       xr  = at(a, 0, i1, i2, i3);
+    int                p2  = 1;
+    while (p2 < n) {
+        p2 <<= 1;
+    }
+    for (int i = threadIdx.x; i < p2; i += 256) {
+        sv[i] = i < n ? *(const float *) (xr + (int64_t) i * a.nb[0]) : -INFINITY;
+        si[i] = i;
+    }
+    __syncthreads();
+    // "before": greater value first, then the lower index
+    auto before = [](float va, int ia, float vb, int ib) { return va > vb || (va == vb && ia < ib); };
+    for (int size = 2; size <= p2; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = threadIdx.x; i < p2; i += 256) {
+                const int j = i ^ stride;
+                if (j > i) {
+                    const bool desc = (i & size) == 0;  // this run sorts in "before" order
+                    const bool swap = desc ? before(sv[j], si[j], sv[i], si[i]) : before(sv[i], si[i], sv[j], si[j]);
+                    if (swap) {
+                        const float tv = sv[i];
+                        sv[i]          = sv[j];
+                        sv[j]          = tv;
+                        const int ti   = si[i];
+                        si[i]          = si[j];
+                        si[j]          = ti;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    for (int i = threadIdx.x; i < n; i += 256) {
+        dst[row * n + i] = si[i];
+    }
+}
+
+// GGML_OP_CUMSUM along dim 0: one thread per row, the running f32 sum.
+__global__ void k_cumsum_rows(TV a, int64_t rows, float * __restrict__ dst) {
+#pragma clang fp contract(off)
+    for (int64_t r = blockIdx.x * (int64_t) blockDim.x + threadIdx.x; r < rows; r += (int64_t) gridDim.x * blockDim.x) {
+        const int64_t i1 = r % a.ne[1], i2 = (r / a.ne[1]) % a.ne[2], i3 = r / (a.ne[1] * a.ne[2]);
+        const char *  xr = at(a, 0, i1, i2, i3);
+        float         acc = 0.0f;
+        for (int64_t i = 0; i < a.ne[0]; i++) {
+            acc = acc + *(const float *) (xr + i * a.nb[0]);
+            dst[r * a.ne[0] + i] = acc;
+        }
+    }
+}
+
+// GGML_OP_SUM: all elements summed in double, one workgroup.
+__global__ __launch_bounds__(256) void k_sum_all(TV a, int64_t n, float * __restrict__ dst) {
+    __shared__ double part[4];
+    double            acc = 0.0;
+    for (int64_t t = threadIdx.x; t < n; t += 256) {
+        int64_t i0, i1, i2, i3;
+        unravel(t, a.ne, i0, i1, i2, i3);
+        acc += (double) *(const float *) at(a, i0, i1, i2, i3);
+    }
+    acc = wave_sum_d(acc);
+    if ((threadIdx.x & 63) == 0) {
+        part[threadIdx.x >> 6] = acc;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        dst[0] = (float) (((part[0] + part[1]) + part[2]) + part[3]);
+    }
+}
+
+// GGML_UNARY_OP_STEP: x > 0 ? 1 : 0; dst contiguous.
+__global__ void k_step(TV a, int64_t n, float * __restrict__ dst) {
+    for (int64_t t = blockIdx.x * (int64_t) blockDim.x + threadIdx.x; t < n; t += (int64_t) gridDim.x * blockDim.x) {
+        int64_t i0, i1, i2, i3;
+        unravel(t, a.ne, i0, i1, i2, i3);
+        dst[t] = *(const float *) at(a, i0, i1, i2, i3) > 0.0f ? 1.0f : 0.0f;
+    }
+}
+
+// CPY I32 -> f32 (ggml_cast of the top-k indices to F32); dst contiguous.
+__global__ void k_cast_f32_of_i32(TV a, int64_t n, float * __restrict__ dst) {
+    for (int64_t t = blockIdx.x * (int64_t) blockDim.x + threadIdx.x; t < n; t += (int64_t) gridDim.x * blockDim.x) {
+        int64_t i0, i1, i2, i3;
+        unravel(t, a.ne, i0, i1, i2, i3);
+        dst[t] = (float) *(const int32_t *) at(a, i0, i1, i2, i3);
+    }
+}
+
+// CPY f32 -> I32 (ggml_cast to I32): truncation toward zero; dst contiguous.
+__global__ void k_cast_i32(TV a, int64_t n, int32_t * __restrict__ dst) {
+    for (int64_t t = blockIdx.x * (int64_t) blockDim.x + threadIdx.x; t < n; t += (int64_t) gridDim.x * blockDim.x) {
+        int64_t i0, i1, i2, i3;
+        unravel(t, a.ne, i0, i1, i2, i3);
+        dst[t] = (int32_t) *(const float *) at(a, i0, i1, i2, i3);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Per-head rows of the QKV projection (the CONT / RMS_NORM / MUL / ROPE /
 // SET_ROWS chain of the attention block): one wave per row (h, t) of D = 64 *
@@ -1038,6 +1147,9 @@ extern "C" int mmhip_cpy(const mmhip_view * src, int src_type, const mmhip_view 
 extern "C" int mmhip_get_rows(int src_type, const mmhip_view * src, const mmhip_view * ids, float * dst,
                               void * stream) {
     MMHIP_API_BEGIN();
+    if (src_type == 26) {
+        src_type = TYPE_F32;  // I32 rows: moved as 4-byte words, bit for bit
+    }
     const bool q = src_type == TYPE_Q8_0 || src_type == TYPE_Q4_K || src_type == TYPE_Q6_K;
     if (!src || !ids || !dst || !(q || src_type == TYPE_F32 || src_type == TYPE_F16) ||
         (src_type == TYPE_Q8_0 && src->ne[0] % 32 != 0) || ((src_type == TYPE_Q4_K || src_type == TYPE_Q6_K) &&
@@ -1173,6 +1285,86 @@ extern "C" int mmhip_soft_max(const mmhip_view * a, float * dst, void * stream) 
     hipLaunchKernelGGL(k_soft_max_rows, dim3((unsigned) ((rows + 3) / 4)), dim3(256), 0, (hipStream_t) stream, tv(a),
                        rows, dst);
     return check_launch("soft_max");
+}
+
+extern "C" int mmhip_argsort_desc(const mmhip_view * a, int32_t * dst, void * stream) {
+    MMHIP_API_BEGIN();
+    if (!a || !dst || a->ne[0] <= 0) {
+        return set_error(MMHIP_ERR_INVALID, "argsort: bad arguments");
+    }
+    if (a->ne[0] > SORT_MAX) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "argsort: rows of %lld > %d", (long long) a->ne[0], SORT_MAX);
+    }
+    const int64_t rows = a->ne[1] * a->ne[2] * a->ne[3];
+    if (rows == 0) {
+        return MMHIP_OK;
+    }
+    if (rows >= ((int64_t) 1 << 31)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "argsort: too many rows");
+    }
+    hipLaunchKernelGGL(k_argsort_desc, dim3((unsigned) rows), dim3(256), 0, (hipStream_t) stream, tv(a), dst);
+    return check_launch("argsort");
+}
+
+extern "C" int mmhip_cumsum(const mmhip_view * a, float * dst, void * stream) {
+    MMHIP_API_BEGIN();
+    if (!a || !dst) {
+        return set_error(MMHIP_ERR_INVALID, "cumsum: bad arguments");
+    }
+    const int64_t rows = a->ne[1] * a->ne[2] * a->ne[3];
+    if (rows == 0 || a->ne[0] == 0) {
+        return MMHIP_OK;
+    }
+    hipLaunchKernelGGL(k_cumsum_rows, dim3(grid_for(rows, 64)), dim3(64), 0, (hipStream_t) stream, tv(a), rows, dst);
+    return check_launch("cumsum");
+}
+
+extern "C" int mmhip_sum(const mmhip_view * a, float * dst, void * stream) {
+    MMHIP_API_BEGIN();
+    if (!a || !dst) {
+        return set_error(MMHIP_ERR_INVALID, "sum: bad arguments");
+    }
+    hipLaunchKernelGGL(k_sum_all, dim3(1), dim3(256), 0, (hipStream_t) stream, tv(a), nel(a), dst);
+    return check_launch("sum");
+}
+
+extern "C" int mmhip_step(const mmhip_view * a, float * dst, void * stream) {
+    MMHIP_API_BEGIN();
+    if (!a || !dst) {
+        return set_error(MMHIP_ERR_INVALID, "step: bad arguments");
+    }
+    const int64_t n = nel(a);
+    if (n == 0) {
+        return MMHIP_OK;
+    }
+    hipLaunchKernelGGL(k_step, dim3(grid_for(n, 256)), dim3(256), 0, (hipStream_t) stream, tv(a), n, dst);
+    return check_launch("step");
+}
+
+extern "C" int mmhip_cast_i32(const mmhip_view * a, int32_t * dst, void * stream) {
+    MMHIP_API_BEGIN();
+    if (!a || !dst) {
+        return set_error(MMHIP_ERR_INVALID, "cast_i32: bad arguments");
+    }
+    const int64_t n = nel(a);
+    if (n == 0) {
+        return MMHIP_OK;
+    }
+    hipLaunchKernelGGL(k_cast_i32, dim3(grid_for(n, 256)), dim3(256), 0, (hipStream_t) stream, tv(a), n, dst);
+    return check_launch("cast_i32");
+}
+
+extern "C" int mmhip_cast_f32_of_i32(const mmhip_view * a, float * dst, void * stream) {
+    MMHIP_API_BEGIN();
+    if (!a || !dst) {
+        return set_error(MMHIP_ERR_INVALID, "cast_f32_of_i32: bad arguments");
+    }
+    const int64_t n = nel(a);
+    if (n == 0) {
+        return MMHIP_OK;
+    }
+    hipLaunchKernelGGL(k_cast_f32_of_i32, dim3(grid_for(n, 256)), dim3(256), 0, (hipStream_t) stream, tv(a), n, dst);
+    return check_launch("cast_f32_of_i32");
 }
 
 extern "C" int mmhip_concat(const mmhip_view * a, const mmhip_view * b, int dim, float * dst, void * stream) {

@@ -158,6 +158,10 @@ extern "C" const char * ggml_op_name(enum ggml_op op) {
         case GGML_OP_SCALE: return "SCALE";
         case GGML_OP_CLAMP: return "CLAMP";
         case GGML_OP_SOFT_MAX: return "SOFT_MAX";
+        case GGML_OP_ARGSORT: return "ARGSORT";
+        case GGML_OP_CUMSUM: return "CUMSUM";
+        case GGML_OP_SUM: return "SUM";
+        case GGML_OP_UNARY: return "UNARY";
         case GGML_OP_DIAG_MASK_INF: return "DIAG_MASK_INF";
         case GGML_OP_NORM: return "NORM";
         case GGML_OP_CONCAT: return "CONCAT";
@@ -582,6 +586,60 @@ extern "C" struct ggml_tensor * ggml_soft_max(struct ggml_context * ctx, struct 
     const float          params[2] = { 1.0f, 0.0f };
     set_op_params(r, params, sizeof(params));
     r->op     = GGML_OP_SOFT_MAX;
+    r->src[0] = a;
+    return r;
+}
+
+// a * s + b; op_params = {s, b} (GGML_OP_SCALE)
+extern "C" struct ggml_tensor * ggml_scale_bias(struct ggml_context * ctx, struct ggml_tensor * a, float s, float b) {
+    struct ggml_tensor * r         = ggml_dup_tensor(ctx, a);
+    const float          params[2] = { s, b };
+    set_op_params(r, params, sizeof(params));
+    r->op     = GGML_OP_SCALE;
+    r->src[0] = a;
+    return r;
+}
+
+// indices (I32) that sort each row; op_params[0] = order
+extern "C" struct ggml_tensor * ggml_argsort(struct ggml_context * ctx, struct ggml_tensor * a,
+                                             enum ggml_sort_order order) {
+    struct ggml_tensor * r         = ggml_new_tensor(ctx, GGML_TYPE_I32, GGML_MAX_DIMS, a->ne);
+    const int32_t        params[1] = { (int32_t) order };
+    set_op_params(r, params, sizeof(params));
+    r->op     = GGML_OP_ARGSORT;
+    r->src[0] = a;
+    return r;
+}
+
+// the first k indices of the descending argsort of each row (a view)
+extern "C" struct ggml_tensor * ggml_argsort_top_k(struct ggml_context * ctx, struct ggml_tensor * a, int k) {
+    CORE_ASSERT(k >= 1 && k <= a->ne[0]);
+    struct ggml_tensor * s = ggml_argsort(ctx, a, GGML_SORT_ORDER_DESC);
+    return ggml_view_4d(ctx, s, k, s->ne[1], s->ne[2], s->ne[3], s->nb[1], s->nb[2], s->nb[3], 0);
+}
+
+// running sum along dim 0
+extern "C" struct ggml_tensor * ggml_cumsum(struct ggml_context * ctx, struct ggml_tensor * a) {
+    struct ggml_tensor * r = ggml_dup_tensor(ctx, a);
+    r->op                  = GGML_OP_CUMSUM;
+    r->src[0]              = a;
+    return r;
+}
+
+// the sum of all elements, a one-element tensor
+extern "C" struct ggml_tensor * ggml_sum(struct ggml_context * ctx, struct ggml_tensor * a) {
+    struct ggml_tensor * r = ggml_new_tensor_1d(ctx, a->type, 1);
+    r->op                  = GGML_OP_SUM;
+    r->src[0]              = a;
+    return r;
+}
+
+// x > 0 ? 1 : 0 (GGML_OP_UNARY, op_params[0] = GGML_UNARY_OP_STEP)
+extern "C" struct ggml_tensor * ggml_step(struct ggml_context * ctx, struct ggml_tensor * a) {
+    struct ggml_tensor * r         = ggml_dup_tensor(ctx, a);
+    const int32_t        params[1] = { (int32_t) GGML_UNARY_OP_STEP };
+    set_op_params(r, params, sizeof(params));
+    r->op     = GGML_OP_UNARY;
     r->src[0] = a;
     return r;
 }

@@ -101,6 +101,12 @@ SIGNATURES = {
     "mmhip_mul_mat_f32": (_i32, [_VP, _VP, _vp, _vp]),
     "mmhip_diag_mask_inf": (_i32, [_VP, _i32, _vp, _vp]),
     "mmhip_soft_max": (_i32, [_VP, _vp, _vp]),
+    "mmhip_argsort_desc": (_i32, [_VP, _vp, _vp]),
+    "mmhip_cumsum": (_i32, [_VP, _vp, _vp]),
+    "mmhip_sum": (_i32, [_VP, _vp, _vp]),
+    "mmhip_step": (_i32, [_VP, _vp, _vp]),
+    "mmhip_cast_i32": (_i32, [_VP, _vp, _vp]),
+    "mmhip_cast_f32_of_i32": (_i32, [_VP, _vp, _vp]),
     "mmhip_clamp": (_i32, [_VP, _f32, _f32, _vp, _vp]),
     # include/mmhip_synth.h
     "mmhip_synth_gguf": (_i32, [_i32, _vp, _i64, ctypes.c_uint64, _vp]),

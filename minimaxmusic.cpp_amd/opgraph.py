@@ -65,6 +65,11 @@ def _load():
         "ggml_swiglu_split": (_T, [vp, _T, _T]),
         "ggml_rms_norm": (_T, [vp, _T, f32]), "ggml_transpose": (_T, [vp, _T]),
         "ggml_soft_max": (_T, [vp, _T]), "ggml_diag_mask_inf": (_T, [vp, _T, i32]),
+        "ggml_sub": (_T, [vp, _T, _T]), "ggml_scale_bias": (_T, [vp, _T, f32, f32]),
+        "ggml_argsort_top_k": (_T, [vp, _T, i32]), "ggml_cumsum": (_T, [vp, _T]), "ggml_sum": (_T, [vp, _T]),
+        "ggml_step": (_T, [vp, _T]), "ggml_get_rows": (_T, [vp, _T, _T]),
+        "ggml_reshape_1d": (_T, [vp, _T, i64]), "ggml_reshape_2d": (_T, [vp, _T, i64, i64]),
+        "ggml_view_1d": (_T, [vp, _T, i64, sz]),
         "ggml_flash_attn_ext": (_T, [vp, _T, _T, _T, _T, f32, f32, f32]),
         "ggml_flash_attn_ext_set_prec": (None, [_T, i32]),
         "ggml_new_graph_custom": (vp, [vp, sz, b]), "ggml_build_forward_expand": (None, [vp, _T]),
@@ -173,6 +178,37 @@ class OpGraph:
 
     def diag_mask_inf(self, a, n_past):
         return self.G.ggml_diag_mask_inf(self.ctx, a, n_past)
+
+    # the depth decoder's in-graph sampler (src/depth-decoder.h:331-361)
+    def sub(self, a, b):
+        return self.G.ggml_sub(self.ctx, a, b)
+
+    def scale_bias(self, a, s, b):
+        return self.G.ggml_scale_bias(self.ctx, a, s, b)
+
+    def argsort_top_k(self, a, k):
+        return self.G.ggml_argsort_top_k(self.ctx, a, k)
+
+    def cumsum(self, a):
+        return self.G.ggml_cumsum(self.ctx, a)
+
+    def sum(self, a):
+        return self.G.ggml_sum(self.ctx, a)
+
+    def step(self, a):
+        return self.G.ggml_step(self.ctx, a)
+
+    def get_rows(self, a, idx):
+        return self.G.ggml_get_rows(self.ctx, a, idx)
+
+    def reshape_1d(self, a, n0):
+        return self.G.ggml_reshape_1d(self.ctx, a, n0)
+
+    def reshape_2d(self, a, n0, n1):
+        return self.G.ggml_reshape_2d(self.ctx, a, n0, n1)
+
+    def view_1d(self, a, n0, offset):
+        return self.G.ggml_view_1d(self.ctx, a, n0, offset)
 
     def build(self, outputs):
         self.graph = self.G.ggml_new_graph_custom(self.ctx, self.n_tensors, False)
