@@ -39,6 +39,11 @@ GGML_API ggml_backend_buffer_type_t ggml_backend_mi355x_host_buffer_type(void);
 /* Number of graph_compute calls served by replaying a captured HIP graph, and
  * by eager launches (diagnostics for tests and the benchmark). */
 GGML_API void ggml_backend_mi355x_graph_stats(ggml_backend_t backend, int64_t * replays, int64_t * eager);
+/* The backend's graph cache: graphs it keeps (at most 8, least recently used
+ * replaced first), how many of them hold a captured HIP graph, and captures
+ * made so far.  Diagnostics, no counterpart in the reference. */
+GGML_API void ggml_backend_mi355x_graph_cache_info(ggml_backend_t backend, int64_t * n_entries, int64_t * n_captured,
+                                                   int64_t * n_captures);
 /* GPU time of this backend's graph_compute calls so far, from HIP events
  * recorded on its stream around each call (waits for the last call to
  * finish); reset != 0 clears the totals.  Backend-specific, no counterpart in

@@ -38,6 +38,11 @@ typedef struct {
 
 /* Create on MI355X device `device`; NULL on failure (see mm_lm_error). */
 void *       mm_lm_create(const mm_lm_config * cfg, int device, uint64_t seed);
+/* The same on an existing MI355X ggml backend (a ggml_backend_t), shared with
+ * other modules as the reference shares one backend between the LM, the DiT
+ * and the depth decoder (src/backend.h:21-23, :150-165); the LM does not free
+ * it. */
+void *       mm_lm_create_on_backend(const mm_lm_config * cfg, void * backend, uint64_t seed);
 const char * mm_lm_error(void);
 void         mm_lm_free(void * lm);
 

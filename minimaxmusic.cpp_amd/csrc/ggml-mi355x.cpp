@@ -20,6 +20,8 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -62,13 +64,22 @@ struct mi_staging {
     bool                    failed = false;
 };
 
+// Streams of freed backends are kept per device and handed to the next
+// backend (after a synchronize), so creating and freeing backends in one
+// process does not create and destroy HIP streams each time.
 struct mi_device {
     int                             id;
     std::string                     name;
     std::string                     desc;
     struct ggml_backend_buffer_type buft;
     mi_staging                      staging;
+    std::mutex                      stream_mu;
+    std::vector<hipStream_t>        idle_streams;
 };
+
+// Buffers whose set_tensor / get_tensor failed: graph_compute refuses graphs
+// that touch them (ggml's buffer interface has no error return there).
+std::atomic<int> g_poisoned_buffers{ 0 };
 
 struct mi_registry {
     std::vector<mi_device *>                 devs;
@@ -100,12 +111,26 @@ mmhip_view view_of(const struct ggml_tensor * t) {
 struct mi_buffer {
     int    device;
     void * ptr;
+    bool   poisoned = false;  // a set_tensor / get_tensor on it failed
 };
 
+void poison(mi_buffer * c) {
+    if (!c->poisoned) {
+        c->poisoned = true;
+        g_poisoned_buffers.fetch_add(1);
+    }
+}
+
+// Work queued on any stream of the device may still read the buffer (a
+// replayed HIP graph holds its addresses): wait for the device before freeing.
 void buf_free(ggml_backend_buffer_t b) {
     mi_buffer * c = (mi_buffer *) b->context;
     hipSetDevice(c->device);
+    HIP_OK(hipDeviceSynchronize());
     (void) hipFree(c->ptr);
+    if (c->poisoned) {
+        g_poisoned_buffers.fetch_sub(1);
+    }
     delete c;
 }
 
@@ -219,26 +244,56 @@ void buf_set_tensor(ggml_backend_buffer_t b, struct ggml_tensor * t, const void 
     hipSetDevice(c->device);
     if (is_repacked(t->type)) {
         if (!quant_rows_io(t, offset, size, data, nullptr)) {
-            abort();
+            MI_LOG("set_tensor %s failed: the buffer is marked failed, graphs using it are refused\n", t->name);
+            poison(c);
         }
         return;
     }
     if (staged_write(c->device, (char *) t->data + offset, data, size)) {
         return;
     }
-    HIP_OK(hipMemcpy((char *) t->data + offset, data, size, hipMemcpyHostToDevice));
+    if (!HIP_OK(hipMemcpy((char *) t->data + offset, data, size, hipMemcpyHostToDevice))) {
+        poison(c);
+    }
 }
 
+// On failure the destination is filled with 0xff bytes (NaN for f32 / f16)
+// so a caller that ignores the log does not read plausible stale values.
 void buf_get_tensor(ggml_backend_buffer_t b, const struct ggml_tensor * t, void * data, size_t offset, size_t size) {
     mi_buffer * c = (mi_buffer *) b->context;
     hipSetDevice(c->device);
+    bool ok;
     if (is_repacked(t->type)) {
-        if (!quant_rows_io(t, offset, size, nullptr, data)) {
-            abort();
-        }
-        return;
+        ok = quant_rows_io(t, offset, size, nullptr, data);
+    } else {
+        ok = HIP_OK(hipMemcpy(data, (const char *) t->data + offset, size, hipMemcpyDeviceToHost));
     }
-    HIP_OK(hipMemcpy(data, (const char *) t->data + offset, size, hipMemcpyDeviceToHost));
+    if (!ok) {
+        MI_LOG("get_tensor %s failed: the buffer is marked failed, graphs using it are refused\n", t->name);
+        memset(data, 0xff, size);
+        poison(c);
+    }
+}
+
+// Is any tensor of the graph (nodes and their sources) in a poisoned buffer?
+bool graph_poisoned(struct ggml_cgraph * g) {
+    auto bad = [](const struct ggml_tensor * t) {
+        const struct ggml_tensor * base = t->view_src ? t->view_src : t;
+        ggml_backend_buffer_t      b    = base->buffer;
+        return b && b->iface.free_buffer == buf_free && ((mi_buffer *) b->context)->poisoned;
+    };
+    for (int i = 0; i < ggml_graph_n_nodes(g); i++) {
+        const struct ggml_tensor * n = ggml_graph_node(g, i);
+        if (bad(n)) {
+            return true;
+        }
+        for (int s = 0; s < GGML_MAX_SRC; s++) {
+            if (n->src[s] && bad(n->src[s])) {
+                return true;
+            }
+        }
+    }
+    return false;
 }
 
 bool buf_cpy_tensor(ggml_backend_buffer_t b, const struct ggml_tensor * src, struct ggml_tensor * dst) {
@@ -355,13 +410,31 @@ bool hbuft_is_host(ggml_backend_buffer_type_t) {
 // ---------------------------------------------------------------------------
 // backend
 
-struct mi_graph_cache {
-    std::vector<uint64_t> sig;        // signature of the captured graph
-    std::vector<uint64_t> seen_sig;   // signature of the last eager run
-    hipGraphExec_t        exec = nullptr;
+struct graph_plan;
+
+// One graph the backend has seen: its signature (every node's identity,
+// op, op_params, shape, strides, data address and sources: anything a launch
+// takes by value), its execution plan and, from its second sight on, the
+// instantiated HIP graph of its launches.  The reference alternates several
+// graphs on one backend (the depth decoder's frame graph and the LM's decode
+// graph every frame, src/pipeline.cpp:458, :545-547, one shared backend
+// src/backend.h:21-23), so the backend keeps several, least recently used
+// first out.
+struct mi_graph_entry {
+    const void *                graph   = nullptr;  // pre-key: the cgraph, its node count, first / last node
+    int                         n_nodes = 0;
+    const void *                first   = nullptr;
+    const void *                last    = nullptr;
+    std::vector<uint64_t>       sig;
+    std::shared_ptr<graph_plan> plan;
+    hipGraphExec_t              exec       = nullptr;
+    int                         sights     = 0;
+    bool                        no_capture = false;  // capture failed once: stay eager
+    uint64_t                    stamp      = 0;
 };
 
 struct mi_backend {
+    static constexpr int GRAPH_ENTRIES = 8;
     mi_device *    dev;
     hipStream_t    stream = nullptr;
     void *         ws     = nullptr;
@@ -370,9 +443,12 @@ struct mi_backend {
     size_t         slot_size = 0;
     bool           capturing = false;
     bool           use_graphs = true;
-    mi_graph_cache cache;
+    std::vector<mi_graph_entry> graphs;
+    std::vector<uint64_t>       sig_buf;  // signature of the call being looked up
+    uint64_t                    clock = 0;
     int64_t        n_replays = 0;
     int64_t        n_eager   = 0;
+    int64_t        n_captures = 0;
     // GPU time of graph_compute calls: events recorded on the stream around
     // each call, read back at the next call (or on query)
     hipEvent_t     ev0 = nullptr, ev1 = nullptr;
@@ -398,12 +474,21 @@ const char * be_name(ggml_backend_t b) {
     return ((mi_backend *) b->context)->dev->name.c_str();
 }
 
+// Teardown in dependency order: the stream's queued work (which may be a
+// replay reading the workspace, the slots and graph tensors) finishes first,
+// then the HIP graphs that launch into those buffers go, then the buffers;
+// the stream goes back to the device for the next backend.
 void be_free(ggml_backend_t b) {
     mi_backend * c = (mi_backend *) b->context;
     hipSetDevice(c->dev->id);
-    if (c->cache.exec) {
-        (void) hipGraphExecDestroy(c->cache.exec);
+    const bool synced = HIP_OK(hipStreamSynchronize(c->stream));
+    for (mi_graph_entry & e : c->graphs) {
+        if (e.exec) {
+            (void) hipGraphExecDestroy(e.exec);
+            e.exec = nullptr;
+        }
     }
+    c->graphs.clear();
     if (c->ws) {
         (void) hipFree(c->ws);
     }
@@ -414,7 +499,12 @@ void be_free(ggml_backend_t b) {
         (void) hipEventDestroy(c->ev0);
         (void) hipEventDestroy(c->ev1);
     }
-    (void) hipStreamDestroy(c->stream);
+    if (synced) {
+        std::lock_guard<std::mutex> lk(c->dev->stream_mu);
+        c->dev->idle_streams.push_back(c->stream);
+    } else {
+        (void) hipStreamDestroy(c->stream);
+    }
     delete c;
     delete b;
 }
@@ -427,13 +517,16 @@ void be_sync(ggml_backend_t b) {
 // Workspace large enough for `need` bytes; returns nullptr when it would have
 // to grow during a capture (the caller then abandons the capture).
 // A captured graph holds the addresses of the workspace and the activation
-// slots: when either moves, the capture is dropped and the graph captured again.
+// slots: when either moves, every capture is dropped (the graphs are captured
+// again on their next sight).  The caller has synchronised the stream.
 void drop_captured(mi_backend * c) {
-    if (c->cache.exec) {
-        (void) hipGraphExecDestroy(c->cache.exec);
-        c->cache.exec = nullptr;
+    for (mi_graph_entry & e : c->graphs) {
+        if (e.exec) {
+            (void) hipGraphExecDestroy(e.exec);
+            e.exec   = nullptr;
+            e.sights = 1;
+        }
     }
-    c->cache.sig.clear();
 }
 
 void * workspace(mi_backend * c, size_t need) {
@@ -499,6 +592,11 @@ bool supports_fa(const struct ggml_tensor * op) {
     if (!(D == 64 || D == 128 || D == 256) || k->ne[0] != D || v->ne[0] != D) {
         return false;
     }
+    // D = 256 runs only on the decode kernels (at most 16 query rows per KV
+    // head); the MFMA prefill kernel takes D 64 / 128
+    if (D == 256 && (k->ne[2] <= 0 || q->ne[2] % k->ne[2] != 0 || q->ne[1] * (q->ne[2] / k->ne[2]) > 16)) {
+        return false;
+    }
     return q->nb[0] == 4 && k->nb[0] == 2 && v->nb[0] == 2 && k->nb[1] % 16 == 0 && v->nb[1] % 16 == 0 &&
            k->nb[2] % 16 == 0 && v->nb[2] % 16 == 0 && k->nb[3] % 16 == 0 && v->nb[3] % 16 == 0;
 }
@@ -518,6 +616,11 @@ bool is_f32_or_f16(enum ggml_type t) {
     return t == GGML_TYPE_F32 || t == GGML_TYPE_F16;
 }
 
+// 16-byte aligned data: the address once allocated, the view offset before
+bool aligned16(const struct ggml_tensor * t) {
+    return (uintptr_t) t->data % 16 == 0 && (t->view_src == nullptr || t->view_offs % 16 == 0);
+}
+
 bool supports(const struct ggml_tensor * op) {
     switch (op->op) {
         case GGML_OP_NONE:
@@ -530,9 +633,12 @@ bool supports(const struct ggml_tensor * op) {
             if (op->src[0]->type == GGML_TYPE_BF16) {  // BF16 weights at up to 16 tokens
                 const struct ggml_tensor * w = op->src[0];
                 const struct ggml_tensor * x = op->src[1];
+                // the kernel's 16-byte loads: rows and bases 16-byte aligned
+                // (also checked before allocation, through the view offsets)
                 return w->nb[0] == 2 && w->ne[2] == 1 && w->ne[3] == 1 && w->ne[0] % 8 == 0 && w->nb[1] % 16 == 0 &&
                        x->type == GGML_TYPE_F32 && mm_collapsible(x) && x->ne[1] * x->ne[2] * x->ne[3] <= 16 &&
-                       op->type == GGML_TYPE_F32 && ggml_is_contiguous(op);
+                       x->nb[1] % 16 == 0 && aligned16(x) && aligned16(w) && op->type == GGML_TYPE_F32 &&
+                       ggml_is_contiguous(op);
             }
             if (op->src[0]->type == GGML_TYPE_F32) {  // activation x activation
                 return op->src[1]->type == GGML_TYPE_F32 && op->src[0]->nb[0] == 4 && op->src[1]->nb[0] == 4 &&
@@ -1799,9 +1905,8 @@ int run_step(mi_backend * c, struct ggml_cgraph * g, const plan_step & st, char 
     return rc == MMHIP_OK ? MMHIP_OK : (fail(n, rc), -1);
 }
 
-bool run_graph(mi_backend * c, struct ggml_cgraph * g) {
-    const graph_plan plan = build_plan(g);
-    char *           slot = nullptr;
+bool run_plan(mi_backend * c, struct ggml_cgraph * g, const graph_plan & plan) {
+    char * slot = nullptr;
     if (plan.slot_bytes) {
         slot = (char *) slots(c, plan.slot_bytes);
         if (!slot) {
@@ -1816,84 +1921,157 @@ bool run_graph(mi_backend * c, struct ggml_cgraph * g) {
     return true;
 }
 
-std::vector<uint64_t> signature(struct ggml_cgraph * g) {
-    std::vector<uint64_t> sig;
-    const int             nn = ggml_graph_n_nodes(g);
-    sig.reserve((size_t) nn * 8);
+// Everything a graph's launches depend on, node by node: the node's address,
+// op and type, data address, shape, strides and op_params (scales, top-k,
+// eps, RoPE parameters are taken by value), and for each source its address
+// and data address, plus shape and strides for sources that are not graph
+// nodes (weights, inputs).  A graph rebuilt at the same addresses with other
+// op_params (the depth decoder's cfg, src/depth-decoder.h:439-447) or other
+// views therefore gets a new signature.
+void signature(struct ggml_cgraph * g, std::vector<uint64_t> & sig) {
+    sig.clear();
+    const int nn = ggml_graph_n_nodes(g);
+    sig.reserve((size_t) nn * 40);
+    static_assert(sizeof(((struct ggml_tensor *) nullptr)->op_params) % sizeof(uint64_t) == 0, "op_params words");
     for (int i = 0; i < nn; i++) {
         const struct ggml_tensor * n = ggml_graph_node(g, i);
         sig.push_back((uint64_t) (uintptr_t) n);
-        sig.push_back((uint64_t) n->op);
+        sig.push_back((uint64_t) n->op | ((uint64_t) n->type << 16) | ((uint64_t) (uint32_t) n->flags << 32));
         sig.push_back((uint64_t) (uintptr_t) n->data);
         for (int d = 0; d < 4; d++) {
             sig.push_back((uint64_t) n->ne[d]);
+            sig.push_back((uint64_t) n->nb[d]);
         }
+        uint64_t op_words[sizeof(n->op_params) / sizeof(uint64_t)];
+        memcpy(op_words, n->op_params, sizeof(n->op_params));
+        sig.insert(sig.end(), op_words, op_words + sizeof(n->op_params) / sizeof(uint64_t));
         for (int s = 0; s < GGML_MAX_SRC; s++) {
-            if (n->src[s]) {
-                sig.push_back((uint64_t) (uintptr_t) n->src[s]->data);
+            const struct ggml_tensor * t = n->src[s];
+            if (!t) {
+                continue;
+            }
+            sig.push_back((uint64_t) s << 56 | (uint64_t) t->type << 48);
+            sig.push_back((uint64_t) (uintptr_t) t);
+            sig.push_back((uint64_t) (uintptr_t) t->data);
+            if (t->op == GGML_OP_NONE) {
+                for (int d = 0; d < 4; d++) {
+                    sig.push_back((uint64_t) t->ne[d]);
+                    sig.push_back((uint64_t) t->nb[d]);
+                }
             }
         }
     }
-    return sig;
 }
 
-enum ggml_status graph_compute_inner(ggml_backend_t b, struct ggml_cgraph * g) {
-    mi_backend * c = (mi_backend *) b->context;
-    hipSetDevice(c->dev->id);
-    for (int i = 0; i < ggml_graph_n_nodes(g); i++) {
-        if (!supports(ggml_graph_node(g, i))) {
-            MI_LOG("graph_compute: node %d %s (%s) is not supported\n", i, ggml_graph_node(g, i)->name,
-                   ggml_op_name(ggml_graph_node(g, i)->op));
-            return GGML_STATUS_FAILED;
+mi_graph_entry * find_graph(mi_backend * c, struct ggml_cgraph * g, const std::vector<uint64_t> & sig) {
+    const int    nn    = ggml_graph_n_nodes(g);
+    const void * first = nn ? ggml_graph_node(g, 0) : nullptr;
+    const void * last  = nn ? ggml_graph_node(g, nn - 1) : nullptr;
+    for (mi_graph_entry & e : c->graphs) {
+        if (e.graph == g && e.n_nodes == nn && e.first == first && e.last == last && e.sig == sig) {
+            return &e;
         }
     }
-    if (!c->use_graphs) {
-        c->n_eager++;
-        return run_graph(c, g) ? GGML_STATUS_SUCCESS : GGML_STATUS_FAILED;
+    return nullptr;
+}
+
+// A new entry for graph g (the least recently used one is replaced when the
+// cache is full); its plan is built here, once.
+mi_graph_entry * add_graph(mi_backend * c, struct ggml_cgraph * g, std::vector<uint64_t> & sig) {
+    mi_graph_entry * e = nullptr;
+    if ((int) c->graphs.size() < mi_backend::GRAPH_ENTRIES) {
+        c->graphs.emplace_back();
+        e = &c->graphs.back();
+    } else {
+        e = &c->graphs[0];
+        for (mi_graph_entry & x : c->graphs) {
+            if (x.stamp < e->stamp) {
+                e = &x;
+            }
+        }
+        if (e->exec) {
+            HIP_OK(hipStreamSynchronize(c->stream));  // a launch of it may still be queued
+            (void) hipGraphExecDestroy(e->exec);
+        }
+        *e = mi_graph_entry();
     }
-    std::vector<uint64_t> sig = signature(g);
-    if (c->cache.exec && sig == c->cache.sig) {
-        c->n_replays++;
-        return HIP_OK(hipGraphLaunch(c->cache.exec, c->stream)) ? GGML_STATUS_SUCCESS : GGML_STATUS_FAILED;
-    }
-    if (sig != c->cache.seen_sig) {
-        // first sight: run eagerly (sizes the workspace, opts kernels in to
-        // their LDS limits) and remember the graph
-        c->cache.seen_sig = std::move(sig);
-        c->n_eager++;
-        return run_graph(c, g) ? GGML_STATUS_SUCCESS : GGML_STATUS_FAILED;
-    }
-    // second sight of the same graph: capture it
+    const int nn = ggml_graph_n_nodes(g);
+    e->graph     = g;
+    e->n_nodes   = nn;
+    e->first     = nn ? ggml_graph_node(g, 0) : nullptr;
+    e->last      = nn ? ggml_graph_node(g, nn - 1) : nullptr;
+    e->sig.swap(sig);
+    e->plan = std::make_shared<graph_plan>(build_plan(g));
+    return e;
+}
+
+// Capture the entry's launches into a HIP graph; false (nothing launched)
+// when the capture or the instantiation fails.
+bool capture_graph(mi_backend * c, struct ggml_cgraph * g, mi_graph_entry * e) {
     hipGraph_t graph = nullptr;
     if (!HIP_OK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeRelaxed))) {
-        return GGML_STATUS_FAILED;
+        (void) hipGetLastError();
+        return false;
     }
-    c->capturing  = true;
-    const bool ok = run_graph(c, g);
-    c->capturing  = false;
+    c->capturing     = true;
+    const bool ok    = run_plan(c, g, *e->plan);
+    c->capturing     = false;
     const bool ended = HIP_OK(hipStreamEndCapture(c->stream, &graph));
     if (!ok || !ended) {
         if (graph) {
             (void) hipGraphDestroy(graph);
         }
         (void) hipGetLastError();
-        c->n_eager++;
-        return run_graph(c, g) ? GGML_STATUS_SUCCESS : GGML_STATUS_FAILED;
+        return false;
     }
-    if (c->cache.exec) {
-        (void) hipGraphExecDestroy(c->cache.exec);
-        c->cache.exec = nullptr;
-    }
-    const bool inst = HIP_OK(hipGraphInstantiate(&c->cache.exec, graph, nullptr, nullptr, 0));
+    const bool inst = HIP_OK(hipGraphInstantiate(&e->exec, graph, nullptr, nullptr, 0));
     (void) hipGraphDestroy(graph);
     if (!inst) {
-        c->cache.exec = nullptr;
-        c->n_eager++;
-        return run_graph(c, g) ? GGML_STATUS_SUCCESS : GGML_STATUS_FAILED;
+        e->exec = nullptr;
+        (void) hipGetLastError();
+        return false;
     }
-    c->cache.sig = c->cache.seen_sig;
-    c->n_replays++;
-    return HIP_OK(hipGraphLaunch(c->cache.exec, c->stream)) ? GGML_STATUS_SUCCESS : GGML_STATUS_FAILED;
+    c->n_captures++;
+    return true;
+}
+
+enum ggml_status graph_compute_inner(ggml_backend_t b, struct ggml_cgraph * g) {
+    mi_backend * c = (mi_backend *) b->context;
+    hipSetDevice(c->dev->id);
+    if (g_poisoned_buffers.load() > 0 && graph_poisoned(g)) {
+        MI_LOG("graph_compute: the graph reads or writes a buffer whose transfer failed\n");
+        return GGML_STATUS_FAILED;
+    }
+    signature(g, c->sig_buf);
+    mi_graph_entry * e = find_graph(c, g, c->sig_buf);
+    if (!e) {
+        // first sight: check every node, build the plan and run eagerly (this
+        // sizes the workspace and opts kernels in to their LDS limits)
+        for (int i = 0; i < ggml_graph_n_nodes(g); i++) {
+            if (!supports(ggml_graph_node(g, i))) {
+                MI_LOG("graph_compute: node %d %s (%s) is not supported\n", i, ggml_graph_node(g, i)->name,
+                       ggml_op_name(ggml_graph_node(g, i)->op));
+                return GGML_STATUS_FAILED;
+            }
+        }
+        e = add_graph(c, g, c->sig_buf);
+    }
+    e->stamp = ++c->clock;
+    e->sights++;
+    if (e->exec) {
+        c->n_replays++;
+        return HIP_OK(hipGraphLaunch(e->exec, c->stream)) ? GGML_STATUS_SUCCESS : GGML_STATUS_FAILED;
+    }
+    if (c->use_graphs && !e->no_capture && e->sights >= 2) {
+        // second sight of the same graph: capture it, then launch the capture
+        if (capture_graph(c, g, e)) {
+            c->n_replays++;
+            return HIP_OK(hipGraphLaunch(e->exec, c->stream)) ? GGML_STATUS_SUCCESS : GGML_STATUS_FAILED;
+        }
+        e->no_capture = true;
+    }
+    c->n_eager++;
+    return run_plan(c, g, *e->plan) ? GGML_STATUS_SUCCESS : GGML_STATUS_FAILED;
 }
 
 enum ggml_status be_graph_compute(ggml_backend_t b, struct ggml_cgraph * g) {
@@ -2006,7 +2184,15 @@ ggml_backend_t dev_init(ggml_backend_dev_t d, const char * params) {
     hipSetDevice(dv->id);
     mi_backend * c = new mi_backend();
     c->dev         = dv;
-    if (!HIP_OK(hipStreamCreate(&c->stream))) {  // default priority, blocking
+    c->graphs.reserve(mi_backend::GRAPH_ENTRIES);  // entries stay at fixed addresses
+    {
+        std::lock_guard<std::mutex> lk(dv->stream_mu);
+        if (!dv->idle_streams.empty()) {
+            c->stream = dv->idle_streams.back();
+            dv->idle_streams.pop_back();
+        }
+    }
+    if (!c->stream && !HIP_OK(hipStreamCreate(&c->stream))) {  // default priority, blocking
         delete c;
         return nullptr;
     }
@@ -2061,6 +2247,9 @@ void * reg_proc(ggml_backend_reg_t, const char * name) {
     }
     if (strcmp(name, "ggml_backend_mi355x_gpu_time") == 0) {
         return (void *) ggml_backend_mi355x_gpu_time;
+    }
+    if (strcmp(name, "ggml_backend_mi355x_graph_cache_info") == 0) {
+        return (void *) ggml_backend_mi355x_graph_cache_info;
     }
     return nullptr;
 }
@@ -2143,6 +2332,18 @@ extern "C" void ggml_backend_mi355x_graph_stats(ggml_backend_t backend, int64_t 
     mi_backend * c = (mi_backend *) backend->context;
     *replays       = c->n_replays;
     *eager         = c->n_eager;
+}
+
+extern "C" void ggml_backend_mi355x_graph_cache_info(ggml_backend_t backend, int64_t * n_entries, int64_t * n_captured,
+                                                     int64_t * n_captures) {
+    mi_backend * c = (mi_backend *) backend->context;
+    int64_t      k = 0;
+    for (const mi_graph_entry & e : c->graphs) {
+        k += e.exec != nullptr;
+    }
+    *n_entries  = (int64_t) c->graphs.size();
+    *n_captured = k;
+    *n_captures = c->n_captures;
 }
 
 extern "C" void ggml_backend_mi355x_gpu_time(ggml_backend_t backend, double * total_ms, int64_t * n_calls, int reset) {

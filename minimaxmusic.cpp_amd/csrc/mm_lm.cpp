@@ -49,6 +49,7 @@ struct Layer {
 struct Lm {
     mm_lm_config          c;
     ggml_backend_t        backend = nullptr;
+    bool                  owns_backend = true;
     ggml_context *        wctx    = nullptr;
     ggml_backend_buffer_t wbuf    = nullptr;
     std::vector<Layer>    layers;
@@ -277,17 +278,26 @@ extern "C" const char * mm_lm_error(void) {
     return g_err;
 }
 
-extern "C" void * mm_lm_create(const mm_lm_config * cfg, int device, uint64_t seed) {
+namespace {
+
+// backend: an MI355X backend shared with other modules (not owned), or NULL
+// to create one on `device` (owned)
+void * lm_create(const mm_lm_config * cfg, int device, ggml_backend_t backend, uint64_t seed) {
     g_err[0] = 0;
     if (!cfg || cfg->n_layers <= 0 || cfg->n_heads % cfg->n_kv_heads != 0 || cfg->n_sets <= 0 ||
         cfg->hidden % 256 != 0 || cfg->ffn % 256 != 0 || (cfg->n_heads * cfg->head_dim) % 256 != 0) {
         err("create: bad config");
         return nullptr;
     }
+    if (backend && !ggml_backend_is_mi355x(backend)) {
+        err("create: the backend is not an MI355X backend");
+        return nullptr;
+    }
     Lm * m = new Lm();
     m->c   = *cfg;
     const mm_lm_config & c = m->c;
-    m->backend             = ggml_backend_mi355x_init(device);
+    m->owns_backend        = backend == nullptr;
+    m->backend             = backend ? backend : ggml_backend_mi355x_init(device);
     if (!m->backend) {
         err("create: no MI355X device %d", device);
         delete m;
@@ -367,10 +377,27 @@ extern "C" void * mm_lm_create(const mm_lm_config * cfg, int device, uint64_t se
     return m;
 }
 
+}  // namespace
+
+extern "C" void * mm_lm_create(const mm_lm_config * cfg, int device, uint64_t seed) {
+    return lm_create(cfg, device, nullptr, seed);
+}
+
+extern "C" void * mm_lm_create_on_backend(const mm_lm_config * cfg, void * backend, uint64_t seed) {
+    if (!backend) {
+        err("create: no backend");
+        return nullptr;
+    }
+    return lm_create(cfg, -1, (ggml_backend_t) backend, seed);
+}
+
 extern "C" void mm_lm_free(void * h) {
     Lm * m = (Lm *) h;
     if (!m) {
         return;
+    }
+    if (m->backend) {
+        ggml_backend_synchronize(m->backend);  // no replay still reading the buffers freed below
     }
     if (m->galloc) {
         ggml_gallocr_free(m->galloc);
@@ -380,7 +407,9 @@ extern "C" void mm_lm_free(void * h) {
     ggml_free(m->kv_ctx);
     ggml_backend_buffer_free(m->wbuf);
     ggml_free(m->wctx);
-    ggml_backend_free(m->backend);
+    if (m->owns_backend) {
+        ggml_backend_free(m->backend);
+    }
     delete m;
 }
 

@@ -32,6 +32,8 @@ def load():
         vp, i32, i64, u64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_uint64
         L.mm_lm_create.argtypes = [ctypes.POINTER(LmConfig), i32, u64]
         L.mm_lm_create.restype = vp
+        L.mm_lm_create_on_backend.argtypes = [ctypes.POINTER(LmConfig), vp, u64]
+        L.mm_lm_create_on_backend.restype = vp
         L.mm_lm_error.restype = ctypes.c_char_p
         L.mm_lm_free.argtypes = [vp]
         L.mm_lm_fill_kv.argtypes = [vp, i32, i32, u64]
@@ -60,10 +62,15 @@ def _p(a):
 
 
 class Lm:
-    def __init__(self, seed=1005, device=0, **cfg):
+    def __init__(self, seed=1005, device=0, backend=None, **cfg):
+        """backend: an existing MI355X ggml backend handle to share (e.g.
+        OpGraph.backend; not freed by the LM), else one is created on device."""
         L = load()
         self.cfg = LmConfig(**cfg)
-        self.h = L.mm_lm_create(ctypes.byref(self.cfg), device, seed)
+        if backend is not None:
+            self.h = L.mm_lm_create_on_backend(ctypes.byref(self.cfg), backend, seed)
+        else:
+            self.h = L.mm_lm_create(ctypes.byref(self.cfg), device, seed)
         if not self.h:
             raise LmError(L.mm_lm_error().decode())
 

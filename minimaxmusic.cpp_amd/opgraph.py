@@ -86,6 +86,8 @@ def _load():
         "ggml_backend_mi355x_init": (vp, [i32]),
         "ggml_backend_mi355x_gpu_time": (None, [vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(i64), i32]),
         "ggml_backend_mi355x_graph_stats": (None, [vp, ctypes.POINTER(i64), ctypes.POINTER(i64)]),
+        "ggml_backend_mi355x_graph_cache_info": (None, [vp, ctypes.POINTER(i64), ctypes.POINTER(i64),
+                                                        ctypes.POINTER(i64)]),
     }
     for n, (r, a) in misig.items():
         fn = getattr(mi, n)
@@ -99,13 +101,16 @@ class OpGraph:
     tensors and ops, call build(outputs), upload inputs with set(), then
     compute() runs the graph through ggml_backend_graph_compute."""
 
-    def __init__(self, n_tensors=256, device=0):
+    def __init__(self, n_tensors=256, device=0, backend=None):
+        """backend: an MI355X backend handle to share with other graphs (not
+        freed by close()), else a new one on `device`."""
         self.G, self.MI = _load()
         mem = n_tensors * self.G.ggml_tensor_overhead() + self.G.ggml_graph_overhead_custom(n_tensors, False)
         self.ctx = self.G.ggml_init(_InitParams(mem, None, True))
         if not self.ctx:
             raise RuntimeError("ggml_init failed")
-        self.backend = self.MI.ggml_backend_mi355x_init(device)
+        self.owns_backend = backend is None
+        self.backend = self.MI.ggml_backend_mi355x_init(device) if backend is None else backend
         if not self.backend:
             raise RuntimeError("MI355X ggml backend: no device")
         self.n_tensors = n_tensors
@@ -251,13 +256,24 @@ class OpGraph:
         self.MI.ggml_backend_mi355x_graph_stats(self.backend, ctypes.byref(r), ctypes.byref(e))
         return r.value, e.value
 
+    def graph_cache_info(self):
+        """(graphs kept by the backend, of which captured, captures so far)."""
+        a, b, c = ctypes.c_int64(0), ctypes.c_int64(0), ctypes.c_int64(0)
+        self.MI.ggml_backend_mi355x_graph_cache_info(self.backend, ctypes.byref(a), ctypes.byref(b), ctypes.byref(c))
+        return a.value, b.value, c.value
+
     def close(self):
+        # the backend first: it waits for its stream and drops the captured
+        # HIP graphs that point into the buffer, then the buffer goes
+        if self.backend:
+            if self.owns_backend:
+                self.G.ggml_backend_free(self.backend)
+            else:
+                self.G.ggml_backend_synchronize(self.backend)
+            self.backend = None
         if self.buf:
             self.G.ggml_backend_buffer_free(self.buf)
             self.buf = None
-        if self.backend:
-            self.G.ggml_backend_free(self.backend)
-            self.backend = None
         if self.ctx:
             self.G.ggml_free(self.ctx)
             self.ctx = None

@@ -70,9 +70,85 @@ def test_lm_decode_matches_reference(lmmod, wtype):
     replays, eager = lm.graph_stats()
     assert eager == 1 and replays == 3, (replays, eager)
     # the device KV cache received this step's rows at the right positions
-    k0 = lm.get("kv_k4_1", np.float16).reshape(2, 2, SMALL["max_seq"], 64)
-    assert np.array_equal(k0[0, :, 300:304], st.k[1][0, :, 300:304]) or \
-        np.abs(k0[0, :, 300:304].astype(np.float32) - st.k[1][0, :, 300:304].astype(np.float32)).max() < 2e-2
+    _check_kv_rows(lm, st, SMALL, {0: (300, 304), 1: (287, 291)})
+    lm.close()
+
+
+def _check_kv_rows(lm, st, cfg, written):
+    """The device caches equal the reference's.  Every layer: rows the steps
+    did not write byte for byte.  Layer 0 (inputs identical to the
+    reference's): the written rows at least 95 % byte-equal, the rest within
+    one f16 ulp or, for elements near zero, 1e-4 of the row's largest
+    magnitude (they come out of the QKV GEMV, whose f32 block sums differ from
+    the reference's in order before the f16 rounding).  Later layers: within
+    2e-2 of the row's largest magnitude (their inputs carry the earlier
+    layers' differences, and one step of the activation quantisation is 1/127
+    of a block's largest value)."""
+    shp = (cfg["n_sets"], cfg["n_kv_heads"], cfg["max_seq"], cfg["head_dim"])
+    for layer in range(cfg["n_layers"]):
+        for name, ref in ((f"kv_k4_{layer}", st.k[layer]), (f"kv_v4_{layer}", st.v[layer])):
+            dev = lm.get(name, np.float16).reshape(shp)
+            for s, (p0, p1) in written.items():
+                a, b = dev[s, :, p0:p1].astype(np.float32), ref[s, :, p0:p1].astype(np.float32)
+                err = np.abs(a - b)
+                if layer == 0:
+                    ulp = np.spacing(np.abs(b).astype(np.float16)).astype(np.float32)
+                    tol = np.maximum(ulp, 1e-4 * np.abs(b).max(axis=-1, keepdims=True))
+                    assert (err <= tol).all(), (name, s, float(err.max()))
+                    same = dev[s, :, p0:p1].view(np.uint16) == ref[s, :, p0:p1].view(np.uint16)
+                    assert same.mean() >= 0.95, (name, s, float(same.mean()))
+                else:
+                    assert (err <= 2e-2 * np.abs(b).max(axis=-1, keepdims=True)).all(), (name, s, float(err.max()))
+                assert np.array_equal(dev[s, :, :p0].view(np.uint16), ref[s, :, :p0].view(np.uint16)), (name, s)
+                assert np.array_equal(dev[s, :, p1:].view(np.uint16), ref[s, :, p1:].view(np.uint16)), (name, s)
+
+
+@pytest.mark.parametrize("wtype", [8, 14])
+def test_lm_decode_headline_width_matches_reference(lmmod, wtype):
+    """Oracle parity at the Qwen3-8B width of the decode benchmark: hidden
+    4096, 32 / 8 heads of 128, FFN 12288, vocab 151936, f16 KV caches of 4096
+    positions on both CFG sets (Q8_0, and the Q6_K variant), 2 layers of the
+    36 (every layer runs the same kernels), for the eager step and the
+    captured one.  Stated tolerance: equal argmax on both CFG rows; logits and
+    hidden cosine against the ggml-CPU-semantics reference >= 0.9999, or,
+    where that reference's own distance from exact arithmetic (1 - cosine vs
+    the f64 reference) exceeds 5e-5, 1 - cosine <= 2x that distance (two
+    evaluations of ggml's activation quantisation whose f32 inputs differ in
+    the last bits round a few int8 codes differently: with the Q6_K variant's
+    synthetic weights ggml's own arithmetic is 1.3e-4 from exact); and at most
+    1.5x as far from exact as the ggml-CPU-semantics reference.  KV rows as
+    _check_kv_rows."""
+    import lm_reference
+
+    cfg = dict(lmmod.QWEN3_8B, n_layers=2, wtype=wtype)
+    lm = lmmod.Lm(seed=77 + wtype, **cfg)
+    lm.fill_kv(0, 4094, seed=31)  # both steps in the 4096-key window
+    lm.fill_kv(1, 4093, seed=32)
+    st = lm_reference.LmState(lm)
+    st64 = lm_reference.LmState(lm)
+    kv_pos = {0: 4094, 1: 4093}
+    rng = np.random.default_rng(1005 + wtype)
+    for step in range(2):
+        print(f"headline-width decode wtype {wtype} step {step}", flush=True)
+        emb = rng.standard_normal((2, cfg["hidden"])).astype(np.float32)
+        lg, hid = lm.decode(emb, [0, 1])
+        rl, rh = lm_reference.decode(st, emb, [0, 1], kv_pos, "ggml")
+        el, eh = lm_reference.decode(st64, emb, [0, 1], kv_pos, "f64")
+        kv_pos = {k: v + 1 for k, v in kv_pos.items()}
+        cl = [cosine(lg[r], rl[r]) for r in range(2)]
+        print(f"  logits cosine {cl}, hidden cosine {[cosine(hid[r], rh[r]) for r in range(2)]}; "
+              f"vs exact {[cosine(lg[r], el[r]) for r in range(2)]}, ggml-ref vs exact "
+              f"{[cosine(rl[r], el[r]) for r in range(2)]}", flush=True)
+        for r in range(2):
+            ref_err = 1 - cosine(rl[r], el[r])
+            bar = 1e-4 if ref_err <= 5e-5 else 2 * ref_err
+            assert 1 - cl[r] <= bar, (step, r, cl[r], ref_err)
+            assert 1 - cosine(hid[r], rh[r]) <= bar, (step, r)
+            assert 1 - cosine(lg[r], el[r]) <= 1.5 * ref_err + 1e-6, (step, r)
+            assert np.argmax(lg[r]) == np.argmax(rl[r]), (step, r)
+    replays, eager = lm.graph_stats()
+    assert eager == 1 and replays == 1, (replays, eager)
+    _check_kv_rows(lm, st, cfg, {0: (4094, 4096), 1: (4093, 4095)})
     lm.close()
 
 
