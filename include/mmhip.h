@@ -179,6 +179,20 @@ int    mmhip_flash_attn_ext_q(const mmhip_view * q, const mmhip_view * k, const 
                               const mmhip_view * mask, float scale, float * out, void * ws, size_t ws_bytes, int type,
                               void * xq, void * stream);
 
+/* The attention of mmhip_flash_attn_ext with no workspace argument and no
+ * allocation: no counterpart in the reference.  For callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The workspace lives in a file-scope
+ * device array of mmhip_flash_attn_noalloc_max_workspace() bytes (8 MiB),
+ * one copy per GPU, held until the process ends; shapes whose
+ * mmhip_flash_attn_workspace exceeds it are rejected with
+ * MMHIP_ERR_WORKSPACE.  Calls on one GPU share the array: calls that overlap
+ * on one GPU (different streams, or host threads) race.  Results equal
+ * mmhip_flash_attn_ext's bit for bit. */
+size_t mmhip_flash_attn_noalloc_max_workspace(void);
+int    mmhip_flash_attn_ext_noalloc(const mmhip_view * q, const mmhip_view * k, const mmhip_view * v,
+                                    const mmhip_view * mask, float scale, float * out, void * stream);
+
 /* ---------------------------------------------------------------------
  * Decode-step glue ops (the nodes between the hot-path ops in the LM
  * batched decode graph, src/qwen3-lm.h:730-859).  Operands are ggml views;

@@ -372,3 +372,80 @@ extern "C" int mmhip_flash_attn_ext_q(const mmhip_view * q, const mmhip_view * k
     // output rows (b, iq) of Hq * D contiguous f32: quantise them separately
     return quantize_act(type, out, K, K, M, xq, (hipStream_t) stream);
 }
+
+// ---------------------------------------------------------------------------
+// Attention without allocation: the workspace of mmhip_flash_attn_ext (the
+// split-KV partials of the decode kernels, the mask prepass rows of the MFMA
+// kernel) lives in a file-scope device array, one copy per GPU, held until the
+// process ends.  Its device address is looked up once per device with that
+// device current; kernels receive that address, never the array's name.
+// Every call on one GPU shares the array (calls that overlap on one GPU race);
+// nothing in it has to start at zero: each launch writes every partial /
+// row entry it later reads.
+
+namespace {
+
+constexpr size_t   NOALLOC_SCRATCH_BYTES = 8u << 20;  // 8 MiB per GPU
+constexpr int      NOALLOC_MAX_DEVICES   = 64;
+std::mutex         g_scratch_mu;
+void *             g_scratch_ptr[NOALLOC_MAX_DEVICES] = {};
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+// The device address of `scratch` on the current device (looked up on the
+// first call per device); nullptr with the error set on failure.
+static void * scratch_on_current_device() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= NOALLOC_MAX_DEVICES) {
+        (void) hipGetLastError();
+        set_error(MMHIP_ERR_HIP, "flash_attn_noalloc: no current device");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *           p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            (void) hipGetLastError();
+            set_error(MMHIP_ERR_HIP, "flash_attn_noalloc: scratch address on device %d: %s", dev,
+                      hipGetErrorString(e));
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    return g_scratch_ptr[dev];
+}
+
+extern "C" size_t mmhip_flash_attn_noalloc_max_workspace(void) {
+    return NOALLOC_SCRATCH_BYTES;
+}
+
+extern "C" int mmhip_flash_attn_ext_noalloc(const mmhip_view * q, const mmhip_view * k, const mmhip_view * v,
+                                            const mmhip_view * mask, float scale, float * out, void * stream) {
+    MMHIP_API_BEGIN();
+    FaArgs a;
+    int    D;
+    int    rc = fa_validate(q, k, v, mask, a, D);
+    if (rc != MMHIP_OK) {
+        return rc;
+    }
+    if (!out) {
+        return set_error(MMHIP_ERR_INVALID, "flash_attn_noalloc: null output");
+    }
+    const size_t need = fa_use_mfma(a, D) ? fa_mfma_workspace(a) : fa_decode_workspace(a, D);
+    if (need > NOALLOC_SCRATCH_BYTES) {
+        return set_error(MMHIP_ERR_WORKSPACE, "flash_attn_noalloc: needs %zu bytes of scratch, the maximum is %zu",
+                         need, NOALLOC_SCRATCH_BYTES);
+    }
+    void * ws = scratch_on_current_device();
+    if (!ws) {
+        return MMHIP_ERR_HIP;
+    }
+    a.scale = scale;
+    if (fa_use_mfma(a, D)) {
+        return fa_mfma(a, D, out, ws, NOALLOC_SCRATCH_BYTES, (hipStream_t) stream);
+    }
+    return fa_decode(a, D, out, ws, NOALLOC_SCRATCH_BYTES, (hipStream_t) stream);
+}

@@ -81,6 +81,8 @@ SIGNATURES = {
                                           _vp]),
     "mmhip_flash_attn_workspace": (_sz, [_VP, _VP, _VP]),
     "mmhip_flash_attn_ext": (_i32, [_VP, _VP, _VP, _VP, _f32, _vp, _vp, _sz, _vp]),
+    "mmhip_flash_attn_noalloc_max_workspace": (_sz, []),
+    "mmhip_flash_attn_ext_noalloc": (_i32, [_VP, _VP, _VP, _VP, _f32, _vp, _vp]),
     "mmhip_flash_attn_ext_q": (_i32, [_VP, _VP, _VP, _VP, _f32, _vp, _vp, _sz, _i32, _vp, _vp]),
     "mmhip_binary": (_i32, [_i32, _VP, _VP, _vp, _vp]),
     "mmhip_rms_norm": (_i32, [_VP, _VP, _f32, _vp, _vp]),

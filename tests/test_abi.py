@@ -61,3 +61,34 @@ def test_error_reporting_without_gpu(pkg):
     assert rc == pkg.mmhip.ERR_UNSUPPORTED
     assert L.mmhip_act_bytes(8, 4096, 2) >= 2 * 4096 + 4 * 2 * 128
     assert L.mmhip_act_bytes(12, 100, 2) == 0
+
+
+def test_noalloc_attention_rejects_oversize_on_host(pkg):
+    """mmhip_flash_attn_ext_noalloc refuses a shape whose workspace exceeds its
+    8 MiB device array before any HIP call (a masked attention of 16384 query
+    rows x 64 heads x 2: 16 MiB of prepass rows); the operand pointers are
+    host addresses that are never dereferenced."""
+    import numpy as np
+
+    mm = pkg.mmhip
+    L = mm.load()
+    assert L.mmhip_flash_attn_noalloc_max_workspace() == 8 << 20
+    buf = np.zeros(64, np.float32)
+    base = buf.ctypes.data + (-buf.ctypes.data) % 16
+
+    def view(ne, nb):
+        v = mm.MmhipView()
+        v.data = base
+        v.ne[:] = list(ne)
+        v.nb[:] = list(nb)
+        return v
+
+    D, nq, Hq, B, nkv = 64, 16384, 64, 2, 64
+    q = view((D, nq, Hq, B), (4, 4 * D, 4 * D * nq, 4 * D * nq * Hq))
+    k = view((D, nkv, 8, B), (2, 2 * D, 2 * D * nkv, 2 * D * nkv * 8))
+    m = view((nkv, nq, 1, 1), (2, 2 * nkv, 2 * nkv * nq, 2 * nkv * nq))
+    need = L.mmhip_flash_attn_workspace(ctypes.byref(q), ctypes.byref(k), ctypes.byref(k))
+    rc = L.mmhip_flash_attn_ext_noalloc(ctypes.byref(q), ctypes.byref(k), ctypes.byref(k), ctypes.byref(m), 0.125,
+                                        ctypes.c_void_p(base), None)
+    assert rc == mm.ERR_WORKSPACE, L.mmhip_last_error()
+    assert b"maximum" in L.mmhip_last_error()
