@@ -49,7 +49,7 @@ LIBS = [
      ["csrc/k_quant.hip", "csrc/k_gemv.hip", "csrc/k_gemm.hip", "csrc/k_fa_decode.hip", "csrc/k_fa_mfma.hip",
       "csrc/k_glue.hip", "csrc/k_synth.hip", "csrc/mmhip_api.hip"], []),
     # stand-in for libggml-base (ggml is not vendored by the reference)
-    ("libggml-base.so", "host", ["ggml/src/ggml_core.cpp"], ["-ldl"]),
+    ("libggml-base.so", "host", ["ggml/src/ggml_core.cpp", "ggml/src/gguf.cpp"], ["-ldl"]),
     # the MI355X ggml backend, on top of the two above
     ("libggml-mi355x.so", "hip", ["csrc/ggml-mi355x.cpp"],
      ["-L{lib}", "-lmmhip", "-lggml-base", "-Wl,-rpath,$ORIGIN"]),

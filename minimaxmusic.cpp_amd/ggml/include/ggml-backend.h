@@ -132,6 +132,33 @@ GGML_API ggml_backend_t     ggml_backend_init_by_type(enum ggml_backend_dev_type
 GGML_API ggml_backend_t     ggml_backend_init_best(void);
 GGML_API void               ggml_backend_load_all(void);
 
+// Scheduler (src/backend.h:172-189, src/static-graph.h:45-58, src/qwen3-lm.h:
+// 599-620, src/dit.h:380-387, src/depth-decoder.h:425, :454).  This build's
+// scheduler places a whole graph on the first backend of the list that
+// supports every node (and the buffers of the weights it reads); graphs no
+// single backend can run are refused by ggml_backend_sched_alloc_graph with a
+// log line naming the node (there is no CPU compute backend here to split to).
+typedef struct ggml_backend_sched * ggml_backend_sched_t;
+
+GGML_API ggml_backend_sched_t ggml_backend_sched_new(ggml_backend_t * backends, ggml_backend_buffer_type_t * bufts,
+                                                     int n_backends, size_t graph_size, bool parallel,
+                                                     bool op_offload);
+GGML_API void                 ggml_backend_sched_free(ggml_backend_sched_t sched);
+GGML_API bool                 ggml_backend_sched_reserve(ggml_backend_sched_t sched, struct ggml_cgraph * measure_graph);
+GGML_API int                  ggml_backend_sched_get_n_backends(ggml_backend_sched_t sched);
+GGML_API ggml_backend_t       ggml_backend_sched_get_backend(ggml_backend_sched_t sched, int i);
+GGML_API int                  ggml_backend_sched_get_n_splits(ggml_backend_sched_t sched);
+GGML_API int                  ggml_backend_sched_get_n_copies(ggml_backend_sched_t sched);
+GGML_API void ggml_backend_sched_set_tensor_backend(ggml_backend_sched_t sched, struct ggml_tensor * node,
+                                                    ggml_backend_t backend);
+GGML_API ggml_backend_t   ggml_backend_sched_get_tensor_backend(ggml_backend_sched_t sched, struct ggml_tensor * node);
+GGML_API bool             ggml_backend_sched_alloc_graph(ggml_backend_sched_t sched, struct ggml_cgraph * graph);
+GGML_API enum ggml_status ggml_backend_sched_graph_compute(ggml_backend_sched_t sched, struct ggml_cgraph * graph);
+GGML_API enum ggml_status ggml_backend_sched_graph_compute_async(ggml_backend_sched_t sched,
+                                                                 struct ggml_cgraph * graph);
+GGML_API void             ggml_backend_sched_synchronize(ggml_backend_sched_t sched);
+GGML_API void             ggml_backend_sched_reset(ggml_backend_sched_t sched);
+
 // context tensors
 GGML_API struct ggml_backend_buffer * ggml_backend_alloc_ctx_tensors_from_buft(struct ggml_context *      ctx,
                                                                               ggml_backend_buffer_type_t buft);

@@ -39,6 +39,15 @@ extern "C" {
 
 #define GGML_PAD(x, n) (((x) + (n) - 1) & ~((n) - 1))
 
+// assertion helpers (ggml aborts with the location on failure)
+#define GGML_ABORT(...) ggml_abort(__FILE__, __LINE__, __VA_ARGS__)
+#define GGML_ASSERT(x)                                          \
+    do {                                                        \
+        if (!(x)) {                                             \
+            ggml_abort(__FILE__, __LINE__, "GGML_ASSERT(%s) failed", #x); \
+        }                                                       \
+    } while (0)
+
 #define GGML_ROPE_TYPE_NEOX 2
 
 #define GGML_KQ_MASK_PAD 1
@@ -268,6 +277,8 @@ struct ggml_tensor {
 
 static const size_t GGML_TENSOR_SIZE = sizeof(struct ggml_tensor);
 
+GGML_API void ggml_abort(const char * file, int line, const char * fmt, ...);
+
 // ---- scalars ----
 GGML_API float       ggml_fp16_to_fp32(ggml_fp16_t);
 GGML_API ggml_fp16_t ggml_fp32_to_fp16(float);
@@ -276,6 +287,23 @@ GGML_API void        ggml_fp32_to_fp16_row(const float *, ggml_fp16_t *, int64_t
 GGML_API void        ggml_bf16_to_fp32_row(const ggml_bf16_t *, float *, int64_t);
 
 // ---- types ----
+typedef void (*ggml_to_float_t)(const void * x, float * y, int64_t k);
+typedef void (*ggml_from_float_t)(const float * x, void * y, int64_t k);
+
+// Per-type traits; to_float decodes k elements (a whole number of blocks)
+// from the GGUF block layout: set for F16, BF16, Q8_0, Q4_K and Q6_K in this
+// build (host dequantisation, src/gguf-weights.h:230-235, :258-283).
+struct ggml_type_traits {
+    const char *      type_name;
+    int64_t           blck_size;
+    int64_t           blck_size_interleave;
+    size_t            type_size;
+    bool              is_quantized;
+    ggml_to_float_t   to_float;
+    ggml_from_float_t from_float_ref;
+};
+GGML_API const struct ggml_type_traits * ggml_get_type_traits(enum ggml_type type);
+
 GGML_API int64_t      ggml_blck_size(enum ggml_type type);
 GGML_API size_t       ggml_type_size(enum ggml_type type);
 GGML_API size_t       ggml_row_size(enum ggml_type type, int64_t ne);
@@ -336,6 +364,10 @@ GGML_API struct ggml_tensor * ggml_mul(struct ggml_context * ctx, struct ggml_te
 GGML_API struct ggml_tensor * ggml_scale(struct ggml_context * ctx, struct ggml_tensor * a, float s);
 GGML_API struct ggml_tensor * ggml_clamp(struct ggml_context * ctx, struct ggml_tensor * a, float min, float max);
 GGML_API struct ggml_tensor * ggml_soft_max(struct ggml_context * ctx, struct ggml_tensor * a);
+// softmax(a * scale + mask) along dim 0, mask f16 / f32 broadcast over dims 2-3
+// (or NULL); op_params = {scale, max_bias} (src/qwen3-enc.h:82, src/dit.h:178)
+GGML_API struct ggml_tensor * ggml_soft_max_ext(struct ggml_context * ctx, struct ggml_tensor * a,
+                                                struct ggml_tensor * mask, float scale, float max_bias);
 GGML_API struct ggml_tensor * ggml_scale_bias(struct ggml_context * ctx, struct ggml_tensor * a, float s, float b);
 GGML_API struct ggml_tensor * ggml_argsort(struct ggml_context * ctx, struct ggml_tensor * a, enum ggml_sort_order order);
 GGML_API struct ggml_tensor * ggml_argsort_top_k(struct ggml_context * ctx, struct ggml_tensor * a, int k);

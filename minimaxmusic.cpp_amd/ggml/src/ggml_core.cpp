@@ -57,6 +57,16 @@ static void core_log(enum ggml_log_level level, const char * fmt, ...) {
         }                                                                               \
     } while (0)
 
+extern "C" void ggml_abort(const char * file, int line, const char * fmt, ...) {
+    char    buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    core_log(GGML_LOG_LEVEL_ERROR, "%s:%d: %s\n", file, line, buf);
+    abort();
+}
+
 // ---------------------------------------------------------------------------
 // scalars
 
@@ -587,6 +597,19 @@ extern "C" struct ggml_tensor * ggml_soft_max(struct ggml_context * ctx, struct 
     set_op_params(r, params, sizeof(params));
     r->op     = GGML_OP_SOFT_MAX;
     r->src[0] = a;
+    return r;
+}
+
+extern "C" struct ggml_tensor * ggml_soft_max_ext(struct ggml_context * ctx, struct ggml_tensor * a,
+                                                  struct ggml_tensor * mask, float scale, float max_bias) {
+    CORE_ASSERT(mask == nullptr || (mask->ne[0] == a->ne[0] && mask->ne[1] >= a->ne[1] &&
+                                    a->ne[2] % mask->ne[2] == 0 && a->ne[3] % mask->ne[3] == 0));
+    struct ggml_tensor * r         = ggml_dup_tensor(ctx, a);
+    const float          params[2] = { scale, max_bias };
+    set_op_params(r, params, sizeof(params));
+    r->op     = GGML_OP_SOFT_MAX;
+    r->src[0] = a;
+    r->src[1] = mask;
     return r;
 }
 
@@ -1669,4 +1692,279 @@ extern "C" bool ggml_gallocr_alloc_graph(ggml_gallocr_t g, struct ggml_cgraph * 
 extern "C" size_t ggml_gallocr_get_buffer_size(ggml_gallocr_t g, int buffer_id) {
     (void) buffer_id;
     return g->buffer ? g->buffer->size : 0;
+}
+
+// ---------------------------------------------------------------------------
+// type traits: host decoders of the GGUF block layouts (to_float)
+//
+// Q8_0: 32 elements per 34-byte block {f16 d; i8 qs[32]}, y = d * q.
+// Q4_K: 256 per 144 bytes {f16 d; f16 dmin; u8 scales[12]; u8 qs[128]}: eight
+//   6-bit (scale, min) pairs packed in scales[] (pairs 0..3 in the low six bits
+//   of bytes 0..3 / 4..7; pairs 4..7 from the nibbles of bytes 8..11 with their
+//   top two bits in the high bits of bytes 0..3 / 4..7); each 64-element chunk
+//   j takes its low nibbles with pair 2j and its high nibbles with pair 2j+1,
+//   y = (d * sc) * q - (dmin * m).
+// Q6_K: 256 per 210 bytes {u8 ql[128]; u8 qh[64]; i8 scales[16]; f16 d}: each
+//   128-element half takes 64 bytes of ql (low nibbles then high nibbles of
+//   two 32-byte rows) and 32 bytes of qh (two bits per element), q in
+//   [0, 63], y = (d * scale[16-element group]) * (q - 32).
+
+namespace {
+
+float h2f(const uint8_t * p) {
+    ggml_fp16_t h;
+    memcpy(&h, p, 2);
+    return ggml_fp16_to_fp32(h);
+}
+
+void to_float_f16(const void * x, float * y, int64_t k) {
+    ggml_fp16_to_fp32_row((const ggml_fp16_t *) x, y, k);
+}
+
+void to_float_bf16(const void * x, float * y, int64_t k) {
+    ggml_bf16_to_fp32_row((const ggml_bf16_t *) x, y, k);
+}
+
+void to_float_q8_0(const void * x, float * y, int64_t k) {
+    const uint8_t * b = (const uint8_t *) x;
+    for (int64_t i = 0; i < k / 32; i++, b += 34) {
+        const float d = h2f(b);
+        for (int j = 0; j < 32; j++) {
+            y[i * 32 + j] = d * (float) (int8_t) b[2 + j];
+        }
+    }
+}
+
+void q4_k_pair(int j, const uint8_t * sc, uint8_t & s, uint8_t & m) {
+    if (j < 4) {
+        s = sc[j] & 63;
+        m = sc[j + 4] & 63;
+    } else {
+        s = (uint8_t) ((sc[j + 4] & 0x0F) | ((sc[j - 4] >> 6) << 4));
+        m = (uint8_t) ((sc[j + 4] >> 4) | ((sc[j] >> 6) << 4));
+    }
+}
+
+void to_float_q4_k(const void * x, float * y, int64_t k) {
+    const uint8_t * b = (const uint8_t *) x;
+    for (int64_t i = 0; i < k / 256; i++, b += 144) {
+        const float     d    = h2f(b);
+        const float     dmin = h2f(b + 2);
+        const uint8_t * sc   = b + 4;
+        const uint8_t * q    = b + 16;
+        float *         out  = y + i * 256;
+        for (int c = 0; c < 4; c++) {
+            uint8_t s0, m0, s1, m1;
+            q4_k_pair(2 * c, sc, s0, m0);
+            q4_k_pair(2 * c + 1, sc, s1, m1);
+            const float d0 = d * s0, n0 = dmin * m0, d1 = d * s1, n1 = dmin * m1;
+            for (int l = 0; l < 32; l++) {
+                out[64 * c + l]      = d0 * (float) (q[32 * c + l] & 0x0F) - n0;
+                out[64 * c + 32 + l] = d1 * (float) (q[32 * c + l] >> 4) - n1;
+            }
+        }
+    }
+}
+
+void to_float_q6_k(const void * x, float * y, int64_t k) {
+    const uint8_t * b = (const uint8_t *) x;
+    for (int64_t i = 0; i < k / 256; i++, b += 210) {
+        const float d = h2f(b + 208);
+        for (int h = 0; h < 2; h++) {
+            const uint8_t * ql  = b + 64 * h;
+            const uint8_t * qh  = b + 128 + 32 * h;
+            const int8_t *  sc  = (const int8_t *) (b + 192 + 8 * h);
+            float *         out = y + i * 256 + 128 * h;
+            for (int l = 0; l < 32; l++) {
+                const int g  = l / 16;
+                const int q1 = (int) ((ql[l] & 0x0F) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                const int q2 = (int) ((ql[l + 32] & 0x0F) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                const int q3 = (int) ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                const int q4 = (int) ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                out[l]      = (d * (float) sc[g]) * (float) q1;
+                out[l + 32] = (d * (float) sc[g + 2]) * (float) q2;
+                out[l + 64] = (d * (float) sc[g + 4]) * (float) q3;
+                out[l + 96] = (d * (float) sc[g + 6]) * (float) q4;
+            }
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" const struct ggml_type_traits * ggml_get_type_traits(enum ggml_type type) {
+    static ggml_type_traits table[GGML_TYPE_COUNT];
+    static bool             init = false;
+    if (!init) {
+        for (int t = 0; t < GGML_TYPE_COUNT; t++) {
+            const type_info ti = tinfo((enum ggml_type) t);
+            table[t]           = { ti.name, ti.blck, 0, ti.size, ti.quantized, nullptr, nullptr };
+        }
+        table[GGML_TYPE_F16].to_float  = to_float_f16;
+        table[GGML_TYPE_BF16].to_float = to_float_bf16;
+        table[GGML_TYPE_Q8_0].to_float = to_float_q8_0;
+        table[GGML_TYPE_Q4_K].to_float = to_float_q4_k;
+        table[GGML_TYPE_Q6_K].to_float = to_float_q6_k;
+        init                           = true;
+    }
+    CORE_ASSERT(type >= 0 && type < GGML_TYPE_COUNT);
+    return &table[type];
+}
+
+// ---------------------------------------------------------------------------
+// scheduler: the whole graph on the first listed backend that runs every node
+
+struct ggml_backend_sched {
+    std::vector<ggml_backend_t>             backends;
+    std::vector<ggml_backend_buffer_type_t> bufts;
+    std::vector<ggml_gallocr_t>             galloc;  // one per backend, made on first use
+    int                                     chosen = -1;  // backend of the allocated graph
+};
+
+extern "C" ggml_backend_sched_t ggml_backend_sched_new(ggml_backend_t * backends, ggml_backend_buffer_type_t * bufts,
+                                                       int n_backends, size_t graph_size, bool parallel,
+                                                       bool op_offload) {
+    (void) graph_size;
+    (void) parallel;
+    (void) op_offload;
+    if (!backends || n_backends < 1) {
+        return nullptr;
+    }
+    auto * s = new ggml_backend_sched();
+    for (int i = 0; i < n_backends; i++) {
+        if (!backends[i]) {
+            delete s;
+            return nullptr;
+        }
+        s->backends.push_back(backends[i]);
+        s->bufts.push_back(bufts && bufts[i] ? bufts[i] : ggml_backend_get_default_buffer_type(backends[i]));
+    }
+    s->galloc.assign(s->backends.size(), nullptr);
+    return s;
+}
+
+extern "C" void ggml_backend_sched_free(ggml_backend_sched_t s) {
+    if (!s) {
+        return;
+    }
+    for (auto * g : s->galloc) {
+        if (g) {
+            ggml_gallocr_free(g);
+        }
+    }
+    delete s;
+}
+
+extern "C" void ggml_backend_sched_reset(ggml_backend_sched_t s) {
+    s->chosen = -1;
+}
+
+extern "C" int ggml_backend_sched_get_n_backends(ggml_backend_sched_t s) {
+    return (int) s->backends.size();
+}
+
+extern "C" ggml_backend_t ggml_backend_sched_get_backend(ggml_backend_sched_t s, int i) {
+    return i >= 0 && (size_t) i < s->backends.size() ? s->backends[(size_t) i] : nullptr;
+}
+
+extern "C" int ggml_backend_sched_get_n_splits(ggml_backend_sched_t s) {
+    return s->chosen >= 0 ? 1 : 0;
+}
+
+extern "C" int ggml_backend_sched_get_n_copies(ggml_backend_sched_t s) {
+    (void) s;
+    return 1;
+}
+
+extern "C" void ggml_backend_sched_set_tensor_backend(ggml_backend_sched_t s, struct ggml_tensor * node,
+                                                      ggml_backend_t backend) {
+    (void) s;
+    (void) node;
+    (void) backend;  // placement is per graph in this scheduler
+}
+
+extern "C" ggml_backend_t ggml_backend_sched_get_tensor_backend(ggml_backend_sched_t s, struct ggml_tensor * node) {
+    (void) node;
+    return s->chosen >= 0 ? s->backends[(size_t) s->chosen] : nullptr;
+}
+
+// Can backend i run the whole graph: every node supported, and every tensor
+// already placed in a buffer (weights, caches) usable by that backend.
+static bool sched_fits(ggml_backend_sched_t s, size_t i, struct ggml_cgraph * g, const struct ggml_tensor ** bad) {
+    ggml_backend_t b = s->backends[i];
+    for (int n = 0; n < g->n_nodes; n++) {
+        const struct ggml_tensor * t = g->nodes[n];
+        if (!ggml_backend_supports_op(b, t)) {
+            *bad = t;
+            return false;
+        }
+        for (int k = 0; k < GGML_MAX_SRC; k++) {
+            const struct ggml_tensor * src = t->src[k];
+            if (!src) {
+                continue;
+            }
+            const struct ggml_tensor * base = src->view_src ? src->view_src : src;
+            if (base->buffer && !ggml_backend_supports_buft(b, ggml_backend_buffer_get_type(base->buffer))) {
+                *bad = t;
+                return false;
+            }
+        }
+    }
+    return true;
+}
+
+extern "C" bool ggml_backend_sched_reserve(ggml_backend_sched_t s, struct ggml_cgraph * g) {
+    const struct ggml_tensor * bad = nullptr;
+    for (size_t i = 0; i < s->backends.size(); i++) {
+        if (sched_fits(s, i, g, &bad)) {
+            if (!s->galloc[i]) {
+                s->galloc[i] = ggml_gallocr_new(s->bufts[i]);
+            }
+            return s->galloc[i] && ggml_gallocr_reserve(s->galloc[i], g);
+        }
+    }
+    return false;
+}
+
+extern "C" bool ggml_backend_sched_alloc_graph(ggml_backend_sched_t s, struct ggml_cgraph * g) {
+    const struct ggml_tensor * bad = nullptr;
+    for (size_t i = 0; i < s->backends.size(); i++) {
+        if (!sched_fits(s, i, g, &bad)) {
+            continue;
+        }
+        if (!s->galloc[i]) {
+            s->galloc[i] = ggml_gallocr_new(s->bufts[i]);
+        }
+        if (!s->galloc[i] || !ggml_gallocr_alloc_graph(s->galloc[i], g)) {
+            core_log(GGML_LOG_LEVEL_ERROR, "ggml_backend_sched_alloc_graph: allocation on %s failed\n",
+                     ggml_backend_name(s->backends[i]));
+            return false;
+        }
+        s->chosen = (int) i;
+        return true;
+    }
+    core_log(GGML_LOG_LEVEL_ERROR,
+             "ggml_backend_sched_alloc_graph: no backend runs the whole graph (first refusal: node %s, %s); this "
+             "build has no CPU compute backend to split to\n",
+             bad ? bad->name : "?", bad ? ggml_op_name(bad->op) : "?");
+    return false;
+}
+
+extern "C" enum ggml_status ggml_backend_sched_graph_compute_async(ggml_backend_sched_t s, struct ggml_cgraph * g) {
+    if (s->chosen < 0 && !ggml_backend_sched_alloc_graph(s, g)) {
+        return GGML_STATUS_ALLOC_FAILED;
+    }
+    return ggml_backend_graph_compute_async(s->backends[(size_t) s->chosen], g);
+}
+
+extern "C" void ggml_backend_sched_synchronize(ggml_backend_sched_t s) {
+    for (auto * b : s->backends) {
+        ggml_backend_synchronize(b);
+    }
+}
+
+extern "C" enum ggml_status ggml_backend_sched_graph_compute(ggml_backend_sched_t s, struct ggml_cgraph * g) {
+    const enum ggml_status st = ggml_backend_sched_graph_compute_async(s, g);
+    ggml_backend_sched_synchronize(s);
+    return st;
 }

@@ -9,6 +9,17 @@ import oracle
 class LmState:
     """Host copies of the model (GGUF bytes / f32) and of the f16 KV caches."""
 
+    @classmethod
+    def from_arrays(cls, cfg, weights, k, v):
+        """cfg: an object with the mm_lm config fields; weights: name -> GGUF
+        bytes / f32 array under the mm_lm names (plus "embed_tokens" for the
+        prefill); k, v: per layer f16 [n_sets, Nkv, max_seq, D]."""
+        st = cls.__new__(cls)
+        st.c, st.w = cfg, dict(weights)
+        st.k = [np.array(a, dtype=np.float16, copy=True) for a in k]
+        st.v = [np.array(a, dtype=np.float16, copy=True) for a in v]
+        return st
+
     def __init__(self, lm):
         c = lm.cfg
         self.c = c
@@ -24,6 +35,69 @@ class LmState:
         shp = (c.n_sets, c.n_kv_heads, c.max_seq, c.head_dim)
         self.k = [lm.get(f"kv_k4_{l}", np.float16).reshape(shp).copy() for l in range(c.n_layers)]
         self.v = [lm.get(f"kv_v4_{l}", np.float16).reshape(shp).copy() for l in range(c.n_layers)]
+
+
+def _qkv_rows(st, l, h, pos, sets_rows, mm):
+    """The attention block's head rows for the token rows h [T, H]: the norm,
+    the QKV projection, q/k-norm and RoPE; writes K / V of token i into cache
+    row sets_rows[i] = (set, row) and returns q [T, Nh, D]."""
+    c = st.c
+    D, Nh, Nkv = c.head_dim, c.n_heads, c.n_kv_heads
+    q_dim, kv_dim, H = Nh * D, Nkv * D, c.hidden
+    T = h.shape[0]
+    p = f"blk.{l}."
+    x = oracle.rms_norm_mul(h, st.w[p + "attn_norm"], c.rms_eps)
+    qkv = mm(p + "qkv", q_dim + 2 * kv_dim, H, x)
+    q = oracle.rms_norm_mul(qkv[:, :q_dim].reshape(T, Nh, D), st.w[p + "q_norm"], c.rms_eps)
+    k = oracle.rms_norm_mul(qkv[:, q_dim:q_dim + kv_dim].reshape(T, Nkv, D), st.w[p + "k_norm"], c.rms_eps)
+    v = qkv[:, q_dim + kv_dim:].reshape(T, Nkv, D)
+    q = oracle.rope_neox(q, pos, D, c.rope_theta)
+    k = oracle.rope_neox(k, pos, D, c.rope_theta)
+    for i, (s, r) in enumerate(sets_rows):
+        st.k[l][s, :, r] = k[i].astype(np.float16)
+        st.v[l][s, :, r] = v[i].astype(np.float16)
+    return q
+
+
+def prefill(st, tokens, kv_set, kv_pos, flavour="ggml"):
+    """qw3lm_forward (src/qwen3-lm.h:451-643) for one set from token ids:
+    embedding rows (GET_ROWS of embed_tokens), the layers with causal attention
+    over the padded window [0, n_kv_pad) of the set's cache, the final norm;
+    returns (logits of the last token [V], final-norm hidden states [T, H])
+    and writes the prompt's K / V rows into st's caches."""
+    c = st.c
+    H, D, Nh = c.hidden, c.head_dim, c.n_heads
+    q_dim = Nh * D
+    T = len(tokens)
+    t = c.wtype
+
+    def mm(name, n_out, k_in, x):
+        if flavour == "ggml":
+            return oracle.mul_mat_ggml(t, st.w[name], n_out, k_in, x)
+        return oracle.mul_mat_f64(t, st.w[name], n_out, k_in, x).astype(np.float32)
+
+    rs = oracle.row_size(t, H)
+    emb = np.asarray(st.w["embed_tokens"], np.uint8).reshape(-1, rs)
+    h = oracle.dequantize(t, emb[np.asarray(tokens)], H, T)
+    kv_len = kv_pos + T
+    n_kv_pad = min((kv_len + 255) // 256 * 256, c.max_seq)
+    mask = np.full((1, 1, T, n_kv_pad), -np.inf, np.float16)
+    for i in range(T):
+        mask[0, 0, i, :kv_pos + i + 1] = 0
+    pos = np.arange(kv_pos, kv_pos + T, dtype=np.int32)
+    scale = float(np.float32(1.0 / np.sqrt(D)))
+    for l in range(c.n_layers):
+        p = f"blk.{l}."
+        q = _qkv_rows(st, l, h, pos, [(kv_set, int(r)) for r in pos], mm)
+        kw = np.ascontiguousarray(st.k[l][kv_set:kv_set + 1, :, :n_kv_pad])
+        vw = np.ascontiguousarray(st.v[l][kv_set:kv_set + 1, :, :n_kv_pad])
+        q4 = np.ascontiguousarray(q.transpose(1, 0, 2)[None])  # [1, Hq, T, D]
+        o = oracle.flash_attn_ext(q4, kw, vw, mask, scale, "ggml" if flavour == "ggml" else "f64")
+        h = h + mm(p + "o_proj", H, q_dim, np.asarray(o, np.float32).reshape(T, q_dim))
+        x = oracle.rms_norm_mul(h, st.w[p + "ffn_norm"], c.rms_eps)
+        h = h + mm(p + "down", H, c.ffn, oracle.swiglu(mm(p + "gate_up", 2 * c.ffn, H, x)))
+    hid = oracle.rms_norm_mul(h, st.w["output_norm"], c.rms_eps)
+    return mm("lm_head", c.vocab, H, hid[-1:])[0], hid
 
 
 def decode(st, embeds, sets, kv_pos, flavour="ggml"):
