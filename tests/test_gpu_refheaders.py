@@ -206,3 +206,200 @@ def test_reference_lm_code_runs_on_the_backend(pkg, mm, tmp_path):
                 assert np.argmax(dl[step, s]) == np.argmax(rl[s])
     finally:
         lm.close()
+
+
+# ---------------------------------------------------------------------------
+# the RVQ depth decoder (src/depth-decoder.h): its dimensions are fixed by the
+# reference (DIM 4096, 4 layers of 16 x 256 heads, FFN 6144, 7 heads of 1024)
+
+DEPTH_DRIVER = ROOT / "tests" / "refheaders" / "_build" / "depth_driver"
+DDIM, DLAYERS, DHEADS, DHD, DFF, DV, DNC = 4096, 4, 16, 256, 6144, 1024, 7
+
+
+def _depth_model(pkg, seed):
+    """GGUF tensors (Q8_0 projections / heads / audio embedding table, f32
+    norms and positional table) and the same by name."""
+    rng = np.random.default_rng(seed)
+    s = [seed * 1000]
+
+    def q8(rows, k):
+        s[0] += 1
+        return pkg.synth.gguf_blocks_np(Q8_0, rows, k, s[0])
+
+    def norm(n):
+        return (1.0 + 0.05 * rng.standard_normal(n)).astype(np.float32)
+
+    w = {"projection.weight": (Q8_0, [DDIM, DDIM], q8(DDIM, DDIM)),
+         "pos_embedding.weight": (F32, [DDIM, 16], (0.5 * rng.standard_normal((16, DDIM))).astype(np.float32)),
+         "norm.weight": (F32, [DDIM], norm(DDIM))}
+    for i in range(DLAYERS):
+        p = f"layers.{i}."
+        w[p + "input_layernorm.weight"] = (F32, [DDIM], norm(DDIM))
+        for n in ("to_q", "to_k", "to_v", "to_out"):
+            w[p + f"attn.{n}.weight"] = (Q8_0, [DDIM, DDIM], q8(DDIM, DDIM))
+        w[p + "post_attention_layernorm.weight"] = (F32, [DDIM], norm(DDIM))
+        w[p + "gate_proj.weight"] = (Q8_0, [DDIM, DFF], q8(DFF, DDIM))
+        w[p + "up_proj.weight"] = (Q8_0, [DDIM, DFF], q8(DFF, DDIM))
+        w[p + "down_proj.weight"] = (Q8_0, [DFF, DDIM], q8(DDIM, DFF))
+    for i in range(DNC):
+        w[f"audio_heads.{i}.weight"] = (Q8_0, [DDIM, DV], q8(DV, DDIM))
+    w["audio_embeddings.weight"] = (Q8_0, [DDIM, DNC * DV], q8(DNC * DV, DDIM))
+    return w
+
+
+class _DepthRef:
+    """Restatement of depth_model (src/depth-decoder.h:196-259) in two
+    flavours: "ggml", the Q8_0 MUL_MATs through the oracle's ggml-CPU
+    arithmetic (Q8_0 activations, integer block dots), and "f64", exact
+    products of the dequantised weights in float64; in both the attention's
+    f32 x f32 products, DIAG_MASK_INF and SOFT_MAX in float64 rounded to f32,
+    RMS norms through the oracle."""
+
+    def __init__(self, orc, w, flavour="ggml"):
+        self.orc, self.w, self.flavour = orc, w, flavour
+
+    def mm(self, name, x):
+        _, ne, data = self.w[name]
+        x = np.ascontiguousarray(x, np.float32)
+        if self.flavour == "ggml":
+            return self.orc.mul_mat_ggml(Q8_0, data, ne[1], ne[0], x)
+        return self.orc.mul_mat_f64(Q8_0, data, ne[1], ne[0], x).astype(np.float32)
+
+    def rms(self, x, name):
+        return self.orc.rms_norm_mul(x, self.w[name][2], 1e-6)
+
+    def forward(self, seq):
+        """seq [B, S, DIM] -> (hiddens [B, S, DIM], last-step logits [B, 1024])."""
+        B, S, _ = seq.shape
+        x = self.mm("projection.weight", seq.reshape(B * S, DDIM)).reshape(B, S, DDIM)
+        x = (x + self.w["pos_embedding.weight"][2][:S]).astype(np.float32)
+        mask = np.triu(np.ones((S, S), bool), 1)
+        for i in range(DLAYERS):
+            p = f"layers.{i}."
+            h = self.rms(x, p + "input_layernorm.weight").reshape(B * S, DDIM)
+            q, k, v = (self.mm(p + f"attn.{n}.weight", h).reshape(B, S, DHEADS, DHD).transpose(0, 2, 1, 3)
+                       .astype(np.float64) for n in ("to_q", "to_k", "to_v"))
+            sc = (q @ k.transpose(0, 1, 3, 2)).astype(np.float32) * np.float32(1.0 / np.sqrt(np.float32(DHD)))
+            sc = np.where(mask, -np.inf, sc).astype(np.float64)
+            pr = np.exp(sc - sc.max(-1, keepdims=True))
+            pr = (pr / pr.sum(-1, keepdims=True)).astype(np.float32)
+            a = (pr.astype(np.float64) @ v).astype(np.float32).transpose(0, 2, 1, 3).reshape(B * S, DDIM)
+            x = (x + self.mm(p + "attn.to_out.weight", a).reshape(B, S, DDIM)).astype(np.float32)
+            h = self.rms(x, p + "post_attention_layernorm.weight").reshape(B * S, DDIM)
+            g, u = self.mm(p + "gate_proj.weight", h), self.mm(p + "up_proj.weight", h)
+            act = (g / (1.0 + np.exp(-g.astype(np.float64)))).astype(np.float32) * u
+            x = (x + self.mm(p + "down_proj.weight", act).reshape(B, S, DDIM)).astype(np.float32)
+        hid = self.rms(x, "norm.weight")
+        return hid, self.mm(f"audio_heads.{S - 2}.weight", np.ascontiguousarray(hid[:, -1]))
+
+    def embed(self, cb, code):
+        """Row (cb - 1) * 1024 + code of the audio embedding table (GET_ROWS of
+        its Q8_0 view: the dequantised row)."""
+        _, ne, data = self.w["audio_embeddings.weight"]
+        rs = data.size // ne[1]
+        r = (cb - 1) * DV + code
+        return self.orc.dequantize(Q8_0, data.reshape(-1)[r * rs:(r + 1) * rs], DDIM, 1)[0]
+
+
+def _sample(logits, cfg, k, u):
+    """The in-graph CFG sampler of one step (src/depth-decoder.h:331-358):
+    (pick index into the top-k, the top-k ids, the CDF)."""
+    cond, uncond = logits[0].astype(np.float32), logits[1].astype(np.float32)
+    guided = uncond + (cond - uncond) * np.float32(cfg)
+    idx = np.lexsort((np.arange(DV), -guided))[:k]
+    g = guided[idx].astype(np.float64)
+    p = np.exp(g - g.max())
+    cdf = np.cumsum((p / p.sum()).astype(np.float32), dtype=np.float32)
+    pick = int(min(max(k - int((cdf > np.float32(u)).sum()), 0), k - 1))
+    return pick, idx, cdf
+
+
+def test_reference_depth_decoder_runs_on_the_backend(pkg, mm, orc, tmp_path):
+    """DepthDecoder::load / forward (S = 2..8) / forward_frame (three CFG
+    frames: the second replays the first's graph, the third changes cfg and
+    top_k, so the reference rebuilds the graph at reused addresses) on the
+    MI355X backend.  Stated tolerances: single-path and frame hidden states
+    and logits cosine >= 0.9999 against the ggml-semantics restatement, and a
+    relative RMS error against the f64 restatement at most 1.5x the ggml
+    restatement's own (+ 1e-4): the Q8_0 activation quantisation rounds a few
+    int8 codes differently when its f32 inputs differ in the last bits, which
+    moves results by ~1e-3 after four layers, as it moves ggml-CPU's own.  The
+    frame graph's per-step head logits (cond and uncond) meet the same
+    tolerance, and each code the in-graph sampler drew is exactly the one the
+    sampler's definition gives on those logits (unless the draw is within 1e-5
+    of a CDF entry).  A code is a discontinuous function of the logits (cfg 3
+    weighs them 3 cond - 2 uncond), so codes are not compared with the
+    restatement's picks; how many agree is printed.  The restatement follows
+    the codes the GPU sampled."""
+    assert DEPTH_DRIVER.exists(), f"{DEPTH_DRIVER} is not built"
+    w = _depth_model(pkg, 21)
+    gguf_writer.write(tmp_path / "depth.gguf", [], [(n, t, ne, d) for n, (t, ne, d) in w.items()])
+    rng = np.random.default_rng(22)
+    seq = rng.standard_normal((8, DDIM)).astype(np.float32)
+    seq.tofile(tmp_path / "single_seq.bin")
+    frames = [(3.0, 50), (3.0, 50), (1.5, 20)]
+    fr_in = []
+    for cfg, k in frames:
+        fr_in.append((rng.standard_normal((2, 2, DDIM)).astype(np.float32), rng.uniform(0.02, 0.98, DNC)
+                      .astype(np.float32), cfg, k))
+    np.concatenate([np.concatenate([s.ravel(), r, np.array([c, k], np.float32)]) for s, r, c, k in fr_in]) \
+        .astype(np.float32).tofile(tmp_path / "frames.bin")
+
+    print("running the reference depth-decoder driver", flush=True)
+    env = dict(os.environ, GGML_BACKEND="MI355X0")
+    r = subprocess.run([str(DEPTH_DRIVER), str(tmp_path / "depth.gguf"), str(tmp_path), str(len(frames))],
+                       capture_output=True, text=True, timeout=280, env=env)
+    print(r.stderr[-2000:], flush=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    info = json.loads(r.stdout.strip().splitlines()[-1])
+    print(info, flush=True)
+    assert info["backend"] == "MI355X0" and info["fused_nodes"] > 500
+    assert info["replays"] >= 1
+
+    ref, ref64 = _DepthRef(orc, w), _DepthRef(orc, w, "f64")
+
+    def relrms(a, b):
+        a, b = np.asarray(a, np.float64).ravel(), np.asarray(b, np.float64).ravel()
+        return float(np.sqrt(np.mean((a - b) ** 2) / np.mean(b * b)))
+
+    def close(a, b, e):
+        assert cosine(a, b) >= 0.9999, cosine(a, b)
+        assert relrms(a, e) <= 1.5 * relrms(b, e) + 1e-4, (relrms(a, e), relrms(b, e))
+
+    hid = np.fromfile(tmp_path / "single_hiddens.bin", np.float32)
+    lg = np.fromfile(tmp_path / "single_logits.bin", np.float32).reshape(DNC, DV)
+    o = 0
+    for S in range(2, 9):
+        rh, rl = ref.forward(seq[None, :S])
+        eh, el = ref64.forward(seq[None, :S])
+        g = hid[o:o + S * DDIM]
+        print(f"single S={S}: hidden cosine {cosine(g, rh)}, rel-RMS vs f64 {relrms(g, eh):.2e} (restatement "
+              f"{relrms(rh, eh):.2e}); logits cosine {cosine(lg[S - 2], rl)}", flush=True)
+        close(g, rh, eh)
+        close(lg[S - 2], rl, el)
+        o += S * DDIM
+
+    codes = np.fromfile(tmp_path / "codes.bin", np.int32).reshape(len(frames), DNC)
+    ch = np.fromfile(tmp_path / "cond_hiddens.bin", np.float32).reshape(len(frames), DNC, DDIM)
+    slg = np.fromfile(tmp_path / "step_logits.bin", np.float32).reshape(len(frames), DNC, 2, DV)
+    for f, (s0, rnd, cfg, k) in enumerate(fr_in):
+        cur = s0.copy()  # [2 streams, S, DIM]
+        exact_picks = 0
+        for cb in range(1, DNC + 1):
+            rh, rl = ref.forward(cur)
+            eh, el = ref64.forward(cur)
+            close(ch[f, cb - 1], rh[0, -1], eh[0, -1])
+            close(slg[f, cb - 1], rl, el)
+            # the in-graph sampler against the GPU's own logits: exact pick
+            # unless the draw is within 1e-5 of a CDF entry
+            gpick, gidx, gcdf = _sample(slg[f, cb - 1], cfg, k, rnd[cb - 1])
+            assert int(codes[f, cb - 1]) == int(gidx[gpick]) or np.abs(gcdf - rnd[cb - 1]).min() < 1e-5, \
+                (f, cb, int(codes[f, cb - 1]), int(gidx[gpick]))
+            pick, idx, _ = _sample(rl, cfg, k, rnd[cb - 1])
+            got = int(codes[f, cb - 1])
+            exact_picks += got == int(idx[pick])
+            if cb < DNC:
+                row = ref.embed(cb, got)
+                cur = np.concatenate([cur, np.stack([row, row])[:, None]], axis=1)
+        print(f"frame {f} (cfg {cfg}, top_k {k}): codes {codes[f].tolist()}, {exact_picks} of {DNC} equal to the "
+              f"restatement's picks", flush=True)
