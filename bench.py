@@ -11,7 +11,7 @@ random-init weights; all inputs resident in HBM before timing):
               cache at 4096 x 2 sets.  value = 2 tokens / the GPU time of one
               step's HIP-graph replay (HIP events on the backend stream; inputs
               resident), wall_tok_s = the same with each step's host input
-              uploads and launch included; roofline = the
+              uploads, launch and logits / hidden readback included; roofline = the
               step's largest kernel (the MLP gate_up GEMV with its RMS-norm
               prologue and SwiGLU epilogue) alone; step_roofline = the step's algorithmic bytes /
               its GPU time from HIP events on the backend stream.
@@ -90,6 +90,30 @@ def graph_time(torch, fn, n, reps=10):
     return float(np.mean(ts)), float(np.min(ts))
 
 
+def profile_value(name, key, conv=float):
+    """A `key: value` line of the committed rocprofv3 summary profiles/<name>.md,
+    or None."""
+    p = ROOT / "profiles" / (name + ".md")
+    if not p.exists():
+        return None
+    for line in p.read_text().splitlines():
+        if line.startswith(key + ":"):
+            return conv(line.split(":", 1)[1].strip())
+    return None
+
+
+def mfma_counters(name):
+    """MFMA busy fraction and MFMA f16 FLOPs per launch of the profiled
+    kernel(s), from the rocprofv3 PMC passes in profiles/<name>.md
+    (SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 1024 SIMDs) and
+    SQ_INSTS_VALU_MFMA_MOPS_F16 x 512)."""
+    util = profile_value(name, "mfma_busy_frac")
+    flops = profile_value(name, "mfma_f16_flops_per_launch")
+    if util is None and flops is None:
+        return None
+    return {"mfma_busy_frac": util, "mfma_f16_flops_per_launch": flops, "source": "profiles/%s.md" % name}
+
+
 def profile_traffic(name):
     """HBM bytes per launch of a kernel, from the committed rocprofv3 PMC
     summary profiles/<name>.md (its `traffic_bytes_per_launch:` line), or None."""
@@ -112,10 +136,42 @@ def cpu_rate(fn, seconds):
     return (time.perf_counter() - t0) / it, it
 
 
+def cpu_threads():
+    """Threads the CPU baseline runs with: the CPUs this process may use
+    (affinity mask, capped by OMP_NUM_THREADS), as the oracle's default."""
+    import oracle
+
+    return oracle.default_threads()
+
+
 def half_threads():
-    """The reference's default CPU thread count: hardware_concurrency() / 2
-    (src/backend.h:25-31)."""
-    return max(1, (os.cpu_count() or 2) // 2)
+    """The reference's default CPU thread count, hardware_concurrency() / 2
+    (src/backend.h:25-31), within the CPUs this process may use."""
+    return max(1, min((os.cpu_count() or 2) // 2, cpu_threads()))
+
+
+def host_cpu():
+    """The host CPU as lscpu reports it: model, sockets x physical cores per
+    socket, threads per core, plus the logical CPUs online and this process's
+    share."""
+    import subprocess
+
+    info = {}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            info[k.strip()] = v.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+
+    def num(k):
+        v = info.get(k, "")
+        return int(v) if v.isdigit() else None
+
+    sockets, cps, tpc = num("Socket(s)"), num("Core(s) per socket"), num("Thread(s) per core")
+    return {"model": info.get("Model name"), "sockets": sockets, "physical_cores": sockets * cps if sockets and cps
+            else None, "threads_per_core": tpc, "logical_cpus": os.cpu_count(), "process_cpus": cpu_threads()}
 
 
 def via_backend(pkg, make, reps=20):
@@ -235,7 +291,7 @@ def bench_gemv(args, torch, pkg):
 
 
 def cpu_gemv(oracle, synth, N, K, M, seconds):
-    n_thr = os.cpu_count() or 1
+    n_thr = cpu_threads()
     rows = 2048  # bounded sample: 2048 of the 12288 rows
     raw = synth.gguf_blocks_np(8, rows, K, 7)
     x = synth.normal_np((M, K), 8)
@@ -312,7 +368,7 @@ def bench_fa(args, torch, pkg):
         qn = q.cpu().numpy()
         kn = ks[0].cpu().numpy()
         vn = vs[0].cpu().numpy()
-        n_thr = os.cpu_count() or 1
+        n_thr = cpu_threads()
         dt, it = cpu_rate(lambda: oracle.flash_attn_ext(qn, kn, vn, None, scale, "ggml", nthreads=n_thr),
                           args.cpu_seconds)
         nh = half_threads()
@@ -398,6 +454,7 @@ def bench_fa_mfma(args, torch, pkg, causal):
         B, Hq, Hkv, S, D, seed = 2, 16, 16, 4096, 128, 1004
         flops = 4.0 * B * Hq * S * S * D
         name = "DiT bidirectional attention B=2 S=4096 H=16 D=128"
+    prof = "fa_prefill_causal_b2_s1024_gqa" if causal else "fa_dit_b2_s4096_h16_d128"
     copies = 2
     step = _fa_common(args, torch, pkg, B, Hq, Hkv, S, D, causal, seed, copies)
     ms, avg_s, med_s = _timed(args, torch, step, copies)
@@ -435,7 +492,7 @@ def bench_fa_mfma(args, torch, pkg, causal):
         q = rng.standard_normal((B, Hq, rows, D)).astype(np.float32)
         k = rng.standard_normal((B, Hkv, S, D)).astype(np.float16)
         v = rng.standard_normal((B, Hkv, S, D)).astype(np.float16)
-        n_thr = os.cpu_count() or 1
+        n_thr = cpu_threads()
         dt, it = cpu_rate(lambda: oracle.flash_attn_ext(q, k, v, None, 1 / np.sqrt(D), "ggml", nthreads=n_thr),
                           args.cpu_seconds)
         nh = half_threads()
@@ -459,7 +516,8 @@ def bench_fa_mfma(args, torch, pkg, causal):
                      "achieved": round(tf, 2),
                      "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
                      "avg_launch_us": round(avg_s * 1e6, 2), "min_launch_us": round(med_s * 1e6, 2),
-                     "alg_flops_per_launch": flops, "traffic": profile_traffic("fa_prefill_causal_b2_s1024_gqa" if causal else "fa_dit_b2_s4096_h16_d128")},
+                     "alg_flops_per_launch": flops, "traffic": profile_traffic(prof),
+                     "mfma_counters": mfma_counters(prof)},
         "cpu_baseline": cpu,
     }
 
@@ -513,7 +571,7 @@ def bench_gemm(args, torch, pkg):
         rows = 64
         raw = synth.gguf_blocks_np(mm.Q4_K, rows, K, 9)
         x = synth.normal_np((64, K), 10)
-        n_thr = os.cpu_count() or 1
+        n_thr = cpu_threads()
         dt, it = cpu_rate(lambda: oracle.mul_mat_ggml(mm.Q4_K, raw, rows, K, x, nthreads=n_thr), args.cpu_seconds)
         nh = half_threads()
         dt_h, _ = cpu_rate(lambda: oracle.mul_mat_ggml(mm.Q4_K, raw, rows, K, x, nthreads=nh), args.cpu_seconds / 2)
@@ -532,7 +590,8 @@ def bench_gemm(args, torch, pkg):
         "roofline": {"bound": "mfma", "kernel": "k_x_to_f16 + k_gemm_q<Q4_K> (one mul_mat call)", "achieved": round(tf, 2),
                      "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
                      "avg_launch_us": round(avg_s * 1e6, 2), "min_launch_us": round(med_s * 1e6, 2),
-                     "alg_flops_per_launch": flops, "traffic": profile_traffic("gemm_q4_k_6144x2048_m8192")},
+                     "alg_flops_per_launch": flops, "traffic": profile_traffic("gemm_q4_k_6144x2048_m8192"),
+                     "mfma_counters": mfma_counters("gemm_q4_k_6144x2048_m8192")},
         "cpu_baseline": cpu,
     }
 
@@ -641,7 +700,7 @@ def bench_dit_block(args, torch, pkg):
         xc = x0[:, :Sc].copy()
         dt, it = cpu_rate(lambda: cpu_dit_block(oracle, dg, ws[0], xc, np.arange(Sc, dtype=np.int32)), args.cpu_seconds)
         cpu = {"value": round(dit_block_flops(Sc, B) / dt / 1e12, 5), "unit": "TFLOP/s",
-               "cores": oracle.default_threads(), "kind": "port",
+               "cores": cpu_threads(), "kind": "port",
                "sample": f"one DiT block from the oracle's ggml-CPU-semantics restatements (Q8_0 mul_mat, LayerNorm, "
                          f"NeoX RoPE, flash_attn_ext, SwiGLU): S={Sc} tokens x B={B}, {it} reps"}
     return {
@@ -658,7 +717,8 @@ def bench_dit_block(args, torch, pkg):
                      "achieved": round(tf, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tf / MFMA_PEAK_TFLOPS, 4), "avg_launch_us": round(avg_s * 1e6, 2),
                      "min_launch_us": round(min_s * 1e6, 2), "alg_flops_per_launch": gf,
-                     "traffic": profile_traffic("dit_block_s690_b2_q8_0")},
+                     "traffic": profile_traffic("dit_block_s690_b2_q8_0"),
+                     "mfma_counters": mfma_counters("dit_block_s690_b2_q8_0")},
         "cpu_baseline": cpu,
     }
 
@@ -724,7 +784,7 @@ def bench_depth(args, torch, pkg):
     if not args.no_cpu:
         raw = ws[0]["w_gate"][:512]
         xc = x0.reshape(-1, dg.DIM)
-        n_thr = os.cpu_count() or 1
+        n_thr = cpu_threads()
         dt, it = cpu_rate(lambda: oracle.mul_mat_ggml(mm.Q8_0, raw, 512, K, xc, nthreads=n_thr), args.cpu_seconds)
         cpu = {"value": round(512 * K * 34 / 32 / dt / 1e9, 3), "unit": "GB/s (weight bytes streamed)", "cores": n_thr,
                "kind": "port", "sample": f"ggml-CPU-semantics Q8_0 mul_mat (oracle/oracle.c): 512 gate rows x {M} "
@@ -776,10 +836,12 @@ def bench_lm(args, torch, pkg):
     emb = np.random.default_rng(1005).standard_normal((2, cfg["hidden"])).astype(np.float32)
 
     def step():
-        # every step attends over KV 4096 (positions reset to 4095)
+        # every step attends over KV 4096 (positions reset to 4095); the
+        # step reads its logits and final hidden states back to the host, as
+        # the reference does after every batched decode (src/qwen3-lm.h:923-927)
         lm.set_pos(0, 4095)
         lm.set_pos(1, 4095)
-        lm.decode_device(emb, [0, 1])
+        lm.decode(emb, [0, 1])
 
     for _ in range(max(args.warmup, 3)):
         step()
@@ -868,7 +930,7 @@ def cpu_lm(args, lm_mod, cfg):
     import oracle
 
     sys.path.insert(0, str(ROOT / "tests"))
-    n_thr = os.cpu_count() or 1
+    n_thr = cpu_threads()
     H, D, Nh, Nkv, F, V = cfg["hidden"], cfg["head_dim"], cfg["n_heads"], cfg["n_kv_heads"], cfg["ffn"], cfg["vocab"]
     t = cfg["wtype"]
     rng = np.random.default_rng(7)
@@ -952,6 +1014,8 @@ def main():
     for k in ("step_roofline", "wall_tok_s", "wall_ms_per_step", "via_backend"):
         if k in res:
             line[k] = res[k]
+    if isinstance(line["cpu_baseline"], dict):
+        line["cpu_baseline"]["host"] = host_cpu()
     print(json.dumps(line), flush=True)
 
 

@@ -84,7 +84,16 @@ def _p(a):
 
 
 def default_threads():
-    return max(1, os.cpu_count() or 1)
+    """Threads the restatement uses: the CPUs this process may run on (its
+    affinity mask), capped by OMP_NUM_THREADS when that is set."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
 
 
 # ---- conversions ----
