@@ -512,7 +512,8 @@ def bench_fa_mfma(args, torch, pkg, causal):
         "config": {"workload": name, "mask": "causal f16" if causal else "none"},
         "via_backend": backend,
         "roofline": {"bound": "mfma",
-                     "kernel": "k_fa_mfma<128,8>" + (" + k_fa_row_end mask prepass (one attention call)" if causal else ""),
+                     "kernel": ("k_fa_mfma<128,8> + k_fa_row_end mask prepass (one attention call)" if causal
+                                else "k_fa_dma"),
                      "achieved": round(tf, 2),
                      "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
                      "avg_launch_us": round(avg_s * 1e6, 2), "min_launch_us": round(med_s * 1e6, 2),

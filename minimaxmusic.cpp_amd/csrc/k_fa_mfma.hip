@@ -19,6 +19,11 @@
 // can see; a workgroup stops at the last key any of its rows can see, so fully
 // masked KV tiles (the causal upper triangle, the -inf padding of the cache
 // window) are never read.
+//
+// The unmasked D = 128 case on a full grid (the DiT) runs k_fa_dma instead,
+// described above its definition below.
+#include <type_traits>
+
 #include "k_fa_common.h"
 #include "mmhip_device.h"
 #include "mmhip_internal.h"
@@ -332,6 +337,351 @@ __global__ __launch_bounds__(NW * 64) void k_fa_mfma(FaArgs a, const int * __res
     }
 }
 
+// ---------------------------------------------------------------------------
+// Unmasked D = 128 with a full grid (the DiT's attention, src/dit.h:221-222):
+// k_fa_dma.  The chip runs MFMA work at a power-limited clock that drops
+// further with every VALU op and LDS byte issued beside it, so this kernel
+// minimises both per MFMA:
+//  - K / V tiles (64 keys, 16 KB each) go from global memory straight into a
+//    double-buffered LDS ring with global_load_lds (no register staging, no
+//    transposing stores); K rows store 16-byte chunk c at c ^ (row & 15), V
+//    rows at c ^ 2 (row & 3), which keeps both read patterns bank-conflict
+//    free;
+//  - V^T operands come from ds_read_b64_tr_b16: within each 16-lane group,
+//    lane i receives element i % 4 of the 4-element rows addressed by lanes
+//    4 j + i / 4 (j = 0..3), so the lanes address V rows in exactly the key
+//    order the S^T accumulator registers hold (bits 2 and 3 of the key swapped);
+//  - Q is scaled by scale * log2(e) before its f16 rounding, and every QK
+//    accumulator starts at -m (the running row max, log2 units): the scores
+//    come out as s - m and p = exp2(s - m) is one v_exp per score; the row
+//    sum adds the f16 p pairs with v_dot2 (the same values the PV MFMA uses);
+//  - the running max moves only on a slow path: on a row's first 32 keys, or
+//    when a lane's partial sum exceeds 2^14 (some score more than 14 above
+//    m); O and l are then rescaled by exp2(-shift).  p stays below 2^15,
+//    inside f16.
+// Pipeline per wave (32 query rows, 8 waves, two per SIMD): unit u = 32 keys;
+// unit u runs the softmax of unit u (VALU) between the MFMAs of QK(u + 1) and
+// PV(u - 1), with the LDS operands of MFMA step i + 2 read during step i.  One
+// barrier per 64-key tile.
+__device__ __forceinline__ void fa_dma16(const void * src, uint32_t lds_addr) {
+    // issued from inline asm: the compiler's wait-count tracking would
+    // otherwise wait for the DMA before unrelated LDS reads; the kernel waits
+    // for it itself before the barrier that publishes a tile
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr) : "memory", "m0");
+}
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4_t lds_short4_t;
+
+__global__ __launch_bounds__(512) void k_fa_dma(FaArgs a, int n_qtiles, float * __restrict__ out) {
+    constexpr int D = 128, NQK = 8, NDB = 4, TILE = FA_BK * 256;
+    __shared__ __attribute__((aligned(1024))) char smem[4 * TILE];  // K ring (2 tiles), V ring (2 tiles)
+    const int  total = n_qtiles * a.Hq * a.B;
+    const int  lin   = xcd_remap((int) blockIdx.x, total);
+    const int  qt    = lin % n_qtiles;
+    const int  h     = (lin / n_qtiles) % a.Hq;
+    const int  b     = lin / (n_qtiles * a.Hq);
+    const int  hk    = h / (a.Hq / a.Hkv);
+    const int  bk    = b / (a.B / a.Bk);
+    const int  tid   = threadIdx.x;
+    const int  wave  = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int  lane  = tid & 63;
+    const int  lq    = lane & 31;
+    const int  hh    = lane >> 5;
+    const int  my_q  = qt * 256 + wave * 32 + lq;
+    const bool q_ok  = my_q < a.nq;
+    const float sl2  = a.scale * 1.4426950408889634f;
+
+    // Q^T operand: dims 16 kk + 8 hh + 0..7 of this lane's query, scaled, f16
+    half8_t qreg[NQK];
+    {
+        const float * qp = (const float *) (a.q + (int64_t) (q_ok ? my_q : 0) * a.qnb1 + h * a.qnb2 + b * a.qnb3);
+#pragma unroll
+        for (int kk = 0; kk < NQK; kk++) {
+            const float4_t x0 = *(const float4_t *) (qp + 16 * kk + 8 * hh);
+            const float4_t x1 = *(const float4_t *) (qp + 16 * kk + 8 * hh + 4);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                qreg[kk][i]     = (_Float16) (x0[i] * sl2);
+                qreg[kk][i + 4] = (_Float16) (x1[i] * sl2);
+            }
+        }
+    }
+    float16_t oacc[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; i++) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            oacc[i][r] = 0.0f;
+        }
+    }
+    float m = 0.0f;  // running row max (log2 units)
+    float l = 0.0f;  // this lane's half of the row sum
+    const int n  = (a.nkv + FA_BK - 1) / FA_BK;  // 64-key tiles
+    const int nu = (a.nkv + 31) / 32;            // 32-key units
+
+    // DMA: this wave fills 1 KB pieces 2 wave and 2 wave + 1 (4 rows each) of
+    // a K and a V tile; lane -> row 4 piece + lane / 16, stored chunk lane % 16
+    const char *   kbase = a.k + hk * a.knb2 + bk * a.knb3;
+    const char *   vbase = a.v + hk * a.vnb2 + bk * a.vnb3;
+    const uint32_t sbase = (uint32_t) (uintptr_t) (__attribute__((address_space(3))) char *) smem;
+    const int      drow = lane >> 4, dpc = lane & 15;
+    auto dma_k = [&](int j) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int piece = 2 * wave + i, r = 4 * piece + drow;
+            const int key   = min(j * FA_BK + r, a.nkv - 1);  // rows past the end repeat the last key (masked below)
+            fa_dma16(kbase + (int64_t) key * a.knb1 + ((dpc ^ (r & 15)) << 4), sbase + (j & 1) * TILE + piece * 1024);
+        }
+    };
+    auto dma_v = [&](int j) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int piece = 2 * wave + i, r = 4 * piece + drow;
+            const int key   = min(j * FA_BK + r, a.nkv - 1);
+            fa_dma16(vbase + (int64_t) key * a.vnb1 + ((dpc ^ (2 * (r & 3))) << 4),
+                     sbase + (2 + (j & 1)) * TILE + piece * 1024);
+        }
+    };
+    // K operand of k-step kk: row lq of the 32-key unit, logical chunk 2 kk + hh
+    uint32_t ka[NQK];
+#pragma unroll
+    for (int kk = 0; kk < NQK; kk++) {
+        ka[kk] = lq * 256 + (((2 * kk + hh) ^ (lq & 15)) << 4);
+    }
+    // V^T operand: source lane (tg, tj, tq) of a transposed read addresses
+    // V[key0 + 4 (tg / 2) + tj][32 db + 16 (tg & 1) + 4 tq]; the V swizzle
+    // 2 (key & 3) = 2 tj folds into +-64 bytes on even / odd db
+    const int      tg = lane >> 4, tj = (lane >> 2) & 3, tq = lane & 3;
+    const int      vx = (tj >> 1) * 64;
+    const uint32_t vlane =
+        (4 * (tg >> 1) + tj) * 256 + 16 * ((2 * (tg & 1) + (tq >> 1)) ^ (2 * (tj & 1))) + 8 * (tq & 1);
+    const uint32_t vb[2] = { vlane + vx, vlane - vx };
+    auto qk_op = [&](int u, int kk) -> half8_t {
+        const char * kt = smem + ((u >> 1) & 1) * TILE;
+        return *(const half8_t *) (kt + ka[kk] + (u & 1) * 8192);
+    };
+    // PV step i of a unit: key half t = i / 4 (16 keys), output block db = i % 4
+    auto pv_op = [&](int u, int i) -> half8_t {
+        const uint32_t vt = sbase + (2 + ((u >> 1) & 1)) * TILE;
+        const int      t = i >> 2, db = i & 3;
+        half8_t        av;
+#pragma unroll
+        for (int hf = 0; hf < 2; hf++) {
+            const uint32_t ad = vt + vb[db & 1] + ((u & 1) * 32 + 16 * t + 8 * hf) * 256 + 64 * db;
+            const half4_t  x  = __builtin_bit_cast(
+                half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t *) (uintptr_t) ad));
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                av[4 * hf + e] = x[e];
+            }
+        }
+        return av;
+    };
+
+    float16_t zero16, negm;  // negm: -m in every register, the C operand of a unit's first QK MFMA
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        zero16[r] = 0.0f;
+        negm[r]   = 0.0f;
+    }
+    float16_t sc, sn;         // s - m of unit u (softmax input) and of unit u + 1 (being computed)
+    half8_t   pp[2], pn[2];   // P of unit u - 1 (PV input) and of unit u (softmax output)
+    float     m_sn = 0.0f;    // the m that sn was computed against
+    const half2_t ones2 = { (_Float16) 1.0f, (_Float16) 1.0f };
+    auto exp_pack = [&](float & rs) {
+        rs = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+            const half2_t pk = { (_Float16) __builtin_amdgcn_exp2f(sc[r]), (_Float16) __builtin_amdgcn_exp2f(sc[r + 1]) };
+            rs                        = __builtin_amdgcn_fdot2(pk, ones2, rs, false);
+            pn[r >> 3][r & 7]         = pk[0];
+            pn[r >> 3][(r & 7) + 1]   = pk[1];
+        }
+    };
+    // move m to the row max (first unit: exactly; later: upwards only),
+    // rescale O and l, redo the unit's p
+    auto slow = [&](float & rs, bool first) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            mx = fmaxf(mx, sc[r]);
+        }
+        mx            = max_xor32(mx);
+        const float d = first ? (mx == -INFINITY ? 0.0f : mx) : (mx > 0.0f ? mx : 0.0f);
+        if (__any(d != 0.0f)) {
+            if (!first) {  // O and l are still zero on the first unit
+                const float alpha = __builtin_amdgcn_exp2f(-d);
+                l *= alpha;
+#pragma unroll
+                for (int q = 0; q < NDB; q++) {
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        oacc[q][r] *= alpha;
+                    }
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                sc[r] -= d;
+            }
+            m += d;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                negm[r] = -m;
+            }
+        }
+        exp_pack(rs);
+    };
+    // unit u: softmax(u) (SM), QK(u + 1) (QK), PV(u - 1) (PV); which parts
+    // are present is a compile-time choice, so the steady-state unit is
+    // branch-free and the compiler interleaves its VALU work with the MFMAs
+    auto unit = [&](int u, auto QKc, auto PVc, auto SMc) {
+        constexpr bool do_qk = decltype(QKc)::value, do_pv = decltype(PVc)::value, do_sm = decltype(SMc)::value;
+        if constexpr (do_sm) {
+            const int k0 = u * 32;
+            if (k0 + 32 > a.nkv) {  // the last, partial unit
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    if (k0 + 8 * (r / 4) + 4 * hh + (r % 4) >= a.nkv) {
+                        sc[r] = -INFINITY;
+                    }
+                }
+            }
+        }
+        const float m_used = m;
+        float       rs     = 0.0f;
+        half8_t     av[3], ak[3];
+        if constexpr (do_pv) {
+            av[0] = pv_op(u - 1, 0);
+            av[1] = pv_op(u - 1, 1);
+        }
+        if constexpr (do_qk) {
+            ak[0] = qk_op(u + 1, 0);
+            ak[1] = qk_op(u + 1, 1);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            if (i + 2 < 8) {
+                if constexpr (do_pv) {
+                    av[(i + 2) % 3] = pv_op(u - 1, i + 2);
+                }
+                if constexpr (do_qk) {
+                    ak[(i + 2) % 3] = qk_op(u + 1, i + 2);
+                }
+            }
+            if constexpr (do_pv) {
+                oacc[i & 3] = mfma32(av[i % 3], pp[i >> 2], oacc[i & 3]);
+            }
+            if constexpr (do_qk) {
+                sn = mfma32(ak[i % 3], qreg[i], i == 0 ? negm : sn);
+            }
+            if constexpr (do_sm) {
+                const int     r  = 2 * i;
+                const half2_t pk = { (_Float16) __builtin_amdgcn_exp2f(sc[r]),
+                                     (_Float16) __builtin_amdgcn_exp2f(sc[r + 1]) };
+                rs                      = __builtin_amdgcn_fdot2(pk, ones2, rs, false);
+                pn[r >> 3][r & 7]       = pk[0];
+                pn[r >> 3][(r & 7) + 1] = pk[1];
+            }
+        }
+        if constexpr (do_sm) {
+            if (u == 0 || __any(rs > 16384.0f)) {
+                slow(rs, u == 0);
+            }
+            l += rs;
+        }
+        if constexpr (do_qk) {
+            m_sn = m_used;
+        }
+    };
+    // after unit u: sn becomes the next softmax input (shifted if m moved
+    // since it was computed); after an even unit 2 j: barrier, then the DMA
+    // of K tile j + 2 (into the buffer of K tile j, last read in unit 2 j) and
+    // V tile j + 1 (buffer of V tile j - 1, last read in unit 2 j), waited
+    // for before the barrier after unit 2 j + 2
+    auto after = [&](int u) {
+        sc = sn;
+        if (__any(m_sn != m)) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                sc[r] += m_sn - m;
+            }
+        }
+        pp[0] = pn[0];
+        pp[1] = pn[1];
+        if ((u & 1) == 0) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            asm volatile("s_barrier" ::: "memory");
+            const int j = u >> 1;
+            if (j + 2 < n) {
+                dma_k(j + 2);
+            }
+            if (j + 1 < n) {
+                dma_v(j + 1);
+            }
+        }
+    };
+
+    // prologue: K tiles 0 and 1, V tile 0 resident; scores of unit 0 (m = 0)
+    dma_k(0);
+    if (n > 1) {
+        dma_k(1);
+    }
+    dma_v(0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");
+    sc = zero16;
+#pragma unroll
+    for (int kk = 0; kk < NQK; kk++) {
+        sc = mfma32(qk_op(0, kk), qreg[kk], sc);
+    }
+    using T_ = std::integral_constant<bool, true>;
+    using F_ = std::integral_constant<bool, false>;
+    if (nu > 1) {
+        unit(0, T_{}, F_{}, T_{});
+    } else {
+        unit(0, F_{}, F_{}, T_{});
+    }
+    after(0);
+    for (int u = 1; u + 1 < nu; u++) {
+        unit(u, T_{}, T_{}, T_{});
+        after(u);
+    }
+    if (nu > 1) {
+        unit(nu - 1, F_{}, T_{}, T_{});
+        after(nu - 1);
+    }
+    unit(nu, F_{}, T_{}, F_{});
+
+    l += __shfl_xor(l, 32);
+    if (q_ok) {
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        float *     op  = out + (((int64_t) b * a.nq + my_q) * a.Hq + h) * D;
+#pragma unroll
+        for (int db = 0; db < NDB; db++) {
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++) {
+                const int d = db * 32 + 8 * g4 + 4 * hh;
+                float4_t  v = { oacc[db][4 * g4] * inv, oacc[db][4 * g4 + 1] * inv, oacc[db][4 * g4 + 2] * inv,
+                                oacc[db][4 * g4 + 3] * inv };
+                *(float4_t *) (op + d) = v;
+            }
+        }
+    }
+}
+
+// k_fa_dma's preconditions: 16-byte aligned Q rows (float4 loads) and K / V
+// rows (16-byte DMA), D = 128, no mask, and at least one workgroup of 256
+// rows per CU
+static bool fa_dma_ok(const FaArgs & a, int D) {
+    auto al16 = [](int64_t v) { return (v & 15) == 0; };
+    const int64_t tiles = (int64_t) ((a.nq + 255) / 256) * a.Hq * a.B;
+    return D == 128 && !a.mask && tiles >= 256 && a.nkv >= 1 && al16((int64_t) (uintptr_t) a.q) && al16(a.qnb1) &&
+           al16(a.qnb2) && al16(a.qnb3) && al16((int64_t) (uintptr_t) a.k) && al16(a.knb1) && al16(a.knb2) &&
+           al16(a.knb3) && al16((int64_t) (uintptr_t) a.v) && al16(a.vnb1) && al16(a.vnb2) && al16(a.vnb3);
+}
+
 // Mask prepass: for every mask plane (mask batch x mask head) and query row,
 // one past the last key whose mask value is not -inf (0 if the row is fully
 // masked), and the length of the row's leading run of exact zeros (+-0: no
@@ -430,7 +780,10 @@ int fa_mfma(const FaArgs & a, int D, float * out, void * ws, size_t ws_bytes, hi
             return rc;
         }
     }
-    if (D == 128) {
+    if (fa_dma_ok(a, D)) {
+        const int nqt = (a.nq + 255) / 256;
+        hipLaunchKernelGGL(k_fa_dma, dim3((unsigned) (nqt * a.Hq * a.B)), dim3(512), 0, stream, a, nqt, out);
+    } else if (D == 128) {
         NW == 8 ? launch_fa_mfma<128, 8>(a, row_end, zero_end, n_qtiles, out, stream)
                 : launch_fa_mfma<128, 4>(a, row_end, zero_end, n_qtiles, out, stream);
     } else if (D == 64) {

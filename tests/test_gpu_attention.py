@@ -229,6 +229,40 @@ def test_mfma_odd_shapes_no_mask(mm, orc, B, Bk, Hq, Hkv, nq, nkv, D):
     check(out, orc.flash_attn_ext(q, k, v, None, s, "f64"))
 
 
+@pytest.mark.parametrize("B,Bk,Hq,Hkv,nq,nkv", [(1, 1, 64, 8, 1000, 333), (2, 1, 32, 32, 1100, 97),
+                                              (1, 1, 64, 64, 1024, 1)])
+def test_dma_kernel_shapes(mm, orc, B, Bk, Hq, Hkv, nq, nkv):
+    """Unmasked D = 128 on at least 256 workgroups of 256 query rows, the
+    shapes that take the DMA-fed kernel: GQA, a broadcast K/V batch, a partial
+    last query tile, partial 32-key units and 64-key tiles, a single key."""
+    q = rnd((B, Hq, nq, 128), 81)
+    k = rnd((Bk, Hkv, nkv, 128), 82, np.float16)
+    v = rnd((Bk, Hkv, nkv, 128), 83, np.float16)
+    s = float(np.float32(1 / np.sqrt(128)))
+    out = mm.flash_attn_ext(torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                            None, s).cpu().numpy()
+    check(out, orc.flash_attn_ext(q, k, v, None, s, "f64"))
+
+
+def test_dma_kernel_running_max_moves(mm, orc):
+    """K rows grow with the key index (x0.25 at the first key to x3.25 at the
+    last), so the row max keeps rising along the sequence and the running max
+    is moved (O and l rescaled) many times.  48 sampled rows against fp64."""
+    B, S, H, D = 2, 2048, 16, 128
+    q = rnd((B, H, S, D), 91)
+    grow = (0.25 + 3.0 * np.arange(S) / S).astype(np.float32)[None, None, :, None]
+    k = (rnd((B, H, S, D), 92) * grow).astype(np.float16)
+    v = rnd((B, H, S, D), 93, np.float16)
+    s = float(np.float32(1 / np.sqrt(D)))
+    out = mm.flash_attn_ext(torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                            None, s).cpu().numpy()
+    rows = np.array([0, 1, 255, 256, 1023, 2046, 2047] + list(np.random.default_rng(9).choice(S, 41, replace=False)))
+    ref = oracle_rows(orc, q, k, v, None, s, rows)
+    assert np.isfinite(out).all()
+    # a sharp softmax: Q's f16 rounding dominates, as in the decode sharp case
+    assert np.abs(out[:, rows] - ref).max() < 5e-3 and cosine(out[:, rows], ref) > 0.9999
+
+
 @pytest.mark.parametrize("wt", [8, 14])
 def test_decode_with_quantised_output(mm, orc, wt):
     """mmhip_flash_attn_ext_q (the attention feeding the output projection,
