@@ -97,6 +97,44 @@ int    mmhip_mul_mat_bias_add(int type, const void * W, int64_t N, int64_t K, in
 int    mmhip_mul_mat_bias_add_h(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const void * xh,
                                 int64_t M, const float * bias, const float * r, int64_t ldr, float * y, int64_t ldy,
                                 void * stream);
+/* The same with a workspace (mmhip_mul_mat_h_workspace bytes, 16-byte
+ * aligned; 0 for shapes that do not need one): a product with few output
+ * tiles and a long K (the DiT's ff_out, src/dit.h:243-246: 2048 rows, K =
+ * 8192) then splits K into parts whose partial sums are added in order before
+ * the ADDs (each ADD rounded as its op). */
+size_t mmhip_mul_mat_h_workspace(int type, int64_t N, int64_t K, int64_t M);
+int    mmhip_mul_mat_bias_add_hw(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const void * xh,
+                                 int64_t M, const float * bias, const float * r, int64_t ldr, float * y, int64_t ldy,
+                                 void * ws, size_t ws_bytes, void * stream);
+/* The DiT feed-forward input (src/dit.h:236-242): ff = MUL_MAT(W, x) + bias
+ * over N = 2F weight rows, value = ff rows [0, F), gate = ff rows [F, 2F)
+ * (swapped: the other way round), act = swiglu_split(gate, value) =
+ * silu(gate) * value, with the GGML_OP_ADD, the two CONTs and the GGML_OP_GLU
+ * in the GEMM's epilogue: ff is never written.  act [M, F] goes to h (f32)
+ * and / or hh (f16, rounded as mmhip_mul_mat_bias_add_h's activation copy);
+ * bias may be NULL.  Values equal those of the separate ops bit for bit.
+ * mmhip_mul_mat_bias_swiglu takes f32 activations and a workspace
+ * (mmhip_mul_mat_workspace of the N x K x M product); the _h form takes
+ * them in f16. */
+int    mmhip_mul_mat_bias_swiglu(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const float * x,
+                                 int64_t ldx, int64_t M, const float * bias, int swapped, float * h, void * hh,
+                                 void * ws, size_t ws_bytes, void * stream);
+int    mmhip_mul_mat_bias_swiglu_h(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const void * xh,
+                                   int64_t M, const float * bias, int swapped, float * h, void * hh, void * stream);
+/* Several MUL_MATs of one activation tensor in one launch: the DiT's
+ * q / k / v projections of the same LayerNorm output (src/dit.h:197-199).
+ * n (1..3) weight matrices W[i] of N rows x K (same type and row stride),
+ * y[i][m*ldy[i] + r] = MUL_MAT(W[i], x)[m, r] (+ bias[i][r] when bias and
+ * bias[i] are given), each equal bit for bit to mmhip_mul_mat_bias_add on
+ * W[i].  N a multiple of 256.  mmhip_mul_mat_multi takes f32 activations and
+ * a workspace (mmhip_mul_mat_workspace of one N x K x M product); the _h form
+ * takes them in f16 (as mmhip_mul_mat_bias_add_h). */
+int    mmhip_mul_mat_multi(int type, int n, const void * const * W, int64_t N, int64_t K, int64_t w_row_stride,
+                           const float * x, int64_t ldx, int64_t M, const float * const * bias, float * const * y,
+                           const int64_t * ldy, void * ws, size_t ws_bytes, void * stream);
+int    mmhip_mul_mat_multi_h(int type, int n, const void * const * W, int64_t N, int64_t K, int64_t w_row_stride,
+                             const void * xh, int64_t M, const float * const * bias, float * const * y,
+                             const int64_t * ldy, void * stream);
 
 /* The two halves of the GEMV path, exposed for fusion and for testing:
  * quantise M activation rows into the layout mmhip_mul_mat_q consumes

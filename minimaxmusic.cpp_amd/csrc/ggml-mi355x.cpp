@@ -939,7 +939,9 @@ struct plan_step {
     int                  norm    = -1;   // MM: the RMS_NORM node whose norm runs in the GEMV's prologue
     int                  norm_mul = -1;  // MM: the MUL by the norm weight (the GEMV's src1)
     int                  glu      = -1;  // MM: the SWIGLU node whose SwiGLU runs in the GEMV's prologue
-    int                  glu_epi  = -1;  // MM: the SWIGLU node computed in the (gate_up) GEMV's epilogue
+    int                  glu_epi  = -1;  // MM / GEMM: the SWIGLU node computed in the GEMV's / GEMM's epilogue
+    int                  glu_swapped = 0;  // GEMM: the gate rows are the first half
+    int                  multi[2]    = { -1, -1 };  // GEMM: further MUL_MATs of the same activations in this launch
     int                  mm       = -1;  // GEMM: the MUL_MAT node
     int                  bias     = -1;  // GEMM: the bias ADD node / LN: the ADD of the LayerNorm bias
     int                  bias_src = -1;  // index 0/1 of that ADD's vector operand
@@ -1456,6 +1458,77 @@ graph_plan build_plan(struct ggml_cgraph * g) {
                 continue;
             }
         }
+        // SWIGLU over the two halves of a bias GEMM's output (the DiT's ff_in,
+        // src/dit.h:236-242): the CONTs of the halves and the SWIGLU run in the
+        // GEMM's epilogue, the product itself is never written; when only GEMMs
+        // read the SwiGLU rows they go out in f16 (their activation format)
+        if (n->op == GGML_OP_GLU && n->op_params[0] == GGML_GLU_OP_SWIGLU && n->src[1] && rows_contiguous_f32(n) &&
+            !no_glu_epi) {
+            const int64_t              F    = n->ne[0];
+            const struct ggml_tensor * view[2] = { nullptr, nullptr };  // gate, value
+            int                        cont[2] = { -1, -1 };
+            bool                       ok      = true;
+            for (int k = 0; k < 2 && ok; k++) {
+                const struct ggml_tensor * c  = n->src[k];
+                const int                  ci = node_index(gi, c);
+                ok = ci >= 0 && c->op == GGML_OP_CONT && gi.uses[(size_t) ci] == 1 && !is_output(c) &&
+                     c->type == GGML_TYPE_F32 && ggml_are_same_shape(c, n);
+                if (ok) {
+                    const struct ggml_tensor * v  = c->src[0];
+                    const int                  vi = node_index(gi, v);
+                    ok = v->op == GGML_OP_VIEW && v->view_src && v->type == GGML_TYPE_F32 && v->nb[0] == 4 &&
+                         ggml_are_same_shape(v, n) && (vi < 0 || (gi.uses[(size_t) vi] == 1 && !is_output(v)));
+                    view[k] = v;
+                    cont[k] = ci;
+                }
+            }
+            const struct ggml_tensor * ff = ok ? view[0]->view_src : nullptr;
+            const int                  fi = ff ? node_index(gi, ff) : -1;
+            ok = ok && ff == view[1]->view_src && fi >= 0 && fi < i && step_at[(size_t) fi] >= 0 && !is_output(ff) &&
+                 ff->type == GGML_TYPE_F32 && ggml_is_contiguous(ff) && ff->ne[0] == 2 * F &&
+                 ggml_nrows(ff) == ggml_nrows(n) && view[0]->nb[1] == ff->nb[1] && view[1]->nb[1] == ff->nb[1] &&
+                 view[0]->nb[2] == ff->nb[2] && view[1]->nb[2] == ff->nb[2] && view[0]->nb[3] == ff->nb[3] &&
+                 view[1]->nb[3] == ff->nb[3] && gi.consumers[(size_t) fi].size() == 2;
+            int swapped = 0;
+            if (ok) {
+                const size_t hb = (size_t) F * sizeof(float);
+                ok = (view[0]->view_offs == hb && view[1]->view_offs == 0) ||
+                     (view[0]->view_offs == 0 && view[1]->view_offs == hb);
+                swapped = view[0]->view_offs == 0 ? 1 : 0;  // gate rows first
+            }
+            if (ok) {
+                plan_step & gs = pending[(size_t) step_at[(size_t) fi]];
+                ok = gs.kind == ST_GEMM && gs.node == fi && gs.add < 0 && gs.glu_epi < 0 &&
+                     quiet_between(fi, i, cont[0], cont[1]);
+                if (ok) {
+                    const struct ggml_tensor * mmn = ggml_graph_node(g, gs.mm);
+                    const struct ggml_tensor * x   = mmn->src[1];
+                    const struct ggml_tensor * w   = mmn->src[0];
+                    ok = w->ne[1] == 2 * F && !overlaps(n, w) && (gs.slot_in >= 0 || !overlaps(n, x)) &&
+                         (gs.bias < 0 || !overlaps(n, ggml_graph_node(g, gs.bias)->src[gs.bias_src]));
+                }
+                if (ok) {
+                    bool only_gemm = !is_output(n) && !gi.consumers[(size_t) i].empty() && F % 64 == 0;
+                    for (int c : gi.consumers[(size_t) i]) {
+                        const struct ggml_tensor * mm = ggml_graph_node(g, c);
+                        only_gemm = only_gemm && mm->op == GGML_OP_MUL_MAT && mm->src[1] == n && mm->src[0] != n &&
+                                    !mm_is_gemv(mm) && supports_mul_mat(mm) && ggml_is_contiguous(mm);
+                    }
+                    gs.glu_epi     = i;
+                    gs.glu_swapped = swapped;
+                    gs.write_f32   = !only_gemm;
+                    if (only_gemm) {
+                        gs.slot_out = (int64_t) plan.slot_bytes;
+                        plan.slot_bytes += ((size_t) ggml_nelements(n) * 2 + 255) / 256 * 256;
+                        f16_slot_of[(size_t) i] = gs.slot_out;
+                    }
+                    absorbed[(size_t) cont[0]] = 1;
+                    absorbed[(size_t) cont[1]] = 1;
+                    absorbed[(size_t) i]       = 1;
+                    continue;
+                }
+            }
+        }
         // SWIGLU reading its gate / value straight from the views the CONTs
         // before it copy (the DiT's value / gate halves of ff_in, src/dit.h:
         // 239-242): the CONTs are not run
@@ -1570,7 +1643,41 @@ graph_plan build_plan(struct ggml_cgraph * g) {
                     }
                 }
             }
-            if (cur != i || st.slot_in >= 0) {
+            if (cur == i) {
+                // more MUL_MATs of the same activations with the same weight shape
+                // (the DiT's q / k / v, src/dit.h:197-199) join this launch; their
+                // outputs are written here, ahead of their own position
+                int nm = 0;
+                for (int j = i + 1; j < gi.nn && nm < 2; j++) {
+                    const struct ggml_tensor * o = ggml_graph_node(g, j);
+                    if (o->op != GGML_OP_MUL_MAT || o->src[1] != n->src[1] || absorbed[(size_t) j] ||
+                        o->src[0]->type != n->src[0]->type || o->src[0]->ne[0] != n->src[0]->ne[0] ||
+                        o->src[0]->ne[1] != n->src[0]->ne[1] || o->src[0]->nb[1] != n->src[0]->nb[1] ||
+                        !ggml_is_contiguous(o) || !ggml_are_same_shape(o, n) || n->src[0]->ne[1] % 256 != 0) {
+                        continue;
+                    }
+                    // o is written early: its memory must hold no other tensor of
+                    // the graph (a buffer the allocator shares with anything else,
+                    // live before j or not, keeps the launches separate)
+                    auto own = [&](const struct ggml_tensor * v) { return v == o || v->view_src == o; };
+                    bool clear = !overlaps(o, n->src[0]) && !overlaps(o, o->src[0]);
+                    for (int t = 0; t < gi.nn && clear; t++) {
+                        const struct ggml_tensor * u = ggml_graph_node(g, t);
+                        clear = own(u) || !overlaps(o, u);
+                        for (int q = 0; q < GGML_MAX_SRC && clear; q++) {
+                            clear = !u->src[q] || own(u->src[q]) || !overlaps(o, u->src[q]);
+                        }
+                    }
+                    if (!clear) {
+                        continue;
+                    }
+                    st.multi[nm++] = j;
+                }
+                for (int k = 0; k < nm; k++) {
+                    absorbed[(size_t) st.multi[k]] = 1;
+                }
+            }
+            if (cur != i || st.slot_in >= 0 || st.multi[0] >= 0) {
                 st.node = cur;
                 absorbed[(size_t) i] = 1;
                 if (st.bias >= 0) {
@@ -1800,10 +1907,66 @@ int run_step(mi_backend * c, struct ggml_cgraph * g, const plan_step & st, char 
             const float *              bias = st.bias >= 0 ? (const float *) ggml_graph_node(g, st.bias)->src[st.bias_src]->data
                                                            : nullptr;
             const struct ggml_tensor * r  = st.add >= 0 ? ggml_graph_node(g, st.add)->src[st.add_res] : nullptr;
+            if (st.multi[0] >= 0) {
+                // this MUL_MAT and up to two more of the same activations in one launch
+                const void * wm[3];
+                float *      ym[3];
+                int64_t      lm[3];
+                int          nmat = 0;
+                for (int k = -1; k < 2; k++) {
+                    const int                  ni = k < 0 ? st.mm : st.multi[k];
+                    const struct ggml_tensor * o  = ni >= 0 ? ggml_graph_node(g, ni) : nullptr;
+                    if (!o) {
+                        continue;
+                    }
+                    wm[nmat] = o->src[0]->data;
+                    ym[nmat] = (float *) o->data;
+                    lm[nmat] = (int64_t) (o->nb[1] / sizeof(float));
+                    nmat++;
+                }
+                if (st.slot_in >= 0) {
+                    rc = mmhip_mul_mat_multi_h(w->type, nmat, wm, N, K, (int64_t) w->nb[1], slot + st.slot_in, M,
+                                               nullptr, ym, lm, s);
+                    break;
+                }
+                const size_t ws = mmhip_mul_mat_workspace(w->type, N, K, M);
+                void *       wp = ws ? workspace(c, ws) : nullptr;
+                if (ws && !wp) {
+                    return -1;
+                }
+                rc = mmhip_mul_mat_multi(w->type, nmat, wm, N, K, (int64_t) w->nb[1], (const float *) x->data,
+                                         (int64_t) (x->nb[1] / sizeof(float)), M, nullptr, ym, lm, wp, ws, s);
+                break;
+            }
+            if (st.glu_epi >= 0) {
+                // the SwiGLU of the two output halves in the epilogue
+                float * h  = st.write_f32 ? (float *) ggml_graph_node(g, st.glu_epi)->data : nullptr;
+                void *  hh = st.slot_out >= 0 ? (void *) (slot + st.slot_out) : nullptr;
+                if (st.slot_in >= 0) {
+                    rc = mmhip_mul_mat_bias_swiglu_h(w->type, w->data, N, K, (int64_t) w->nb[1], slot + st.slot_in, M,
+                                                     bias, st.glu_swapped, h, hh, s);
+                    break;
+                }
+                const size_t ws = mmhip_mul_mat_workspace(w->type, N, K, M);
+                void *       wp = ws ? workspace(c, ws) : nullptr;
+                if (ws && !wp) {
+                    return -1;
+                }
+                rc = mmhip_mul_mat_bias_swiglu(w->type, w->data, N, K, (int64_t) w->nb[1], (const float *) x->data,
+                                               (int64_t) (x->nb[1] / sizeof(float)), M, bias, st.glu_swapped, h, hh,
+                                               wp, ws, s);
+                break;
+            }
             if (st.slot_in >= 0) {
-                rc = mmhip_mul_mat_bias_add_h(w->type, w->data, N, K, (int64_t) w->nb[1], slot + st.slot_in, M, bias,
-                                              r ? (const float *) r->data : nullptr,
-                                              r ? (int64_t) (r->nb[1] / sizeof(float)) : 0, (float *) n->data, N, s);
+                const size_t hws = mmhip_mul_mat_h_workspace(w->type, N, K, M);  // split-K partial sums
+                void *       hwp = hws ? workspace(c, hws) : nullptr;
+                if (hws && !hwp) {
+                    return -1;
+                }
+                rc = mmhip_mul_mat_bias_add_hw(w->type, w->data, N, K, (int64_t) w->nb[1], slot + st.slot_in, M, bias,
+                                               r ? (const float *) r->data : nullptr,
+                                               r ? (int64_t) (r->nb[1] / sizeof(float)) : 0, (float *) n->data, N, hwp,
+                                               hws, s);
                 break;
             }
             const size_t               ws = mmhip_mul_mat_workspace(w->type, N, K, M);

@@ -183,12 +183,21 @@ __device__ __forceinline__ int swz(int r, int c) {
 // into one of two LDS weight buffers.  The next step's DMA and weight loads
 // are issued before the current step's MFMAs, so one step of MFMA work hides
 // their latency; one barrier per step.
-template <int WT, int NW, int WM, int BK, int BM>
+//
+// GLU: the N = 2 F weight rows are the value and gate halves of a SwiGLU
+// (swiglu_split(gate, value) over the two halves of the product, with the
+// bias ADD before it).  A tile then covers BT / 2 SwiGLU columns j: in each
+// wave's 64 rows, block 0 holds value rows and block 1 the gate rows of the
+// same 32 columns, so the accumulators of a (value, gate) pair sit in the
+// same lane and register.  The epilogue adds both biases, forms
+// silu(g) * v with k_swiglu's arithmetic and stores the SwiGLU rows [M, F]
+// in f32 and / or f16 (the next GEMM's activation format).
+template <int WT, int NW, int WM, int BK, int BM, bool GLU>
 __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__ W, int64_t N, int64_t K, int64_t rs,
                                                      const _Float16 * __restrict__ xh, int64_t M,
                                                      const float * __restrict__ bias, const float * res, int64_t ldr,
-                                                     float * y, int64_t ldy,
-                                                     int64_t n_ntiles, int64_t n_tiles) {
+                                                     float * y, int64_t ldy, GemmGlu glu, GemmMulti mul,
+                                                     GemmSplit spl, int64_t n_ntiles, int64_t n_tiles) {
 #pragma clang fp contract(off)
     constexpr int BT  = 32 * NW;       // weight rows per tile (thread t stages row t / 2)
     constexpr int T   = NW * 64;
@@ -201,6 +210,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
     constexpr int TIX = BM * BK;       // halves per activation tile
     constexpr int TIL = BT * BK;       // halves per weight tile
     static_assert(MB >= 1 && XI >= 1, "tile shape");
+    static_assert(!GLU || NB == 2, "GLU tiles pair one value and one gate block per wave");
     extern __shared__ __attribute__((aligned(16))) _Float16 g_lds[];
     _Float16 * sX = g_lds;            // 2 stages
     _Float16 * sW = g_lds + 2 * TIX;  // 2 buffers
@@ -208,11 +218,25 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
     // consecutive work items (one XCD, one L2) share the operand that is
     // re-read most: the weight tile when there are more weight tiles than
     // token tiles (m_fast), else the activation tile
-    const int64_t work    = gm_xcd_remap(blockIdx.x, n_tiles);
-    const int64_t n_mt    = n_tiles / n_ntiles;
+    // split-K: work items (part, tile), the parts of one tile n_base apart
+    const int64_t n_base  = n_tiles / spl.n;
+    const int64_t lin     = gm_xcd_remap(blockIdx.x, n_tiles);
+    const int     kpart   = (int) (lin / n_base);
+    const int64_t work    = lin % n_base;
+    const int64_t n_mt    = n_base / n_ntiles;
     const bool    m_fast  = n_ntiles > n_mt;
     const int64_t m0      = (m_fast ? work % n_mt : work / n_ntiles) * BM;
-    const int64_t n0      = (m_fast ? work / n_mt : work % n_ntiles) * BT;
+    int64_t       n0      = (m_fast ? work / n_mt : work % n_ntiles) * BT;
+    if (mul.n > 0) {
+        // several weight matrices: this tile's rows come from matrix n0 / Nper
+        const int mi = (int) (n0 / mul.Nper);
+        n0 -= mi * mul.Nper;
+        W    = mul.W[mi];
+        y    = mul.y[mi];
+        ldy  = mul.ldy[mi];
+        bias = mul.bias[mi];
+        N    = mul.Nper;
+    }
     const int     tid  = threadIdx.x;
     const int     wave = tid >> 6;
     const int     lane = tid & 63;
@@ -240,8 +264,19 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
 
     const int       srow  = tid >> 1;
     const int       shalf = tid & 1;
-    const bool      w_ok  = n0 + srow < N;
-    const uint8_t * wrow  = W + (w_ok ? n0 + srow : 0) * rs;
+    bool            w_ok;
+    int64_t         wsel;  // weight row staged by this thread
+    if constexpr (GLU) {
+        // local row (wave block, value / gate, 32-row offset) -> SwiGLU column j
+        const int     wq = srow / (BT / WN), blk = (srow % (BT / WN)) / 32;
+        const int64_t j  = n0 / 2 + wq * 32 + (srow % 32);
+        w_ok             = j < glu.F;
+        wsel             = (blk == 1) != (glu.swapped != 0) ? glu.F + j : j;
+    } else {
+        w_ok = n0 + srow < N;
+        wsel = n0 + srow;
+    }
+    const uint8_t * wrow = W + (w_ok ? wsel : 0) * rs;
     WRaw            wr[SUB];
     auto            wload = [&](int k0) {
 #pragma unroll
@@ -297,29 +332,85 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
         }
     };
 
-    const int nk = (int) (K / BK);
-    dma(0, 0);
-    wload(0);
-    wstore(0, 0);
+    const int nk = (int) (K / BK / spl.n);  // K steps of this part
+    const int kb = kpart * nk * BK;         // its first column
+    dma(0, kb);
+    wload(kb);
+    wstore(0, kb);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     for (int ks = 0; ks < nk; ks++) {
         const int nxt = (ks + 1) & 1;
         if (ks + 1 < nk) {
-            dma(nxt, (ks + 1) * BK);
+            dma(nxt, kb + (ks + 1) * BK);
             __builtin_amdgcn_sched_barrier(0);
-            wload((ks + 1) * BK);
+            wload(kb + (ks + 1) * BK);
             __builtin_amdgcn_sched_barrier(0);
         }
         compute(ks & 1);
         if (ks + 1 < nk) {
-            wstore(nxt, (ks + 1) * BK);
+            wstore(nxt, kb + (ks + 1) * BK);
         }
         __builtin_amdgcn_s_waitcnt(0);  // this thread's DMA and LDS writes
         __syncthreads();
     }
 
     // C[i = token][j = weight row]: lane holds row j = lq, tokens 8(r/4) + 4hh + r%4.
+    if constexpr (GLU) {
+        const int64_t j = n0 / 2 + wn * 32 + lq;
+        if (j >= glu.F) {
+            return;
+        }
+        const int64_t rv = glu.swapped ? glu.F + j : j;  // value row
+        const int64_t rg = glu.swapped ? j : glu.F + j;  // gate row
+        const float   bv = bias ? bias[rv] : 0.0f;
+        const float   bg = bias ? bias[rg] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < MB; i++) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int64_t m = m0 + wm * (BM / WM) + i * 32 + 8 * (r / 4) + 4 * hh + (r % 4);
+                if (m < M) {
+                    float v = acc[i][0][r], g = acc[i][1][r];
+                    if (bias) {
+                        v = v + bv;
+                        g = g + bg;
+                    }
+                    const float silu = g / (1.0f + expf(-g));
+                    const float o    = silu * v;
+                    if (glu.h) {
+                        glu.h[m * glu.F + j] = o;
+                    }
+                    if (glu.hh) {
+                        glu.hh[m * glu.F + j] = (_Float16) o;
+                    }
+                }
+            }
+        }
+        return;
+    }
+    if (spl.n > 1) {
+        // partial sums of this K part; the reduce kernel adds the ADDs
+        float * pp = spl.part + (int64_t) kpart * M * N;
+#pragma unroll
+        for (int i = 0; i < MB; i++) {
+#pragma unroll
+            for (int j = 0; j < NB; j++) {
+                const int64_t n = n0 + wn * (BT / WN) + j * 32 + lq;
+                if (n >= N) {
+                    continue;
+                }
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int64_t m = m0 + wm * (BM / WM) + i * 32 + 8 * (r / 4) + 4 * hh + (r % 4);
+                    if (m < M) {
+                        pp[m * N + n] = acc[i][j][r];
+                    }
+                }
+            }
+        }
+        return;
+    }
     // Epilogue: the bias ADD, then the residual ADD, each rounded as its op.
 #pragma unroll
     for (int i = 0; i < MB; i++) {
@@ -344,6 +435,36 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
                     y[m * ldy + n] = v;
                 }
             }
+        }
+    }
+}
+
+// Split-K reduction: y[m, n] = ((part_0 + part_1 + ...) + bias[n]) + res[m, n],
+// the parts summed in order, each ADD rounded as its op; 4 columns per thread.
+__global__ void k_splitk_reduce(const float * __restrict__ part, int nparts, int64_t M, int64_t N,
+                                const float * __restrict__ bias, const float * res, int64_t ldr, float * y,
+                                int64_t ldy) {
+#pragma clang fp contract(off)
+    const int64_t n4 = N / 4;
+    for (int64_t t = blockIdx.x * (int64_t) blockDim.x + threadIdx.x; t < M * n4; t += (int64_t) gridDim.x * blockDim.x) {
+        const int64_t m = t / n4, n = (t % n4) * 4;
+        float4_t      v = *(const float4_t *) (part + m * N + n);
+        for (int p = 1; p < nparts; p++) {
+            const float4_t w = *(const float4_t *) (part + ((int64_t) p * M + m) * N + n);
+            v[0]             = v[0] + w[0];
+            v[1]             = v[1] + w[1];
+            v[2]             = v[2] + w[2];
+            v[3]             = v[3] + w[3];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            if (bias) {
+                v[k] = v[k] + bias[n + k];
+            }
+            if (res) {
+                v[k] = res[m * ldr + n + k] + v[k];
+            }
+            y[m * ldy + n + k] = v[k];
         }
     }
 }
@@ -384,11 +505,12 @@ size_t gemm_workspace(int64_t K, int64_t M) {
 
 template <int NW, int WM, int BK, int BM = 32 * NW>
 static int launch_gemm(int wtype, const uint8_t * W, int64_t N, int64_t K, int64_t rs, const _Float16 * xh, int64_t M,
-                       const float * bias, const float * res, int64_t ldr, float * y, int64_t ldy, hipStream_t stream) {
+                       const float * bias, const float * res, int64_t ldr, float * y, int64_t ldy, const GemmGlu & glu,
+                       const GemmMulti & mul, const GemmSplit & spl, hipStream_t stream) {
     constexpr int BT   = 32 * NW;
     const int64_t n_nt = (N + BT - 1) / BT;
     const int64_t n_mt = (M + BM - 1) / BM;
-    const int64_t n    = n_nt * n_mt;
+    const int64_t n    = n_nt * n_mt * spl.n;
     if (n > 0x7fffffff) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat gemm: too many tiles");
     }
@@ -398,42 +520,95 @@ static int launch_gemm(int wtype, const uint8_t * W, int64_t N, int64_t K, int64
             return set_error(MMHIP_ERR_HIP, "mul_mat gemm: cannot raise LDS limit to %zu", lds);
         }
         hipLaunchKernelGGL(kern, dim3((unsigned) n), dim3(NW * 64), lds, stream, W, N, K, rs, xh, M, bias, res, ldr, y,
-                           ldy, n_nt, n);
+                           ldy, glu, mul, spl, n_nt, n);
         return check_launch("mul_mat gemm");
     };
+    if (glu.F > 0) {
+        switch (wtype) {
+            case TYPE_Q8_0: return go(k_gemm_q<TYPE_Q8_0, NW, WM, BK, BM, true>);
+            case TYPE_Q4_K: return go(k_gemm_q<TYPE_Q4_K, NW, WM, BK, BM, true>);
+            default: return go(k_gemm_q<TYPE_Q6_K, NW, WM, BK, BM, true>);
+        }
+    }
     switch (wtype) {
-        case TYPE_Q8_0: return go(k_gemm_q<TYPE_Q8_0, NW, WM, BK, BM>);
-        case TYPE_Q4_K: return go(k_gemm_q<TYPE_Q4_K, NW, WM, BK, BM>);
-        default: return go(k_gemm_q<TYPE_Q6_K, NW, WM, BK, BM>);
+        case TYPE_Q8_0: return go(k_gemm_q<TYPE_Q8_0, NW, WM, BK, BM, false>);
+        case TYPE_Q4_K: return go(k_gemm_q<TYPE_Q4_K, NW, WM, BK, BM, false>);
+        default: return go(k_gemm_q<TYPE_Q6_K, NW, WM, BK, BM, false>);
     }
 }
 
 // Tile configuration by shape (activations already f16, rows of K).
 static int gemm_launch(int wtype, const uint8_t * wb, int64_t N, int64_t K, int64_t rs, const _Float16 * xh, int64_t M,
-                       const float * bias, const float * res, int64_t ldr, float * y, int64_t ldy, hipStream_t stream) {
+                       const float * bias, const float * res, int64_t ldr, float * y, int64_t ldy, const GemmGlu & glu,
+                       const GemmMulti & mul, const GemmSplit & spl, hipStream_t stream) {
     const int64_t tiles256 = ((N + 255) / 256) * ((M + 255) / 256);
-    if (tiles256 >= 256) {
-        return launch_gemm<8, 2, 64>(wtype, wb, N, K, rs, xh, M, bias, res, ldr, y, ldy, stream);
+    if (spl.n > 1) {
+        // 256 x 256 tiles over K parts, then the ordered reduction with the ADDs
+        const GemmSplit sp = spl;
+        int rc = launch_gemm<8, 2, 64>(wtype, wb, N, K, rs, xh, M, nullptr, nullptr, 0, nullptr, N, glu, mul, sp, stream);
+        if (rc != MMHIP_OK) {
+            return rc;
+        }
+        const int64_t nt = M * (N / 4);
+        const int64_t nb = (nt + 255) / 256;
+        hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned) (nb < 16384 ? nb : 16384)), dim3(256), 0, stream,
+                           (const float *) spl.part, spl.n, M, N, bias, res, ldr, y, ldy);
+        return check_launch("mul_mat gemm: split-K reduce");
+    }
+    // several weight matrices in one launch: 256 x 256 tiles once they fill
+    // half the CUs (the DiT's q / k / v: 144 tiles), where three launches of
+    // small tiles ran at half the MFMA rate
+    if (tiles256 >= 256 || (mul.n > 0 && tiles256 >= 128)) {
+        return launch_gemm<8, 2, 64>(wtype, wb, N, K, rs, xh, M, bias, res, ldr, y, ldy, glu, mul, spl, stream);
     }
     // small grids (the DiT's 2048-row projections at 1380 tokens: 176 tiles of
     // 128 x 128): 64-token x 128-row tiles, twice the workgroups, three per CU
     // in LDS (a 128-wide K step on 128 x 128 tiles: 2.6 % slower per DiT block;
     // 32 x 128 and 128 x 256 tiles: 1 % and 25 % slower)
-    return launch_gemm<4, 2, 64, 64>(wtype, wb, N, K, rs, xh, M, bias, res, ldr, y, ldy, stream);
+    return launch_gemm<4, 2, 64, 64>(wtype, wb, N, K, rs, xh, M, bias, res, ldr, y, ldy, glu, mul, spl, stream);
+}
+
+// K parts for a shape: few 256 x 256 tiles (under half the CUs) and a long
+// K (the DiT's ff_out: 48 tiles, K = 8192) split K four ways.
+int gemm_split(int64_t N, int64_t K, int64_t M) {
+    const int64_t tiles256 = ((N + 255) / 256) * ((M + 255) / 256);
+    return tiles256 < 128 && K >= 4096 && K % (4 * GM_BK) == 0 && N % 4 == 0 ? 4 : 1;
+}
+
+size_t gemm_split_bytes(int64_t N, int64_t K, int64_t M) {
+    const int s = gemm_split(N, K, M);
+    return s > 1 ? (size_t) s * (size_t) M * (size_t) N * sizeof(float) : 0;
 }
 
 int gemm_q_h(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const void * xh, int64_t M, float * y,
-             int64_t ldy, hipStream_t stream, const float * bias, const float * res, int64_t ldr) {
+             int64_t ldy, hipStream_t stream, const float * bias, const float * res, int64_t ldr, const GemmGlu * glu,
+             const GemmMulti * mul, void * split_ws, size_t split_ws_bytes) {
     if (!gemm_supported(wtype, N, K, rs, W, (const float *) xh, K) || ((uintptr_t) xh) % 16 != 0) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat gemm (f16 activations): type %d N=%lld K=%lld rs=%lld not supported",
                          wtype, (long long) N, (long long) K, (long long) rs);
     }
-    return gemm_launch(wtype, (const uint8_t *) W, N, K, rs, (const _Float16 *) xh, M, bias, res, ldr, y, ldy, stream);
+    const GemmGlu   none{};
+    const GemmMulti single{};
+    GemmSplit       spl;
+    if (!glu && !mul && split_ws && split_ws_bytes >= gemm_split_bytes(N, K, M) && ((uintptr_t) split_ws) % 16 == 0) {
+        spl.n    = gemm_split(N, K, M);
+        spl.part = (float *) split_ws;
+    }
+    return gemm_launch(wtype, (const uint8_t *) W, N, K, rs, (const _Float16 *) xh, M, bias, res, ldr, y, ldy,
+                       glu ? *glu : none, mul ? *mul : single, spl, stream);
+}
+
+int convert_act_f16(const float * x, int64_t ldx, int64_t K, int64_t M, void * xh, hipStream_t stream) {
+    const int64_t n8 = M * K / 8;
+    const int64_t nb = (n8 + 255) / 256;
+    hipLaunchKernelGGL(k_x_to_f16, dim3((unsigned) (nb < 8192 ? nb : 8192)), dim3(256), 0, stream, x, ldx, K, n8,
+                       (_Float16 *) xh);
+    return check_launch("mul_mat gemm: convert");
 }
 
 int gemm_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const float * x, int64_t ldx, int64_t M,
            float * y, int64_t ldy, void * ws, size_t ws_bytes, hipStream_t stream, const float * bias,
-           const float * res, int64_t ldr) {
+           const float * res, int64_t ldr, const GemmGlu * glu) {
     if (!gemm_supported(wtype, N, K, rs, W, x, ldx)) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat gemm: type %d N=%lld K=%lld rs=%lld not supported", wtype,
                          (long long) N, (long long) K, (long long) rs);
@@ -450,7 +625,17 @@ int gemm_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const fl
     if (rc != MMHIP_OK) {
         return rc;
     }
-    return gemm_launch(wtype, (const uint8_t *) W, N, K, rs, xh, M, bias, res, ldr, y, ldy, stream);
+    const GemmGlu   none{};
+    const GemmMulti single{};
+    GemmSplit       spl;
+    const size_t    sb = gemm_split_bytes(N, K, M);
+    const size_t    xo = (need + 255) / 256 * 256;  // partial sums after the f16 copy
+    if (!glu && sb && ws_bytes >= xo + sb) {
+        spl.n    = gemm_split(N, K, M);
+        spl.part = (float *) ((char *) ws + xo);
+    }
+    return gemm_launch(wtype, (const uint8_t *) W, N, K, rs, xh, M, bias, res, ldr, y, ldy, glu ? *glu : none, single,
+                       spl, stream);
 }
 
 }  // namespace mmhip

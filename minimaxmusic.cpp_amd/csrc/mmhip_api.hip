@@ -74,11 +74,15 @@ extern "C" int mmhip_version(void) {
 }
 
 extern "C" size_t mmhip_mul_mat_workspace(int type, int64_t N, int64_t K, int64_t M) {
-    (void) N;
     if (use_gemm(type, M)) {
-        return gemm_workspace(K, M);
+        const size_t sb = gemm_split_bytes(N, K, M);  // split-K partial sums after the f16 copy
+        return sb ? (gemm_workspace(K, M) + 255) / 256 * 256 + sb : gemm_workspace(K, M);
     }
     return act_layout(type, K, M).total;
+}
+
+extern "C" size_t mmhip_mul_mat_h_workspace(int type, int64_t N, int64_t K, int64_t M) {
+    return is_repacked_type(type) && use_gemm(type, M) ? gemm_split_bytes(N, K, M) : 0;
 }
 
 extern "C" int mmhip_mul_mat(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const float * x,
@@ -142,6 +146,137 @@ extern "C" int mmhip_mul_mat_bias_add_h(int type, const void * W, int64_t N, int
                          (long long) M);
     }
     return gemm_q_h(type, W, N, K, w_row_stride, xh, M, y, ldy, (hipStream_t) stream, bias, r, ldr);
+}
+
+extern "C" int mmhip_mul_mat_bias_add_hw(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride,
+                                         const void * xh, int64_t M, const float * bias, const float * r, int64_t ldr,
+                                         float * y, int64_t ldy, void * ws, size_t ws_bytes, void * stream) {
+    MMHIP_API_BEGIN();
+    if (!W || !xh || !y || N <= 0 || K <= 0 || M <= 0 || ldy < N || (r && ldr < N)) {
+        return set_error(MMHIP_ERR_INVALID, "mul_mat_bias_add_hw: bad arguments N=%lld K=%lld M=%lld", (long long) N,
+                         (long long) K, (long long) M);
+    }
+    if (!is_repacked_type(type) || !use_gemm(type, M)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat_bias_add_hw: weight type %d at %lld tokens", type,
+                         (long long) M);
+    }
+    return gemm_q_h(type, W, N, K, w_row_stride, xh, M, y, ldy, (hipStream_t) stream, bias, r, ldr, nullptr, nullptr,
+                    ws, ws_bytes);
+}
+
+static int swiglu_gemm_args(const char * who, int type, const void * W, int64_t N, int64_t K, int64_t M,
+                            const float * h, const void * hh) {
+    if (!W || (!h && !hh) || N <= 0 || (N & 1) || K <= 0 || M <= 0 || ((uintptr_t) hh) % 2 != 0) {
+        return set_error(MMHIP_ERR_INVALID, "%s: bad arguments N=%lld K=%lld M=%lld", who, (long long) N,
+                         (long long) K, (long long) M);
+    }
+    if (!is_repacked_type(type) || !use_gemm(type, M)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "%s: weight type %d at %lld tokens", who, type, (long long) M);
+    }
+    return MMHIP_OK;
+}
+
+extern "C" int mmhip_mul_mat_bias_swiglu(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride,
+                                         const float * x, int64_t ldx, int64_t M, const float * bias, int swapped,
+                                         float * h, void * hh, void * ws, size_t ws_bytes, void * stream) {
+    MMHIP_API_BEGIN();
+    int rc = swiglu_gemm_args("mul_mat_bias_swiglu", type, W, N, K, M, h, hh);
+    if (rc != MMHIP_OK) {
+        return rc;
+    }
+    if (!x || ldx < K) {
+        return set_error(MMHIP_ERR_INVALID, "mul_mat_bias_swiglu: bad activations");
+    }
+    GemmGlu glu;
+    glu.F       = N / 2;
+    glu.swapped = swapped ? 1 : 0;
+    glu.h       = h;
+    glu.hh      = (_Float16 *) hh;
+    return gemm_q(type, W, N, K, w_row_stride, x, ldx, M, nullptr, N, ws, ws_bytes, (hipStream_t) stream, bias,
+                  nullptr, 0, &glu);
+}
+
+extern "C" int mmhip_mul_mat_bias_swiglu_h(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride,
+                                           const void * xh, int64_t M, const float * bias, int swapped, float * h,
+                                           void * hh, void * stream) {
+    MMHIP_API_BEGIN();
+    int rc = swiglu_gemm_args("mul_mat_bias_swiglu_h", type, W, N, K, M, h, hh);
+    if (rc != MMHIP_OK) {
+        return rc;
+    }
+    if (!xh) {
+        return set_error(MMHIP_ERR_INVALID, "mul_mat_bias_swiglu_h: null activations");
+    }
+    GemmGlu glu;
+    glu.F       = N / 2;
+    glu.swapped = swapped ? 1 : 0;
+    glu.h       = h;
+    glu.hh      = (_Float16 *) hh;
+    return gemm_q_h(type, W, N, K, w_row_stride, xh, M, nullptr, N, (hipStream_t) stream, bias, nullptr, 0, &glu);
+}
+
+static int multi_args(const char * who, int type, int n, const void * const * W, int64_t N, int64_t K,
+                      int64_t w_row_stride, int64_t M, const float * const * bias, float * const * y,
+                      const int64_t * ldy, GemmMulti & mul) {
+    if (n < 1 || n > 3 || !W || !y || !ldy || N <= 0 || N % 256 != 0 || K <= 0 || M <= 0) {
+        return set_error(MMHIP_ERR_INVALID, "%s: bad arguments n=%d N=%lld K=%lld M=%lld", who, n, (long long) N,
+                         (long long) K, (long long) M);
+    }
+    if (!is_repacked_type(type) || !use_gemm(type, M)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "%s: weight type %d at %lld tokens", who, type, (long long) M);
+    }
+    mul.n    = n;
+    mul.Nper = N;
+    for (int i = 0; i < n; i++) {
+        if (!W[i] || !y[i] || ldy[i] < N || ((uintptr_t) W[i]) % 16 != 0) {
+            return set_error(MMHIP_ERR_INVALID, "%s: matrix %d: null or unaligned operand", who, i);
+        }
+        mul.W[i]    = (const uint8_t *) W[i];
+        mul.y[i]    = y[i];
+        mul.ldy[i]  = ldy[i];
+        mul.bias[i] = bias ? bias[i] : nullptr;
+    }
+    return MMHIP_OK;
+}
+
+extern "C" int mmhip_mul_mat_multi(int type, int n, const void * const * W, int64_t N, int64_t K, int64_t w_row_stride,
+                                   const float * x, int64_t ldx, int64_t M, const float * const * bias,
+                                   float * const * y, const int64_t * ldy, void * ws, size_t ws_bytes, void * stream) {
+    MMHIP_API_BEGIN();
+    GemmMulti mul;
+    int       rc = multi_args("mul_mat_multi", type, n, W, N, K, w_row_stride, M, bias, y, ldy, mul);
+    if (rc != MMHIP_OK) {
+        return rc;
+    }
+    if (!x || ldx < K || !gemm_supported(type, N, K, w_row_stride, W[0], x, ldx)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat_multi: activations or weights not supported");
+    }
+    const size_t need = gemm_workspace(K, M);
+    if (!ws || ws_bytes < need || ((uintptr_t) ws) % 16 != 0) {
+        return set_error(MMHIP_ERR_WORKSPACE, "mul_mat_multi: workspace %zu < %zu (16-byte aligned)", ws_bytes, need);
+    }
+    rc = convert_act_f16(x, ldx, K, M, ws, (hipStream_t) stream);
+    if (rc != MMHIP_OK) {
+        return rc;
+    }
+    return gemm_q_h(type, W[0], (int64_t) n * N, K, w_row_stride, ws, M, y[0], ldy[0], (hipStream_t) stream, nullptr,
+                    nullptr, 0, nullptr, &mul);
+}
+
+extern "C" int mmhip_mul_mat_multi_h(int type, int n, const void * const * W, int64_t N, int64_t K,
+                                     int64_t w_row_stride, const void * xh, int64_t M, const float * const * bias,
+                                     float * const * y, const int64_t * ldy, void * stream) {
+    MMHIP_API_BEGIN();
+    GemmMulti mul;
+    int       rc = multi_args("mul_mat_multi_h", type, n, W, N, K, w_row_stride, M, bias, y, ldy, mul);
+    if (rc != MMHIP_OK) {
+        return rc;
+    }
+    if (!xh) {
+        return set_error(MMHIP_ERR_INVALID, "mul_mat_multi_h: null activations");
+    }
+    return gemm_q_h(type, W[0], (int64_t) n * N, K, w_row_stride, xh, M, y[0], ldy[0], (hipStream_t) stream, nullptr,
+                    nullptr, 0, nullptr, &mul);
 }
 
 // ---------------------------------------------------------------------

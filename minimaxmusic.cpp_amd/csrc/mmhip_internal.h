@@ -81,13 +81,53 @@ int  gemv_q(int wtype, const void * W, int64_t N, int64_t K, int64_t row_stride,
 // MFMA GEMM with in-LDS dequantisation (any M); the workspace holds the f16
 // copy of the activations (gemm_workspace bytes, 16-byte aligned).
 size_t gemm_workspace(int64_t K, int64_t M);
+// SwiGLU epilogue: the N = 2 F weight rows are the value (first half, second
+// if swapped) and gate halves; the GEMM then writes silu(gate + bias) *
+// (value + bias) rows [M, F] to h (f32) and / or hh (f16) instead of y.
+struct GemmGlu {
+    int64_t    F       = 0;  // 0: the plain epilogue
+    int        swapped = 0;
+    float *    h       = nullptr;
+    _Float16 * hh      = nullptr;
+};
+// Up to 3 weight matrices of Nper rows each (same type, K and activations)
+// in one launch: weight rows [i Nper, (i + 1) Nper) come from W[i], their
+// outputs go to y[i] (row stride ldy[i]) with bias[i]; Nper is a multiple of
+// the tile height, so no tile straddles two matrices.
+struct GemmMulti {
+    int             n    = 0;  // 0: the single matrix of the call
+    int64_t         Nper = 0;
+    const uint8_t * W[3]{};
+    float *         y[3]{};
+    int64_t         ldy[3]{};
+    const float *   bias[3]{};
+};
+// Split-K: the K range is cut into n parts, each tile-and-part writes its
+// f32 partial sums to part[(i M + m) N + n], and a reduce kernel sums the
+// parts in order, then adds the bias and the residual as the epilogue would.
+struct GemmSplit {
+    int     n    = 1;
+    float * part = nullptr;
+};
+// Parts the GEMM would split K into for this shape (1: no split), and the
+// bytes of partial sums that takes.
+int    gemm_split(int64_t N, int64_t K, int64_t M);
+size_t gemm_split_bytes(int64_t N, int64_t K, int64_t M);
 // The epilogue adds bias[n] (if given), then res[m * ldr + n] (if given).
 int    gemm_q(int wtype, const void * W, int64_t N, int64_t K, int64_t row_stride, const float * x, int64_t ldx,
               int64_t M, float * y, int64_t ldy, void * ws, size_t ws_bytes, hipStream_t stream,
-              const float * bias = nullptr, const float * res = nullptr, int64_t ldr = 0);
+              const float * bias = nullptr, const float * res = nullptr, int64_t ldr = 0,
+              const GemmGlu * glu = nullptr);
+// Shape / alignment the GEMM takes (16-byte weight rows and activations).
+bool   gemm_supported(int wtype, int64_t N, int64_t K, int64_t rs, const void * W, const float * x, int64_t ldx);
+// f32 activation rows -> the packed f16 copy the GEMM reads (K % 8 == 0).
+int    convert_act_f16(const float * x, int64_t ldx, int64_t K, int64_t M, void * xh, hipStream_t stream);
 // The same on activations already rounded to f16 (rows of K halves, 16-byte aligned).
+// With a workspace of gemm_split_bytes (else none) the plain form may split K.
 int    gemm_q_h(int wtype, const void * W, int64_t N, int64_t K, int64_t row_stride, const void * xh, int64_t M,
-                float * y, int64_t ldy, hipStream_t stream, const float * bias, const float * res, int64_t ldr);
+                float * y, int64_t ldy, hipStream_t stream, const float * bias, const float * res, int64_t ldr,
+                const GemmGlu * glu = nullptr, const GemmMulti * mul = nullptr, void * split_ws = nullptr,
+                size_t split_ws_bytes = 0);
 
 }  // namespace mmhip
 

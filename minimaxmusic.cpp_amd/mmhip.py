@@ -64,6 +64,14 @@ SIGNATURES = {
     "mmhip_mul_mat_bias_add": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _vp,
                                       _sz, _vp]),
     "mmhip_mul_mat_bias_add_h": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _vp]),
+    "mmhip_mul_mat_bias_swiglu": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i32, _vp, _vp, _vp, _sz,
+                                         _vp]),
+    "mmhip_mul_mat_bias_swiglu_h": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _i32, _vp, _vp, _vp]),
+    "mmhip_mul_mat_h_workspace": (_sz, [_i32, _i64, _i64, _i64]),
+    "mmhip_mul_mat_bias_add_hw": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _sz,
+                                         _vp]),
+    "mmhip_mul_mat_multi": (_i32, [_i32, _i32, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "mmhip_mul_mat_multi_h": (_i32, [_i32, _i32, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _vp]),
     "mmhip_act_bytes": (_sz, [_i32, _i64, _i64]),
     "mmhip_quantize_act": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _vp]),
     "mmhip_mul_mat_q": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp]),
@@ -228,6 +236,53 @@ def mul_mat(W, x, out=None, workspace=None):
     wsp = _ptr(workspace) if need else None
     _check(L.mmhip_mul_mat(W.qtype, _ptr(W.data), W.N, W.K, W.row_bytes, _ptr(x), x.stride(0), M, _ptr(out),
                            out.stride(0), wsp, need, _stream()))
+    return out
+
+
+def mul_mat_bias_swiglu(W, x, bias=None, swapped=False, f32_out=True, f16_out=False, workspace=None):
+    """silu(gate) * value over the two halves of (x @ deq(W).T + bias) in the
+    GEMM's epilogue (value = first W.N / 2 rows, gate = the rest; swapped:
+    the other way round).  x is f32 [M, K] or f16 [M, K] (then used as the
+    GEMM's activation copy).  Returns (h f32 [M, F] or None, hh f16 or None)."""
+    torch = _torch()
+    assert x.dim() == 2 and x.shape[1] == W.K and x.stride(1) == 1 and W.N % 2 == 0
+    M, F = x.shape[0], W.N // 2
+    h = torch.empty((M, F), dtype=torch.float32, device=x.device) if f32_out else None
+    hh = torch.empty((M, F), dtype=torch.float16, device=x.device) if f16_out else None
+    L = load()
+    bp = _ptr(bias) if bias is not None else None
+    if x.dtype == torch.float16:
+        assert x.is_contiguous()
+        _check(L.mmhip_mul_mat_bias_swiglu_h(W.qtype, _ptr(W.data), W.N, W.K, W.row_bytes, _ptr(x), M, bp,
+                                             int(swapped), _ptr(h) if h is not None else None,
+                                             _ptr(hh) if hh is not None else None, _stream()))
+        return h, hh
+    assert x.dtype == torch.float32
+    need = L.mmhip_mul_mat_workspace(W.qtype, W.N, W.K, M)
+    if need and (workspace is None or workspace.numel() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    _check(L.mmhip_mul_mat_bias_swiglu(W.qtype, _ptr(W.data), W.N, W.K, W.row_bytes, _ptr(x), x.stride(0), M, bp,
+                                       int(swapped), _ptr(h) if h is not None else None,
+                                       _ptr(hh) if hh is not None else None, _ptr(workspace) if need else None, need,
+                                       _stream()))
+    return h, hh
+
+
+def mul_mat_bias_add(W, x, bias=None, r=None, out=None, workspace=None):
+    """y = x @ deq(W).T (+ bias) (+ r), the GEMM with its ADDs in the store."""
+    torch = _torch()
+    assert x.dtype == torch.float32 and x.dim() == 2 and x.shape[1] == W.K and x.stride(1) == 1
+    M = x.shape[0]
+    if out is None:
+        out = torch.empty((M, W.N), dtype=torch.float32, device=x.device)
+    L = load()
+    need = L.mmhip_mul_mat_workspace(W.qtype, W.N, W.K, M)
+    if need and (workspace is None or workspace.numel() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    _check(L.mmhip_mul_mat_bias_add(W.qtype, _ptr(W.data), W.N, W.K, W.row_bytes, _ptr(x), x.stride(0), M,
+                                    _ptr(bias) if bias is not None else None, _ptr(r) if r is not None else None,
+                                    r.stride(0) if r is not None else 0, _ptr(out), out.stride(0),
+                                    _ptr(workspace) if need else None, need, _stream()))
     return out
 
 
