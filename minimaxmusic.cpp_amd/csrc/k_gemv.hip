@@ -40,8 +40,13 @@ template <int V> __device__ __forceinline__ float wave_reduce_scatter(float (&a)
         const bool upper = (lane & o) != 0;
 #pragma unroll
         for (int i = 0; i < half; i++) {
-            const float send = upper ? a[i] : a[i + half];
-            const float keep = upper ? a[i + half] : a[i];
+            // both operands pinned in registers: a select between two array
+            // loads would otherwise become one load at a lane-dependent index,
+            // which puts the array in scratch memory
+            float lo = a[i], hi = a[i + half];
+            asm volatile("" : "+v"(lo), "+v"(hi));
+            const float send = upper ? lo : hi;
+            const float keep = upper ? hi : lo;
             a[i]             = keep + __shfl_xor(send, o, WAVE);
         }
     }
@@ -436,6 +441,126 @@ __global__ __launch_bounds__(64 * PG_WAVES) void k_gemv_q8_0_pro(PgArgs a) {
                 break;
             }
             pg_load<CH>(ba, a, it * TW + gw, lane);
+        }
+    }
+}
+
+// MUL_MAT of Q8_0 weights against 9..16 activation columns already
+// quantised (the depth decoder's projections at S x CFG = 16 tokens,
+// src/depth-decoder.h:206-257): one 16-wave workgroup per CU copies the
+// columns' int8 values and block scales into LDS once (columns past ncv as
+// zeros), then streams the weight rows as k_gemv_q8_0_pro does, each byte
+// read once in the grid, and dots each row against all 16 columns.  Sums
+// and the residual ADD as store_rows<16, 1>; only the ncv real columns are
+// stored.
+template <int CH>
+__global__ __launch_bounds__(64 * PG_WAVES) void k_gemv_q8_0_wide(PgArgs a, const int8_t * __restrict__ xq,
+                                                                   const float * __restrict__ xd, int ncv) {
+    constexpr int  NC   = 16;
+    constexpr int  MAXK = 1024 * CH;
+    constexpr bool DB   = CH <= 4;
+    extern __shared__ __attribute__((aligned(16))) int8_t g_wide[];
+    int8_t *      s_q  = g_wide;                        // [NC][MAXK]
+    float *       s_d  = (float *) (g_wide + NC * MAXK);  // [NC][MAXK / 32]
+    const int     lane = threadIdx.x & 63;
+    const int     wv   = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t gw   = (int64_t) blockIdx.x * PG_WAVES + wv;
+    const int64_t TW   = (int64_t) gridDim.x * PG_WAVES;
+    const int     K    = a.K;
+    // the first rows in flight while the columns are copied
+    PgBuf<CH>          ba;
+    PgBuf<DB ? CH : 1> bb;
+    pg_load<CH>(ba, a, gw, lane);
+    if constexpr (DB) {
+        pg_load<CH>(bb, a, TW + gw, lane);
+    }
+    for (int i = threadIdx.x; i < NC * (MAXK / 16); i += 64 * PG_WAVES) {
+        const int c = i / (MAXK / 16), e = (i % (MAXK / 16)) * 16;
+        int4_t    v = { 0, 0, 0, 0 };
+        if (c < ncv && e < K) {
+            v = *(const int4_t *) (xq + (int64_t) c * K + e);
+        }
+        *(int4_t *) (s_q + c * MAXK + e) = v;
+    }
+    for (int i = threadIdx.x; i < NC * (MAXK / 32); i += 64 * PG_WAVES) {
+        const int c = i / (MAXK / 32), b = i % (MAXK / 32);
+        s_d[i]      = c < ncv && b < K / 32 ? xd[(int64_t) c * (K / 32) + b] : 0.0f;
+    }
+    __syncthreads();
+    // the 16 waves' rows of one iteration (16 consecutive rows) x 16 columns
+    // are staged in LDS and stored by 256 threads, 16 consecutive rows (64
+    // bytes) per column: single-float stores to 16 output rows per wave had
+    // their lines evicted by the weight stream and written back per store
+    __shared__ float s_out[2][NC][PG_WAVES];
+    auto dot_stage = [&](const auto & buf, int off, int par) {
+        // pg_acc's arithmetic, with the LDS reads bounded to 4 columns at a time
+        // (16 columns' operands do not fit in registers beside the row buffers)
+        float v[NC];
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            v[c] = 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < CH; u++) {
+            const int   o  = min(1024 * u + lane * 16, K - 16);
+            const bool  ok = 1024 * u + lane * 16 < K;
+            const float dw = ok ? h2f(buf.s[u]) : 0.0f;
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                const int4_t xq = *(const int4_t *) &s_q[c * MAXK + o + off];
+                const float  dx = s_d[c * (MAXK / 32) + (o >> 5) + off];
+                v[c] += (float) dot16(buf.w[u], xq) * (dw * dx);
+                if (c % 4 == 3) {
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        }
+        const float total = wave_reduce_scatter<NC>(v, lane);
+        const int   c     = reduce_index<NC>(lane);
+        if ((lane & ((64 / NC) - 1)) == 0) {
+            s_out[par][c][wv] = total;
+        }
+    };
+    // rows it TW + 16 blockIdx.x + 0..15, columns < ncv (the residual ADD here)
+    auto flush = [&](int it) {
+        __syncthreads();
+        if (threadIdx.x < NC * PG_WAVES) {
+            const int     c   = threadIdx.x / PG_WAVES, r = threadIdx.x % PG_WAVES;
+            const int64_t row = (int64_t) it * TW + (int64_t) blockIdx.x * PG_WAVES + r;
+            if (c < ncv && row < a.N) {
+                const float t        = s_out[it & 1][c][r];
+                a.y[c * a.ldy + row] = a.res ? t + a.res[c * a.ldr + row] : t;
+            }
+        }
+    };
+    const int nit = a.nit;
+    if constexpr (DB) {
+        for (int it = 0; it < nit; it += 2) {
+            dot_stage(ba, 0, 0);
+            if (it + 2 < nit) {
+                pg_load<CH>(ba, a, (it + 2) * TW + gw, lane);
+            }
+            flush(it);
+            if (it + 1 < nit) {
+                dot_stage(bb, 0, 1);
+                if (it + 3 < nit) {
+                    pg_load<CH>(bb, a, (it + 3) * TW + gw, lane);
+                }
+                flush(it + 1);
+            }
+        }
+    } else {
+        for (int it = 0;;) {
+            int off = 0;
+            asm volatile("" : "+v"(off));  // the LDS rows are re-read per row
+            dot_stage(ba, off, it & 1);
+            if (it + 1 < nit) {
+                pg_load<CH>(ba, a, (it + 1) * TW + gw, lane);
+            }
+            flush(it);
+            if (++it >= nit) {
+                break;
+            }
         }
     }
 }
@@ -931,14 +1056,20 @@ __global__ __launch_bounds__(256) void k_gemv_bf16(const uint16_t * __restrict__
     }
 }
 
+static int gemv_wide(const uint8_t * W, int64_t N, int64_t K, int64_t rs, const ActPtrs & x, int64_t M, float * y,
+                     int64_t ldy, hipStream_t stream, const float * r, int64_t ldr);
+
 int gemv_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const ActPtrs & x, int64_t M, float * y,
            int64_t ldy, hipStream_t stream, const float * r, int64_t ldr) {
     if (!gemv_supported(wtype, N, K, rs, W) || M < 1 || ldy < N) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "gemv: type %d N=%lld K=%lld M=%lld rs=%lld not supported", wtype,
                          (long long) N, (long long) K, (long long) M, (long long) rs);
     }
-    const int mc = 8;  // column groups of up to 8
     const uint8_t * wb = (const uint8_t *) W;
+    if (wtype == TYPE_Q8_0 && M > 8 && M <= 16 && K <= 8192 && K % 32 == 0) {
+        return gemv_wide(wb, N, K, rs, x, M, y, ldy, stream, r, ldr);
+    }
+    const int mc = 8;  // column groups of up to 8
     for (int64_t c0 = 0; c0 < M; c0 += mc) {
         const int64_t nc = std::min<int64_t>(mc, M - c0);
         ActPtrs       xs = x.slice(c0, K);
@@ -1038,6 +1169,39 @@ template <int NC, int CH, int PRO> static int launch_pro(PgArgs a, hipStream_t s
     auto kern = k_gemv_q8_0_pro<NC, CH, PRO>;
     hipLaunchKernelGGL(kern, dim3((unsigned) wgs), dim3(64 * PG_WAVES), 0, stream, a);
     return check_launch(what);
+}
+
+template <int CH>
+static int launch_wide(PgArgs a, const int8_t * xq, const float * xd, int ncv, hipStream_t stream) {
+    const int64_t need = (a.N + PG_WAVES - 1) / PG_WAVES;
+    const int64_t nit  = (need + pg_cus() - 1) / pg_cus();
+    const int64_t wgs  = (need + nit - 1) / nit;
+    if (nit > 0x7fffffff) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "gemv (16 columns): N=%lld too large", (long long) a.N);
+    }
+    a.nit             = (int) nit;
+    const size_t lds  = (size_t) 16 * 1024 * CH + (size_t) 16 * 32 * CH * sizeof(float);
+    auto         kern = k_gemv_q8_0_wide<CH>;
+    if (lds > 64 * 1024 && !ensure_lds_limit((const void *) kern, lds)) {
+        return set_error(MMHIP_ERR_HIP, "gemv (16 columns): cannot raise LDS limit to %zu", lds);
+    }
+    hipLaunchKernelGGL(kern, dim3((unsigned) wgs), dim3(64 * PG_WAVES), lds, stream, a, xq, xd, ncv);
+    return check_launch("gemv (16 columns)");
+}
+
+static int gemv_wide(const uint8_t * W, int64_t N, int64_t K, int64_t rs, const ActPtrs & x, int64_t M, float * y,
+                     int64_t ldy, hipStream_t stream, const float * r, int64_t ldr) {
+    const PgArgs a{ W, N, (int) K, rs, nullptr, 0, nullptr, 0, nullptr, 0.0f, nullptr, y, ldy, r, ldr, 1 };
+    const int    ch = (int) ((K + 1023) / 1024);
+    switch (ch) {
+        case 1: return launch_wide<1>(a, x.qs, x.d, (int) M, stream);
+        case 2: return launch_wide<2>(a, x.qs, x.d, (int) M, stream);
+        case 3:
+        case 4: return launch_wide<4>(a, x.qs, x.d, (int) M, stream);
+        case 5:
+        case 6: return launch_wide<6>(a, x.qs, x.d, (int) M, stream);
+        default: return launch_wide<8>(a, x.qs, x.d, (int) M, stream);
+    }
 }
 
 template <int PRO> static int dispatch_pro(const PgArgs & a, int64_t M, hipStream_t stream, const char * what) {
