@@ -14,6 +14,8 @@
 // log2(e) folded into the scale.
 #include "mmhip_device.h"
 #include "mmhip_internal.h"
+#include <cstdlib>
+
 #include "k_fa_common.h"
 
 namespace mmhip {
@@ -646,6 +648,392 @@ __global__ __launch_bounds__(64 * NW) void k_fa_dec_mfma(FaArgs a, FaHead h, int
     }
 }
 
+// ---------------------------------------------------------------------
+// The split combine of one output element (a head's dim d; its splits'
+// partial rows at pr0 .. pr0 + nsplit - 1): the weights exp2(m_s - M) from
+// the split maxima sm[] and sums sl[], the weighted sums in split order
+// without contraction, then O / L (k_fa_combine_q's arithmetic).
+__device__ __forceinline__ float fa_combine_elem(const float * __restrict__ part_o, int64_t pr0, int D, int d,
+                                                 int nsplit, const float * sm, const float * sl) {
+#pragma clang fp contract(off)
+    float M = -INFINITY;
+    for (int sidx = 0; sidx < nsplit; sidx++) {
+        M = fmaxf(M, sm[sidx]);
+    }
+    float L = 0.0f, O = 0.0f;
+    if (M != -INFINITY) {
+#pragma unroll 8
+        for (int sidx = 0; sidx < nsplit; sidx++) {
+            const float ms = sm[sidx];
+            const float f  = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
+            L += sl[sidx] * f;
+            O += part_o[(pr0 + sidx) * D + d] * f;
+        }
+    }
+    return L > 0.0f ? O / L : 0.0f;
+}
+
+// Quantisation of an output element v (element e of activation row `row`,
+// K elements a row) into the activation layout of qtype, with k_quant.hip's
+// arithmetic.  Q8_0: a block is 32 consecutive lanes.  Q8_K: a super-block
+// is the 256 threads of 4 consecutive waves, t the thread's index among them,
+// s_red / s_idx / s_amax 4 LDS entries of theirs; every thread of the
+// workgroup calls it together (it synchronises the workgroup), and only the
+// valid ones store.
+__device__ __forceinline__ void fa_quant_elem(float v, bool valid, int t, int64_t row, int e, int K, int qtype,
+                                              int8_t * __restrict__ xq_qs, float * __restrict__ xq_d,
+                                              int16_t * __restrict__ xq_bs, float * s_red, int * s_idx,
+                                              float * s_amax) {
+#pragma clang fp contract(off)
+    int8_t * qs = xq_qs + row * K + e;
+    if (qtype == TYPE_Q8_0) {
+        const float a  = group32_max(fabsf(v));
+        const float dd = a / 127.0f;
+        const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+        if (valid) {
+            *qs = (int8_t) roundf(v * id);
+            if ((t & 31) == 0) {
+                xq_d[row * (K / 32) + e / 32] = h2f(f2h(dd));
+            }
+        }
+        return;
+    }
+    // Q8_K super-block of 256: the first element of largest |x|
+    const int lane = t & 63;
+    float     a    = fabsf(v);
+    float     vm   = v;
+    int       ix   = t;
+    wave_argmax_abs(a, vm, ix);
+    if (lane == 0) {
+        s_red[t >> 6]  = vm;
+        s_idx[t >> 6]  = ix;
+        s_amax[t >> 6] = a;
+    }
+    __syncthreads();
+    float bestA = s_amax[0], bestV = s_red[0];
+    int   bestI = s_idx[0];
+    for (int w = 1; w < 4; w++) {
+        const float aw = s_amax[w];
+        if (aw > bestA || (aw == bestA && s_idx[w] < bestI)) {
+            bestA = aw;
+            bestV = s_red[w];
+            bestI = s_idx[w];
+        }
+    }
+    int   q  = 0;
+    float dd = 0.0f;
+    if (bestA != 0.0f) {
+        const float iscale = -127.0f / bestV;
+        const int   qi     = (int) rintf(iscale * v);
+        q                  = qi > 127 ? 127 : qi;
+        dd                 = 1.0f / iscale;
+    }
+    const int sb = group16_sum_i(q);
+    if (valid) {
+        *qs = (int8_t) q;
+        if ((t & 15) == 0) {
+            xq_bs[row * (K / 16) + e / 16] = (int16_t) sb;
+        }
+        if (t == 0) {
+            xq_d[row * (K / 256) + e / 256] = dd;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------
+// Decode with the head prologue and the split's whole KV range in LDS
+// (D = 128, <= 256 keys per split, one query row, one mask row per
+// workgroup: the LM's batched CFG decode, src/qwen3-lm.h:762-826).  The waves
+// the prologue leaves free DMA the split's K and V rows into LDS with
+// global_load_lds at kernel start, so the KV stream runs while
+// the query / key / value rows are loaded, normalised and rotated; the
+// prologue waves issue no DMA, so their waits are on their own row loads
+// only.  Then the new key / value row replaces the stale cache row in LDS and
+// every wave computes its 16-key tiles from LDS: K as the A operand of
+// mfma_f32_16x16x32_f16 (chunk c of key row r stored at c ^ (r & 15)), V^T by
+// ds_read_b64_tr_b16 as the A operand of mfma_f32_16x16x16f16 (chunk c of V
+// row r at c ^ 2 (r & 3)).  Scores, softmax, wave merge and the partial
+// format are those of k_fa_dec_mfma.
+constexpr int DD_D     = 128;
+constexpr int DD_NW    = 8;
+constexpr int DD_MAXK  = 256;                       // keys per split
+constexpr int DD_ROW   = DD_D * 2;                  // bytes per K / V row
+constexpr int DD_KV    = DD_MAXK * DD_ROW;          // bytes of the K (or V) range
+constexpr int DD_OS    = DD_D + 4;                  // merge-buffer row stride (floats)
+constexpr int DD_LDS   = 2 * DD_KV + DD_MAXK * 2;   // K, V, mask row
+typedef short dd_short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) dd_short4_t dd_lds_short4_t;
+
+__device__ __forceinline__ void dd_dma16(const void * src, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr) : "memory", "m0");
+}
+
+__global__ __launch_bounds__(64 * DD_NW) void k_fa_dec_dma(FaArgs a, FaHead h, int chunk, int nsplit,
+                                                            float * __restrict__ part_o, float * __restrict__ part_ml,
+                                                            float * __restrict__ out) {
+    constexpr int D = DD_D, NW = DD_NW, NS = D / 32, NDB = D / 16, EPL = D / 64;
+    extern __shared__ __attribute__((aligned(1024))) char dd_lds[];  // K [256][256 B], V [256][256 B], mask [256] f16
+    __shared__ float s_m[NW][16], s_l[NW][16];
+    __shared__ __attribute__((aligned(16))) float    s_qrow[16][D];
+    __shared__ __attribute__((aligned(16))) _Float16 s_new[2][D];
+
+    const int split = blockIdx.x;
+    const int g     = blockIdx.y;
+    const int b     = blockIdx.z;
+    const int G     = a.Hq / a.Hkv;
+    const int ncol  = G * a.nq;
+    const int wave  = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane  = threadIdx.x & 63;
+    const int col   = lane & 15;
+    const int kq    = lane >> 4;
+    const int kbeg  = split * chunk;
+    const int kend  = min(a.nkv, kbeg + chunk);
+    const int nkey  = kend - kbeg;
+    const int ntile = (nkey + 15) / 16;
+    const bool cvalid = col < ncol;
+    const int  cc     = cvalid ? col : 0;
+    const uint32_t lbase = (uint32_t) (uintptr_t) (__attribute__((address_space(3))) char *) dd_lds;
+
+    // 1. the DMA waves (past the prologue's tasks): K and V rows of the
+    // split, 1 KB (4 rows) per instruction, then the mask row
+    const int ndma = NW - (ncol + 2);
+    if (wave >= ncol + 2) {
+        const int    dw    = wave - (ncol + 2);
+        const char * kbase = a.k + g * a.knb2 + b * a.knb3;
+        const char * vbase = a.v + g * a.vnb2 + b * a.vnb3;
+        const int    npc   = (nkey + 3) / 4;  // 1 KB pieces per tensor
+        const int    r4 = lane >> 4, c16 = lane & 15;
+        for (int pc = dw; pc < 2 * npc; pc += ndma) {
+            const bool isv = pc >= npc;
+            const int  p   = isv ? pc - npc : pc;
+            const int  r   = 4 * p + r4;
+            const int  key = kbeg + min(r, nkey - 1);
+            const int  ch  = isv ? (c16 ^ (2 * (r & 3))) : (c16 ^ (r & 15));
+            const char * src = (isv ? vbase + (int64_t) key * a.vnb1 : kbase + (int64_t) key * a.knb1) + 16 * ch;
+            dd_dma16(src, lbase + (isv ? DD_KV : 0) + p * 1024);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+
+    // 2. the head prologue (waves 0 .. ncol + 1), as k_fa_dec_mfma's: all
+    // of a wave's loads (cache row id, row, weight, position, mask) go out
+    // together, then the wave computes
+    int64_t id = -1;  // the new rows' cache row (prologue waves)
+    if (wave < ncol + 2) {
+        const int       task = wave;
+        const char *    src;
+        const float *   wp;
+        const int32_t * pp;
+        if (task < ncol) {
+            const int     hq_t = g * G + task % G;
+            const int     iq_t = task / G;
+            const int64_t r    = h.qr0 + iq_t * h.qr1 + hq_t * h.qr2 + b * h.qr3;
+            src                = h.q_src + (r / h.q_H) * h.q_nbt + (r % h.q_H) * h.q_nbh;
+            wp                 = h.q_w ? h.q_w : (const float *) src;
+            pp                 = h.q_pos ? h.q_pos + r / h.q_H : (const int32_t *) src;
+        } else if (task == ncol) {
+            src = h.k_src + b * h.k_nbt + g * h.k_nbh;
+            wp  = h.k_w ? h.k_w : (const float *) src;
+            pp  = h.k_pos ? h.k_pos + b : (const int32_t *) src;
+        } else {
+            src = h.v_src + b * h.v_nbt + g * h.v_nbh;
+            wp  = (const float *) src;
+            pp  = (const int32_t *) src;
+        }
+        // the id as one or two words, without a branch on its type (an i32
+        // id reads its one word twice)
+        const bool      i64  = h.ids_type == 27;
+        const int32_t * ip   = (const int32_t *) (h.ids + (g % h.ids_ne1) * h.ids_nb1 + (b % h.ids_ne2) * h.ids_nb2);
+        const int32_t   idlo = ip[0];
+        const int32_t   idhi = ip[i64 ? 1 : 0];
+        float           tv[EPL], tw[EPL];
+#pragma unroll
+        for (int k = 0; k < EPL; k++) {
+            tv[k] = ((const float *) src)[EPL * lane + k];
+            tw[k] = wp[EPL * lane + k];
+        }
+        const int32_t tpos = *pp;
+        // the value-row wave (no norm, no rope) also brings the split's mask
+        // row into LDS: keys kbeg + 4 lane + i, clamped into the split
+        if (a.mask && task == ncol + 1) {
+            const char * mrow = a.mask + (b % a.mne3) * a.mnb3;
+            uint16_t     mk[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                mk[i] = *(const uint16_t *) (mrow + (int64_t) min(kbeg + 4 * lane + i, kend - 1) * 2);
+            }
+            uint16_t * sm = (uint16_t *) (dd_lds + 2 * DD_KV);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                sm[4 * lane + i] = mk[i];
+            }
+        }
+        id                = i64 ? (int64_t) (((uint64_t) (uint32_t) idhi << 32) | (uint32_t) idlo) : (int64_t) idlo;
+        const bool is_q   = task < ncol;
+        fa_head_row<D>(tv, tw, is_q ? h.q_norm != 0 : task == ncol && h.k_norm != 0,
+                       is_q ? h.q_w != nullptr : h.k_w != nullptr, is_q ? h.q_eps : h.k_eps,
+                       is_q ? h.q_pos != nullptr : task == ncol && h.k_pos != nullptr, tpos, is_q ? h.q_ts : h.k_ts,
+                       lane);
+        const bool writer = split == ((id >= 0 && id < a.nkv) ? (int) (id / chunk) : 0);
+        if (is_q) {
+#pragma unroll
+            for (int k = 0; k < EPL; k++) {
+                s_qrow[task][EPL * lane + k] = tv[k];
+            }
+        } else {
+            const int nr = task - ncol;  // 0 key, 1 value
+            char *    dp = (char *) (nr == 0 ? a.k : a.v) + id * (nr == 0 ? a.knb1 : a.vnb1) +
+                        g * (nr == 0 ? a.knb2 : a.vnb2) + b * (nr == 0 ? a.knb3 : a.vnb3);
+#pragma unroll
+            for (int k = 0; k < EPL; k++) {
+                const uint16_t hb         = f2h(tv[k]);
+                s_new[nr][EPL * lane + k] = __builtin_bit_cast(_Float16, hb);
+                if (writer && id >= 0) {
+                    ((uint16_t *) dp)[EPL * lane + k] = hb;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    // 3. the new rows over the stale cache rows (LDS, swizzled as the DMA stores)
+    if (id >= kbeg && id < kend && wave < 2 && lane < 16) {
+        const int r  = (int) (id - kbeg);
+        const int ch = wave == 0 ? (lane ^ (r & 15)) : (lane ^ (2 * (r & 3)));
+        *(int4_t *) (dd_lds + wave * DD_KV + r * DD_ROW + 16 * ch) = *(const int4_t *) &s_new[wave][8 * lane];
+    }
+    // Q^T B operand: column col, dims 32s + 8kq .. +7
+    half8_t qb[NS];
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            qb[s][i] = cvalid ? (_Float16) s_qrow[cc][32 * s + 8 * kq + i] : (_Float16) 0.0f;
+        }
+    }
+    __syncthreads();
+
+    // 4. the wave's tiles (t = wave, wave + NW, ...) from LDS
+    float4_t oacc[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; i++) {
+        oacc[i] = float4_t{ 0.0f, 0.0f, 0.0f, 0.0f };
+    }
+    float       m     = -INFINITY;
+    float       l     = 0.0f;
+    const float log2e = 1.4426950408889634f;
+    const float sl2   = a.scale * log2e;
+    const _Float16 * smask = (const _Float16 *) (dd_lds + 2 * DD_KV);
+    // V^T tr-read source lane: group tg = lane / 16 (keys 4 tg + tj), tq: dims 4 tq
+    const int tg = lane >> 4, tj = (lane >> 2) & 3, tq = lane & 3;
+    for (int t = wave; t < ntile; t += NW) {
+        // S^T tile: K rows 16 t + col, dims 32s + 8kq
+        float4_t sacc = { 0.0f, 0.0f, 0.0f, 0.0f };
+        const int rk  = 16 * t + col;
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            const half8_t kf = *(const half8_t *) (dd_lds + rk * DD_ROW + 16 * ((4 * s + kq) ^ (rk & 15)));
+            sacc             = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qb[s], sacc, 0, 0, 0);
+        }
+        // scores of keys 4kq + i for this lane's column
+        float sc[4];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int   kr = 16 * t + 4 * kq + i;  // key row in the split
+            const bool  ok = kr < nkey && cvalid;
+            const float mv = a.mask ? (float) smask[kr] : 0.0f;
+            sc[i]          = ok ? sacc[i] * sl2 + mv * log2e : -INFINITY;
+            mx             = fmaxf(mx, sc[i]);
+        }
+        mx                = max_xor32(max_xor16(mx));
+        const float mnew  = fmaxf(m, mx);
+        const bool  live  = mnew != -INFINITY;
+        const float mref  = live ? mnew : 0.0f;
+        const float alpha = live ? __builtin_amdgcn_exp2f(m - mnew) : 1.0f;
+        half4_t     pb;
+        float       rs = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float pv = __builtin_amdgcn_exp2f(sc[i] - mref);
+            rs += pv;
+            pb[i] = (_Float16) pv;
+        }
+        rs = sum_xor32(sum_xor16(rs));
+        l  = l * alpha + rs;
+        m  = mnew;
+        // O^T += V^T P^T: lane (dim 16db + i, keys 4 tg ..) via transposed reads
+        const int rv = 16 * t + 4 * tg + tj;
+#pragma unroll
+        for (int db = 0; db < NDB; db++) {
+            const int      d  = 16 * db + 4 * tq;
+            const uint32_t ad = lbase + DD_KV + rv * DD_ROW + 16 * ((d >> 3) ^ (2 * (rv & 3))) + 2 * (d & 7);
+            const half4_t  av = __builtin_bit_cast(
+                half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((dd_lds_short4_t *) (uintptr_t) ad));
+            oacc[db] = oacc[db] * alpha;
+            oacc[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, pb, oacc[db], 0, 0, 0);
+        }
+    }
+
+    // 5. merge the NW waves (the K / V space reused) and write the partials
+    __syncthreads();
+    float * s_o = (float *) dd_lds;  // [NW][16][DD_OS]
+    if (kq == 0) {
+        s_m[wave][col] = m;
+        s_l[wave][col] = l;
+    }
+    if (cvalid) {
+#pragma unroll
+        for (int db = 0; db < NDB; db++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                s_o[(wave * 16 + col) * DD_OS + 16 * db + 4 * kq + i] = oacc[db][i];
+            }
+        }
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < ncol * D; idx += 64 * NW) {
+        const int c = idx / D;
+        const int d = idx % D;
+        float     M = s_m[0][c];
+#pragma unroll
+        for (int w = 1; w < NW; w++) {
+            M = fmaxf(M, s_m[w][c]);
+        }
+        float L = 0.0f, O = 0.0f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < NW; w++) {
+                const float f = s_m[w][c] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s_m[w][c] - M);
+                L += s_l[w][c] * f;
+                O += s_o[(w * 16 + c) * DD_OS + d] * f;
+            }
+        }
+        const int hh = g * G + c % G;
+        const int qi = c / G;
+        if (nsplit == 1) {
+            out[(((int64_t) b * a.nq + qi) * a.Hq + hh) * D + d] = L > 0.0f ? O / L : 0.0f;
+        } else {
+            const int64_t pr = (((int64_t) b * a.Hq + hh) * a.nq + qi) * nsplit + split;
+            part_o[pr * D + d] = O;
+            if (d == 0) {
+                part_ml[pr * 2 + 0] = M;
+                part_ml[pr * 2 + 1] = L;
+            }
+        }
+    }
+}
+
+// k_fa_dec_dma's preconditions
+static bool dec_dma_ok(const FaArgs & a, int D, int chunk, const FaHead * hd) {
+    auto al16 = [](int64_t v) { return (v & 15) == 0; };
+    const int G = a.Hq / a.Hkv;
+    return hd && D == DD_D && chunk <= DD_MAXK && a.nq == 1 && G * a.nq + 3 <= DD_NW && a.Bk == a.B &&
+           (!a.mask || a.mne2 == 1) &&
+           al16((int64_t) (uintptr_t) a.k) && al16(a.knb1) && al16(a.knb2) && al16(a.knb3) &&
+           al16((int64_t) (uintptr_t) a.v) && al16(a.vnb1) && al16(a.vnb2) && al16(a.vnb3) &&
+           getenv("GGML_MI355X_DISABLE_DEC_DMA") == nullptr;
+}
+
 // One workgroup of D threads per output row (b, hq, iq): the split weights
 // exp2(m_s - M) / L are formed once in LDS, then every thread sums its dim.
 __global__ __launch_bounds__(256) void k_fa_combine(const float * __restrict__ part_o,
@@ -713,18 +1101,18 @@ __global__ __launch_bounds__(256) void k_fa_combine(const float * __restrict__ p
 // consumes them (the attention output projection): one 256-thread workgroup
 // per 256-element chunk of an output row (b, iq), thread t owning element t
 // (head e / D, dim e % D), so a workgroup holds whole Q8_0 blocks and a whole
-// Q8_K super-block.  The quantisation arithmetic is k_quant.hip's.
+// Q8_K super-block.  The quantisation arithmetic is k_quant.hip's.  With
+// xq_qs null it is the plain combine (the decode's default: the same
+// arithmetic as the decode kernel's own combine).
 __global__ __launch_bounds__(256) void k_fa_combine_q(const float * __restrict__ part_o,
                                                       const float * __restrict__ part_ml, int nsplit, int D, int nq,
                                                       int Hq, float * __restrict__ out, int qtype,
                                                       int8_t * __restrict__ xq_qs, float * __restrict__ xq_d,
                                                       int16_t * __restrict__ xq_bs) {
-#pragma clang fp contract(off)
     __shared__ float s_m[4][128], s_l[4][128];
     __shared__ float s_red[4], s_amax[4];
     __shared__ int   s_idx[4];
     const int t    = threadIdx.x;
-    const int lane = t & 63;
     const int e    = 256 * blockIdx.x + t;  // element of the output row
     const int iq   = blockIdx.y;
     const int b    = blockIdx.z;
@@ -738,75 +1126,12 @@ __global__ __launch_bounds__(256) void k_fa_combine_q(const float * __restrict__
         s_l[hl][sidx] = part_ml[(pr0 + sidx) * 2 + 1];
     }
     __syncthreads();
-    float M = -INFINITY;
-    for (int sidx = 0; sidx < nsplit; sidx++) {
-        M = fmaxf(M, s_m[hl][sidx]);
-    }
-    float L = 0.0f, O = 0.0f;
-    if (M != -INFINITY) {
-#pragma unroll 8
-        for (int sidx = 0; sidx < nsplit; sidx++) {
-            const float ms = s_m[hl][sidx];
-            const float f  = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
-            L += s_l[hl][sidx] * f;
-            O += part_o[(pr0 + sidx) * D + d] * f;
-        }
-    }
-    const float v   = L > 0.0f ? O / L : 0.0f;
+    const float   v   = fa_combine_elem(part_o, pr0, D, d, nsplit, s_m[hl], s_l[hl]);
     const int64_t row = (int64_t) b * nq + iq;
     const int     K   = Hq * D;
     out[row * K + e]  = v;
-    if (!xq_qs) {
-        return;
-    }
-    int8_t * qs = xq_qs + row * K + e;
-    if (qtype == TYPE_Q8_0) {
-        // blocks of 32 = half a wave
-        const float a = group32_max(fabsf(v));
-        const float dd = a / 127.0f;
-        const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
-        *qs            = (int8_t) roundf(v * id);
-        if ((t & 31) == 0) {
-            xq_d[row * (K / 32) + e / 32] = h2f(f2h(dd));
-        }
-        return;
-    }
-    // Q8_K super-block of 256: the first element of largest |x|
-    float a  = fabsf(v);
-    float vm = v;
-    int   ix = t;
-    wave_argmax_abs(a, vm, ix);
-    if (lane == 0) {
-        s_red[t >> 6]  = vm;
-        s_idx[t >> 6]  = ix;
-        s_amax[t >> 6] = a;
-    }
-    __syncthreads();
-    float bestA = s_amax[0], bestV = s_red[0];
-    int   bestI = s_idx[0];
-    for (int w = 1; w < 4; w++) {
-        const float aw = s_amax[w];
-        if (aw > bestA || (aw == bestA && s_idx[w] < bestI)) {
-            bestA = aw;
-            bestV = s_red[w];
-            bestI = s_idx[w];
-        }
-    }
-    int   q  = 0;
-    float dd = 0.0f;
-    if (bestA != 0.0f) {
-        const float iscale = -127.0f / bestV;
-        const int   qi     = (int) rintf(iscale * v);
-        q                  = qi > 127 ? 127 : qi;
-        dd                 = 1.0f / iscale;
-    }
-    *qs    = (int8_t) q;
-    const int sb = group16_sum_i(q);
-    if ((t & 15) == 0) {
-        xq_bs[row * (K / 16) + e / 16] = (int16_t) sb;
-    }
-    if (t == 0) {
-        xq_d[row * (K / 256) + e / 256] = dd;
+    if (xq_qs) {
+        fa_quant_elem(v, true, t, row, e, K, qtype, xq_qs, xq_d, xq_bs, s_red, s_idx, s_amax);
     }
 }
 
@@ -911,7 +1236,20 @@ int fa_decode(const FaArgs & a, int D, float * out, void * ws, size_t ws_bytes, 
     if ((int64_t) a.B * rg > 65535) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "flash_attn decode: B * row groups too large");
     }
-    if (dec_mfma(a)) {
+    // the split combine: quantising for xq's weights where its layout allows,
+    // by k_fa_combine_q's arithmetic wherever the rows are whole 256-chunks
+    const int64_t   K      = (int64_t) a.Hq * D;
+    const ActLayout L      = xq ? act_layout(qtype, K, (int64_t) a.B * a.nq) : ActLayout{};
+    const bool      comb_q = K % 256 == 0 && nsplit <= 128;
+    const bool      quant  = xq && L.total != 0 && comb_q;
+    if (dec_dma_ok(a, D, chunk, hd)) {
+        const dim3 g3(nsplit, a.Hkv, a.B);
+        if (!ensure_lds_limit((const void *) k_fa_dec_dma, DD_LDS)) {
+            return set_error(MMHIP_ERR_HIP, "flash_attn decode: cannot raise LDS limit to %d", DD_LDS);
+        }
+        hipLaunchKernelGGL(k_fa_dec_dma, g3, dim3(64 * DD_NW), DD_LDS, stream, a, *hd, chunk, nsplit, part_o, part_ml,
+                           out);
+    } else if (dec_mfma(a)) {
         const dim3 g3(nsplit, a.Hkv, a.B);
         // tiles per wave: the split's tiles in one load round where that fits
         const int tiles = (chunk / 16 + dec_nw(D) - 1) / dec_nw(D);
@@ -945,15 +1283,13 @@ int fa_decode(const FaArgs & a, int D, float * out, void * ws, size_t ws_bytes, 
     if (rc != MMHIP_OK || nsplit == 1) {
         return rc;
     }
-    const int64_t   K = (int64_t) a.Hq * D;
-    const ActLayout L = xq ? act_layout(qtype, K, (int64_t) a.B * a.nq) : ActLayout{};
-    if (xq && L.total != 0 && K % 256 == 0 && nsplit <= 128) {
+    if (comb_q) {
         hipLaunchKernelGGL(k_fa_combine_q, dim3((unsigned) (K / 256), a.nq, a.B), dim3(256), 0, stream, part_o, part_ml,
-                           nsplit, D, a.nq, a.Hq, out, L.vec_type, (int8_t *) xq + L.qs_off,
-                           (float *) ((char *) xq + L.d_off),
-                           L.vec_type == TYPE_Q8_K ? (int16_t *) ((char *) xq + L.bs_off) : nullptr);
+                           nsplit, D, a.nq, a.Hq, out, L.vec_type, quant ? (int8_t *) xq + L.qs_off : nullptr,
+                           quant ? (float *) ((char *) xq + L.d_off) : nullptr,
+                           quant && L.vec_type == TYPE_Q8_K ? (int16_t *) ((char *) xq + L.bs_off) : nullptr);
         if (quantised) {
-            *quantised = true;
+            *quantised = quant;
         }
         return check_launch("flash_attn combine");
     }

@@ -326,64 +326,76 @@ def test_head_rows_three_chains_one_launch(mm, orc):
 
 @pytest.mark.parametrize("D,nkv,ids_", [(128, 512, (300, 45)), (128, 4096, (4095, 4095)), (64, 700, (699, 0)),
                                         (128, 256, (900, 3))])
-@pytest.mark.parametrize("quant", [False, True])
+@pytest.mark.parametrize("quant", [0, 8, 14])
 def test_flash_attn_head_equals_separate(mm, D, nkv, ids_, quant):
     """Decode attention with the Q/K/V head chains in its prologue equals
     mmhip_head_rows_n then the attention: the same caches (the new rows
-    written), the same output (and quantised output) bit for bit.  Cases: new
-    rows inside the window, at its last key, and past it (900 > nkv: written,
-    not attended)."""
+    written), the same output (and quantised output: Q8_0 blocks for Q8_0
+    weights, Q8_K super-blocks for Q6_K weights) bit for bit.  At D = 128 the
+    fused call runs k_fa_dec_dma (the split's K / V DMA'd into LDS while the
+    prologue runs, the new rows substituted there), the separate one
+    k_fa_dec_mfma.  Both run the inputs A, B, A in a row through one
+    workspace.  Cases: new rows inside the window, at its last key, and past
+    it (900 > nkv: written, not attended)."""
     L = mm.load()
     rng = np.random.default_rng(31)
     T, Hq, Hk, S = 2, 32, 8, 4608
     C = (Hq + 2 * Hk) * D
-    qkv = torch.from_numpy((rng.standard_normal((T, C)) * 2).astype(np.float32)).cuda()
+    qkvs = [torch.from_numpy((rng.standard_normal((T, C)) * 2).astype(np.float32)).cuda() for _ in range(2)]
     wq = torch.from_numpy((1 + 0.02 * rng.standard_normal(D)).astype(np.float32)).cuda()
     wk = torch.from_numpy((1 + 0.02 * rng.standard_normal(D)).astype(np.float32)).cuda()
     pos = torch.tensor(list(ids_), dtype=torch.int32, device="cuda")
     ids = torch.tensor(list(ids_), dtype=torch.int64, device="cuda")
-    kc0 = torch.from_numpy(rng.standard_normal((T, Hk, S, D)).astype(np.float16)).cuda()
-    vc0 = torch.from_numpy(rng.standard_normal((T, Hk, S, D)).astype(np.float16)).cuda()
+    kc0s = [torch.from_numpy(rng.standard_normal((T, Hk, S, D)).astype(np.float16)).cuda() for _ in range(2)]
+    vc0s = [torch.from_numpy(rng.standard_normal((T, Hk, S, D)).astype(np.float16)).cuda() for _ in range(2)]
     keys = np.arange(nkv)[None, :]
     allow = keys <= np.minimum(np.array(ids_), nkv - 1)[:, None]
     mask = torch.from_numpy(np.where(allow, 0, -np.inf).astype(np.float16).reshape(T, 1, 1, nkv)).cuda()
     kvne, kvnb = [D, nkv, Hk, T], [2, 2 * D, 2 * D * S, 2 * D * S * Hk]
     K = Hq * D
-    res = []
+    qout = torch.zeros((T, Hq, D), dtype=torch.float32, device="cuda")
+    qv = mm.view_of(qout, [D, 1, Hq, T], [4, 4 * D * Hq, 4 * D, 4 * D * Hq])
+    kc, vc = kc0s[0].clone(), vc0s[0].clone()
+    kv, vv = mm.view_of(kc, kvne, kvnb), mm.view_of(vc, kvne, kvnb)
+    mv = mm.view_of(mask)
+    need = L.mmhip_flash_attn_workspace(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv))
+    ws = torch.empty(max(need, 256), dtype=torch.uint8, device="cuda")
+    res = {}
     for fused in (False, True):
-        qout = torch.zeros((T, Hq, D), dtype=torch.float32, device="cuda")
-        kc, vc = kc0.clone(), vc0.clone()
-        a = (mm.HeadRowsArgs * 3)(
-            _head_args(mm, qkv, D, Hq, T, C * 4, norm_w=wq, pos=pos, dst=qout),
-            _head_args(mm, qkv[:, Hq * D:], D, Hk, T, C * 4, norm_w=wk, pos=pos, ids=ids, cache=kc),
-            _head_args(mm, qkv[:, (Hq + Hk) * D:], D, Hk, T, C * 4, ids=ids, cache=vc))
-        qv = mm.view_of(qout, [D, 1, Hq, T], [4, 4 * D * Hq, 4 * D, 4 * D * Hq])
-        kv, vv = mm.view_of(kc, kvne, kvnb), mm.view_of(vc, kvne, kvnb)
-        mv = mm.view_of(mask)
-        need = L.mmhip_flash_attn_workspace(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv))
-        ws = torch.empty(max(need, 256), dtype=torch.uint8, device="cuda")
-        out = torch.full((T, 1, Hq, D), float("nan"), device="cuda")
-        xq = torch.zeros(L.mmhip_act_bytes(8, K, T), dtype=torch.uint8, device="cuda") if quant else None
-        args = (ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), ctypes.byref(mv), float(1 / np.sqrt(D)),
-                ptr(out), ptr(ws), need)
-        if fused:
-            assert L.mmhip_flash_attn_ext_head_supported(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv)) == 1
-            assert L.mmhip_flash_attn_ext_head(*args, 8 if quant else 0, ptr(xq) if quant else None,
-                                               ctypes.byref(a), st()) == 0
-        else:
-            assert L.mmhip_head_rows_n(ctypes.byref(a), 3, st()) == 0
-            if quant:
-                assert L.mmhip_flash_attn_ext_q(*args, 8, ptr(xq), st()) == 0
+        for rep, sel in enumerate((0, 1, 0)):
+            qkv = qkvs[sel]
+            kc.copy_(kc0s[sel])
+            vc.copy_(vc0s[sel])
+            qout.zero_()
+            a = (mm.HeadRowsArgs * 3)(
+                _head_args(mm, qkv, D, Hq, T, C * 4, norm_w=wq, pos=pos, dst=qout),
+                _head_args(mm, qkv[:, Hq * D:], D, Hk, T, C * 4, norm_w=wk, pos=pos, ids=ids, cache=kc),
+                _head_args(mm, qkv[:, (Hq + Hk) * D:], D, Hk, T, C * 4, ids=ids, cache=vc))
+            out = torch.full((T, 1, Hq, D), float("nan"), device="cuda")
+            xq = torch.zeros(L.mmhip_act_bytes(quant, K, T), dtype=torch.uint8, device="cuda") if quant else None
+            args = (ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), ctypes.byref(mv), float(1 / np.sqrt(D)),
+                    ptr(out), ptr(ws), need)
+            if fused:
+                assert L.mmhip_flash_attn_ext_head_supported(ctypes.byref(qv), ctypes.byref(kv),
+                                                             ctypes.byref(vv)) == 1
+                assert L.mmhip_flash_attn_ext_head(*args, quant, ptr(xq) if quant else None,
+                                                   ctypes.byref(a), st()) == 0
             else:
-                assert L.mmhip_flash_attn_ext(*args, st()) == 0
-        torch.cuda.synchronize()
-        res.append((out, kc, vc, xq))
-    (o1, k1, v1, x1), (o2, k2, v2, x2) = res
-    assert torch.equal(k1, k2) and torch.equal(v1, v2)
-    assert not torch.equal(k1, kc0)  # the new rows were written
-    assert torch.equal(o1, o2)
-    if quant:
-        assert torch.equal(x1, x2)
+                assert L.mmhip_head_rows_n(ctypes.byref(a), 3, st()) == 0
+                if quant:
+                    assert L.mmhip_flash_attn_ext_q(*args, quant, ptr(xq), st()) == 0
+                else:
+                    assert L.mmhip_flash_attn_ext(*args, st()) == 0
+            torch.cuda.synchronize()
+            assert not torch.equal(kc, kc0s[sel])  # the new rows were written
+            res[fused, rep] = (out, kc.clone(), vc.clone(), xq)
+    assert not torch.equal(res[False, 0][0], res[False, 1][0])  # A and B differ
+    for rep in range(3):
+        (o1, k1, v1, x1), (o2, k2, v2, x2) = res[False, rep], res[True, rep]
+        assert torch.equal(k1, k2) and torch.equal(v1, v2)
+        assert torch.equal(o1, o2), rep
+        if quant:
+            assert torch.equal(x1, x2), rep
 
 
 def test_flash_attn_head_rejects_prefill_shapes(mm):
