@@ -11,6 +11,8 @@
 // a field per step (every field of the row-grouped layout is contiguous).
 // The quantised activations of the M columns (a few KB) are read through the
 // L1/L2 caches by every wave, so HBM carries essentially only the weights.
+#include <cstdlib>
+
 #include "mmhip_device.h"
 #include "mmhip_internal.h"
 
@@ -284,10 +286,19 @@ __device__ __forceinline__ void pg_dot(const PgBuf<CH> & b, const int8_t * sq, c
 // kernels' unfused f32 arithmetic; the dot products keep the plain GEMV's
 // FMAs), quantised into LDS (s_q: [NC][MAXK] int8, s_d: [NC][MAXK / 32]).
 // xv / xw hold chunk j of thread t: elements 4 t + 4096 j .. + 3.
-template <int NC, int J, int MAXK, int PRO>
+// Byte position of Q8_K activation byte b in LDS: 16-byte granule g of
+// super-block sb = g / 16 stored at g ^ 2 (sb % 4), so that the Q6_K dot's
+// 16-byte reads (lanes 4 s + 2 a + b0 at 256 s + 128 a + 16 b0 + 32 t) fall
+// in 16 different bank groups per 16 lanes
+__device__ __forceinline__ int q8k_swz(int b) {
+    const int g = b >> 4;
+    return ((g ^ (2 * ((g >> 4) & 3))) << 4) | (b & 15);
+}
+
+template <int NC, int J, int MAXK, int PRO, int QT = TYPE_Q8_0>
 __device__ __forceinline__ void pg_prologue(const float4_t (&xv)[J][NC], const float4_t (&xw)[J][PRO == PRO_NORM ? 1 : NC],
                                             int8_t * s_q, float * s_d, double (*s_ss)[PG_WAVES], const PgArgs & a,
-                                            int lane, int wv, int K) {
+                                            int lane, int wv, int K, int16_t * s_bs = nullptr) {
 #pragma clang fp contract(off)
     float sc[NC];
     if constexpr (PRO == PRO_NORM) {
@@ -336,6 +347,20 @@ __device__ __forceinline__ void pg_prologue(const float4_t (&xv)[J][NC], const f
                     const float silu = g / (1.0f + expf(-g));
                     o[k]             = silu * xw[j][c][k];
                 }
+            }
+            if constexpr (QT == TYPE_Q8_K) {
+                // the wave's 256 elements are one super-block (K % 256 == 0:
+                // the condition is uniform over the wave)
+                const int ch = e / 256;
+                if (e < K) {
+                    const char4 q4 = quant_chunk256_q(o, lane, TYPE_Q8_K, s_d + c * (MAXK / 256) + ch,
+                                                      s_bs + c * (MAXK / 16) + 16 * ch);
+                    *(char4 *) &s_q[c * MAXK + q8k_swz(256 * ch + 4 * lane)] = q4;
+                    if (a.xo && blockIdx.x == 0) {
+                        *(float4_t *) (a.xo + (int64_t) c * K + e) = float4_t{ o[0], o[1], o[2], o[3] };
+                    }
+                }
+                continue;
             }
             const float m = group8_max(fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3]))));
             const float dd = m / 127.0f;
@@ -441,6 +466,270 @@ __global__ __launch_bounds__(64 * PG_WAVES) void k_gemv_q8_0_pro(PgArgs a) {
                 break;
             }
             pg_load<CH>(ba, a, it * TW + gw, lane);
+        }
+    }
+}
+
+// Persistent Q6_K GEMVs with the same prologues, the activation rows
+// quantised to Q8_K (super-blocks of 256 with 16-element sums) into LDS.
+// A row is read in units of 64 elements as k_gemv_q6_K reads it: lane l owns
+// units l + 64 u (u < CH), unit un covering elements eb + 32 t + 0..15
+// (t < 4, eb = 256 sb + 128 h + l0 with sb = un / 4, h = un / 2 % 2, l0 =
+// 16 (un % 2)) from 16 bytes of ql at 128 sb + 64 h + l0 and + 32, 16 bytes of
+// qh at K/2 + 64 sb + 32 h + l0, the half's 8 scales and the super-block's d;
+// the row is planar (ql, qh, scales, d), as the backend stores Q6_K.  Each
+// lane adds its units in u order and the sums are reduced as store_rows
+// reduces them, so the result is k_gemv_q6_K's to the bit.
+template <int CH> struct Pg6Buf {
+    int4_t   ql0[CH], ql1[CH], qh[CH];
+    uint2    sc[CH];
+    uint16_t d[CH];
+};
+
+template <int CH, int U0 = 0, int U1 = CH>
+__device__ __forceinline__ void pg6_load(Pg6Buf<CH> & b, const PgArgs & a, int64_t row, int lane) {
+    const uint8_t *              wr = a.W + (row < a.N ? row : a.N - 1) * a.rs;
+    const int                    K  = a.K;
+    const __amdgpu_buffer_rsrc_t rr =
+        __builtin_amdgcn_make_buffer_rsrc((void *) wr, (short) 0, K / 2 + K / 4 + K / 16 + K / 128, 0x00020000);
+    // unit lane + 64 u sits 16 super-blocks after unit lane: its offsets are
+    // the lane's plus constants (the units past the row read other bytes of
+    // the row, or zeros past its end, and are weighted by zero)
+    const int sb = lane >> 2, h = (lane >> 1) & 1, l0 = (lane & 1) * 16;
+    const int oql = sb * 128 + h * 64 + l0;
+    const int oqh = sb * 64 + h * 32 + l0;
+    const int osc = sb * 16 + h * 8;
+    const int od  = 2 * sb;
+#pragma unroll
+    for (int u = U0; u < U1; u++) {
+        b.ql0[u] = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(rr, oql + 2048 * u, 0, 0));
+        b.ql1[u] = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(rr, oql + 2048 * u + 32, 0, 0));
+        b.qh[u]  = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(rr, oqh + 1024 * u, K / 2, 0));
+        b.sc[u]  = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rr, osc + 256 * u, K / 2 + K / 4, 0));
+        b.d[u]   = __builtin_amdgcn_raw_buffer_load_b16(rr, od + 32 * u, K / 2 + K / 4 + K / 16, 0);
+    }
+}
+
+// The activation operands of one unit: 4 x 16 values, their 16-element sums
+// and the super-block scale, per column
+template <int NC> struct Pg6X {
+    int4_t v[NC][4];
+    int    bs[NC][4];
+    float  d[NC];
+};
+
+template <int NC, int MAXK>
+__device__ __forceinline__ void pg6_x(Pg6X<NC> & x, const int8_t * sq, const float * sd, const int16_t * sb16, int un) {
+    const int sb = un >> 2, h = (un >> 1) & 1, l0 = (un & 1) * 16;
+    const int eb = sb * 256 + h * 128 + l0;
+    const int g0 = sb * 16 + h * 8 + (l0 >> 4);
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            x.v[c][t]  = *(const int4_t *) &sq[c * MAXK + q8k_swz(eb + 32 * t)];
+            x.bs[c][t] = sb16[c * (MAXK / 16) + g0 + 2 * t];
+        }
+        x.d[c] = sd[c * (MAXK / 256) + sb];
+    }
+}
+
+// the 6-bit values and scales of one unit (k_gemv_q6_K's unpacking)
+template <int CH>
+__device__ __forceinline__ void pg6_decode(const Pg6Buf<CH> & b, int u, int un, bool ok, int4_t (&q)[4], int (&sc)[4],
+                                           float & dw) {
+    const int l0 = (un & 1) * 16;
+    dw           = ok ? h2f(b.d[u]) : 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int4_t src = (t & 1) ? b.ql1[u] : b.ql0[u];
+        const int    sh  = (t < 2) ? 0 : 4;
+        q[t].x = ((src.x >> sh) & 0x0F0F0F0F) | (((b.qh[u].x >> (2 * t)) & 0x03030303) << 4);
+        q[t].y = ((src.y >> sh) & 0x0F0F0F0F) | (((b.qh[u].y >> (2 * t)) & 0x03030303) << 4);
+        q[t].z = ((src.z >> sh) & 0x0F0F0F0F) | (((b.qh[u].z >> (2 * t)) & 0x03030303) << 4);
+        q[t].w = ((src.w >> sh) & 0x0F0F0F0F) | (((b.qh[u].w >> (2 * t)) & 0x03030303) << 4);
+        const int      bi = (l0 >> 4) + 2 * t;
+        const uint32_t wd = bi < 4 ? b.sc[u].x : b.sc[u].y;
+        sc[t]             = (int) (int8_t) ((wd >> (8 * (bi & 3))) & 0xff);
+    }
+}
+
+// column c's share of one unit (k_gemv_q6_K's arithmetic)
+template <int NC>
+__device__ __forceinline__ void pg6_col(const int4_t (&q)[4], const int (&sc)[4], float dw, const int4_t (&xv)[4],
+                                        const int (&bs)[4], float dx, float & acc) {
+    int isum = 0;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        isum += sc[t] * (dot16(q[t], xv[t]) - 32 * bs[t]);
+    }
+    acc += (dw * dx) * (float) isum;
+}
+
+template <int NC, int CH>
+__device__ __forceinline__ void pg6_unit(const Pg6Buf<CH> & b, int u, const Pg6X<NC> & x, bool ok, int un,
+                                         float (&acc)[1][NC]) {
+    int4_t q[4];
+    int    sc[4];
+    float  dw;
+    pg6_decode<CH>(b, u, un, ok, q, sc, dw);
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        pg6_col<NC>(q, sc, dw, x.v[c], x.bs[c], x.d[c], acc[0][c]);
+    }
+}
+
+// PRO_NORM / PRO_SWIGLU as k_gemv_q8_0_pro; PRO_NONE: the Q8_K activation
+// rows (qs, d, bsums) are copied into LDS instead.  CH = 1 (K <= 4096): a
+// lane's activation operands are the same for every row and stay in
+// registers, two rows in flight per wave; CH > 1: one row in flight, the
+// operands read from LDS per unit.
+constexpr int PRO_NONE = 2;
+
+struct Pg6Act {
+    const int8_t *  qs;  // PRO_NONE: [NC][K]
+    const float *   d;   // [NC][K / 256]
+    const int16_t * bs;  // [NC][K / 16]
+};
+
+template <int NC, int CH, int PRO>
+__global__ __launch_bounds__(64 * PG_WAVES) void k_gemv_q6_K_pro(PgArgs a, Pg6Act xa) {
+    constexpr int  MAXK = 4096 * CH;
+    constexpr int  J    = MAXK / (256 * PG_WAVES);
+    constexpr bool DB   = CH == 1;
+    constexpr int  NW   = PRO == PRO_NORM ? 1 : NC;
+    __shared__ __attribute__((aligned(16))) int8_t s_q[NC * MAXK];
+    __shared__ float   s_d[NC * MAXK / 256];
+    __shared__ int16_t s_bs[NC * MAXK / 16];
+    __shared__ double  s_ss[NC][PG_WAVES];
+    const int     lane  = threadIdx.x & 63;
+    const int     wv    = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t gw    = (int64_t) blockIdx.x * PG_WAVES + wv;
+    const int64_t TW    = (int64_t) gridDim.x * PG_WAVES;
+    const int     K     = a.K;
+    const int     units = K / 64;
+    // 1. activations (or the quantised rows), then the first weight rows
+    float4_t xv[J][NC], xw[J][NW];
+    if constexpr (PRO != PRO_NONE) {
+#pragma unroll
+        for (int j = 0; j < J; j++) {
+            const unsigned e = min(4u * threadIdx.x + 256u * PG_WAVES * j, (unsigned) K - 4u);
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                xv[j][c] = *(const float4_t *) (a.x + c * a.ldx + e);
+                if constexpr (PRO == PRO_SWIGLU) {
+                    xw[j][c] = *(const float4_t *) (a.u + c * a.ldu + e);
+                }
+            }
+            if constexpr (PRO == PRO_NORM) {
+                xw[j][0] = *(const float4_t *) (a.nw + e);
+            }
+        }
+    } else {
+        // int8 values 16 per thread per step, then the scales and sums
+        for (int i = threadIdx.x; i < NC * K / 16; i += 64 * PG_WAVES) {
+            const int c = i / (K / 16), o = i % (K / 16);
+            *(int4_t *) &s_q[c * MAXK + q8k_swz(16 * o)] = *(const int4_t *) (xa.qs + (int64_t) c * K + 16 * o);
+            s_bs[c * (MAXK / 16) + o]          = xa.bs[(int64_t) c * (K / 16) + o];
+        }
+        for (int i = threadIdx.x; i < NC * K / 256; i += 64 * PG_WAVES) {
+            const int c = i / (K / 256), o = i % (K / 256);
+            s_d[c * (MAXK / 256) + o] = xa.d[(int64_t) c * (K / 256) + o];
+        }
+    }
+    // a long row: its first unit ahead of an f32 prologue, the rest after it
+    // (the activation values would not fit in registers beside them); the
+    // whole row ahead of a copy of quantised rows
+    constexpr int       PRE = DB || PRO == PRO_NONE ? CH : 1;
+    Pg6Buf<CH>          ba;
+    Pg6Buf<DB ? CH : 1> bb;
+    pg6_load<CH, 0, PRE>(ba, a, gw, lane);
+    if constexpr (DB) {
+        if constexpr (PRO != PRO_NONE) {
+#pragma unroll
+            for (int j = 0; j < J; j++) {
+#pragma unroll
+                for (int c = 0; c < NC; c++) {
+                    asm volatile("" ::"v"(xv[j][c][0]), "v"(xw[j][PRO == PRO_NORM ? 0 : c][0]) : "memory");
+                }
+            }
+        }
+        pg6_load<CH>(bb, a, TW + gw, lane);
+    }
+    // 2. the activation values, quantised into LDS
+    if constexpr (PRO != PRO_NONE) {
+        pg_prologue<NC, J, MAXK, PRO, TYPE_Q8_K>(xv, xw, s_q, s_d, s_ss, a, lane, wv, K, s_bs);
+    }
+    if constexpr (PRE < CH) {
+        pg6_load<CH, PRE, CH>(ba, a, gw, lane);
+    }
+    __syncthreads();
+    // 3. stream the rows
+    const int nit = a.nit;
+    if constexpr (DB) {
+        const bool ok = lane < units;
+        const int  un = ok ? lane : 0;
+        Pg6X<NC>   x;
+        pg6_x<NC, MAXK>(x, s_q, s_d, s_bs, un);
+        auto dot = [&](const Pg6Buf<CH> & b, int64_t row) {
+            float acc[1][NC];
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                acc[0][c] = 0.0f;
+            }
+            pg6_unit<NC, CH>(b, 0, x, ok, un, acc);
+            store_rows<NC, 1>(acc, lane, row, a.N, a.y, a.ldy, a.res, a.ldr);
+        };
+        int it = 0;
+        for (; it + 2 < nit; it += 2) {
+            dot(ba, it * TW + gw);
+            pg6_load<CH>(ba, a, (it + 2) * TW + gw, lane);
+            dot(bb, (it + 1) * TW + gw);
+            pg6_load<CH>(bb, a, (it + 3) * TW + gw, lane);
+        }
+        dot(ba, it * TW + gw);
+        if (it + 1 < nit) {
+            dot(bb, (it + 1) * TW + gw);
+        }
+    } else {
+        // one buffer: the next row's loads after the current row is
+        // reduced (N = 4096 rows over 4096 waves: one row each); the
+        // activation operands one column at a time from LDS
+        for (int it = 0;;) {
+            float acc[1][NC];
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                acc[0][c] = 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < CH; u++) {
+                const bool ok = lane + 64 * u < units;
+                const int  un = ok ? lane + 64 * u : 0;
+                int4_t     q[4];
+                int        sc[4];
+                float      dw;
+                pg6_decode<CH>(ba, u, un, ok, q, sc, dw);
+                const int sb = un >> 2, h = (un >> 1) & 1, l0 = (un & 1) * 16;
+                const int eb = sb * 256 + h * 128 + l0;
+                const int g0 = sb * 16 + h * 8 + (l0 >> 4);
+#pragma unroll
+                for (int c = 0; c < NC; c++) {
+                    int4_t xv[4];
+                    int    bs[4];
+#pragma unroll
+                    for (int t = 0; t < 4; t++) {
+                        xv[t] = *(const int4_t *) &s_q[c * MAXK + q8k_swz(eb + 32 * t)];
+                        bs[t] = s_bs[c * (MAXK / 16) + g0 + 2 * t];
+                    }
+                    pg6_col<NC>(q, sc, dw, xv, bs, s_d[c * (MAXK / 256) + sb], acc[0][c]);
+                    __builtin_amdgcn_sched_barrier(0);  // bounds the LDS operands in flight (registers)
+                }
+            }
+            store_rows<NC, 1>(acc, lane, it * TW + gw, a.N, a.y, a.ldy, a.res, a.ldr);
+            if (++it >= nit) {
+                break;
+            }
+            pg6_load<CH>(ba, a, it * TW + gw, lane);
         }
     }
 }
@@ -1059,11 +1348,18 @@ __global__ __launch_bounds__(256) void k_gemv_bf16(const uint16_t * __restrict__
 static int gemv_wide(const uint8_t * W, int64_t N, int64_t K, int64_t rs, const ActPtrs & x, int64_t M, float * y,
                      int64_t ldy, hipStream_t stream, const float * r, int64_t ldr);
 
+static bool gemv_q6_pro_ok(int64_t K, int64_t M, int64_t rs, const void * W);
+static int  gemv_q6_pro(const void * W, int64_t N, int64_t K, int64_t rs, const ActPtrs & x, int64_t M, float * y,
+                        int64_t ldy, hipStream_t stream, const float * r, int64_t ldr);
+
 int gemv_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const ActPtrs & x, int64_t M, float * y,
            int64_t ldy, hipStream_t stream, const float * r, int64_t ldr) {
     if (!gemv_supported(wtype, N, K, rs, W) || M < 1 || ldy < N) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "gemv: type %d N=%lld K=%lld M=%lld rs=%lld not supported", wtype,
                          (long long) N, (long long) K, (long long) M, (long long) rs);
+    }
+    if (wtype == TYPE_Q6_K && gemv_q6_pro_ok(K, M, rs, W) && getenv("GGML_MI355X_DISABLE_Q6_PRO") == nullptr) {
+        return gemv_q6_pro(W, N, K, rs, x, M, y, ldy, stream, r, ldr);
     }
     const uint8_t * wb = (const uint8_t *) W;
     if (wtype == TYPE_Q8_0 && M > 8 && M <= 16 && K <= 8192 && K % 32 == 0) {
@@ -1204,7 +1500,48 @@ static int gemv_wide(const uint8_t * W, int64_t N, int64_t K, int64_t rs, const 
     }
 }
 
-template <int PRO> static int dispatch_pro(const PgArgs & a, int64_t M, hipStream_t stream, const char * what) {
+template <int NC, int CH, int PRO>
+static int launch_pro6(PgArgs a, Pg6Act xa, hipStream_t stream, const char * what) {
+    const int64_t need = (a.N + PG_WAVES - 1) / PG_WAVES;
+    const int64_t nit  = (need + pg_cus() - 1) / pg_cus();
+    const int64_t wgs  = (need + nit - 1) / nit;
+    if (nit > 0x7fffffff) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "%s: N=%lld too large", what, (long long) a.N);
+    }
+    a.nit     = (int) nit;
+    auto kern = k_gemv_q6_K_pro<NC, CH, PRO>;
+    hipLaunchKernelGGL(kern, dim3((unsigned) wgs), dim3(64 * PG_WAVES), 0, stream, a, xa);
+    return check_launch(what);
+}
+
+// Q6_K GEMV on quantised activations (M <= 2) through the persistent kernel:
+// the Q8_K rows copied into LDS once per workgroup instead of re-read per wave
+static bool gemv_q6_pro_ok(int64_t K, int64_t M, int64_t rs, const void * W) {
+    return M >= 1 && M <= 2 && K % 2048 == 0 && K <= 12288 && rs % 16 == 0 && ((uintptr_t) W) % 16 == 0;
+}
+
+static int gemv_q6_pro(const void * W, int64_t N, int64_t K, int64_t rs, const ActPtrs & x, int64_t M, float * y,
+                       int64_t ldy, hipStream_t stream, const float * r, int64_t ldr) {
+    const PgArgs a{ (const uint8_t *) W, N, (int) K, rs, nullptr, 0, nullptr, 0, nullptr, 0.0f, nullptr, y, ldy, r,
+                    ldr, 1 };
+    const Pg6Act xa{ x.qs, x.d, x.bs };
+    const char * what = "gemv q6_K";
+    if (K <= 4096) {
+        return M == 1 ? launch_pro6<1, 1, PRO_NONE>(a, xa, stream, what)
+                      : launch_pro6<2, 1, PRO_NONE>(a, xa, stream, what);
+    }
+    return M == 1 ? launch_pro6<1, 3, PRO_NONE>(a, xa, stream, what) : launch_pro6<2, 3, PRO_NONE>(a, xa, stream, what);
+}
+
+template <int PRO>
+static int dispatch_pro(int type, const PgArgs & a, int64_t M, hipStream_t stream, const char * what) {
+    if (type == TYPE_Q6_K) {
+        const Pg6Act xa{};
+        if (a.K <= 4096) {
+            return M == 1 ? launch_pro6<1, 1, PRO>(a, xa, stream, what) : launch_pro6<2, 1, PRO>(a, xa, stream, what);
+        }
+        return set_error(MMHIP_ERR_UNSUPPORTED, "%s: K=%d", what, a.K);
+    }
     if (a.K <= 4096) {
         return M == 1 ? launch_pro<1, 4, PRO>(a, stream, what) : launch_pro<2, 4, PRO>(a, stream, what);
     }
@@ -1215,10 +1552,19 @@ template <int PRO> static int dispatch_pro(const PgArgs & a, int64_t M, hipStrea
 }
 
 // M <= 2 (two activation columns in registers); the norm over K <= 4096 (the
-// model widths), the SwiGLU over K <= 12288 (the FFN widths)
+// model widths), the SwiGLU over K <= 12288 (the FFN widths).  Q6_K rows are
+// read with 16-byte loads: K % 2048 == 0 makes the packed row 16-byte sized.
 static bool pro_supported(int pro, int type, int64_t N, int64_t K, int64_t M) {
-    return type == TYPE_Q8_0 && N > 0 && M >= 1 && M <= 2 && K >= 256 && K <= (pro == PRO_NORM ? 4096 : 12288) &&
-           K % 256 == 0;
+    // Q6_K SwiGLU prologue at K <= 4096 only: over the FFN's 12288 the
+    // gate / up reads of every workgroup (196 KB each at M = 2) cost more
+    // than the separate SwiGLU + quantisation pass they replace
+    return (type == TYPE_Q8_0 || (type == TYPE_Q6_K && K % 2048 == 0 && (pro == PRO_NORM || K <= 4096))) && N > 0 &&
+           M >= 1 && M <= 2 && K >= 256 && K <= (pro == PRO_NORM ? 4096 : 12288) && K % 256 == 0;
+}
+
+// the 16-byte row loads of the persistent Q6_K GEMV
+static bool pro_rows_ok(int type, int64_t rs, const void * W) {
+    return type != TYPE_Q6_K || (rs % 16 == 0 && ((uintptr_t) W) % 16 == 0);
 }
 }  // namespace mmhip
 
@@ -1236,13 +1582,13 @@ extern "C" int mmhip_rms_norm_mul_mat(int type, const void * W, int64_t N, int64
                          (long long) K, (long long) M);
     }
     if (!W || !x || !norm_w || !y || ldx < K || ldy < N || (res && ldr < N) ||
-        !gemv_supported(type, N, K, w_row_stride, W) ||
+        !gemv_supported(type, N, K, w_row_stride, W) || !pro_rows_ok(type, w_row_stride, W) ||
         ((uintptr_t) x | (uintptr_t) norm_w | (uintptr_t) xn_out) % 16 != 0 || (ldx % 4) != 0) {
         return set_error(MMHIP_ERR_INVALID, "rms_norm_mul_mat: bad arguments / alignment");
     }
     const PgArgs a{ (const uint8_t *) W, N, (int) K, w_row_stride, x, ldx, nullptr, 0, norm_w, eps, xn_out, y, ldy,
                     res, ldr, 1 };
-    return dispatch_pro<PRO_NORM>(a, M, (hipStream_t) stream, "rms_norm_mul_mat");
+    return dispatch_pro<PRO_NORM>(type, a, M, (hipStream_t) stream, "rms_norm_mul_mat");
 }
 
 extern "C" int mmhip_swiglu_mul_mat_supported(int type, int64_t N, int64_t K, int64_t M) {
@@ -1259,13 +1605,13 @@ extern "C" int mmhip_swiglu_mul_mat(int type, const void * W, int64_t N, int64_t
                          (long long) K, (long long) M);
     }
     if (!W || !g || !u || !y || ldg < K || ldu < K || ldy < N || (res && ldr < N) ||
-        !gemv_supported(type, N, K, w_row_stride, W) ||
+        !gemv_supported(type, N, K, w_row_stride, W) || !pro_rows_ok(type, w_row_stride, W) ||
         ((uintptr_t) g | (uintptr_t) u | (uintptr_t) h_out) % 16 != 0 || (ldg % 4) != 0 || (ldu % 4) != 0) {
         return set_error(MMHIP_ERR_INVALID, "swiglu_mul_mat: bad arguments / alignment");
     }
     const PgArgs a{ (const uint8_t *) W, N, (int) K, w_row_stride, g, ldg, u, ldu, nullptr, 0.0f, h_out, y, ldy,
                     res, ldr, 1 };
-    return dispatch_pro<PRO_SWIGLU>(a, M, (hipStream_t) stream, "swiglu_mul_mat");
+    return dispatch_pro<PRO_SWIGLU>(type, a, M, (hipStream_t) stream, "swiglu_mul_mat");
 }
 
 extern "C" int mmhip_rms_norm_mul_mat_glu_supported(int type, int64_t N, int64_t K, int64_t M) {

@@ -272,4 +272,77 @@ __host__ __device__ constexpr int64_t row_bytes(int type, int64_t k) {
          : 0;
 }
 
+// Activation quantisation of a 256-element chunk held in registers, lane l
+// owning elements 4l .. 4l+3, with exactly the arithmetic of k_quant.hip
+// (ggml quantize_row_q8_0_ref / quantize_row_q8_K_ref):
+//   Q8_0: eight blocks of 32 (8 lanes each); d = amax/127 rounded to f16,
+//         q = roundf(x / d)
+//   Q8_K: one super-block; the first element of largest |x| gives
+//         iscale = -127 / x_max, q = min(127, nearest-even(iscale * x)),
+//         d = 1 / iscale, plus the sixteen 16-element sums of q.
+// qs, d, bs point at the chunk's first element / scale / sum.
+
+// The lane's four values (the caller stores them); the scales and sums are
+// stored here.
+__device__ __forceinline__ char4 quant_chunk256_q(const float (&v)[4], int lane, int qtype, float * __restrict__ d,
+                                                  int16_t * __restrict__ bs) {
+#pragma clang fp contract(off)
+    char4 q4;
+    if (qtype == TYPE_Q8_0) {
+        const float a = group8_max(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+        const float dd = a / 127.0f;
+        const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+        q4.x           = (signed char) roundf(v[0] * id);
+        q4.y           = (signed char) roundf(v[1] * id);
+        q4.z           = (signed char) roundf(v[2] * id);
+        q4.w           = (signed char) roundf(v[3] * id);
+        if ((lane & 7) == 0) {
+            d[lane >> 3] = h2f(f2h(dd));
+        }
+    } else {
+        float a = 0.0f, vm = 0.0f;
+        int   ix = 4 * lane;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float t = fabsf(v[k]);
+            if (t > a) {
+                a  = t;
+                vm = v[k];
+                ix = 4 * lane + k;
+            }
+        }
+        wave_argmax_abs(a, vm, ix);
+        int   qv[4] = { 0, 0, 0, 0 };
+        float dd    = 0.0f;
+        if (a != 0.0f) {
+            const float iscale = -127.0f / vm;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int q = (int) rintf(iscale * v[k]);
+                qv[k]       = q > 127 ? 127 : q;
+            }
+            dd = 1.0f / iscale;
+        }
+        q4.x   = (signed char) qv[0];
+        q4.y   = (signed char) qv[1];
+        q4.z   = (signed char) qv[2];
+        q4.w   = (signed char) qv[3];
+        int sb = qv[0] + qv[1] + qv[2] + qv[3];
+        sb += dpp_i<DPP_XOR1>(sb);
+        sb += dpp_i<DPP_XOR2>(sb);
+        if ((lane & 3) == 0) {
+            bs[lane >> 2] = (int16_t) sb;
+        }
+        if (lane == 0) {
+            d[0] = dd;
+        }
+    }
+    return q4;
+}
+
+__device__ __forceinline__ void quant_chunk256(const float (&v)[4], int lane, int qtype, int8_t * __restrict__ qs,
+                                               float * __restrict__ d, int16_t * __restrict__ bs) {
+    *(char4 *) (qs + 4 * lane) = quant_chunk256_q(v, lane, qtype, d, bs);
+}
+
 }  // namespace mmhip

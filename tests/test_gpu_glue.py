@@ -409,32 +409,37 @@ def test_flash_attn_head_rejects_prefill_shapes(mm):
     assert L.mmhip_flash_attn_ext_head_supported(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(kv)) == 0
 
 
-@pytest.mark.parametrize("M,K,N,ldx", [(2, 4096, 6144, 4096), (1, 1024, 300, 1088), (2, 2048, 9000, 2048),
-                                       (2, 4096, 30000, 4096), (1, 256, 77, 320), (2, 1024, 70001, 1024)])
-def test_rms_norm_mul_mat_equals_two_pass(mm, pkg, M, K, N, ldx):
+@pytest.mark.parametrize("wt,M,K,N,ldx", [(8, 2, 4096, 6144, 4096), (8, 1, 1024, 300, 1088), (8, 2, 2048, 9000, 2048),
+                                          (8, 2, 4096, 30000, 4096), (8, 1, 256, 77, 320), (8, 2, 1024, 70001, 1024),
+                                          (14, 2, 4096, 6144, 4096), (14, 1, 2048, 300, 2112),
+                                          (14, 2, 4096, 30000, 4096), (14, 2, 2048, 9001, 2048),
+                                          (14, 2, 4096, 24576, 4096)])
+def test_rms_norm_mul_mat_equals_two_pass(mm, pkg, wt, M, K, N, ldx):
     """GEMV with the RMS norm + quantisation in its prologue is bit-identical
     to rms_norm_quant then mul_mat_q (and mul_mat_q_add with a residual);
-    N from one to eight row iterations of the persistent grid, odd tails."""
+    N from one to eight row iterations of the persistent grid, odd tails.
+    Q8_0 weights (Q8_0 activation blocks) and Q6_K weights (Q8_K
+    super-blocks, the persistent Q6_K kernel)."""
     L = mm.load()
-    Wq = mm.QuantWeight.from_gguf(8, pkg.synth.gguf_blocks_np(8, N, K, 5), N, K)
+    Wq = mm.QuantWeight.from_gguf(wt, pkg.synth.gguf_blocks_np(wt, N, K, 5), N, K)
     rng = np.random.default_rng(26)
     xb = torch.from_numpy((rng.standard_normal((M, ldx)) * 3).astype(np.float32)).cuda()
     x = xb[:, :K]
     w = torch.from_numpy((1 + 0.05 * rng.standard_normal(K)).astype(np.float32)).cuda()
     r = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float32)).cuda()
-    assert L.mmhip_rms_norm_mul_mat_supported(8, N, K, M) == 1
+    assert L.mmhip_rms_norm_mul_mat_supported(wt, N, K, M) == 1
     xn = torch.empty((M, K), dtype=torch.float32, device="cuda")
-    xq = torch.zeros(L.mmhip_act_bytes(8, K, M), dtype=torch.uint8, device="cuda")
-    assert L.mmhip_rms_norm_quant(ctypes.byref(mm.view_of(x)), ctypes.byref(mm.view_of(w)), 1e-6, ptr(xn), 8,
+    xq = torch.zeros(L.mmhip_act_bytes(wt, K, M), dtype=torch.uint8, device="cuda")
+    assert L.mmhip_rms_norm_quant(ctypes.byref(mm.view_of(x)), ctypes.byref(mm.view_of(w)), 1e-6, ptr(xn), wt,
                                   ptr(xq), st()) == 0
     y1 = torch.empty((M, N), dtype=torch.float32, device="cuda")
-    assert L.mmhip_mul_mat_q(8, ptr(Wq.data), N, K, Wq.row_bytes, ptr(xq), M, ptr(y1), N, st()) == 0
+    assert L.mmhip_mul_mat_q(wt, ptr(Wq.data), N, K, Wq.row_bytes, ptr(xq), M, ptr(y1), N, st()) == 0
     y2 = torch.full((M, N), float("nan"), device="cuda")
     xn2 = torch.full((M, K), float("nan"), device="cuda")
-    assert L.mmhip_rms_norm_mul_mat(8, ptr(Wq.data), N, K, Wq.row_bytes, ptr(x), ldx, M, ptr(w), 1e-6, ptr(xn2),
+    assert L.mmhip_rms_norm_mul_mat(wt, ptr(Wq.data), N, K, Wq.row_bytes, ptr(x), ldx, M, ptr(w), 1e-6, ptr(xn2),
                                     None, 0, ptr(y2), N, st()) == 0
     y3 = torch.empty_like(y1)
-    assert L.mmhip_rms_norm_mul_mat(8, ptr(Wq.data), N, K, Wq.row_bytes, ptr(x), ldx, M, ptr(w), 1e-6, None,
+    assert L.mmhip_rms_norm_mul_mat(wt, ptr(Wq.data), N, K, Wq.row_bytes, ptr(x), ldx, M, ptr(w), 1e-6, None,
                                     ptr(r), N, ptr(y3), N, st()) == 0
     torch.cuda.synchronize()
     assert torch.equal(y2, y1)
@@ -448,6 +453,7 @@ def test_rms_norm_mul_mat_rejects_unsupported(mm):
     assert L.mmhip_rms_norm_mul_mat_supported(8, 4096, 4352, 2) == 0   # K > 4096
     assert L.mmhip_rms_norm_mul_mat_supported(8, 4096, 4096, 3) == 0   # M > 2
     assert L.mmhip_rms_norm_mul_mat_supported(12, 4096, 4096, 2) == 0  # Q4_K weights
+    assert L.mmhip_rms_norm_mul_mat_supported(14, 4096, 1024, 2) == 0  # Q6_K rows not 16-byte sized
     assert L.mmhip_rms_norm_mul_mat_supported(8, 4096, 1000, 2) == 0   # K % 256
     dummy = torch.zeros(16, dtype=torch.float32, device="cuda")
     rc = L.mmhip_rms_norm_mul_mat(8, ptr(dummy), 4096, 4352, 4624, ptr(dummy), 4352, 2, ptr(dummy), 1e-6, None,
@@ -455,15 +461,19 @@ def test_rms_norm_mul_mat_rejects_unsupported(mm):
     assert rc != 0
 
 
-@pytest.mark.parametrize("M,F,N,mode", [(2, 12288, 4096, "fused"), (1, 3072, 1000, "split"), (2, 2048, 9001, "swapped"),
-                                        (2, 12288, 5000, "fused"), (1, 256, 77, "fused")])
-def test_swiglu_mul_mat_equals_two_pass(mm, pkg, M, F, N, mode):
+@pytest.mark.parametrize("wt,M,F,N,mode", [(8, 2, 12288, 4096, "fused"), (8, 1, 3072, 1000, "split"),
+                                           (8, 2, 2048, 9001, "swapped"), (8, 2, 12288, 5000, "fused"),
+                                           (8, 1, 256, 77, "fused"), (14, 2, 4096, 4096, "fused"),
+                                           (14, 1, 4096, 1000, "split"), (14, 2, 2048, 9001, "swapped"),
+                                           (14, 2, 4096, 30000, "fused")])
+def test_swiglu_mul_mat_equals_two_pass(mm, pkg, wt, M, F, N, mode):
     """GEMV with the SwiGLU + quantisation in its prologue is bit-identical to
     swiglu_quant then mul_mat_q / mul_mat_q_add: fused gate|up rows (also
     swapped) and split gate / up tensors; one and two row iterations of the
-    persistent grid for the long (K = 12288) rows."""
+    persistent grid for the long (K = 12288) rows.  Q8_0 and Q6_K weights
+    (Q6_K up to K = 4096)."""
     L = mm.load()
-    Wq = mm.QuantWeight.from_gguf(8, pkg.synth.gguf_blocks_np(8, N, F, 6), N, F)
+    Wq = mm.QuantWeight.from_gguf(wt, pkg.synth.gguf_blocks_np(wt, N, F, 6), N, F)
     rng = np.random.default_rng(27)
     a = torch.from_numpy((rng.standard_normal((M, 2 * F)) * 2).astype(np.float32)).cuda()
     r = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float32)).cuda()
@@ -478,19 +488,19 @@ def test_swiglu_mul_mat_equals_two_pass(mm, pkg, M, F, N, mode):
         first, second = a[:, :F], a[:, F:]
         gp, up = (second, first) if swapped else (first, second)
         ldg = ldu = 2 * F
-    assert L.mmhip_swiglu_mul_mat_supported(8, N, F, M) == 1
+    assert L.mmhip_swiglu_mul_mat_supported(wt, N, F, M) == 1
     h = torch.empty((M, F), dtype=torch.float32, device="cuda")
-    xq = torch.zeros(L.mmhip_act_bytes(8, F, M), dtype=torch.uint8, device="cuda")
-    assert L.mmhip_swiglu_quant(a_view, b_view, swapped, ptr(h), 8, ptr(xq), st()) == 0
+    xq = torch.zeros(L.mmhip_act_bytes(wt, F, M), dtype=torch.uint8, device="cuda")
+    assert L.mmhip_swiglu_quant(a_view, b_view, swapped, ptr(h), wt, ptr(xq), st()) == 0
     y1 = torch.empty((M, N), dtype=torch.float32, device="cuda")
-    assert L.mmhip_mul_mat_q(8, ptr(Wq.data), N, F, Wq.row_bytes, ptr(xq), M, ptr(y1), N, st()) == 0
+    assert L.mmhip_mul_mat_q(wt, ptr(Wq.data), N, F, Wq.row_bytes, ptr(xq), M, ptr(y1), N, st()) == 0
     y2 = torch.full((M, N), float("nan"), device="cuda")
     h2 = torch.full((M, F), float("nan"), device="cuda")
-    assert L.mmhip_swiglu_mul_mat(8, ptr(Wq.data), N, F, Wq.row_bytes, ptr(gp), ldg, ptr(up), ldu, M, ptr(h2), None, 0,
-                                  ptr(y2), N, st()) == 0
+    assert L.mmhip_swiglu_mul_mat(wt, ptr(Wq.data), N, F, Wq.row_bytes, ptr(gp), ldg, ptr(up), ldu, M, ptr(h2), None,
+                                  0, ptr(y2), N, st()) == 0
     y3 = torch.empty_like(y1)
-    assert L.mmhip_swiglu_mul_mat(8, ptr(Wq.data), N, F, Wq.row_bytes, ptr(gp), ldg, ptr(up), ldu, M, None, ptr(r), N,
-                                  ptr(y3), N, st()) == 0
+    assert L.mmhip_swiglu_mul_mat(wt, ptr(Wq.data), N, F, Wq.row_bytes, ptr(gp), ldg, ptr(up), ldu, M, None, ptr(r),
+                                  N, ptr(y3), N, st()) == 0
     torch.cuda.synchronize()
     assert torch.equal(h2, h)
     assert torch.equal(y2, y1)
@@ -553,7 +563,10 @@ def test_swiglu_mul_mat_rejects_unsupported(mm):
     L = mm.load()
     assert L.mmhip_swiglu_mul_mat_supported(8, 4096, 12544, 2) == 0  # K > 12288
     assert L.mmhip_swiglu_mul_mat_supported(8, 4096, 12288, 3) == 0  # M > 2
-    assert L.mmhip_swiglu_mul_mat_supported(14, 4096, 12288, 2) == 0  # Q6_K weights
+    assert L.mmhip_swiglu_mul_mat_supported(12, 4096, 12288, 2) == 0  # Q4_K weights
+    assert L.mmhip_swiglu_mul_mat_supported(14, 4096, 4096, 2) == 1   # Q6_K weights
+    assert L.mmhip_swiglu_mul_mat_supported(14, 4096, 12288, 2) == 0  # Q6_K: the FFN width goes the two-pass way
+    assert L.mmhip_swiglu_mul_mat_supported(14, 4096, 3072, 2) == 0   # Q6_K rows not 16-byte sized
     assert L.mmhip_rms_norm_mul_mat_supported(8, 4096, 8192, 2) == 0  # the norm: K <= 4096
 
 

@@ -213,3 +213,37 @@ def test_mul_mat_bf16_rejects_and_backend(mm, pkg):
     assert L.mmhip_mul_mat_bf16(Q(W.cuda()), N, K, K, Q(x.cuda()), K, M, Q(y), N, None) == 0
     torch.cuda.synchronize()
     assert np.array_equal(yb, y.cpu().numpy())
+
+
+@pytest.mark.parametrize("N,K,M", [(4096, 12288, 2), (4096, 4096, 2), (1000, 8192, 1), (6144, 4096, 2),
+                                   (30000, 2048, 2), (77, 4096, 1)])
+def test_gemv_q6_K_persistent_equals_wave_kernel(mm, pkg, monkeypatch, N, K, M):
+    """Q6_K GEMV at 1-2 tokens through the persistent kernel (Q8_K rows in
+    LDS, 16-wave workgroups streaming rows) equals the one-wave-per-row-pair
+    kernel (GGML_MI355X_DISABLE_Q6_PRO) bit for bit, with and without the
+    residual: each lane adds the same units in the same order and the sums
+    reduce by the same butterfly.  K = 8192 leaves a third of the lanes
+    without a third unit; N from a partial to several row iterations."""
+    import ctypes
+    L = mm.load()
+    W = mm.QuantWeight.from_gguf(14, pkg.synth.gguf_blocks_np(14, N, K, 7), N, K)
+    x = torch.from_numpy(pkg.synth.normal_np((M, K), 8)).cuda()
+    r = torch.from_numpy(pkg.synth.normal_np((M, N), 9)).cuda()
+    xq = torch.zeros(L.mmhip_act_bytes(14, K, M), dtype=torch.uint8, device="cuda")
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    assert L.mmhip_quantize_act(14, p(x), K, K, M, p(xq), s) == 0
+    outs = []
+    for wave_kernel in (False, True):
+        if wave_kernel:
+            monkeypatch.setenv("GGML_MI355X_DISABLE_Q6_PRO", "1")
+        y = torch.full((M, N), float("nan"), device="cuda")
+        ya = torch.full((M, N), float("nan"), device="cuda")
+        assert L.mmhip_mul_mat_q(14, p(W.data), N, K, W.row_bytes, p(xq), M, p(y), N, s) == 0
+        assert L.mmhip_mul_mat_q_add(14, p(W.data), N, K, W.row_bytes, p(xq), M, p(r), N, p(ya), N, s) == 0
+        torch.cuda.synchronize()
+        outs.append((y, ya))
+    monkeypatch.delenv("GGML_MI355X_DISABLE_Q6_PRO")
+    assert torch.equal(outs[0][0], outs[1][0])
+    assert torch.equal(outs[0][1], outs[1][1])
+    assert torch.isfinite(outs[0][0]).all()
