@@ -13,6 +13,8 @@
 // k-contiguous rows in LDS, the operand order of the MFMA A (tokens) and B
 // (weight rows) inputs.  The output accumulator layout gives each lane one
 // weight row, so stores of 32 lanes are 128 contiguous bytes of a y row.
+#include <cstdlib>
+
 #include "mmhip_device.h"
 #include "mmhip_internal.h"
 
@@ -176,6 +178,13 @@ __device__ __forceinline__ int swz(int r, int c) {
     return r * BK + 8 * (c ^ (r & 7));
 }
 
+// Rows of 32 halves (the f16-weight ring's K step): chunk c of row r at
+// c ^ ((r >> 2) & 3), so the 16 rows one 16-lane operand read touches fall in
+// 16 different bank groups.
+__device__ __forceinline__ int swz32(int r, int c) {
+    return r * 32 + 8 * (c ^ ((r >> 2) & 3));
+}
+
 // NW waves; tile BT x BT with BT = 32 * NW tokens x weight rows.  Waves in a
 // WM x (NW/WM) grid, each computing MB x NB blocks of 32 x 32.  Per 64-wide K
 // step: the activation tile (f16, from the converted copy) is DMA'd into one
@@ -192,7 +201,15 @@ __device__ __forceinline__ int swz(int r, int c) {
 // same lane and register.  The epilogue adds both biases, forms
 // silu(g) * v with k_swiglu's arithmetic and stores the SwiGLU rows [M, F]
 // in f32 and / or f16 (the next GEMM's activation format).
-template <int WT, int NW, int WM, int BK, int BM, bool GLU>
+//
+// WH: the weights come as f16 rows [N][K] (dequantised once by k_w_to_f16
+// with the same arithmetic), so both tiles are DMA'd: a ring of GM_NS stages
+// of 32-wide K steps, each stage's DMA issued GM_NS - 1 steps ahead, one
+// barrier per step.  The MFMAs run in the same k order, so the sums are the
+// register-staged kernel's to the bit.
+constexpr int GM_NS = 4;
+
+template <int WT, int NW, int WM, int BK, int BM, bool GLU, bool WH = false>
 __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__ W, int64_t N, int64_t K, int64_t rs,
                                                      const _Float16 * __restrict__ xh, int64_t M,
                                                      const float * __restrict__ bias, const float * res, int64_t ldr,
@@ -205,11 +222,12 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
     constexpr int MB  = BM / WM / 32;
     constexpr int NB  = BT / WN / 32;
     constexpr int CPR = BK / 8;        // 16-byte chunks per tile row
-    constexpr int SUB = BK / GM_BK;    // 64-wide weight sub-steps per K step
+    constexpr int SUB = BK / GM_BK > 0 ? BK / GM_BK : 1;  // 64-wide weight sub-steps per K step (register path)
     constexpr int XI  = BM * CPR / T;  // DMA instructions per thread per stage
     constexpr int TIX = BM * BK;       // halves per activation tile
     constexpr int TIL = BT * BK;       // halves per weight tile
     static_assert(MB >= 1 && XI >= 1, "tile shape");
+    static_assert(!WH || BK == 32, "the f16-weight ring steps 32 columns");
     static_assert(!GLU || NB == 2, "GLU tiles pair one value and one gate block per wave");
     extern __shared__ __attribute__((aligned(16))) _Float16 g_lds[];
     _Float16 * sX = g_lds;            // 2 stages
@@ -264,18 +282,21 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
 
     const int       srow  = tid >> 1;
     const int       shalf = tid & 1;
-    bool            w_ok;
-    int64_t         wsel;  // weight row staged by this thread
-    if constexpr (GLU) {
-        // local row (wave block, value / gate, 32-row offset) -> SwiGLU column j
-        const int     wq = srow / (BT / WN), blk = (srow % (BT / WN)) / 32;
-        const int64_t j  = n0 / 2 + wq * 32 + (srow % 32);
-        w_ok             = j < glu.F;
-        wsel             = (blk == 1) != (glu.swapped != 0) ? glu.F + j : j;
-    } else {
-        w_ok = n0 + srow < N;
-        wsel = n0 + srow;
-    }
+    // the weight row of local tile row r (valid: inside the matrix)
+    auto wrow_of = [&](int r, bool & valid) -> int64_t {
+        if constexpr (GLU) {
+            // local row (wave block, value / gate, 32-row offset) -> SwiGLU column j
+            const int     wq = r / (BT / WN), blk = (r % (BT / WN)) / 32;
+            const int64_t j  = n0 / 2 + wq * 32 + (r % 32);
+            valid            = j < glu.F;
+            return (blk == 1) != (glu.swapped != 0) ? glu.F + j : j;
+        } else {
+            valid = n0 + r < N;
+            return n0 + r;
+        }
+    };
+    bool          w_ok;
+    const int64_t wsel = wrow_of(srow, w_ok);  // weight row staged by this thread
     const uint8_t * wrow = W + (w_ok ? wsel : 0) * rs;
     WRaw            wr[SUB];
     auto            wload = [&](int k0) {
@@ -334,6 +355,91 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
 
     const int nk = (int) (K / BK / spl.n);  // K steps of this part
     const int kb = kpart * nk * BK;         // its first column
+    if constexpr (WH) {
+        // stage s: the activation tile then the weight tile; rows outside
+        // the matrices read a valid row and are never stored
+        constexpr int STG = TIX + TIL;
+        constexpr int WI  = BT * CPR / T;  // weight DMA instructions per thread per stage
+        constexpr int PER = XI + WI;
+        static_assert(WI >= 1, "tile shape");
+        const _Float16 * wsrc[WI];
+#pragma unroll
+        for (int i = 0; i < WI; i++) {
+            const int     c = (wave * WI + i) * 64 + lane, r = c / CPR;
+            bool          ok;
+            const int64_t n = wrow_of(r, ok);
+            wsrc[i]         = (const _Float16 *) W + (ok ? n : 0) * K + 8 * ((c % CPR) ^ ((r >> 2) & 3));
+        }
+        const _Float16 * xs[XI];
+#pragma unroll
+        for (int i = 0; i < XI; i++) {
+            const int     c = (wave * XI + i) * 64 + lane, r = c / CPR;
+            const int64_t m = m0 + r < M ? m0 + r : M - 1;
+            xs[i]           = xh + m * K + 8 * ((c % CPR) ^ ((r >> 2) & 3));
+        }
+        auto dma2 = [&](int st, int k0) {
+#pragma unroll
+            for (int i = 0; i < XI; i++) {
+                dma16(xs[i] + k0, lds_x + 2u * (uint32_t) (st * STG + (wave_s * XI + i) * 512));
+            }
+#pragma unroll
+            for (int i = 0; i < WI; i++) {
+                dma16(wsrc[i] + k0, lds_x + 2u * (uint32_t) (st * STG + TIX + (wave_s * WI + i) * 512));
+            }
+        };
+        auto compute2 = [&](int st) {
+            const _Float16 * bx = g_lds + st * STG;
+            const _Float16 * bw = bx + TIX;
+#pragma unroll
+            for (int kk = 0; kk < BK / 16; kk++) {
+                half8_t a[MB], b[NB];
+#pragma unroll
+                for (int i = 0; i < MB; i++) {
+                    a[i] = *(const half8_t *) &bx[swz32(wm * (BM / WM) + i * 32 + lq, 2 * kk + hh)];
+                }
+#pragma unroll
+                for (int j = 0; j < NB; j++) {
+                    b[j] = *(const half8_t *) &bw[swz32(wn * (BT / WN) + j * 32 + lq, 2 * kk + hh)];
+                }
+#pragma unroll
+                for (int i = 0; i < MB; i++) {
+#pragma unroll
+                    for (int j = 0; j < NB; j++) {
+                        acc[i][j] = gm_mfma(a[i], b[j], acc[i][j]);
+                    }
+                }
+            }
+        };
+#pragma unroll
+        for (int st = 0; st < GM_NS - 1; st++) {
+            if (st < nk) {
+                dma2(st, kb + st * BK);
+            }
+        }
+        // stage 0 in (the later stages may fly); every wait counts this
+        // thread's own DMA instructions, loads returning in issue order
+        if (nk >= GM_NS - 1) {
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"((GM_NS - 2) * PER) : "memory");
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        __syncthreads();
+        for (int ks = 0; ks < nk; ks++) {
+            const bool more = ks + GM_NS - 1 < nk;
+            if (more) {
+                dma2((ks + GM_NS - 1) % GM_NS, kb + (ks + GM_NS - 1) * BK);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            compute2(ks % GM_NS);
+            // step ks + 1's stage in before the barrier that publishes it
+            if (more) {
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"((GM_NS - 2) * PER) : "memory");
+            } else {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            }
+            __syncthreads();
+        }
+    } else {
     dma(0, kb);
     wload(kb);
     wstore(0, kb);
@@ -353,6 +459,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
         }
         __builtin_amdgcn_s_waitcnt(0);  // this thread's DMA and LDS writes
         __syncthreads();
+    }
     }
 
     // C[i = token][j = weight row]: lane holds row j = lq, tokens 8(r/4) + 4hh + r%4.
@@ -487,6 +594,48 @@ __global__ void k_x_to_f16(const float * __restrict__ x, int64_t ldx, int64_t K,
     }
 }
 
+// Weights -> f16 rows [N][K] (row stride K), the register-staged kernel's
+// dequantisation: thread (row, 64-wide K step, half) dequantises its 32
+// values exactly (f32, then f16) and writes them as four 16-byte chunks.
+template <int WT>
+__global__ __launch_bounds__(256) void k_w_to_f16(const uint8_t * __restrict__ W, int64_t N, int64_t K, int64_t rs,
+                                                   _Float16 * __restrict__ wh) {
+    const int64_t nsteps = K / GM_BK;
+    const int64_t t      = (int64_t) blockIdx.x * 256 + threadIdx.x;
+    if (t >= N * nsteps * 2) {
+        return;
+    }
+    const int       half = (int) (t & 1);
+    const int64_t   st   = (t >> 1) % nsteps;
+    const int64_t   row  = (t >> 1) / nsteps;
+    const uint8_t * wr   = W + row * rs;
+    const int       k0   = (int) (st * GM_BK);
+    WRaw            w;
+    w_load<WT>(w, wr, K, k0, half);
+    half8_t o[4];
+    int     ch[4];
+    w_dequant<WT>(w, wr, K, k0, half, o, ch);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        *(half8_t *) (wh + row * K + k0 + 8 * ch[j]) = o[j];
+    }
+}
+
+static int weights_to_f16(int wtype, const uint8_t * W, int64_t N, int64_t K, int64_t rs, _Float16 * wh,
+                          hipStream_t stream) {
+    const int64_t n  = N * (K / GM_BK) * 2;
+    const int64_t nb = (n + 255) / 256;
+    if (nb > 0x7fffffff) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat gemm: weight rows too large");
+    }
+    switch (wtype) {
+        case TYPE_Q8_0: hipLaunchKernelGGL(k_w_to_f16<TYPE_Q8_0>, dim3((unsigned) nb), dim3(256), 0, stream, W, N, K, rs, wh); break;
+        case TYPE_Q4_K: hipLaunchKernelGGL(k_w_to_f16<TYPE_Q4_K>, dim3((unsigned) nb), dim3(256), 0, stream, W, N, K, rs, wh); break;
+        default: hipLaunchKernelGGL(k_w_to_f16<TYPE_Q6_K>, dim3((unsigned) nb), dim3(256), 0, stream, W, N, K, rs, wh); break;
+    }
+    return check_launch("mul_mat gemm: weights to f16");
+}
+
 bool gemm_supported(int wtype, int64_t N, int64_t K, int64_t rs, const void * W, const float * x, int64_t ldx) {
     if (!(wtype == TYPE_Q8_0 || wtype == TYPE_Q4_K || wtype == TYPE_Q6_K) || N <= 0 || K % GM_BK != 0 ||
         rs < row_bytes(wtype, K)) {
@@ -503,7 +652,7 @@ size_t gemm_workspace(int64_t K, int64_t M) {
     return (size_t) M * (size_t) K * sizeof(_Float16);
 }
 
-template <int NW, int WM, int BK, int BM = 32 * NW>
+template <int NW, int WM, int BK, int BM = 32 * NW, bool WH = false>
 static int launch_gemm(int wtype, const uint8_t * W, int64_t N, int64_t K, int64_t rs, const _Float16 * xh, int64_t M,
                        const float * bias, const float * res, int64_t ldr, float * y, int64_t ldy, const GemmGlu & glu,
                        const GemmMulti & mul, const GemmSplit & spl, hipStream_t stream) {
@@ -514,7 +663,7 @@ static int launch_gemm(int wtype, const uint8_t * W, int64_t N, int64_t K, int64
     if (n > 0x7fffffff) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat gemm: too many tiles");
     }
-    const size_t lds = (size_t) 2 * (BM + BT) * BK * sizeof(_Float16);
+    const size_t lds = (size_t) (WH ? GM_NS : 2) * (BM + BT) * BK * sizeof(_Float16);
     auto         go  = [&](auto kern) -> int {
         if (lds > 64 * 1024 && !ensure_lds_limit((const void *) kern, lds)) {
             return set_error(MMHIP_ERR_HIP, "mul_mat gemm: cannot raise LDS limit to %zu", lds);
@@ -523,25 +672,53 @@ static int launch_gemm(int wtype, const uint8_t * W, int64_t N, int64_t K, int64
                            ldy, glu, mul, spl, n_nt, n);
         return check_launch("mul_mat gemm");
     };
-    if (glu.F > 0) {
-        switch (wtype) {
-            case TYPE_Q8_0: return go(k_gemm_q<TYPE_Q8_0, NW, WM, BK, BM, true>);
-            case TYPE_Q4_K: return go(k_gemm_q<TYPE_Q4_K, NW, WM, BK, BM, true>);
-            default: return go(k_gemm_q<TYPE_Q6_K, NW, WM, BK, BM, true>);
+    if constexpr (WH) {
+        // f16 weights: the block type plays no part
+        (void) wtype;
+        return glu.F > 0 ? go(k_gemm_q<TYPE_Q8_0, NW, WM, BK, BM, true, true>)
+                         : go(k_gemm_q<TYPE_Q8_0, NW, WM, BK, BM, false, true>);
+    } else {
+        if (glu.F > 0) {
+            switch (wtype) {
+                case TYPE_Q8_0: return go(k_gemm_q<TYPE_Q8_0, NW, WM, BK, BM, true>);
+                case TYPE_Q4_K: return go(k_gemm_q<TYPE_Q4_K, NW, WM, BK, BM, true>);
+                default: return go(k_gemm_q<TYPE_Q6_K, NW, WM, BK, BM, true>);
+            }
         }
-    }
-    switch (wtype) {
-        case TYPE_Q8_0: return go(k_gemm_q<TYPE_Q8_0, NW, WM, BK, BM, false>);
-        case TYPE_Q4_K: return go(k_gemm_q<TYPE_Q4_K, NW, WM, BK, BM, false>);
-        default: return go(k_gemm_q<TYPE_Q6_K, NW, WM, BK, BM, false>);
+        switch (wtype) {
+            case TYPE_Q8_0: return go(k_gemm_q<TYPE_Q8_0, NW, WM, BK, BM, false>);
+            case TYPE_Q4_K: return go(k_gemm_q<TYPE_Q4_K, NW, WM, BK, BM, false>);
+            default: return go(k_gemm_q<TYPE_Q6_K, NW, WM, BK, BM, false>);
+        }
     }
 }
 
 // Tile configuration by shape (activations already f16, rows of K).
 static int gemm_launch(int wtype, const uint8_t * wb, int64_t N, int64_t K, int64_t rs, const _Float16 * xh, int64_t M,
                        const float * bias, const float * res, int64_t ldr, float * y, int64_t ldy, const GemmGlu & glu,
-                       const GemmMulti & mul, const GemmSplit & spl, hipStream_t stream) {
+                       const GemmMulti & mul, const GemmSplit & spl, hipStream_t stream, bool wh = false) {
     const int64_t tiles256 = ((N + 255) / 256) * ((M + 255) / 256);
+    if (wh) {
+        // f16 weight rows (row stride K): the DMA ring on the same tile choice
+        if (spl.n > 1) {
+            int rc = launch_gemm<8, 2, 32, 256, true>(wtype, wb, N, K, K * 2, xh, M, nullptr, nullptr, 0, nullptr, N,
+                                                      glu, mul, spl, stream);
+            if (rc != MMHIP_OK) {
+                return rc;
+            }
+            const int64_t nt = M * (N / 4);
+            const int64_t nb = (nt + 255) / 256;
+            hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned) (nb < 16384 ? nb : 16384)), dim3(256), 0, stream,
+                               (const float *) spl.part, spl.n, M, N, bias, res, ldr, y, ldy);
+            return check_launch("mul_mat gemm: split-K reduce");
+        }
+        if (tiles256 >= 256 || (mul.n > 0 && tiles256 >= 128)) {
+            return launch_gemm<8, 2, 32, 256, true>(wtype, wb, N, K, K * 2, xh, M, bias, res, ldr, y, ldy, glu, mul,
+                                                    spl, stream);
+        }
+        return launch_gemm<4, 2, 32, 64, true>(wtype, wb, N, K, K * 2, xh, M, bias, res, ldr, y, ldy, glu, mul, spl,
+                                               stream);
+    }
     if (spl.n > 1) {
         // 256 x 256 tiles over K parts, then the ordered reduction with the ADDs
         const GemmSplit sp = spl;
@@ -578,6 +755,28 @@ int gemm_split(int64_t N, int64_t K, int64_t M) {
 size_t gemm_split_bytes(int64_t N, int64_t K, int64_t M) {
     const int s = gemm_split(N, K, M);
     return s > 1 ? (size_t) s * (size_t) M * (size_t) N * sizeof(float) : 0;
+}
+
+// Whether the weights go to f16 once before the GEMM.  In the register-staged
+// kernel every token tile dequantises the whole weight tile again, and that
+// VALU work, not the MFMAs, sets its pace; the f16 ring kernel runs 10-25 %
+// faster on the same shapes, which pays for the extra pass over the weights
+// (their bytes plus 2 per value) from about 1500 tokens on (measured: 8192
+// tokens x 6144 x 2048 Q4_K 270 -> 229 + 8 us; 1380 tokens x 16384 x 2048
+// Q8_0 147 -> 133 + 25 us).
+bool gemm_use_wh(int64_t N, int64_t K, int64_t M) {
+    (void) N;
+    (void) K;
+    return M >= 2048 && getenv("GGML_MI355X_DISABLE_GEMM_WH") == nullptr;
+}
+
+size_t gemm_wh_bytes(int64_t N, int64_t K, int64_t M) {
+    return gemm_use_wh(N, K, M) ? ((size_t) N * (size_t) K * sizeof(_Float16) + 255) / 256 * 256 : 0;
+}
+
+size_t gemm_q_workspace(int64_t N, int64_t K, int64_t M) {
+    const size_t xo = (gemm_workspace(K, M) + 255) / 256 * 256;
+    return xo + gemm_wh_bytes(N, K, M) + gemm_split_bytes(N, K, M);
 }
 
 int gemm_q_h(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const void * xh, int64_t M, float * y,
@@ -628,14 +827,26 @@ int gemm_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const fl
     const GemmGlu   none{};
     const GemmMulti single{};
     GemmSplit       spl;
-    const size_t    sb = gemm_split_bytes(N, K, M);
-    const size_t    xo = (need + 255) / 256 * 256;  // partial sums after the f16 copy
-    if (!glu && sb && ws_bytes >= xo + sb) {
+    // workspace: the f16 activations, [the f16 weights,] [the partial sums]
+    const size_t    xo  = (need + 255) / 256 * 256;
+    const size_t    whb = gemm_wh_bytes(N, K, M);
+    const bool      wh  = whb && ws_bytes >= xo + whb;
+    const size_t    so  = xo + (wh ? whb : 0);
+    const size_t    sb  = gemm_split_bytes(N, K, M);
+    if (!glu && sb && ws_bytes >= so + sb) {
         spl.n    = gemm_split(N, K, M);
-        spl.part = (float *) ((char *) ws + xo);
+        spl.part = (float *) ((char *) ws + so);
     }
-    return gemm_launch(wtype, (const uint8_t *) W, N, K, rs, xh, M, bias, res, ldr, y, ldy, glu ? *glu : none, single,
-                       spl, stream);
+    const uint8_t * wb = (const uint8_t *) W;
+    if (wh) {
+        _Float16 * whp = (_Float16 *) ((char *) ws + xo);
+        rc             = weights_to_f16(wtype, wb, N, K, rs, whp, stream);
+        if (rc != MMHIP_OK) {
+            return rc;
+        }
+        wb = (const uint8_t *) whp;
+    }
+    return gemm_launch(wtype, wb, N, K, rs, xh, M, bias, res, ldr, y, ldy, glu ? *glu : none, single, spl, stream, wh);
 }
 
 }  // namespace mmhip

@@ -75,8 +75,7 @@ extern "C" int mmhip_version(void) {
 
 extern "C" size_t mmhip_mul_mat_workspace(int type, int64_t N, int64_t K, int64_t M) {
     if (use_gemm(type, M)) {
-        const size_t sb = gemm_split_bytes(N, K, M);  // split-K partial sums after the f16 copy
-        return sb ? (gemm_workspace(K, M) + 255) / 256 * 256 + sb : gemm_workspace(K, M);
+        return gemm_q_workspace(N, K, M);
     }
     return act_layout(type, K, M).total;
 }

@@ -113,6 +113,11 @@ struct GemmSplit {
 // bytes of partial sums that takes.
 int    gemm_split(int64_t N, int64_t K, int64_t M);
 size_t gemm_split_bytes(int64_t N, int64_t K, int64_t M);
+// the f16 weight copy gemm_q makes first at large token counts (0: none), and
+// gemm_q's whole workspace: f16 activations, f16 weights, split-K partials
+bool   gemm_use_wh(int64_t N, int64_t K, int64_t M);
+size_t gemm_wh_bytes(int64_t N, int64_t K, int64_t M);
+size_t gemm_q_workspace(int64_t N, int64_t K, int64_t M);
 // The epilogue adds bias[n] (if given), then res[m * ldr + n] (if given).
 int    gemm_q(int wtype, const void * W, int64_t N, int64_t K, int64_t row_stride, const float * x, int64_t ldx,
               int64_t M, float * y, int64_t ldy, void * ws, size_t ws_bytes, hipStream_t stream,

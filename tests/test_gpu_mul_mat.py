@@ -247,3 +247,52 @@ def test_gemv_q6_K_persistent_equals_wave_kernel(mm, pkg, monkeypatch, N, K, M):
     assert torch.equal(outs[0][0], outs[1][0])
     assert torch.equal(outs[0][1], outs[1][1])
     assert torch.isfinite(outs[0][0]).all()
+
+
+@pytest.mark.parametrize("t,N,K,M,kind", [(12, 6144, 2048, 2048, "plain"), (8, 2048, 2048, 2100, "plain"),
+                                          (14, 3000, 2048, 2051, "bias_res"), (8, 2048, 8192, 2200, "bias_res"),
+                                          (12, 1024, 2048, 2077, "swiglu"), (8, 16384, 2048, 2048, "swiglu"),
+                                          (8, 512, 2048, 2049, "plain")])
+def test_gemm_f16_weight_copy_equals_register_path(mm, pkg, monkeypatch, t, N, K, M, kind):
+    """At 2048+ tokens the GEMM first writes the weights to f16 rows
+    (k_w_to_f16, the in-kernel dequantisation's arithmetic) and streams both
+    tiles by DMA through a 4-stage ring; the MFMAs run in the same k order, so
+    the output equals the register-staged kernel's (GGML_MI355X_DISABLE_GEMM_WH)
+    bit for bit: plain, with bias + residual (K = 8192 also takes split-K),
+    and with the SwiGLU epilogue; ragged N and M tails; 256 x 256 tiles and
+    (few tiles) 64 x 128 tiles."""
+    import ctypes
+
+    L = mm.load()
+    raw = pkg.synth.gguf_blocks_np(t, N, K, 5100 + t)
+    W = mm.QuantWeight.from_gguf(t, raw, N, K)
+    x = torch.from_numpy(pkg.synth.normal_np((M, K), 5200 + t)).cuda()
+    b = torch.randn(N, device="cuda")
+    r = torch.randn(M, N, device="cuda")
+    P = lambda a: ctypes.c_void_p(a.data_ptr()) if a is not None else None  # noqa: E731
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    outs = []
+    for reg in (False, True):
+        if reg:
+            monkeypatch.setenv("GGML_MI355X_DISABLE_GEMM_WH", "1")
+        need = L.mmhip_mul_mat_workspace(t, N, K, M)
+        ws = torch.empty(max(need, 256), dtype=torch.uint8, device="cuda")
+        if kind == "swiglu":
+            h = torch.full((M, N // 2), float("nan"), device="cuda")
+            hh = torch.zeros((M, N // 2), dtype=torch.float16, device="cuda")
+            rc = L.mmhip_mul_mat_bias_swiglu(t, P(W.data), N, K, W.row_bytes, P(x), K, M, P(b), 0, P(h), P(hh),
+                                             P(ws), need, st)
+            out = (h, hh)
+        else:
+            y = torch.full((M, N), float("nan"), device="cuda")
+            rc = L.mmhip_mul_mat_bias_add(t, P(W.data), N, K, W.row_bytes, P(x), K, M,
+                                          P(b) if kind == "bias_res" else None, P(r) if kind == "bias_res" else None,
+                                          N, P(y), N, P(ws), need, st)
+            out = (y,)
+        assert rc == 0, L.mmhip_last_error()
+        torch.cuda.synchronize()
+        outs.append(out)
+    monkeypatch.delenv("GGML_MI355X_DISABLE_GEMM_WH")
+    for a, c in zip(outs[0], outs[1]):
+        assert torch.equal(a, c)
+    assert torch.isfinite(outs[0][0]).all()
