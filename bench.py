@@ -585,10 +585,11 @@ def bench_gemm(args, torch, pkg):
         "value": round(flops / (ms * 1e-3) / 1e12, 2),
         "unit": "TFLOP/s",
         "ms_per_step": round(ms, 4),
-        "dtype": "f16 MFMA (Q4_K dequantised to f16), f32 accumulate",
+        "dtype": "f16 MFMA (Q4_K dequantised to f16 rows once per call), f32 accumulate",
         "config": {"workload": "Q4_K GEMM W[6144x2048] x[8192x2048] f32 -> f32"},
         "via_backend": backend,
-        "roofline": {"bound": "mfma", "kernel": "k_x_to_f16 + k_gemm_q<Q4_K> (one mul_mat call)", "achieved": round(tf, 2),
+        "roofline": {"bound": "mfma", "kernel": "k_x_to_f16 + k_w_to_f16<Q4_K> + k_gemm_q<f16 weights, 4-stage DMA ring> "
+                                               "(one mul_mat call)", "achieved": round(tf, 2),
                      "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
                      "avg_launch_us": round(avg_s * 1e6, 2), "min_launch_us": round(med_s * 1e6, 2),
                      "alg_flops_per_launch": flops, "traffic": profile_traffic("gemm_q4_k_6144x2048_m8192"),

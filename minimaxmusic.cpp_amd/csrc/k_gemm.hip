@@ -235,16 +235,32 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
 
     // consecutive work items (one XCD, one L2) share the operand that is
     // re-read most: the weight tile when there are more weight tiles than
-    // token tiles (m_fast), else the activation tile
+    // token tiles (m_fast: its token tiles run together), else the
+    // activation tiles, in groups of GM_GROUP token tiles with the token tile
+    // fastest, so that the workgroups running together on an XCD cover a
+    // block of GM_GROUP token tiles by several weight tiles and each weight
+    // tile is fetched once per group rather than once per token tile
     // split-K: work items (part, tile), the parts of one tile n_base apart
+    constexpr int GM_GROUP = 4;
     const int64_t n_base  = n_tiles / spl.n;
     const int64_t lin     = gm_xcd_remap(blockIdx.x, n_tiles);
     const int     kpart   = (int) (lin / n_base);
     const int64_t work    = lin % n_base;
     const int64_t n_mt    = n_base / n_ntiles;
     const bool    m_fast  = n_ntiles > n_mt;
-    const int64_t m0      = (m_fast ? work % n_mt : work / n_ntiles) * BM;
-    int64_t       n0      = (m_fast ? work / n_mt : work % n_ntiles) * BT;
+    int64_t       tm, tn;  // token tile, weight tile
+    if (m_fast) {
+        tm = work % n_mt;
+        tn = work / n_mt;
+    } else {
+        const int64_t gsz = (int64_t) GM_GROUP * n_ntiles;
+        const int64_t g   = work / gsz, r = work % gsz;
+        const int64_t gw  = min((int64_t) GM_GROUP, n_mt - g * GM_GROUP);
+        tm                = g * GM_GROUP + r % gw;
+        tn                = r / gw;
+    }
+    const int64_t m0 = tm * BM;
+    int64_t       n0 = tn * BT;
     if (mul.n > 0) {
         // several weight matrices: this tile's rows come from matrix n0 / Nper
         const int mi = (int) (n0 / mul.Nper);
@@ -673,10 +689,10 @@ static int launch_gemm(int wtype, const uint8_t * W, int64_t N, int64_t K, int64
         return check_launch("mul_mat gemm");
     };
     if constexpr (WH) {
-        // f16 weights: the block type plays no part
+        // f16 weight rows: the block type plays no part
         (void) wtype;
-        return glu.F > 0 ? go(k_gemm_q<TYPE_Q8_0, NW, WM, BK, BM, true, true>)
-                         : go(k_gemm_q<TYPE_Q8_0, NW, WM, BK, BM, false, true>);
+        return glu.F > 0 ? go(k_gemm_q<TYPE_F16, NW, WM, BK, BM, true, true>)
+                         : go(k_gemm_q<TYPE_F16, NW, WM, BK, BM, false, true>);
     } else {
         if (glu.F > 0) {
             switch (wtype) {
