@@ -535,27 +535,48 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
         return;
     }
     // Epilogue: the bias ADD, then the residual ADD, each rounded as its op.
+    // The loads of a 32 x 32 block all come before its stores: loads and
+    // stores share one completion counter, so a load issued behind stores
+    // would wait for those stores as well.  (In place, res == y: every
+    // element is read before this thread writes it, and no other thread
+    // touches it.)
+    const int64_t nl = n0 + wn * (BT / WN) + lq;  // this lane's column in weight block 0
+    float         bn[NB];
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+        bn[j] = bias && nl + 32 * j < N ? bias[nl + 32 * j] : 0.0f;
+    }
 #pragma unroll
     for (int i = 0; i < MB; i++) {
+        const int64_t mb = m0 + wm * (BM / WM) + i * 32 + 4 * hh;  // row of register 0
 #pragma unroll
         for (int j = 0; j < NB; j++) {
-            const int64_t n = n0 + wn * (BT / WN) + j * 32 + lq;
+            const int64_t n = nl + 32 * j;
             if (n >= N) {
                 continue;
             }
-            const float bn = bias ? bias[n] : 0.0f;
+            float v[16];
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int64_t m = m0 + wm * (BM / WM) + i * 32 + 8 * (r / 4) + 4 * hh + (r % 4);
+                v[r] = bias ? acc[i][j][r] + bn[j] : acc[i][j][r];
+            }
+            if (res) {
+                float rv[16];
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int64_t m = mb + 8 * (r / 4) + (r % 4);
+                    rv[r]           = m < M ? res[m * ldr + n] : 0.0f;
+                }
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    v[r] = rv[r] + v[r];
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int64_t m = mb + 8 * (r / 4) + (r % 4);
                 if (m < M) {
-                    float v = acc[i][j][r];
-                    if (bias) {
-                        v = v + bn;
-                    }
-                    if (res) {
-                        v = res[m * ldr + n] + v;
-                    }
-                    y[m * ldy + n] = v;
+                    y[m * ldy + n] = v[r];
                 }
             }
         }
