@@ -14,6 +14,7 @@
 // (weight rows) inputs.  The output accumulator layout gives each lane one
 // weight row, so stores of 32 lanes are 128 contiguous bytes of a y row.
 #include <cstdlib>
+#include <type_traits>
 
 #include "mmhip_device.h"
 #include "mmhip_internal.h"
@@ -479,6 +480,11 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
     }
 
     // C[i = token][j = weight row]: lane holds row j = lq, tokens 8(r/4) + 4hh + r%4.
+    // Each epilogue runs branch-free on whole tiles (all but the last row and
+    // column of tiles): at the joins of per-element bounds branches the
+    // compiler waits for every store in flight, one wait per element.
+    const int64_t mw     = m0 + wm * (BM / WM) + 4 * hh;  // token of register 0 in block i = 0
+    const bool    full_m = m0 + BM <= M;
     if constexpr (GLU) {
         const int64_t j = n0 / 2 + wn * 32 + lq;
         if (j >= glu.F) {
@@ -488,98 +494,137 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
         const int64_t rg = glu.swapped ? j : glu.F + j;  // gate row
         const float   bv = bias ? bias[rv] : 0.0f;
         const float   bg = bias ? bias[rg] : 0.0f;
+        // the bias in registers before any store: a use behind a store's
+        // bounds branch would otherwise wait for all stores in flight
+        __builtin_amdgcn_s_waitcnt(0);
+        auto go = [&](auto full_c) {
+            constexpr bool FULL = decltype(full_c)::value;
 #pragma unroll
-        for (int i = 0; i < MB; i++) {
+            for (int i = 0; i < MB; i++) {
+                float o[16];
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int64_t m = m0 + wm * (BM / WM) + i * 32 + 8 * (r / 4) + 4 * hh + (r % 4);
-                if (m < M) {
+                for (int r = 0; r < 16; r++) {
                     float v = acc[i][0][r], g = acc[i][1][r];
                     if (bias) {
                         v = v + bv;
                         g = g + bg;
                     }
                     const float silu = g / (1.0f + expf(-g));
-                    const float o    = silu * v;
-                    if (glu.h) {
-                        glu.h[m * glu.F + j] = o;
-                    }
-                    if (glu.hh) {
-                        glu.hh[m * glu.F + j] = (_Float16) o;
-                    }
-                }
-            }
-        }
-        return;
-    }
-    if (spl.n > 1) {
-        // partial sums of this K part; the reduce kernel adds the ADDs
-        float * pp = spl.part + (int64_t) kpart * M * N;
-#pragma unroll
-        for (int i = 0; i < MB; i++) {
-#pragma unroll
-            for (int j = 0; j < NB; j++) {
-                const int64_t n = n0 + wn * (BT / WN) + j * 32 + lq;
-                if (n >= N) {
-                    continue;
+                    o[r]             = silu * v;
                 }
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    const int64_t m = m0 + wm * (BM / WM) + i * 32 + 8 * (r / 4) + 4 * hh + (r % 4);
-                    if (m < M) {
-                        pp[m * N + n] = acc[i][j][r];
+                    const int64_t m = mw + i * 32 + 8 * (r / 4) + (r % 4);
+                    if (FULL || m < M) {
+                        if (glu.h) {
+                            glu.h[m * glu.F + j] = o[r];
+                        }
+                        if (glu.hh) {
+                            glu.hh[m * glu.F + j] = (_Float16) o[r];
+                        }
                     }
                 }
             }
+        };
+        if (full_m) {
+            go(std::integral_constant<bool, true>{});
+        } else {
+            go(std::integral_constant<bool, false>{});
+        }
+        return;
+    }
+    const int64_t nl   = n0 + wn * (BT / WN) + lq;  // this lane's column in weight block 0
+    const bool    full = full_m && n0 + BT <= N;
+    if (spl.n > 1) {
+        // partial sums of this K part; the reduce kernel adds the ADDs
+        float * pp = spl.part + (int64_t) kpart * M * N;
+        auto    go = [&](auto full_c) {
+            constexpr bool FULL = decltype(full_c)::value;
+#pragma unroll
+            for (int i = 0; i < MB; i++) {
+#pragma unroll
+                for (int j = 0; j < NB; j++) {
+                    const int64_t n = nl + 32 * j;
+                    if (!FULL && n >= N) {
+                        continue;
+                    }
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int64_t m = mw + i * 32 + 8 * (r / 4) + (r % 4);
+                        if (FULL || m < M) {
+                            pp[m * N + n] = acc[i][j][r];
+                        }
+                    }
+                }
+            }
+        };
+        if (full) {
+            go(std::integral_constant<bool, true>{});
+        } else {
+            go(std::integral_constant<bool, false>{});
         }
         return;
     }
     // Epilogue: the bias ADD, then the residual ADD, each rounded as its op.
-    // The loads of a 32 x 32 block all come before its stores: loads and
-    // stores share one completion counter, so a load issued behind stores
-    // would wait for those stores as well.  (In place, res == y: every
-    // element is read before this thread writes it, and no other thread
-    // touches it.)
-    const int64_t nl = n0 + wn * (BT / WN) + lq;  // this lane's column in weight block 0
-    float         bn[NB];
+    // The bias is loaded once per column, and each 32 x 32 block's residual
+    // values are loaded before the previous block's stores are issued (loads
+    // and stores share one completion counter, so a load issued behind
+    // stores would wait for them too).  In place (res == y) every element is
+    // read before this thread writes it, and no other thread touches it.
+    float bn[NB];
 #pragma unroll
     for (int j = 0; j < NB; j++) {
         bn[j] = bias && nl + 32 * j < N ? bias[nl + 32 * j] : 0.0f;
     }
+    __builtin_amdgcn_s_waitcnt(0);  // the bias in registers before any store
+    auto go = [&](auto full_c) {
+        constexpr bool FULL = decltype(full_c)::value;
+        float          rv[16];
+        auto           rload = [&](int b) {
+            const int64_t n = nl + 32 * (b % NB);
 #pragma unroll
-    for (int i = 0; i < MB; i++) {
-        const int64_t mb = m0 + wm * (BM / WM) + i * 32 + 4 * hh;  // row of register 0
-#pragma unroll
-        for (int j = 0; j < NB; j++) {
-            const int64_t n = nl + 32 * j;
-            if (n >= N) {
-                continue;
+            for (int r = 0; r < 16; r++) {
+                const int64_t m = mw + (b / NB) * 32 + 8 * (r / 4) + (r % 4);
+                rv[r]           = FULL || (m < M && n < N) ? res[m * ldr + n] : 0.0f;
             }
-            float v[16];
+        };
+        if (res) {
+            rload(0);
+        }
+#pragma unroll
+        for (int b = 0; b < MB * NB; b++) {
+            const int     i = b / NB, j = b % NB;
+            const int64_t n = nl + 32 * j;
+            float         v[16];
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 v[r] = bias ? acc[i][j][r] + bn[j] : acc[i][j][r];
             }
             if (res) {
-                float rv[16];
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int64_t m = mb + 8 * (r / 4) + (r % 4);
-                    rv[r]           = m < M ? res[m * ldr + n] : 0.0f;
-                }
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     v[r] = rv[r] + v[r];
                 }
+                if (b + 1 < MB * NB) {
+                    rload(b + 1);
+                }
+            }
+            if (!FULL && n >= N) {
+                continue;
             }
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int64_t m = mb + 8 * (r / 4) + (r % 4);
-                if (m < M) {
+                const int64_t m = mw + i * 32 + 8 * (r / 4) + (r % 4);
+                if (FULL || m < M) {
                     y[m * ldy + n] = v[r];
                 }
             }
         }
+    };
+    if (full) {
+        go(std::integral_constant<bool, true>{});
+    } else {
+        go(std::integral_constant<bool, false>{});
     }
 }
 
