@@ -30,6 +30,7 @@ extern "C" {
 /* GGUF-stable type ids used below. */
 #define MMHIP_TYPE_F32  0
 #define MMHIP_TYPE_F16  1
+#define MMHIP_TYPE_BF16 30
 #define MMHIP_TYPE_Q8_0 8
 #define MMHIP_TYPE_Q4_K 12
 #define MMHIP_TYPE_Q6_K 14
@@ -74,6 +75,11 @@ int mmhip_dequantize_rows(int type, const void * w, int64_t nrows, int64_t ne0, 
  * M <= 16: activation-quantised GEMV (ggml-CPU arithmetic: Q8_0 / Q8_K
  * activations, integer block dots).  M > 16: MFMA GEMM on f16-rounded
  * dequantised weights and f16-rounded activations, f32 accumulation.
+ * type MMHIP_TYPE_BF16 (BF16 weight rows as stored, w_row_stride bytes apart,
+ * 16-byte aligned; the native-BF16 model files): ggml's BF16 arithmetic
+ * (activations rounded to bf16, exact products, f32 sums) -- at M <= 16
+ * mmhip_mul_mat_bf16 with no workspace (K % 8 == 0), above it the bf16 MFMA
+ * GEMM on a bf16 copy of the activations in the workspace (K % 32 == 0).
  * ------------------------------------------------------------------- */
 size_t mmhip_mul_mat_workspace(int type, int64_t N, int64_t K, int64_t M);
 int    mmhip_mul_mat(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const float * x, int64_t ldx,

@@ -630,15 +630,17 @@ bool supports(const struct ggml_tensor * op) {
         case GGML_OP_TRANSPOSE:
             return true;
         case GGML_OP_MUL_MAT:
-            if (op->src[0]->type == GGML_TYPE_BF16) {  // BF16 weights at up to 16 tokens
+            if (op->src[0]->type == GGML_TYPE_BF16) {
+                // BF16 weights: the GEMV up to 16 tokens (K % 8 == 0), the
+                // 16-bit DMA GEMM above (K % 32 == 0); both make 16-byte loads,
+                // so rows and bases are 16-byte aligned (also checked before
+                // allocation, through the view offsets)
                 const struct ggml_tensor * w = op->src[0];
                 const struct ggml_tensor * x = op->src[1];
-                // the kernel's 16-byte loads: rows and bases 16-byte aligned
-                // (also checked before allocation, through the view offsets)
-                return w->nb[0] == 2 && w->ne[2] == 1 && w->ne[3] == 1 && w->ne[0] % 8 == 0 && w->nb[1] % 16 == 0 &&
-                       x->type == GGML_TYPE_F32 && mm_collapsible(x) && x->ne[1] * x->ne[2] * x->ne[3] <= 16 &&
-                       x->nb[1] % 16 == 0 && aligned16(x) && aligned16(w) && op->type == GGML_TYPE_F32 &&
-                       ggml_is_contiguous(op);
+                const int64_t              M = x->ne[1] * x->ne[2] * x->ne[3];
+                return w->nb[0] == 2 && w->ne[2] == 1 && w->ne[3] == 1 && w->ne[0] % (M <= 16 ? 8 : 32) == 0 &&
+                       w->nb[1] % 16 == 0 && x->type == GGML_TYPE_F32 && mm_collapsible(x) && x->nb[1] % 16 == 0 &&
+                       aligned16(x) && aligned16(w) && op->type == GGML_TYPE_F32 && ggml_is_contiguous(op);
             }
             if (op->src[0]->type == GGML_TYPE_F32) {  // activation x activation
                 return op->src[1]->type == GGML_TYPE_F32 && op->src[0]->nb[0] == 4 && op->src[1]->nb[0] == 4 &&
@@ -761,6 +763,9 @@ int run_node(mi_backend * c, const struct ggml_tensor * n) {
         case GGML_OP_TRANSPOSE:
             return MMHIP_OK;
         case GGML_OP_MUL_MAT:
+            if (n->src[0]->type == GGML_TYPE_BF16 && n->src[1]->ne[1] * n->src[1]->ne[2] * n->src[1]->ne[3] > 16) {
+                return run_mul_mat(c, n) ? MMHIP_OK : -1;  // the GEMM, with its bf16 activation copy
+            }
             if (n->src[0]->type == GGML_TYPE_BF16) {
                 const struct ggml_tensor * w = n->src[0];
                 const struct ggml_tensor * x = n->src[1];

@@ -28,6 +28,15 @@ __device__ __forceinline__ float16_t gm_mfma(half8_t a, half8_t b, float16_t c) 
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// The same product on bf16 operands (carried as 16-bit patterns in half8_t):
+// bf16 x bf16 products are exact in f32 and accumulate in f32.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ float16_t gm_mfma_bf16(half8_t a, half8_t b, float16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                   0, 0, 0);
+}
+
 // Raw bytes a thread needs for its half row (32 weights) of one K step.
 struct WRaw {
     int4_t   q0, q1;     // quant bytes
@@ -203,11 +212,13 @@ __device__ __forceinline__ int swz32(int r, int c) {
 // silu(g) * v with k_swiglu's arithmetic and stores the SwiGLU rows [M, F]
 // in f32 and / or f16 (the next GEMM's activation format).
 //
-// WH: the weights come as f16 rows [N][K] (dequantised once by k_w_to_f16
-// with the same arithmetic), so both tiles are DMA'd: a ring of GM_NS stages
-// of 32-wide K steps, each stage's DMA issued GM_NS - 1 steps ahead, one
-// barrier per step.  The MFMAs run in the same k order, so the sums are the
-// register-staged kernel's to the bit.
+// WH: the weights come as 16-bit rows rs bytes apart, so both tiles are
+// DMA'd: a ring of GM_NS stages of 32-wide K steps, each stage's DMA issued
+// GM_NS - 1 steps ahead, one barrier per step.  WT = TYPE_F16: the quantised
+// weights dequantised once by k_w_to_f16 with the same arithmetic (the MFMAs
+// run in the same k order, so the sums are the register-staged kernel's to the
+// bit).  WT = TYPE_BF16: BF16 weight rows as stored, bf16 activations, the
+// bf16 MFMA.
 constexpr int GM_NS = 4;
 
 template <int WT, int NW, int WM, int BK, int BM, bool GLU, bool WH = false>
@@ -385,7 +396,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
             const int     c = (wave * WI + i) * 64 + lane, r = c / CPR;
             bool          ok;
             const int64_t n = wrow_of(r, ok);
-            wsrc[i]         = (const _Float16 *) W + (ok ? n : 0) * K + 8 * ((c % CPR) ^ ((r >> 2) & 3));
+            wsrc[i]         = (const _Float16 *) (W + (ok ? n : 0) * rs) + 8 * ((c % CPR) ^ ((r >> 2) & 3));
         }
         const _Float16 * xs[XI];
 #pragma unroll
@@ -422,7 +433,11 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
                 for (int i = 0; i < MB; i++) {
 #pragma unroll
                     for (int j = 0; j < NB; j++) {
-                        acc[i][j] = gm_mfma(a[i], b[j], acc[i][j]);
+                        if constexpr (WT == TYPE_BF16) {
+                            acc[i][j] = gm_mfma_bf16(a[i], b[j], acc[i][j]);
+                        } else {
+                            acc[i][j] = gm_mfma(a[i], b[j], acc[i][j]);
+                        }
                     }
                 }
             }
@@ -676,6 +691,24 @@ __global__ void k_x_to_f16(const float * __restrict__ x, int64_t ldx, int64_t K,
     }
 }
 
+// Activations f32 -> bf16 (ggml's rounding: nearest-even, NaN quiet) into a
+// packed [M, K] copy of 16-bit patterns, 8 elements per thread per pass.
+__global__ void k_x_to_bf16(const float * __restrict__ x, int64_t ldx, int64_t K, int64_t n8,
+                            uint16_t * __restrict__ xb) {
+    for (int64_t t = blockIdx.x * (int64_t) blockDim.x + threadIdx.x; t < n8; t += (int64_t) gridDim.x * blockDim.x) {
+        const int64_t  e = t * 8, m = e / K, k = e % K;
+        const float4_t a = *(const float4_t *) (x + m * ldx + k);
+        const float4_t b = *(const float4_t *) (x + m * ldx + k + 4);
+        uint32_t       o[4];
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            o[j]     = (__float_as_uint(round_bf16(a[2 * j])) >> 16) | (__float_as_uint(round_bf16(a[2 * j + 1])) & 0xffff0000u);
+            o[2 + j] = (__float_as_uint(round_bf16(b[2 * j])) >> 16) | (__float_as_uint(round_bf16(b[2 * j + 1])) & 0xffff0000u);
+        }
+        *(int4_t *) (xb + e) = int4_t{ (int) o[0], (int) o[1], (int) o[2], (int) o[3] };
+    }
+}
+
 // Weights -> f16 rows [N][K] (row stride K), the register-staged kernel's
 // dequantisation: thread (row, 64-wide K step, half) dequantises its 32
 // values exactly (f32, then f16) and writes them as four 16-byte chunks.
@@ -755,8 +788,10 @@ static int launch_gemm(int wtype, const uint8_t * W, int64_t N, int64_t K, int64
         return check_launch("mul_mat gemm");
     };
     if constexpr (WH) {
-        // f16 weight rows: the block type plays no part
-        (void) wtype;
+        // 16-bit weight rows: f16 copies of any block type, or BF16 as stored
+        if (wtype == TYPE_BF16) {
+            return go(k_gemm_q<TYPE_BF16, NW, WM, BK, BM, false, true>);
+        }
         return glu.F > 0 ? go(k_gemm_q<TYPE_F16, NW, WM, BK, BM, true, true>)
                          : go(k_gemm_q<TYPE_F16, NW, WM, BK, BM, false, true>);
     } else {
@@ -929,6 +964,52 @@ int gemm_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const fl
         wb = (const uint8_t *) whp;
     }
     return gemm_launch(wtype, wb, N, K, rs, xh, M, bias, res, ldr, y, ldy, glu ? *glu : none, single, spl, stream, wh);
+}
+
+// BF16 weights at token counts: rows rs bytes apart read in place by the
+// 16-bit DMA ring (K % 32 == 0, 16-byte rows), activations rounded to bf16
+// into the workspace first.
+bool gemm_bf16_supported(int64_t N, int64_t K, int64_t rs, const void * W, const float * x, int64_t ldx) {
+    return N > 0 && K > 0 && K % 32 == 0 && rs >= 2 * K && rs % 16 == 0 && ((uintptr_t) W) % 16 == 0 &&
+           ((uintptr_t) x) % 16 == 0 && ldx % 4 == 0;
+}
+
+size_t gemm_bf16_workspace(int64_t K, int64_t M) {
+    return (size_t) M * (size_t) K * sizeof(uint16_t);
+}
+
+int gemm_bf16(const void * W, int64_t N, int64_t K, int64_t rs, const float * x, int64_t ldx, int64_t M, float * y,
+              int64_t ldy, void * ws, size_t ws_bytes, hipStream_t stream) {
+    if (!gemm_bf16_supported(N, K, rs, W, x, ldx)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED,
+                         "mul_mat bf16 gemm: N=%lld K=%lld rs=%lld (K %% 32 == 0, 16-byte aligned rows)",
+                         (long long) N, (long long) K, (long long) rs);
+    }
+    const size_t need = gemm_bf16_workspace(K, M);
+    if (!ws || ws_bytes < need || ((uintptr_t) ws) % 16 != 0) {
+        return set_error(MMHIP_ERR_WORKSPACE, "mul_mat bf16 gemm: workspace %zu < %zu (16-byte aligned)", ws_bytes,
+                         need);
+    }
+    const int64_t n8 = M * K / 8;
+    const int64_t nb = (n8 + 255) / 256;
+    hipLaunchKernelGGL(k_x_to_bf16, dim3((unsigned) (nb < 8192 ? nb : 8192)), dim3(256), 0, stream, x, ldx, K, n8,
+                       (uint16_t *) ws);
+    int rc = check_launch("mul_mat bf16 gemm: convert");
+    if (rc != MMHIP_OK) {
+        return rc;
+    }
+    const GemmGlu   none{};
+    const GemmMulti single{};
+    const GemmSplit one{};
+    const uint8_t * wb       = (const uint8_t *) W;
+    const auto *    xb       = (const _Float16 *) ws;  // 16-bit patterns
+    const int64_t   tiles256 = ((N + 255) / 256) * ((M + 255) / 256);
+    if (tiles256 >= 256) {
+        return launch_gemm<8, 2, 32, 256, true>(TYPE_BF16, wb, N, K, rs, xb, M, nullptr, nullptr, 0, y, ldy, none,
+                                                single, one, stream);
+    }
+    return launch_gemm<4, 2, 32, 64, true>(TYPE_BF16, wb, N, K, rs, xb, M, nullptr, nullptr, 0, y, ldy, none, single,
+                                           one, stream);
 }
 
 }  // namespace mmhip

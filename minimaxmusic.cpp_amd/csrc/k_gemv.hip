@@ -1272,26 +1272,12 @@ bool gemv_supported(int wtype, int64_t N, int64_t K, int64_t rs, const void * W)
     return rs % align == 0 && ((uintptr_t) W) % align == 0;
 }
 
-// f32 -> bf16 as ggml rounds it: nearest-even on the upper 16 bits, NaN kept
-// quiet.
-__device__ __forceinline__ float round_bf16(float v) {
-    uint32_t u = __float_as_uint(v);
-    if ((u & 0x7fffffffu) > 0x7f800000u) {
-        u = (u | 0x00400000u) & 0xffff0000u;
-    } else {
-        u = (u + (0x7fffu + ((u >> 16) & 1u))) & 0xffff0000u;
-    }
-    return __uint_as_float(u);
-}
-
 // GGML_OP_MUL_MAT over BF16 weights at 1..16 activation rows (the BF16 files
 // of the depth decoder and the LM, src/depth-decoder.h:206-257): ggml's BF16
 // dot rounds the activations to bf16 and sums the f32 products of the pairs.
 // One wave per weight row; lane l takes the 8-element chunks l, l + 64, ..;
 // the activation chunks come from cache.  Sums: per-lane f32, then a
-// symmetric wave reduction.
-constexpr int BF16_MAXM = 16;
-
+// symmetric wave reduction.  At most BF16_GEMV_MAXM activation rows.
 __global__ __launch_bounds__(256) void k_gemv_bf16(const uint16_t * __restrict__ W, int64_t N, int64_t K, int64_t ldw,
                                                    const float * __restrict__ x, int64_t ldx, int M,
                                                    float * __restrict__ y, int64_t ldy) {
@@ -1302,9 +1288,9 @@ __global__ __launch_bounds__(256) void k_gemv_bf16(const uint16_t * __restrict__
         return;  // wave-uniform
     }
     const uint16_t * wr = W + row * ldw;
-    float            acc[BF16_MAXM];
+    float            acc[BF16_GEMV_MAXM];
 #pragma unroll
-    for (int c = 0; c < BF16_MAXM; c++) {
+    for (int c = 0; c < BF16_GEMV_MAXM; c++) {
         acc[c] = 0.0f;
     }
     for (int64_t k = (int64_t) lane * 8; k < K; k += 512) {
@@ -1317,7 +1303,7 @@ __global__ __launch_bounds__(256) void k_gemv_bf16(const uint16_t * __restrict__
             wf[2 * e + 1] = __uint_as_float(ww[e] & 0xffff0000u);
         }
 #pragma unroll
-        for (int c = 0; c < BF16_MAXM; c++) {
+        for (int c = 0; c < BF16_GEMV_MAXM; c++) {
             if (c < M) {
                 const float4_t a = *(const float4_t *) (x + c * ldx + k);
                 const float4_t b = *(const float4_t *) (x + c * ldx + k + 4);
@@ -1335,7 +1321,7 @@ __global__ __launch_bounds__(256) void k_gemv_bf16(const uint16_t * __restrict__
         }
     }
 #pragma unroll
-    for (int c = 0; c < BF16_MAXM; c++) {
+    for (int c = 0; c < BF16_GEMV_MAXM; c++) {
         if (c < M) {
             const float v = wave_sum(acc[c]);
             if (lane == 0) {
@@ -1400,7 +1386,7 @@ extern "C" int mmhip_mul_mat_bf16(const void * W, int64_t N, int64_t K, int64_t 
         return set_error(MMHIP_ERR_INVALID, "mul_mat_bf16: bad arguments N=%lld K=%lld M=%lld", (long long) N,
                          (long long) K, (long long) M);
     }
-    if (M > BF16_MAXM || K % 8 != 0 || ldw % 8 != 0 || ldx % 4 != 0 || ((uintptr_t) W) % 16 != 0 ||
+    if (M > BF16_GEMV_MAXM || K % 8 != 0 || ldw % 8 != 0 || ldx % 4 != 0 || ((uintptr_t) W) % 16 != 0 ||
         ((uintptr_t) x) % 16 != 0) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat_bf16: M=%lld K=%lld (M <= 16, K %% 8 == 0, aligned rows)",
                          (long long) M, (long long) K);

@@ -74,6 +74,10 @@ extern "C" int mmhip_version(void) {
 }
 
 extern "C" size_t mmhip_mul_mat_workspace(int type, int64_t N, int64_t K, int64_t M) {
+    if (type == TYPE_BF16) {
+        // the GEMV reads f32 activations; the GEMM their bf16 copy
+        return M > BF16_GEMV_MAXM ? gemm_bf16_workspace(K, M) : 0;
+    }
     if (use_gemm(type, M)) {
         return gemm_q_workspace(N, K, M);
     }
@@ -92,10 +96,19 @@ extern "C" int mmhip_mul_mat(int type, const void * W, int64_t N, int64_t K, int
         return set_error(MMHIP_ERR_INVALID, "mul_mat: bad arguments N=%lld K=%lld M=%lld", (long long) N,
                          (long long) K, (long long) M);
     }
+    hipStream_t st = (hipStream_t) stream;
+    if (type == TYPE_BF16) {
+        if (M <= BF16_GEMV_MAXM) {
+            if (w_row_stride % 2 != 0) {
+                return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat bf16: row stride %lld bytes", (long long) w_row_stride);
+            }
+            return mmhip_mul_mat_bf16(W, N, K, w_row_stride / 2, x, ldx, M, y, ldy, stream);
+        }
+        return gemm_bf16(W, N, K, w_row_stride, x, ldx, M, y, ldy, ws, ws_bytes, st);
+    }
     if (!is_repacked_type(type)) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat: weight type %d", type);
     }
-    hipStream_t st = (hipStream_t) stream;
     if (use_gemm(type, M)) {
         return gemm_q(type, W, N, K, w_row_stride, x, ldx, M, y, ldy, ws, ws_bytes, st);
     }

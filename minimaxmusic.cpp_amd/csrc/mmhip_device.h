@@ -24,6 +24,18 @@ constexpr int TYPE_Q6_K = 14;
 constexpr int TYPE_Q8_K = 15;
 constexpr int TYPE_BF16 = 30;
 
+// f32 -> bf16 as ggml rounds it (ggml_compute_fp32_to_bf16): nearest-even on
+// the upper 16 bits, NaN kept quiet; returned as the f32 of the bf16 value.
+__device__ __forceinline__ float round_bf16(float v) {
+    uint32_t u = __float_as_uint(v);
+    if ((u & 0x7fffffffu) > 0x7f800000u) {
+        u = (u | 0x00400000u) & 0xffff0000u;
+    } else {
+        u = (u + (0x7fffu + ((u >> 16) & 1u))) & 0xffff0000u;
+    }
+    return __uint_as_float(u);
+}
+
 constexpr int QK8_0 = 32;
 constexpr int QK_K  = 256;
 

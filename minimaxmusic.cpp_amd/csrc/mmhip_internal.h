@@ -118,6 +118,15 @@ size_t gemm_split_bytes(int64_t N, int64_t K, int64_t M);
 bool   gemm_use_wh(int64_t N, int64_t K, int64_t M);
 size_t gemm_wh_bytes(int64_t N, int64_t K, int64_t M);
 size_t gemm_q_workspace(int64_t N, int64_t K, int64_t M);
+// BF16 weights: the GEMV takes up to this many activation rows, the GEMM more.
+constexpr int BF16_GEMV_MAXM = 16;
+// BF16 weights at token counts (rows rs bytes apart, read in place): the
+// bf16 activation copy the workspace holds, the shape / alignment check, and
+// the call (y = x W^T, ggml's BF16 arithmetic: bf16 activations, f32 sums).
+size_t gemm_bf16_workspace(int64_t K, int64_t M);
+bool   gemm_bf16_supported(int64_t N, int64_t K, int64_t rs, const void * W, const float * x, int64_t ldx);
+int    gemm_bf16(const void * W, int64_t N, int64_t K, int64_t rs, const float * x, int64_t ldx, int64_t M, float * y,
+                 int64_t ldy, void * ws, size_t ws_bytes, hipStream_t stream);
 // The epilogue adds bias[n] (if given), then res[m * ldr + n] (if given).
 int    gemm_q(int wtype, const void * W, int64_t N, int64_t K, int64_t row_stride, const float * x, int64_t ldx,
               int64_t M, float * y, int64_t ldy, void * ws, size_t ws_bytes, hipStream_t stream,

@@ -215,6 +215,79 @@ def test_mul_mat_bf16_rejects_and_backend(mm, pkg):
     assert np.array_equal(yb, y.cpu().numpy())
 
 
+@pytest.mark.parametrize("N,K,M,pad", [(2048, 2048, 1380, 0), (6144, 4096, 100, 0), (37, 544, 33, 32),
+                                       (4096, 2048, 8192, 0), (300, 1024, 17, 64), (1000, 8192, 257, 0)])
+def test_mul_mat_bf16_gemm(mm, N, K, M, pad):
+    """MUL_MAT over BF16 weights above 16 tokens: the bf16 MFMA GEMM reading
+    the weight rows in place (row stride K + pad elements) through the 16-bit
+    DMA ring, on a bf16 copy of the activations.  ggml's BF16 arithmetic --
+    activations rounded to bf16 (torch's rounding, nearest-even), exact
+    products, f32 sums -- against float64 of the same bf16 operands, max-rel
+    2e-5 (f32 sums over K <= 8192).  Shapes cover both tile configurations
+    (8192 tokens: 256 x 256 tiles), ragged N and M, and padded rows; the
+    workspace is the bf16 copy and a smaller one is refused."""
+    import ctypes
+
+    g = torch.Generator().manual_seed(N + K + M)
+    Wp = (torch.randn((N, K + pad), generator=g) * 0.02).bfloat16()
+    W = Wp[:, :K]
+    x = torch.randn((M, K), generator=g)
+    ref = (x.bfloat16().double().cuda() @ W.double().cuda().T).cpu()
+    L = mm.load()
+    need = L.mmhip_mul_mat_workspace(30, N, K, M)
+    assert need == M * K * 2
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    tw, tx = Wp.cuda(), x.cuda()
+    y = torch.full((M, N), float("nan"), device="cuda")
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rs = (K + pad) * 2
+    assert L.mmhip_mul_mat(30, P(tw), N, K, rs, P(tx), K, M, P(y), N, P(ws), need - 16, st) == -4
+    assert L.mmhip_mul_mat(30, P(tw), N, K, rs, P(tx), K, M, P(y), N, P(ws), need, st) == 0, L.mmhip_last_error()
+    torch.cuda.synchronize()
+    yc = y.cpu().double()
+    assert torch.isfinite(yc).all()
+    assert float((yc - ref).abs().max() / ref.abs().max()) < 2e-5
+
+
+def test_mul_mat_bf16_gemm_backend(mm, pkg):
+    """A BF16 MUL_MAT node at 100 tokens runs on the backend (supports_op
+    takes BF16 above 16 tokens at K % 32 == 0) and gives the C-ABI GEMM's
+    result bit for bit; at K % 32 != 0 above 16 tokens the C-ABI refuses."""
+    import ctypes
+    import importlib
+
+    L = mm.load()
+    d = torch.zeros(1 << 16, device="cuda")
+    Pd = ctypes.c_void_p(d.data_ptr())
+    assert L.mmhip_mul_mat(30, Pd, 64, 272, 544, Pd, 272, 17, Pd, 64, Pd, 1 << 18, None) != 0
+    og = importlib.import_module(pkg.__name__ + ".opgraph")
+    N, K, M = 512, 2048, 100
+    g = torch.Generator().manual_seed(6)
+    W = (torch.randn((N, K), generator=g) * 0.02).bfloat16()
+    x = torch.randn((M, K), generator=g)
+    gr = og.OpGraph()
+    try:
+        tw = gr.tensor(30, [K, N])  # GGML_TYPE_BF16
+        tx = gr.tensor(og.F32, [K, M])
+        out = gr.mul_mat(tw, tx)
+        gr.build([out])
+        gr.set(tw, W.view(torch.int16).numpy())
+        gr.set(tx, x.numpy())
+        gr.compute()
+        yb = gr.get(out).reshape(M, N)
+    finally:
+        gr.close()
+    need = L.mmhip_mul_mat_workspace(30, N, K, M)
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    y = torch.empty((M, N), device="cuda")
+    Q = lambda t: ctypes.c_void_p(t.data_ptr())
+    tw_, tx_ = W.cuda(), x.cuda()
+    assert L.mmhip_mul_mat(30, Q(tw_), N, K, K * 2, Q(tx_), K, M, Q(y), N, Q(ws), need, None) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(yb, y.cpu().numpy())
+
+
 @pytest.mark.parametrize("N,K,M", [(4096, 12288, 2), (4096, 4096, 2), (1000, 8192, 1), (6144, 4096, 2),
                                    (30000, 2048, 2), (77, 4096, 1)])
 def test_gemv_q6_K_persistent_equals_wave_kernel(mm, pkg, monkeypatch, N, K, M):
