@@ -10,7 +10,8 @@ build_input() makes the graph head (src/dit.h:250-268): the channel concat
 [latent, zeros, condition], the residual preprocess projection, proj_in and
 the prepended timestep token.  Weights are GGUF Q8_0 rows (the default DiT
 file), synthesised here: int8 quants uniform in [-127, 127], fp16 scales
-|N(0, 0.02)| / 127.
+|N(0, 0.02)| / 127; or BF16 rows (the native-BF16 files), N(0, 0.02)
+rounded to bf16.
 """
 import numpy as np
 
@@ -32,14 +33,22 @@ def q8_0_rows(rng, n, k):
     return blk.view(np.uint8).reshape(n, k // 32 * 34)
 
 
-def synth_block(seed, dim=DIM, ff=FF_INNER):
-    """Host arrays of one block's tensors: Q8_0 rows [N, K/32*34] for the
-    projections, f32 vectors for norms and biases."""
+def bf16_rows(rng, n, k):
+    """n BF16 rows of k elements (uint16 bit patterns): N(0, 0.02) rounded
+    to the nearest bf16, ties to even."""
+    u = (rng.standard_normal((n, k)) * 0.02).astype(np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def synth_block(seed, dim=DIM, ff=FF_INNER, wtype=opgraph.Q8_0):
+    """Host arrays of one block's tensors: Q8_0 rows [N, K/32*34] (or BF16
+    rows [N, K]) for the projections, f32 vectors for norms and biases."""
     rng = np.random.default_rng(seed)
     w = {}
+    rows_of = q8_0_rows if wtype == opgraph.Q8_0 else bf16_rows
     for n, (rows, k) in {"wq": (dim, dim), "wk": (dim, dim), "wv": (dim, dim), "wo": (dim, dim),
                          "ff_in_w": (2 * ff, dim), "ff_out_w": (dim, ff)}.items():
-        w[n] = q8_0_rows(rng, rows, k)
+        w[n] = rows_of(rng, rows, k)
     for n, size in {"norm1_w": dim, "norm1_b": dim, "norm2_w": dim, "norm2_b": dim,
                     "ff_in_b": 2 * ff, "ff_out_b": dim}.items():
         base = 1.0 if n.endswith("_w") else 0.0
@@ -50,11 +59,11 @@ def synth_block(seed, dim=DIM, ff=FF_INNER):
 class Block:
     """Graph tensors of one block's weights, created in g."""
 
-    def __init__(self, g, dim=DIM, ff=FF_INNER):
+    def __init__(self, g, dim=DIM, ff=FF_INNER, wtype=opgraph.Q8_0):
         t = g.tensor
-        self.wq, self.wk, self.wv, self.wo = (t(opgraph.Q8_0, [dim, dim]) for _ in range(4))
-        self.ff_in_w = t(opgraph.Q8_0, [dim, 2 * ff])
-        self.ff_out_w = t(opgraph.Q8_0, [ff, dim])
+        self.wq, self.wk, self.wv, self.wo = (t(wtype, [dim, dim]) for _ in range(4))
+        self.ff_in_w = t(wtype, [dim, 2 * ff])
+        self.ff_out_w = t(wtype, [ff, dim])
         self.norm1_w, self.norm1_b, self.norm2_w, self.norm2_b = (t(opgraph.F32, [dim]) for _ in range(4))
         self.ff_in_b = t(opgraph.F32, [2 * ff])
         self.ff_out_b = t(opgraph.F32, [dim])

@@ -25,6 +25,8 @@ def _mods(pkg):
 
 
 def _deq(orc, rows, k):
+    if rows.dtype == np.uint16:  # BF16 rows: the f32 of each bf16
+        return torch.from_numpy((rows.astype(np.uint32) << 16).view(np.float32))
     return torch.from_numpy(orc.dequantize(8, rows, k, rows.shape[0]).reshape(rows.shape[0], k))
 
 
@@ -71,19 +73,21 @@ def ref_block(orc, dg, w, x, pos, ff):
     return x + (torch.nn.functional.silu(gate) * value) @ W["ff_out_w"].T + t["ff_out_b"]
 
 
-@pytest.mark.parametrize("S,B,seed", [(690, 2, 51), (37, 1, 52)])
-def test_dit_block_through_backend(pkg, orc, S, B, seed):
+@pytest.mark.parametrize("S,B,seed,wt", [(690, 2, 51, 8), (37, 1, 52, 8), (690, 2, 54, 30), (37, 1, 55, 30)])
+def test_dit_block_through_backend(pkg, orc, S, B, seed, wt):
     """One DiT block at the model's shape (S = T + 1 = 690 tokens, CFG B = 2)
-    and a ragged small case."""
+    and a ragged small case, with Q8_0 weights (wt 8) and with BF16 weights
+    (wt 30, the native-BF16 files: every projection on the bf16 MFMA GEMM,
+    activations rounded to bf16 as ggml's BF16 dot does)."""
     og, dg = _mods(pkg)
     torch.set_num_threads(16)
-    w = dg.synth_block(seed)
+    w = dg.synth_block(seed, wtype=wt)
     rng = np.random.default_rng(seed + 100)
     x = rng.standard_normal((B, S, dg.DIM)).astype(np.float32)
     pos = np.arange(S, dtype=np.int32)
     g = og.OpGraph()
     try:
-        blk = dg.Block(g)
+        blk = dg.Block(g, wtype=wt)
         tx = g.tensor(og.F32, [dg.DIM, S, B])
         tp = g.tensor(26, [S])  # GGML_TYPE_I32
         out = dg.build_block(g, blk, tx, tp, S, B)
