@@ -49,6 +49,12 @@ GGML_API void ggml_backend_mi355x_graph_cache_info(ggml_backend_t backend, int64
  * finish); reset != 0 clears the totals.  Backend-specific, no counterpart in
  * the reference (used to report kernel-side time next to wall-clock). */
 GGML_API void ggml_backend_mi355x_gpu_time(ggml_backend_t backend, double * total_ms, int64_t * n_calls, int reset);
+/* Bytes of f16 weight copies the backend holds for its token-count GEMMs:
+ * made, within GGML_MI355X_F16_WEIGHTS_MB (default 32768), for the quantised
+ * weights that a graph computed three or more times multiplies at more than 16
+ * tokens (the DiT's, once per diffusion step).  Diagnostics, no counterpart in
+ * the reference. */
+GGML_API size_t ggml_backend_mi355x_f16_weight_bytes(void);
 
 #ifdef __cplusplus
 }

@@ -84,6 +84,22 @@ int mmhip_dequantize_rows(int type, const void * w, int64_t nrows, int64_t ne0, 
 size_t mmhip_mul_mat_workspace(int type, int64_t N, int64_t K, int64_t M);
 int    mmhip_mul_mat(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const float * x, int64_t ldx,
                      int64_t M, float * y, int64_t ldy, void * ws, size_t ws_bytes, void * stream);
+/* f16 copies of quantised weights for the token-count GEMMs.  No counterpart
+ * in the reference: ggml's MUL_MAT on quantised weights (src/dit.h:197-199,
+ * :228, :237, :243) is what they speed up.  A weight multiplied at M > 16 many
+ * times (the DiT's, once per diffusion step) can be converted once to f16 rows
+ * [N][K] (mmhip_weights_f16_bytes bytes, 16-byte aligned; the GEMM's own exact
+ * dequantisation) and registered under the quantised weight's address; every
+ * GEMM form above 16 tokens on that weight (plain, bias / residual, SwiGLU,
+ * multi-matrix, f32 or f16 activations) then reads the copy with no per-call
+ * conversion and returns the same bits.  The caller keeps the copy current
+ * (convert again after rewriting the weight) and unregisters it before
+ * freeing either.  Registration is process-wide and thread-safe. */
+size_t mmhip_weights_f16_bytes(int64_t N, int64_t K);
+int    mmhip_weights_to_f16(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, void * wh,
+                            void * stream);
+int    mmhip_register_weights_f16(const void * W, int64_t N, int64_t K, const void * wh);
+int    mmhip_unregister_weights_f16(const void * W);
 /* MUL_MAT at token counts (M > 16) with the ADDs that follow it fused into the
  * store: y = (x W^T + bias[n]) + r[m*ldr + n], each ADD rounded as its op;
  * bias and r may be NULL (r may alias y).  The DiT's projection biases and

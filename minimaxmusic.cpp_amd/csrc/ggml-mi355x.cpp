@@ -108,11 +108,39 @@ mmhip_view view_of(const struct ggml_tensor * t) {
 // ---------------------------------------------------------------------------
 // device buffers
 
-struct mi_buffer {
-    int    device;
-    void * ptr;
-    bool   poisoned = false;  // a set_tensor / get_tensor on it failed
+// An f16 copy of a quantised weight in the buffer (rows [N][K], the GEMM's
+// exact dequantisation), registered with the kernel library so the
+// token-count GEMMs read it instead of converting per call.
+struct mi_f16_copy {
+    const void * w;      // the quantised weight (its tensor's data)
+    void *       wh;     // the copy
+    size_t       bytes;  // of the copy
+    size_t       wbytes; // of the quantised weight
+    int          type;
+    int64_t      N, K, rs;
 };
+
+struct mi_buffer {
+    int                      device;
+    void *                   ptr;
+    bool                     poisoned = false;  // a set_tensor / get_tensor on it failed
+    std::vector<mi_f16_copy> f16;               // f16 weight copies made for its tensors
+};
+
+// f16 weight copies, process-wide: their total size (bounded by
+// GGML_MI355X_F16_WEIGHTS_MB, default 32768; 0 makes none) and a generation
+// that moves whenever copies appear or go, so that captured HIP graphs, which
+// hold the addresses the GEMMs read, are captured again.
+std::atomic<size_t>   g_f16_bytes{ 0 };
+std::atomic<uint64_t> g_f16_gen{ 0 };
+
+size_t f16_limit() {
+    static const size_t lim = [] {
+        const char * e = getenv("GGML_MI355X_F16_WEIGHTS_MB");
+        return (e ? (size_t) strtoull(e, nullptr, 10) : (size_t) 32768) << 20;
+    }();
+    return lim;
+}
 
 void poison(mi_buffer * c) {
     if (!c->poisoned) {
@@ -127,6 +155,14 @@ void buf_free(ggml_backend_buffer_t b) {
     mi_buffer * c = (mi_buffer *) b->context;
     hipSetDevice(c->device);
     HIP_OK(hipDeviceSynchronize());
+    for (const mi_f16_copy & f : c->f16) {
+        (void) mmhip_unregister_weights_f16(f.w);
+        (void) hipFree(f.wh);
+        g_f16_bytes.fetch_sub(f.bytes);
+    }
+    if (!c->f16.empty()) {
+        g_f16_gen.fetch_add(1);
+    }
     (void) hipFree(c->ptr);
     if (c->poisoned) {
         g_poisoned_buffers.fetch_sub(1);
@@ -239,6 +275,22 @@ bool staged_write(int device, void * dst, const void * src, size_t size) {
     return true;
 }
 
+// A write into a weight that has an f16 copy converts the copy again, in
+// place (captured graphs keep its address), before the write returns.
+void refresh_f16_copies(mi_buffer * c, const char * lo, const char * hi) {
+    for (const mi_f16_copy & f : c->f16) {
+        const char * w = (const char *) f.w;
+        if (lo < w + f.wbytes && w < hi) {
+            if (mmhip_weights_to_f16(f.type, f.w, f.N, f.K, f.rs, f.wh, nullptr) != MMHIP_OK ||
+                !HIP_OK(hipDeviceSynchronize())) {
+                MI_LOG("set_tensor: refreshing an f16 weight copy failed (%s): the buffer is marked failed\n",
+                       mmhip_last_error());
+                poison(c);
+            }
+        }
+    }
+}
+
 void buf_set_tensor(ggml_backend_buffer_t b, struct ggml_tensor * t, const void * data, size_t offset, size_t size) {
     mi_buffer * c = (mi_buffer *) b->context;
     hipSetDevice(c->device);
@@ -247,6 +299,7 @@ void buf_set_tensor(ggml_backend_buffer_t b, struct ggml_tensor * t, const void 
             MI_LOG("set_tensor %s failed: the buffer is marked failed, graphs using it are refused\n", t->name);
             poison(c);
         }
+        refresh_f16_copies(c, (const char *) t->data + offset, (const char *) t->data + offset + size);
         return;
     }
     if (staged_write(c->device, (char *) t->data + offset, data, size)) {
@@ -431,6 +484,7 @@ struct mi_graph_entry {
     int                         sights     = 0;
     bool                        no_capture = false;  // capture failed once: stay eager
     uint64_t                    stamp      = 0;
+    uint64_t                    f16_gen    = 0;      // g_f16_gen when captured
 };
 
 struct mi_backend {
@@ -2203,6 +2257,55 @@ bool capture_graph(mi_backend * c, struct ggml_cgraph * g, mi_graph_entry * e) {
     return true;
 }
 
+// f16 copies (within the budget) of the quantised weights that the graph
+// multiplies at more than 16 tokens and that have none yet; the conversions
+// run on the backend's stream ahead of the graph's own work.
+void make_f16_copies(mi_backend * c, struct ggml_cgraph * g) {
+    const size_t lim  = f16_limit();
+    bool         made = false;
+    for (int i = 0; i < ggml_graph_n_nodes(g) && lim > 0; i++) {
+        const struct ggml_tensor * n = ggml_graph_node(g, i);
+        if (n->op != GGML_OP_MUL_MAT || !is_repacked(n->src[0]->type) || mm_is_gemv(n) || !supports_mul_mat(n)) {
+            continue;
+        }
+        const struct ggml_tensor * w    = n->src[0];
+        const struct ggml_tensor * base = w->view_src ? w->view_src : w;
+        ggml_backend_buffer_t      wb   = base->buffer;
+        if (!wb || wb->iface.free_buffer != buf_free) {
+            continue;
+        }
+        mi_buffer * bc   = (mi_buffer *) wb->context;
+        bool        have = false;
+        for (const mi_f16_copy & f : bc->f16) {
+            have = have || f.w == w->data;
+        }
+        const int64_t N = w->ne[1], K = w->ne[0];
+        const size_t  bytes = mmhip_weights_f16_bytes(N, K);
+        if (have || bc->device != c->dev->id || g_f16_bytes.load() + bytes > lim) {
+            continue;
+        }
+        void * p = nullptr;
+        if (hipMalloc(&p, bytes) != hipSuccess) {
+            (void) hipGetLastError();
+            break;  // out of memory: the GEMMs convert per call as before
+        }
+        mi_f16_copy f{ w->data, p, bytes, ggml_nbytes(w), (int) w->type, N, K, (int64_t) w->nb[1] };
+        if (mmhip_weights_to_f16(f.type, f.w, N, K, f.rs, p, c->stream) != MMHIP_OK ||
+            mmhip_register_weights_f16(f.w, N, K, p) != MMHIP_OK) {
+            MI_LOG("f16 weight copy of %s not made: %s\n", w->name, mmhip_last_error());
+            HIP_OK(hipStreamSynchronize(c->stream));
+            (void) hipFree(p);
+            continue;
+        }
+        bc->f16.push_back(f);
+        g_f16_bytes.fetch_add(bytes);
+        made = true;
+    }
+    if (made) {
+        g_f16_gen.fetch_add(1);
+    }
+}
+
 enum ggml_status graph_compute_inner(ggml_backend_t b, struct ggml_cgraph * g) {
     mi_backend * c = (mi_backend *) b->context;
     hipSetDevice(c->dev->id);
@@ -2226,13 +2329,26 @@ enum ggml_status graph_compute_inner(ggml_backend_t b, struct ggml_cgraph * g) {
     }
     e->stamp = ++c->clock;
     e->sights++;
+    if (e->sights == 3) {
+        // a graph that repeats (the DiT's, once per diffusion step): f16
+        // copies of the weights its token-count GEMMs multiply
+        make_f16_copies(c, g);
+    }
+    if (e->exec && e->f16_gen != g_f16_gen.load()) {
+        // weight copies appeared or went since the capture: capture again
+        HIP_OK(hipStreamSynchronize(c->stream));
+        (void) hipGraphExecDestroy(e->exec);
+        e->exec = nullptr;
+    }
     if (e->exec) {
         c->n_replays++;
         return HIP_OK(hipGraphLaunch(e->exec, c->stream)) ? GGML_STATUS_SUCCESS : GGML_STATUS_FAILED;
     }
     if (c->use_graphs && !e->no_capture && e->sights >= 2) {
         // second sight of the same graph: capture it, then launch the capture
+        const uint64_t gen = g_f16_gen.load();
         if (capture_graph(c, g, e)) {
+            e->f16_gen = gen;
             c->n_replays++;
             return HIP_OK(hipGraphLaunch(e->exec, c->stream)) ? GGML_STATUS_SUCCESS : GGML_STATUS_FAILED;
         }
@@ -2419,6 +2535,9 @@ void * reg_proc(ggml_backend_reg_t, const char * name) {
     if (strcmp(name, "ggml_backend_mi355x_graph_cache_info") == 0) {
         return (void *) ggml_backend_mi355x_graph_cache_info;
     }
+    if (strcmp(name, "ggml_backend_mi355x_f16_weight_bytes") == 0) {
+        return (void *) ggml_backend_mi355x_f16_weight_bytes;
+    }
     return nullptr;
 }
 
@@ -2524,6 +2643,10 @@ extern "C" void ggml_backend_mi355x_gpu_time(ggml_backend_t backend, double * to
         c->gpu_ms = 0.0;
         c->gpu_n  = 0;
     }
+}
+
+extern "C" size_t ggml_backend_mi355x_f16_weight_bytes(void) {
+    return g_f16_bytes.load();
 }
 
 // dynamic-loading entry points

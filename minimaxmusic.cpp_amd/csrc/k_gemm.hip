@@ -14,7 +14,9 @@
 // (weight rows) inputs.  The output accumulator layout gives each lane one
 // weight row, so stores of 32 lanes are 128 contiguous bytes of a y row.
 #include <cstdlib>
+#include <mutex>
 #include <type_traits>
+#include <unordered_map>
 
 #include "mmhip_device.h"
 #include "mmhip_internal.h"
@@ -896,6 +898,51 @@ size_t gemm_q_workspace(int64_t N, int64_t K, int64_t M) {
     return xo + gemm_wh_bytes(N, K, M) + gemm_split_bytes(N, K, M);
 }
 
+// f16 copies of quantised weights (rows [N][K], k_w_to_f16's values) that a
+// caller made once and registered, keyed by the quantised weight's address:
+// the token-count GEMMs then run the DMA ring on them with no conversion.
+// The results are the register-staged kernel's to the bit either way.
+struct F16Weights {
+    int64_t      N, K;
+    const void * wh;
+};
+
+static std::mutex                                     g_f16w_mu;
+static std::unordered_map<const void *, F16Weights> g_f16w;
+
+int register_f16_weights(const void * W, int64_t N, int64_t K, const void * wh) {
+    if (!W || !wh || N <= 0 || K <= 0 || K % 32 != 0 || ((uintptr_t) wh) % 16 != 0) {
+        return set_error(MMHIP_ERR_INVALID, "register_weights_f16: bad arguments N=%lld K=%lld", (long long) N,
+                         (long long) K);
+    }
+    std::lock_guard<std::mutex> lk(g_f16w_mu);
+    g_f16w[W] = F16Weights{ N, K, wh };
+    return MMHIP_OK;
+}
+
+int unregister_f16_weights(const void * W) {
+    std::lock_guard<std::mutex> lk(g_f16w_mu);
+    return g_f16w.erase(W) ? MMHIP_OK : set_error(MMHIP_ERR_INVALID, "unregister_weights_f16: not registered");
+}
+
+// The registered copy of W (N rows of K), or null.
+static const void * f16_weights(const void * W, int64_t N, int64_t K) {
+    std::lock_guard<std::mutex> lk(g_f16w_mu);
+    if (g_f16w.empty()) {
+        return nullptr;
+    }
+    const auto it = g_f16w.find(W);
+    return it != g_f16w.end() && it->second.N == N && it->second.K == K ? it->second.wh : nullptr;
+}
+
+int weights_to_f16_checked(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, void * wh, hipStream_t stream) {
+    if (!W || !wh || !gemm_supported(wtype, N, K, rs, W, (const float *) wh, K)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "weights_to_f16: type %d N=%lld K=%lld rs=%lld", wtype, (long long) N,
+                         (long long) K, (long long) rs);
+    }
+    return weights_to_f16(wtype, (const uint8_t *) W, N, K, rs, (_Float16 *) wh, stream);
+}
+
 int gemm_q_h(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const void * xh, int64_t M, float * y,
              int64_t ldy, hipStream_t stream, const float * bias, const float * res, int64_t ldr, const GemmGlu * glu,
              const GemmMulti * mul, void * split_ws, size_t split_ws_bytes) {
@@ -910,8 +957,25 @@ int gemm_q_h(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const 
         spl.n    = gemm_split(N, K, M);
         spl.part = (float *) split_ws;
     }
-    return gemm_launch(wtype, (const uint8_t *) W, N, K, rs, (const _Float16 *) xh, M, bias, res, ldr, y, ldy,
-                       glu ? *glu : none, mul ? *mul : single, spl, stream);
+    // registered f16 copies (every matrix of a multi call): the DMA ring
+    GemmMulti    mf = mul ? *mul : single;
+    const void * wh = nullptr;
+    if (mul) {
+        bool all = mul->n > 0;
+        for (int i = 0; i < mul->n && all; i++) {
+            const void * p = f16_weights(mul->W[i], mul->Nper, K);
+            all            = p != nullptr;
+            mf.W[i]        = (const uint8_t *) p;
+        }
+        wh = all ? mf.W[0] : nullptr;
+        if (!all) {
+            mf = *mul;
+        }
+    } else {
+        wh = f16_weights(W, N, K);
+    }
+    return gemm_launch(wtype, (const uint8_t *) (wh ? wh : W), N, K, rs, (const _Float16 *) xh, M, bias, res, ldr, y,
+                       ldy, glu ? *glu : none, mf, spl, stream, wh != nullptr);
 }
 
 int convert_act_f16(const float * x, int64_t ldx, int64_t K, int64_t M, void * xh, hipStream_t stream) {
@@ -954,8 +1018,11 @@ int gemm_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const fl
         spl.n    = gemm_split(N, K, M);
         spl.part = (float *) ((char *) ws + so);
     }
-    const uint8_t * wb = (const uint8_t *) W;
-    if (wh) {
+    const uint8_t * wb  = (const uint8_t *) W;
+    const void *    reg = f16_weights(W, N, K);  // a registered f16 copy: no conversion
+    if (reg) {
+        wb = (const uint8_t *) reg;
+    } else if (wh) {
         _Float16 * whp = (_Float16 *) ((char *) ws + xo);
         rc             = weights_to_f16(wtype, wb, N, K, rs, whp, stream);
         if (rc != MMHIP_OK) {
@@ -963,7 +1030,8 @@ int gemm_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const fl
         }
         wb = (const uint8_t *) whp;
     }
-    return gemm_launch(wtype, wb, N, K, rs, xh, M, bias, res, ldr, y, ldy, glu ? *glu : none, single, spl, stream, wh);
+    return gemm_launch(wtype, wb, N, K, rs, xh, M, bias, res, ldr, y, ldy, glu ? *glu : none, single, spl, stream,
+                       wh || reg);
 }
 
 // BF16 weights at token counts: rows rs bytes apart read in place by the

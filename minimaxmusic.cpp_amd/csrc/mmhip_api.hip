@@ -84,6 +84,26 @@ extern "C" size_t mmhip_mul_mat_workspace(int type, int64_t N, int64_t K, int64_
     return act_layout(type, K, M).total;
 }
 
+extern "C" size_t mmhip_weights_f16_bytes(int64_t N, int64_t K) {
+    return N > 0 && K > 0 ? (size_t) N * (size_t) K * 2 : 0;
+}
+
+extern "C" int mmhip_weights_to_f16(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, void * wh,
+                                    void * stream) {
+    MMHIP_API_BEGIN();
+    return weights_to_f16_checked(type, W, N, K, w_row_stride, wh, (hipStream_t) stream);
+}
+
+extern "C" int mmhip_register_weights_f16(const void * W, int64_t N, int64_t K, const void * wh) {
+    MMHIP_API_BEGIN();
+    return register_f16_weights(W, N, K, wh);
+}
+
+extern "C" int mmhip_unregister_weights_f16(const void * W) {
+    MMHIP_API_BEGIN();
+    return unregister_f16_weights(W);
+}
+
 extern "C" size_t mmhip_mul_mat_h_workspace(int type, int64_t N, int64_t K, int64_t M) {
     return is_repacked_type(type) && use_gemm(type, M) ? gemm_split_bytes(N, K, M) : 0;
 }

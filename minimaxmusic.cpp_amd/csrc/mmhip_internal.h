@@ -118,6 +118,11 @@ size_t gemm_split_bytes(int64_t N, int64_t K, int64_t M);
 bool   gemm_use_wh(int64_t N, int64_t K, int64_t M);
 size_t gemm_wh_bytes(int64_t N, int64_t K, int64_t M);
 size_t gemm_q_workspace(int64_t N, int64_t K, int64_t M);
+// Registered f16 copies of quantised weights (k_w_to_f16's rows [N][K]),
+// which the token-count GEMMs use in place of converting per call.
+int register_f16_weights(const void * W, int64_t N, int64_t K, const void * wh);
+int unregister_f16_weights(const void * W);
+int weights_to_f16_checked(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, void * wh, hipStream_t stream);
 // BF16 weights: the GEMV takes up to this many activation rows, the GEMM more.
 constexpr int BF16_GEMV_MAXM = 16;
 // BF16 weights at token counts (rows rs bytes apart, read in place): the

@@ -68,6 +68,10 @@ SIGNATURES = {
                                          _vp]),
     "mmhip_mul_mat_bias_swiglu_h": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _i32, _vp, _vp, _vp]),
     "mmhip_mul_mat_h_workspace": (_sz, [_i32, _i64, _i64, _i64]),
+    "mmhip_weights_f16_bytes": (_sz, [_i64, _i64]),
+    "mmhip_weights_to_f16": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _vp]),
+    "mmhip_register_weights_f16": (_i32, [_vp, _i64, _i64, _vp]),
+    "mmhip_unregister_weights_f16": (_i32, [_vp]),
     "mmhip_mul_mat_bias_add_hw": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _sz,
                                          _vp]),
     "mmhip_mul_mat_multi": (_i32, [_i32, _i32, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),

@@ -88,6 +88,7 @@ def _load():
         "ggml_backend_mi355x_graph_stats": (None, [vp, ctypes.POINTER(i64), ctypes.POINTER(i64)]),
         "ggml_backend_mi355x_graph_cache_info": (None, [vp, ctypes.POINTER(i64), ctypes.POINTER(i64),
                                                         ctypes.POINTER(i64)]),
+        "ggml_backend_mi355x_f16_weight_bytes": (ctypes.c_size_t, []),
     }
     for n, (r, a) in misig.items():
         fn = getattr(mi, n)
@@ -255,6 +256,10 @@ class OpGraph:
         r, e = ctypes.c_int64(0), ctypes.c_int64(0)
         self.MI.ggml_backend_mi355x_graph_stats(self.backend, ctypes.byref(r), ctypes.byref(e))
         return r.value, e.value
+
+    def f16_weight_bytes(self):
+        """Bytes of f16 weight copies the backend holds (process-wide)."""
+        return int(self.MI.ggml_backend_mi355x_f16_weight_bytes())
 
     def graph_cache_info(self):
         """(graphs kept by the backend, of which captured, captures so far)."""

@@ -178,3 +178,84 @@ def test_split_k(mm, orc, pkg, t, N, K, M):
     rows = np.arange(0, M, 97)
     ref = orc.mul_mat_f64(t, raw, N, K, xn[rows]) + pkg.synth.normal_np((N,), 8200)[None] + res.cpu().numpy()[rows]
     assert cosine(y_split.cpu().numpy()[rows], ref) > 0.9999
+
+
+# f16 weight copies registered under the quantised weight (the backend's
+# copies for repeating graphs, such as the DiT's per diffusion step)
+
+@pytest.mark.parametrize("t,N,K,M,kind", [
+    (8, 2048, 2048, 1380, "bias_res_h"),   # the DiT's o projection: 64 x 128 ring tiles
+    (8, 16384, 2048, 1380, "swiglu_h"),    # ff_in with the SwiGLU epilogue: 256 x 256 ring tiles
+    (8, 2048, 8192, 1380, "split_h"),      # ff_out: split-K on the ring, then the ordered reduce
+    (8, 2048, 2048, 690, "multi_h"),       # q / k / v in one launch
+    (12, 6144, 2048, 300, "plain"),        # f32 activations below the per-call copy threshold
+    (14, 3000, 2048, 2100, "plain"),       # f32 activations above it (the registered copy replaces it)
+])
+def test_registered_f16_weights_give_the_same_bits(mm, pkg, t, N, K, M, kind):
+    """GEMMs above 16 tokens on weights with a registered f16 copy
+    (mmhip_weights_to_f16 + mmhip_register_weights_f16) read the copy through
+    the DMA ring and return the unregistered call's bits in every form; once
+    unregistered the same call takes its own path again.  A copy registered
+    for another shape is not used."""
+    L = mm.load()
+    nm = 3 if kind == "multi_h" else 1
+    Ws = [mm.QuantWeight.from_gguf(t, pkg.synth.gguf_blocks_np(t, N, K, 7300 + t + i), N, K) for i in range(nm)]
+    x = torch.from_numpy(pkg.synth.normal_np((M, K), 7400 + t)).cuda()
+    xh = x.half().contiguous()
+    b = torch.from_numpy(pkg.synth.normal_np((N,), 7500)).cuda()
+    r = torch.from_numpy(pkg.synth.normal_np((M, N), 7600)).cuda()
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rs = Ws[0].row_bytes
+
+    def run():
+        if kind == "swiglu_h":
+            h = torch.full((M, N // 2), float("nan"), device="cuda")
+            hh = torch.zeros((M, N // 2), dtype=torch.float16, device="cuda")
+            rc = L.mmhip_mul_mat_bias_swiglu_h(t, ptr(Ws[0].data), N, K, rs, ptr(xh), M, ptr(b), 0, ptr(h), ptr(hh), st)
+            outs = [h, hh]
+        elif kind == "multi_h":
+            ys = [torch.full((M, N), float("nan"), device="cuda") for _ in range(nm)]
+            rc = L.mmhip_mul_mat_multi_h(t, nm, _arr(ctypes.c_void_p, [W.data.data_ptr() for W in Ws]), N, K, rs,
+                                         ptr(xh), M, None, _arr(ctypes.c_void_p, [y.data_ptr() for y in ys]),
+                                         _arr(ctypes.c_int64, [N] * nm), st)
+            outs = ys
+        else:
+            y = torch.full((M, N), float("nan"), device="cuda")
+            if kind == "bias_res_h":
+                rc = L.mmhip_mul_mat_bias_add_h(t, ptr(Ws[0].data), N, K, rs, ptr(xh), M, ptr(b), ptr(r), N, ptr(y), N, st)
+            elif kind == "split_h":
+                need = L.mmhip_mul_mat_h_workspace(t, N, K, M)
+                assert need > 0
+                ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+                rc = L.mmhip_mul_mat_bias_add_hw(t, ptr(Ws[0].data), N, K, rs, ptr(xh), M, ptr(b), ptr(r), N, ptr(y),
+                                                 N, ptr(ws), need, st)
+            else:
+                need = L.mmhip_mul_mat_workspace(t, N, K, M)
+                ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+                rc = L.mmhip_mul_mat(t, ptr(Ws[0].data), N, K, rs, ptr(x), K, M, ptr(y), N, ptr(ws), need, st)
+            outs = [y]
+        assert rc == 0, L.mmhip_last_error()
+        torch.cuda.synchronize()
+        return outs
+
+    base = run()
+    copies = [torch.empty(L.mmhip_weights_f16_bytes(N, K), dtype=torch.uint8, device="cuda") for _ in Ws]
+    for W, c in zip(Ws, copies):
+        assert L.mmhip_weights_to_f16(t, ptr(W.data), N, K, rs, ptr(c), st) == 0, L.mmhip_last_error()
+        assert L.mmhip_register_weights_f16(ptr(W.data), N + 256, K, ptr(c)) == 0  # another shape: ignored
+    assert all(torch.equal(a, b_) for a, b_ in zip(run(), base))
+    try:
+        for W, c in zip(Ws, copies):
+            assert L.mmhip_register_weights_f16(ptr(W.data), N, K, ptr(c)) == 0
+        reg = run()
+    finally:
+        for W in Ws:
+            assert L.mmhip_unregister_weights_f16(ptr(W.data)) == 0
+    assert L.mmhip_unregister_weights_f16(ptr(Ws[0].data)) != 0  # already gone
+    after = run()
+    for a, c, d in zip(base, reg, after):
+        assert torch.equal(a.view(torch.int16 if a.dtype == torch.float16 else torch.int32),
+                           c.view(torch.int16 if c.dtype == torch.float16 else torch.int32))
+        assert torch.equal(a.view(torch.int16 if a.dtype == torch.float16 else torch.int32),
+                           d.view(torch.int16 if d.dtype == torch.float16 else torch.int32))
+    assert torch.isfinite(base[0]).all()

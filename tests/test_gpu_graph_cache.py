@@ -181,3 +181,49 @@ def test_backend_teardown_three_times(mods):
             assert np.array_equal(r, res[0])
         outs.append(res[0])
     assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+
+
+def test_f16_weight_copies_of_a_repeating_graph(mods, pkg, mm):
+    """A graph computed three or more times gets f16 copies of the weights its
+    token-count GEMMs multiply (registered with the kernel library, so the
+    GEMMs read them through the DMA ring): the results stay bit-identical
+    across the eager run, the first capture, the copies' creation with the
+    recapture it forces, and replays.  Uploading new weights afterwards
+    refreshes the copy in place: the next replay equals the C-ABI product of
+    the new weights.  Freeing the graph's buffers frees the copies."""
+    og = mods[0]
+    N, K, M = 2048, 2048, 300
+    g = og.OpGraph()
+    before = g.f16_weight_bytes()
+    try:
+        tw = g.tensor(og.Q8_0, [K, N])
+        tx = g.tensor(og.F32, [K, M])
+        tb = g.tensor(og.F32, [N])
+        out = g.add(g.mul_mat(tw, tx), tb)
+        g.build([out])
+        raw = pkg.synth.gguf_blocks_np(8, N, K, 7700)
+        x = pkg.synth.normal_np((M, K), 7701)
+        bias = pkg.synth.normal_np((N,), 7702)
+        g.set(tw, raw)
+        g.set(tx, x)
+        g.set(tb, bias)
+        ys = []
+        for _ in range(5):
+            g.compute()
+            ys.append(g.get(out))
+        assert all(np.array_equal(y.view(np.int32), ys[0].view(np.int32)) for y in ys)
+        assert g.f16_weight_bytes() >= before + N * K * 2
+        replays, _ = g.graph_stats()
+        assert replays >= 3
+        raw2 = pkg.synth.gguf_blocks_np(8, N, K, 7703)
+        g.set(tw, raw2)
+        g.compute()
+        y2 = g.get(out).reshape(M, N)
+    finally:
+        g.close()
+    assert g.f16_weight_bytes() == before
+    W2 = mm.QuantWeight.from_gguf(8, raw2, N, K)
+    ref = (mm.mul_mat(W2, __import__("torch").from_numpy(x).cuda()) +
+           __import__("torch").from_numpy(bias).cuda()).cpu().numpy()
+    assert np.array_equal(y2.view(np.int32), ref.view(np.int32))
+    assert not np.array_equal(y2.view(np.int32), ys[0].reshape(M, N).view(np.int32))
