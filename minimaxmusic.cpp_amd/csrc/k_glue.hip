@@ -265,6 +265,92 @@ __global__ __launch_bounds__(256) void k_layer_norm(TV x, float eps, const float
     }
 }
 
+// The same on rows held in registers: 16-byte aligned rows of n % 4 == 0
+// floats, n <= 1024 C, read once as float4 (the three passes above read each
+// row three times).  The same f32 steps; the double sums add each thread's
+// four consecutive values first, then across threads.
+template <int C>
+__global__ __launch_bounds__(256) void k_layer_norm_v(TV x, float eps, const float * __restrict__ w,
+                                                       const float * __restrict__ b, float * dst,
+                                                       _Float16 * __restrict__ dsth) {
+#pragma clang fp contract(off)
+    __shared__ double s_part[4];
+    const int64_t     row = blockIdx.x;
+    const int64_t     i1 = row % x.ne[1], i2 = (row / x.ne[1]) % x.ne[2], i3 = row / (x.ne[1] * x.ne[2]);
+    const int         n  = (int) x.ne[0], n4 = n / 4;
+    const float4_t *  xr = (const float4_t *) at(x, 0, i1, i2, i3);
+    float4_t          v[C];
+    double            sm = 0.0;
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+        const int j = threadIdx.x + 256 * c;
+        v[c]        = j < n4 ? xr[j] : float4_t{ 0.0f, 0.0f, 0.0f, 0.0f };
+        sm += (double) v[c][0] + (double) v[c][1] + (double) v[c][2] + (double) v[c][3];
+    }
+    sm = wave_sum_d(sm);
+    if ((threadIdx.x & 63) == 0) {
+        s_part[threadIdx.x >> 6] = sm;
+    }
+    __syncthreads();
+    const float mean = (float) ((s_part[0] + s_part[1] + s_part[2] + s_part[3]) / (double) n);
+    __syncthreads();
+    double ss = 0.0;
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+        if (threadIdx.x + 256 * c < n4) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float d = v[c][e] - mean;
+                ss += (double) (d * d);
+            }
+        }
+    }
+    ss = wave_sum_d(ss);
+    if ((threadIdx.x & 63) == 0) {
+        s_part[threadIdx.x >> 6] = ss;
+    }
+    __syncthreads();
+    const float var = (float) ((s_part[0] + s_part[1] + s_part[2] + s_part[3]) / (double) n);
+    const float sc  = 1.0f / sqrtf(var + eps);
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+        const int j = threadIdx.x + 256 * c;
+        if (j >= n4) {
+            continue;
+        }
+        float4_t t;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            t[e] = (v[c][e] - mean) * sc;
+        }
+        if (w) {
+            const float4_t wv = ((const float4_t *) w)[j];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                t[e] = t[e] * wv[e];
+            }
+        }
+        if (b) {
+            const float4_t bv = ((const float4_t *) b)[j];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                t[e] = t[e] + bv[e];
+            }
+        }
+        if (dst) {
+            ((float4_t *) (dst + row * n))[j] = t;
+        }
+        if (dsth) {
+            half4_t h;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                h[e] = (_Float16) t[e];
+            }
+            ((half4_t *) (dsth + row * n))[j] = h;
+        }
+    }
+}
+
 // GGML_OP_CONCAT of two f32 tensors along dim (src/dit.h:262-273): dst is
 // contiguous; an index below a's extent along dim reads a, the rest b.
 __global__ void k_concat(TV a, TV b, int dim, int64_t n, float * __restrict__ dst) {
@@ -1157,6 +1243,26 @@ extern "C" int mmhip_norm_affine_h(const mmhip_view * x, float eps, const float 
     }
     if (rows >= ((int64_t) 1 << 31) || nel(x) >= ((int64_t) 1 << 31)) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "norm: too many elements");
+    }
+    // rows read once into registers when they are whole 16-byte aligned float4s
+    auto          al = [](uint64_t v, uint64_t a) { return v % a == 0; };
+    const int64_t n  = x->ne[0];
+    const bool    vec = x->nb[0] == 4 && n % 4 == 0 && n <= 4096 && al((uintptr_t) x->data, 16) && al(x->nb[1], 16) &&
+                     al(x->nb[2], 16) && al(x->nb[3], 16) && (!dst || al((uintptr_t) dst, 16)) &&
+                     (!dsth || al((uintptr_t) dsth, 8)) && (!w || al((uintptr_t) w, 16)) && (!b || al((uintptr_t) b, 16));
+    if (vec) {
+        const TV xv = tv(x);
+        if (n <= 1024) {
+            hipLaunchKernelGGL(k_layer_norm_v<1>, dim3((unsigned) rows), dim3(256), 0, (hipStream_t) stream, xv, eps, w,
+                               b, dst, (_Float16 *) dsth);
+        } else if (n <= 2048) {
+            hipLaunchKernelGGL(k_layer_norm_v<2>, dim3((unsigned) rows), dim3(256), 0, (hipStream_t) stream, xv, eps, w,
+                               b, dst, (_Float16 *) dsth);
+        } else {
+            hipLaunchKernelGGL(k_layer_norm_v<4>, dim3((unsigned) rows), dim3(256), 0, (hipStream_t) stream, xv, eps, w,
+                               b, dst, (_Float16 *) dsth);
+        }
+        return check_launch("norm");
     }
     hipLaunchKernelGGL(k_layer_norm, dim3((unsigned) rows), dim3(256), 0, (hipStream_t) stream, tv(x), eps, w, b, dst,
                        (_Float16 *) dsth);
