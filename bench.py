@@ -812,7 +812,7 @@ def bench_depth(args, torch, pkg):
         "via_backend": {"path": "ggml_backend_graph_compute, MI355X backend, HIP-graph replay", "layers_per_graph": NL,
                         "gpu_us_per_stack": round(us, 2), "wall_us_per_stack": round(wall * 1e6, 2),
                         "replays": replays, "eager": eager},
-        "roofline": {"bound": "hbm", "kernel": "k_quant_q8_0 + k_gemv_q8_0_wide<4> (gate 6144x4096, 16 tokens)",
+        "roofline": {"bound": "hbm", "kernel": "k_quant_q8_0 + k_gemv_q8_0_mfma<2> (gate 6144x4096, 16 tokens, int8 MFMA)",
                      "achieved": round(alg / avg_s / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(alg / avg_s / 1e9 / HBM_PEAK_GBS, 4), "avg_launch_us": round(avg_s * 1e6, 2),
                      "min_launch_us": round(min_s * 1e6, 2), "alg_bytes_per_launch": alg,

@@ -854,6 +854,236 @@ __global__ __launch_bounds__(64 * PG_WAVES) void k_gemv_q8_0_wide(PgArgs a, cons
     }
 }
 
+// MUL_MAT of Q8_0 weights against 3..16 quantised activation columns on the
+// int8 MFMA (the depth decoder's projections at S x CFG tokens,
+// src/depth-decoder.h:206-257).  One 16-wave workgroup per CU copies the 16
+// columns (past M: zeros) and their block scales into LDS once, then takes
+// groups of 16 weight rows in turn, the 16 waves splitting each group's K
+// in chunks of two Q8_0 block pairs; the next group's weight loads are in
+// flight while the current one is computed.  Per pair, lane (r, q) (r =
+// lane % 16, q = lane / 16) loads bytes 16 q .. 16 q + 15 of row r's 64 pair
+// bytes; one v_permlane32_swap per dword turns the two halves into the B
+// operands of the pair's two v_mfma_i32_16x16x32_i8 (one block each, so
+// every block's integer sum is separate, as ggml's vec_dot): operand quad q'
+// of either block holds block bytes QMAP[q'] .. + 7, and the activation (A)
+// operand is read from LDS with the same map.  A lane's four sums are then
+// columns 4 q + i of one weight row, so it loads that row's scales only.  Each block's exact int32 sums
+// are scaled as ggml scales them, (float) isum * (d_w * d_x), and added in
+// block order per wave; the waves' partial sums are added in wave order.
+constexpr int MF_PC   = 2;   // block pairs per chunk
+constexpr int MF_PAD  = 32;  // LDS pitch padding of an activation column (bank spread)
+
+__device__ __forceinline__ int mf_qmap(int q) {
+    return (q & 1) * 16 + (q >> 1) * 8;  // 0, 16, 8, 24
+}
+
+struct MfChunk {
+    int4_t w[MF_PC];  // weight bytes of the lane's row, one 16-byte piece per pair
+    uint2  sw;        // f16 scales of the lane's row, the chunk's 4 blocks
+};
+constexpr int MF_LOADS = MF_PC + 1;  // load instructions of mf_load (the DMA wait counts them)
+
+struct MfArgs {
+    const uint8_t * W;
+    int64_t         N;
+    int             K;
+    int64_t         rs;
+    const int8_t *  xq;  // [M][K]
+    const float *   xd;  // [M][K / 32]
+    int             M;
+    float *         y;
+    int64_t         ldy;
+    const float *   res;
+    int64_t         ldr;
+};
+
+// chunk starting at pair p0 of row group g: weight pieces and row scales
+// (rows past N re-read row N - 1; chunks past the wave's range are not
+// loaded, their buffers not used)
+__device__ __forceinline__ void mf_load(MfChunk & b, const MfArgs & a, int64_t g, int p0, int r, int q) {
+    const int64_t row0 = g * 16;
+    const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+        (void *) (a.W + row0 * a.rs), (short) 0, (int) (min((int64_t) 16, a.N - row0) * a.rs), 0x00020000);
+    const int      nr = (int) min((int64_t) 16, a.N - row0);
+    const unsigned wo = (unsigned) (min(r, nr - 1) * (int) a.rs + 16 * q);
+#pragma unroll
+    for (int j = 0; j < MF_PC; j++) {
+        const int p = min(p0 + j, (int) (a.K / 64) - 1);
+        b.w[j]      = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(rr, wo, 64 * p, 0));
+    }
+    // scales of blocks 2 p0 .. 2 p0 + 3 (8-byte aligned: p0 even, K % 256 == 0)
+    const unsigned so = (unsigned) (min(r, nr - 1) * (int) a.rs + a.K);
+    b.sw              = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rr, so, 4 * p0, 0));
+}
+
+// the chunk's four blocks against the LDS columns; pairs at or past pe add
+// nothing (computed on a valid pair and not added: every register of the
+// chunk is read on every path, so no path leaves its loads outstanding)
+__device__ __forceinline__ void mf_acc(const MfChunk & b, const int8_t * s_x, const float * s_xd, int pitch,
+                                       int nb, int p0, int pe, int lane, float (&acc)[4]) {
+#pragma clang fp contract(off)
+    const int c = lane & 15, q = lane >> 4;
+#pragma unroll
+    for (int j = 0; j < MF_PC; j++) {
+        const bool use = p0 + j < pe;
+        const int  p   = use ? p0 + j : 0;
+        const auto lo = __builtin_amdgcn_permlane32_swap((unsigned) b.w[j].x, (unsigned) b.w[j].z, false, false);
+        const auto hi = __builtin_amdgcn_permlane32_swap((unsigned) b.w[j].y, (unsigned) b.w[j].w, false, false);
+        const long aa = (long) (((uint64_t) hi[0] << 32) | lo[0]);  // block 2 p
+        const long ab = (long) (((uint64_t) hi[1] << 32) | lo[1]);  // block 2 p + 1
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int4_t z   = { 0, 0, 0, 0 };
+            const uint2  xv  = *(const uint2 *) (s_x + c * pitch + 64 * p + 32 * h + mf_qmap(q));
+            const long   bx  = (long) (((uint64_t) xv.y << 32) | xv.x);
+            // D[column 4 q + i][row r]: the activations as the A operand,
+            // the weights as B, so a lane's four sums share one weight row
+            const int4_t   s   = __builtin_amdgcn_mfma_i32_16x16x32_i8(bx, h ? ab : aa, z, 0, 0, 0);
+            const int      blk = 2 * j + h;  // block of the chunk
+            const uint32_t wd  = blk >> 1 ? b.sw.y : b.sw.x;
+            const float    dw  = h2f((uint16_t) (blk & 1 ? wd >> 16 : wd & 0xffff));
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float dx = s_xd[(4 * q + i) * nb + 2 * p + h];
+                const float t  = acc[i] + (float) s[i] * (dw * dx);
+                acc[i]         = use ? t : acc[i];
+            }
+        }
+    }
+}
+
+// workgroup barrier ordering LDS accesses only (__syncthreads would also
+// wait for the output stores and the weight loads in flight)
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int MAXC>  // chunks per wave and row group (K <= 16 waves x MAXC x MF_PC x 64)
+__global__ __launch_bounds__(64 * PG_WAVES) void k_gemv_q8_0_mfma(MfArgs a) {
+    extern __shared__ __attribute__((aligned(16))) int8_t g_mf[];
+    const int pitch = a.K + MF_PAD;
+    const int nb    = a.K / 32;
+    int8_t *  s_x   = g_mf;                                           // [16][pitch]
+    float *   s_xd  = (float *) (g_mf + 16 * pitch);                  // [16][nb]
+    float *   s_pt  = s_xd + 16 * nb;                                 // [PG_WAVES][4][64]
+    const int lane  = threadIdx.x & 63;
+    const int wv    = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r     = lane & 15, q = lane >> 4;
+    const int np    = a.K / 64;                                  // block pairs per row
+    const int nch   = (np + MF_PC - 1) / MF_PC;                  // chunks per row, split over the waves
+    const int cb    = wv * nch / PG_WAVES, ce = (wv + 1) * nch / PG_WAVES;
+    const int pe    = min(ce * MF_PC, np);  // the wave's pairs: [cb MF_PC, pe)
+    const int64_t ng = (a.N + 15) / 16;
+    // 1. the M columns and their block scales DMA'd into LDS (global_load_lds,
+    // issued first: they return first), 1 KB of a column or 64 scales per
+    // instruction, instructions dealt round-robin to the waves; columns past
+    // M are not written (their outputs are not stored)
+    // (issued from inline asm, which the compiler does not track: its own
+    // tracking would wait for the whole DMA, and every load after it, at
+    // the barrier; this wave waits for its DMA itself below)
+    const uint32_t lbase = (uint32_t) (uintptr_t) (__attribute__((address_space(3))) int8_t *) g_mf;
+    const int      nxi = a.M * (a.K / 1024), nsi = (a.M * nb + 63) / 64;
+    int            ndma = 0;
+    for (int i = wv; i < nxi + nsi; i += PG_WAVES, ndma++) {
+        if (i < nxi) {
+            const int c = i / (a.K / 1024), u = i % (a.K / 1024);
+            asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                         ::"v"(a.xq + (int64_t) c * a.K + 1024 * u + 16 * lane), "s"(lbase + c * pitch + 1024 * u)
+                         : "memory", "m0");
+        } else {
+            // the last instruction's lanes past M nb re-read the last scale and
+            // land in the scales of column M (< 16 columns of room)
+            const int e = min(64 * (i - nxi) + lane, a.M * nb - 1);
+            asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off"
+                         ::"v"(a.xd + e), "s"(lbase + 16 * pitch + 4 * 64 * (i - nxi)) : "memory", "m0");
+        }
+    }
+    // 2. the first group's rows; every wave issues MAXC chunk loads per group
+    // (a chunk past its range re-reads the row's last chunk and is not
+    // used), so that the waits on them are the same on every path
+    MfChunk ca[MAXC], cn[MAXC];
+    int64_t g = blockIdx.x;
+#pragma unroll
+    for (int k = 0; k < MAXC; k++) {
+        mf_load(ca[k], a, g, min(cb + k, nch - 1) * MF_PC, r, q);
+    }
+    // 3. this wave's DMA done (the row loads issued after it may still fly),
+    // then every wave's
+    if (ndma > 0) {
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(MAXC * MF_LOADS) : "memory");
+    }
+    __syncthreads();
+    // one group: the next group's loads into nxt, the current from cur
+    auto group = [&](MfChunk (&cur)[MAXC], MfChunk (&nxt)[MAXC], int64_t gc) {
+        const int64_t gn = gc + gridDim.x;  // past the last group: the last group again
+        // output (row lane % 16, column 4 (lane / 16) + i) of lane l and
+        // register i is stored by thread t = 16 column + row (consecutive
+        // rows per column); its residual is loaded first (loads return in
+        // order: loaded after the next group's rows it would wait for them)
+        const int     ocol = (int) (threadIdx.x >> 4) & 15, orr = threadIdx.x & 15;
+        const int     ol = orr + 16 * (ocol >> 2), oi = ocol & 3;
+        const int64_t orow = gc * 16 + orr;
+        const bool    ost  = threadIdx.x < 256 && ocol < a.M && orow < a.N;
+        const float   ores = ost && a.res ? a.res[ocol * a.ldr + orow] : 0.0f;
+#pragma unroll
+        for (int k = 0; k < MAXC; k++) {
+            mf_load(nxt[k], a, min(gn, ng - 1), min(cb + k, nch - 1) * MF_PC, r, q);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // the next group's loads issue before this group's arithmetic
+        float acc[4] = { 0.0f, 0.0f, 0.0f, 0.0f };
+#pragma unroll
+        for (int k = 0; k < MAXC; k++) {
+            mf_acc(cur[k], s_x, s_xd, pitch, nb, (cb + k) * MF_PC, pe, lane, acc);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            s_pt[(wv * 4 + i) * 64 + lane] = acc[i];
+        }
+        lds_barrier();
+        if (threadIdx.x < 256) {
+            float t = s_pt[oi * 64 + ol];
+#pragma unroll
+            for (int w = 1; w < PG_WAVES; w++) {
+                t += s_pt[(w * 4 + oi) * 64 + ol];
+            }
+            if (ost) {
+                a.y[ocol * a.ldy + orow] = a.res ? t + ores : t;
+            }
+        }
+        lds_barrier();  // the partial sums are read before the next group writes them
+    };
+    // ping-pong between the two buffer sets (no register copies, which would
+    // wait for the next group's loads)
+    for (;;) {
+        group(ca, cn, g);
+        g += gridDim.x;
+        if (g >= ng) {
+            break;
+        }
+        group(cn, ca, g);
+        g += gridDim.x;
+        if (g >= ng) {
+            break;
+        }
+    }
+}
+
+static int64_t pg_cus();
+
+template <int MAXC> static int launch_mf(const MfArgs & a, hipStream_t stream) {
+    const int64_t ng   = (a.N + 15) / 16;
+    const int64_t wgs  = std::min<int64_t>(ng, pg_cus());
+    const size_t  lds  = (size_t) 16 * (a.K + MF_PAD) + (size_t) 16 * (a.K / 32) * 4 + (size_t) PG_WAVES * 4 * 64 * 4;
+    auto          kern = k_gemv_q8_0_mfma<MAXC>;
+    if (lds > 64 * 1024 && !ensure_lds_limit((const void *) kern, lds)) {
+        return set_error(MMHIP_ERR_HIP, "gemv (int8 MFMA): cannot raise LDS limit to %zu", lds);
+    }
+    hipLaunchKernelGGL(kern, dim3((unsigned) wgs), dim3(64 * PG_WAVES), lds, stream, a);
+    return check_launch("gemv (int8 MFMA, 3-16 columns)");
+}
+
 // The MLP's gate_up GEMV with the RMS norm in its prologue (as
 // k_gemv_q8_0_pro<PRO_NORM>) and the SwiGLU plus the down GEMV's Q8_0
 // activation quantisation in its epilogue: the arithmetic of
@@ -1348,6 +1578,17 @@ int gemv_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const Ac
         return gemv_q6_pro(W, N, K, rs, x, M, y, ldy, stream, r, ldr);
     }
     const uint8_t * wb = (const uint8_t *) W;
+    // the int8-MFMA GEMV at 9..16 columns, and at 3..8 columns for rows longer
+    // than 4096 (shorter rows at <= 8 columns: the column-group GEMV below is
+    // faster, one row per wave with no LDS staging or cross-wave sum)
+    static const bool mfma = getenv("GGML_MI355X_DISABLE_GEMV_MFMA") == nullptr;
+    if (mfma && wtype == TYPE_Q8_0 && (M >= 9 || (M >= 3 && K > 4096)) && M <= 16 && K % 1024 == 0 &&
+        K <= 16 * 3 * MF_PC * 64 &&
+        rs % 16 == 0 &&
+        (uintptr_t) W % 16 == 0 && (uintptr_t) x.qs % 16 == 0 && (uintptr_t) x.d % 16 == 0) {
+        const MfArgs a{ wb, N, (int) K, rs, x.qs, x.d, (int) M, y, ldy, r, ldr };
+        return K <= 16 * 2 * MF_PC * 64 ? launch_mf<2>(a, stream) : launch_mf<3>(a, stream);
+    }
     if (wtype == TYPE_Q8_0 && M > 8 && M <= 16 && K <= 8192 && K % 32 == 0) {
         return gemv_wide(wb, N, K, rs, x, M, y, ldy, stream, r, ldr);
     }

@@ -369,3 +369,16 @@ def test_gemm_f16_weight_copy_equals_register_path(mm, pkg, monkeypatch, t, N, K
     for a, c in zip(outs[0], outs[1]):
         assert torch.equal(a, c)
     assert torch.isfinite(outs[0][0]).all()
+
+
+@pytest.mark.parametrize("N,K", [(6144, 4096), (4096, 6144), (2048, 1024), (37, 256), (1000, 4096), (4106, 2048)])
+@pytest.mark.parametrize("M", [3, 4, 7, 9, 16])
+def test_gemv_q8_0_int8_mfma_columns(mm, orc, pkg, N, K, M):
+    """Q8_0 at 3..16 activation columns (the int8-MFMA GEMV: 16-row groups,
+    K split over the waves by block pairs, each block's int32 sum scaled as
+    ggml scales it): the depth decoder's projection shapes, a row count that
+    is not a multiple of 16 (last group partial, 10 of 16 rows), one-chunk
+    and uneven K splits, against the ggml-semantics and float64 oracles."""
+    y, yg, yf = run(mm, orc, pkg, 8, N, K, M, 7000 + N + K + M)
+    assert rel_err(y, yg) < 2e-5
+    assert cosine(y, yf) > 0.9999
