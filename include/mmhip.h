@@ -371,6 +371,15 @@ int mmhip_diag_mask_inf(const mmhip_view * a, int n_past, float * dst, void * st
 /* GGML_OP_SOFT_MAX without mask, scale 1 (src/depth-decoder.h:217, :348):
  * row softmax with ggml-CPU's steps (f32 exp, double sum); dst contiguous. */
 int mmhip_soft_max(const mmhip_view * a, float * dst, void * stream);
+/* The depth decoder's manual causal attention in one launch
+ * (src/depth-decoder.h:214-221): SOFT_MAX(DIAG_MASK_INF(SCALE(MUL_MAT(k, q)),
+ * n_past)) times the keys' V rows, written as CONT(PERMUTE(.., 0, 2, 1, 3)):
+ * q, k, v are [D, S, H, B] f32 views with contiguous dim 0 (k / v heads and
+ * batches may broadcast); SCALE is x * scale + bias; S_q, S_kv <= 16 and
+ * D <= 256 (else MMHIP_ERR_UNSUPPORTED); dst
+ * contiguous [D, H, S_q, B].  The same bits as the seven separate ops. */
+int mmhip_small_attn(const mmhip_view * q, const mmhip_view * k, const mmhip_view * v, float scale, float bias,
+                     int n_past, float * dst, void * stream);
 /* The depth decoder's in-graph CFG sampler (src/depth-decoder.h:345-361):
  * GGML_OP_ARGSORT descending (I32 indices, rows of <= 4096; equal values in
  * ascending index order), GGML_OP_CUMSUM along dim 0 (running f32 sum),

@@ -985,9 +985,12 @@ int run_node(mi_backend * c, const struct ggml_tensor * n) {
 //             those GEMVs' slot run in the gate_up GEMV's epilogue.
 //   MM_ADD    a GEMV MUL_MAT whose only consumer is an ADD with a same-shape
 //             residual: the ADD is done in the GEMV's store.
+//   SATTN     CONT(PERMUTE(MUL_MAT(CONT(TRANSPOSE(v)), SOFT_MAX(DIAG_MASK_INF(
+//             SCALE(MUL_MAT(k, q))))))): the depth decoder's manual causal
+//             attention (src/depth-decoder.h:214-221) in one launch.
 // MUL_MATs reading a slot skip their activation quantisation.
 
-enum step_kind { ST_NODE, ST_NORM, ST_SWIGLU_Q, ST_HEAD, ST_MM, ST_FA_Q, ST_GEMM, ST_LN, ST_GLU_V };
+enum step_kind { ST_NODE, ST_NORM, ST_SWIGLU_Q, ST_HEAD, ST_MM, ST_FA_Q, ST_GEMM, ST_LN, ST_GLU_V, ST_SATTN };
 
 struct plan_step {
     int                  kind = ST_NODE;
@@ -1184,6 +1187,124 @@ bool glu_into_gemvs(struct ggml_cgraph * g, const graph_info & gi, int i) {
 }
 
 // Try the HEAD chain starting at CONT node i; fills st and marks absorbed nodes.
+// The depth decoder's manual attention chain ending at CONT node i
+// (src/depth-decoder.h:214-221): CONT(PERMUTE_0213(m2)), m2 = MUL_MAT(vt, sm),
+// vt = CONT(TRANSPOSE(v)), sm = SOFT_MAX(dm) (no mask, scale 1), dm =
+// DIAG_MASK_INF(sc), sc = SCALE(m1), m1 = MUL_MAT(k, q), all f32 and each
+// intermediate read only by the next; S_q, S_kv <= 16, D <= 256.  Every node executed
+// between the chain's first and last node must be one of its own (views
+// otherwise), and the output must not overlap q, k or v (read until the end).
+bool plan_small_attn(struct ggml_cgraph * g, const graph_info & gi, int i, plan_step & st,
+                     std::vector<char> & absorbed) {
+    static const bool dbg = getenv("GGML_MI355X_PLAN_DEBUG") != nullptr;
+#define SATTN_NO(why)                                                         \
+    do {                                                                      \
+        if (dbg) {                                                            \
+            fprintf(stderr, "small_attn at node %d (%s): %s\n", i, n->name, why); \
+        }                                                                     \
+        return false;                                                         \
+    } while (0)
+    const struct ggml_tensor * n  = ggml_graph_node(g, i);
+    const struct ggml_tensor * pm = n->src[0];
+    if (n->type != GGML_TYPE_F32 || !ggml_is_contiguous(n) || !pm || pm->op != GGML_OP_PERMUTE ||
+        pm->op_params[0] != 0 || pm->op_params[1] != 2 || pm->op_params[2] != 1 || pm->op_params[3] != 3) {
+        return false;
+    }
+    const struct ggml_tensor * m2 = pm->src[0];
+    if (!m2 || m2->op != GGML_OP_MUL_MAT) {
+        return false;
+    }
+    const struct ggml_tensor * vt = m2->src[0];
+    const struct ggml_tensor * sm = m2->src[1];
+    if (vt->op != GGML_OP_CONT || !vt->src[0] || vt->src[0]->op != GGML_OP_TRANSPOSE || sm->op != GGML_OP_SOFT_MAX ||
+        sm->src[1] != nullptr) {
+        return false;
+    }
+    float sm_scale, sm_bias;
+    memcpy(&sm_scale, &sm->op_params[0], sizeof(float));
+    memcpy(&sm_bias, &sm->op_params[1], sizeof(float));
+    const struct ggml_tensor * dm = sm->src[0];
+    if (sm_scale != 1.0f || sm_bias != 0.0f || dm->op != GGML_OP_DIAG_MASK_INF) {
+        return false;
+    }
+    const struct ggml_tensor * sc = dm->src[0];
+    if (sc->op != GGML_OP_SCALE) {
+        return false;
+    }
+    const struct ggml_tensor * m1 = sc->src[0];
+    if (m1->op != GGML_OP_MUL_MAT) {
+        return false;
+    }
+    const struct ggml_tensor * q = m1->src[1];
+    const struct ggml_tensor * k = m1->src[0];
+    const struct ggml_tensor * v = vt->src[0]->src[0];
+    for (const struct ggml_tensor * t : { q, k, v }) {
+        if (t->type != GGML_TYPE_F32 || t->nb[0] != 4 || t->ne[0] != q->ne[0]) {
+            return false;
+        }
+    }
+    if (q->ne[1] > 16 || k->ne[1] > 16 || q->ne[0] > 256 || k->ne[1] != v->ne[1] || q->ne[1] <= 0 || k->ne[1] <= 0 ||
+        k->ne[2] <= 0 || v->ne[2] <= 0 || k->ne[3] <= 0 || v->ne[3] <= 0 || q->ne[2] % k->ne[2] != 0 ||
+        q->ne[3] % k->ne[3] != 0 || q->ne[2] % v->ne[2] != 0 || q->ne[3] % v->ne[3] != 0 ||
+        n->ne[0] != q->ne[0] || n->ne[1] != q->ne[2] || n->ne[2] != q->ne[1] || n->ne[3] != q->ne[3]) {
+        SATTN_NO("shapes");
+    }
+    if (overlaps(n, q) || overlaps(n, k) || overlaps(n, v)) {
+        SATTN_NO("output overlaps q / k / v");
+    }
+    // the chain's nodes: each read only by the next, none a graph output
+    const struct ggml_tensor * chain[] = { m1, sc, dm, sm, vt->src[0], vt, m2, pm };
+    int                        idx[8];
+    int                        lo = i;
+    for (int c = 0; c < 8; c++) {
+        idx[c] = node_index(gi, chain[c]);
+        if (idx[c] < 0 || idx[c] >= i || gi.uses[(size_t) idx[c]] != 1 || is_output(chain[c]) || absorbed[(size_t) idx[c]]) {
+            SATTN_NO(absorbed[(size_t) std::max(idx[c], 0)] ? "a chain node is in another fused step" : "chain node uses");
+        }
+        lo = std::min(lo, idx[c]);
+    }
+    // nodes run between the chain's first node and i (the graph's other
+    // branches, e.g. the q / k projections after CONT(TRANSPOSE(v))) must not
+    // write over an input produced before them: the allocator, which planned
+    // for the unfused order, may reuse an input's memory once its last
+    // (absorbed) reader has run
+    const struct ggml_tensor * ins[3] = { q, k, v };
+    int                        prod[3];
+    for (int x = 0; x < 3; x++) {
+        const struct ggml_tensor * b = ins[x];
+        while (b->view_src) {
+            b = b->view_src;
+        }
+        prod[x] = node_index(gi, b);  // -1: a leaf, produced before the graph
+    }
+    for (int t = lo + 1; t < i; t++) {
+        const struct ggml_tensor * nt  = ggml_graph_node(g, t);
+        const bool                 own = std::find(std::begin(idx), std::end(idx), t) != std::end(idx);
+        if (own || is_noop(nt->op)) {
+            continue;
+        }
+        for (int x = 0; x < 3; x++) {
+            if (prod[x] < t && overlaps(nt, ins[x])) {
+                SATTN_NO("a node inside the chain writes over an input");
+            }
+        }
+    }
+#undef SATTN_NO
+    if (dbg) {
+        fprintf(stderr, "small_attn at node %d (%s): fused\n", i, n->name);
+    }
+    st.kind = ST_SATTN;
+    st.node = i;
+    st.mm   = idx[0];  // m1: k = src0, q = src1
+    st.mul  = idx[1];  // SCALE
+    st.bias = idx[2];  // DIAG_MASK_INF
+    st.src  = idx[5];  // vt: v = its TRANSPOSE's source
+    for (int c : { 0, 1, 2, 3, 5, 6 }) {
+        absorbed[(size_t) idx[c]] = 1;
+    }
+    return true;
+}
+
 bool plan_head(struct ggml_cgraph * g, const graph_info & gi, int i, plan_step & st, std::vector<char> & absorbed) {
     const struct ggml_tensor * n0 = ggml_graph_node(g, i);
     const struct ggml_tensor * v  = n0->src[0];
@@ -1403,6 +1524,7 @@ graph_plan build_plan(struct ggml_cgraph * g) {
     std::vector<char>        glu_mm((size_t) gi.nn, 0);  // SWIGLU node done by its GEMVs
     const bool               no_glu_mm  = getenv("GGML_MI355X_DISABLE_SWIGLU_GEMV") != nullptr;
     const bool               no_glu_epi = getenv("GGML_MI355X_DISABLE_SWIGLU_EPILOGUE") != nullptr;
+    const bool               no_sattn   = getenv("GGML_MI355X_DISABLE_SMALL_ATTN") != nullptr;
     auto add_pending = [&](const plan_step & st) {
         step_at[(size_t) st.node] = (int) pending.size();
         pending.push_back(st);
@@ -1619,6 +1741,10 @@ graph_plan build_plan(struct ggml_cgraph * g) {
         }
         if (n->op == GGML_OP_CONT) {
             plan_step st;
+            if (!no_sattn && plan_small_attn(g, gi, i, st, absorbed)) {
+                add_pending(st);
+                continue;
+            }
             if (plan_head(g, gi, i, st, absorbed)) {
                 add_pending(st);
                 continue;
@@ -1772,9 +1898,11 @@ graph_plan build_plan(struct ggml_cgraph * g) {
                 const int                  oth = ad->op == GGML_OP_ADD ? (ad->src[0] == n ? 1 : ad->src[1] == n ? 0 : -1) : -1;
                 if (oth >= 0 && ad->src[oth] != n) {
                     const struct ggml_tensor * r = ad->src[oth];
+                    // rows over dims 1-3 collapse to M = ne1 ne2 ne3 rows of one
+                    // stride (the depth decoder's [DIM, S, B] residual stream)
                     if (r->type == GGML_TYPE_F32 && ggml_are_same_shape(r, n) && ggml_are_same_shape(ad, n) &&
-                        rows_contiguous_f32(ad) && r->nb[0] == 4 && r->ne[2] == 1 && r->ne[3] == 1 &&
-                        r->nb[1] % 4 == 0 && n->ne[2] == 1 && n->ne[3] == 1 && node_index(gi, r) < j) {
+                        rows_contiguous_f32(ad) && mm_collapsible(r) && ggml_is_contiguous(n) &&
+                        node_index(gi, r) < j) {
                         st.add     = j;
                         st.add_res = oth;
                         st.node    = j;
@@ -1939,6 +2067,18 @@ int run_step(mi_backend * c, struct ggml_cgraph * g, const plan_step & st, char 
         case ST_HEAD:
             rc = mmhip_head_rows_n(st.head, st.n_head, s);
             break;
+        case ST_SATTN: {
+            const struct ggml_tensor * m1 = ggml_graph_node(g, st.mm);
+            const struct ggml_tensor * sc = ggml_graph_node(g, st.mul);
+            const struct ggml_tensor * dm = ggml_graph_node(g, st.bias);
+            const struct ggml_tensor * vt = ggml_graph_node(g, st.src);
+            float                      scale, bias;
+            memcpy(&scale, &sc->op_params[0], sizeof(float));
+            memcpy(&bias, &sc->op_params[1], sizeof(float));
+            mmhip_view q = view_of(m1->src[1]), k = view_of(m1->src[0]), v = view_of(vt->src[0]->src[0]);
+            rc = mmhip_small_attn(&q, &k, &v, scale, bias, dm->op_params[0], (float *) n->data, s);
+            break;
+        }
         case ST_GLU_V: {
             const struct ggml_tensor * ga = st.src >= 0 ? ggml_graph_node(g, st.src)->src[0] : n->src[0];
             const struct ggml_tensor * gb = st.mul >= 0 ? ggml_graph_node(g, st.mul)->src[0] : n->src[1];

@@ -468,6 +468,93 @@ __global__ __launch_bounds__(256) void k_soft_max_rows(TV a, int64_t rows, float
     }
 }
 
+// The depth decoder's manual causal attention as one launch
+// (src/depth-decoder.h:214-221): scores = MUL_MAT(k, q), SCALE (x s + b),
+// DIAG_MASK_INF(n_past), SOFT_MAX, MUL_MAT(CONT(TRANSPOSE(v)), P) and the
+// CONT of its (0, 2, 1, 3) permutation.  One workgroup per (head, batch):
+// the head's q, k and v rows are copied into LDS first (every load in flight
+// at once), then each step repeats the separate kernels' arithmetic in their
+// order, so the output equals the seven-kernel chain's bit for bit:
+//   scores as k_mul_mat_f32_wave (lanes stride over d, f32 products summed in
+//   double, wave_sum_d), SCALE with two roundings, the mask, the softmax as
+//   k_soft_max_rows (one key per lane), P.V as k_mul_mat_f32 (a sequential
+//   double sum over the keys).
+// q, k, v: [D, S, H, B] views (d contiguous); dst contiguous [D, H, S_q, B].
+constexpr int SATT_MAXS = 16;   // queries and keys
+constexpr int SATT_MAXD = 256;  // head dim
+
+__global__ __launch_bounds__(256) void k_small_attn(TV q, TV k, TV v, float s, float bias, int n_past,
+                                                    float * __restrict__ dst) {
+#pragma clang fp contract(off)
+    __shared__ float sq[SATT_MAXS][SATT_MAXD], sk[SATT_MAXS][SATT_MAXD], sv[SATT_MAXS][SATT_MAXD];
+    __shared__ float sp[SATT_MAXS][SATT_MAXS];  // scores, then P: [query][key]
+    const int     D = (int) q.ne[0], Sq = (int) q.ne[1], Sk = (int) k.ne[1];
+    const int64_t H = q.ne[2];
+    const int64_t h = blockIdx.x % H, b = blockIdx.x / H;
+    const int64_t hk = h / (H / k.ne[2]), bk = b / (q.ne[3] / k.ne[3]);
+    const int64_t hv = h / (H / v.ne[2]), bv = b / (q.ne[3] / v.ne[3]);
+    const int     wv = threadIdx.x >> 6, l = threadIdx.x & 63;
+    // 0. the head's rows into LDS: every thread's loads issued before its stores
+    {
+        constexpr int PER = 3 * SATT_MAXS * SATT_MAXD / 256;
+        float         val[PER];
+#pragma unroll
+        for (int u = 0; u < PER; u++) {
+            const int e = (int) threadIdx.x + 256 * u;  // over [3][S][D]
+            const int which = e / (SATT_MAXS * SATT_MAXD), r = (e / SATT_MAXD) % SATT_MAXS, d = e % SATT_MAXD;
+            const int nr = which == 0 ? Sq : Sk;
+            val[u]       = 0.0f;
+            if (r < nr && d < D) {
+                const TV & t = which == 0 ? q : which == 1 ? k : v;
+                val[u] = *(const float *) (which == 0 ? at(t, d, r, h, b) : which == 1 ? at(t, d, r, hk, bk)
+                                                                                        : at(t, d, r, hv, bv));
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < PER; u++) {
+            const int e = (int) threadIdx.x + 256 * u;
+            const int which = e / (SATT_MAXS * SATT_MAXD), r = (e / SATT_MAXD) % SATT_MAXS, d = e % SATT_MAXD;
+            (which == 0 ? sq : which == 1 ? sk : sv)[r][d] = val[u];
+        }
+    }
+    __syncthreads();
+    // 1. scores, one wave per (query, key), then SCALE and DIAG_MASK_INF
+    for (int t = wv; t < Sq * Sk; t += 4) {
+        const int i = t / Sk, j = t % Sk;
+        double    acc = 0.0;
+        for (int d = l; d < D; d += 64) {
+            acc += (double) (sk[j][d] * sq[i][d]);
+        }
+        acc = wave_sum_d(acc);
+        if (l == 0) {
+            const float x = (float) acc * s + bias;
+            sp[i][j]      = j > n_past + i ? -INFINITY : x;
+        }
+    }
+    __syncthreads();
+    // 2. the softmax of each query row over its keys, one wave per row
+    for (int i = wv; i < Sq; i += 4) {
+        const float  x   = l < Sk ? sp[i][l] : -INFINITY;
+        const float  mx  = wave_max(x);
+        const float  e   = l < Sk ? expf(x - mx) : 0.0f;
+        const double sum = wave_sum_d(l < Sk ? (double) e : 0.0);
+        const float  is  = (float) (1.0 / sum);
+        if (l < Sk) {
+            sp[i][l] = e * is;
+        }
+    }
+    __syncthreads();
+    // 3. out[d, h, i, b] = sum_j v[d, j] p[i, j], keys in order
+    for (int t = threadIdx.x; t < D * Sq; t += 256) {
+        const int d = t % D, i = t / D;
+        double    acc = 0.0;
+        for (int j = 0; j < Sk; j++) {
+            acc += (double) (sv[j][d] * sp[i][j]);
+        }
+        dst[d + (int64_t) D * (h + H * (i + (int64_t) Sq * b))] = (float) acc;
+    }
+}
+
 // The depth decoder's in-graph sampler (src/depth-decoder.h:345-361).
 // GGML_OP_ARGSORT, descending: one workgroup per row of n <= 4096 f32 values,
 // a bitonic sort of (value, index) pairs in LDS padded with -inf; equal values
@@ -1324,6 +1411,35 @@ extern "C" int mmhip_soft_max(const mmhip_view * a, float * dst, void * stream) 
     hipLaunchKernelGGL(k_soft_max_rows, dim3((unsigned) ((rows + 3) / 4)), dim3(256), 0, (hipStream_t) stream, tv(a),
                        rows, dst);
     return check_launch("soft_max");
+}
+
+extern "C" int mmhip_small_attn(const mmhip_view * q, const mmhip_view * k, const mmhip_view * v, float scale,
+                                float bias, int n_past, float * dst, void * stream) {
+    MMHIP_API_BEGIN();
+    if (!q || !k || !v || !dst || q->ne[0] != k->ne[0] || q->ne[0] != v->ne[0] || k->ne[1] != v->ne[1] ||
+        q->nb[0] != 4 || k->nb[0] != 4 || v->nb[0] != 4) {
+        return set_error(MMHIP_ERR_INVALID, "small_attn: bad arguments");
+    }
+    for (const mmhip_view * t : { k, v }) {
+        if (t->ne[2] <= 0 || t->ne[3] <= 0 || q->ne[2] % t->ne[2] != 0 || q->ne[3] % t->ne[3] != 0) {
+            return set_error(MMHIP_ERR_INVALID, "small_attn: k / v heads or batches do not divide q's");
+        }
+    }
+    if (q->ne[1] > SATT_MAXS || k->ne[1] > SATT_MAXS || q->ne[1] <= 0 || k->ne[1] <= 0 || q->ne[0] <= 0 ||
+        q->ne[0] > SATT_MAXD) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "small_attn: S_q=%lld S_kv=%lld D=%lld (at most %d keys, D %d)",
+                         (long long) q->ne[1], (long long) k->ne[1], (long long) q->ne[0], SATT_MAXS, SATT_MAXD);
+    }
+    const int64_t wgs = q->ne[2] * q->ne[3];
+    if (wgs == 0) {
+        return MMHIP_OK;
+    }
+    if (wgs > 0x7fffffff || q->ne[0] * q->ne[1] > 0x7fffffff) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "small_attn: too large");
+    }
+    hipLaunchKernelGGL(k_small_attn, dim3((unsigned) wgs), dim3(256), 0, (hipStream_t) stream, tv(q), tv(k), tv(v), scale,
+                       bias, n_past, dst);
+    return check_launch("small_attn");
 }
 
 extern "C" int mmhip_argsort_desc(const mmhip_view * a, int32_t * dst, void * stream) {

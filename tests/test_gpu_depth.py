@@ -120,3 +120,96 @@ def test_diag_mask_inf_and_soft_max(mm):
     pv = torch.empty((2, 1000), device="cuda")
     assert L.mmhip_soft_max(ctypes.byref(mm.view_of(v[:, 24:])), ptr(pv), st()) == 0
     assert float((pv.cpu().double() - torch.softmax(v[:, 24:].cpu().double(), -1)).abs().max()) < 1e-6
+
+
+def _small_attn_chain(mm, q, k, v, scale, bias, n_past):
+    """The seven separate ops of src/depth-decoder.h:214-221 through the C-ABI:
+    MUL_MAT(k, q), SCALE, DIAG_MASK_INF, SOFT_MAX, CONT(TRANSPOSE(v)),
+    MUL_MAT(vt, P), CONT(PERMUTE(.., 0, 2, 1, 3)).  q, k, v: torch [B, H, S, D]
+    views (ggml [D, S, H, B])."""
+    L = mm.load()
+    V = lambda t: ctypes.byref(mm.view_of(t))
+    B, H, Sq, D = q.shape
+    Sk = k.shape[2]
+    sc = torch.empty((B, H, Sq, Sk), device="cuda")         # ggml [Sk, Sq, H, B]
+    assert L.mmhip_mul_mat_f32(V(k), V(q), ptr(sc), st()) == 0
+    s2 = torch.empty_like(sc)
+    assert L.mmhip_scale(V(sc), ctypes.c_float(scale), ctypes.c_float(bias), ptr(s2), st()) == 0
+    dm = torch.empty_like(sc)
+    assert L.mmhip_diag_mask_inf(V(s2), n_past, ptr(dm), st()) == 0
+    p = torch.empty_like(sc)
+    assert L.mmhip_soft_max(V(dm), ptr(p), st()) == 0
+    vt = v.transpose(2, 3).contiguous()                     # ggml [Sk, D, Hv, Bv] (a copy: the CONT)
+    o = torch.empty((B, H, Sq, D), device="cuda")           # ggml [D, Sq, H, B]
+    assert L.mmhip_mul_mat_f32(V(vt), V(p), ptr(o), st()) == 0
+    return o.permute(0, 2, 1, 3).contiguous()               # ggml [D, H, Sq, B]
+
+
+@pytest.mark.parametrize("B,H,Hkv,S,D,scale,bias,n_past",
+                         [(2, 16, 16, 8, 256, 0.0625, 0.0, 0), (1, 16, 16, 2, 256, 0.0625, 0.0, 0),
+                          (2, 16, 16, 16, 256, 0.0625, 0.0, 0), (2, 4, 2, 5, 64, 0.125, 0.5, 0),
+                          (1, 3, 3, 13, 96, 0.1, 0.0, 2), (2, 2, 1, 16, 128, 0.08, 0.0, 0)])
+def test_small_attn_equals_the_op_chain(mm, B, H, Hkv, S, D, scale, bias, n_past):
+    """mmhip_small_attn (the depth decoder's manual causal attention in one
+    launch) gives the bits of the seven separate ops: q / k / v as permuted
+    views of projection rows, k / v heads broadcast (Hkv < H), a SCALE bias,
+    n_past > 0, two to 16 keys, head dims up to 256."""
+    L = mm.load()
+    g = torch.Generator().manual_seed(900 + S * H + D)
+    # projection rows [B, S, H, D] permuted to [B, H, S, D]: strided views
+    q = (torch.randn((B, S, H, D), generator=g)).cuda().permute(0, 2, 1, 3)
+    k = (torch.randn((B, S, Hkv, D), generator=g)).cuda().permute(0, 2, 1, 3)
+    v = (torch.randn((B, S, Hkv, D), generator=g)).cuda().permute(0, 2, 1, 3)
+    ref = _small_attn_chain(mm, q, k, v, scale, bias, n_past)
+    out = torch.empty((B, S, H, D), device="cuda")
+    V = lambda t: ctypes.byref(mm.view_of(t))
+    assert L.mmhip_small_attn(V(q), V(k), V(v), ctypes.c_float(scale), ctypes.c_float(bias), n_past, ptr(out),
+                              st()) == 0
+    assert torch.equal(out, ref)
+    # and against float64 (causal softmax attention)
+    q64, k64, v64 = (t.cpu().double().repeat_interleave(H // t.shape[1], dim=1) for t in (q, k, v))
+    s64 = (q64 @ k64.transpose(-1, -2)) * np.float32(scale) + bias
+    s64 = s64.masked_fill(torch.triu(torch.ones(S, S, dtype=torch.bool), 1 + n_past), float("-inf"))
+    o64 = (torch.softmax(s64, -1) @ v64).permute(0, 2, 1, 3)
+    assert float((out.cpu().double() - o64).abs().max()) < 1e-5
+
+
+def test_small_attn_rejects_long_rows(mm):
+    L = mm.load()
+    q = torch.zeros((1, 1, 17, 64), device="cuda")
+    out = torch.empty((1, 17, 1, 64), device="cuda")
+    V = lambda t: ctypes.byref(mm.view_of(t))
+    assert L.mmhip_small_attn(V(q), V(q), V(q), ctypes.c_float(1.0), ctypes.c_float(0.0), 0, ptr(out), st()) == \
+        mm.ERR_UNSUPPORTED
+
+
+@pytest.mark.parametrize("S,B", [(8, 2), (3, 1)])
+def test_depth_layer_fusions_give_the_same_bits(pkg, S, B, monkeypatch):
+    """The depth layer through the backend with the manual attention as one
+    launch (and the output / down projections' residual ADDs in the GEMV
+    store over the [DIM, S, B] rows) equals the same graph with those two
+    fusions off, bit for bit."""
+    og = importlib.import_module(pkg.__name__ + ".opgraph")
+    dg = importlib.import_module(pkg.__name__ + ".depthgraph")
+    w = dg.synth_layer(81 + S)
+    x = np.random.default_rng(90 + S * B).standard_normal((B, S, dg.DIM)).astype(np.float32)
+
+    def run():
+        g = og.OpGraph()
+        try:
+            lw = dg.Layer(g)
+            tx = g.tensor(og.F32, [dg.DIM, S, B])
+            out = dg.build_layer(g, lw, tx, S, B)
+            g.build([out])
+            lw.upload(g, w)
+            g.set(tx, x)
+            g.compute()
+            return g.get(out)
+        finally:
+            g.close()
+
+    fused = run()
+    monkeypatch.setenv("GGML_MI355X_DISABLE_SMALL_ATTN", "1")
+    monkeypatch.setenv("GGML_MI355X_DISABLE_FUSION", "1")
+    plain = run()
+    assert np.array_equal(fused, plain)
