@@ -483,10 +483,11 @@ __global__ __launch_bounds__(256) void k_soft_max_rows(TV a, int64_t rows, float
 constexpr int SATT_MAXS = 16;   // queries and keys
 constexpr int SATT_MAXD = 256;  // head dim
 
-__global__ __launch_bounds__(256) void k_small_attn(TV q, TV k, TV v, float s, float bias, int n_past,
-                                                    float * __restrict__ dst) {
+__global__ __launch_bounds__(1024) void k_small_attn(TV q, TV k, TV v, float s, float bias, int n_past,
+                                                     float * __restrict__ dst) {
 #pragma clang fp contract(off)
-    __shared__ float sq[SATT_MAXS][SATT_MAXD], sk[SATT_MAXS][SATT_MAXD], sv[SATT_MAXS][SATT_MAXD];
+    __shared__ __attribute__((aligned(16))) float sq[SATT_MAXS][SATT_MAXD], sk[SATT_MAXS][SATT_MAXD],
+        sv[SATT_MAXS][SATT_MAXD];
     __shared__ float sp[SATT_MAXS][SATT_MAXS];  // scores, then P: [query][key]
     const int     D = (int) q.ne[0], Sq = (int) q.ne[1], Sk = (int) k.ne[1];
     const int64_t H = q.ne[2];
@@ -494,32 +495,55 @@ __global__ __launch_bounds__(256) void k_small_attn(TV q, TV k, TV v, float s, f
     const int64_t hk = h / (H / k.ne[2]), bk = b / (q.ne[3] / k.ne[3]);
     const int64_t hv = h / (H / v.ne[2]), bv = b / (q.ne[3] / v.ne[3]);
     const int     wv = threadIdx.x >> 6, l = threadIdx.x & 63;
-    // 0. the head's rows into LDS: every thread's loads issued before its stores
+    constexpr int NWV = 16;  // waves
+    // 0. the head's rows into LDS, 16 bytes per load when the rows allow it;
+    // every thread's loads issued before its stores
     {
-        constexpr int PER = 3 * SATT_MAXS * SATT_MAXD / 256;
-        float         val[PER];
+        const char * bq = at(q, 0, 0, h, b);
+        const char * bkp = at(k, 0, 0, hk, bk);
+        const char * bvp = at(v, 0, 0, hv, bv);
+        const bool   vec = D % 4 == 0 && ((((uintptr_t) bq | (uintptr_t) bkp | (uintptr_t) bvp) & 15) == 0) &&
+                         q.nb[1] % 16 == 0 && k.nb[1] % 16 == 0 && v.nb[1] % 16 == 0;
+        if (vec) {
+            constexpr int PER = 3 * SATT_MAXS * SATT_MAXD / 4 / 1024;  // float4 per thread
+            const int     D4  = D / 4;
+            float4_t      val[PER];
 #pragma unroll
-        for (int u = 0; u < PER; u++) {
-            const int e = (int) threadIdx.x + 256 * u;  // over [3][S][D]
-            const int which = e / (SATT_MAXS * SATT_MAXD), r = (e / SATT_MAXD) % SATT_MAXS, d = e % SATT_MAXD;
-            const int nr = which == 0 ? Sq : Sk;
-            val[u]       = 0.0f;
-            if (r < nr && d < D) {
-                const TV & t = which == 0 ? q : which == 1 ? k : v;
-                val[u] = *(const float *) (which == 0 ? at(t, d, r, h, b) : which == 1 ? at(t, d, r, hk, bk)
-                                                                                        : at(t, d, r, hv, bv));
+            for (int u = 0; u < PER; u++) {
+                const int e = (int) threadIdx.x + 1024 * u;  // float4 index over [3][S][D / 4]
+                // slot e: tensor `which`, row rr (rows past the tensor's are not loaded), float4 c
+                const int which = e / (SATT_MAXS * SATT_MAXD / 4), c = e % D4;
+                const int rr = (e % (SATT_MAXS * SATT_MAXD / 4)) / D4;
+                val[u]       = float4_t{ 0.0f, 0.0f, 0.0f, 0.0f };
+                if (rr < (which == 0 ? Sq : Sk)) {
+                    const char * base = which == 0 ? bq + rr * q.nb[1] : which == 1 ? bkp + rr * k.nb[1]
+                                                                                    : bvp + rr * v.nb[1];
+                    val[u] = *(const float4_t *) (base + 16 * c);
+                }
             }
-        }
 #pragma unroll
-        for (int u = 0; u < PER; u++) {
-            const int e = (int) threadIdx.x + 256 * u;
-            const int which = e / (SATT_MAXS * SATT_MAXD), r = (e / SATT_MAXD) % SATT_MAXS, d = e % SATT_MAXD;
-            (which == 0 ? sq : which == 1 ? sk : sv)[r][d] = val[u];
+            for (int u = 0; u < PER; u++) {
+                const int e = (int) threadIdx.x + 1024 * u;
+                const int which = e / (SATT_MAXS * SATT_MAXD / 4), c = e % D4;
+                const int rr = (e % (SATT_MAXS * SATT_MAXD / 4)) / D4;
+                if (rr < SATT_MAXS) {
+                    *(float4_t *) &(which == 0 ? sq : which == 1 ? sk : sv)[rr][4 * c] = val[u];
+                }
+            }
+        } else {
+            for (int e = threadIdx.x; e < 3 * SATT_MAXS * D; e += 1024) {
+                const int which = e / (SATT_MAXS * D), r = (e / D) % SATT_MAXS, d = e % D;
+                if (r < (which == 0 ? Sq : Sk)) {
+                    (which == 0 ? sq : which == 1 ? sk : sv)[r][d] =
+                        *(const float *) (which == 0 ? at(q, d, r, h, b) : which == 1 ? at(k, d, r, hk, bk)
+                                                                                      : at(v, d, r, hv, bv));
+                }
+            }
         }
     }
     __syncthreads();
     // 1. scores, one wave per (query, key), then SCALE and DIAG_MASK_INF
-    for (int t = wv; t < Sq * Sk; t += 4) {
+    for (int t = wv; t < Sq * Sk; t += NWV) {
         const int i = t / Sk, j = t % Sk;
         double    acc = 0.0;
         for (int d = l; d < D; d += 64) {
@@ -533,7 +557,7 @@ __global__ __launch_bounds__(256) void k_small_attn(TV q, TV k, TV v, float s, f
     }
     __syncthreads();
     // 2. the softmax of each query row over its keys, one wave per row
-    for (int i = wv; i < Sq; i += 4) {
+    for (int i = wv; i < Sq; i += NWV) {
         const float  x   = l < Sk ? sp[i][l] : -INFINITY;
         const float  mx  = wave_max(x);
         const float  e   = l < Sk ? expf(x - mx) : 0.0f;
@@ -545,7 +569,7 @@ __global__ __launch_bounds__(256) void k_small_attn(TV q, TV k, TV v, float s, f
     }
     __syncthreads();
     // 3. out[d, h, i, b] = sum_j v[d, j] p[i, j], keys in order
-    for (int t = threadIdx.x; t < D * Sq; t += 256) {
+    for (int t = threadIdx.x; t < D * Sq; t += 1024) {
         const int d = t % D, i = t / D;
         double    acc = 0.0;
         for (int j = 0; j < Sk; j++) {
@@ -1437,8 +1461,8 @@ extern "C" int mmhip_small_attn(const mmhip_view * q, const mmhip_view * k, cons
     if (wgs > 0x7fffffff || q->ne[0] * q->ne[1] > 0x7fffffff) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "small_attn: too large");
     }
-    hipLaunchKernelGGL(k_small_attn, dim3((unsigned) wgs), dim3(256), 0, (hipStream_t) stream, tv(q), tv(k), tv(v), scale,
-                       bias, n_past, dst);
+    hipLaunchKernelGGL(k_small_attn, dim3((unsigned) wgs), dim3(1024), 0, (hipStream_t) stream, tv(q), tv(k), tv(v),
+                       scale, bias, n_past, dst);
     return check_launch("small_attn");
 }
 
