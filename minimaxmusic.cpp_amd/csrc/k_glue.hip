@@ -1219,6 +1219,52 @@ __global__ void k_rope_neox_heads(TV x, const int32_t * __restrict__ pos, int n_
     }
 }
 
+// NeoX RoPE with one workgroup per position (i2, i3): the n_dims / 2
+// angles of the position computed once into LDS (theta = pos, multiplied
+// by theta_scale once per pair index, as k_rope_neox_heads does), then the
+// position's rows (every head) four elements per thread, consecutive threads
+// on consecutive elements, each reading its own 16 bytes and its partner's
+// (d +- n_dims / 2).  Rows with contiguous elements, D and n_dims / 2
+// multiples of 4.  The arithmetic of k_rope_neox_heads, so the same bits.
+__global__ __launch_bounds__(256) void k_rope_neox_pos(TV x, const int32_t * __restrict__ pos, int n_dims,
+                                                       float theta_scale, float * __restrict__ dst) {
+#pragma clang fp contract(off)
+    __shared__ float s_c[128], s_s[128];  // n_dims / 2 <= 128
+    const int64_t i2 = blockIdx.x % x.ne[2], i3 = blockIdx.x / x.ne[2];
+    const int     D = (int) x.ne[0], half = n_dims / 2, D4 = D / 4, H = (int) x.ne[1];
+    for (int j = threadIdx.x; j < half; j += 256) {
+        float theta = (float) pos[i2];
+        for (int k = 0; k < j; k++) {
+            theta *= theta_scale;
+        }
+        s_c[j] = cosf(theta);
+        s_s[j] = sinf(theta);
+    }
+    __syncthreads();
+    const char * xb = x.data + i2 * x.nb[2] + i3 * x.nb[3];
+    float *      dp = dst + (i3 * x.ne[2] + i2) * (int64_t) H * D;
+    for (int e4 = threadIdx.x; e4 < H * D4; e4 += 256) {
+        const int      i1 = e4 / D4, d = 4 * (e4 - i1 * D4);
+        const float *  xr = (const float *) (xb + (int64_t) i1 * x.nb[1]);
+        const float4_t a  = *(const float4_t *) (xr + d);
+        float4_t       o  = a;
+        if (d < half) {
+            const float4_t b = *(const float4_t *) (xr + d + half);
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                o[u] = a[u] * s_c[d + u] - b[u] * s_s[d + u];
+            }
+        } else if (d < n_dims) {
+            const float4_t b = *(const float4_t *) (xr + d - half);
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                o[u] = b[u] * s_s[d - half + u] + a[u] * s_c[d - half + u];
+            }
+        }
+        *(float4_t *) (dp + (int64_t) i1 * D + d) = o;
+    }
+}
+
 extern "C" int mmhip_rope_neox(const mmhip_view * x, const int32_t * pos, int n_dims, float theta_scale, float * dst,
                                void * stream) {
     MMHIP_API_BEGIN();
@@ -1229,6 +1275,13 @@ extern "C" int mmhip_rope_neox(const mmhip_view * x, const int32_t * pos, int n_
     const int64_t total = rows * (n_dims / 2 + (x->ne[0] - n_dims));
     if (total == 0) {
         return MMHIP_OK;
+    }
+    if (n_dims <= 256 && (n_dims / 2) % 4 == 0 && x->ne[0] % 4 == 0 && x->nb[0] == 4 && x->nb[1] % 16 == 0 &&
+        x->nb[2] % 16 == 0 && x->nb[3] % 16 == 0 && ((uintptr_t) x->data) % 16 == 0 && ((uintptr_t) dst) % 16 == 0 &&
+        x->ne[2] * x->ne[3] <= 0x7fffffff && x->ne[0] * x->ne[1] <= 0x7fffffff) {
+        hipLaunchKernelGGL(k_rope_neox_pos, dim3((unsigned) (x->ne[2] * x->ne[3])), dim3(256), 0, (hipStream_t) stream,
+                           tv(x), pos, n_dims, theta_scale, dst);
+        return check_launch("rope");
     }
     if (x->ne[1] >= RH && n_dims >= 2) {
         const int64_t items = (n_dims / 2) * ((x->ne[1] + RH - 1) / RH) * x->ne[2] * x->ne[3];
