@@ -380,6 +380,13 @@ int mmhip_soft_max(const mmhip_view * a, float * dst, void * stream);
  * contiguous [D, H, S_q, B].  The same bits as the seven separate ops. */
 int mmhip_small_attn(const mmhip_view * q, const mmhip_view * k, const mmhip_view * v, float scale, float bias,
                      int n_past, float * dst, void * stream);
+/* mmhip_small_attn that also quantises its output rows (D x H values, S_q x B
+ * rows) for the following projection (src/depth-decoder.h:222-223,
+ * MUL_MAT(wo, attn)) into xq, laid out as mmhip_quantize_act writes
+ * (mmhip_act_bytes(qtype, D * H, S_q * B) bytes), with the same bits;
+ * qtype 0 = no quantisation, else GGML_TYPE_Q8_0 (8) with D % 32 == 0. */
+int mmhip_small_attn_q(const mmhip_view * q, const mmhip_view * k, const mmhip_view * v, float scale, float bias,
+                       int n_past, float * dst, int qtype, void * xq, void * stream);
 /* The depth decoder's in-graph CFG sampler (src/depth-decoder.h:345-361):
  * GGML_OP_ARGSORT descending (I32 indices, rows of <= 4096; equal values in
  * ascending index order), GGML_OP_CUMSUM along dim 0 (running f32 sum),

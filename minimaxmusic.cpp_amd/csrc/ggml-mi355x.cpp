@@ -1937,6 +1937,16 @@ graph_plan build_plan(struct ggml_cgraph * g) {
                     fs.vec_wtype = st.vec_wtype;
                     add_pending(fs);
                     st.src = -1;
+                } else if (fi >= 0 && fi < i && step_at[(size_t) fi] >= 0 &&
+                           pending[(size_t) step_at[(size_t) fi]].kind == ST_SATTN && st.vec_wtype == GGML_TYPE_Q8_0 &&
+                           fa->ne[0] % 32 == 0 && ggml_is_contiguous(x) && fa->ne[0] * fa->ne[1] == x->ne[0] &&
+                           fa->ne[2] * fa->ne[3] == x->ne[1] * x->ne[2] * x->ne[3]) {
+                    // the one-launch manual attention quantises its output
+                    // rows the same way
+                    plan_step & as = pending[(size_t) step_at[(size_t) fi]];
+                    as.slot_out    = st.slot_in;
+                    as.vec_wtype   = st.vec_wtype;
+                    st.src         = -1;
                 }
             }
             if (st.slot_in >= 0 || st.add >= 0 || st.norm >= 0 || st.glu >= 0) {
@@ -2076,7 +2086,9 @@ int run_step(mi_backend * c, struct ggml_cgraph * g, const plan_step & st, char 
             memcpy(&scale, &sc->op_params[0], sizeof(float));
             memcpy(&bias, &sc->op_params[1], sizeof(float));
             mmhip_view q = view_of(m1->src[1]), k = view_of(m1->src[0]), v = view_of(vt->src[0]->src[0]);
-            rc = mmhip_small_attn(&q, &k, &v, scale, bias, dm->op_params[0], (float *) n->data, s);
+            rc = mmhip_small_attn_q(&q, &k, &v, scale, bias, dm->op_params[0], (float *) n->data,
+                                    st.slot_out >= 0 ? st.vec_wtype : 0, st.slot_out >= 0 ? slot + st.slot_out : nullptr,
+                                    s);
             break;
         }
         case ST_GLU_V: {

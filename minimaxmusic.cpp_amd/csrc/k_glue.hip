@@ -484,7 +484,8 @@ constexpr int SATT_MAXS = 16;   // queries and keys
 constexpr int SATT_MAXD = 256;  // head dim
 
 __global__ __launch_bounds__(1024) void k_small_attn(TV q, TV k, TV v, float s, float bias, int n_past,
-                                                     float * __restrict__ dst) {
+                                                     float * __restrict__ dst, int8_t * __restrict__ xq_qs,
+                                                     float * __restrict__ xq_d) {
 #pragma clang fp contract(off)
     __shared__ __attribute__((aligned(16))) float sq[SATT_MAXS][SATT_MAXD], sk[SATT_MAXS][SATT_MAXD],
         sv[SATT_MAXS][SATT_MAXD];
@@ -575,7 +576,20 @@ __global__ __launch_bounds__(1024) void k_small_attn(TV q, TV k, TV v, float s, 
         for (int j = 0; j < Sk; j++) {
             acc += (double) (sv[j][d] * sp[i][j]);
         }
-        dst[d + (int64_t) D * (h + H * (i + (int64_t) Sq * b))] = (float) acc;
+        const float   o   = (float) acc;
+        const int64_t row = i + (int64_t) Sq * b, e = d + (int64_t) D * h, K = D * H;
+        dst[e + K * row] = o;
+        if (xq_qs) {
+            // the output row's Q8_0 activation blocks (32 consecutive d of one
+            // query, D % 32 == 0) with k_quant_q8_0's arithmetic
+            const float a  = group32_max(fabsf(o));
+            const float dd = a / 127.0f;
+            const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+            xq_qs[row * K + e] = (int8_t) roundf(o * id);
+            if ((d & 31) == 0) {
+                xq_d[row * (K / 32) + e / 32] = h2f(f2h(dd));
+            }
+        }
     }
 }
 
@@ -1492,6 +1506,11 @@ extern "C" int mmhip_soft_max(const mmhip_view * a, float * dst, void * stream) 
 
 extern "C" int mmhip_small_attn(const mmhip_view * q, const mmhip_view * k, const mmhip_view * v, float scale,
                                 float bias, int n_past, float * dst, void * stream) {
+    return mmhip_small_attn_q(q, k, v, scale, bias, n_past, dst, 0, nullptr, stream);
+}
+
+extern "C" int mmhip_small_attn_q(const mmhip_view * q, const mmhip_view * k, const mmhip_view * v, float scale,
+                                  float bias, int n_past, float * dst, int qtype, void * xq, void * stream) {
     MMHIP_API_BEGIN();
     if (!q || !k || !v || !dst || q->ne[0] != k->ne[0] || q->ne[0] != v->ne[0] || k->ne[1] != v->ne[1] ||
         q->nb[0] != 4 || k->nb[0] != 4 || v->nb[0] != 4) {
@@ -1514,8 +1533,20 @@ extern "C" int mmhip_small_attn(const mmhip_view * q, const mmhip_view * k, cons
     if (wgs > 0x7fffffff || q->ne[0] * q->ne[1] > 0x7fffffff) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "small_attn: too large");
     }
+    int8_t * xq_qs = nullptr;
+    float *  xq_d  = nullptr;
+    if (qtype != 0) {
+        // the output rows (D x H values each, S_q x B of them) quantised for Q8_0 weights
+        const ActLayout L = act_layout(qtype, q->ne[0] * q->ne[2], q->ne[1] * q->ne[3]);
+        if (qtype != TYPE_Q8_0 || L.vec_type != TYPE_Q8_0 || q->ne[0] % 32 != 0 || !xq) {
+            return set_error(MMHIP_ERR_UNSUPPORTED, "small_attn: quantisation for weight type %d at D=%lld", qtype,
+                             (long long) q->ne[0]);
+        }
+        xq_qs = (int8_t *) ((uint8_t *) xq + L.qs_off);
+        xq_d  = (float *) ((uint8_t *) xq + L.d_off);
+    }
     hipLaunchKernelGGL(k_small_attn, dim3((unsigned) wgs), dim3(1024), 0, (hipStream_t) stream, tv(q), tv(k), tv(v),
-                       scale, bias, n_past, dst);
+                       scale, bias, n_past, dst, xq_qs, xq_d);
     return check_launch("small_attn");
 }
 

@@ -116,6 +116,7 @@ SIGNATURES = {
     "mmhip_diag_mask_inf": (_i32, [_VP, _i32, _vp, _vp]),
     "mmhip_soft_max": (_i32, [_VP, _vp, _vp]),
     "mmhip_small_attn": (_i32, [_VP, _VP, _VP, _f32, _f32, _i32, _vp, _vp]),
+    "mmhip_small_attn_q": (_i32, [_VP, _VP, _VP, _f32, _f32, _i32, _vp, _i32, _vp, _vp]),
     "mmhip_argsort_desc": (_i32, [_VP, _vp, _vp]),
     "mmhip_cumsum": (_i32, [_VP, _vp, _vp]),
     "mmhip_sum": (_i32, [_VP, _vp, _vp]),

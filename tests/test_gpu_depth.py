@@ -166,6 +166,19 @@ def test_small_attn_equals_the_op_chain(mm, B, H, Hkv, S, D, scale, bias, n_past
     assert L.mmhip_small_attn(V(q), V(k), V(v), ctypes.c_float(scale), ctypes.c_float(bias), n_past, ptr(out),
                               st()) == 0
     assert torch.equal(out, ref)
+    if D % 32 == 0:
+        # the quantising form: the same f32 rows, and their Q8_0 activation
+        # blocks byte-equal to mmhip_quantize_act over those rows
+        K, M = H * D, S * B
+        xq = torch.full((L.mmhip_act_bytes(8, K, M),), 0x5A, dtype=torch.uint8, device="cuda")
+        ref_q = torch.full_like(xq, 0x5A)
+        out2 = torch.full_like(out, float("nan"))
+        assert L.mmhip_small_attn_q(V(q), V(k), V(v), ctypes.c_float(scale), ctypes.c_float(bias), n_past,
+                                    ptr(out2), 8, ptr(xq), st()) == 0
+        assert L.mmhip_quantize_act(8, ptr(out), K, K, M, ptr(ref_q), st()) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(out2, ref)
+        assert torch.equal(xq, ref_q)
     # and against float64 (causal softmax attention)
     q64, k64, v64 = (t.cpu().double().repeat_interleave(H // t.shape[1], dim=1) for t in (q, k, v))
     s64 = (q64 @ k64.transpose(-1, -2)) * np.float32(scale) + bias
@@ -181,6 +194,16 @@ def test_small_attn_rejects_long_rows(mm):
     V = lambda t: ctypes.byref(mm.view_of(t))
     assert L.mmhip_small_attn(V(q), V(q), V(q), ctypes.c_float(1.0), ctypes.c_float(0.0), 0, ptr(out), st()) == \
         mm.ERR_UNSUPPORTED
+    # quantisation only for Q8_0 weights and head dims of whole blocks
+    q = torch.zeros((1, 1, 4, 48), device="cuda")
+    out = torch.empty((1, 4, 1, 48), device="cuda")
+    xq = torch.empty(4096, dtype=torch.uint8, device="cuda")
+    assert L.mmhip_small_attn_q(V(q), V(q), V(q), ctypes.c_float(1.0), ctypes.c_float(0.0), 0, ptr(out), 8, ptr(xq),
+                                st()) == mm.ERR_UNSUPPORTED
+    q = torch.zeros((1, 1, 4, 64), device="cuda")
+    out = torch.empty((1, 4, 1, 64), device="cuda")
+    assert L.mmhip_small_attn_q(V(q), V(q), V(q), ctypes.c_float(1.0), ctypes.c_float(0.0), 0, ptr(out), 12,
+                                ptr(xq), st()) == mm.ERR_UNSUPPORTED
 
 
 @pytest.mark.parametrize("S,B", [(8, 2), (3, 1)])
