@@ -331,6 +331,14 @@ int mmhip_swiglu_quant(const mmhip_view * a, const mmhip_view * b, int swapped, 
  * powf(freq_base, -2/n_dims) computed by the caller. */
 int mmhip_rope_neox(const mmhip_view * x, const int32_t * pos, int n_dims, float theta_scale, float * dst,
                     void * stream);
+/* mmhip_rope_neox whose result is rounded to f16 (as GGML_OP_CPY rounds) and
+ * stored through the strided f16 view dst (same ne as x; nb[0] == 2): the
+ * DiT's ggml_cast(ggml_permute(ggml_rope_ext(k))) to F16 (src/dit.h:207-220)
+ * as one launch, dst being the cast's rows seen in the rope's dim order.
+ * Takes n_dims <= 256 with n_dims / 2 % 4 == 0, ne0 % 4 == 0, 16-byte
+ * aligned x rows and 8-byte aligned dst rows (else MMHIP_ERR_UNSUPPORTED). */
+int mmhip_rope_neox_f16(const mmhip_view * x, const int32_t * pos, int n_dims, float theta_scale,
+                        const mmhip_view * dst, void * stream);
 /* GGML_OP_CPY / GGML_OP_CONT between f32 and f16 views of equal element count:
  * src/qwen3-lm.h:775-777, src/dit.h:219-220 (f32 -> f16 cast). */
 int mmhip_cpy(const mmhip_view * src, int src_type, const mmhip_view * dst, int dst_type, void * stream);

@@ -988,9 +988,12 @@ int run_node(mi_backend * c, const struct ggml_tensor * n) {
 //   SATTN     CONT(PERMUTE(MUL_MAT(CONT(TRANSPOSE(v)), SOFT_MAX(DIAG_MASK_INF(
 //             SCALE(MUL_MAT(k, q))))))): the depth decoder's manual causal
 //             attention (src/depth-decoder.h:214-221) in one launch.
+//   ROPE_H    CPY(PERMUTE(ROPE(x))) to F16 (the DiT's K cast,
+//             src/dit.h:207-220): the rotation stores f16 straight into the
+//             cast's rows.
 // MUL_MATs reading a slot skip their activation quantisation.
 
-enum step_kind { ST_NODE, ST_NORM, ST_SWIGLU_Q, ST_HEAD, ST_MM, ST_FA_Q, ST_GEMM, ST_LN, ST_GLU_V, ST_SATTN };
+enum step_kind { ST_NODE, ST_NORM, ST_SWIGLU_Q, ST_HEAD, ST_MM, ST_FA_Q, ST_GEMM, ST_LN, ST_GLU_V, ST_SATTN, ST_ROPE_H };
 
 struct plan_step {
     int                  kind = ST_NODE;
@@ -1194,6 +1197,57 @@ bool glu_into_gemvs(struct ggml_cgraph * g, const graph_info & gi, int i) {
 // intermediate read only by the next; S_q, S_kv <= 16, D <= 256.  Every node executed
 // between the chain's first and last node must be one of its own (views
 // otherwise), and the output must not overlap q, k or v (read until the end).
+// The f16 view a ROPE_H step writes: the rope's shape, and per rope dim the
+// stride of the cast's destination dim it lands in (ggml_permute sends
+// source dim a to position op_params[a]).
+mmhip_view rope_h_dst(const struct ggml_tensor * cpy) {
+    const struct ggml_tensor * pm = cpy->src[0];
+    const struct ggml_tensor * r  = pm->src[0];
+    mmhip_view                 v{};
+    v.data = cpy->data;
+    for (int a = 0; a < 4; a++) {
+        v.ne[a] = r->ne[a];
+        v.nb[a] = (int64_t) cpy->nb[pm->op_params[a]];
+    }
+    return v;
+}
+
+// CPY(PERMUTE(ROPE(x))) into a contiguous F16 tensor, the rope and the
+// permutation read by nothing else, only views between the rope and the CPY
+// (so the rope's input is still intact at the CPY's position), and the
+// shapes the position-parallel rope kernel takes.
+bool plan_rope_h(struct ggml_cgraph * g, const graph_info & gi, int i, const std::vector<int> & step_at,
+                 const std::vector<char> & absorbed) {
+    const struct ggml_tensor * n  = ggml_graph_node(g, i);
+    const struct ggml_tensor * pm = n->src[0];
+    if (getenv("GGML_MI355X_DISABLE_ROPE_F16") || n->type != GGML_TYPE_F16 || !ggml_is_contiguous(n) || !pm ||
+        pm->op != GGML_OP_PERMUTE || !pm->src[0] || pm->src[0]->op != GGML_OP_ROPE) {
+        return false;
+    }
+    const struct ggml_tensor * r  = pm->src[0];
+    const int                  ri = node_index(gi, r), pi = node_index(gi, pm);
+    if (ri < 0 || pi < 0 || ri >= i || gi.uses[(size_t) ri] != 1 || gi.uses[(size_t) pi] != 1 || is_output(r) ||
+        is_output(pm) || step_at[(size_t) ri] >= 0 || absorbed[(size_t) ri] || r->type != GGML_TYPE_F32 ||
+        !supports_rope(r)) {
+        return false;
+    }
+    for (int t = ri + 1; t < i; t++) {
+        if (!is_noop(ggml_graph_node(g, t)->op)) {
+            return false;
+        }
+    }
+    const struct ggml_tensor * x      = r->src[0];
+    const int                  n_dims = r->op_params[1];
+    const mmhip_view           d      = rope_h_dst(n);
+    bool ok = x->type == GGML_TYPE_F32 && ggml_are_same_shape(x, r) && n_dims > 0 && n_dims <= 256 &&
+              (n_dims / 2) % 4 == 0 && x->ne[0] % 4 == 0 && x->nb[0] == 4 && ((uintptr_t) x->data) % 16 == 0 &&
+              ((uintptr_t) n->data) % 8 == 0 && d.nb[0] == 2;
+    for (int a = 1; a < 4; a++) {
+        ok = ok && x->nb[a] % 16 == 0 && d.nb[a] % 8 == 0;
+    }
+    return ok;
+}
+
 bool plan_small_attn(struct ggml_cgraph * g, const graph_info & gi, int i, plan_step & st,
                      std::vector<char> & absorbed) {
     static const bool dbg = getenv("GGML_MI355X_PLAN_DEBUG") != nullptr;
@@ -1739,6 +1793,15 @@ graph_plan build_plan(struct ggml_cgraph * g) {
                 continue;
             }
         }
+        if (n->op == GGML_OP_CPY && plan_rope_h(g, gi, i, step_at, absorbed)) {
+            plan_step st;
+            st.kind = ST_ROPE_H;
+            st.node = i;
+            st.src  = node_index(gi, n->src[0]->src[0]);
+            absorbed[(size_t) st.src] = 1;
+            add_pending(st);
+            continue;
+        }
         if (n->op == GGML_OP_CONT) {
             plan_step st;
             if (!no_sattn && plan_small_attn(g, gi, i, st, absorbed)) {
@@ -2089,6 +2152,16 @@ int run_step(mi_backend * c, struct ggml_cgraph * g, const plan_step & st, char 
             rc = mmhip_small_attn_q(&q, &k, &v, scale, bias, dm->op_params[0], (float *) n->data,
                                     st.slot_out >= 0 ? st.vec_wtype : 0, st.slot_out >= 0 ? slot + st.slot_out : nullptr,
                                     s);
+            break;
+        }
+        case ST_ROPE_H: {
+            const struct ggml_tensor * r      = ggml_graph_node(g, st.src);
+            const int                  n_dims = r->op_params[1];
+            float                      base;
+            memcpy(&base, &r->op_params[5], sizeof(float));
+            mmhip_view x = view_of(r->src[0]), d = rope_h_dst(n);
+            rc = mmhip_rope_neox_f16(&x, (const int32_t *) r->src[1]->data, n_dims, powf(base, -2.0f / (float) n_dims),
+                                     &d, s);
             break;
         }
         case ST_GLU_V: {

@@ -1241,7 +1241,7 @@ __global__ void k_rope_neox_heads(TV x, const int32_t * __restrict__ pos, int n_
 // (d +- n_dims / 2).  Rows with contiguous elements, D and n_dims / 2
 // multiples of 4.  The arithmetic of k_rope_neox_heads, so the same bits.
 __global__ __launch_bounds__(256) void k_rope_neox_pos(TV x, const int32_t * __restrict__ pos, int n_dims,
-                                                       float theta_scale, float * __restrict__ dst) {
+                                                       float theta_scale, float * __restrict__ dst, TV dh) {
 #pragma clang fp contract(off)
     __shared__ float s_c[128], s_s[128];  // n_dims / 2 <= 128
     const int64_t i2 = blockIdx.x % x.ne[2], i3 = blockIdx.x / x.ne[2];
@@ -1275,7 +1275,15 @@ __global__ __launch_bounds__(256) void k_rope_neox_pos(TV x, const int32_t * __r
                 o[u] = b[u] * s_s[d - half + u] + a[u] * s_c[d - half + u];
             }
         }
-        *(float4_t *) (dp + (int64_t) i1 * D + d) = o;
+        if (dh.data) {
+            // rounded to f16 (as CPY rounds) into the strided f16 view
+            uint2 hv;
+            hv.x = (uint32_t) f2h(o[0]) | ((uint32_t) f2h(o[1]) << 16);
+            hv.y = (uint32_t) f2h(o[2]) | ((uint32_t) f2h(o[3]) << 16);
+            *(uint2 *) (dh.data + 2 * (int64_t) d + i1 * dh.nb[1] + i2 * dh.nb[2] + i3 * dh.nb[3]) = hv;
+        } else {
+            *(float4_t *) (dp + (int64_t) i1 * D + d) = o;
+        }
     }
 }
 
@@ -1294,7 +1302,7 @@ extern "C" int mmhip_rope_neox(const mmhip_view * x, const int32_t * pos, int n_
         x->nb[2] % 16 == 0 && x->nb[3] % 16 == 0 && ((uintptr_t) x->data) % 16 == 0 && ((uintptr_t) dst) % 16 == 0 &&
         x->ne[2] * x->ne[3] <= 0x7fffffff && x->ne[0] * x->ne[1] <= 0x7fffffff) {
         hipLaunchKernelGGL(k_rope_neox_pos, dim3((unsigned) (x->ne[2] * x->ne[3])), dim3(256), 0, (hipStream_t) stream,
-                           tv(x), pos, n_dims, theta_scale, dst);
+                           tv(x), pos, n_dims, theta_scale, dst, TV{});
         return check_launch("rope");
     }
     if (x->ne[1] >= RH && n_dims >= 2) {
@@ -1306,6 +1314,35 @@ extern "C" int mmhip_rope_neox(const mmhip_view * x, const int32_t * pos, int n_
     hipLaunchKernelGGL(k_rope_neox, dim3(grid_for(total, 256)), dim3(256), 0, (hipStream_t) stream, tv(x), pos, n_dims,
                        theta_scale, dst);
     return check_launch("rope");
+}
+
+extern "C" int mmhip_rope_neox_f16(const mmhip_view * x, const int32_t * pos, int n_dims, float theta_scale,
+                                   const mmhip_view * dst, void * stream) {
+    MMHIP_API_BEGIN();
+    if (!x || !pos || !dst || !dst->data || n_dims <= 0 || n_dims % 2 != 0 || n_dims > x->ne[0]) {
+        return set_error(MMHIP_ERR_INVALID, "rope_f16: bad arguments");
+    }
+    for (int a = 0; a < 4; a++) {
+        if (dst->ne[a] != x->ne[a]) {
+            return set_error(MMHIP_ERR_INVALID, "rope_f16: dst shape differs from x");
+        }
+    }
+    if (x->ne[0] * x->ne[1] * x->ne[2] * x->ne[3] == 0) {
+        return MMHIP_OK;
+    }
+    bool ok = n_dims <= 256 && (n_dims / 2) % 4 == 0 && x->ne[0] % 4 == 0 && x->nb[0] == 4 && dst->nb[0] == 2 &&
+              ((uintptr_t) x->data) % 16 == 0 && ((uintptr_t) dst->data) % 8 == 0 &&
+              x->ne[2] * x->ne[3] <= 0x7fffffff && x->ne[0] * x->ne[1] <= 0x7fffffff;
+    for (int a = 1; a < 4; a++) {
+        ok = ok && x->nb[a] % 16 == 0 && dst->nb[a] % 8 == 0;
+    }
+    if (!ok) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "rope_f16: n_dims=%d ne0=%lld or strides / alignment not taken", n_dims,
+                         (long long) x->ne[0]);
+    }
+    hipLaunchKernelGGL(k_rope_neox_pos, dim3((unsigned) (x->ne[2] * x->ne[3])), dim3(256), 0, (hipStream_t) stream,
+                       tv(x), pos, n_dims, theta_scale, nullptr, tv(dst));
+    return check_launch("rope_f16");
 }
 
 extern "C" int mmhip_cpy(const mmhip_view * src, int src_type, const mmhip_view * dst, int dst_type, void * stream) {

@@ -103,6 +103,7 @@ SIGNATURES = {
     "mmhip_head_rows_n": (_i32, [ctypes.c_void_p, _i32, _vp]),
     "mmhip_swiglu_quant": (_i32, [_VP, _VP, _i32, _vp, _i32, _vp, _vp]),
     "mmhip_rope_neox": (_i32, [_VP, _vp, _i32, _f32, _vp, _vp]),
+    "mmhip_rope_neox_f16": (_i32, [_VP, _vp, _i32, _f32, _VP, _vp]),
     "mmhip_cpy": (_i32, [_VP, _i32, _VP, _i32, _vp]),
     "mmhip_get_rows": (_i32, [_i32, _VP, _VP, _vp, _vp]),
     "mmhip_set_rows": (_i32, [_VP, _VP, _i32, _VP, _i32, _vp]),

@@ -9,6 +9,7 @@ quantized to Q8_0 before each Q8_0 dot and K/V are rounded to f16, both of
 which the reference does in exact arithmetic except the f16 rounding of K/V,
 which it applies too.  The first compute runs eagerly, later ones replay the
 captured HIP graph: every replay must equal the eager result bit for bit."""
+import ctypes
 import importlib
 
 import numpy as np
@@ -145,3 +146,58 @@ def test_dit_graph_head_through_backend(pkg, orc):
     assert np.array_equal(y[:, 0], temb[:, 0])
     rel_rms = float(np.sqrt(((y.astype(np.float64) - ref) ** 2).mean() / (ref.astype(np.float64) ** 2).mean()))
     assert cosine(y, ref) >= 0.9999 and rel_rms <= 5e-3, (cosine(y, ref), rel_rms)
+
+
+@pytest.mark.parametrize("S,B", [(690, 2), (37, 1)])
+def test_rope_f16_equals_rope_then_cast(pkg, S, B):
+    """mmhip_rope_neox_f16 (the DiT's K rope and its f16 cast in one launch)
+    writes the bytes of mmhip_rope_neox followed by the CPY of the permuted
+    view to f16: [D, Nh, S, B] rows in, [D, S, Nh, B] f16 rows out."""
+    mm = importlib.import_module(pkg.__name__ + ".mmhip")
+    L = mm.load()
+    _, dg = _mods(pkg)
+    D, H = dg.DIM // dg.N_HEADS, dg.N_HEADS
+    g = torch.Generator().manual_seed(S + B)
+    x = torch.randn((B, S, H, D), generator=g).cuda()          # ggml [D, H, S, B]
+    pos = torch.arange(S, dtype=torch.int32, device="cuda")
+    theta = ctypes.c_float(dg.ROPE_BASE ** (-2.0 / dg.ROTARY_DIM))
+    V = lambda t: ctypes.byref(mm.view_of(t))
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    r = torch.empty_like(x)
+    assert L.mmhip_rope_neox(V(x), P(pos), dg.ROTARY_DIM, theta, P(r), None) == 0
+    ref = r.permute(0, 2, 1, 3).contiguous().half()           # ggml [D, S, H, B] f16 (CPY rounds to nearest)
+    out = torch.full((B, H, S, D), float("nan"), dtype=torch.float16, device="cuda")
+    dv = out.permute(0, 2, 1, 3)                               # the cast's rows in the rope's dim order
+    assert L.mmhip_rope_neox_f16(V(x), P(pos), dg.ROTARY_DIM, theta, V(dv), None) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+
+
+def test_dit_block_rope_cast_fusion_gives_the_same_bits(pkg, monkeypatch):
+    """The DiT block with K's rope storing f16 into the cast's rows equals the
+    same graph with that fusion off, bit for bit."""
+    og, dg = _mods(pkg)
+    S, B = 690, 2
+    w = dg.synth_block(61)
+    x = np.random.default_rng(62).standard_normal((B, S, dg.DIM)).astype(np.float32)
+
+    def run():
+        g = og.OpGraph()
+        try:
+            blk = dg.Block(g)
+            tx = g.tensor(og.F32, [dg.DIM, S, B])
+            tp = g.tensor(26, [S])
+            out = dg.build_block(g, blk, tx, tp, S, B)
+            g.build([out])
+            blk.upload(g, w)
+            g.set(tx, x)
+            g.set(tp, np.arange(S, dtype=np.int32))
+            g.compute()
+            return g.get(out)
+        finally:
+            g.close()
+
+    fused = run()
+    monkeypatch.setenv("GGML_MI355X_DISABLE_ROPE_F16", "1")
+    plain = run()
+    assert np.array_equal(fused, plain)
