@@ -26,17 +26,19 @@ def write(path, kvs, tensors, alignment=32):
     (ne[0] innermost), raw bytes)]."""
     head = b"GGUF" + struct.pack("<IqQ", 3, len(tensors), len(kvs))
     head += b"".join(_kv(k, t, v) for k, t, v in kvs)
-    infos, offset, blobs = b"", 0, []
+    infos, offset, blobs = [], 0, []
     for name, gtype, ne, data in tensors:
-        data = bytes(data)  # raw bytes of any buffer (numpy arrays of any dtype)
-        infos += _str(name) + struct.pack("<I", len(ne)) + b"".join(struct.pack("<q", int(n)) for n in ne)
-        infos += struct.pack("<IQ", gtype, offset)
-        pad = (-len(data)) % alignment
-        blobs.append(data + b"\0" * pad)
-        offset += len(data) + pad
-    body = head + infos
+        data = memoryview(data)  # raw bytes of any buffer; contiguous ones are not copied
+        data = data.cast("B") if data.c_contiguous else memoryview(data.tobytes())
+        infos.append(_str(name) + struct.pack("<I", len(ne)) + b"".join(struct.pack("<q", int(n)) for n in ne))
+        infos.append(struct.pack("<IQ", gtype, offset))
+        pad = (-data.nbytes) % alignment
+        blobs.append((data, pad))
+        offset += data.nbytes + pad
+    body = head + b"".join(infos)
     body += b"\0" * ((-len(body)) % alignment)
     with open(path, "wb") as f:
         f.write(body)
-        for b in blobs:
-            f.write(b)
+        for data, pad in blobs:
+            f.write(data)
+            f.write(b"\0" * pad)

@@ -20,7 +20,7 @@ REF_SRC = pathlib.Path("/root/reference/src")
 GGML_INC = ROOT / "minimaxmusic.cpp_amd" / "ggml" / "include"
 LIB = ROOT / "minimaxmusic.cpp_amd" / "lib"
 OUT = HERE / "_build"
-DRIVERS = ["lm_driver", "depth_driver"]
+DRIVERS = ["lm_driver", "depth_driver", "dit_driver"]
 
 
 def available():
