@@ -1080,4 +1080,119 @@ int gemm_bf16(const void * W, int64_t N, int64_t K, int64_t rs, const float * x,
                                            one, stream);
 }
 
+// F32 weights at token counts (the DiT's k = 1 convs, src/dit.h:258 and
+// :285, which the quantiser leaves in F32): y[m, n] = sum_k x[m, k] * W[n, k]
+// on v_mfma_f32_32x32x2f32, f32 products summed in f32 as ggml-CPU's f32 dot
+// sums them (in another order).  One wave per 64 tokens x 64 weight rows,
+// four 32 x 32 accumulators (tokens are the A operand, so a lane's outputs
+// share one weight row and 32 lanes store 128 contiguous bytes of a y row).
+// Per 32-wide K chunk lane l reads 16 consecutive floats (64 bytes) of token
+// row / weight row l % 32 at k offset 16 (l / 32); MFMA step s (0..15) takes
+// element s, so the two lane halves supply k = s and k = 16 + s: every k of
+// the chunk once, the same k for both operands.  Rows past M or N are read as
+// the last row (in bounds) and not stored.  The next chunk's loads are in
+// flight while the current chunk's 64 MFMAs run.
+__global__ __launch_bounds__(64) void k_gemm_f32(const float * __restrict__ W, int64_t ldw, const float * __restrict__ x,
+                                                 int64_t ldx, int64_t N, int64_t K, int64_t M, float * __restrict__ y,
+                                                 int64_t ldy) {
+    const int     l = threadIdx.x, li = l & 31, h = l >> 5;
+    const int64_t n0 = (int64_t) blockIdx.x * 64, m0 = (int64_t) blockIdx.y * 64;
+    const float * pw[2];
+    const float * px[2];
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+        const int64_t n = n0 + 32 * b + li, m = m0 + 32 * b + li;
+        pw[b]           = W + (n < N ? n : N - 1) * ldw + 16 * h;
+        px[b]           = x + (m < M ? m : M - 1) * ldx + 16 * h;
+    }
+    float16_t acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                acc[i][j][r] = 0.0f;
+            }
+        }
+    }
+    float4_t ca[2][4], cw[2][4];
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            ca[b][c] = *(const float4_t *) (px[b] + 4 * c);
+            cw[b][c] = *(const float4_t *) (pw[b] + 4 * c);
+        }
+    }
+    for (int64_t k0 = 0; k0 < K; k0 += 32) {
+        float4_t na[2][4], nw[2][4];
+        const int64_t kn = k0 + 32 < K ? k0 + 32 : k0;  // the last chunk reloads itself (in bounds)
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                na[b][c] = *(const float4_t *) (px[b] + kn + 4 * c);
+                nw[b][c] = *(const float4_t *) (pw[b] + kn + 4 * c);
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 16; s++) {
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(ca[i][s >> 2][s & 3], cw[j][s >> 2][s & 3],
+                                                                      acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                ca[b][c] = na[b][c];
+                cw[b][c] = nw[b][c];
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int64_t n = n0 + 32 * j + li;
+        if (n >= N) {
+            continue;
+        }
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int64_t m = m0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (m < M) {
+                    y[m * ldy + n] = acc[i][j][r];
+                }
+            }
+        }
+    }
+}
+
+bool gemm_f32_supported(int64_t N, int64_t K, int64_t ldw, const void * W, const float * x, int64_t ldx) {
+    return N > 0 && K > 0 && K % 32 == 0 && ldw >= K && ldw % 4 == 0 && ldx >= K && ldx % 4 == 0 &&
+           ((uintptr_t) W) % 16 == 0 && ((uintptr_t) x) % 16 == 0;
+}
+
+int gemm_f32(const float * W, int64_t ldw, const float * x, int64_t ldx, int64_t N, int64_t K, int64_t M, float * y,
+             int64_t ldy, hipStream_t stream) {
+    if (!gemm_f32_supported(N, K, ldw, W, x, ldx) || M <= 0 || ldy < N) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat f32 gemm: N=%lld K=%lld M=%lld (K %% 32 == 0, 16-byte rows)",
+                         (long long) N, (long long) K, (long long) M);
+    }
+    const int64_t gx = (N + 63) / 64, gy = (M + 63) / 64;
+    if (gx > INT32_MAX || gy > 65535) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat f32 gemm: grid too large");
+    }
+    hipLaunchKernelGGL(k_gemm_f32, dim3((unsigned) gx, (unsigned) gy), dim3(64), 0, stream, W, ldw, x, ldx, N, K, M, y,
+                       ldy);
+    return check_launch("mul_mat f32 gemm");
+}
+
 }  // namespace mmhip

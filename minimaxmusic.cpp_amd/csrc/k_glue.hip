@@ -1497,6 +1497,16 @@ extern "C" int mmhip_mul_mat_f32(const mmhip_view * a, const mmhip_view * b, flo
     if (n >= ((int64_t) 1 << 31)) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat_f32: too many outputs");
     }
+    // a 2-D weight against >= 32 activation rows that collapse to one stride
+    // (the DiT's k = 1 convs): the f32 MFMA GEMM
+    const int64_t M = b->ne[1] * b->ne[2] * b->ne[3];
+    if (a->ne[2] == 1 && a->ne[3] == 1 && M >= 32 && b->nb[2] == b->ne[1] * b->nb[1] &&
+        b->nb[3] == b->ne[2] * b->nb[2] && a->nb[1] % 4 == 0 && b->nb[1] % 4 == 0 &&
+        gemm_f32_supported(a->ne[1], a->ne[0], (int64_t) (a->nb[1] / 4), a->data, (const float *) b->data,
+                           (int64_t) (b->nb[1] / 4))) {
+        return gemm_f32((const float *) a->data, (int64_t) (a->nb[1] / 4), (const float *) b->data,
+                        (int64_t) (b->nb[1] / 4), a->ne[1], a->ne[0], M, dst, a->ne[1], (hipStream_t) stream);
+    }
     if (a->ne[0] >= 128 && n <= ((int64_t) 1 << 24)) {
         hipLaunchKernelGGL(k_mul_mat_f32_wave, dim3((unsigned) ((n + 3) / 4)), dim3(256), 0, (hipStream_t) stream, tv(a),
                            tv(b), dst, a->ne[1], b->ne[1], b->ne[2], a->ne[0], b->ne[2] / a->ne[2], b->ne[3] / a->ne[3], n);

@@ -128,6 +128,11 @@ constexpr int BF16_GEMV_MAXM = 16;
 // BF16 weights at token counts (rows rs bytes apart, read in place): the
 // bf16 activation copy the workspace holds, the shape / alignment check, and
 // the call (y = x W^T, ggml's BF16 arithmetic: bf16 activations, f32 sums).
+// F32 weight rows (ldw floats apart) x f32 activation rows at token counts
+// (K % 32 == 0, 16-byte aligned rows), f32 MFMA.
+bool   gemm_f32_supported(int64_t N, int64_t K, int64_t ldw, const void * W, const float * x, int64_t ldx);
+int    gemm_f32(const float * W, int64_t ldw, const float * x, int64_t ldx, int64_t N, int64_t K, int64_t M, float * y,
+                int64_t ldy, hipStream_t stream);
 size_t gemm_bf16_workspace(int64_t K, int64_t M);
 bool   gemm_bf16_supported(int64_t N, int64_t K, int64_t rs, const void * W, const float * x, int64_t ldx);
 int    gemm_bf16(const void * W, int64_t N, int64_t K, int64_t rs, const float * x, int64_t ldx, int64_t M, float * y,

@@ -4,6 +4,8 @@ Tolerances (stated): against the ggml-CPU-semantics oracle, which quantises
 activations the same way and differs only in f32 summation order,
 max|y - y_ggml| <= 2e-5 * max|y_ggml|; against the exact fp64 oracle,
 cosine >= 0.9999 (ggml-CPU's own activation-quantisation error)."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -382,3 +384,27 @@ def test_gemv_q8_0_int8_mfma_columns(mm, orc, pkg, N, K, M):
     y, yg, yf = run(mm, orc, pkg, 8, N, K, M, 7000 + N + K + M)
     assert rel_err(y, yg) < 2e-5
     assert cosine(y, yf) > 0.9999
+
+
+@pytest.mark.parametrize("N,K,T,B,pad", [(2304, 2304, 689, 2, 0), (128, 128, 689, 2, 0), (100, 96, 45, 1, 0),
+                                         (64, 256, 32, 1, 8), (257, 512, 70, 3, 4)])
+def test_mul_mat_f32_weights_at_token_counts(mm, N, K, T, B, pad):
+    """F32 weight rows against f32 activations at >= 32 tokens (the DiT's
+    k = 1 convs, src/dit.h:258 and :285, stored F32 by the quantiser): the f32
+    MFMA GEMM, 3-D activations collapsed to K x (T*B), partial 64-row / 64-token
+    tiles, and weight rows `pad` floats longer than K (a view).  Tolerance:
+    max|y - y64| <= 1e-5 * max|y64| against float64 (f32 products, f32 sums)."""
+    L = mm.load()
+    g = torch.Generator().manual_seed(N + K + T)
+    wfull = torch.randn((N, K + pad), generator=g) / np.sqrt(K)
+    x = torch.randn((B, T, K), generator=g)
+    tw = wfull.cuda()[:, :K]                                  # ggml [K, N], row stride K + pad
+    tx = x.cuda()                                             # ggml [K, T, B]
+    out = torch.full((B, T, N), float("nan"), device="cuda")  # ggml [N, T, B]
+    va, vb = mm.view_of(tw), mm.view_of(tx)
+    assert L.mmhip_mul_mat_f32(ctypes.byref(va), ctypes.byref(vb), ctypes.c_void_p(out.data_ptr()),
+                               ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)) == 0, L.mmhip_last_error()
+    ref = x.double() @ wfull[:, :K].double().T
+    y = out.cpu().double()
+    assert torch.isfinite(y).all()
+    assert float((y - ref).abs().max() / ref.abs().max()) < 1e-5
