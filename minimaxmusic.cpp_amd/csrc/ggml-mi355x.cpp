@@ -180,10 +180,16 @@ enum ggml_status buf_init_tensor(ggml_backend_buffer_t b, struct ggml_tensor * t
     return GGML_STATUS_SUCCESS;
 }
 
+void refresh_f16_copies(mi_buffer * c, const char * lo, const char * hi);
+
+// A constant byte fill is the same in the GGUF and the row-grouped layout.
 void buf_memset(ggml_backend_buffer_t b, struct ggml_tensor * t, uint8_t value, size_t offset, size_t size) {
     mi_buffer * c = (mi_buffer *) b->context;
     hipSetDevice(c->device);
-    HIP_OK(hipMemset((char *) t->data + offset, value, size));
+    if (!HIP_OK(hipMemset((char *) t->data + offset, value, size))) {
+        poison(c);
+    }
+    refresh_f16_copies(c, (const char *) t->data + offset, (const char *) t->data + offset + size);
 }
 
 // Quantized rows are converted between GGUF bytes (host side) and the
@@ -275,8 +281,9 @@ bool staged_write(int device, void * dst, const void * src, size_t size) {
     return true;
 }
 
-// A write into a weight that has an f16 copy converts the copy again, in
-// place (captured graphs keep its address), before the write returns.
+// A write into a weight that has an f16 copy (set_tensor, memset_tensor,
+// cpy_tensor, clear) converts the copy again, in place (captured graphs keep
+// its address), before the write returns.
 void refresh_f16_copies(mi_buffer * c, const char * lo, const char * hi) {
     for (const mi_f16_copy & f : c->f16) {
         const char * w = (const char *) f.w;
@@ -357,7 +364,11 @@ bool buf_cpy_tensor(ggml_backend_buffer_t b, const struct ggml_tensor * src, str
     }
     mi_buffer * c = (mi_buffer *) b->context;
     hipSetDevice(c->device);
-    return HIP_OK(hipMemcpy(dst->data, src->data, ggml_nbytes(src), hipMemcpyDeviceToDevice));
+    if (!HIP_OK(hipMemcpy(dst->data, src->data, ggml_nbytes(src), hipMemcpyDeviceToDevice))) {
+        return false;
+    }
+    refresh_f16_copies(c, (const char *) dst->data, (const char *) dst->data + ggml_nbytes(dst));
+    return true;
 }
 
 void buf_clear(ggml_backend_buffer_t b, uint8_t value) {
@@ -365,6 +376,7 @@ void buf_clear(ggml_backend_buffer_t b, uint8_t value) {
     hipSetDevice(c->device);
     HIP_OK(hipMemset(c->ptr, value, b->size));
     HIP_OK(hipDeviceSynchronize());
+    refresh_f16_copies(c, (const char *) c->ptr, (const char *) c->ptr + b->size);
 }
 
 const struct ggml_backend_buffer_i k_buf_iface = {
@@ -1239,7 +1251,10 @@ bool plan_rope_h(struct ggml_cgraph * g, const graph_info & gi, int i, const std
     const struct ggml_tensor * x      = r->src[0];
     const int                  n_dims = r->op_params[1];
     const mmhip_view           d      = rope_h_dst(n);
-    bool ok = x->type == GGML_TYPE_F32 && ggml_are_same_shape(x, r) && n_dims > 0 && n_dims <= 256 &&
+    // the fused launch reads x while it writes n: an allocator that reused
+    // x's memory for the cast's output (x is dead after the rope in the
+    // unfused order) would have n overlap x
+    bool ok = !overlaps(n, x) && x->type == GGML_TYPE_F32 && ggml_are_same_shape(x, r) && n_dims > 0 && n_dims <= 256 &&
               (n_dims / 2) % 4 == 0 && x->ne[0] % 4 == 0 && x->nb[0] == 4 && ((uintptr_t) x->data) % 16 == 0 &&
               ((uintptr_t) n->data) % 8 == 0 && d.nb[0] == 2;
     for (int a = 1; a < 4; a++) {
@@ -2485,9 +2500,19 @@ bool capture_graph(mi_backend * c, struct ggml_cgraph * g, mi_graph_entry * e) {
 // f16 copies (within the budget) of the quantised weights that the graph
 // multiplies at more than 16 tokens and that have none yet; the conversions
 // run on the backend's stream ahead of the graph's own work.
+// Copies are a cache and must not crowd out the caller's own allocations (the
+// reference sizes residency by its weight buffers, src/model-store.h:81-84, :115):
+// besides the process-wide budget, a copy is made only while at least half
+// of the device's memory stays free after it.  The copies are device
+// allocations, so the device's get_memory (hipMemGetInfo) reports them as
+// used; ggml_backend_mi355x_f16_weight_bytes gives their total.
 void make_f16_copies(mi_backend * c, struct ggml_cgraph * g) {
     const size_t lim  = f16_limit();
     bool         made = false;
+    size_t       dev_free = 0, dev_total = 0;
+    if (lim > 0 && !HIP_OK(hipMemGetInfo(&dev_free, &dev_total))) {
+        return;
+    }
     for (int i = 0; i < ggml_graph_n_nodes(g) && lim > 0; i++) {
         const struct ggml_tensor * n = ggml_graph_node(g, i);
         if (n->op != GGML_OP_MUL_MAT || !is_repacked(n->src[0]->type) || mm_is_gemv(n) || !supports_mul_mat(n)) {
@@ -2509,6 +2534,9 @@ void make_f16_copies(mi_backend * c, struct ggml_cgraph * g) {
         if (have || bc->device != c->dev->id || g_f16_bytes.load() + bytes > lim) {
             continue;
         }
+        if (dev_free < bytes || dev_free - bytes < dev_total / 2) {
+            break;
+        }
         void * p = nullptr;
         if (hipMalloc(&p, bytes) != hipSuccess) {
             (void) hipGetLastError();
@@ -2524,6 +2552,7 @@ void make_f16_copies(mi_backend * c, struct ggml_cgraph * g) {
         }
         bc->f16.push_back(f);
         g_f16_bytes.fetch_add(bytes);
+        dev_free -= bytes;
         made = true;
     }
     if (made) {

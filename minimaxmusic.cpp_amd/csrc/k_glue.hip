@@ -814,7 +814,7 @@ __global__ __launch_bounds__(256) void k_head_rows(HeadSegs hs) {
 // multiplied in f32 step by step (ggml's cache recurrence).
 
 __global__ void k_rope_neox(TV x, const int32_t * __restrict__ pos, int n_dims, float theta_scale,
-                            float * __restrict__ dst) {
+                            float * dst) {  // dst may be x (in place): each thread owns its pair
 #pragma clang fp contract(off)
     const int64_t D     = x.ne[0];
     const int64_t rows  = x.ne[1] * x.ne[2] * x.ne[3];
@@ -1206,7 +1206,7 @@ extern "C" int mmhip_rms_norm_quant(const mmhip_view * x, const mmhip_view * w, 
 constexpr int RH = 8;
 
 __global__ void k_rope_neox_heads(TV x, const int32_t * __restrict__ pos, int n_dims, float theta_scale,
-                                  float * __restrict__ dst, int64_t n_items) {
+                                  float * dst, int64_t n_items) {  // dst may be x, as k_rope_neox
 #pragma clang fp contract(off)
     const int64_t D = x.ne[0], half = n_dims / 2, ng = (x.ne[1] + RH - 1) / RH;
     for (int64_t t = blockIdx.x * (int64_t) blockDim.x + threadIdx.x; t < n_items;
@@ -1240,8 +1240,11 @@ __global__ void k_rope_neox_heads(TV x, const int32_t * __restrict__ pos, int n_
 // on consecutive elements, each reading its own 16 bytes and its partner's
 // (d +- n_dims / 2).  Rows with contiguous elements, D and n_dims / 2
 // multiples of 4.  The arithmetic of k_rope_neox_heads, so the same bits.
+// In place (dst == x, contiguous) when a row's D / 4 chunks divide 64: the two
+// elements of a pair are then read and written by lanes of one wave in one
+// loop iteration, whose loads all issue before its stores.
 __global__ __launch_bounds__(256) void k_rope_neox_pos(TV x, const int32_t * __restrict__ pos, int n_dims,
-                                                       float theta_scale, float * __restrict__ dst, TV dh) {
+                                                       float theta_scale, float * dst, TV dh) {
 #pragma clang fp contract(off)
     __shared__ float s_c[128], s_s[128];  // n_dims / 2 <= 128
     const int64_t i2 = blockIdx.x % x.ne[2], i3 = blockIdx.x / x.ne[2];
@@ -1298,7 +1301,21 @@ extern "C" int mmhip_rope_neox(const mmhip_view * x, const int32_t * pos, int n_
     if (total == 0) {
         return MMHIP_OK;
     }
-    if (n_dims <= 256 && (n_dims / 2) % 4 == 0 && x->ne[0] % 4 == 0 && x->nb[0] == 4 && x->nb[1] % 16 == 0 &&
+    // dst is contiguous [ne0, ne1, ne2, ne3]; it may be x itself (ggml runs
+    // ROPE in place) but not overlap x otherwise
+    const char * x_lo = (const char *) x->data, *x_hi = (const char *) x->data;
+    for (int a = 0; a < 4; a++) {
+        x_hi += (x->ne[a] - 1) * x->nb[a];
+    }
+    x_hi += 4;
+    const char * d_lo = (const char *) dst, *d_hi = d_lo + 4 * (rows * x->ne[0]);
+    const bool   in_place = d_lo < x_hi && x_lo < d_hi;
+    if (in_place && (d_lo != x_lo || x->nb[0] != 4 || x->nb[1] != 4 * x->ne[0] || x->nb[2] != x->nb[1] * x->ne[1] ||
+                     x->nb[3] != x->nb[2] * x->ne[2])) {
+        return set_error(MMHIP_ERR_INVALID, "rope: dst overlaps x without being x (contiguous) itself");
+    }
+    if (n_dims <= 256 && (n_dims / 2) % 4 == 0 && x->ne[0] % 4 == 0 && (!in_place || 64 % (x->ne[0] / 4) == 0) &&
+        x->nb[0] == 4 && x->nb[1] % 16 == 0 &&
         x->nb[2] % 16 == 0 && x->nb[3] % 16 == 0 && ((uintptr_t) x->data) % 16 == 0 && ((uintptr_t) dst) % 16 == 0 &&
         x->ne[2] * x->ne[3] <= 0x7fffffff && x->ne[0] * x->ne[1] <= 0x7fffffff) {
         hipLaunchKernelGGL(k_rope_neox_pos, dim3((unsigned) (x->ne[2] * x->ne[3])), dim3(256), 0, (hipStream_t) stream,

@@ -6,6 +6,7 @@
 // before it is used.
 #include "gguf.h"
 
+#include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -184,6 +185,17 @@ extern "C" struct gguf_context * gguf_init_from_file(const char * fname, struct 
                 r.ok = false;
             }
         }
+        // the element count must fit int64 (as upstream checks: INT64_MAX / ne)
+        for (uint32_t d = 1; d < nd && r.ok; d++) {
+            int64_t prod = 1;
+            for (uint32_t e = 0; e <= d; e++) {
+                if (ti.ne[e] != 0 && prod > INT64_MAX / ti.ne[e]) {
+                    r.ok = false;
+                    break;
+                }
+                prod *= ti.ne[e];
+            }
+        }
         if (!r.get(ty) || ty >= GGML_TYPE_COUNT || ggml_blck_size((ggml_type) ty) <= 0 || !r.get(ti.offset) ||
             ti.ne[0] % ggml_blck_size((ggml_type) ty) != 0 || ti.name.size() >= GGML_MAX_NAME) {
             r.ok = false;
@@ -203,9 +215,21 @@ extern "C" struct gguf_context * gguf_init_from_file(const char * fname, struct 
     if (params.ctx) {
         size_t data_bytes = 0;
         for (const gguf_tinfo & ti : ctx->tensors) {
-            const size_t nb = ggml_row_size(ti.type, ti.ne[0]) * (size_t) (ti.ne[1] * ti.ne[2] * ti.ne[3]);
-            if (ti.offset % ctx->alignment != 0 || ti.offset > r.size || nb > r.size - ctx->data_offset - ti.offset ||
-                ctx->data_offset > r.size) {
+            // bytes of the tensor; rows x row size is checked against overflow
+            // before it is formed, and the data range against the file size
+            // without wrap-around
+            const size_t rs   = ggml_row_size(ti.type, ti.ne[0]);
+            const size_t rows = (size_t) ti.ne[1] * (size_t) ti.ne[2] * (size_t) ti.ne[3];
+            const bool   big  = rs != 0 && rows > SIZE_MAX / rs;
+            const size_t nb   = big ? SIZE_MAX : rs * rows;
+            if (big) {
+                fail(fname, "tensor size overflows");
+                fclose(f);
+                delete ctx;
+                return nullptr;
+            }
+            if (ti.offset % ctx->alignment != 0 || ctx->data_offset > r.size || ti.offset > r.size - ctx->data_offset ||
+                nb > r.size - ctx->data_offset - ti.offset) {
                 if (!params.no_alloc) {  // data requested: it must be in the file
                     fail(fname, "tensor data outside the file");
                     fclose(f);
@@ -213,7 +237,9 @@ extern "C" struct gguf_context * gguf_init_from_file(const char * fname, struct 
                     return nullptr;
                 }
             }
-            data_bytes += nb + GGUF_DEFAULT_ALIGNMENT;
+            data_bytes = nb > SIZE_MAX - GGUF_DEFAULT_ALIGNMENT || data_bytes > SIZE_MAX - GGUF_DEFAULT_ALIGNMENT - nb
+                             ? SIZE_MAX
+                             : data_bytes + nb + GGUF_DEFAULT_ALIGNMENT;
         }
         const size_t meta = (ctx->tensors.size() + 1) * ggml_tensor_overhead();
         struct ggml_init_params ip = { meta + (params.no_alloc ? 0 : data_bytes), nullptr, params.no_alloc };

@@ -121,6 +121,26 @@ def test_gguf_reader_refuses_bad_files(L, pkg, tmp_path):
     assert not L.gguf_init_from_file(str(bad).encode(), GgufInit(False, ctypes.pointer(meta)))
 
 
+def test_gguf_reader_refuses_overflowing_sizes(L, tmp_path):
+    """Tensor shapes whose element count passes INT64_MAX, or whose byte size
+    passes SIZE_MAX, are refused whether data is requested or not (a wrapped
+    size would size the data context too small for the read)."""
+    bad = tmp_path / "huge.gguf"
+    for ne in ([32, 1 << 40, 1 << 40], [1 << 31, 1 << 31, 4], [256, 1 << 30, 1 << 30, 1 << 10], [256, 1 << 54]):
+        gguf_writer.write(bad, [], [("huge", F32, ne, np.zeros(8, np.float32))])
+        for no_alloc in (True, False):
+            meta = ctypes.c_void_p()
+            assert not L.gguf_init_from_file(str(bad).encode(), GgufInit(no_alloc, ctypes.pointer(meta))), (ne, no_alloc)
+    # large but representable: the header parses, the data cannot be in the file
+    gguf_writer.write(bad, [], [("big", F32, [256, 1 << 50], np.zeros(8, np.float32))])
+    meta = ctypes.c_void_p()
+    g = L.gguf_init_from_file(str(bad).encode(), GgufInit(True, ctypes.pointer(meta)))
+    assert g
+    L.gguf_free(g)
+    L.ggml_free(meta)
+    assert not L.gguf_init_from_file(str(bad).encode(), GgufInit(False, ctypes.pointer(meta)))
+
+
 @pytest.mark.parametrize("gtype,K", [(Q8_0, 512), (Q4_K, 512), (Q6_K, 768)])
 def test_to_float_matches_oracle(L, pkg, orc, gtype, K):
     rows = 7

@@ -201,3 +201,68 @@ def test_dit_block_rope_cast_fusion_gives_the_same_bits(pkg, monkeypatch):
     monkeypatch.setenv("GGML_MI355X_DISABLE_ROPE_F16", "1")
     plain = run()
     assert np.array_equal(fused, plain)
+
+
+@pytest.mark.parametrize("D,H,S,B,n_dims", [(64, 32, 690, 2, 32), (128, 8, 37, 1, 128), (96, 4, 20, 2, 32)])
+def test_rope_in_place(pkg, D, H, S, B, n_dims):
+    """ggml runs ROPE in place when its allocator lets it (dst == x): the
+    position-parallel kernel at the DiT's shape (a row's D / 4 chunks divide
+    a wave), the LM's head dim, and a head dim whose rows straddle waves (the
+    pair-per-thread kernel then runs) all give the out-of-place bytes."""
+    mm = importlib.import_module(pkg.__name__ + ".mmhip")
+    L = mm.load()
+    g = torch.Generator().manual_seed(D + S)
+    x = torch.randn((B, S, H, D), generator=g).cuda()          # ggml [D, H, S, B]
+    pos = torch.arange(S, dtype=torch.int32, device="cuda") * 3
+    theta = ctypes.c_float(1e4 ** (-2.0 / n_dims))
+    V = lambda t: ctypes.byref(mm.view_of(t))
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    ref = torch.empty_like(x)
+    assert L.mmhip_rope_neox(V(x), P(pos), n_dims, theta, P(ref), None) == 0
+    y = x.clone()
+    assert L.mmhip_rope_neox(V(y), P(pos), n_dims, theta, P(y), None) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int32), ref.view(torch.int32))
+    # a destination overlapping x without being x is refused
+    assert L.mmhip_rope_neox(V(y), P(pos), n_dims, theta, ctypes.c_void_p(y.data_ptr() + 16), None) != 0
+
+
+def test_rope_cast_into_the_rope_input_is_not_fused(pkg):
+    """K's rope + f16 cast (plan step ROPE_H) is not fused when the cast's
+    destination overlaps the rope's input, which an allocator may do since
+    the input is dead after the rope in the unfused order: the fused launch
+    would read x while writing over it.  The graph then runs ROPE and CPY
+    apart and writes the rope-then-cast bytes."""
+    og, dg = _mods(pkg)
+    mm = importlib.import_module(pkg.__name__ + ".mmhip")
+    L = mm.load()
+    D, H, S, B = dg.DIM // dg.N_HEADS, dg.N_HEADS, 690, 2
+    G = og._load()[0]
+    G.ggml_cpy.restype, G.ggml_cpy.argtypes = og._T, [ctypes.c_void_p, og._T, og._T]
+    xs = torch.randn((B, S, H, D), generator=torch.Generator().manual_seed(77))
+    g = og.OpGraph()
+    try:
+        tx = g.tensor(og.F32, [D, H, S, B])
+        tp = g.tensor(26, [S])
+        r = g.rope_neox(tx, tp, dg.ROTARY_DIM, dg.ROPE_BASE)
+        p = g.permute(r, 0, 2, 1, 3)
+        dst = g.tensor(og.F16, [D, S, H, B])
+        c = G.ggml_cpy(g.ctx, p, dst)
+        g.build([c])
+        # the cast writes into the first half of x's memory
+        dst.contents.data = tx.contents.data
+        c.contents.data = tx.contents.data
+        g.set(tx, xs.numpy())
+        g.set(tp, np.arange(S, dtype=np.int32))
+        g.compute()
+        got = g.get(c, np.float16)
+    finally:
+        g.close()
+    xr = xs.cuda()
+    rr = torch.empty_like(xr)
+    theta = ctypes.c_float(dg.ROPE_BASE ** (-2.0 / dg.ROTARY_DIM))
+    pos = torch.arange(S, dtype=torch.int32, device="cuda")
+    assert L.mmhip_rope_neox(ctypes.byref(mm.view_of(xr)), ctypes.c_void_p(pos.data_ptr()), dg.ROTARY_DIM, theta,
+                             ctypes.c_void_p(rr.data_ptr()), None) == 0
+    ref = rr.permute(0, 2, 1, 3).contiguous().half().cpu().numpy().ravel()  # ggml [D, S, H, B]
+    assert np.array_equal(got.view(np.int16), ref.view(np.int16))

@@ -227,3 +227,58 @@ def test_f16_weight_copies_of_a_repeating_graph(mods, pkg, mm):
            __import__("torch").from_numpy(bias).cuda()).cpu().numpy()
     assert np.array_equal(y2.view(np.int32), ref.view(np.int32))
     assert not np.array_equal(y2.view(np.int32), ys[0].reshape(M, N).view(np.int32))
+
+
+def test_f16_weight_copies_follow_copy_memset_and_clear(mods, pkg, mm):
+    """Every buffer write into a weight that has an f16 copy refreshes the
+    copy: ggml_backend_tensor_copy (cpy_tensor) of other weights into it,
+    ggml_backend_tensor_memset (zero weights: the GEMM then gives the bias),
+    and ggml_backend_buffer_clear of the whole buffer; each next replay equals
+    what the written weights give."""
+    import torch
+
+    og = mods[0]
+    N, K, M = 1024, 2048, 300
+    g = og.OpGraph()
+    G = g.G
+    for n, r, a in [("ggml_backend_tensor_copy", None, [og._T, og._T]),
+                    ("ggml_backend_tensor_memset", None, [og._T, ctypes.c_uint8, ctypes.c_size_t, ctypes.c_size_t]),
+                    ("ggml_backend_buffer_clear", None, [ctypes.c_void_p, ctypes.c_uint8])]:
+        getattr(G, n).restype, getattr(G, n).argtypes = r, a
+    try:
+        tw = g.tensor(og.Q8_0, [K, N])
+        tw2 = g.tensor(og.Q8_0, [K, N])  # the copy's source, not in the graph
+        tx = g.tensor(og.F32, [K, M])
+        tb = g.tensor(og.F32, [N])
+        out = g.add(g.mul_mat(tw, tx), tb)
+        g.build([out])
+        raw, raw2 = pkg.synth.gguf_blocks_np(8, N, K, 7710), pkg.synth.gguf_blocks_np(8, N, K, 7711)
+        x, bias = pkg.synth.normal_np((M, K), 7712), pkg.synth.normal_np((N,), 7713)
+        for t, a in ((tw, raw), (tw2, raw2), (tx, x), (tb, bias)):
+            g.set(t, a)
+        for _ in range(4):
+            g.compute()
+        y1 = g.get(out).reshape(M, N)
+        assert g.f16_weight_bytes() > 0
+
+        def product(r):
+            W = mm.QuantWeight.from_gguf(8, r, N, K)
+            return (mm.mul_mat(W, torch.from_numpy(x).cuda()) + torch.from_numpy(bias).cuda()).cpu().numpy()
+
+        assert np.array_equal(y1.view(np.int32), product(raw).view(np.int32))
+        G.ggml_backend_tensor_copy(tw2, tw)
+        g.compute()
+        assert np.array_equal(g.get(out).reshape(M, N).view(np.int32), product(raw2).view(np.int32))
+        G.ggml_backend_tensor_memset(tw, 0, 0, G.ggml_nbytes(tw))
+        g.compute()
+        assert np.array_equal(g.get(out).reshape(M, N), np.broadcast_to(bias, (M, N)))
+        g.set(tw, raw)
+        g.compute()
+        assert np.array_equal(g.get(out).reshape(M, N).view(np.int32), y1.view(np.int32))
+        G.ggml_backend_buffer_clear(g.buf, 0)
+        g.set(tx, x)
+        g.set(tb, bias)
+        g.compute()
+        assert np.array_equal(g.get(out).reshape(M, N), np.broadcast_to(bias, (M, N)))
+    finally:
+        g.close()
