@@ -63,7 +63,10 @@ int mm_lm_decode(void * lm, const float * embeds, const int * kv_sets, int N, fl
 int mm_lm_decode_device(void * lm, const float * embeds, const int * kv_sets, int N);
 
 /* Host copy of a weight or cache tensor by name ("blk.3.qkv", "lm_head",
- * "output_norm", "kv_k4_3", ...): quantized weights come back as GGUF bytes. */
+ * "output_norm", "kv_k4_3", ...): quantized weights come back as GGUF bytes.
+ * Tensors of the last decode step's graph are found by name too: each
+ * layer's output rows "layer_out-<l>" f32 [N][hidden], "hidden_out",
+ * "logits". */
 int64_t mm_lm_tensor_nbytes(void * lm, const char * name);
 int     mm_lm_get_tensor(void * lm, const char * name, void * dst, size_t size);
 /* Overwrite a tensor from host bytes (GGUF bytes for quantized weights). */

@@ -106,9 +106,13 @@ bool fill_normal(ggml_tensor * t, uint64_t seed, float mean, float stdv) {
            hipDeviceSynchronize() == hipSuccess;
 }
 
+// Weights and caches by name, then the current decode graph's tensors (the
+// graph allocator gives each its own memory, so a node's rows stay readable
+// until the next step).
 ggml_tensor * find_tensor(Lm * m, const char * name) {
     ggml_tensor * t = ggml_get_tensor(m->wctx, name);
-    return t ? t : ggml_get_tensor(m->kv_ctx, name);
+    t               = t ? t : ggml_get_tensor(m->kv_ctx, name);
+    return t || !m->gf ? t : ggml_graph_get_tensor(m->gf, name);
 }
 
 // Build the batched decode graph: src/qwen3-lm.h:695-856.
@@ -195,6 +199,7 @@ void build_graph(Lm * m, int N, int n_kv_pad, int s0) {
         ggml_tensor * ff = ggml_swiglu(ctx, gu);
         ggml_tensor * mlp = ggml_mul_mat(ctx, ly->down, ff);
         hidden            = ggml_add(ctx, hidden, mlp);
+        ggml_format_name(hidden, "layer_out-%d", l);  // readable after the step (mm_lm_get_tensor)
     }
 
     hidden = rms_norm_mul(ctx, hidden, m->final_norm, c.rms_eps);

@@ -32,6 +32,11 @@ class LmState:
         self.w["output_norm"] = lm.get("output_norm", np.float32)
         self.w["lm_head"] = lm.get("lm_head")
         # caches: ggml [D, max_seq, Nkv, n_sets] -> numpy [n_sets, Nkv, max_seq, D]
+        self.refresh_kv(lm)
+
+    def refresh_kv(self, lm):
+        """Take the device's KV caches as they are now."""
+        c = self.c
         shp = (c.n_sets, c.n_kv_heads, c.max_seq, c.head_dim)
         self.k = [lm.get(f"kv_k4_{l}", np.float16).reshape(shp).copy() for l in range(c.n_layers)]
         self.v = [lm.get(f"kv_v4_{l}", np.float16).reshape(shp).copy() for l in range(c.n_layers)]
@@ -100,11 +105,8 @@ def prefill(st, tokens, kv_set, kv_pos, flavour="ggml"):
     return mm("lm_head", c.vocab, H, hid[-1:])[0], hid
 
 
-def decode(st, embeds, sets, kv_pos, flavour="ggml"):
-    """One step; updates st's caches. kv_pos: positions of the sets before the step."""
+def _decode_setup(st, sets, kv_pos, flavour):
     c = st.c
-    H, D, Nh, Nkv = c.hidden, c.head_dim, c.n_heads, c.n_kv_heads
-    q_dim, kv_dim = Nh * D, Nkv * D
     N = len(sets)
     t = c.wtype
 
@@ -119,33 +121,71 @@ def decode(st, embeds, sets, kv_pos, flavour="ggml"):
     for i, s in enumerate(sets):
         mask[i, ..., kv_pos[s] + 1:] = -np.inf
     pos = np.array([kv_pos[s] for s in sets], np.int32)
+    return mm, mask, pos, n_kv_pad
+
+
+def _decode_layer(st, l, h, sets, mm, mask, pos, n_kv_pad, flavour):
+    """One layer of qw3lm_forward_batch (src/qwen3-lm.h:730-840) on the rows
+    h [N, H]; writes the step's K / V rows into st's caches."""
+    c = st.c
+    H, D, Nh, Nkv = c.hidden, c.head_dim, c.n_heads, c.n_kv_heads
+    q_dim, kv_dim = Nh * D, Nkv * D
+    N = len(sets)
     scale = float(np.float32(1.0 / np.sqrt(D)))
-    h = np.asarray(embeds, np.float32)
-    for l in range(c.n_layers):
-        p = f"blk.{l}."
-        x = oracle.rms_norm_mul(h, st.w[p + "attn_norm"], c.rms_eps)
-        qkv = mm(p + "qkv", q_dim + 2 * kv_dim, H, x)
-        q = qkv[:, :q_dim].reshape(N, Nh, D)
-        k = qkv[:, q_dim:q_dim + kv_dim].reshape(N, Nkv, D)
-        v = qkv[:, q_dim + kv_dim:].reshape(N, Nkv, D)
-        q = oracle.rms_norm_mul(q, st.w[p + "q_norm"], c.rms_eps)
-        k = oracle.rms_norm_mul(k, st.w[p + "k_norm"], c.rms_eps)
-        q = oracle.rope_neox(q, pos, D, c.rope_theta)
-        k = oracle.rope_neox(k, pos, D, c.rope_theta)
-        for i, s in enumerate(sets):
-            st.k[l][s, :, pos[i]] = k[i].astype(np.float16)
-            st.v[l][s, :, pos[i]] = v[i].astype(np.float16)
-        s0 = sets[0]
-        kw = np.ascontiguousarray(st.k[l][s0:s0 + N, :, :n_kv_pad])
-        vw = np.ascontiguousarray(st.v[l][s0:s0 + N, :, :n_kv_pad])
-        q4 = np.ascontiguousarray(q[:, :, None, :])  # [B=N, Hq, nq=1, D]
-        o = oracle.flash_attn_ext(q4, kw, vw, mask, scale, "ggml" if flavour == "ggml" else "f64")
-        attn = np.asarray(o, np.float32).reshape(N, q_dim)
-        h = h + mm(p + "o_proj", H, q_dim, attn)
-        x = oracle.rms_norm_mul(h, st.w[p + "ffn_norm"], c.rms_eps)
-        gu = mm(p + "gate_up", 2 * c.ffn, H, x)
-        ff = oracle.swiglu(gu)
-        h = h + mm(p + "down", H, c.ffn, ff)
+    p = f"blk.{l}."
+    x = oracle.rms_norm_mul(h, st.w[p + "attn_norm"], c.rms_eps)
+    qkv = mm(p + "qkv", q_dim + 2 * kv_dim, H, x)
+    q = qkv[:, :q_dim].reshape(N, Nh, D)
+    k = qkv[:, q_dim:q_dim + kv_dim].reshape(N, Nkv, D)
+    v = qkv[:, q_dim + kv_dim:].reshape(N, Nkv, D)
+    q = oracle.rms_norm_mul(q, st.w[p + "q_norm"], c.rms_eps)
+    k = oracle.rms_norm_mul(k, st.w[p + "k_norm"], c.rms_eps)
+    q = oracle.rope_neox(q, pos, D, c.rope_theta)
+    k = oracle.rope_neox(k, pos, D, c.rope_theta)
+    for i, s in enumerate(sets):
+        st.k[l][s, :, pos[i]] = k[i].astype(np.float16)
+        st.v[l][s, :, pos[i]] = v[i].astype(np.float16)
+    s0 = sets[0]
+    kw = np.ascontiguousarray(st.k[l][s0:s0 + N, :, :n_kv_pad])
+    vw = np.ascontiguousarray(st.v[l][s0:s0 + N, :, :n_kv_pad])
+    q4 = np.ascontiguousarray(q[:, :, None, :])  # [B=N, Hq, nq=1, D]
+    o = oracle.flash_attn_ext(q4, kw, vw, mask, scale, "ggml" if flavour == "ggml" else "f64")
+    attn = np.asarray(o, np.float32).reshape(N, q_dim)
+    h = h + mm(p + "o_proj", H, q_dim, attn)
+    x = oracle.rms_norm_mul(h, st.w[p + "ffn_norm"], c.rms_eps)
+    gu = mm(p + "gate_up", 2 * c.ffn, H, x)
+    ff = oracle.swiglu(gu)
+    return h + mm(p + "down", H, c.ffn, ff)
+
+
+def _decode_head(st, h, mm):
+    """Final norm and lm_head (src/qwen3-lm.h:843-856): (logits, hidden)."""
+    c = st.c
     hid = oracle.rms_norm_mul(h, st.w["output_norm"], c.rms_eps)
-    logits = mm("lm_head", c.vocab, H, hid)
-    return logits, hid
+    return mm("lm_head", c.vocab, c.hidden, hid), hid
+
+
+def decode(st, embeds, sets, kv_pos, flavour="ggml"):
+    """One step; updates st's caches. kv_pos: positions of the sets before the step."""
+    mm, mask, pos, n_kv_pad = _decode_setup(st, sets, kv_pos, flavour)
+    h = np.asarray(embeds, np.float32)
+    for l in range(st.c.n_layers):
+        h = _decode_layer(st, l, h, sets, mm, mask, pos, n_kv_pad, flavour)
+    return _decode_head(st, h, mm)
+
+
+def decode_teacher_forced(st, embeds, layer_outs, sets, kv_pos, flavour="ggml"):
+    """The step with each layer restated from the device's own input rows of
+    that layer: layer l starts from layer_outs[l - 1] (the device's rows after
+    layer l - 1; the embeddings for layer 0), the final norm and lm_head from
+    layer_outs[-1].  A difference in one layer is therefore not carried into
+    the next (a few int8 activation codes rounding the other way when their
+    f32 inputs differ in the last bits would otherwise cascade).  Returns
+    (restated layer outputs, logits, hidden); updates st's caches."""
+    mm, mask, pos, n_kv_pad = _decode_setup(st, sets, kv_pos, flavour)
+    outs = []
+    for l in range(st.c.n_layers):
+        h = np.asarray(embeds if l == 0 else layer_outs[l - 1], np.float32)
+        outs.append(_decode_layer(st, l, h, sets, mm, mask, pos, n_kv_pad, flavour))
+    logits, hid = _decode_head(st, np.asarray(layer_outs[-1], np.float32), mm)
+    return outs, logits, hid

@@ -11,11 +11,9 @@ path, HIP-graph replays).
 
 Stated tolerances:
 - prefill logits / hidden against the ggml-CPU-semantics restatement
-  (tests/lm_reference.py): equal argmax, cosine >= 0.9999, or 1 - cosine at
-  most 2x the restatement's own distance from f64 arithmetic where that
-  exceeds 5e-5 (the GEMM path rounds activations to f16 where ggml-CPU
-  quantises them to Q8_0); never more than 1.5x as far from f64 as the
-  restatement;
+  (tests/lm_reference.py): equal argmax, cosine >= 0.9999, and never more
+  than 1.5x as far from f64 as the restatement (the GEMM path rounds
+  activations to f16 where ggml-CPU quantises them to Q8_0);
 - KV rows written by the prefill: within 2e-2 of each row's largest
   magnitude, unwritten rows byte-equal (zero);
 - decode logits and hidden states: bit-identical to mm_lm (this build's
@@ -109,10 +107,10 @@ def _check_weights(path, refw):
 
 def _close(a, ref, exact):
     """The stated tolerance of a GPU result against the ggml-semantics
-    restatement `ref` and the f64 restatement `exact`."""
+    restatement `ref` and the f64 restatement `exact`: cosine >= 0.9999, and
+    at most 1.5x as far from exact as the restatement is."""
     ref_err = 1 - cosine(ref, exact)
-    bar = 1e-4 if ref_err <= 5e-5 else 2 * ref_err
-    assert 1 - cosine(a, ref) <= bar, (cosine(a, ref), ref_err)
+    assert cosine(a, ref) >= 0.9999, (cosine(a, ref), ref_err)
     assert 1 - cosine(a, exact) <= 1.5 * ref_err + 1e-6, (cosine(a, exact), ref_err)
 
 
