@@ -373,9 +373,29 @@ __device__ __forceinline__ void fa_dma16(const void * src, uint32_t lds_addr) {
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 
-__global__ __launch_bounds__(512) void k_fa_dma(FaArgs a, int n_qtiles, float * __restrict__ out) {
-    constexpr int D = 128, NQK = 8, NDB = 4, TILE = FA_BK * 256;
-    __shared__ __attribute__((aligned(1024))) char smem[4 * TILE];  // K ring (2 tiles), V ring (2 tiles)
+// Masked form (MASK: the LM's causal prefill, src/qwen3-lm.h:432-436, or any
+// f16 mask), with the mask prepass's per-row ends: the workgroup pairs the
+// 128-row query tile t (waves 0-3) with tile n128 - 1 - t (waves 4-7), so that
+// under a causal mask every SIMD holds one short and one long row range; the
+// K / V tiles are staged up to the last key any row of the workgroup can
+// see, and a wave computes up to the last key its own rows can see, then only
+// takes part in the staging.  A unit past the wave's all-zero mask prefix
+// adds the mask (log2 units) to its scores, loaded while the unit before it
+// runs.  A row's running max is set on its first unit with a visible key.
+//
+// Both forms stage K and V through 4-tile rings (128 KB of LDS, one
+// workgroup per CU as the registers allow anyway), each tile issued three
+// 64-key steps before its first reader and waited for by count, so the
+// loads of the two younger steps stay in flight across a barrier: once the
+// short rows of a masked workgroup are done, one wave per SIMD is left to
+// cover the load latency of each step.
+template <bool MASK>
+__global__ __launch_bounds__(512, 2) void k_fa_dma(FaArgs a, const int * __restrict__ row_end,
+                                                   const int * __restrict__ zero_end, int n_qtiles,
+                                                   float * __restrict__ out) {
+    constexpr int D = 128, NQK = 8, NDB = 4, TILE = FA_BK * 256, NW = 8;
+    constexpr int KR = 4, US = 1;  // ring tiles (K and V each); unit stride of a wave
+    extern __shared__ __attribute__((aligned(1024))) char smem[];  // K ring, then V ring
     const int  total = n_qtiles * a.Hq * a.B;
     const int  lin   = xcd_remap((int) blockIdx.x, total);
     const int  qt    = lin % n_qtiles;
@@ -388,9 +408,45 @@ __global__ __launch_bounds__(512) void k_fa_dma(FaArgs a, int n_qtiles, float * 
     const int  lane  = tid & 63;
     const int  lq    = lane & 31;
     const int  hh    = lane >> 5;
-    const int  my_q  = qt * 256 + wave * 32 + lq;
-    const bool q_ok  = my_q < a.nq;
-    const float sl2  = a.scale * 1.4426950408889634f;
+    const int   par  = 0;  // the wave's first unit
+    int         my_q;
+    if constexpr (MASK) {
+        const int n128 = (a.nq + 127) / 128;
+        const int half = wave >> 2;
+        const int t128 = half ? n128 - 1 - qt : qt;
+        my_q           = half && t128 <= qt ? a.nq : t128 * 128 + (wave & 3) * 32 + lq;
+    } else {
+        my_q = qt * 256 + wave * 32 + lq;
+    }
+    const bool  q_ok = my_q < a.nq;
+    const float log2e = 1.4426950408889634f;
+    const float sl2   = a.scale * log2e;
+
+    // keys: the workgroup stages [0, kv_end), this wave computes [0, w_end),
+    // and units wholly inside [0, zfast) need no mask (all-zero prefix)
+    int          kv_end = a.nkv, w_end = a.nkv, zfast = a.nkv;
+    const char * mrow   = nullptr;
+    if constexpr (MASK) {
+        __shared__ int s_end[NW];
+        const int      plane = (b % a.mne3) * a.mne2 + (h % a.mne2);
+        const int      e     = q_ok ? row_end[(int64_t) plane * a.nq + my_q] : 0;
+        const int      z     = q_ok ? zero_end[(int64_t) plane * a.nq + my_q] : a.nkv;
+        // wave-uniform values (readfirstlane: the loop bounds and DMA
+        // addresses below must live in scalar registers)
+        w_end = __builtin_amdgcn_readfirstlane(min(a.nkv, (int) wave_max((float) e)));
+        zfast = __builtin_amdgcn_readfirstlane(-(int) wave_max((float) -z));
+        if (lane == 0) {
+            s_end[wave] = w_end;
+        }
+        __syncthreads();
+        int te = 0;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            te = max(te, s_end[w]);
+        }
+        kv_end = __builtin_amdgcn_readfirstlane(te);
+        mrow   = a.mask + (int64_t) (q_ok ? my_q : 0) * a.mnb1 + (h % a.mne2) * a.mnb2 + (b % a.mne3) * a.mnb3;
+    }
 
     // Q^T operand: dims 16 kk + 8 hh + 0..7 of this lane's query, scaled, f16
     half8_t qreg[NQK];
@@ -417,8 +473,42 @@ __global__ __launch_bounds__(512) void k_fa_dma(FaArgs a, int n_qtiles, float * 
     }
     float m = 0.0f;  // running row max (log2 units)
     float l = 0.0f;  // this lane's half of the row sum
-    const int n  = (a.nkv + FA_BK - 1) / FA_BK;  // 64-key tiles
-    const int nu = (a.nkv + 31) / 32;            // 32-key units
+    bool  mset = false;                           // (MASK) the running max is set for this lane's row
+    const int n     = (kv_end + FA_BK - 1) / FA_BK;  // 64-key tiles staged
+    const int nu_wg = (kv_end + 31) / 32;            // 32-key units staged
+    const int nu    = (w_end + 31) / 32;             // 32-key units the wave's rows see
+    const int nk    = nu;                            // units this wave computes
+
+    // the mask of this lane's query at the 16 keys of unit u it holds
+    // (k0 + 8 g4 + 4 hh + i, i = 0..3), f16 bits; -inf past the keys
+    uint2      mw[4];
+    const bool m8 = MASK && ((((uintptr_t) mrow) & 7) == 0);
+    auto mask_need = [&](int u) { return MASK && u * 32 + 32 > zfast; };
+    auto mask_load = [&](int u) {
+#pragma unroll
+        for (int g4 = 0; g4 < 4; g4++) {
+            const int key0 = u * 32 + 8 * g4 + 4 * hh;
+            if (m8 && key0 + 3 < a.nkv) {
+                mw[g4] = *(const uint2 *) (mrow + (int64_t) key0 * 2);
+            } else {
+                uint16_t hv[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    hv[i] = key0 + i < a.nkv ? ((const uint16_t *) mrow)[key0 + i] : (uint16_t) 0xfc00;
+                }
+                mw[g4] = uint2{ (uint32_t) hv[0] | ((uint32_t) hv[1] << 16), (uint32_t) hv[2] | ((uint32_t) hv[3] << 16) };
+            }
+        }
+    };
+    auto mask_apply = [&](float16_t & s) {
+#pragma unroll
+        for (int g4 = 0; g4 < 4; g4++) {
+            s[4 * g4 + 0] += h2f((uint16_t) (mw[g4].x & 0xffff)) * log2e;
+            s[4 * g4 + 1] += h2f((uint16_t) (mw[g4].x >> 16)) * log2e;
+            s[4 * g4 + 2] += h2f((uint16_t) (mw[g4].y & 0xffff)) * log2e;
+            s[4 * g4 + 3] += h2f((uint16_t) (mw[g4].y >> 16)) * log2e;
+        }
+    };
 
     // DMA: this wave fills 1 KB pieces 2 wave and 2 wave + 1 (4 rows each) of
     // a K and a V tile; lane -> row 4 piece + lane / 16, stored chunk lane % 16
@@ -431,7 +521,7 @@ __global__ __launch_bounds__(512) void k_fa_dma(FaArgs a, int n_qtiles, float * 
         for (int i = 0; i < 2; i++) {
             const int piece = 2 * wave + i, r = 4 * piece + drow;
             const int key   = min(j * FA_BK + r, a.nkv - 1);  // rows past the end repeat the last key (masked below)
-            fa_dma16(kbase + (int64_t) key * a.knb1 + ((dpc ^ (r & 15)) << 4), sbase + (j & 1) * TILE + piece * 1024);
+            fa_dma16(kbase + (int64_t) key * a.knb1 + ((dpc ^ (r & 15)) << 4), sbase + (j & 3) * TILE + piece * 1024);
         }
     };
     auto dma_v = [&](int j) {
@@ -440,7 +530,7 @@ __global__ __launch_bounds__(512) void k_fa_dma(FaArgs a, int n_qtiles, float * 
             const int piece = 2 * wave + i, r = 4 * piece + drow;
             const int key   = min(j * FA_BK + r, a.nkv - 1);
             fa_dma16(vbase + (int64_t) key * a.vnb1 + ((dpc ^ (2 * (r & 3))) << 4),
-                     sbase + (2 + (j & 1)) * TILE + piece * 1024);
+                     sbase + (KR + (j & 3)) * TILE + piece * 1024);
         }
     };
     // K operand of k-step kk: row lq of the 32-key unit, logical chunk 2 kk + hh
@@ -458,12 +548,12 @@ __global__ __launch_bounds__(512) void k_fa_dma(FaArgs a, int n_qtiles, float * 
         (4 * (tg >> 1) + tj) * 256 + 16 * ((2 * (tg & 1) + (tq >> 1)) ^ (2 * (tj & 1))) + 8 * (tq & 1);
     const uint32_t vb[2] = { vlane + vx, vlane - vx };
     auto qk_op = [&](int u, int kk) -> half8_t {
-        const char * kt = smem + ((u >> 1) & 1) * TILE;
+        const char * kt = smem + ((u >> 1) & 3) * TILE;
         return *(const half8_t *) (kt + ka[kk] + (u & 1) * 8192);
     };
     // PV step i of a unit: key half t = i / 4 (16 keys), output block db = i % 4
     auto pv_op = [&](int u, int i) -> half8_t {
-        const uint32_t vt = sbase + (2 + ((u >> 1) & 1)) * TILE;
+        const uint32_t vt = sbase + (KR + ((u >> 1) & 3)) * TILE;
         const int      t = i >> 2, db = i & 3;
         half8_t        av;
 #pragma unroll
@@ -501,17 +591,23 @@ __global__ __launch_bounds__(512) void k_fa_dma(FaArgs a, int n_qtiles, float * 
     };
     // move m to the row max (first unit: exactly; later: upwards only),
     // rescale O and l, redo the unit's p
-    auto slow = [&](float & rs, bool first) {
+    auto slow = [&](float & rs, bool first_unit) {
         float mx = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             mx = fmaxf(mx, sc[r]);
         }
-        mx            = max_xor32(mx);
-        const float d = first ? (mx == -INFINITY ? 0.0f : mx) : (mx > 0.0f ? mx : 0.0f);
+        mx = max_xor32(mx);
+        // first: nothing visible accumulated yet (O and l zero), m goes to
+        // the unit's max exactly; otherwise it moves up only
+        const bool  first = MASK ? !mset : first_unit;
+        const float d     = first ? (mx == -INFINITY ? 0.0f : mx) : (mx > 0.0f ? mx : 0.0f);
+        if constexpr (MASK) {
+            mset = mset || mx != -INFINITY;
+        }
         if (__any(d != 0.0f)) {
-            if (!first) {  // O and l are still zero on the first unit
-                const float alpha = __builtin_amdgcn_exp2f(-d);
+            if (__any(!first)) {
+                const float alpha = first ? 1.0f : __builtin_amdgcn_exp2f(-d);
                 l *= alpha;
 #pragma unroll
                 for (int q = 0; q < NDB; q++) {
@@ -533,7 +629,7 @@ __global__ __launch_bounds__(512) void k_fa_dma(FaArgs a, int n_qtiles, float * 
         }
         exp_pack(rs);
     };
-    // unit u: softmax(u) (SM), QK(u + 1) (QK), PV(u - 1) (PV); which parts
+    // unit u: softmax(u) (SM), QK(u + US) (QK), PV(u - US) (PV); which parts
     // are present is a compile-time choice, so the steady-state unit is
     // branch-free and the compiler interleaves its VALU work with the MFMAs
     auto unit = [&](int u, auto QKc, auto PVc, auto SMc) {
@@ -553,21 +649,21 @@ __global__ __launch_bounds__(512) void k_fa_dma(FaArgs a, int n_qtiles, float * 
         float       rs     = 0.0f;
         half8_t     av[3], ak[3];
         if constexpr (do_pv) {
-            av[0] = pv_op(u - 1, 0);
-            av[1] = pv_op(u - 1, 1);
+            av[0] = pv_op(u - US, 0);
+            av[1] = pv_op(u - US, 1);
         }
         if constexpr (do_qk) {
-            ak[0] = qk_op(u + 1, 0);
-            ak[1] = qk_op(u + 1, 1);
+            ak[0] = qk_op(u + US, 0);
+            ak[1] = qk_op(u + US, 1);
         }
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             if (i + 2 < 8) {
                 if constexpr (do_pv) {
-                    av[(i + 2) % 3] = pv_op(u - 1, i + 2);
+                    av[(i + 2) % 3] = pv_op(u - US, i + 2);
                 }
                 if constexpr (do_qk) {
-                    ak[(i + 2) % 3] = qk_op(u + 1, i + 2);
+                    ak[(i + 2) % 3] = qk_op(u + US, i + 2);
                 }
             }
             if constexpr (do_pv) {
@@ -586,7 +682,7 @@ __global__ __launch_bounds__(512) void k_fa_dma(FaArgs a, int n_qtiles, float * 
             }
         }
         if constexpr (do_sm) {
-            if (u == 0 || __any(rs > 16384.0f)) {
+            if ((MASK ? __any(!mset) : u == 0) || __any(rs > 16384.0f)) {
                 slow(rs, u == 0);
             }
             l += rs;
@@ -595,11 +691,24 @@ __global__ __launch_bounds__(512) void k_fa_dma(FaArgs a, int n_qtiles, float * 
             m_sn = m_used;
         }
     };
+    // DMA group g (g >= -2): K tile g + 4 and V tile g + 3, each 2 loads per
+    // wave when the tile exists; group -2 and -1 go out after the prologue,
+    // group j after the barrier that follows unit 2 j
+    auto group_loads = [&](int g) { return 2 * (g + 4 < n) + 2 * (g + 3 < n); };
+    auto issue_group = [&](int g) {
+        if (g + 4 < n) {
+            dma_k(g + 4);
+        }
+        if (g + 3 < n) {
+            dma_v(g + 3);
+        }
+    };
     // after unit u: sn becomes the next softmax input (shifted if m moved
-    // since it was computed); after an even unit 2 j: barrier, then the DMA
-    // of K tile j + 2 (into the buffer of K tile j, last read in unit 2 j) and
-    // V tile j + 1 (buffer of V tile j - 1, last read in unit 2 j), waited
-    // for before the barrier after unit 2 j + 2
+    // since it was computed); after an even unit 2 j: the wait for K tile
+    // j + 1 and V tile j (group j - 3: only the loads of groups j - 2 and
+    // j - 1 may still be in flight), the barrier, then group j: K tile j + 4
+    // into the buffer of K tile j (last read in unit 2 j), V tile j + 3 into
+    // that of V tile j - 1 (last read in unit 2 j)
     auto after = [&](int u) {
         sc = sn;
         if (__any(m_sn != m)) {
@@ -608,51 +717,90 @@ __global__ __launch_bounds__(512) void k_fa_dma(FaArgs a, int n_qtiles, float * 
                 sc[r] += m_sn - m;
             }
         }
+        if (mask_need(u + US) && u + US < nu) {
+            mask_apply(sc);
+        }
         pp[0] = pn[0];
         pp[1] = pn[1];
         if ((u & 1) == 0) {
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            asm volatile("s_barrier" ::: "memory");
             const int j = u >> 1;
-            if (j + 2 < n) {
-                dma_k(j + 2);
+            switch (group_loads(j - 2) + group_loads(j - 1)) {
+                case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+                case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
+                case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+                case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
+                default: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
             }
-            if (j + 1 < n) {
-                dma_v(j + 1);
-            }
+            asm volatile("s_barrier" ::: "memory");
+            issue_group(j);
         }
     };
 
-    // prologue: K tiles 0 and 1, V tile 0 resident; scores of unit 0 (m = 0)
+    // prologue: K tiles 0 and 1, V tile 0 resident, groups -2 and -1 issued
+    // behind the barrier; the scores of the wave's first unit (m = 0)
+    const int u0 = par;
     dma_k(0);
     if (n > 1) {
         dma_k(1);
     }
-    dma_v(0);
+    if (n > 0) {
+        dma_v(0);
+    }
+    if (mask_need(u0) && nk > 0) {
+        mask_load(u0);
+    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     asm volatile("s_barrier" ::: "memory");
+    issue_group(-2);
+    issue_group(-1);
     sc = zero16;
+    if (nk > 0) {
 #pragma unroll
-    for (int kk = 0; kk < NQK; kk++) {
-        sc = mfma32(qk_op(0, kk), qreg[kk], sc);
+        for (int kk = 0; kk < NQK; kk++) {
+            sc = mfma32(qk_op(u0, kk), qreg[kk], sc);
+        }
+        if (mask_need(u0)) {
+            mask_apply(sc);
+        }
     }
     using T_ = std::integral_constant<bool, true>;
     using F_ = std::integral_constant<bool, false>;
-    if (nu > 1) {
-        unit(0, T_{}, F_{}, T_{});
-    } else {
-        unit(0, F_{}, F_{}, T_{});
+    // the wave's own units u0, u0 + US, ... (nk of them, each followed by
+    // after(u): the barrier and the wave's share of the staging), the PV of
+    // its last unit, then (masked: a wave whose rows see fewer keys than the
+    // workgroup stages) after() alone for the remaining staged tiles.  The
+    // drained PV reads a V tile that is restaged after the next step at the
+    // earliest.
+    if (nk > 0) {
+        if (nk > 1 && mask_need(u0 + US)) {
+            mask_load(u0 + US);
+        }
+        if (nk > 1) {
+            unit(u0, T_{}, F_{}, T_{});
+        } else {
+            unit(u0, F_{}, F_{}, T_{});
+        }
+        after(u0);
+        for (int i = 1; i + 1 < nk; i++) {
+            const int u = u0 + i * US;
+            if (mask_need(u + US)) {
+                mask_load(u + US);
+            }
+            unit(u, T_{}, T_{}, T_{});
+            after(u);
+        }
+        if (nk > 1) {
+            const int u = u0 + (nk - 1) * US;
+            unit(u, F_{}, T_{}, T_{});
+            after(u);
+        }
+        unit(u0 + nk * US, F_{}, T_{}, F_{});
     }
-    after(0);
-    for (int u = 1; u + 1 < nu; u++) {
-        unit(u, T_{}, T_{}, T_{});
-        after(u);
+    if constexpr (MASK) {
+        for (int u = nu; u < nu_wg; u++) {
+            after(u);
+        }
     }
-    if (nu > 1) {
-        unit(nu - 1, F_{}, T_{}, T_{});
-        after(nu - 1);
-    }
-    unit(nu, F_{}, T_{}, F_{});
 
     l += __shfl_xor(l, 32);
     if (q_ok) {
@@ -672,12 +820,19 @@ __global__ __launch_bounds__(512) void k_fa_dma(FaArgs a, int n_qtiles, float * 
 }
 
 // k_fa_dma's preconditions: 16-byte aligned Q rows (float4 loads) and K / V
-// rows (16-byte DMA), D = 128, no mask, and at least one workgroup of 256
-// rows per CU
+// rows (16-byte DMA), D = 128, and at least one workgroup of 256 rows per CU
+// (MMHIP_DISABLE_FA_DMA=1 takes the register-staged kernel instead)
+constexpr size_t FA_DMA_LDS = 8 * FA_BK * 256;  // K and V rings of 4 tiles
+
+static int fa_dma_qtiles(const FaArgs & a) {
+    return a.mask ? ((a.nq + 127) / 128 + 1) / 2 : (a.nq + 255) / 256;
+}
+
 static bool fa_dma_ok(const FaArgs & a, int D) {
     auto al16 = [](int64_t v) { return (v & 15) == 0; };
-    const int64_t tiles = (int64_t) ((a.nq + 255) / 256) * a.Hq * a.B;
-    return D == 128 && !a.mask && tiles >= 256 && a.nkv >= 1 && al16((int64_t) (uintptr_t) a.q) && al16(a.qnb1) &&
+    const int64_t tiles = (int64_t) fa_dma_qtiles(a) * a.Hq * a.B;
+    return D == 128 && !getenv("MMHIP_DISABLE_FA_DMA") && tiles >= 256 && a.nkv >= 1 &&
+           al16((int64_t) (uintptr_t) a.q) && al16(a.qnb1) &&
            al16(a.qnb2) && al16(a.qnb3) && al16((int64_t) (uintptr_t) a.k) && al16(a.knb1) && al16(a.knb2) &&
            al16(a.knb3) && al16((int64_t) (uintptr_t) a.v) && al16(a.vnb1) && al16(a.vnb2) && al16(a.vnb3);
 }
@@ -781,8 +936,21 @@ int fa_mfma(const FaArgs & a, int D, float * out, void * ws, size_t ws_bytes, hi
         }
     }
     if (fa_dma_ok(a, D)) {
-        const int nqt = (a.nq + 255) / 256;
-        hipLaunchKernelGGL(k_fa_dma, dim3((unsigned) (nqt * a.Hq * a.B)), dim3(512), 0, stream, a, nqt, out);
+        const int    nqt = fa_dma_qtiles(a);
+        const size_t lds = FA_DMA_LDS;
+        if (a.mask) {
+            if (!ensure_lds_limit((const void *) k_fa_dma<true>, lds)) {
+                return set_error(MMHIP_ERR_HIP, "flash_attn dma: cannot raise the LDS limit");
+            }
+            hipLaunchKernelGGL(k_fa_dma<true>, dim3((unsigned) (nqt * a.Hq * a.B)), dim3(512), lds, stream, a,
+                               row_end, zero_end, nqt, out);
+        } else {
+            if (!ensure_lds_limit((const void *) k_fa_dma<false>, lds)) {
+                return set_error(MMHIP_ERR_HIP, "flash_attn dma: cannot raise the LDS limit");
+            }
+            hipLaunchKernelGGL(k_fa_dma<false>, dim3((unsigned) (nqt * a.Hq * a.B)), dim3(512), lds, stream, a,
+                               nullptr, nullptr, nqt, out);
+        }
     } else if (D == 128) {
         NW == 8 ? launch_fa_mfma<128, 8>(a, row_end, zero_end, n_qtiles, out, stream)
                 : launch_fa_mfma<128, 4>(a, row_end, zero_end, n_qtiles, out, stream);

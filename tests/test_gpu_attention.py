@@ -299,3 +299,60 @@ def test_decode_with_quantised_output(mm, orc, wt):
     assert torch.equal(xq, ref_q)
     kn, vn = kw.cpu().numpy(), vw.cpu().numpy()
     check(out.cpu().numpy(), orc.flash_attn_ext(q, kn, vn, mask, s, "f64"), orc.flash_attn_ext(q, kn, vn, mask, s, "ggml"))
+
+
+@pytest.mark.parametrize("B,Bk,Hq,Hkv,nq,nkv,kind", [(1, 1, 64, 8, 1000, 1100, "random"),
+                                                   (2, 2, 32, 8, 1100, 1300, "causal"),
+                                                   (2, 1, 64, 64, 257, 333, "random"),
+                                                   (1, 1, 256, 32, 130, 130, "causal")])
+def test_dma_kernel_masked(mm, orc, B, Bk, Hq, Hkv, nq, nkv, kind):
+    """Masked D = 128 on >= 256 workgroups: the DMA-fed kernel with the mask
+    prepass's row ends, 128-row query tiles paired from opposite ends (an odd
+    count leaves the middle tile alone), waves that stop before the
+    workgroup's last staged key, the mask added past each wave's all-zero
+    prefix.  Random masks (-inf, biases, a fully masked row -> 0) and causal
+    masks behind a 170-key visible prefix; 48 sampled rows against fp64."""
+    q = rnd((B, Hq, nq, 128), 111)
+    k = rnd((Bk, Hkv, nkv, 128), 112, np.float16)
+    v = rnd((Bk, Hkv, nkv, 128), 113, np.float16)
+    rng = np.random.default_rng(114)
+    if kind == "random":
+        mask = np.where(rng.random((B, 1, nq, nkv)) < 0.3, -np.inf, rng.normal(0, 1, (B, 1, nq, nkv)))
+        mask[:, :, 5] = -np.inf
+    else:
+        off = nkv - nq if nkv > nq else 0
+        mask = np.full((1, 1, nq, nkv), -np.inf)
+        for i in range(nq):
+            mask[0, 0, i, :off + i + 1] = 0
+    mask = mask.astype(np.float16)
+    s = float(np.float32(1 / np.sqrt(128)))
+    out = mm.flash_attn_ext(torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                            torch.from_numpy(mask).cuda(), s).cpu().numpy()
+    rows = np.unique(np.array([0, 1, 5, 31, 32, 127, 128, nq // 2, nq - 2, nq - 1] +
+                              list(rng.choice(nq, 38, replace=False))))
+    check(out[:, rows], oracle_rows(orc, q, k, v, mask, s, rows))
+    if kind == "random":
+        assert not out[:, 5].any()
+
+
+def test_replay_prefill_9000_tokens(mm, orc):
+    """The replay prefill (src/pipeline.cpp:288, one qw3lm_forward over up to
+    9000 feedback frames; qw3lm_build_attn, src/qwen3-lm.h:346-443) for one
+    CFG set: Q the permuted view of [D, Nh, S], K / V the [0, n_kv_pad = 9216)
+    windows of the [D, max_seq, Nkv] f16 cache, the [n_kv_pad, S] f16 causal
+    mask with its -inf padded tail (166 MB).  32 sampled rows against fp64."""
+    S, Hq, Hkv, D, max_seq, pad = 9000, 32, 8, 128, 9472, 9216
+    qst = rnd((S, Hq, D), 121)                                       # ggml [D, Nh, S]
+    cache_k = torch.from_numpy(rnd((Hkv, max_seq, D), 122, np.float16)).cuda()
+    cache_v = torch.from_numpy(rnd((Hkv, max_seq, D), 123, np.float16)).cuda()
+    kw, vw = cache_k[:, :pad], cache_v[:, :pad]
+    mask = np.triu(np.full((S, pad), -np.inf, np.float32), 1).astype(np.float16)[None, None]
+    s = float(np.float32(1 / np.sqrt(D)))
+    qt = torch.from_numpy(qst).cuda()
+    qview = mm.view_of(qt, ne=[D, S, Hq, 1], nb=[4, Hq * D * 4, D * 4, S * Hq * D * 4])
+    out = mm.flash_attn_ext(qt, kw, vw, torch.from_numpy(mask).cuda(), s, q_view=qview).cpu().numpy()
+    rows = np.unique(np.array([0, 1, 127, 128, 4499, 4500, 8191, 8999] +
+                              list(np.random.default_rng(124).choice(S, 24, replace=False))))
+    qn = np.ascontiguousarray(qst.transpose(1, 0, 2))[None]
+    kn, vn = kw.cpu().numpy()[None], vw.cpu().numpy()[None]
+    check(out[:, rows], oracle_rows(orc, qn, kn, vn, mask, s, rows))
