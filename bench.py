@@ -52,7 +52,7 @@ def parse():
     ap.add_argument("--workload", default="lm_decode",
                     choices=["lm_decode", "gemv_q8_0", "fa_decode", "fa_prefill", "fa_dit", "gemm_q4_k",
                              "dit_block", "depth"])
-    ap.add_argument("--wtype", default="q8_0", choices=["q8_0", "q6_k"], help="lm_decode weight type")
+    ap.add_argument("--wtype", default="q8_0", choices=["q8_0", "q6_k", "bf16"], help="lm_decode weight type")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     return ap.parse_args()
@@ -824,7 +824,7 @@ def bench_depth(args, torch, pkg):
 # Algorithmic HBM bytes of one Qwen3-8B-shape CFG decode step at KV 4096:
 # weights + KV read + norm weights + logits + KV write (per step, both rows).
 def lm_step_bytes(cfg, wtype):
-    be, bb = {8: (32, 34), 14: (256, 210), 12: (256, 144)}[wtype]
+    be, bb = {8: (32, 34), 14: (256, 210), 12: (256, 144), 30: (1, 2)}[wtype]
     H, D, Nh, Nkv, F, V, L = (cfg["hidden"], cfg["head_dim"], cfg["n_heads"], cfg["n_kv_heads"], cfg["ffn"],
                               cfg["vocab"], cfg["n_layers"])
     per_layer_w = H * (Nh * D + 2 * Nkv * D) + Nh * D * H + H * 2 * F + F * H
@@ -842,7 +842,7 @@ def bench_lm(args, torch, pkg):
 
     lm_mod = importlib.import_module(pkg.__name__ + ".lm")
     cfg = dict(lm_mod.QWEN3_8B)
-    cfg["wtype"] = 8 if args.wtype == "q8_0" else 14
+    cfg["wtype"] = {"q8_0": 8, "q6_k": 14, "bf16": 30}[args.wtype]
     lm = lm_mod.Lm(seed=1005, **cfg)
     lm.fill_kv(0, 4095, seed=1)
     lm.fill_kv(1, 4095, seed=2)
@@ -869,9 +869,9 @@ def bench_lm(args, torch, pkg):
     replays, eager = lm.graph_stats()
     nodes = lm.graph_nodes()
     lm.close()
-    dom = lm_dominant_kernel(torch, pkg, cfg)
+    dom = lm_dominant_kernel(torch, pkg, cfg) if cfg["wtype"] != 30 else lm_dominant_kernel_bf16(torch, pkg, cfg)
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and cfg["wtype"] != 30:
         cpu = cpu_lm(args, lm_mod, cfg)
     return {
         "metric": "LM decode tok/s (CFG B=2, %s, KV 4096)" % args.wtype.upper(),
@@ -882,7 +882,8 @@ def bench_lm(args, torch, pkg):
         "ms_per_step": round(gpu_s * 1e3, 4),
         "wall_tok_s": round(2.0 / dt, 2),
         "wall_ms_per_step": round(dt * 1e3, 4),
-        "dtype": args.wtype + " weights (int8-dot GEMV), f16 KV, f32 activations",
+        "dtype": (args.wtype + " weights (int8-dot GEMV), f16 KV, f32 activations") if args.wtype != "bf16" else
+                 "bf16 weights x bf16-rounded activations (f32 sums), f16 KV, f32 activations",
         "config": {"workload": "Qwen3-8B-shape batched CFG decode step: 36 layers, hidden 4096, 32q/8kv d128, "
                                "FFN 12288 SwiGLU, vocab 151936, KV 4096 x 2 sets",
                    "weights": args.wtype, "graph_nodes": nodes, "graph_replays": replays, "eager_runs": eager,
@@ -933,6 +934,43 @@ def lm_dominant_kernel(torch, pkg, cfg):
             "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": profile_traffic("gemv_norm_glu_gate_up_24576x4096_m2"),
+            "avg_launch_us": round(avg_s * 1e6, 3), "min_launch_us": round(min_s * 1e6, 3),
+            "alg_bytes_per_launch": alg_bytes}
+
+
+def lm_dominant_kernel_bf16(torch, pkg, cfg):
+    """The BF16 step's largest kernel alone: the gate_up decode GEMV with the
+    RMS norm in its prologue and the SwiGLU in its epilogue (W [2 ffn x
+    hidden] bf16, 2 columns), three weight copies (1.2 GB) rotating past the
+    256 MB Infinity Cache, replayed as a HIP graph."""
+    L = pkg.mmhip.load()
+    N, K, M = 2 * cfg["ffn"], cfg["hidden"], 2
+    copies = 3
+    if not L.mmhip_mul_mat_bf16_dec_supported(N, K, M, 1):
+        return None
+    g = torch.Generator(device="cuda")
+    g.manual_seed(2101)
+    Ws = [(torch.randn((N, K), device="cuda", generator=g) * 0.02).to(torch.bfloat16) for _ in range(copies)]
+    x = torch.randn((M, K), device="cuda", generator=g)
+    nw = torch.ones(K, device="cuda")
+    y = torch.empty((M, N // 2), device="cuda")
+
+    def launch(i, st):
+        W = Ws[i % copies]
+        rc = L.mmhip_mul_mat_bf16_dec(ctypes.c_void_p(W.data_ptr()), N, K, K, ctypes.c_void_p(x.data_ptr()), K, M,
+                                      ctypes.c_void_p(nw.data_ptr()), 1e-6, None, 0, 1, ctypes.c_void_p(y.data_ptr()),
+                                      N // 2, st)
+        assert rc == 0, L.mmhip_last_error()
+
+    avg_s, min_s = graph_time(torch, launch, 36)
+    alg_bytes = N * K * 2 + M * K * 4 + K * 4 + M * (N // 2) * 4
+    achieved = alg_bytes / avg_s / 1e9
+    del Ws
+    torch.cuda.empty_cache()
+    return {"bound": "hbm", "kernel": "k_gemv_bf16_dec<2,NORM,GLU>: RMS norm + gate_up GEMV %d x %d BF16 + SwiGLU, "
+                                      "2 columns (the BF16 step's largest kernel)" % (N, K),
+            "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
             "avg_launch_us": round(avg_s * 1e6, 3), "min_launch_us": round(min_s * 1e6, 3),
             "alg_bytes_per_launch": alg_bytes}
 

@@ -110,6 +110,21 @@ int    mmhip_unregister_weights_f16(const void * W);
  * src/qwen3-lm.h:743-856).  K % 8 == 0, 16-byte aligned rows. */
 int    mmhip_mul_mat_bf16(const void * W, int64_t N, int64_t K, int64_t ldw, const float * x, int64_t ldx, int64_t M,
                           float * y, int64_t ldy, void * stream);
+/* BF16 weights at decode, 1-2 activation columns, as one persistent launch:
+ * the LM's projections from a BF16 model file (qwen3_linear,
+ * src/qwen3-enc.h:67-69, in qw3lm_forward_batch, src/qwen3-lm.h:742-856).
+ * norm_w != NULL: x is the block's input and its RMS norm times norm_w
+ * (src/qwen3-enc.h:87-93, eps) is computed first, with k_rms_norm_row's
+ * arithmetic; the activations are then rounded to bf16 as ggml rounds the
+ * src1 of a BF16 MUL_MAT.  r != NULL: y = r + W x (the residual ADD,
+ * src/qwen3-lm.h:827, :836).  glu != 0: the rows are a fused gate|up pair
+ * (src/qwen3-enc.h:106-108) and y[j] = silu(W_j x) * W_{N/2 + j} x, N / 2
+ * outputs per column.  W rows ldw elements apart, 16-byte aligned;
+ * K % 4096 == 0 and M K <= 32768. */
+int    mmhip_mul_mat_bf16_dec_supported(int64_t N, int64_t K, int64_t M, int glu);
+int    mmhip_mul_mat_bf16_dec(const void * W, int64_t N, int64_t K, int64_t ldw, const float * x, int64_t ldx,
+                              int64_t M, const float * norm_w, float eps, const float * r, int64_t ldr, int glu,
+                              float * y, int64_t ldy, void * stream);
 int    mmhip_mul_mat_bias_add(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const float * x,
                               int64_t ldx, int64_t M, const float * bias, const float * r, int64_t ldr, float * y,
                               int64_t ldy, void * ws, size_t ws_bytes, void * stream);

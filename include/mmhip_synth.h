@@ -24,7 +24,8 @@ extern "C" {
 /* nblocks GGUF blocks of `type` (Q8_0 / Q4_K / Q6_K) written to dst_gguf. */
 int mmhip_synth_gguf(int type, void * dst_gguf, int64_t nblocks, uint64_t seed, void * stream);
 
-/* n values of N(mean, std) as f32 (type 0) or f16 (type 1). */
+/* n values of N(mean, std) as f32 (type 0), f16 (type 1) or bf16 (type 30,
+ * rounded as ggml rounds f32 to bf16). */
 int mmhip_synth_normal(int type, void * dst, int64_t n, uint64_t seed, float mean, float std, void * stream);
 
 #ifdef __cplusplus

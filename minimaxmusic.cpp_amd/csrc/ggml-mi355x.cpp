@@ -1072,10 +1072,23 @@ int add_row_vector(const struct ggml_tensor * add, const struct ggml_tensor * n)
     return ok ? oth : -1;
 }
 
+// BF16 weights at 1-2 columns: the persistent BF16 decode GEMV (activations
+// read as f32, no quantised slot)
+bool mm_is_bf16_dec(const struct ggml_tensor * n) {
+    const struct ggml_tensor * w = n->src[0];
+    const struct ggml_tensor * x = n->src[1];
+    const int64_t              M = x->ne[1] * x->ne[2] * x->ne[3];
+    return n->op == GGML_OP_MUL_MAT && w->type == GGML_TYPE_BF16 && w->ne[2] == 1 && w->ne[3] == 1 &&
+           x->type == GGML_TYPE_F32 && mm_collapsible(x) && x->nb[1] % 16 == 0 && ((uintptr_t) x->data) % 16 == 0 &&
+           w->nb[1] % 16 == 0 && ((uintptr_t) w->data) % 16 == 0 && ggml_is_contiguous(n) &&
+           mmhip_mul_mat_bf16_dec_supported(w->ne[1], w->ne[0], M, 0) && !getenv("GGML_MI355X_DISABLE_BF16_DEC");
+}
+
 bool mm_is_gemv(const struct ggml_tensor * n) {
     const struct ggml_tensor * x = n->src[1];
     const int64_t              M = x->ne[1] * x->ne[2] * x->ne[3];
-    return n->op == GGML_OP_MUL_MAT && M >= 1 && M <= 16 && mmhip_act_bytes(n->src[0]->type, n->src[0]->ne[0], M) > 0;
+    return n->op == GGML_OP_MUL_MAT && M >= 1 && M <= 16 &&
+           (mmhip_act_bytes(n->src[0]->type, n->src[0]->ne[0], M) > 0 || mm_is_bf16_dec(n));
 }
 
 int act_vec_type(int wtype) {
@@ -1092,8 +1105,8 @@ int gemv_consumer_type(struct ggml_cgraph * g, const graph_info & gi, int p) {
     for (int ci : gi.consumers[(size_t) p]) {
         const struct ggml_tensor * m = ggml_graph_node(g, ci);
         if (m->op != GGML_OP_MUL_MAT || m->src[1] != ggml_graph_node(g, p) || m->src[0] == m->src[1] ||
-            !mm_is_gemv(m)) {
-            return 0;
+            !mm_is_gemv(m) || m->src[0]->type == GGML_TYPE_BF16) {
+            return 0;  // BF16 GEMVs read f32 activations: no slot
         }
         if (wt && act_vec_type(wt) != act_vec_type(m->src[0]->type)) {
             return 0;
@@ -1134,8 +1147,10 @@ bool norm_into_gemvs(struct ggml_cgraph * g, const graph_info & gi, int i, int j
     int last = j;
     for (int ci : gi.consumers[(size_t) j]) {
         const struct ggml_tensor * mm = ggml_graph_node(g, ci);
+        const bool bf = mm->src[0]->type == GGML_TYPE_BF16;
         if (mm->op != GGML_OP_MUL_MAT || mm->src[1] != m || mm->src[0] == m || !mm_is_gemv(mm) ||
-            !mmhip_rms_norm_mul_mat_supported(mm->src[0]->type, mm->src[0]->ne[1], K, M)) {
+            !(bf ? mmhip_mul_mat_bf16_dec_supported(mm->src[0]->ne[1], K, M, 0)
+                 : mmhip_rms_norm_mul_mat_supported(mm->src[0]->type, mm->src[0]->ne[1], K, M))) {
             return false;
         }
         last = std::max(last, gi.uses[(size_t) ci] == 1 ? std::max(ci, gi.cons[(size_t) ci]) : ci);
@@ -1663,6 +1678,26 @@ graph_plan build_plan(struct ggml_cgraph * g) {
             for (int t = p + 1; only_views && t < i; t++) {
                 only_views = is_noop(ggml_graph_node(g, t)->op);
             }
+            // BF16: every consumer a BF16 decode GEMV, the SwiGLU rows written in f32
+            bool bf_cons = !gi.consumers[(size_t) i].empty() && n->op_params[1] == 0;
+            for (int ci : gi.consumers[(size_t) i]) {
+                const struct ggml_tensor * cm = ggml_graph_node(g, ci);
+                bf_cons = bf_cons && cm->op == GGML_OP_MUL_MAT && cm->src[1] == n && cm->src[0] != n &&
+                          mm_is_bf16_dec(cm);
+            }
+            if (!n->src[1] && only_views && step_at[(size_t) p] >= 0 && gi.uses[(size_t) p] == 1 && bf_cons &&
+                !is_output(a) && a->op == GGML_OP_MUL_MAT && a->ne[0] == 2 * F && ggml_nrows(a) == M &&
+                a->src[0]->type == GGML_TYPE_BF16) {
+                plan_step & ms = pending[(size_t) step_at[(size_t) p]];
+                if (ms.kind == ST_MM && ms.node == p && ms.norm >= 0 && ms.add < 0 && ms.glu < 0 &&
+                    mmhip_mul_mat_bf16_dec_supported(a->ne[0], a->src[0]->ne[0], M, 1)) {
+                    ms.glu_epi           = i;
+                    ms.slot_out          = -1;
+                    ms.write_f32         = true;
+                    absorbed[(size_t) i] = 1;
+                    continue;
+                }
+            }
             if (!n->src[1] && only_views && step_at[(size_t) p] >= 0 && gi.uses[(size_t) p] == 1 &&
                 !is_output(a) && a->op == GGML_OP_MUL_MAT && a->ne[0] == 2 * F && ggml_nrows(a) == M &&
                 gemv_consumer_type(g, gi, i) == GGML_TYPE_Q8_0) {
@@ -1988,7 +2023,7 @@ graph_plan build_plan(struct ggml_cgraph * g) {
                     }
                 }
             }
-            if (st.slot_in < 0 && st.norm < 0 && st.glu < 0 && st.add >= 0) {
+            if (st.slot_in < 0 && st.norm < 0 && st.glu < 0 && st.add >= 0 && n->src[0]->type != GGML_TYPE_BF16) {
                 // quantise the activations into a slot of their own
                 st.vec_wtype = n->src[0]->type;
                 st.slot_in   = new_slot(st.vec_wtype, n->src[0]->ne[0], n->src[1]->ne[1]);
@@ -2308,6 +2343,28 @@ int run_step(mi_backend * c, struct ggml_cgraph * g, const plan_step & st, char 
             const struct ggml_tensor * w  = mm->src[0];
             const struct ggml_tensor * x  = mm->src[1];
             const int64_t              N = w->ne[1], K = w->ne[0], M = x->ne[1] * x->ne[2] * x->ne[3];
+            if (w->type == GGML_TYPE_BF16) {
+                // the BF16 decode GEMV: norm prologue, residual or SwiGLU epilogue
+                const float * xp  = (const float *) x->data;
+                int64_t       ldx = (int64_t) (x->nb[1] / 4);
+                const float * nwp = nullptr;
+                float         eps = 0.0f;
+                if (st.norm >= 0) {
+                    const struct ggml_tensor * rn = ggml_graph_node(g, st.norm);
+                    xp                            = (const float *) rn->src[0]->data;
+                    ldx                           = (int64_t) (rn->src[0]->nb[1] / 4);
+                    nwp = (const float *) ggml_graph_node(g, st.norm_mul)->src[1]->data;
+                    memcpy(&eps, &rn->op_params[0], sizeof(float));
+                }
+                const struct ggml_tensor * r   = st.add >= 0 ? ggml_graph_node(g, st.add)->src[st.add_res] : nullptr;
+                const struct ggml_tensor * gn  = st.glu_epi >= 0 ? ggml_graph_node(g, st.glu_epi) : nullptr;
+                float *                    yp  = gn ? (float *) gn->data : (float *) n->data;
+                const int64_t              ldy = gn ? N / 2 : N;
+                rc = mmhip_mul_mat_bf16_dec(w->data, N, K, (int64_t) (w->nb[1] / 2), xp, ldx, M, nwp, eps,
+                                            r ? (const float *) r->data : nullptr, r ? (int64_t) (r->nb[1] / 4) : 0,
+                                            gn ? 1 : 0, yp, ldy, s);
+                break;
+            }
             if (st.norm >= 0) {
                 const struct ggml_tensor * rn  = ggml_graph_node(g, st.norm);
                 const struct ggml_tensor * xr  = rn->src[0];

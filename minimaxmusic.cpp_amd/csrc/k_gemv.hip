@@ -1616,6 +1616,249 @@ int gemv_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const Ac
     return MMHIP_OK;
 }
 
+// ---------------------------------------------------------------------------
+// BF16 weights at decode (1-2 activation columns): the LM's projections from a
+// BF16 model file (qwen3_linear, src/qwen3-enc.h:67-69, in qw3lm_forward_batch,
+// src/qwen3-lm.h:742-856) with the block's RMS norm (src/qwen3-enc.h:87-93) in
+// the prologue, the residual ADD in the store, or the SwiGLU of the fused
+// gate|up rows (src/qwen3-enc.h:106-108) in the epilogue.  Persistent: one
+// 8-wave workgroup per CU (two register buffers of a 4096-element segment per
+// wave: 128 KB of loads in flight per CU).  The prologue computes the activation columns once
+// per workgroup -- the RMS norm as k_rms_norm_row does (double sum of the f32
+// squares, the mean rounded to f32, 1 / sqrtf(mean + eps), x * scale, then
+// * w), rounded to bf16 as ggml rounds the src1 of a BF16 MUL_MAT -- into LDS.
+// Each wave streams whole rows in segments of 4096 elements (lane l holds the
+// 16-byte chunks l + 64 i, i < 8), the next segment's loads in flight while
+// the current one is multiplied: exact products of bf16 values summed in f32
+// by pairs (v_dot2_f32_bf16; ggml-CPU's vec_dot_bf16 sums the same products
+// in another order), reduced across the wave.  EPI 0: store; 1: residual ADD (one f32 rounding, as the
+// ADD node); 2: SwiGLU pairs, gate row j and up row N / 2 + j -> silu(g) * u
+// (k_swiglu's arithmetic).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+struct BfDecArgs {
+    const uint16_t * W;
+    int64_t          N, K, ldw;  // rows, row length, row stride (elements)
+    const float *    x;
+    int64_t          ldx;
+    const float *    nw;  // norm weight (NORM)
+    float            eps;
+    const float *    r;  // residual (EPI 1)
+    int64_t          ldr;
+    float *          y;
+    int64_t          ldy;
+};
+
+template <int NC, bool NORM, int EPI>
+__global__ __launch_bounds__(512) void k_gemv_bf16_dec(BfDecArgs a) {
+#pragma clang fp contract(off)
+    extern __shared__ __attribute__((aligned(16))) uint16_t s_x[];  // [NC][K] bf16 activation columns
+    __shared__ double s_ss[8];
+    const int     tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t K   = a.K;
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        const float * xc = a.x + c * a.ldx;
+        float         sc = 1.0f;
+        if constexpr (NORM) {
+            double ss = 0.0;
+            for (int64_t k = 4 * (int64_t) tid; k < K; k += 2048) {
+                const float4_t v = *(const float4_t *) (xc + k);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    ss += (double) (v[e] * v[e]);
+                }
+            }
+            ss = wave_sum_d(ss);
+            if (lane == 0) {
+                s_ss[wave] = ss;
+            }
+            __syncthreads();
+            double t = 0.0;
+#pragma unroll
+            for (int w = 0; w < 8; w++) {
+                t += s_ss[w];
+            }
+            __syncthreads();  // s_ss is reused by the next column
+            const float mean = (float) (t / (double) K);
+            sc               = 1.0f / sqrtf(mean + a.eps);
+        }
+        for (int64_t k = 4 * (int64_t) tid; k < K; k += 2048) {
+            const float4_t v = *(const float4_t *) (xc + k);
+            float4_t       w = { 1.0f, 1.0f, 1.0f, 1.0f };
+            if constexpr (NORM) {
+                w = *(const float4_t *) (a.nw + k);
+            }
+            uint32_t h[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float o = NORM ? (v[e] * sc) * w[e] : v[e];
+                h[e]          = __float_as_uint(round_bf16(o)) >> 16;
+            }
+            *(uint2 *) (s_x + c * K + k) = uint2{ h[0] | (h[1] << 16), h[2] | (h[3] << 16) };
+        }
+    }
+    __syncthreads();
+
+    const int64_t items = EPI == 2 ? a.N / 2 : a.N;
+    constexpr int64_t seg = 4096;  // elements per segment: 8 chunks of 16 bytes per lane
+    const int     nseg  = (int) (K / seg);
+    const int     nrow  = EPI == 2 ? 2 : 1;
+    const int     spi   = nrow * nseg;  // segments per item
+    const int64_t W     = (int64_t) gridDim.x * 8;
+    int64_t       it    = (int64_t) blockIdx.x * 8 + wave;
+    if (it >= items) {
+        return;  // wave-uniform; no barrier follows
+    }
+    auto seg_ptr = [&](int64_t item, int t) {
+        const int     rr  = t / nseg;
+        const int64_t row = rr ? item + a.N / 2 : item;
+        return a.W + row * a.ldw + (int64_t) (t - rr * nseg) * seg + 8 * lane;
+    };
+    // unconditional loads (a finished wave reloads its last segment): the
+    // compiler's wait counts then leave the next segment in flight
+    auto load = [&](uint4 (&b)[8], const uint16_t * p) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            b[i] = *(const uint4 *) (p + 512 * i);
+        }
+    };
+    // per-lane sums of the current row, and (SwiGLU) of the pair's gate row;
+    // no runtime-indexed arrays, so both stay in registers
+    float acc[NC], gacc[NC];
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        acc[c]  = 0.0f;
+        gacc[c] = 0.0f;
+    }
+    // v_dot2_f32_bf16: two exact bf16 products added to an f32 sum per
+    // instruction, on the packed pairs as loaded (the dot of ggml-CPU's
+    // AVX512-BF16 path, vdpbf16ps, sums the same pairs the same way)
+    auto compute = [&](const uint4 (&b)[8], int t) {
+        const int64_t k0 = (int64_t) (t % nseg) * seg + 8 * lane;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t ww[4] = { b[i].x, b[i].y, b[i].z, b[i].w };
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                const uint4    xv    = *(const uint4 *) (s_x + c * K + k0 + 512 * i);
+                const uint32_t xx[4] = { xv.x, xv.y, xv.z, xv.w };
+                float          s     = acc[c];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, ww[e]),
+                                                        __builtin_bit_cast(bf16x2_t, xx[e]), s, false);
+                }
+                acc[c] = s;
+            }
+        }
+    };
+    // after segment t of an item: at the end of the gate row keep its sums,
+    // at the end of the item reduce and store
+    auto row_end = [&](int64_t item, int t) {
+        if (t % nseg != nseg - 1) {
+            return;
+        }
+        if (EPI == 2 && t < nseg) {
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                gacc[c] = acc[c];
+                acc[c]  = 0.0f;
+            }
+            return;
+        }
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const float v = wave_sum(acc[c]);
+            const float g = EPI == 2 ? wave_sum(gacc[c]) : 0.0f;
+            if (lane == 0) {
+                float o;
+                if constexpr (EPI == 2) {
+                    const float silu = g / (1.0f + expf(-g));
+                    o                = silu * v;
+                } else if constexpr (EPI == 1) {
+                    o = a.r[c * a.ldr + item] + v;
+                } else {
+                    o = v;
+                }
+                a.y[c * a.ldy + item] = o;
+            }
+            acc[c] = 0.0f;
+        }
+    };
+    // the wave's stream: items it, it + W, ...; within an item its rows, each
+    // in nseg segments; two register buffers alternate
+    uint4 b0[8], b1[8];
+    int   t = 0;
+    load(b0, seg_ptr(it, 0));
+    // the segment after (it, t), or (it, t) itself at the end of the stream
+    auto next = [&](int64_t & i2, int & t2) {
+        i2 = it;
+        t2 = t + 1;
+        if (t2 == spi) {
+            t2 = 0;
+            i2 += W;
+        }
+        const bool more = i2 < items;
+        if (!more) {
+            i2 = it;
+            t2 = t;
+        }
+        return more;
+    };
+    for (;;) {
+        int64_t    it1;
+        int        t1;
+        const bool more = next(it1, t1);
+        load(b1, seg_ptr(it1, t1));
+        compute(b0, t);
+        row_end(it, t);
+        if (!more) {
+            break;
+        }
+        it              = it1;
+        t               = t1;
+        const bool more2 = next(it1, t1);
+        load(b0, seg_ptr(it1, t1));
+        compute(b1, t);
+        row_end(it, t);
+        if (!more2) {
+            break;
+        }
+        it = it1;
+        t  = t1;
+    }
+}
+
+bool bf16_dec_supported(int64_t N, int64_t K, int64_t M, bool glu) {
+    return N > 0 && K > 0 && M >= 1 && M <= 2 && K % 4096 == 0 && (size_t) M * K * 2 <= 64 * 1024 &&
+           (!glu || N % 2 == 0);
+}
+
+static int64_t pg_cus();
+
+template <int NC, bool NORM, int EPI>
+static int launch_bf16_dec(const BfDecArgs & a, hipStream_t stream) {
+    const size_t lds = (size_t) NC * a.K * 2;
+    if (lds > 64 * 1024 || !ensure_lds_limit((const void *) k_gemv_bf16_dec<NC, NORM, EPI>, lds)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "bf16 decode GEMV: %zu bytes of LDS", lds);
+    }
+    const int64_t items = EPI == 2 ? a.N / 2 : a.N;
+    const int64_t wgs   = std::max<int64_t>(1, std::min<int64_t>((items + 7) / 8, pg_cus()));
+    hipLaunchKernelGGL((k_gemv_bf16_dec<NC, NORM, EPI>), dim3((unsigned) wgs), dim3(512), lds, stream, a);
+    return check_launch("bf16 decode GEMV");
+}
+
+template <int NC>
+static int bf16_dec_dispatch(const BfDecArgs & a, bool norm, int epi, hipStream_t stream) {
+    if (norm) {
+        return epi == 2 ? launch_bf16_dec<NC, true, 2>(a, stream)
+                        : epi == 1 ? launch_bf16_dec<NC, true, 1>(a, stream) : launch_bf16_dec<NC, true, 0>(a, stream);
+    }
+    return epi == 2 ? launch_bf16_dec<NC, false, 2>(a, stream)
+                    : epi == 1 ? launch_bf16_dec<NC, false, 1>(a, stream) : launch_bf16_dec<NC, false, 0>(a, stream);
+}
+
 }  // namespace mmhip
 
 using namespace mmhip;
@@ -1639,6 +1882,31 @@ extern "C" int mmhip_mul_mat_bf16(const void * W, int64_t N, int64_t K, int64_t 
     hipLaunchKernelGGL(k_gemv_bf16, dim3((unsigned) nwg), dim3(256), 0, (hipStream_t) stream, (const uint16_t *) W, N,
                        K, ldw, x, ldx, (int) M, y, ldy);
     return check_launch("mul_mat_bf16");
+}
+
+extern "C" int mmhip_mul_mat_bf16_dec_supported(int64_t N, int64_t K, int64_t M, int glu) {
+    return bf16_dec_supported(N, K, M, glu != 0) ? 1 : 0;
+}
+
+extern "C" int mmhip_mul_mat_bf16_dec(const void * W, int64_t N, int64_t K, int64_t ldw, const float * x, int64_t ldx,
+                                      int64_t M, const float * norm_w, float eps, const float * r, int64_t ldr, int glu,
+                                      float * y, int64_t ldy, void * stream) {
+    MMHIP_API_BEGIN();
+    const int64_t nout = glu ? N / 2 : N;
+    if (!W || !x || !y || ldw < K || ldx < K || ldy < nout || (r && ldr < nout) || (r && glu)) {
+        return set_error(MMHIP_ERR_INVALID, "mul_mat_bf16_dec: bad arguments N=%lld K=%lld M=%lld", (long long) N,
+                         (long long) K, (long long) M);
+    }
+    if (!bf16_dec_supported(N, K, M, glu != 0) || ldw % 8 != 0 || ldx % 4 != 0 || ((uintptr_t) W) % 16 != 0 ||
+        ((uintptr_t) x) % 16 != 0 || (norm_w && ((uintptr_t) norm_w) % 16 != 0)) {
+        return set_error(MMHIP_ERR_UNSUPPORTED,
+                         "mul_mat_bf16_dec: N=%lld K=%lld M=%lld (M <= 2, K %% 4096 == 0, M K bf16 in 64 KB, aligned rows)",
+                         (long long) N, (long long) K, (long long) M);
+    }
+    BfDecArgs a{ (const uint16_t *) W, N, K, ldw, x, ldx, norm_w, eps, r, ldr, y, ldy };
+    const int epi = glu ? 2 : r ? 1 : 0;
+    return M == 1 ? bf16_dec_dispatch<1>(a, norm_w != nullptr, epi, (hipStream_t) stream)
+                  : bf16_dec_dispatch<2>(a, norm_w != nullptr, epi, (hipStream_t) stream);
 }
 
 extern "C" int mmhip_mul_mat_q(int type, const void * W, int64_t N, int64_t K, int64_t w_row_stride, const void * xq,

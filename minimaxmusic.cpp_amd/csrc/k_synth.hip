@@ -73,6 +73,8 @@ __global__ void k_synth_normal(int type, void * __restrict__ dst, int64_t n, uin
         const float v = mean + stdv * normal01(seed, (uint64_t) i);
         if (type == TYPE_F32) {
             ((float *) dst)[i] = v;
+        } else if (type == TYPE_BF16) {
+            ((uint16_t *) dst)[i] = (uint16_t) (__float_as_uint(round_bf16(v)) >> 16);
         } else {
             ((uint16_t *) dst)[i] = f2h(v);
         }
@@ -100,7 +102,7 @@ extern "C" int mmhip_synth_gguf(int type, void * dst, int64_t nblocks, uint64_t 
 extern "C" int mmhip_synth_normal(int type, void * dst, int64_t n, uint64_t seed, float mean, float stdv,
                                   void * stream) {
     MMHIP_API_BEGIN();
-    if (!dst || n < 0 || !(type == TYPE_F32 || type == TYPE_F16)) {
+    if (!dst || n < 0 || !(type == TYPE_F32 || type == TYPE_F16 || type == TYPE_BF16)) {
         return set_error(MMHIP_ERR_INVALID, "synth_normal: bad arguments");
     }
     if (n == 0) {

@@ -101,8 +101,11 @@ bool fill_quant(ggml_tensor * t, uint64_t seed) {
 }
 
 bool fill_normal(ggml_tensor * t, uint64_t seed, float mean, float stdv) {
-    return mmhip_synth_normal(t->type == GGML_TYPE_F16 ? 1 : 0, t->data, ggml_nelements(t), seed, mean, stdv,
-                              nullptr) == MMHIP_OK &&
+    const int ty = t->type == GGML_TYPE_F16 ? 1 : t->type == GGML_TYPE_BF16 ? 30 : 0;
+    if (!(t->type == GGML_TYPE_F16 || t->type == GGML_TYPE_BF16 || t->type == GGML_TYPE_F32)) {
+        return false;
+    }
+    return mmhip_synth_normal(ty, t->data, ggml_nelements(t), seed, mean, stdv, nullptr) == MMHIP_OK &&
            hipDeviceSynchronize() == hipSuccess;
 }
 

@@ -61,6 +61,9 @@ SIGNATURES = {
     "mmhip_mul_mat_workspace": (_sz, [_i32, _i64, _i64, _i64]),
     "mmhip_mul_mat": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _sz, _vp]),
     "mmhip_mul_mat_bf16": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp]),
+    "mmhip_mul_mat_bf16_dec_supported": (_i32, [_i64, _i64, _i64, _i32]),
+    "mmhip_mul_mat_bf16_dec": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _f32, _vp, _i64, _i32, _vp, _i64,
+                                      _vp]),
     "mmhip_mul_mat_bias_add": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _vp,
                                       _sz, _vp]),
     "mmhip_mul_mat_bias_add_h": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _vp]),

@@ -105,15 +105,38 @@ def prefill(st, tokens, kv_set, kv_pos, flavour="ggml"):
     return mm("lm_head", c.vocab, H, hid[-1:])[0], hid
 
 
-def _decode_setup(st, sets, kv_pos, flavour):
-    c = st.c
-    N = len(sets)
-    t = c.wtype
+def round_bf16(x):
+    """f32 -> bf16 -> f32 as ggml rounds (nearest-even on the upper 16 bits;
+    finite inputs)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
+    return r.view(np.float32).reshape(np.shape(x))
+
+
+def _mm_fn(st, flavour):
+    """The MUL_MAT of a weight by name.  Quantised weights: ggml-CPU's
+    activation quantisation and integer dots ("ggml") or exact f64 ("f64").
+    BF16 weights (type 30): ggml's BF16 dot multiplies bf16 weights by the
+    activations rounded to bf16, each product exact, and sums them ("ggml":
+    in f64 here, as the generic C path does), or the unrounded activations
+    ("f64")."""
+    t = st.c.wtype
 
     def mm(name, n_out, k_in, x):
+        if t == 30:
+            xr = round_bf16(x) if flavour == "ggml" else np.asarray(x, np.float32)
+            return oracle.mul_mat_f64(t, st.w[name], n_out, k_in, xr).astype(np.float32)
         if flavour == "ggml":
             return oracle.mul_mat_ggml(t, st.w[name], n_out, k_in, x)
         return oracle.mul_mat_f64(t, st.w[name], n_out, k_in, x).astype(np.float32)
+
+    return mm
+
+
+def _decode_setup(st, sets, kv_pos, flavour):
+    c = st.c
+    N = len(sets)
+    mm = _mm_fn(st, flavour)
 
     max_len = max(kv_pos[s] + 1 for s in sets)
     n_kv_pad = min((max_len + 255) // 256 * 256, c.max_seq)

@@ -103,13 +103,14 @@ def _check_kv_rows(lm, st, cfg, written):
                 assert np.array_equal(dev[s, :, p1:].view(np.uint16), ref[s, :, p1:].view(np.uint16)), (name, s)
 
 
-@pytest.mark.parametrize("wtype", [8, 14])
+@pytest.mark.parametrize("wtype", [8, 14, 30])
 def test_lm_decode_headline_width_matches_reference(lmmod, wtype):
     """Oracle parity at the Qwen3-8B width of the decode benchmark: hidden
     4096, 32 / 8 heads of 128, FFN 12288, vocab 151936, f16 KV caches of 4096
     positions on both CFG sets (Q8_0, and the Q6_K variant), 2 layers of the
     36 (every layer runs the same kernels), for the eager step and the
-    captured one.
+    captured one; and with BF16 weights (type 30, the native-BF16 files: the
+    persistent BF16 decode GEMV with the norm, residual and SwiGLU fused).
 
     Stated tolerance, teacher-forced (each layer restated from the device's
     own input rows of that layer and the device's caches, the logits from its
@@ -183,9 +184,9 @@ def test_lm_decode_window_crosses_256(lmmod):
     lm.close()
 
 
-@pytest.mark.parametrize("wtype", [8, 14])
+@pytest.mark.parametrize("wtype", [8, 14, 30])
 def test_lm_decode_benchmark_shape(lmmod, wtype):
-    """The Qwen3-8B-shape decode step (36 layers, Q8_0 and the Q6_K variant,
+    """The Qwen3-8B-shape decode step (36 layers, Q8_0, the Q6_K variant and BF16,
     vocab 151936) at KV 4096 on both CFG sets: finite, deterministic, graph
     replayed."""
     cfg = dict(lmmod.QWEN3_8B, wtype=wtype)

@@ -408,3 +408,64 @@ def test_mul_mat_f32_weights_at_token_counts(mm, N, K, T, B, pad):
     y = out.cpu().double()
     assert torch.isfinite(y).all()
     assert float((y - ref).abs().max() / ref.abs().max()) < 1e-5
+
+
+def _bf16_rows(rng, N, K):
+    """bf16 weight rows (uint16) ~ N(0, 0.02) and their exact f32 values."""
+    import lm_reference
+
+    w = lm_reference.round_bf16((0.02 * rng.standard_normal((N, K))).astype(np.float32))
+    return (w.view(np.uint32) >> 16).astype(np.uint16), w
+
+
+@pytest.mark.parametrize("N,K,M,mode", [(6144, 4096, 2, "norm"), (24576, 4096, 2, "norm_glu"), (4096, 12288, 2, "add"),
+                                        (4096, 4096, 1, "add"), (1000, 4096, 2, "plain"), (1030, 8192, 1, "norm"),
+                                        (24576, 4096, 1, "norm_glu"), (6, 4096, 2, "norm_glu")])
+def test_bf16_decode_gemv(mm, N, K, M, mode):
+    """The persistent BF16 decode GEMV (mmhip_mul_mat_bf16_dec) at the LM's
+    projection shapes: RMS-norm prologue (QKV, gate_up), SwiGLU pairs (gate_up),
+    residual ADD (O, down).  Against float64 of the same bf16 operands (weights
+    exact, activations rounded to bf16 after the norm, as ggml's BF16 MUL_MAT
+    rounds its src1): max|y - y64| <= 1e-5 max|y64| (f32 sums); the
+    residual / SwiGLU epilogues restated from the f64 dot products."""
+    import lm_reference
+
+    L = mm.load()
+    assert L.mmhip_mul_mat_bf16_dec_supported(N, 2048, M, 0) == 0  # K % 4096 != 0: the plain BF16 GEMV's shapes
+    assert L.mmhip_mul_mat_bf16_dec_supported(N, K, 3, 0) == 0
+    rng = np.random.default_rng(N + K + M)
+    Wb, Wf = _bf16_rows(rng, N, K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    nw = (1.0 + 0.05 * rng.standard_normal(K)).astype(np.float32)
+    r = rng.standard_normal((M, N)).astype(np.float32)
+    eps = 1e-6
+    norm = mode.startswith("norm")
+    glu = mode.endswith("glu")
+    if norm:
+        x64 = x.astype(np.float64)
+        sc = (1.0 / np.sqrt(np.float32((x64 * x64).mean(axis=1)) + np.float32(eps))).astype(np.float32)
+        xa = (x * sc[:, None]).astype(np.float32) * nw
+    else:
+        xa = x
+    xa = lm_reference.round_bf16(xa).astype(np.float64)
+    d = xa @ Wf.astype(np.float64).T                          # [M, N]
+    if glu:
+        g, u = d[:, :N // 2], d[:, N // 2:]
+        ref = g / (1.0 + np.exp(-g)) * u
+    elif mode == "add":
+        ref = r.astype(np.float64) + d
+    else:
+        ref = d
+    tW, tx, tn, tr = (torch.from_numpy(a).cuda() for a in (Wb.view(np.int16), x, nw, r))
+    nout = N // 2 if glu else N
+    y = torch.full((M, nout), float("nan"), device="cuda")
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    assert L.mmhip_mul_mat_bf16_dec_supported(N, K, M, int(glu)) == 1
+    rc = L.mmhip_mul_mat_bf16_dec(P(tW), N, K, K, P(tx), K, M, P(tn) if norm else None, eps,
+                                  P(tr) if mode == "add" else None, N, int(glu), P(y), nout,
+                                  ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0, L.mmhip_last_error()
+    out = y.cpu().numpy().astype(np.float64)
+    assert np.isfinite(out).all()
+    scale = np.abs(d).max() if mode == "add" else np.abs(ref).max()
+    assert np.abs(out - ref).max() <= 1e-5 * max(scale, np.abs(ref).max() * 1e-2), np.abs(out - ref).max() / scale

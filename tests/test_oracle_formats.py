@@ -163,3 +163,19 @@ def test_quantize_q8_K_closed_forms(orc):
     assert np.array_equal(qs, q.astype(np.int8)) and np.all(d == 0.125)
     d, qs, bs = _q8_K_fields(orc.quantize_q8_K(np.zeros(256, np.float32)))
     assert d[0] == 0 and not qs.any() and not bs.any()
+
+
+def test_lm_reference_round_bf16_matches_the_oracle(orc):
+    """tests/lm_reference.round_bf16 (numpy, used by the BF16 restatement)
+    equals the oracle's f32 -> bf16 conversion, ties and near-ties included."""
+    import lm_reference
+
+    rng = np.random.default_rng(5)
+    u = rng.integers(0, 1 << 31, 4000, dtype=np.uint64).astype(np.uint32)
+    u[:1000] = (u[:1000] & 0xFFFF0000) | 0x8000          # exact ties
+    u[1000:1500] = (u[1000:1500] & 0xFFFF0000) | 0x7FFF  # just below a tie
+    u = u[(u & 0x7F800000) != 0x7F800000]                # finite values
+    x = u.view(np.float32)
+    got = lm_reference.round_bf16(x).view(np.uint32) >> 16
+    exp = np.array([orc.lib().orc_fp32_to_bf16(float(v)) for v in x], dtype=np.uint32)
+    assert np.array_equal(got, exp)
