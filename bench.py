@@ -52,7 +52,8 @@ def parse():
     ap.add_argument("--workload", default="lm_decode",
                     choices=["lm_decode", "gemv_q8_0", "fa_decode", "fa_prefill", "fa_dit", "gemm_q4_k",
                              "dit_block", "depth"])
-    ap.add_argument("--wtype", default="q8_0", choices=["q8_0", "q6_k", "bf16"], help="lm_decode weight type")
+    ap.add_argument("--wtype", default="q8_0", choices=["q8_0", "q6_k", "q5_k_m", "bf16"],
+                    help="lm_decode weight type (q5_k_m: Q5_K with the bumped layers' V / down in Q6_K)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     return ap.parse_args()
@@ -512,8 +513,8 @@ def bench_fa_mfma(args, torch, pkg, causal):
         "config": {"workload": name, "mask": "causal f16" if causal else "none"},
         "via_backend": backend,
         "roofline": {"bound": "mfma",
-                     "kernel": ("k_fa_mfma<128,8> + k_fa_row_end mask prepass (one attention call)" if causal
-                                else "k_fa_dma"),
+                     "kernel": ("k_fa_dma<true> + k_fa_row_end mask prepass (one attention call)" if causal
+                                else "k_fa_dma<false>"),
                      "achieved": round(tf, 2),
                      "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
                      "avg_launch_us": round(avg_s * 1e6, 2), "min_launch_us": round(med_s * 1e6, 2),
@@ -823,12 +824,30 @@ def bench_depth(args, torch, pkg):
 
 # Algorithmic HBM bytes of one Qwen3-8B-shape CFG decode step at KV 4096:
 # weights + KV read + norm weights + logits + KV write (per step, both rows).
+def lm_bumped_layers(cfg):
+    """Layers whose V / down projections take bump_type (the "_M" rule of
+    tools/quantize.cpp:127-150)."""
+    L = cfg["n_layers"]
+    if not cfg.get("bump_type"):
+        return []
+    return [l for l in range(L) if l < L // 9 or l >= L - L // 7 or l % 3 == 0]
+
+
 def lm_step_bytes(cfg, wtype):
-    be, bb = {8: (32, 34), 14: (256, 210), 12: (256, 144), 30: (1, 2)}[wtype]
+    size = {8: (32, 34), 14: (256, 210), 13: (256, 176), 12: (256, 144), 30: (1, 2)}
+
+    def nbytes(n, t):
+        be, bb = size[t]
+        return n * bb // be
+
     H, D, Nh, Nkv, F, V, L = (cfg["hidden"], cfg["head_dim"], cfg["n_heads"], cfg["n_kv_heads"], cfg["ffn"],
                               cfg["vocab"], cfg["n_layers"])
-    per_layer_w = H * (Nh * D + 2 * Nkv * D) + Nh * D * H + H * 2 * F + F * H
-    weights = (per_layer_w * L + H * V) * bb // be
+    bumped = set(lm_bumped_layers(cfg))
+    weights = nbytes(H * V, wtype)
+    for l in range(L):
+        bt = cfg["bump_type"] if l in bumped else wtype
+        weights += (nbytes(H * (Nh * D + Nkv * D) + Nh * D * H + H * 2 * F, wtype) +
+                    nbytes(H * Nkv * D + F * H, bt))
     kv_len, sets = 4096, 2
     kv_read = L * 2 * sets * Nkv * kv_len * D * 2
     norms = (L * (2 * H + 2 * D) + H) * 4
@@ -842,7 +861,8 @@ def bench_lm(args, torch, pkg):
 
     lm_mod = importlib.import_module(pkg.__name__ + ".lm")
     cfg = dict(lm_mod.QWEN3_8B)
-    cfg["wtype"] = {"q8_0": 8, "q6_k": 14, "bf16": 30}[args.wtype]
+    cfg["wtype"] = {"q8_0": 8, "q6_k": 14, "q5_k_m": 13, "bf16": 30}[args.wtype]
+    cfg["bump_type"] = 14 if args.wtype == "q5_k_m" else 0
     lm = lm_mod.Lm(seed=1005, **cfg)
     lm.fill_kv(0, 4095, seed=1)
     lm.fill_kv(1, 4095, seed=2)
@@ -869,7 +889,12 @@ def bench_lm(args, torch, pkg):
     replays, eager = lm.graph_stats()
     nodes = lm.graph_nodes()
     lm.close()
-    dom = lm_dominant_kernel(torch, pkg, cfg) if cfg["wtype"] != 30 else lm_dominant_kernel_bf16(torch, pkg, cfg)
+    if cfg["wtype"] == 30:
+        dom = lm_dominant_kernel_bf16(torch, pkg, cfg)
+    elif cfg["wtype"] == 13:
+        dom = lm_dominant_kernel_gemv(torch, pkg, cfg)
+    else:
+        dom = lm_dominant_kernel(torch, pkg, cfg)
     cpu = None
     if not args.no_cpu and cfg["wtype"] != 30:
         cpu = cpu_lm(args, lm_mod, cfg)
@@ -938,6 +963,41 @@ def lm_dominant_kernel(torch, pkg, cfg):
             "alg_bytes_per_launch": alg_bytes}
 
 
+def lm_dominant_kernel_gemv(torch, pkg, cfg):
+    """The step's largest kernel alone where no fused form exists (Q5_K): the
+    gate_up GEMV (W [2 ffn x hidden], 2 columns) on activations already
+    quantised to Q8_K, six weight copies (415 MB) rotating past the 256 MB
+    Infinity Cache, replayed as a HIP graph."""
+    mm, synth = pkg.mmhip, pkg.synth
+    N, K, M = 2 * cfg["ffn"], cfg["hidden"], 2
+    wt = cfg["wtype"]
+    copies = 6
+    L = mm.load()
+    Ws = [mm.QuantWeight.from_gguf(wt, synth.gguf_blocks_torch(wt, N, K, 2201 + c), N, K) for c in range(copies)]
+    x = torch.from_numpy(synth.normal_np((M, K), 2211)).cuda()
+    xq = mm.quantize_act(wt, x)
+    y = torch.empty((M, N), device="cuda")
+
+    def launch(i, st):
+        W = Ws[i % copies]
+        rc = L.mmhip_mul_mat_q(wt, ctypes.c_void_p(W.data.data_ptr()), N, K, W.row_bytes,
+                               ctypes.c_void_p(xq.data_ptr()), M, ctypes.c_void_p(y.data_ptr()), N, st)
+        assert rc == 0, L.mmhip_last_error()
+
+    avg_s, min_s = graph_time(torch, launch, 36)
+    # weights + the Q8_K activations (int8 + f32 scales + int16 block sums) + y
+    alg_bytes = Ws[0].data.numel() + M * K + M * (K // 256) * 4 + M * (K // 16) * 2 + M * N * 4
+    achieved = alg_bytes / avg_s / 1e9
+    del Ws
+    torch.cuda.empty_cache()
+    return {"bound": "hbm", "kernel": "k_gemv_q4_K<2,2,2,Q5>: gate_up GEMV %d x %d Q5_K on Q8_K activations, "
+                                      "2 columns (the Q5_K_M step's largest kernel)" % (N, K),
+            "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "avg_launch_us": round(avg_s * 1e6, 3), "min_launch_us": round(min_s * 1e6, 3),
+            "alg_bytes_per_launch": alg_bytes}
+
+
 def lm_dominant_kernel_bf16(torch, pkg, cfg):
     """The BF16 step's largest kernel alone: the gate_up decode GEMV with the
     RMS norm in its prologue and the SwiGLU in its epilogue (W [2 ffn x
@@ -990,26 +1050,44 @@ def cpu_lm(args, lm_mod, cfg):
     synth = importlib.import_module(lm_mod.__name__.rsplit(".", 1)[0] + ".synth")
     W = {n: synth.gguf_blocks_np(t, r, k, 50 + i) for i, (n, r, k) in enumerate(
         [("qkv", Nh * D + 2 * Nkv * D, H), ("o", H, Nh * D), ("gu", 2 * F, H), ("down", H, F)])}
+    bt = cfg.get("bump_type") or t
+    n_bumped = len(lm_bumped_layers(cfg))
+    if n_bumped:
+        W.update({n: synth.gguf_blocks_np(tt, r, k, 60 + i) for i, (n, tt, r, k) in enumerate(
+            [("qk", t, Nh * D + Nkv * D, H), ("v", bt, Nkv * D, H), ("down_b", bt, H, F)])})
     kc = rng.standard_normal((2, Nkv, 4096, D)).astype(np.float16)
     vc = rng.standard_normal((2, Nkv, 4096, D)).astype(np.float16)
     x = rng.standard_normal((2, H)).astype(np.float32)
     wn = np.ones(H, np.float32)
 
-    def layer(nt):
+    def layer(nt, bumped=False):
         h = oracle.rms_norm_mul(x, wn, 1e-6)
-        qkv = oracle.mul_mat_ggml(t, W["qkv"], Nh * D + 2 * Nkv * D, H, h, nthreads=nt)
+        if bumped:
+            qkv = np.concatenate([oracle.mul_mat_ggml(t, W["qk"], Nh * D + Nkv * D, H, h, nthreads=nt),
+                                  oracle.mul_mat_ggml(bt, W["v"], Nkv * D, H, h, nthreads=nt)], axis=1)
+        else:
+            qkv = oracle.mul_mat_ggml(t, W["qkv"], Nh * D + 2 * Nkv * D, H, h, nthreads=nt)
         q = oracle.rope_neox(qkv[:, :Nh * D].reshape(2, Nh, D), np.array([4095, 4095], np.int32), D, 1e6)
         o = oracle.flash_attn_ext(np.ascontiguousarray(q[:, :, None]), kc, vc, None, 1 / np.sqrt(D), "ggml",
                                   nthreads=nt).reshape(2, Nh * D)
         h2 = x + oracle.mul_mat_ggml(t, W["o"], H, Nh * D, np.asarray(o, np.float32), nthreads=nt)
         gu = oracle.mul_mat_ggml(t, W["gu"], 2 * F, H, oracle.rms_norm_mul(h2, wn, 1e-6), nthreads=nt)
+        if bumped:
+            return h2 + oracle.mul_mat_ggml(bt, W["down_b"], H, F, oracle.swiglu(gu), nthreads=nt)
         return h2 + oracle.mul_mat_ggml(t, W["down"], H, F, oracle.swiglu(gu), nthreads=nt)
 
     rows = 8192  # lm_head sample: 8192 of the 151936 vocab rows
     Wl = synth.gguf_blocks_np(t, rows, H, 99)
 
     def step_s(nt, seconds):
-        t_layer, it = cpu_rate(lambda: layer(nt), seconds)
+        if n_bumped:
+            # one layer of each kind, weighted by how many of the 36 there are
+            t_plain, it = cpu_rate(lambda: layer(nt), seconds / 2)
+            t_bump, it_b = cpu_rate(lambda: layer(nt, True), seconds / 2)
+            t_layer = ((36 - n_bumped) * t_plain + n_bumped * t_bump) / 36
+            it += it_b
+        else:
+            t_layer, it = cpu_rate(lambda: layer(nt), seconds)
         t_head, _ = cpu_rate(lambda: oracle.mul_mat_ggml(t, Wl, rows, H, x, nthreads=nt), 0.0)
         return 36 * t_layer + t_head * V / rows, t_layer, it
 

@@ -31,9 +31,15 @@ typedef struct {
     int   vocab;        /* 151936 (config) / 200000 (real model) */
     int   max_seq;      /* KV cache capacity */
     int   n_sets;       /* KV sets (2 = CFG cond + uncond) */
-    int   wtype;        /* GGML type of the linear weights and lm_head: 8 Q8_0, 14 Q6_K, 12 Q4_K */
+    int   wtype;        /* GGML type of the linear weights and lm_head: 8 Q8_0, 14 Q6_K, 13 Q5_K,
+                           12 Q4_K, 30 BF16 */
     float rms_eps;      /* 1e-6 */
     float rope_theta;   /* 1e6 */
+    int   bump_type;    /* 0, or the "_M" files' type of v_proj and down_proj in the first
+                           n_layers/9, the last n_layers/7 and every third layer
+                           (tools/quantize.cpp:47-48, :127-150; Q5_K_M: wtype 13,
+                           bump_type 14); q_proj | k_proj are then one weight "blk.<l>.qk"
+                           and v_proj is "blk.<l>.v" (src/qwen3-lm.h:749-753) */
 } mm_lm_config;
 
 /* Create on MI355X device `device`; NULL on failure (see mm_lm_error). */
@@ -68,6 +74,10 @@ int mm_lm_decode_device(void * lm, const float * embeds, const int * kv_sets, in
  * layer's output rows "layer_out-<l>" f32 [N][hidden], "hidden_out",
  * "logits". */
 int64_t mm_lm_tensor_nbytes(void * lm, const char * name);
+/* GGML type of the tensor of that name, -1 if there is none ("blk.<l>.qkv"
+ * exists in the layers of one weight type, "blk.<l>.qk" / "blk.<l>.v" in the
+ * others). */
+int     mm_lm_tensor_type(void * lm, const char * name);
 int     mm_lm_get_tensor(void * lm, const char * name, void * dst, size_t size);
 /* Overwrite a tensor from host bytes (GGUF bytes for quantized weights). */
 int     mm_lm_set_tensor(void * lm, const char * name, const void * src, size_t size);

@@ -33,6 +33,7 @@ extern "C" {
 #define MMHIP_TYPE_BF16 30
 #define MMHIP_TYPE_Q8_0 8
 #define MMHIP_TYPE_Q4_K 12
+#define MMHIP_TYPE_Q5_K 13
 #define MMHIP_TYPE_Q6_K 14
 #define MMHIP_TYPE_Q8_K 15
 
@@ -67,7 +68,7 @@ int mmhip_dequantize_rows(int type, const void * w, int64_t nrows, int64_t ne0, 
 
 /* ---------------------------------------------------------------------
  * Quantized matrix products: GGML_OP_MUL_MAT with src0 in {Q8_0, Q4_K,
- * Q6_K} (row-grouped layout), src1 f32, as emitted by qwen3_linear
+ * Q5_K, Q6_K} (row-grouped layout), src1 f32, as emitted by qwen3_linear
  * (src/qwen3-enc.h:67-69), the DiT projections (src/dit.h:197-199, :228,
  * :237, :243) and the depth decoder (src/depth-decoder.h:206-230).
  *   y[m*ldy + n] = sum_k deq(W)[n,k] * x[m*ldx + k],  n < N, m < M

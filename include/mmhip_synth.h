@@ -8,6 +8,8 @@
  * (seed, i)):
  *   Q8_0: quants uniform in [-127, 127]; d = f16(|N(0, 0.02)| / 127)
  *   Q4_K: quant and 6-bit scale/min bytes uniform; d, dmin = f16(|N(0, 0.02)|)
+ *   Q5_K: quant, fifth-bit and scale/min bytes uniform; d = f16(|N(0, 0.02)| / 512),
+ *         dmin = f16(|N(0, 0.02)| / 32) (blocks centred on zero, |w| ~ 0.01)
  *   Q6_K: ql/qh bytes uniform; int8 scales uniform in [-64, 63];
  *         d = f16(|N(0, 0.02)| / 1024)  (|w| ~ 0.01 like real weights)
  */
@@ -21,7 +23,7 @@
 extern "C" {
 #endif
 
-/* nblocks GGUF blocks of `type` (Q8_0 / Q4_K / Q6_K) written to dst_gguf. */
+/* nblocks GGUF blocks of `type` (Q8_0 / Q4_K / Q5_K / Q6_K) written to dst_gguf. */
 int mmhip_synth_gguf(int type, void * dst_gguf, int64_t nblocks, uint64_t seed, void * stream);
 
 /* n values of N(mean, std) as f32 (type 0), f16 (type 1) or bf16 (type 30,

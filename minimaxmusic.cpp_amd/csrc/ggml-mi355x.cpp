@@ -92,7 +92,7 @@ mi_registry * g_reg = nullptr;
 std::mutex    g_reg_mu;
 
 bool is_repacked(enum ggml_type t) {
-    return t == GGML_TYPE_Q8_0 || t == GGML_TYPE_Q4_K || t == GGML_TYPE_Q6_K;
+    return t == GGML_TYPE_Q8_0 || t == GGML_TYPE_Q4_K || t == GGML_TYPE_Q5_K || t == GGML_TYPE_Q6_K;
 }
 
 mmhip_view view_of(const struct ggml_tensor * t) {

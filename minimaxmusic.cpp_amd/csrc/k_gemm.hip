@@ -41,8 +41,8 @@ __device__ __forceinline__ float16_t gm_mfma_bf16(half8_t a, half8_t b, float16_
 
 // Raw bytes a thread needs for its half row (32 weights) of one K step.
 struct WRaw {
-    int4_t   q0, q1;     // quant bytes
-    uint32_t s0, s1, s2;  // Q4_K scales / Q6_K scales (s0, s1) / unused
+    int4_t   q0, q1;     // quant bytes (Q5_K: q1 = the fifth-bit bytes)
+    uint32_t s0, s1, s2;  // Q4_K / Q5_K scales; Q6_K high bits (with dm)
     uint32_t dm;          // f16 scale(s)
 };
 
@@ -56,15 +56,20 @@ __device__ __forceinline__ void w_load(WRaw & w, const uint8_t * row, int64_t K,
         w.q0         = *(const int4_t *) (row + kb);
         w.q1         = *(const int4_t *) (row + kb + 16);
         w.dm         = *(const uint16_t *) (row + K + 2 * (kb >> 5));
-    } else if constexpr (WT == TYPE_Q4_K) {
-        // 16 bytes of the 32-byte chunk holding sub-blocks 2c, 2c+1
-        const int sb = k0 >> 8, c = (k0 & 255) >> 6;
+    } else if constexpr (WT == TYPE_Q4_K || WT == TYPE_Q5_K) {
+        // 16 bytes of the 32-byte chunk holding sub-blocks 2c, 2c+1; Q5_K:
+        // the qh bytes of the same 16 columns (bits 2c, 2c+1)
+        const int64_t qh_sz = WT == TYPE_Q5_K ? K / 8 : 0;
+        const int     sb = k0 >> 8, c = (k0 & 255) >> 6;
         w.q0         = *(const int4_t *) (row + sb * 128 + c * 32 + half * 16);
-        const uint32_t * sc = (const uint32_t *) (row + K / 2 + 12 * sb);
+        if constexpr (WT == TYPE_Q5_K) {
+            w.q1 = *(const int4_t *) (row + K / 2 + sb * 32 + half * 16);
+        }
+        const uint32_t * sc = (const uint32_t *) (row + K / 2 + qh_sz + 12 * sb);
         w.s0         = sc[0];
         w.s1         = sc[1];
         w.s2         = sc[2];
-        w.dm         = *(const uint32_t *) (row + K / 2 + 12 * (K / 256) + 4 * sb);
+        w.dm         = *(const uint32_t *) (row + K / 2 + qh_sz + 12 * (K / 256) + 4 * sb);
     } else {
         // Q6_K: K step = quarter pair (t, t+1) of half hf; 16 columns l0..l0+15
         const int sb = k0 >> 8, hf = (k0 & 255) >> 7, tq = (k0 & 127) >> 5;  // tq in {0, 2}
@@ -119,7 +124,7 @@ __device__ __forceinline__ void w_dequant(const WRaw & w, const uint8_t * row, i
         for (int j = 0; j < 4; j++) {
             chunk[j] = 4 * half + j;
         }
-    } else if constexpr (WT == TYPE_Q4_K) {
+    } else if constexpr (WT == TYPE_Q4_K || WT == TYPE_Q5_K) {
         const int c = (k0 & 255) >> 6;
         int       sc_lo, mn_lo, sc_hi, mn_hi;
         q4k_scale_min_w(2 * c, w.s0, w.s1, w.s2, sc_lo, mn_lo);
@@ -130,9 +135,15 @@ __device__ __forceinline__ void w_dequant(const WRaw & w, const uint8_t * row, i
         const float d2 = d * (float) sc_hi, m2 = dmin * (float) mn_hi;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const int q         = byte_u(w.q0, i);
-            o[i / 8][i % 8]     = (_Float16) (d1 * (float) (q & 15) - m1);
-            o[2 + i / 8][i % 8] = (_Float16) (d2 * (float) (q >> 4) - m2);
+            const int q  = byte_u(w.q0, i);
+            int       ql = q & 15, qh = q >> 4;
+            if constexpr (WT == TYPE_Q5_K) {
+                const int h = byte_u(w.q1, i);
+                ql |= ((h >> (2 * c)) & 1) << 4;
+                qh |= ((h >> (2 * c + 1)) & 1) << 4;
+            }
+            o[i / 8][i % 8]     = (_Float16) (d1 * (float) ql - m1);
+            o[2 + i / 8][i % 8] = (_Float16) (d2 * (float) qh - m2);
         }
         chunk[0] = 2 * half;
         chunk[1] = 2 * half + 1;
@@ -748,17 +759,17 @@ static int weights_to_f16(int wtype, const uint8_t * W, int64_t N, int64_t K, in
     switch (wtype) {
         case TYPE_Q8_0: hipLaunchKernelGGL(k_w_to_f16<TYPE_Q8_0>, dim3((unsigned) nb), dim3(256), 0, stream, W, N, K, rs, wh); break;
         case TYPE_Q4_K: hipLaunchKernelGGL(k_w_to_f16<TYPE_Q4_K>, dim3((unsigned) nb), dim3(256), 0, stream, W, N, K, rs, wh); break;
+        case TYPE_Q5_K: hipLaunchKernelGGL(k_w_to_f16<TYPE_Q5_K>, dim3((unsigned) nb), dim3(256), 0, stream, W, N, K, rs, wh); break;
         default: hipLaunchKernelGGL(k_w_to_f16<TYPE_Q6_K>, dim3((unsigned) nb), dim3(256), 0, stream, W, N, K, rs, wh); break;
     }
     return check_launch("mul_mat gemm: weights to f16");
 }
 
 bool gemm_supported(int wtype, int64_t N, int64_t K, int64_t rs, const void * W, const float * x, int64_t ldx) {
-    if (!(wtype == TYPE_Q8_0 || wtype == TYPE_Q4_K || wtype == TYPE_Q6_K) || N <= 0 || K % GM_BK != 0 ||
-        rs < row_bytes(wtype, K)) {
+    if (!is_repacked_type(wtype) || N <= 0 || K % GM_BK != 0 || rs < row_bytes(wtype, K)) {
         return false;
     }
-    if ((wtype == TYPE_Q4_K || wtype == TYPE_Q6_K) && K % 256 != 0) {
+    if (wtype != TYPE_Q8_0 && K % 256 != 0) {
         return false;
     }
     // 16-byte weight and activation loads
@@ -801,12 +812,14 @@ static int launch_gemm(int wtype, const uint8_t * W, int64_t N, int64_t K, int64
             switch (wtype) {
                 case TYPE_Q8_0: return go(k_gemm_q<TYPE_Q8_0, NW, WM, BK, BM, true>);
                 case TYPE_Q4_K: return go(k_gemm_q<TYPE_Q4_K, NW, WM, BK, BM, true>);
+                case TYPE_Q5_K: return go(k_gemm_q<TYPE_Q5_K, NW, WM, BK, BM, true>);
                 default: return go(k_gemm_q<TYPE_Q6_K, NW, WM, BK, BM, true>);
             }
         }
         switch (wtype) {
             case TYPE_Q8_0: return go(k_gemm_q<TYPE_Q8_0, NW, WM, BK, BM, false>);
             case TYPE_Q4_K: return go(k_gemm_q<TYPE_Q4_K, NW, WM, BK, BM, false>);
+            case TYPE_Q5_K: return go(k_gemm_q<TYPE_Q5_K, NW, WM, BK, BM, false>);
             default: return go(k_gemm_q<TYPE_Q6_K, NW, WM, BK, BM, false>);
         }
     }

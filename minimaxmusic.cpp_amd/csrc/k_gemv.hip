@@ -1214,10 +1214,12 @@ __global__ __launch_bounds__(64 * PG_WAVES) void k_gemv_q8_0_norm_glu(PgArgs a, 
     }
 }
 
-// Q4_K.  Wave-chunk = 1024 bytes of qs (8 super-blocks); lane l owns 16
-// bytes = elements e_lo..e_lo+15 (low nibbles, sub-block 2c) and
-// e_lo+32..e_lo+47 (high nibbles, sub-block 2c+1) of super-block sb.
-template <int NC, int R, int U>
+// Q4_K and Q5_K.  Wave-chunk = 1024 bytes of qs (8 super-blocks); lane l
+// owns 16 bytes = elements e_lo..e_lo+15 (low nibbles, sub-block 2c) and
+// e_lo+32..e_lo+47 (high nibbles, sub-block 2c+1) of super-block sb.  Q5
+// adds the 16 qh bytes of the same columns (qh[32sb + (e_lo & 31) + i]), whose
+// bits 2c and 2c+1 are the fifth bits of the two nibbles.
+template <int NC, int R, int U, bool Q5 = false>
 __global__ __launch_bounds__(256) void k_gemv_q4_K(const uint8_t * __restrict__ W, int64_t N, int64_t K, int64_t rs,
                                                     const int8_t * __restrict__ xq, const float * __restrict__ xd,
                                                     const int16_t * __restrict__ xbs, float * y,
@@ -1228,6 +1230,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4_K(const uint8_t * __restrict__ 
         return;
     }
     const int64_t   half_k = K / 2;
+    const int64_t   sc_off = half_k + (Q5 ? K / 8 : 0);
     const int       nsb    = (int) (K / 256);
     const int       ngrp   = (int) (K / 16);
     const uint8_t * wr[R];
@@ -1245,6 +1248,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4_K(const uint8_t * __restrict__ 
     }
     for (int64_t base = 0; base < half_k; base += 1024 * U) {
         int4_t   wv[U][R];
+        int4_t   hv[U][R];
         uint32_t s0[U][R], s1[U][R], s2[U][R], dm[U][R];
         int4_t   xlo[U][NC], xhi[U][NC];
         int      blo[U][NC], bhi[U][NC];
@@ -1260,11 +1264,14 @@ __global__ __launch_bounds__(256) void k_gemv_q4_K(const uint8_t * __restrict__ 
 #pragma unroll
             for (int r = 0; r < R; r++) {
                 wv[u][r]            = ld16(wr[r] + o);
-                const uint32_t * sw = (const uint32_t *) (wr[r] + half_k + 12 * sb);
+                if constexpr (Q5) {
+                    hv[u][r] = ld16(wr[r] + half_k + 32 * sb + (o & 16));
+                }
+                const uint32_t * sw = (const uint32_t *) (wr[r] + sc_off + 12 * sb);
                 s0[u][r]            = sw[0];
                 s1[u][r]            = sw[1];
                 s2[u][r]            = sw[2];
-                dm[u][r]            = *(const uint32_t *) (wr[r] + half_k + 12 * (int64_t) nsb + 4 * sb);
+                dm[u][r]            = *(const uint32_t *) (wr[r] + sc_off + 12 * (int64_t) nsb + 4 * sb);
             }
 #pragma unroll
             for (int c = 0; c < NC; c++) {
@@ -1289,9 +1296,17 @@ __global__ __launch_bounds__(256) void k_gemv_q4_K(const uint8_t * __restrict__ 
                 const float  d    = h2f((uint16_t) (dm[u][r] & 0xffff));
                 const float  dmin = h2f((uint16_t) (dm[u][r] >> 16));
                 const int4_t w    = wv[u][r];
-                const int4_t lo = { w.x & 0x0F0F0F0F, w.y & 0x0F0F0F0F, w.z & 0x0F0F0F0F, w.w & 0x0F0F0F0F };
-                const int4_t hi = { (w.x >> 4) & 0x0F0F0F0F, (w.y >> 4) & 0x0F0F0F0F, (w.z >> 4) & 0x0F0F0F0F,
-                                    (w.w >> 4) & 0x0F0F0F0F };
+                int4_t lo = { w.x & 0x0F0F0F0F, w.y & 0x0F0F0F0F, w.z & 0x0F0F0F0F, w.w & 0x0F0F0F0F };
+                int4_t hi = { (w.x >> 4) & 0x0F0F0F0F, (w.y >> 4) & 0x0F0F0F0F, (w.z >> 4) & 0x0F0F0F0F,
+                              (w.w >> 4) & 0x0F0F0F0F };
+                if constexpr (Q5) {
+                    const int4_t h = hv[u][r];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        lo[i] |= ((h[i] >> (2 * c64)) & 0x01010101) << 4;
+                        hi[i] |= ((h[i] >> (2 * c64 + 1)) & 0x01010101) << 4;
+                    }
+                }
 #pragma unroll
                 for (int c = 0; c < NC; c++) {
                     const int isum = sc_lo * dot16(lo, xlo[u][c]) + sc_hi * dot16(hi, xhi[u][c]);
@@ -1485,6 +1500,11 @@ static int gemv_dispatch(int wtype, const uint8_t * W, int64_t N, int64_t K, int
         constexpr int U4 = U > 2 ? 2 : U;
         return launch_gemv(k_gemv_q4_K<NC, R, U4>, R, N, stream, W, N, K, rs, x.qs, x.d, x.bs, y, ldy, r, ldr);
     }
+    if (wtype == TYPE_Q5_K) {
+        constexpr int U5 = U > 2 ? 2 : U;
+        return launch_gemv(k_gemv_q4_K<NC, R, U5, true>, R, N, stream, W, N, K, rs, x.qs, x.d, x.bs, y, ldy, r,
+                           ldr);
+    }
     constexpr int U6 = 1;
     if (rs % 16 == 0 && ((uintptr_t) W) % 16 == 0) {
         return launch_gemv(k_gemv_q6_K<NC, R, U6, true>, R, N, stream, W, N, K, rs, x.qs, x.d, x.bs, y, ldy, r, ldr);
@@ -1493,11 +1513,12 @@ static int gemv_dispatch(int wtype, const uint8_t * W, int64_t N, int64_t K, int
 }
 
 bool gemv_supported(int wtype, int64_t N, int64_t K, int64_t rs, const void * W) {
-    if (!(wtype == TYPE_Q8_0 || wtype == TYPE_Q4_K || wtype == TYPE_Q6_K) || K % 256 != 0 || N <= 0 ||
-        K > ((int64_t) 1 << 30) || rs < row_bytes(wtype, K)) {
+    if (!is_repacked_type(wtype) || K % 256 != 0 || N <= 0 || K > ((int64_t) 1 << 30) ||
+        rs < row_bytes(wtype, K)) {
         return false;
     }
-    // Q8_0 / Q4_K rows are read with 16-byte loads; Q6_K rows may be 2-byte aligned
+    // Q8_0 / Q4_K / Q5_K rows are read with 16-byte loads; Q6_K rows may be
+    // 2-byte aligned
     const int64_t align = wtype == TYPE_Q6_K ? 2 : 16;
     return rs % align == 0 && ((uintptr_t) W) % align == 0;
 }

@@ -917,15 +917,21 @@ __device__ __forceinline__ float deq_elem(int type, const uint8_t * r, int64_t K
         const float d = h2f(((const uint16_t *) (r + K))[k >> 5]);
         return d * (float) ((const int8_t *) r)[k];
     }
-    if (type == TYPE_Q4_K) {
-        const int64_t sb = k >> 8;
-        const int     e  = (int) (k & 255);
-        const int     j  = e >> 5;
+    if (type == TYPE_Q4_K || type == TYPE_Q5_K) {
+        // Q5_K: qh[K/8] after qs, fifth bit of element e at bit e / 32 of
+        // the super-block's qh byte e % 32
+        const int64_t sb    = k >> 8;
+        const int     e     = (int) (k & 255);
+        const int     j     = e >> 5;
+        const int64_t qh_sz = type == TYPE_Q5_K ? K / 8 : 0;
         int           s, m;
-        q4k_scale_min(j, r + K / 2 + 12 * sb, s, m);
-        const uint16_t * dm = (const uint16_t *) (r + K / 2 + 12 * (K / 256)) + 2 * sb;
+        q4k_scale_min(j, r + K / 2 + qh_sz + 12 * sb, s, m);
+        const uint16_t * dm = (const uint16_t *) (r + K / 2 + qh_sz + 12 * (K / 256)) + 2 * sb;
         const uint8_t    b  = r[sb * 128 + (e >> 6) * 32 + (e & 31)];
-        const int        q  = (e & 32) ? (b >> 4) : (b & 15);
+        int              q  = (e & 32) ? (b >> 4) : (b & 15);
+        if (type == TYPE_Q5_K) {
+            q |= ((r[K / 2 + sb * 32 + (e & 31)] >> j) & 1) << 4;
+        }
         const float      d1 = h2f(dm[0]) * (float) s;
         const float      m1 = h2f(dm[1]) * (float) m;
         return d1 * (float) q - m1;
@@ -1401,10 +1407,9 @@ extern "C" int mmhip_get_rows(int src_type, const mmhip_view * src, const mmhip_
     if (src_type == 26) {
         src_type = TYPE_F32;  // I32 rows: moved as 4-byte words, bit for bit
     }
-    const bool q = src_type == TYPE_Q8_0 || src_type == TYPE_Q4_K || src_type == TYPE_Q6_K;
+    const bool q = is_repacked_type(src_type);
     if (!src || !ids || !dst || !(q || src_type == TYPE_F32 || src_type == TYPE_F16) ||
-        (src_type == TYPE_Q8_0 && src->ne[0] % 32 != 0) || ((src_type == TYPE_Q4_K || src_type == TYPE_Q6_K) &&
-                                                            src->ne[0] % 256 != 0)) {
+        (src_type == TYPE_Q8_0 && src->ne[0] % 32 != 0) || (q && src_type != TYPE_Q8_0 && src->ne[0] % 256 != 0)) {
         return set_error(MMHIP_ERR_INVALID, "get_rows: bad arguments");
     }
     const int64_t n = src->ne[0] * ids->ne[0] * ids->ne[1] * ids->ne[2];

@@ -20,6 +20,7 @@ static __host__ __device__ FieldTable field_table(int type) {
     switch (type) {
         case TYPE_Q8_0: return { 2, { 2, 0, 0, 0 }, { 32, 2, 0, 0 }, 34, 32 };
         case TYPE_Q4_K: return { 3, { 16, 4, 0, 0 }, { 128, 12, 4, 0 }, 144, 256 };
+        case TYPE_Q5_K: return { 4, { 48, 16, 4, 0 }, { 128, 32, 12, 4 }, 176, 256 };
         case TYPE_Q6_K: return { 4, { 0, 128, 192, 208 }, { 128, 64, 16, 2 }, 210, 256 };
         default:        return { 0, { 0 }, { 0 }, 0, 0 };
     }
@@ -67,20 +68,27 @@ __global__ void k_dequant(int type, const uint8_t * __restrict__ w, int64_t nrow
             for (int j = 0; j < 32; j++) {
                 out[j] = d * (float) qs[j];
             }
-        } else if (type == TYPE_Q4_K) {
+        } else if (type == TYPE_Q4_K || type == TYPE_Q5_K) {
+            // Q5_K: qh[K/8] follows qs; the fifth bit of element 32j + l of a
+            // super-block is bit j of its qh byte l
             const int64_t   nbk   = K / 256;
             const int64_t   sb    = g / 8;
             const int       j     = (int) (g % 8);
+            const int64_t   qh_sz = type == TYPE_Q5_K ? K / 8 : 0;
             const uint8_t * qs    = r + sb * 128 + (j / 2) * 32;
-            const uint8_t * sc    = r + K / 2 + sb * 12;
-            const uint16_t * dm   = (const uint16_t *) (r + K / 2 + nbk * 12) + 2 * sb;
+            const uint8_t * qh    = r + K / 2 + sb * 32;
+            const uint8_t * sc    = r + K / 2 + qh_sz + sb * 12;
+            const uint16_t * dm   = (const uint16_t *) (r + K / 2 + qh_sz + nbk * 12) + 2 * sb;
             int             s, m;
             q4k_scale_min(j, sc, s, m);
             const float d1 = h2f(dm[0]) * (float) s;
             const float m1 = h2f(dm[1]) * (float) m;
             for (int l = 0; l < 32; l++) {
-                const int q = (j & 1) ? (qs[l] >> 4) : (qs[l] & 0x0f);
-                out[l]      = d1 * (float) q - m1;
+                int q = (j & 1) ? (qs[l] >> 4) : (qs[l] & 0x0f);
+                if (type == TYPE_Q5_K) {
+                    q |= ((qh[l] >> j) & 1) << 4;
+                }
+                out[l] = d1 * (float) q - m1;
             }
         } else if (type == TYPE_Q6_K) {
             const int64_t   nbk = K / 256;
@@ -234,8 +242,8 @@ extern "C" int mmhip_unpack_rows(int type, const void * src, void * dst, int64_t
 extern "C" int mmhip_dequantize_rows(int type, const void * w, int64_t nrows, int64_t ne0, int64_t row_stride,
                                      float * dst, void * stream) {
     MMHIP_API_BEGIN();
-    const int blk = (type == TYPE_Q4_K || type == TYPE_Q6_K) ? 256 : 32;
-    if (!(type == TYPE_Q8_0 || type == TYPE_Q4_K || type == TYPE_Q6_K || type == TYPE_F16 || type == TYPE_F32)) {
+    const int blk = (type == TYPE_Q4_K || type == TYPE_Q5_K || type == TYPE_Q6_K) ? 256 : 32;
+    if (!(is_repacked_type(type) || type == TYPE_F16 || type == TYPE_F32)) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "dequantize: type %d", type);
     }
     if (ne0 <= 0 || ne0 % blk != 0 || nrows < 0 || row_stride < row_bytes(type, ne0)) {

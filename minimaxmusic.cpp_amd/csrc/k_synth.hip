@@ -29,7 +29,7 @@ __device__ __forceinline__ float normal01(uint64_t seed, uint64_t i) {
 }
 
 __global__ void k_synth_gguf(int type, uint8_t * __restrict__ dst, int64_t nblocks, uint64_t seed) {
-    const int bb = type == TYPE_Q8_0 ? 34 : type == TYPE_Q4_K ? 144 : 210;
+    const int bb = (int) row_bytes(type, type == TYPE_Q8_0 ? 32 : 256);
     for (int64_t b = blockIdx.x * (int64_t) blockDim.x + threadIdx.x; b < nblocks;
          b += (int64_t) gridDim.x * blockDim.x) {
         uint8_t *     p    = dst + b * bb;
@@ -49,9 +49,12 @@ __global__ void k_synth_gguf(int type, uint8_t * __restrict__ dst, int64_t nbloc
             const uint16_t d = f2h(fabsf(normal01(seed ^ 0xd0d0ull, (uint64_t) b)) * 0.02f / 127.0f);
             p[0]             = (uint8_t) (d & 0xff);
             p[1]             = (uint8_t) (d >> 8);
-        } else if (type == TYPE_Q4_K) {
-            const uint16_t d  = f2h(fabsf(normal01(seed ^ 0xd0d0ull, (uint64_t) b)) * 0.02f);
-            const uint16_t dm = f2h(fabsf(normal01(seed ^ 0xd1d1ull, (uint64_t) b)) * 0.02f);
+        } else if (type == TYPE_Q4_K || type == TYPE_Q5_K) {
+            // Q5_K: blocks centred on zero, |w| ~ 0.01
+            const float    dd = type == TYPE_Q5_K ? 512.0f : 1.0f;
+            const float    dn = type == TYPE_Q5_K ? 32.0f : 1.0f;
+            const uint16_t d  = f2h(fabsf(normal01(seed ^ 0xd0d0ull, (uint64_t) b)) * 0.02f / dd);
+            const uint16_t dm = f2h(fabsf(normal01(seed ^ 0xd1d1ull, (uint64_t) b)) * 0.02f / dn);
             p[0]              = (uint8_t) (d & 0xff);
             p[1]              = (uint8_t) (d >> 8);
             p[2]              = (uint8_t) (dm & 0xff);

@@ -37,7 +37,9 @@ constexpr int GRAPH_NODES = 16384;  // QW3LM_GRAPH_NODES, src/qwen3-lm.h:35
 
 struct Layer {
     ggml_tensor * input_layernorm;
-    ggml_tensor * qkv;  // [H, q_dim + 2 kv_dim]: q | k | v rows
+    ggml_tensor * qkv;  // [H, q_dim + 2 kv_dim]: q | k | v rows (one type)
+    ggml_tensor * qk;   // [H, q_dim + kv_dim]: q | k rows, when v's type differs
+    ggml_tensor * v;    // [H, kv_dim]
     ggml_tensor * q_norm;
     ggml_tensor * k_norm;
     ggml_tensor * o_proj;
@@ -112,6 +114,14 @@ bool fill_normal(ggml_tensor * t, uint64_t seed, float mean, float stdv) {
 // Weights and caches by name, then the current decode graph's tensors (the
 // graph allocator gives each its own memory, so a node's rows stay readable
 // until the next step).
+// The "_M" variants' choice of layers whose V and down projections take the
+// larger type (tools/quantize.cpp:127-150, bump_mode 2): the first n/9, the
+// last n/7 and every third layer.
+bool lm_layer_bumped(const mm_lm_config & c, int l) {
+    const int n = c.n_layers;
+    return c.bump_type != 0 && c.bump_type != c.wtype && (l < n / 9 || l >= n - n / 7 || l % 3 == 0);
+}
+
 ggml_tensor * find_tensor(Lm * m, const char * name) {
     ggml_tensor * t = ggml_get_tensor(m->wctx, name);
     t               = t ? t : ggml_get_tensor(m->kv_ctx, name);
@@ -154,11 +164,19 @@ void build_graph(Lm * m, int N, int n_kv_pad, int s0) {
 
         ggml_tensor * norm = rms_norm_mul(ctx, hidden, ly->input_layernorm, c.rms_eps);
 
-        ggml_tensor * qkv = ggml_mul_mat(ctx, ly->qkv, norm);
-        ggml_tensor * q   = ggml_cont(ctx, ggml_view_2d(ctx, qkv, q_dim, N, qkv->nb[1], 0));
-        ggml_tensor * k   = ggml_cont(ctx, ggml_view_2d(ctx, qkv, kv_dim, N, qkv->nb[1], (size_t) q_dim * qkv->nb[0]));
-        ggml_tensor * v =
-            ggml_cont(ctx, ggml_view_2d(ctx, qkv, kv_dim, N, qkv->nb[1], (size_t) (q_dim + kv_dim) * qkv->nb[0]));
+        // fused Q | K | V, or fused Q | K and a separate V (src/qwen3-lm.h:742-757)
+        ggml_tensor *q, *k, *v;
+        if (ly->qkv) {
+            ggml_tensor * qkv = ggml_mul_mat(ctx, ly->qkv, norm);
+            q = ggml_cont(ctx, ggml_view_2d(ctx, qkv, q_dim, N, qkv->nb[1], 0));
+            k = ggml_cont(ctx, ggml_view_2d(ctx, qkv, kv_dim, N, qkv->nb[1], (size_t) q_dim * qkv->nb[0]));
+            v = ggml_cont(ctx, ggml_view_2d(ctx, qkv, kv_dim, N, qkv->nb[1], (size_t) (q_dim + kv_dim) * qkv->nb[0]));
+        } else {
+            ggml_tensor * qk = ggml_mul_mat(ctx, ly->qk, norm);
+            q = ggml_cont(ctx, ggml_view_2d(ctx, qk, q_dim, N, qk->nb[1], 0));
+            k = ggml_cont(ctx, ggml_view_2d(ctx, qk, kv_dim, N, qk->nb[1], (size_t) q_dim * qk->nb[0]));
+            v = ggml_mul_mat(ctx, ly->v, norm);
+        }
 
         q = ggml_reshape_3d(ctx, q, D, Nh, N);
         k = ggml_reshape_3d(ctx, k, D, Nkv, N);
@@ -297,6 +315,11 @@ void * lm_create(const mm_lm_config * cfg, int device, ggml_backend_t backend, u
         err("create: bad config");
         return nullptr;
     }
+    if (cfg->bump_type != 0 && !(cfg->bump_type == GGML_TYPE_Q8_0 || cfg->bump_type == GGML_TYPE_Q4_K ||
+                                 cfg->bump_type == GGML_TYPE_Q5_K || cfg->bump_type == GGML_TYPE_Q6_K)) {
+        err("create: bad bump_type %d", cfg->bump_type);
+        return nullptr;
+    }
     if (backend && !ggml_backend_is_mi355x(backend)) {
         err("create: the backend is not an MI355X backend");
         return nullptr;
@@ -316,26 +339,33 @@ void * lm_create(const mm_lm_config * cfg, int device, ggml_backend_t backend, u
     const int            kv_dim = c.n_kv_heads * c.head_dim;
 
     // weights (src/qwen3-enc.h:119-160 layout: ne0 = input dim)
-    const size_t n_w = (size_t) c.n_layers * 8 + 4;
+    const size_t n_w = (size_t) c.n_layers * 9 + 4;
     m->wctx          = ggml_init({ n_w * ggml_tensor_overhead() + 1024, nullptr, true });
     m->layers.resize((size_t) c.n_layers);
     char name[96];
     for (int l = 0; l < c.n_layers; l++) {
         Layer & ly              = m->layers[(size_t) l];
+        const bool bump         = lm_layer_bumped(c, l);
+        const enum ggml_type bt = bump ? (enum ggml_type) c.bump_type : wt;
         ly.input_layernorm      = ggml_new_tensor_1d(m->wctx, GGML_TYPE_F32, c.hidden);
-        ly.qkv                  = ggml_new_tensor_2d(m->wctx, wt, c.hidden, q_dim + 2 * kv_dim);
+        ly.qkv                  = bt == wt ? ggml_new_tensor_2d(m->wctx, wt, c.hidden, q_dim + 2 * kv_dim) : nullptr;
+        ly.qk                   = bt == wt ? nullptr : ggml_new_tensor_2d(m->wctx, wt, c.hidden, q_dim + kv_dim);
+        ly.v                    = bt == wt ? nullptr : ggml_new_tensor_2d(m->wctx, bt, c.hidden, kv_dim);
         ly.q_norm               = ggml_new_tensor_1d(m->wctx, GGML_TYPE_F32, c.head_dim);
         ly.k_norm               = ggml_new_tensor_1d(m->wctx, GGML_TYPE_F32, c.head_dim);
         ly.o_proj               = ggml_new_tensor_2d(m->wctx, wt, q_dim, c.hidden);
         ly.post_attn_layernorm  = ggml_new_tensor_1d(m->wctx, GGML_TYPE_F32, c.hidden);
         ly.gate_up              = ggml_new_tensor_2d(m->wctx, wt, c.hidden, 2 * c.ffn);
-        ly.down                 = ggml_new_tensor_2d(m->wctx, wt, c.ffn, c.hidden);
-        const char * names[8]   = { "attn_norm", "qkv", "q_norm", "k_norm", "o_proj", "ffn_norm", "gate_up", "down" };
-        ggml_tensor * ts[8] = { ly.input_layernorm, ly.qkv, ly.q_norm, ly.k_norm,
-                                ly.o_proj, ly.post_attn_layernorm, ly.gate_up, ly.down };
-        for (int i = 0; i < 8; i++) {
-            snprintf(name, sizeof(name), "blk.%d.%s", l, names[i]);
-            ggml_set_name(ts[i], name);
+        ly.down                 = ggml_new_tensor_2d(m->wctx, bt, c.ffn, c.hidden);
+        const char * names[10]  = { "attn_norm", "qkv", "qk", "v", "q_norm", "k_norm", "o_proj", "ffn_norm",
+                                    "gate_up", "down" };
+        ggml_tensor * ts[10] = { ly.input_layernorm, ly.qkv, ly.qk, ly.v, ly.q_norm, ly.k_norm,
+                                 ly.o_proj, ly.post_attn_layernorm, ly.gate_up, ly.down };
+        for (int i = 0; i < 10; i++) {
+            if (ts[i]) {
+                snprintf(name, sizeof(name), "blk.%d.%s", l, names[i]);
+                ggml_set_name(ts[i], name);
+            }
         }
     }
     m->final_norm = ggml_new_tensor_1d(m->wctx, GGML_TYPE_F32, c.hidden);
@@ -494,6 +524,12 @@ extern "C" int64_t mm_lm_tensor_nbytes(void * h, const char * name) {
     Lm *          m = (Lm *) h;
     ggml_tensor * t = m ? find_tensor(m, name) : nullptr;
     return t ? (int64_t) ggml_nbytes(t) : -1;
+}
+
+extern "C" int mm_lm_tensor_type(void * h, const char * name) {
+    Lm *          m = (Lm *) h;
+    ggml_tensor * t = m ? find_tensor(m, name) : nullptr;
+    return t ? (int) t->type : -1;
 }
 
 extern "C" int mm_lm_get_tensor(void * h, const char * name, void * dst, size_t size) {

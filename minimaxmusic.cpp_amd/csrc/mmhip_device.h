@@ -6,6 +6,7 @@
 // grouped so that every field streams with aligned 16-byte loads:
 //   Q8_0 : qs[K] (int8)        | d[K/32] (f16)
 //   Q4_K : qs[K/2] (nibbles)   | scales[12*K/256] | dm[2*K/256] (f16 d, dmin)
+//   Q5_K : qs[K/2] (nibbles)   | qh[K/8] | scales[12*K/256] | dm[2*K/256]
 //   Q6_K : ql[K/2] | qh[K/4]   | sc[K/16] (int8)  | d[K/256] (f16)
 // Within a field, blocks keep their GGUF order and their GGUF byte order.
 #pragma once
@@ -20,6 +21,7 @@ constexpr int TYPE_F32  = 0;
 constexpr int TYPE_F16  = 1;
 constexpr int TYPE_Q8_0 = 8;
 constexpr int TYPE_Q4_K = 12;
+constexpr int TYPE_Q5_K = 13;
 constexpr int TYPE_Q6_K = 14;
 constexpr int TYPE_Q8_K = 15;
 constexpr int TYPE_BF16 = 30;
@@ -278,6 +280,7 @@ __device__ __forceinline__ void q4k_scale_min_w(int j, uint32_t w0, uint32_t w1,
 __host__ __device__ constexpr int64_t row_bytes(int type, int64_t k) {
     return type == TYPE_Q8_0 ? (k / 32) * 34
          : type == TYPE_Q4_K ? (k / 256) * 144
+         : type == TYPE_Q5_K ? (k / 256) * 176
          : type == TYPE_Q6_K ? (k / 256) * 210
          : type == TYPE_F16 || type == TYPE_BF16 ? k * 2
          : type == TYPE_F32 ? k * 4

@@ -20,7 +20,7 @@ int  check_launch(const char * what);
 void clear_error();
 
 inline bool is_repacked_type(int type) {
-    return type == 8 /*Q8_0*/ || type == 12 /*Q4_K*/ || type == 14 /*Q6_K*/;
+    return type == 8 /*Q8_0*/ || type == 12 /*Q4_K*/ || type == 13 /*Q5_K*/ || type == 14 /*Q6_K*/;
 }
 
 // Quantised-activation buffer layout for M rows of K elements:
@@ -41,7 +41,7 @@ inline ActLayout act_layout(int wtype, int64_t K, int64_t M) {
     if (wtype == 8 && K % 32 == 0) {
         L.vec_type = 8;
         L.blk      = 32;
-    } else if ((wtype == 12 || wtype == 14) && K % 256 == 0) {
+    } else if ((wtype == 12 || wtype == 13 || wtype == 14) && K % 256 == 0) {
         L.vec_type = 15;
         L.blk      = 256;
     } else {

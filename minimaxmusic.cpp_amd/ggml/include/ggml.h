@@ -291,7 +291,7 @@ typedef void (*ggml_to_float_t)(const void * x, float * y, int64_t k);
 typedef void (*ggml_from_float_t)(const float * x, void * y, int64_t k);
 
 // Per-type traits; to_float decodes k elements (a whole number of blocks)
-// from the GGUF block layout: set for F16, BF16, Q8_0, Q4_K and Q6_K in this
+// from the GGUF block layout: set for F16, BF16, Q8_0, Q4_K, Q5_K and Q6_K in this
 // build (host dequantisation, src/gguf-weights.h:230-235, :258-283).
 struct ggml_type_traits {
     const char *      type_name;

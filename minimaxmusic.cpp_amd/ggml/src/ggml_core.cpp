@@ -1704,6 +1704,9 @@ extern "C" size_t ggml_gallocr_get_buffer_size(ggml_gallocr_t g, int buffer_id) 
 //   top two bits in the high bits of bytes 0..3 / 4..7); each 64-element chunk
 //   j takes its low nibbles with pair 2j and its high nibbles with pair 2j+1,
 //   y = (d * sc) * q - (dmin * m).
+// Q5_K: 256 per 176 bytes {f16 d; f16 dmin; u8 scales[12]; u8 qh[32];
+//   u8 qs[128]}: Q4_K's scales and nibbles, plus a fifth quant bit per
+//   element (bit j of qh[l] for element 32j + l), q in [0, 31].
 // Q6_K: 256 per 210 bytes {u8 ql[128]; u8 qh[64]; i8 scales[16]; f16 d}: each
 //   128-element half takes 64 bytes of ql (low nibbles then high nibbles of
 //   two 32-byte rows) and 32 bytes of qh (two bits per element), q in
@@ -1766,6 +1769,30 @@ void to_float_q4_k(const void * x, float * y, int64_t k) {
     }
 }
 
+void to_float_q5_k(const void * x, float * y, int64_t k) {
+    const uint8_t * b = (const uint8_t *) x;
+    for (int64_t i = 0; i < k / 256; i++, b += 176) {
+        const float     d    = h2f(b);
+        const float     dmin = h2f(b + 2);
+        const uint8_t * sc   = b + 4;
+        const uint8_t * qh   = b + 16;
+        const uint8_t * q    = b + 48;
+        float *         out  = y + i * 256;
+        for (int c = 0; c < 4; c++) {
+            uint8_t s0, m0, s1, m1;
+            q4_k_pair(2 * c, sc, s0, m0);
+            q4_k_pair(2 * c + 1, sc, s1, m1);
+            const float d0 = d * s0, n0 = dmin * m0, d1 = d * s1, n1 = dmin * m1;
+            for (int l = 0; l < 32; l++) {
+                const int lo = (q[32 * c + l] & 0x0F) | (((qh[l] >> (2 * c)) & 1) << 4);
+                const int hi = (q[32 * c + l] >> 4) | (((qh[l] >> (2 * c + 1)) & 1) << 4);
+                out[64 * c + l]      = d0 * (float) lo - n0;
+                out[64 * c + 32 + l] = d1 * (float) hi - n1;
+            }
+        }
+    }
+}
+
 void to_float_q6_k(const void * x, float * y, int64_t k) {
     const uint8_t * b = (const uint8_t *) x;
     for (int64_t i = 0; i < k / 256; i++, b += 210) {
@@ -1804,6 +1831,7 @@ extern "C" const struct ggml_type_traits * ggml_get_type_traits(enum ggml_type t
         table[GGML_TYPE_BF16].to_float = to_float_bf16;
         table[GGML_TYPE_Q8_0].to_float = to_float_q8_0;
         table[GGML_TYPE_Q4_K].to_float = to_float_q4_k;
+        table[GGML_TYPE_Q5_K].to_float = to_float_q5_k;
         table[GGML_TYPE_Q6_K].to_float = to_float_q6_k;
         init                           = true;
     }

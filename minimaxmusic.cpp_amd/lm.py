@@ -13,7 +13,8 @@ class LmConfig(ctypes.Structure):
     _fields_ = [("n_layers", ctypes.c_int), ("hidden", ctypes.c_int), ("n_heads", ctypes.c_int),
                 ("n_kv_heads", ctypes.c_int), ("head_dim", ctypes.c_int), ("ffn", ctypes.c_int),
                 ("vocab", ctypes.c_int), ("max_seq", ctypes.c_int), ("n_sets", ctypes.c_int),
-                ("wtype", ctypes.c_int), ("rms_eps", ctypes.c_float), ("rope_theta", ctypes.c_float)]
+                ("wtype", ctypes.c_int), ("rms_eps", ctypes.c_float), ("rope_theta", ctypes.c_float),
+                ("bump_type", ctypes.c_int)]
 
 
 # Qwen3-8B shape of the decode benchmark (36 layers, vocab 151936, Q8_0)
@@ -44,6 +45,7 @@ def load():
         L.mm_lm_tensor_nbytes.argtypes = [vp, ctypes.c_char_p]
         L.mm_lm_tensor_nbytes.restype = i64
         L.mm_lm_get_tensor.argtypes = [vp, ctypes.c_char_p, vp, ctypes.c_size_t]
+        L.mm_lm_tensor_type.argtypes = [vp, ctypes.c_char_p]
         L.mm_lm_set_tensor.argtypes = [vp, ctypes.c_char_p, vp, ctypes.c_size_t]
         L.mm_lm_graph_nodes.argtypes = [vp]
         L.mm_lm_graph_stats.argtypes = [vp, ctypes.POINTER(i64), ctypes.POINTER(i64)]
@@ -117,6 +119,14 @@ class Lm:
         out = np.empty(n, np.uint8)
         self._check(load().mm_lm_get_tensor(self.h, name.encode(), _p(out), n))
         return out.view(dtype)
+
+    def type_of(self, name):
+        """GGML type of a weight or cache tensor; None if there is none."""
+        t = load().mm_lm_tensor_type(self.h, name.encode())
+        return None if t < 0 else t
+
+    def has(self, name):
+        return self.type_of(name) is not None
 
     def set(self, name, data):
         data = np.ascontiguousarray(data).view(np.uint8)

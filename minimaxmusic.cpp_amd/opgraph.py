@@ -17,7 +17,7 @@ import numpy as np
 
 LIBDIR = pathlib.Path(__file__).resolve().parent / "lib"
 GGML_MAX_NAME = 128
-F32, F16, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 8, 12, 14, 30
+F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, BF16 = 0, 1, 8, 12, 13, 14, 30
 PREC_F32 = 10
 ROPE_NEOX = 2
 

@@ -6,6 +6,10 @@ distributions used for every measurement here:
 * Q8_0: quants uniform in [-127, 127]; d = f16(|N(0, 0.02)| / 127).
 * Q4_K: 4-bit quants and 6-bit (scale, min) pairs uniform (random bytes);
   d, dmin = f16(|N(0, 0.02)|).
+* Q5_K: quant, fifth-bit and 6-bit (scale, min) bytes uniform;
+  d = f16(|N(0, 0.02)| / 512), dmin = f16(|N(0, 0.02)| / 32), so that
+  E[d sc q] = E[dmin m] (blocks centred on zero) and |w| ~ 0.01 like real
+  weights and like the Q6_K blocks it is mixed with in the "_M" files.
 * Q6_K: low/high quant bits uniform (random bytes); int8 scales uniform in
   [-64, 63]; d = f16(|N(0, 0.02)| / 1024), so |w| ~ 0.01 like real weights.
 
@@ -14,10 +18,11 @@ the same distributions directly in device memory (large benchmarks).
 """
 import numpy as np
 
-Q8_0, Q4_K, Q6_K = 8, 12, 14
-BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
+BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
 # byte offset of the f16 scale fields inside each GGUF block
-_D_FIELDS = {Q8_0: [0], Q4_K: [0, 2], Q6_K: [208]}
+_D_FIELDS = {Q8_0: [0], Q4_K: [0, 2], Q5_K: [0, 2], Q6_K: [208]}
+_DMIN_DIV = {Q4_K: (1.0, 1.0), Q5_K: (512.0, 32.0)}
 
 
 def _scale_bits(rng, n, div):
@@ -35,9 +40,10 @@ def gguf_blocks_np(qtype, N, K, seed):
         blk[:, 2:34] = q.view(np.uint8)
         d = _scale_bits(rng, nb, 127.0)
         blk[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
-    elif qtype == Q4_K:
-        blk[:, 0:2] = _scale_bits(rng, nb, 1.0).view(np.uint8).reshape(nb, 2)
-        blk[:, 2:4] = _scale_bits(rng, nb, 1.0).view(np.uint8).reshape(nb, 2)
+    elif qtype in (Q4_K, Q5_K):
+        dd, dm = _DMIN_DIV[qtype]
+        blk[:, 0:2] = _scale_bits(rng, nb, dd).view(np.uint8).reshape(nb, 2)
+        blk[:, 2:4] = _scale_bits(rng, nb, dm).view(np.uint8).reshape(nb, 2)
     elif qtype == Q6_K:
         sc = rng.integers(-64, 64, size=(nb, 16), dtype=np.int16).astype(np.int8)
         blk[:, 192:208] = sc.view(np.uint8)
@@ -63,9 +69,10 @@ def gguf_blocks_torch(qtype, N, K, seed, device="cuda"):
         q = torch.randint(-127, 128, (nb, 32), dtype=torch.int8, device=device, generator=g)
         blk[:, 2:34] = q.view(torch.uint8)
         blk[:, 0:2] = scale(127.0)
-    elif qtype == Q4_K:
-        blk[:, 0:2] = scale(1.0)
-        blk[:, 2:4] = scale(1.0)
+    elif qtype in (Q4_K, Q5_K):
+        dd, dm = _DMIN_DIV[qtype]
+        blk[:, 0:2] = scale(dd)
+        blk[:, 2:4] = scale(dm)
     elif qtype == Q6_K:
         sc = torch.randint(-64, 64, (nb, 16), dtype=torch.int8, device=device, generator=g)
         blk[:, 192:208] = sc.view(torch.uint8)

@@ -15,9 +15,9 @@ import numpy as np
 HERE = pathlib.Path(__file__).resolve().parent
 LIB_PATH = HERE / "liboracle.so"
 
-F32, F16, Q8_0, Q4_K, Q6_K, Q8_K, I32, I64, BF16 = 0, 1, 8, 12, 14, 15, 26, 27, 30
+F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K, I32, I64, BF16 = 0, 1, 8, 12, 13, 14, 15, 26, 27, 30
 
-BLOCK = {F32: (1, 4), F16: (1, 2), BF16: (1, 2), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210), Q8_K: (256, 292)}
+BLOCK = {F32: (1, 4), F16: (1, 2), BF16: (1, 2), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_K: (256, 292)}
 
 
 def row_size(t, ne0):

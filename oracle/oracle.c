@@ -8,13 +8,14 @@
  *   fp16/bf16 conversions  exhaustive fp16->fp32 and 2^20 random fp32->fp16
  *                          against numpy's IEEE conversions; bf16 vs the torch
  *                          rounding of the same values.
- *   dequantize Q8_0/Q4_K/Q6_K
+ *   dequantize Q8_0/Q4_K/Q5_K/Q6_K
  *                          hand-built known-answer blocks with literal expected
  *                          values (tests/golden/known_blocks.json), covering
  *                          d = 1, q = -127..127; Q4_K 6-bit scale packing for
- *                          sub-blocks j < 4 and j >= 4; dmin != 0; Q6_K's -32
- *                          offset and all 16 scales; plus an independent numpy
- *                          bit-field decoder on random blocks.
+ *                          sub-blocks j < 4 and j >= 4; dmin != 0; Q5_K's fifth
+ *                          bit from qh (bit j of byte l for sub-block j); Q6_K's
+ *                          -32 offset and all 16 scales; plus an independent
+ *                          numpy bit-field decoder on random blocks.
  *   quantize_row_q8_0/_q8_K
  *                          closed forms: x = d*q exactly representable round-
  *                          trips; all-zero rows; the Q8_K max element maps to
@@ -150,6 +151,7 @@ size_t orc_type_size(int type) {
         case ORC_TYPE_I64:  return 8;
         case ORC_TYPE_Q8_0: return sizeof(orc_block_q8_0);
         case ORC_TYPE_Q4_K: return sizeof(orc_block_q4_K);
+        case ORC_TYPE_Q5_K: return sizeof(orc_block_q5_K);
         case ORC_TYPE_Q6_K: return sizeof(orc_block_q6_K);
         case ORC_TYPE_Q8_K: return sizeof(orc_block_q8_K);
         default:            return 0;
@@ -160,6 +162,7 @@ int orc_blck_size(int type) {
     switch (type) {
         case ORC_TYPE_Q8_0: return ORC_QK8_0;
         case ORC_TYPE_Q4_K:
+        case ORC_TYPE_Q5_K:
         case ORC_TYPE_Q6_K:
         case ORC_TYPE_Q8_K: return ORC_QK_K;
         default:            return 1;
@@ -190,6 +193,16 @@ static int q4k_quant(const orc_block_q4_K * b, int e) {
     const int c = e >> 6, r = e & 63;
     const uint8_t byte = b->qs[32 * c + (r & 31)];
     return r < 32 ? (byte & 0x0f) : (byte >> 4);
+}
+
+/* Q5_K element e (0..255): the Q4_K nibble of e (qs laid out as Q4_K's) plus
+ * 16 times bit j = e/32 of qh[e%32] (dequantize_row_q5_K walks qh with one
+ * mask bit per 32-element sub-block). */
+static int q5k_quant(const orc_block_q5_K * b, int e) {
+    const int c = e >> 6, r = e & 63, l = e & 31;
+    const uint8_t byte = b->qs[32 * c + l];
+    const int     lo   = r < 32 ? (byte & 0x0f) : (byte >> 4);
+    return lo + (((b->qh[l] >> (e >> 5)) & 1) << 4);
 }
 
 /* Q6_K element e (0..255): half h = e/128, within the half quarter t = r/32,
@@ -240,6 +253,24 @@ void orc_dequantize_row(int type, const void * src, float * dst, int64_t k) {
                     for (int l = 0; l < 32; l++) {
                         const int e = 32 * j + l;
                         dst[i * ORC_QK_K + e] = d1 * (float) q4k_quant(&b[i], e) - m1;
+                    }
+                }
+            }
+            return;
+        }
+        case ORC_TYPE_Q5_K: {
+            const orc_block_q5_K * b = (const orc_block_q5_K *) src;
+            for (int64_t i = 0; i < k / ORC_QK_K; i++) {
+                const float d    = orc_fp16_to_fp32(b[i].d);
+                const float dmin = orc_fp16_to_fp32(b[i].dmin);
+                for (int j = 0; j < 8; j++) {
+                    int sc, mn;
+                    q4k_scale_min(j, b[i].scales, &sc, &mn);
+                    const float d1 = d * (float) sc;
+                    const float m1 = dmin * (float) mn;
+                    for (int l = 0; l < 32; l++) {
+                        const int e = 32 * j + l;
+                        dst[i * ORC_QK_K + e] = d1 * (float) q5k_quant(&b[i], e) - m1;
                     }
                 }
             }
@@ -352,6 +383,28 @@ float orc_vec_dot(int type, int64_t k, const void * wrow, const void * xq) {
                     int s = 0;
                     for (int l = 0; l < 32; l++) {
                         s += q4k_quant(&w[i], 32 * j + l) * (int) x[i].qs[32 * j + l];
+                    }
+                    isum += sc * s;
+                    msum += mn * ((int) x[i].bsums[2 * j] + (int) x[i].bsums[2 * j + 1]);
+                }
+                const float d    = orc_fp16_to_fp32(w[i].d) * x[i].d;
+                const float dmin = orc_fp16_to_fp32(w[i].dmin) * x[i].d;
+                sumf += d * (float) isum;
+                sumf -= dmin * (float) msum;
+            }
+            return sumf;
+        }
+        case ORC_TYPE_Q5_K: {
+            const orc_block_q5_K * w = (const orc_block_q5_K *) wrow;
+            const orc_block_q8_K * x = (const orc_block_q8_K *) xq;
+            for (int64_t i = 0; i < k / ORC_QK_K; i++) {
+                int isum = 0, msum = 0;
+                for (int j = 0; j < 8; j++) {
+                    int sc, mn;
+                    q4k_scale_min(j, w[i].scales, &sc, &mn);
+                    int s = 0;
+                    for (int l = 0; l < 32; l++) {
+                        s += q5k_quant(&w[i], 32 * j + l) * (int) x[i].qs[32 * j + l];
                     }
                     isum += sc * s;
                     msum += mn * ((int) x[i].bsums[2 * j] + (int) x[i].bsums[2 * j + 1]);

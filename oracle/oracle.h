@@ -10,7 +10,7 @@
  * .gitmodules:1-3 of the reference; its pinned commit is unknown, so every
  * ggml-internal statement below is a restatement of public upstream ggml
  * behaviour, marked [ext]):
- *   - GGUF block formats Q8_0 / Q4_K / Q6_K / Q8_K and their dequantisation
+ *   - GGUF block formats Q8_0 / Q4_K / Q5_K / Q6_K / Q8_K and their dequantisation
  *     (the weights the reference's quantizer writes, tools/quantize.cpp:40-51,
  *     :375-383, and uploads raw, src/gguf-weights.h:161-203);
  *   - ggml-CPU mul_mat semantics: activations quantized to Q8_0 (for Q8_0
@@ -41,6 +41,7 @@ enum {
     ORC_TYPE_F16  = 1,
     ORC_TYPE_Q8_0 = 8,
     ORC_TYPE_Q4_K = 12,
+    ORC_TYPE_Q5_K = 13,
     ORC_TYPE_Q6_K = 14,
     ORC_TYPE_Q8_K = 15,
     ORC_TYPE_I32  = 26,
@@ -54,6 +55,7 @@ enum {
 /* Block layouts (byte-exact GGUF layouts). */
 typedef struct { uint16_t d; int8_t qs[32]; } orc_block_q8_0;                               /* 34 B  */
 typedef struct { uint16_t d; uint16_t dmin; uint8_t scales[12]; uint8_t qs[128]; } orc_block_q4_K; /* 144 B */
+typedef struct { uint16_t d; uint16_t dmin; uint8_t scales[12]; uint8_t qh[32]; uint8_t qs[128]; } orc_block_q5_K; /* 176 B */
 typedef struct { uint8_t ql[128]; uint8_t qh[64]; int8_t scales[16]; uint16_t d; } orc_block_q6_K;  /* 210 B */
 typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } orc_block_q8_K;               /* 292 B */
 
@@ -87,7 +89,7 @@ void orc_quantize_row_q8_K(const float * x, void * y, int64_t k);
 
 /* Block dot products with ggml's generic (scalar) accumulation [ext]:
  * weight row of `type` against the activation row already quantized to the
- * matching vec_dot type (Q8_0 for Q8_0, Q8_K for Q4_K / Q6_K). */
+ * matching vec_dot type (Q8_0 for Q8_0, Q8_K for Q4_K / Q5_K / Q6_K). */
 float orc_vec_dot(int type, int64_t k, const void * wrow, const void * xq);
 
 /* mul_mat on a 2-D weight W (N rows of K elements, row stride = row_size)

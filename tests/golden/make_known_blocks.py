@@ -16,6 +16,10 @@ reference's quantizer, tools/quantize.cpp:375-383):
                the top bits of bytes j-4 / j; element e: chunk c=e//64 byte
                qs[32c + e%32], low nibble if e%64<32 else high nibble;
                                                     y = (d*sc_j)*q - dmin*m_j
+  Q5_K 176 B : f16 d, f16 dmin, u8 scales[12], u8 qh[32], u8 qs[128]
+               scales and the low 4 bits of each quant as Q4_K; the fifth
+               bit of element e is bit e//32 of qh[e%32];
+                                                    y = (d*sc_j)*q - dmin*m_j
   Q6_K 210 B : u8 ql[128], u8 qh[64], int8 sc[16], f16 d
                element e: h=e//128, t=(e%128)//32, l=e%32:
                low 4 bits in ql[64h+l+32(t&1)] (low nibble if t<2),
@@ -76,6 +80,18 @@ def q4_K_block(d_bits, dmin_bits, sc, mn, q):
     return b, exp
 
 
+def q5_K_block(d_bits, dmin_bits, sc, mn, q):
+    assert all(0 <= v < 32 for v in q)
+    b4, exp = q4_K_block(d_bits, dmin_bits, sc, mn, q)
+    # the 4-bit block holds d, dmin, scales, qs (low nibbles); splice qh in
+    qh = [0] * 32
+    for e in range(256):
+        qh[e % 32] |= ((q[e] >> 4) & 1) << (e // 32)
+    b = b4[:16] + bytes(qh) + b4[16:]
+    assert len(b) == 176
+    return b, exp
+
+
 def q6_K_block(d_bits, sc, q):
     assert len(sc) == 16 and len(q) == 256
     ql = [0] * 128
@@ -115,6 +131,13 @@ def main():
     b, e = q4_K_block(f16bits(0.0123), f16bits(0.00771), [63] * 4 + [48, 16, 32, 1],
                       [0, 63, 31, 32, 63, 15, 16, 47], [15 - (e % 16) for e in range(256)])
     blocks.append({"name": "q4_K_f16", "type": 12, "ne0": 256, "hex": b.hex(), "expected": e})
+    # Q5_K: the Q4_K fields with 5-bit quants (0..31), every qh bit position used
+    q5 = [(e * 11 + 5) % 32 for e in range(256)]
+    b, e = q5_K_block(f16bits(1.0), f16bits(0.5), sc, mn, q5)
+    blocks.append({"name": "q5_K_exact", "type": 13, "ne0": 256, "hex": b.hex(), "expected": e})
+    b, e = q5_K_block(f16bits(0.00417), f16bits(0.0213), [0, 63, 7, 40, 63, 1, 22, 9],
+                      [63, 0, 12, 63, 5, 63, 31, 0], [31 - (e % 32) for e in range(256)])
+    blocks.append({"name": "q5_K_f16", "type": 13, "ne0": 256, "hex": b.hex(), "expected": e})
     # Q6_K: d = 1, scales covering int8 extremes, quants 0..63 (values -32..31)
     sc6 = [-128, -64, -1, 0, 1, 2, 3, 7, 15, 31, 63, 64, 100, 126, 127, -100]
     q6 = [(e * 5 + 1) % 64 for e in range(256)]

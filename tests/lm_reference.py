@@ -16,6 +16,7 @@ class LmState:
         prefill); k, v: per layer f16 [n_sets, Nkv, max_seq, D]."""
         st = cls.__new__(cls)
         st.c, st.w = cfg, dict(weights)
+        st.t = {}
         st.k = [np.array(a, dtype=np.float16, copy=True) for a in k]
         st.v = [np.array(a, dtype=np.float16, copy=True) for a in v]
         return st
@@ -24,13 +25,18 @@ class LmState:
         c = lm.cfg
         self.c = c
         self.w = {}
+        self.t = {}  # GGML type of each linear weight (absent: c.wtype)
         for l in range(c.n_layers):
             for n in ("attn_norm", "q_norm", "k_norm", "ffn_norm"):
                 self.w[f"blk.{l}.{n}"] = lm.get(f"blk.{l}.{n}", np.float32)
-            for n in ("qkv", "o_proj", "gate_up", "down"):
-                self.w[f"blk.{l}.{n}"] = lm.get(f"blk.{l}.{n}")
+            for n in ("qkv", "qk", "v", "o_proj", "gate_up", "down"):
+                name = f"blk.{l}.{n}"
+                if lm.has(name):
+                    self.w[name] = lm.get(name)
+                    self.t[name] = lm.type_of(name)
         self.w["output_norm"] = lm.get("output_norm", np.float32)
         self.w["lm_head"] = lm.get("lm_head")
+        self.t["lm_head"] = lm.type_of("lm_head")
         # caches: ggml [D, max_seq, Nkv, n_sets] -> numpy [n_sets, Nkv, max_seq, D]
         self.refresh_kv(lm)
 
@@ -40,6 +46,16 @@ class LmState:
         shp = (c.n_sets, c.n_kv_heads, c.max_seq, c.head_dim)
         self.k = [lm.get(f"kv_k4_{l}", np.float16).reshape(shp).copy() for l in range(c.n_layers)]
         self.v = [lm.get(f"kv_v4_{l}", np.float16).reshape(shp).copy() for l in range(c.n_layers)]
+
+
+def _qkv(st, p, mm, x):
+    """The Q | K | V rows of the normed rows x: one fused weight, or the
+    fused Q | K weight and a separate V of another type (src/qwen3-lm.h:742-757)."""
+    c = st.c
+    q_dim, kv_dim, H = c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim, c.hidden
+    if p + "qkv" in st.w:
+        return mm(p + "qkv", q_dim + 2 * kv_dim, H, x)
+    return np.concatenate([mm(p + "qk", q_dim + kv_dim, H, x), mm(p + "v", kv_dim, H, x)], axis=1)
 
 
 def _qkv_rows(st, l, h, pos, sets_rows, mm):
@@ -52,7 +68,7 @@ def _qkv_rows(st, l, h, pos, sets_rows, mm):
     T = h.shape[0]
     p = f"blk.{l}."
     x = oracle.rms_norm_mul(h, st.w[p + "attn_norm"], c.rms_eps)
-    qkv = mm(p + "qkv", q_dim + 2 * kv_dim, H, x)
+    qkv = _qkv(st, p, mm, x)
     q = oracle.rms_norm_mul(qkv[:, :q_dim].reshape(T, Nh, D), st.w[p + "q_norm"], c.rms_eps)
     k = oracle.rms_norm_mul(qkv[:, q_dim:q_dim + kv_dim].reshape(T, Nkv, D), st.w[p + "k_norm"], c.rms_eps)
     v = qkv[:, q_dim + kv_dim:].reshape(T, Nkv, D)
@@ -75,11 +91,7 @@ def prefill(st, tokens, kv_set, kv_pos, flavour="ggml"):
     q_dim = Nh * D
     T = len(tokens)
     t = c.wtype
-
-    def mm(name, n_out, k_in, x):
-        if flavour == "ggml":
-            return oracle.mul_mat_ggml(t, st.w[name], n_out, k_in, x)
-        return oracle.mul_mat_f64(t, st.w[name], n_out, k_in, x).astype(np.float32)
+    mm = _mm_fn(st, flavour)
 
     rs = oracle.row_size(t, H)
     emb = np.asarray(st.w["embed_tokens"], np.uint8).reshape(-1, rs)
@@ -119,10 +131,10 @@ def _mm_fn(st, flavour):
     BF16 weights (type 30): ggml's BF16 dot multiplies bf16 weights by the
     activations rounded to bf16, each product exact, and sums them ("ggml":
     in f64 here, as the generic C path does), or the unrounded activations
-    ("f64")."""
-    t = st.c.wtype
+    ("f64").  Each weight in its own type (st.t; c.wtype where absent)."""
 
     def mm(name, n_out, k_in, x):
+        t = st.t.get(name, st.c.wtype)
         if t == 30:
             xr = round_bf16(x) if flavour == "ggml" else np.asarray(x, np.float32)
             return oracle.mul_mat_f64(t, st.w[name], n_out, k_in, xr).astype(np.float32)
@@ -157,7 +169,7 @@ def _decode_layer(st, l, h, sets, mm, mask, pos, n_kv_pad, flavour):
     scale = float(np.float32(1.0 / np.sqrt(D)))
     p = f"blk.{l}."
     x = oracle.rms_norm_mul(h, st.w[p + "attn_norm"], c.rms_eps)
-    qkv = mm(p + "qkv", q_dim + 2 * kv_dim, H, x)
+    qkv = _qkv(st, p, mm, x)
     q = qkv[:, :q_dim].reshape(N, Nh, D)
     k = qkv[:, q_dim:q_dim + kv_dim].reshape(N, Nkv, D)
     v = qkv[:, q_dim + kv_dim:].reshape(N, Nkv, D)

@@ -11,7 +11,7 @@ pytestmark = pytest.mark.gpu
 GOLDEN = pathlib.Path(__file__).resolve().parent / "golden" / "known_blocks.json"
 
 
-@pytest.mark.parametrize("t", [8, 12, 14])
+@pytest.mark.parametrize("t", [8, 12, 13, 14])
 @pytest.mark.parametrize("N,K", [(37, 512), (5, 4096), (64, 2304)])
 def test_repack_roundtrip_and_dequant_bit_exact(mm, orc, pkg, t, N, K):
     raw = pkg.synth.gguf_blocks_np(t, N, K, 1000 + t + K)

@@ -109,7 +109,7 @@ def test_set_rows_into_f16_cache(mm):
     assert not c.any()
 
 
-@pytest.mark.parametrize("t", [8, 12, 14])
+@pytest.mark.parametrize("t", [8, 12, 13, 14])
 def test_get_rows_quantized(mm, orc, pkg, t):
     L = mm.load()
     V, K = 50, 512
@@ -158,7 +158,7 @@ def test_rms_norm_rows(mm, orc, shape):
     assert rel_err(out.cpu().numpy(), ref) < 1e-5
 
 
-@pytest.mark.parametrize("wt", [8, 12, 14])
+@pytest.mark.parametrize("wt", [8, 12, 13, 14])
 def test_rms_norm_quant_equals_two_pass(mm, wt):
     """Fused norm + quantisation is byte-identical to norm then quantize_act."""
     L = mm.load()
@@ -270,7 +270,7 @@ def test_head_rows_v_store(mm):
     assert torch.equal(cache[0, :, 3], want[0]) and torch.equal(cache[1, :, 9], want[1])
 
 
-@pytest.mark.parametrize("wt", [8, 12, 14])
+@pytest.mark.parametrize("wt", [8, 12, 13, 14])
 def test_mul_mat_q_add(mm, pkg, wt):
     """GEMV with the residual ADD in its store equals GEMV then a separate f32 add."""
     L = mm.load()

@@ -1,4 +1,4 @@
-"""GPU: GGML_OP_MUL_MAT over Q8_0 / Q4_K / Q6_K weights against the oracle.
+"""GPU: GGML_OP_MUL_MAT over Q8_0 / Q4_K / Q5_K / Q6_K weights against the oracle.
 
 Tolerances (stated): against the ggml-CPU-semantics oracle, which quantises
 activations the same way and differs only in f32 summation order,
@@ -23,7 +23,7 @@ def run(mm, orc, pkg, t, N, K, M, seed):
     return y, orc.mul_mat_ggml(t, raw, N, K, x), orc.mul_mat_f64(t, raw, N, K, x)
 
 
-@pytest.mark.parametrize("t", [8, 12, 14])
+@pytest.mark.parametrize("t", [8, 12, 13, 14])
 @pytest.mark.parametrize("M", [1, 2, 3, 5, 8, 12, 16])
 def test_gemv_small(mm, orc, pkg, t, M):
     y, yg, yf = run(mm, orc, pkg, t, 1000, 2048, M, 2000 + 10 * t + M)
@@ -31,7 +31,7 @@ def test_gemv_small(mm, orc, pkg, t, M):
     assert cosine(y, yf) > 0.9999
 
 
-@pytest.mark.parametrize("t", [8, 12, 14])
+@pytest.mark.parametrize("t", [8, 12, 13, 14])
 @pytest.mark.parametrize("N,K", [(6144, 4096), (4096, 12288), (2048, 2304), (3, 256), (513, 1280), (256, 512),
                                  (1000, 256), (1024, 256)])
 def test_gemv_decode_shapes(mm, orc, pkg, t, N, K):
@@ -74,7 +74,7 @@ def rel_rms(a, b):
     return float(np.linalg.norm(a - b) / np.linalg.norm(b))
 
 
-@pytest.mark.parametrize("t", [8, 12, 14])
+@pytest.mark.parametrize("t", [8, 12, 13, 14])
 @pytest.mark.parametrize("N,K,M", [(384, 2048, 200), (100, 4096, 17), (130, 2048, 1380)])
 def test_gemm_shapes(mm, orc, pkg, t, N, K, M):
     y, yg, yf = run(mm, orc, pkg, t, N, K, M, 5000 + t + M)
@@ -121,7 +121,7 @@ def test_gemm_matches_gemv_semantics_closely(mm, pkg):
     assert cosine(a, b) > 0.9999
 
 
-@pytest.mark.parametrize("t", [8, 12, 14])
+@pytest.mark.parametrize("t", [8, 12, 13, 14])
 @pytest.mark.parametrize("bias,res", [(True, False), (False, True), (True, True)])
 def test_gemm_bias_add_equals_separate_ops(mm, pkg, t, bias, res):
     """mmhip_mul_mat_bias_add (the DiT's projection + bias, + residual) is
@@ -327,7 +327,8 @@ def test_gemv_q6_K_persistent_equals_wave_kernel(mm, pkg, monkeypatch, N, K, M):
 @pytest.mark.parametrize("t,N,K,M,kind", [(12, 6144, 2048, 2048, "plain"), (8, 2048, 2048, 2100, "plain"),
                                           (14, 3000, 2048, 2051, "bias_res"), (8, 2048, 8192, 2200, "bias_res"),
                                           (12, 1024, 2048, 2077, "swiglu"), (8, 16384, 2048, 2048, "swiglu"),
-                                          (8, 512, 2048, 2049, "plain")])
+                                          (8, 512, 2048, 2049, "plain"), (13, 4096, 2048, 2048, "plain"),
+                                          (13, 1024, 2048, 2077, "swiglu")])
 def test_gemm_f16_weight_copy_equals_register_path(mm, pkg, monkeypatch, t, N, K, M, kind):
     """At 2048+ tokens the GEMM first writes the weights to f16 rows
     (k_w_to_f16, the in-kernel dequantisation's arithmetic) and streams both

@@ -63,12 +63,12 @@ def np_decode(t, raw, ne0):
         d = blk[:, 0:2].copy().view(np.float16).astype(np.float32)
         q = blk[:, 2:].view(np.int8).astype(np.float32)
         return (d * q).reshape(-1)
-    if t == 12:
-        blk = raw.reshape(-1, 144)
+    if t in (12, 13):
+        blk = raw.reshape(-1, 144 if t == 12 else 176)
         d = blk[:, 0:2].copy().view(np.float16).astype(np.float32)
         dmin = blk[:, 2:4].copy().view(np.float16).astype(np.float32)
         s = blk[:, 4:16].astype(np.int32)
-        qs = blk[:, 16:].astype(np.int32)
+        qs = blk[:, 16:].astype(np.int32) if t == 12 else blk[:, 48:].astype(np.int32)
         sc = np.zeros((blk.shape[0], 8), np.int32)
         mn = np.zeros((blk.shape[0], 8), np.int32)
         sc[:, :4] = s[:, 0:4] & 63
@@ -79,6 +79,11 @@ def np_decode(t, raw, ne0):
         for c in range(4):
             q[:, 64 * c: 64 * c + 32] = qs[:, 32 * c: 32 * c + 32] & 15
             q[:, 64 * c + 32: 64 * c + 64] = qs[:, 32 * c: 32 * c + 32] >> 4
+        if t == 13:
+            # fifth bit of element e: bit e // 32 of qh[e % 32]
+            qh = blk[:, 16:48].astype(np.int32)
+            e = np.arange(256)
+            q |= ((qh[:, e % 32] >> (e // 32)) & 1) << 4
         j = np.arange(256) // 32
         d1 = (d * sc[:, j].astype(np.float32)).astype(np.float32)
         m1 = (dmin * mn[:, j].astype(np.float32)).astype(np.float32)
@@ -101,7 +106,7 @@ def np_decode(t, raw, ne0):
     raise ValueError(t)
 
 
-@pytest.mark.parametrize("t", [8, 12, 14])
+@pytest.mark.parametrize("t", [8, 12, 13, 14])
 def test_dequant_vs_independent_decoder(orc, pkg, t):
     K, N = 1024, 9
     raw = pkg.synth.gguf_blocks_np(t, N, K, 100 + t)

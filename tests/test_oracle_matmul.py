@@ -5,7 +5,7 @@ import pytest
 from conftest import cosine, rel_err
 from test_oracle_formats import np_decode
 
-TYPES = [8, 12, 14]
+TYPES = [8, 12, 13, 14]
 
 
 @pytest.mark.parametrize("t", TYPES)
