@@ -991,7 +991,9 @@ int run_node(mi_backend * c, const struct ggml_tensor * n) {
 //             slot as well.
 //   HEAD      CONT(view) -> RESHAPE -> [RMS_NORM -> MUL] -> [ROPE] -> [CONT]
 //             -> [RESHAPE -> SET_ROWS]: the per-head Q / K / V rows of the
-//             attention block in one launch.
+//             attention block in one launch; also RESHAPE(rows) -> ... ->
+//             SET_ROWS, a projection's own output (the V of the "_M" files'
+//             layers whose V weight has its own type, src/qwen3-lm.h:749-757).
 //   MM_GLU    a norm-fused gate_up GEMV MUL_MAT whose only consumer is a
 //             SwiGLU feeding Q8_0 GEMVs: the SwiGLU and its quantisation into
 //             those GEMVs' slot run in the gate_up GEMV's epilogue.
@@ -1029,6 +1031,7 @@ struct plan_step {
     bool                 write_f32 = true;
     mmhip_head_rows_args head[4]{};  // HEAD: the chains run by this step (FA_Q: the fused Q, K, V chains)
     int                  head_end[4]{ -1, -1, -1, -1 };  // the chains' last nodes
+    const struct ggml_tensor * head_in[4]{};               // the chains' source rows
     int                  n_head = 0;
 };
 
@@ -1392,8 +1395,11 @@ bool plan_small_attn(struct ggml_cgraph * g, const graph_info & gi, int i, plan_
 bool plan_head(struct ggml_cgraph * g, const graph_info & gi, int i, plan_step & st, std::vector<char> & absorbed) {
     const struct ggml_tensor * n0 = ggml_graph_node(g, i);
     const struct ggml_tensor * v  = n0->src[0];
-    if (n0->op != GGML_OP_CONT || n0->type != GGML_TYPE_F32 || v->type != GGML_TYPE_F32 || v->nb[0] != 4 ||
-        v->ne[2] != 1 || v->ne[3] != 1 || v->nb[1] % 4 != 0) {
+    // entry: CONT of a 2-D view, then RESHAPE [D, H, T]; or a RESHAPE
+    // [D, H, T] of 2-D rows (whose chain must then end in the cache write)
+    const bool from_rows = n0->op == GGML_OP_RESHAPE;
+    if (!(n0->op == GGML_OP_CONT || from_rows) || n0->type != GGML_TYPE_F32 || !v || v->type != GGML_TYPE_F32 ||
+        v->nb[0] != 4 || v->ne[2] != 1 || v->ne[3] != 1 || v->nb[1] % 4 != 0) {
         return false;
     }
     std::vector<int> chain{ i };
@@ -1403,17 +1409,22 @@ bool plan_head(struct ggml_cgraph * g, const graph_info & gi, int i, plan_step &
         }
         return gi.cons[(size_t) k];
     };
-    int j = next(i);
-    if (j < 0) {
-        return false;
+    int j = i;
+    if (!from_rows) {
+        j = next(i);
+        if (j < 0) {
+            return false;
+        }
     }
     const struct ggml_tensor * r1 = ggml_graph_node(g, j);
     const int64_t              D  = r1->ne[0], H = r1->ne[1], T = r1->ne[2];
-    if (r1->op != GGML_OP_RESHAPE || r1->src[0] != n0 || r1->ne[3] != 1 || D * H != v->ne[0] || T != v->ne[1] ||
-        !(D == 64 || D == 128 || D == 256)) {
+    if (r1->op != GGML_OP_RESHAPE || (!from_rows && r1->src[0] != n0) || r1->ne[3] != 1 || D * H != v->ne[0] ||
+        T != v->ne[1] || !(D == 64 || D == 128 || D == 256)) {
         return false;
     }
-    chain.push_back(j);
+    if (!from_rows) {
+        chain.push_back(j);
+    }
     mmhip_head_rows_args a{};
     a.src      = v->data;
     a.src_nb_h = D * 4;
@@ -1496,7 +1507,7 @@ bool plan_head(struct ggml_cgraph * g, const graph_info & gi, int i, plan_step &
             }
         }
     }
-    if (end < 0) {
+    if (end < 0 || (from_rows && !a.ids)) {
         return false;  // nothing but a copy: the plain CONT is as good
     }
     const struct ggml_tensor * e = ggml_graph_node(g, end);
@@ -1510,6 +1521,7 @@ bool plan_head(struct ggml_cgraph * g, const graph_info & gi, int i, plan_step &
     st.node    = end;
     st.head[0]     = a;
     st.head_end[0] = end;
+    st.head_in[0]  = v;
     st.n_head      = 1;
     for (int x : chain) {
         absorbed[(size_t) x] = 1;
@@ -1524,6 +1536,25 @@ bool feeds_only(struct ggml_cgraph * g, const graph_info & gi, int e, int fa, in
     }
     for (int c : gi.consumers[(size_t) e]) {
         if (c != fa && !(is_noop(ggml_graph_node(g, c)->op) && feeds_only(g, gi, c, fa, depth + 1))) {
+            return false;
+        }
+    }
+    return true;
+}
+
+// May GEMV step s run before HEAD step h?  Its output must not overlap the
+// chains' source rows or their outputs, its input rows not their outputs
+// (no fused ADD: the residual would be another operand to check).
+bool mm_commutes_with_head(struct ggml_cgraph * g, const plan_step & h, const plan_step & s) {
+    if (s.kind != ST_MM || s.add >= 0 || s.glu >= 0 || s.glu_epi >= 0) {
+        return false;
+    }
+    const struct ggml_tensor * mm = ggml_graph_node(g, s.node);
+    const struct ggml_tensor * x  = s.norm >= 0 ? ggml_graph_node(g, s.norm)->src[0] : mm->src[1];
+    for (int c = 0; c < h.n_head; c++) {
+        const struct ggml_tensor * in  = h.head_in[c];
+        const struct ggml_tensor * out = ggml_graph_node(g, h.head_end[c]);
+        if (!in || overlaps(mm, in) || overlaps(mm, out) || overlaps(x, out)) {
             return false;
         }
     }
@@ -1863,6 +1894,13 @@ graph_plan build_plan(struct ggml_cgraph * g) {
                 continue;
             }
         }
+        if (n->op == GGML_OP_RESHAPE && !absorbed[(size_t) i]) {
+            plan_step st;
+            if (plan_head(g, gi, i, st, absorbed)) {
+                add_pending(st);
+                continue;
+            }
+        }
         // LayerNorm with its weight MUL and bias ADD (dit_layer_norm): one kernel
         if (n->op == GGML_OP_NORM && gi.uses[(size_t) i] == 1 && !is_output(n) && rows_contiguous_f32(n)) {
             const int                  j  = gi.cons[(size_t) i];
@@ -2090,12 +2128,21 @@ graph_plan build_plan(struct ggml_cgraph * g) {
             plan_step m = merged[(size_t) last_head];
             for (int k = 0; k < st.n_head; k++) {
                 m.head_end[m.n_head] = st.head_end[k];
+                m.head_in[m.n_head]  = st.head_in[k];
                 m.head[m.n_head++]   = st.head[k];
             }
             m.node = st.node;
             merged.erase(merged.begin() + last_head);
             merged.push_back(m);
             last_head = (int) merged.size() - 1;
+            continue;
+        }
+        if (last_head >= 0 && st.kind == ST_MM && mm_commutes_with_head(g, merged[(size_t) last_head], st)) {
+            // a GEMV that neither reads nor writes the open HEAD step's rows
+            // (a separately typed V projection between the K and the V / Q
+            // chains) runs before it, so the chains stay one step
+            merged.insert(merged.begin() + last_head, st);
+            last_head++;
             continue;
         }
         merged.push_back(st);

@@ -734,6 +734,256 @@ __global__ __launch_bounds__(64 * PG_WAVES) void k_gemv_q6_K_pro(PgArgs a, Pg6Ac
     }
 }
 
+// Persistent Q4_K / Q5_K GEMVs (M <= 2, K = 4096 CH) with the structure of
+// k_gemv_q6_K_pro: PRO_NORM (the RMS norm and the Q8_K quantisation of the
+// activation rows in the prologue) or PRO_NONE (a copy of quantised Q8_K
+// rows into LDS).  A row is read in units of 64 elements: unit un = lane +
+// 64 u of super-block sb = un / 4 takes the chunk pair c = 2 cp, 2 cp + 1
+// (cp = un / 2 % 2) and the column half hf = un % 2, i.e. for each of the two
+// chunks the 16 low-nibble elements 256 sb + 64 c + 16 hf + i and the 16
+// high-nibble ones 32 further.  Its bytes: 32 of qs at 128 sb + 64 cp + 16 hf
+// (and + 32), Q5: the 16 qh bytes K/2 + 32 sb + 16 hf (bits 2c and 2c + 1 of
+// byte i are the fifth bits of the low and high nibble), the super-block's 12
+// scale bytes and its f16 d, dmin.  Per unit and column ggml's super-block
+// form: the integer sums of the four 16-element groups, then
+// acc += (d dx) isum - (dmin dx) msum; the lane sums reduce as store_rows
+// reduces them.
+template <int CH, bool Q5> struct Pg5Buf {
+    int4_t   q0[CH], q1[CH];
+    int4_t   qh[Q5 ? CH : 1];
+    uint32_t s0[CH], s1[CH], s2[CH], dm[CH];
+};
+
+typedef uint32_t u32x3_t __attribute__((ext_vector_type(3)));
+
+template <int CH, bool Q5, int U0 = 0, int U1 = CH>
+__device__ __forceinline__ void pg5_load(Pg5Buf<CH, Q5> & b, const PgArgs & a, int64_t row, int lane) {
+    const uint8_t *              wr    = a.W + (row < a.N ? row : a.N - 1) * a.rs;
+    const int                    K     = a.K;
+    const int                    qh_sz = Q5 ? K / 8 : 0;
+    const int                    sc_at = K / 2 + qh_sz;
+    const int                    dm_at = sc_at + 12 * (K / 256);
+    const __amdgpu_buffer_rsrc_t rr    = __builtin_amdgcn_make_buffer_rsrc((void *) wr, (short) 0,
+                                                                           dm_at + 4 * (K / 256), 0x00020000);
+    // unit lane + 64 u sits 16 super-blocks after unit lane: its offsets are
+    // the lane's plus constants
+    const int sb = lane >> 2, cp = (lane >> 1) & 1, hf = lane & 1;
+    const int oq = sb * 128 + cp * 64 + hf * 16;
+    const int oh = sb * 32 + hf * 16;
+#pragma unroll
+    for (int u = U0; u < U1; u++) {
+        b.q0[u] = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(rr, oq + 2048 * u, 0, 0));
+        b.q1[u] = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(rr, oq + 2048 * u + 32, 0, 0));
+        if constexpr (Q5) {
+            b.qh[u] = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(rr, oh + 512 * u, K / 2, 0));
+        }
+        const u32x3_t sc = __builtin_bit_cast(u32x3_t,
+                                              __builtin_amdgcn_raw_buffer_load_b96(rr, sb * 12 + 192 * u, sc_at, 0));
+        b.s0[u] = sc.x;
+        b.s1[u] = sc.y;
+        b.s2[u] = sc.z;
+        b.dm[u] = __builtin_amdgcn_raw_buffer_load_b32(rr, sb * 4 + 64 * u, dm_at, 0);
+    }
+}
+
+// The activation operands of one unit: the four 16-value groups (chunk 2cp
+// low, high, chunk 2cp + 1 low, high), their sums and the super-block scale
+template <int NC> struct Pg5X {
+    int4_t v[NC][4];
+    int    bs[NC][4];
+    float  d[NC];
+};
+
+template <int NC, int MAXK>
+__device__ __forceinline__ void pg5_x(Pg5X<NC> & x, const int8_t * sq, const float * sd, const int16_t * sb16, int un) {
+    const int sb = un >> 2, cp = (un >> 1) & 1, hf = un & 1;
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int e = sb * 256 + (2 * cp + (t >> 1)) * 64 + 32 * (t & 1) + 16 * hf;
+            x.v[c][t]   = *(const int4_t *) &sq[c * MAXK + q8k_swz(e)];
+            x.bs[c][t]  = sb16[c * (MAXK / 16) + (e >> 4)];
+        }
+        x.d[c] = sd[c * (MAXK / 256) + sb];
+    }
+}
+
+// the 4- / 5-bit values of one unit's four groups and their (scale, min):
+// pairs j = 4 cp + t, t < 4 (q4k_scale_min_w's fields, computed for both
+// halves of the scales and selected by the lane's cp without a branch)
+template <int CH, bool Q5>
+__device__ __forceinline__ void pg5_decode(const Pg5Buf<CH, Q5> & b, int u, int cp, int4_t (&q)[4], int (&sc)[4],
+                                           int (&mn)[4], float & d, float & dmin) {
+    const uint32_t w0 = b.s0[u], w1 = b.s1[u], w2 = b.s2[u];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int      lo_sc = (int) ((w0 >> (8 * t)) & 63);
+        const int      lo_mn = (int) ((w1 >> (8 * t)) & 63);
+        const uint32_t b8    = (w2 >> (8 * t)) & 0xff;
+        const int      hi_sc = (int) ((b8 & 0x0f) | (((w0 >> (8 * t + 6)) & 3) << 4));
+        const int      hi_mn = (int) ((b8 >> 4) | (((w1 >> (8 * t + 6)) & 3) << 4));
+        sc[t]                = cp ? hi_sc : lo_sc;
+        mn[t]                = cp ? hi_mn : lo_mn;
+    }
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int4_t w = k ? b.q1[u] : b.q0[u];
+        const int    c = 2 * cp + k;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            int lo = w[i] & 0x0F0F0F0F;
+            int hi = (w[i] >> 4) & 0x0F0F0F0F;
+            if constexpr (Q5) {
+                lo |= ((b.qh[u][i] >> (2 * c)) & 0x01010101) << 4;
+                hi |= ((b.qh[u][i] >> (2 * c + 1)) & 0x01010101) << 4;
+            }
+            q[2 * k][i]     = lo;
+            q[2 * k + 1][i] = hi;
+        }
+    }
+    d    = h2f((uint16_t) (b.dm[u] & 0xffff));
+    dmin = h2f((uint16_t) (b.dm[u] >> 16));
+}
+
+// column c's share of one unit
+__device__ __forceinline__ void pg5_col(const int4_t (&q)[4], const int (&sc)[4], const int (&mn)[4], float d,
+                                        float dmin, const int4_t (&xv)[4], const int (&bs)[4], float dx, float & acc) {
+    int isum = 0, msum = 0;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        isum += sc[t] * dot16(q[t], xv[t]);
+        msum += mn[t] * bs[t];
+    }
+    acc += (d * dx) * (float) isum - (dmin * dx) * (float) msum;
+}
+
+template <int NC, int CH, int PRO, bool Q5>
+__global__ __launch_bounds__(64 * PG_WAVES) void k_gemv_q45_K_pro(PgArgs a, Pg6Act xa) {
+    static_assert(PRO == PRO_NORM || PRO == PRO_NONE, "Q4_K / Q5_K: norm or quantised-row prologue");
+    constexpr int  MAXK = 4096 * CH;
+    constexpr int  J    = MAXK / (256 * PG_WAVES);
+    constexpr bool DB   = CH == 1;
+    __shared__ __attribute__((aligned(16))) int8_t s_q[NC * MAXK];
+    __shared__ float   s_d[NC * MAXK / 256];
+    __shared__ int16_t s_bs[NC * MAXK / 16];
+    __shared__ double  s_ss[NC][PG_WAVES];
+    const int     lane = threadIdx.x & 63;
+    const int     wv   = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t gw   = (int64_t) blockIdx.x * PG_WAVES + wv;
+    const int64_t TW   = (int64_t) gridDim.x * PG_WAVES;
+    const int     K    = a.K;
+    // 1. activations (or the quantised rows), then the first weight rows
+    float4_t xv[J][NC], xw[J][1];
+    if constexpr (PRO == PRO_NORM) {
+#pragma unroll
+        for (int j = 0; j < J; j++) {
+            const unsigned e = min(4u * threadIdx.x + 256u * PG_WAVES * j, (unsigned) K - 4u);
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                xv[j][c] = *(const float4_t *) (a.x + c * a.ldx + e);
+            }
+            xw[j][0] = *(const float4_t *) (a.nw + e);
+        }
+    } else {
+        for (int i = threadIdx.x; i < NC * K / 16; i += 64 * PG_WAVES) {
+            const int c = i / (K / 16), o = i % (K / 16);
+            *(int4_t *) &s_q[c * MAXK + q8k_swz(16 * o)] = *(const int4_t *) (xa.qs + (int64_t) c * K + 16 * o);
+            s_bs[c * (MAXK / 16) + o]                    = xa.bs[(int64_t) c * (K / 16) + o];
+        }
+        for (int i = threadIdx.x; i < NC * K / 256; i += 64 * PG_WAVES) {
+            const int c = i / (K / 256), o = i % (K / 256);
+            s_d[c * (MAXK / 256) + o] = xa.d[(int64_t) c * (K / 256) + o];
+        }
+    }
+    Pg5Buf<CH, Q5>          ba;
+    Pg5Buf<DB ? CH : 1, Q5> bb;
+    pg5_load<CH, Q5>(ba, a, gw, lane);
+    if constexpr (DB) {
+        if constexpr (PRO == PRO_NORM) {
+            // the second row once the activations are in (loads return in order)
+#pragma unroll
+            for (int j = 0; j < J; j++) {
+#pragma unroll
+                for (int c = 0; c < NC; c++) {
+                    asm volatile("" ::"v"(xv[j][c][0]), "v"(xw[j][0][0]) : "memory");
+                }
+            }
+        }
+        pg5_load<CH, Q5>(bb, a, TW + gw, lane);
+    }
+    // 2. the activation values, quantised into LDS
+    if constexpr (PRO == PRO_NORM) {
+        pg_prologue<NC, J, MAXK, PRO, TYPE_Q8_K>(xv, xw, s_q, s_d, s_ss, a, lane, wv, K, s_bs);
+    }
+    __syncthreads();
+    // 3. stream the rows
+    const int nit = a.nit;
+    const int cp  = (lane >> 1) & 1;
+    if constexpr (DB) {
+        Pg5X<NC> x;
+        pg5_x<NC, MAXK>(x, s_q, s_d, s_bs, lane);
+        auto dot = [&](const Pg5Buf<CH, Q5> & b, int64_t row) {
+            float acc[1][NC];
+            int4_t q[4];
+            int    sc[4], mn[4];
+            float  d, dmin;
+            pg5_decode<CH, Q5>(b, 0, cp, q, sc, mn, d, dmin);
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                acc[0][c] = 0.0f;
+                pg5_col(q, sc, mn, d, dmin, x.v[c], x.bs[c], x.d[c], acc[0][c]);
+            }
+            store_rows<NC, 1>(acc, lane, row, a.N, a.y, a.ldy, a.res, a.ldr);
+        };
+        int it = 0;
+        for (; it + 2 < nit; it += 2) {
+            dot(ba, it * TW + gw);
+            pg5_load<CH, Q5>(ba, a, (it + 2) * TW + gw, lane);
+            dot(bb, (it + 1) * TW + gw);
+            pg5_load<CH, Q5>(bb, a, (it + 3) * TW + gw, lane);
+        }
+        dot(ba, it * TW + gw);
+        if (it + 1 < nit) {
+            dot(bb, (it + 1) * TW + gw);
+        }
+    } else {
+        // one buffer: the next row's loads after the current row is reduced;
+        // the activation operands one column at a time from LDS (an opaque
+        // zero added to their indices keeps the reads inside the row loop:
+        // hoisted, they would not fit in registers beside the row)
+        for (int it = 0;;) {
+            float acc[1][NC];
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                acc[0][c] = 0.0f;
+            }
+            int off = 0;
+            asm volatile("" : "+v"(off));
+#pragma unroll
+            for (int u = 0; u < CH; u++) {
+                int4_t q[4];
+                int    sc[4], mn[4];
+                float  d, dmin;
+                pg5_decode<CH, Q5>(ba, u, cp, q, sc, mn, d, dmin);
+#pragma unroll
+                for (int c = 0; c < NC; c++) {
+                    Pg5X<1> x;
+                    pg5_x<1, MAXK>(x, s_q + c * MAXK + off, s_d + c * (MAXK / 256) + off, s_bs + c * (MAXK / 16) + off,
+                                   lane + 64 * u);
+                    pg5_col(q, sc, mn, d, dmin, x.v[0], x.bs[0], x.d[0], acc[0][c]);
+                    __builtin_amdgcn_sched_barrier(0);  // bounds the LDS operands in flight (registers)
+                }
+            }
+            store_rows<NC, 1>(acc, lane, it * TW + gw, a.N, a.y, a.ldy, a.res, a.ldr);
+            if (++it >= nit) {
+                break;
+            }
+            pg5_load<CH, Q5>(ba, a, it * TW + gw, lane);
+        }
+    }
+}
+
 // MUL_MAT of Q8_0 weights against 9..16 activation columns already
 // quantised (the depth decoder's projections at S x CFG = 16 tokens,
 // src/depth-decoder.h:206-257): one 16-wave workgroup per CU copies the
@@ -1585,6 +1835,9 @@ __global__ __launch_bounds__(256) void k_gemv_bf16(const uint16_t * __restrict__
 static int gemv_wide(const uint8_t * W, int64_t N, int64_t K, int64_t rs, const ActPtrs & x, int64_t M, float * y,
                      int64_t ldy, hipStream_t stream, const float * r, int64_t ldr);
 
+static bool gemv_q45_pro_ok(int64_t K, int64_t M, int64_t rs, const void * W);
+static int  gemv_q45_pro(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const ActPtrs & x, int64_t M,
+                         float * y, int64_t ldy, hipStream_t stream, const float * r, int64_t ldr);
 static bool gemv_q6_pro_ok(int64_t K, int64_t M, int64_t rs, const void * W);
 static int  gemv_q6_pro(const void * W, int64_t N, int64_t K, int64_t rs, const ActPtrs & x, int64_t M, float * y,
                         int64_t ldy, hipStream_t stream, const float * r, int64_t ldr);
@@ -1597,6 +1850,10 @@ int gemv_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const Ac
     }
     if (wtype == TYPE_Q6_K && gemv_q6_pro_ok(K, M, rs, W) && getenv("GGML_MI355X_DISABLE_Q6_PRO") == nullptr) {
         return gemv_q6_pro(W, N, K, rs, x, M, y, ldy, stream, r, ldr);
+    }
+    if ((wtype == TYPE_Q4_K || wtype == TYPE_Q5_K) && gemv_q45_pro_ok(K, M, rs, W) &&
+        getenv("GGML_MI355X_DISABLE_Q45_PRO") == nullptr) {
+        return gemv_q45_pro(wtype, W, N, K, rs, x, M, y, ldy, stream, r, ldr);
     }
     const uint8_t * wb = (const uint8_t *) W;
     // the int8-MFMA GEMV at 9..16 columns, and at 3..8 columns for rows longer
@@ -2049,8 +2306,69 @@ static int gemv_q6_pro(const void * W, int64_t N, int64_t K, int64_t rs, const A
     return M == 1 ? launch_pro6<1, 3, PRO_NONE>(a, xa, stream, what) : launch_pro6<2, 3, PRO_NONE>(a, xa, stream, what);
 }
 
+template <int NC, int CH, int PRO, bool Q5>
+static int launch_pro45(PgArgs a, Pg6Act xa, hipStream_t stream, const char * what) {
+    const int64_t need = (a.N + PG_WAVES - 1) / PG_WAVES;
+    const int64_t nit  = (need + pg_cus() - 1) / pg_cus();
+    const int64_t wgs  = (need + nit - 1) / nit;
+    if (nit > 0x7fffffff) {
+        return set_error(MMHIP_ERR_UNSUPPORTED, "%s: N=%lld too large", what, (long long) a.N);
+    }
+    a.nit     = (int) nit;
+    auto kern = k_gemv_q45_K_pro<NC, CH, PRO, Q5>;
+    hipLaunchKernelGGL(kern, dim3((unsigned) wgs), dim3(64 * PG_WAVES), 0, stream, a, xa);
+    return check_launch(what);
+}
+
+template <int NC, int PRO>
+static int launch_pro45_k(int type, const PgArgs & a, const Pg6Act & xa, hipStream_t stream, const char * what) {
+    const bool q5 = type == TYPE_Q5_K;
+    switch (a.K / 4096) {
+        case 1: return q5 ? launch_pro45<NC, 1, PRO, true>(a, xa, stream, what)
+                          : launch_pro45<NC, 1, PRO, false>(a, xa, stream, what);
+        case 2:
+            if constexpr (PRO == PRO_NONE) {
+                return q5 ? launch_pro45<NC, 2, PRO, true>(a, xa, stream, what)
+                          : launch_pro45<NC, 2, PRO, false>(a, xa, stream, what);
+            }
+            break;
+        case 3:
+            if constexpr (PRO == PRO_NONE) {
+                return q5 ? launch_pro45<NC, 3, PRO, true>(a, xa, stream, what)
+                          : launch_pro45<NC, 3, PRO, false>(a, xa, stream, what);
+            }
+            break;
+        default: break;
+    }
+    return set_error(MMHIP_ERR_UNSUPPORTED, "%s: K=%d", what, a.K);
+}
+
+// Q4_K / Q5_K GEMV on quantised activations (M <= 2, K = 4096, 8192 or 12288)
+// through the persistent kernel: the Q8_K rows copied into LDS once per
+// workgroup instead of re-read per wave
+static bool gemv_q45_pro_ok(int64_t K, int64_t M, int64_t rs, const void * W) {
+    return M >= 1 && M <= 2 && K % 4096 == 0 && K <= 12288 && rs % 16 == 0 && ((uintptr_t) W) % 16 == 0;
+}
+
+static int gemv_q45_pro(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const ActPtrs & x, int64_t M,
+                        float * y, int64_t ldy, hipStream_t stream, const float * r, int64_t ldr) {
+    const PgArgs a{ (const uint8_t *) W, N, (int) K, rs, nullptr, 0, nullptr, 0, nullptr, 0.0f, nullptr, y, ldy, r,
+                    ldr, 1 };
+    const Pg6Act xa{ x.qs, x.d, x.bs };
+    return M == 1 ? launch_pro45_k<1, PRO_NONE>(wtype, a, xa, stream, "gemv q4_K / q5_K")
+                  : launch_pro45_k<2, PRO_NONE>(wtype, a, xa, stream, "gemv q4_K / q5_K");
+}
+
 template <int PRO>
 static int dispatch_pro(int type, const PgArgs & a, int64_t M, hipStream_t stream, const char * what) {
+    if (type == TYPE_Q4_K || type == TYPE_Q5_K) {
+        if constexpr (PRO == PRO_NORM) {
+            const Pg6Act xa{};
+            return M == 1 ? launch_pro45_k<1, PRO>(type, a, xa, stream, what)
+                          : launch_pro45_k<2, PRO>(type, a, xa, stream, what);
+        }
+        return set_error(MMHIP_ERR_UNSUPPORTED, "%s: type %d", what, type);
+    }
     if (type == TYPE_Q6_K) {
         const Pg6Act xa{};
         if (a.K <= 4096) {
@@ -2074,13 +2392,15 @@ static bool pro_supported(int pro, int type, int64_t N, int64_t K, int64_t M) {
     // Q6_K SwiGLU prologue at K <= 4096 only: over the FFN's 12288 the
     // gate / up reads of every workgroup (196 KB each at M = 2) cost more
     // than the separate SwiGLU + quantisation pass they replace
-    return (type == TYPE_Q8_0 || (type == TYPE_Q6_K && K % 2048 == 0 && (pro == PRO_NORM || K <= 4096))) && N > 0 &&
+    // Q4_K / Q5_K: the RMS norm over K = 4096 rows
+    return (type == TYPE_Q8_0 || (type == TYPE_Q6_K && K % 2048 == 0 && (pro == PRO_NORM || K <= 4096)) ||
+            ((type == TYPE_Q4_K || type == TYPE_Q5_K) && pro == PRO_NORM && K == 4096)) && N > 0 &&
            M >= 1 && M <= 2 && K >= 256 && K <= (pro == PRO_NORM ? 4096 : 12288) && K % 256 == 0;
 }
 
-// the 16-byte row loads of the persistent Q6_K GEMV
+// the 16-byte row loads of the persistent Q4_K / Q5_K / Q6_K GEMVs
 static bool pro_rows_ok(int type, int64_t rs, const void * W) {
-    return type != TYPE_Q6_K || (rs % 16 == 0 && ((uintptr_t) W) % 16 == 0);
+    return type == TYPE_Q8_0 || (rs % 16 == 0 && ((uintptr_t) W) % 16 == 0);
 }
 }  // namespace mmhip
 

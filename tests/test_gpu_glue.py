@@ -413,13 +413,18 @@ def test_flash_attn_head_rejects_prefill_shapes(mm):
                                           (8, 2, 4096, 30000, 4096), (8, 1, 256, 77, 320), (8, 2, 1024, 70001, 1024),
                                           (14, 2, 4096, 6144, 4096), (14, 1, 2048, 300, 2112),
                                           (14, 2, 4096, 30000, 4096), (14, 2, 2048, 9001, 2048),
-                                          (14, 2, 4096, 24576, 4096)])
+                                          (14, 2, 4096, 24576, 4096), (13, 2, 4096, 6144, 4096),
+                                          (13, 1, 4096, 300, 4160), (13, 2, 4096, 30000, 4096),
+                                          (13, 2, 4096, 24576, 4096), (12, 2, 4096, 9001, 4096),
+                                          (12, 1, 4096, 5120, 4096)])
 def test_rms_norm_mul_mat_equals_two_pass(mm, pkg, wt, M, K, N, ldx):
     """GEMV with the RMS norm + quantisation in its prologue is bit-identical
     to rms_norm_quant then mul_mat_q (and mul_mat_q_add with a residual);
     N from one to eight row iterations of the persistent grid, odd tails.
-    Q8_0 weights (Q8_0 activation blocks) and Q6_K weights (Q8_K
-    super-blocks, the persistent Q6_K kernel)."""
+    Q8_0 weights (Q8_0 activation blocks), Q6_K weights (Q8_K super-blocks,
+    the persistent Q6_K kernel) and Q5_K / Q4_K weights (Q8_K, the
+    persistent Q4_K / Q5_K kernel, whose quantised-row form mul_mat_q takes
+    at 1-2 columns)."""
     L = mm.load()
     Wq = mm.QuantWeight.from_gguf(wt, pkg.synth.gguf_blocks_np(wt, N, K, 5), N, K)
     rng = np.random.default_rng(26)
@@ -452,7 +457,8 @@ def test_rms_norm_mul_mat_rejects_unsupported(mm):
     L = mm.load()
     assert L.mmhip_rms_norm_mul_mat_supported(8, 4096, 4352, 2) == 0   # K > 4096
     assert L.mmhip_rms_norm_mul_mat_supported(8, 4096, 4096, 3) == 0   # M > 2
-    assert L.mmhip_rms_norm_mul_mat_supported(12, 4096, 4096, 2) == 0  # Q4_K weights
+    assert L.mmhip_rms_norm_mul_mat_supported(12, 4096, 2048, 2) == 0  # Q4_K / Q5_K: K = 4096 only
+    assert L.mmhip_rms_norm_mul_mat_supported(13, 4096, 8192, 2) == 0
     assert L.mmhip_rms_norm_mul_mat_supported(14, 4096, 1024, 2) == 0  # Q6_K rows not 16-byte sized
     assert L.mmhip_rms_norm_mul_mat_supported(8, 4096, 1000, 2) == 0   # K % 256
     dummy = torch.zeros(16, dtype=torch.float32, device="cuda")

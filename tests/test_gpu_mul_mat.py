@@ -324,6 +324,30 @@ def test_gemv_q6_K_persistent_equals_wave_kernel(mm, pkg, monkeypatch, N, K, M):
     assert torch.isfinite(outs[0][0]).all()
 
 
+@pytest.mark.parametrize("t", [12, 13])
+@pytest.mark.parametrize("N,K", [(6144, 4096), (4097, 4096), (37, 8192), (4096, 12288), (5000, 12288), (151, 4096)])
+@pytest.mark.parametrize("M", [1, 2])
+def test_gemv_q45_persistent(mm, orc, pkg, monkeypatch, t, N, K, M):
+    """Q4_K / Q5_K at 1-2 columns and K = 4096 / 8192 / 12288 take the
+    persistent kernel (the quantised Q8_K rows copied into LDS once per
+    workgroup, 64-element units per lane, two rows in flight at K = 4096):
+    within the ggml-semantics oracle's 2e-5, and within 1e-5 of the
+    one-wave-per-row-pair kernel (GGML_MI355X_DISABLE_Q45_PRO), which sums in
+    another order; ragged N (one to several rows per wave)."""
+    raw = pkg.synth.gguf_blocks_np(t, N, K, 7100 + t + K + M)
+    x = pkg.synth.normal_np((M, K), 7200 + M)
+    W = mm.QuantWeight.from_gguf(t, raw, N, K)
+    xt = torch.from_numpy(x).cuda()
+    y = mm.mul_mat(W, xt).cpu().numpy()
+    monkeypatch.setenv("GGML_MI355X_DISABLE_Q45_PRO", "1")
+    yp = mm.mul_mat(W, xt).cpu().numpy()
+    monkeypatch.delenv("GGML_MI355X_DISABLE_Q45_PRO")
+    yg = orc.mul_mat_ggml(t, raw, N, K, x)
+    assert rel_err(y, yg) < 2e-5
+    assert rel_err(y, yp) < 1e-5
+    assert np.isfinite(y).all()
+
+
 @pytest.mark.parametrize("t,N,K,M,kind", [(12, 6144, 2048, 2048, "plain"), (8, 2048, 2048, 2100, "plain"),
                                           (14, 3000, 2048, 2051, "bias_res"), (8, 2048, 8192, 2200, "bias_res"),
                                           (12, 1024, 2048, 2077, "swiglu"), (8, 16384, 2048, 2048, "swiglu"),
