@@ -964,36 +964,40 @@ def lm_dominant_kernel(torch, pkg, cfg):
 
 
 def lm_dominant_kernel_gemv(torch, pkg, cfg):
-    """The step's largest kernel alone where no fused form exists (Q5_K): the
-    gate_up GEMV (W [2 ffn x hidden], 2 columns) on activations already
-    quantised to Q8_K, six weight copies (415 MB) rotating past the 256 MB
-    Infinity Cache, replayed as a HIP graph."""
+    """The Q5_K_M step's largest kernel alone: the gate_up GEMV with the RMS
+    norm and the Q8_K quantisation in its prologue (W [2 ffn x hidden] Q5_K,
+    2 columns; the step's SwiGLU is a separate quantising pass), six weight
+    copies (415 MB) rotating past the 256 MB Infinity Cache, replayed as a
+    HIP graph."""
     mm, synth = pkg.mmhip, pkg.synth
     N, K, M = 2 * cfg["ffn"], cfg["hidden"], 2
     wt = cfg["wtype"]
     copies = 6
     L = mm.load()
+    if not L.mmhip_rms_norm_mul_mat_supported(wt, N, K, M):
+        return None
     Ws = [mm.QuantWeight.from_gguf(wt, synth.gguf_blocks_torch(wt, N, K, 2201 + c), N, K) for c in range(copies)]
     x = torch.from_numpy(synth.normal_np((M, K), 2211)).cuda()
-    xq = mm.quantize_act(wt, x)
+    nw = torch.ones(K, device="cuda")
     y = torch.empty((M, N), device="cuda")
 
     def launch(i, st):
         W = Ws[i % copies]
-        rc = L.mmhip_mul_mat_q(wt, ctypes.c_void_p(W.data.data_ptr()), N, K, W.row_bytes,
-                               ctypes.c_void_p(xq.data_ptr()), M, ctypes.c_void_p(y.data_ptr()), N, st)
+        rc = L.mmhip_rms_norm_mul_mat(wt, ctypes.c_void_p(W.data.data_ptr()), N, K, W.row_bytes,
+                                      ctypes.c_void_p(x.data_ptr()), K, M, ctypes.c_void_p(nw.data_ptr()), 1e-6, None,
+                                      None, 0, ctypes.c_void_p(y.data_ptr()), N, st)
         assert rc == 0, L.mmhip_last_error()
 
     avg_s, min_s = graph_time(torch, launch, 36)
-    # weights + the Q8_K activations (int8 + f32 scales + int16 block sums) + y
-    alg_bytes = Ws[0].data.numel() + M * K + M * (K // 256) * 4 + M * (K // 16) * 2 + M * N * 4
+    # weights + x + norm weight + y
+    alg_bytes = Ws[0].data.numel() + M * K * 4 + K * 4 + M * N * 4
     achieved = alg_bytes / avg_s / 1e9
     del Ws
     torch.cuda.empty_cache()
-    return {"bound": "hbm", "kernel": "k_gemv_q4_K<2,2,2,Q5>: gate_up GEMV %d x %d Q5_K on Q8_K activations, "
+    return {"bound": "hbm", "kernel": "k_gemv_q45_K_pro<2,1,PRO_NORM,Q5>: RMS norm + gate_up GEMV %d x %d Q5_K, "
                                       "2 columns (the Q5_K_M step's largest kernel)" % (N, K),
             "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profile_traffic("lm_decode_q5_k_m_kv4096"),
             "avg_launch_us": round(avg_s * 1e6, 3), "min_launch_us": round(min_s * 1e6, 3),
             "alg_bytes_per_launch": alg_bytes}
 
