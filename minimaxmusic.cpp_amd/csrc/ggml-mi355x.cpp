@@ -2100,7 +2100,10 @@ graph_plan build_plan(struct ggml_cgraph * g) {
                     st.src         = -1;
                 }
             }
-            if (st.slot_in >= 0 || st.add >= 0 || st.norm >= 0 || st.glu >= 0) {
+            // (a BF16 GEMV without a fusion too: the persistent decode kernel
+            // streams the rows faster than the node's plain BF16 GEMV, e.g.
+            // the lm_head behind the final norm, whose rows are a graph output)
+            if (st.slot_in >= 0 || st.add >= 0 || st.norm >= 0 || st.glu >= 0 || mm_is_bf16_dec(n)) {
                 absorbed[(size_t) i] = 1;
                 add_pending(st);
                 continue;
