@@ -647,30 +647,40 @@ __global__ __launch_bounds__(512, 2) void k_fa_dma(FaArgs a, const int * __restr
         }
         const float m_used = m;
         float       rs     = 0.0f;
-        half8_t     av[3], ak[3];
+        // operands three MFMA steps ahead; the scheduling barrier keeps each
+        // step's LDS reads above it (left alone, the scheduler sank them to
+        // just before their MFMA, reusing one register set, so every MFMA
+        // waited out a whole LDS read).  Masked: nothing crosses it (the
+        // lone long-row waves of a causal workgroup: 50.1 -> 44.8 us at B = 2,
+        // S = 1024); unmasked: ALU, MFMA and transcendental work may
+        // (the DiT shape: 295 -> 291 us)
+        half8_t     av[4], ak[4];
         if constexpr (do_pv) {
             av[0] = pv_op(u - US, 0);
             av[1] = pv_op(u - US, 1);
+            av[2] = pv_op(u - US, 2);
         }
         if constexpr (do_qk) {
             ak[0] = qk_op(u + US, 0);
             ak[1] = qk_op(u + US, 1);
+            ak[2] = qk_op(u + US, 2);
         }
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            if (i + 2 < 8) {
+            if (i + 3 < 8) {
                 if constexpr (do_pv) {
-                    av[(i + 2) % 3] = pv_op(u - US, i + 2);
+                    av[(i + 3) % 4] = pv_op(u - US, i + 3);
                 }
                 if constexpr (do_qk) {
-                    ak[(i + 2) % 3] = qk_op(u + US, i + 2);
+                    ak[(i + 3) % 4] = qk_op(u + US, i + 3);
                 }
             }
+            __builtin_amdgcn_sched_barrier(MASK ? 0 : 0x040F);
             if constexpr (do_pv) {
-                oacc[i & 3] = mfma32(av[i % 3], pp[i >> 2], oacc[i & 3]);
+                oacc[i & 3] = mfma32(av[i % 4], pp[i >> 2], oacc[i & 3]);
             }
             if constexpr (do_qk) {
-                sn = mfma32(ak[i % 3], qreg[i], i == 0 ? negm : sn);
+                sn = mfma32(ak[i % 4], qreg[i], i == 0 ? negm : sn);
             }
             if constexpr (do_sm) {
                 const int     r  = 2 * i;
