@@ -219,9 +219,9 @@ __device__ __forceinline__ int swz32(int r, int c) {
 // GLU: the N = 2 F weight rows are the value and gate halves of a SwiGLU
 // (swiglu_split(gate, value) over the two halves of the product, with the
 // bias ADD before it).  A tile then covers BT / 2 SwiGLU columns j: in each
-// wave's 64 rows, block 0 holds value rows and block 1 the gate rows of the
-// same 32 columns, so the accumulators of a (value, gate) pair sit in the
-// same lane and register.  The epilogue adds both biases, forms
+// wave's NB blocks of 32 rows, block 2p holds value rows and block 2p + 1 the
+// gate rows of the same 32 columns, so the accumulators of a (value, gate)
+// pair sit in the same lane and register.  The epilogue adds both biases, forms
 // silu(g) * v with k_swiglu's arithmetic and stores the SwiGLU rows [M, F]
 // in f32 and / or f16 (the next GEMM's activation format).
 //
@@ -232,16 +232,25 @@ __device__ __forceinline__ int swz32(int r, int c) {
 // run in the same k order, so the sums are the register-staged kernel's to the
 // bit).  WT = TYPE_BF16: BF16 weight rows as stored, bf16 activations, the
 // bf16 MFMA.
+//
+// WIDE (WH, NW = 4, BM = 256): 256 x 256 tiles on four waves, one per SIMD,
+// each computing 128 x 128 (256 accumulators, in the AGPRs).  With no second
+// wave on the SIMD to cover LDS latency, the operands of step ks + 1 are read
+// into a second register set while the MFMAs of step ks run, and this
+// thread's DMA instructions for step ks + 3 sit between those reads, so the
+// MFMA pipe never waits on an LDS read or a DMA issue.  Per K step a wave
+// reads (128 + 128) rows from LDS where the eight-wave layout read
+// (128 + 64) rows per wave, a third less LDS traffic per MFMA.
 constexpr int GM_NS = 4;
 
-template <int WT, int NW, int WM, int BK, int BM, bool GLU, bool WH = false>
+template <int WT, int NW, int WM, int BK, int BM, bool GLU, bool WH = false, bool WIDE = false>
 __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__ W, int64_t N, int64_t K, int64_t rs,
                                                      const _Float16 * __restrict__ xh, int64_t M,
                                                      const float * __restrict__ bias, const float * res, int64_t ldr,
                                                      float * y, int64_t ldy, GemmGlu glu, GemmMulti mul,
                                                      GemmSplit spl, int64_t n_ntiles, int64_t n_tiles) {
 #pragma clang fp contract(off)
-    constexpr int BT  = 32 * NW;       // weight rows per tile (thread t stages row t / 2)
+    constexpr int BT  = WIDE ? 256 : 32 * NW;  // weight rows per tile (thread t stages row t / 2)
     constexpr int T   = NW * 64;
     constexpr int WN  = NW / WM;
     constexpr int MB  = BM / WM / 32;
@@ -253,7 +262,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
     constexpr int TIL = BT * BK;       // halves per weight tile
     static_assert(MB >= 1 && XI >= 1, "tile shape");
     static_assert(!WH || BK == 32, "the f16-weight ring steps 32 columns");
-    static_assert(!GLU || NB == 2, "GLU tiles pair one value and one gate block per wave");
+    static_assert(!GLU || NB % 2 == 0, "GLU tiles pair value and gate blocks in each wave");
+    static_assert(!WIDE || (WH && NW == 4 && BM == 256), "the wide tiles run on the DMA ring, four waves");
     extern __shared__ __attribute__((aligned(16))) _Float16 g_lds[];
     _Float16 * sX = g_lds;            // 2 stages
     _Float16 * sW = g_lds + 2 * TIX;  // 2 buffers
@@ -328,9 +338,9 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
         if constexpr (GLU) {
             // local row (wave block, value / gate, 32-row offset) -> SwiGLU column j
             const int     wq = r / (BT / WN), blk = (r % (BT / WN)) / 32;
-            const int64_t j  = n0 / 2 + wq * 32 + (r % 32);
+            const int64_t j  = n0 / 2 + wq * (BT / WN / 2) + (blk / 2) * 32 + (r % 32);
             valid            = j < glu.F;
-            return (blk == 1) != (glu.swapped != 0) ? glu.F + j : j;
+            return (blk & 1) != (glu.swapped != 0) ? glu.F + j : j;
         } else {
             valid = n0 + r < N;
             return n0 + r;
@@ -455,6 +465,97 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
                 }
             }
         };
+        if constexpr (WIDE) {
+        constexpr int KK = BK / 16;
+        half8_t ra0[KK][MB], rb0[KK][NB], ra1[KK][MB], rb1[KK][NB];
+        auto mf = [&](const half8_t (&a)[KK][MB], const half8_t (&b)[KK][NB]) {
+#pragma unroll
+            for (int kk = 0; kk < KK; kk++) {
+#pragma unroll
+                for (int i = 0; i < MB; i++) {
+#pragma unroll
+                    for (int j = 0; j < NB; j++) {
+                        if constexpr (WT == TYPE_BF16) {
+                            acc[i][j] = gm_mfma_bf16(a[kk][i], b[kk][j], acc[i][j]);
+                        } else {
+                            acc[i][j] = gm_mfma(a[kk][i], b[kk][j], acc[i][j]);
+                        }
+                    }
+                }
+            }
+        };
+        // the operand reads of the step in stage sr, with this thread's DMA
+        // of columns kd into stage sd spread between them (one instruction
+        // every SP reads)
+        auto rd = [&](half8_t (&a)[KK][MB], half8_t (&b)[KK][NB], int sr, auto dma_c, int sd, int kd) {
+            constexpr bool D  = decltype(dma_c)::value;
+            constexpr int  SP = KK * (MB + NB) / PER;
+            static_assert(SP >= 1 && KK * (MB + NB) % PER == 0, "DMA spread");
+            const _Float16 * bx = g_lds + sr * STG;
+            const _Float16 * bw = bx + TIX;
+#pragma unroll
+            for (int g = 0; g < KK * (MB + NB); g++) {
+                const int kk = g / (MB + NB), e = g % (MB + NB);
+                if (e < MB) {
+                    a[kk][e] = *(const half8_t *) &bx[swz32(wm * (BM / WM) + e * 32 + lq, 2 * kk + hh)];
+                } else {
+                    b[kk][e - MB] = *(const half8_t *) &bw[swz32(wn * (BT / WN) + (e - MB) * 32 + lq, 2 * kk + hh)];
+                }
+                if constexpr (D) {
+                    if (g % SP == 0) {
+                        const int d = g / SP;
+                        if (d < XI) {
+                            dma16(xs[d] + kd, lds_x + 2u * (uint32_t) (sd * STG + (wave_s * XI + d) * 512));
+                        } else {
+                            dma16(wsrc[d - XI] + kd,
+                                  lds_x + 2u * (uint32_t) (sd * STG + TIX + (wave_s * WI + d - XI) * 512));
+                        }
+                    }
+                }
+            }
+        };
+        // every DMA runs, past the last step on the last step's columns into a
+        // stage no step reads, so that the waits below count a fixed number
+        // of instructions
+#pragma unroll
+        for (int st = 0; st < GM_NS - 1; st++) {
+            dma2(st, kb + min(st, nk - 1) * BK);
+        }
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((GM_NS - 2) * PER) : "memory");
+        __syncthreads();
+        rd(ra0, rb0, 0, std::false_type{}, 0, 0);
+        auto step = [&](auto cur_c, int ks) {
+            // this thread's DMA of step ks + 1 in; the barrier publishes every
+            // thread's and retires all reads of the stage the next DMA fills
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PER) : "memory");
+            __syncthreads();
+            __builtin_amdgcn_sched_barrier(0);
+            const int sd = (ks + GM_NS - 1) % GM_NS, kd = kb + min(ks + GM_NS - 1, nk - 1) * BK;
+            // past the last step the reads fetch a stage no step uses
+            if constexpr (decltype(cur_c)::value == 0) {
+                rd(ra1, rb1, (ks + 1) % GM_NS, std::true_type{}, sd, kd);
+                mf(ra0, rb0);
+            } else {
+                rd(ra0, rb0, (ks + 1) % GM_NS, std::true_type{}, sd, kd);
+                mf(ra1, rb1);
+            }
+            // one LDS read (and its DMA) between consecutive MFMA pairs
+#pragma unroll
+            for (int g = 0; g < KK * (MB + NB); g++) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        int ks = 0;
+        for (; ks + 1 < nk; ks += 2) {
+            step(std::integral_constant<int, 0>{}, ks);
+            step(std::integral_constant<int, 1>{}, ks + 1);
+        }
+        if (ks < nk) {
+            step(std::integral_constant<int, 0>{}, ks);
+        }
+        } else {
 #pragma unroll
         for (int st = 0; st < GM_NS - 1; st++) {
             if (st < nk) {
@@ -483,6 +584,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             }
             __syncthreads();
+        }
         }
     } else {
     dma(0, kb);
@@ -514,41 +616,53 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
     const int64_t mw     = m0 + wm * (BM / WM) + 4 * hh;  // token of register 0 in block i = 0
     const bool    full_m = m0 + BM <= M;
     if constexpr (GLU) {
-        const int64_t j = n0 / 2 + wn * 32 + lq;
-        if (j >= glu.F) {
-            return;
+        // pair p of this wave: value block 2p, gate block 2p + 1, SwiGLU column j
+        constexpr int NP = NB / 2;
+        int64_t       jp[NP];
+        float         bv[NP], bg[NP];
+#pragma unroll
+        for (int q = 0; q < NP; q++) {
+            jp[q]            = n0 / 2 + wn * (BT / WN / 2) + q * 32 + lq;
+            const bool    ok = jp[q] < glu.F;
+            const int64_t rv = glu.swapped ? glu.F + jp[q] : jp[q];  // value row
+            const int64_t rg = glu.swapped ? jp[q] : glu.F + jp[q];  // gate row
+            bv[q]            = bias && ok ? bias[rv] : 0.0f;
+            bg[q]            = bias && ok ? bias[rg] : 0.0f;
         }
-        const int64_t rv = glu.swapped ? glu.F + j : j;  // value row
-        const int64_t rg = glu.swapped ? j : glu.F + j;  // gate row
-        const float   bv = bias ? bias[rv] : 0.0f;
-        const float   bg = bias ? bias[rg] : 0.0f;
         // the bias in registers before any store: a use behind a store's
         // bounds branch would otherwise wait for all stores in flight
         __builtin_amdgcn_s_waitcnt(0);
         auto go = [&](auto full_c) {
             constexpr bool FULL = decltype(full_c)::value;
 #pragma unroll
-            for (int i = 0; i < MB; i++) {
-                float o[16];
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    float v = acc[i][0][r], g = acc[i][1][r];
-                    if (bias) {
-                        v = v + bv;
-                        g = g + bg;
-                    }
-                    const float silu = g / (1.0f + expf(-g));
-                    o[r]             = silu * v;
+            for (int q = 0; q < NP; q++) {
+                const int64_t j = jp[q];
+                if (j >= glu.F) {
+                    continue;
                 }
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int64_t m = mw + i * 32 + 8 * (r / 4) + (r % 4);
-                    if (FULL || m < M) {
-                        if (glu.h) {
-                            glu.h[m * glu.F + j] = o[r];
+                for (int i = 0; i < MB; i++) {
+                    float o[16];
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        float v = acc[i][2 * q][r], g = acc[i][2 * q + 1][r];
+                        if (bias) {
+                            v = v + bv[q];
+                            g = g + bg[q];
                         }
-                        if (glu.hh) {
-                            glu.hh[m * glu.F + j] = (_Float16) o[r];
+                        const float silu = g / (1.0f + expf(-g));
+                        o[r]             = silu * v;
+                    }
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int64_t m = mw + i * 32 + 8 * (r / 4) + (r % 4);
+                        if (FULL || m < M) {
+                            if (glu.h) {
+                                glu.h[m * glu.F + j] = o[r];
+                            }
+                            if (glu.hh) {
+                                glu.hh[m * glu.F + j] = (_Float16) o[r];
+                            }
                         }
                     }
                 }
@@ -780,11 +894,11 @@ size_t gemm_workspace(int64_t K, int64_t M) {
     return (size_t) M * (size_t) K * sizeof(_Float16);
 }
 
-template <int NW, int WM, int BK, int BM = 32 * NW, bool WH = false>
+template <int NW, int WM, int BK, int BM = 32 * NW, bool WH = false, bool WIDE = false>
 static int launch_gemm(int wtype, const uint8_t * W, int64_t N, int64_t K, int64_t rs, const _Float16 * xh, int64_t M,
                        const float * bias, const float * res, int64_t ldr, float * y, int64_t ldy, const GemmGlu & glu,
                        const GemmMulti & mul, const GemmSplit & spl, hipStream_t stream) {
-    constexpr int BT   = 32 * NW;
+    constexpr int BT   = WIDE ? 256 : 32 * NW;
     const int64_t n_nt = (N + BT - 1) / BT;
     const int64_t n_mt = (M + BM - 1) / BM;
     const int64_t n    = n_nt * n_mt * spl.n;
@@ -803,10 +917,10 @@ static int launch_gemm(int wtype, const uint8_t * W, int64_t N, int64_t K, int64
     if constexpr (WH) {
         // 16-bit weight rows: f16 copies of any block type, or BF16 as stored
         if (wtype == TYPE_BF16) {
-            return go(k_gemm_q<TYPE_BF16, NW, WM, BK, BM, false, true>);
+            return go(k_gemm_q<TYPE_BF16, NW, WM, BK, BM, false, true, WIDE>);
         }
-        return glu.F > 0 ? go(k_gemm_q<TYPE_F16, NW, WM, BK, BM, true, true>)
-                         : go(k_gemm_q<TYPE_F16, NW, WM, BK, BM, false, true>);
+        return glu.F > 0 ? go(k_gemm_q<TYPE_F16, NW, WM, BK, BM, true, true, WIDE>)
+                         : go(k_gemm_q<TYPE_F16, NW, WM, BK, BM, false, true, WIDE>);
     } else {
         if (glu.F > 0) {
             switch (wtype) {
@@ -833,8 +947,8 @@ static int gemm_launch(int wtype, const uint8_t * wb, int64_t N, int64_t K, int6
     if (wh) {
         // f16 weight rows (row stride K): the DMA ring on the same tile choice
         if (spl.n > 1) {
-            int rc = launch_gemm<8, 2, 32, 256, true>(wtype, wb, N, K, K * 2, xh, M, nullptr, nullptr, 0, nullptr, N,
-                                                      glu, mul, spl, stream);
+            int rc = launch_gemm<4, 2, 32, 256, true, true>(wtype, wb, N, K, K * 2, xh, M, nullptr, nullptr, 0, nullptr,
+                                                            N, glu, mul, spl, stream);
             if (rc != MMHIP_OK) {
                 return rc;
             }
@@ -845,8 +959,8 @@ static int gemm_launch(int wtype, const uint8_t * wb, int64_t N, int64_t K, int6
             return check_launch("mul_mat gemm: split-K reduce");
         }
         if (tiles256 >= 256 || (mul.n > 0 && tiles256 >= 128)) {
-            return launch_gemm<8, 2, 32, 256, true>(wtype, wb, N, K, K * 2, xh, M, bias, res, ldr, y, ldy, glu, mul,
-                                                    spl, stream);
+            return launch_gemm<4, 2, 32, 256, true, true>(wtype, wb, N, K, K * 2, xh, M, bias, res, ldr, y, ldy, glu,
+                                                          mul, spl, stream);
         }
         return launch_gemm<4, 2, 32, 64, true>(wtype, wb, N, K, K * 2, xh, M, bias, res, ldr, y, ldy, glu, mul, spl,
                                                stream);
@@ -1086,8 +1200,8 @@ int gemm_bf16(const void * W, int64_t N, int64_t K, int64_t rs, const float * x,
     const auto *    xb       = (const _Float16 *) ws;  // 16-bit patterns
     const int64_t   tiles256 = ((N + 255) / 256) * ((M + 255) / 256);
     if (tiles256 >= 256) {
-        return launch_gemm<8, 2, 32, 256, true>(TYPE_BF16, wb, N, K, rs, xb, M, nullptr, nullptr, 0, y, ldy, none,
-                                                single, one, stream);
+        return launch_gemm<4, 2, 32, 256, true, true>(TYPE_BF16, wb, N, K, rs, xb, M, nullptr, nullptr, 0, y, ldy, none,
+                                                      single, one, stream);
     }
     return launch_gemm<4, 2, 32, 64, true>(TYPE_BF16, wb, N, K, rs, xb, M, nullptr, nullptr, 0, y, ldy, none, single,
                                            one, stream);
