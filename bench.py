@@ -589,7 +589,7 @@ def bench_gemm(args, torch, pkg):
         "dtype": "f16 MFMA (Q4_K dequantised to f16 rows once per call), f32 accumulate",
         "config": {"workload": "Q4_K GEMM W[6144x2048] x[8192x2048] f32 -> f32"},
         "via_backend": backend,
-        "roofline": {"bound": "mfma", "kernel": "k_x_to_f16 + k_w_to_f16<Q4_K> + k_gemm_q<f16 weights, 4-stage DMA ring> "
+        "roofline": {"bound": "mfma", "kernel": "k_xw_to_f16<Q4_K> (activations and weights to f16, one launch) + k_gemm_q<f16 weights, 4-stage DMA ring, four waves> "
                                                "(one mul_mat call)", "achieved": round(tf, 2),
                      "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
                      "avg_launch_us": round(avg_s * 1e6, 2), "min_launch_us": round(med_s * 1e6, 2),

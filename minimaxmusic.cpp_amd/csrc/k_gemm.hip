@@ -802,9 +802,9 @@ __global__ void k_splitk_reduce(const float * __restrict__ part, int nparts, int
 
 // Activations f32 -> f16 (round to nearest even), rows of K into a packed
 // [M, K] copy: 8 elements per thread per pass.
-__global__ void k_x_to_f16(const float * __restrict__ x, int64_t ldx, int64_t K, int64_t n8,
-                           _Float16 * __restrict__ xh) {
-    for (int64_t t = blockIdx.x * (int64_t) blockDim.x + threadIdx.x; t < n8; t += (int64_t) gridDim.x * blockDim.x) {
+__device__ __forceinline__ void x_to_f16_part(const float * __restrict__ x, int64_t ldx, int64_t K, int64_t n8,
+                                              _Float16 * __restrict__ xh, int64_t t0, int64_t stride) {
+    for (int64_t t = t0; t < n8; t += stride) {
         const int64_t  e = t * 8, m = e / K, k = e % K;
         const float4_t a = *(const float4_t *) (x + m * ldx + k);
         const float4_t b = *(const float4_t *) (x + m * ldx + k + 4);
@@ -816,6 +816,11 @@ __global__ void k_x_to_f16(const float * __restrict__ x, int64_t ldx, int64_t K,
         }
         *(half8_t *) (xh + e) = o;
     }
+}
+
+__global__ void k_x_to_f16(const float * __restrict__ x, int64_t ldx, int64_t K, int64_t n8,
+                           _Float16 * __restrict__ xh) {
+    x_to_f16_part(x, ldx, K, n8, xh, blockIdx.x * (int64_t) blockDim.x + threadIdx.x, (int64_t) gridDim.x * blockDim.x);
 }
 
 // Activations f32 -> bf16 (ggml's rounding: nearest-even, NaN quiet) into a
@@ -840,10 +845,9 @@ __global__ void k_x_to_bf16(const float * __restrict__ x, int64_t ldx, int64_t K
 // dequantisation: thread (row, 64-wide K step, half) dequantises its 32
 // values exactly (f32, then f16) and writes them as four 16-byte chunks.
 template <int WT>
-__global__ __launch_bounds__(256) void k_w_to_f16(const uint8_t * __restrict__ W, int64_t N, int64_t K, int64_t rs,
-                                                   _Float16 * __restrict__ wh) {
+__device__ __forceinline__ void w_to_f16_part(const uint8_t * __restrict__ W, int64_t N, int64_t K, int64_t rs,
+                                              _Float16 * __restrict__ wh, int64_t t) {
     const int64_t nsteps = K / GM_BK;
-    const int64_t t      = (int64_t) blockIdx.x * 256 + threadIdx.x;
     if (t >= N * nsteps * 2) {
         return;
     }
@@ -860,6 +864,27 @@ __global__ __launch_bounds__(256) void k_w_to_f16(const uint8_t * __restrict__ W
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         *(half8_t *) (wh + row * K + k0 + 8 * ch[j]) = o[j];
+    }
+}
+
+template <int WT>
+__global__ __launch_bounds__(256) void k_w_to_f16(const uint8_t * __restrict__ W, int64_t N, int64_t K, int64_t rs,
+                                                   _Float16 * __restrict__ wh) {
+    w_to_f16_part<WT>(W, N, K, rs, wh, (int64_t) blockIdx.x * 256 + threadIdx.x);
+}
+
+// Both conversions of a GEMM call in one launch: workgroups [0, nbx) convert
+// the activations (grid-stride over them), the rest the weight rows, so the
+// two streams share one launch and overlap their tails.
+template <int WT>
+__global__ __launch_bounds__(256) void k_xw_to_f16(const float * __restrict__ x, int64_t ldx, int64_t K, int64_t n8,
+                                                    _Float16 * __restrict__ xh, int nbx,
+                                                    const uint8_t * __restrict__ W, int64_t N, int64_t rs,
+                                                    _Float16 * __restrict__ wh) {
+    if ((int) blockIdx.x < nbx) {
+        x_to_f16_part(x, ldx, K, n8, xh, blockIdx.x * (int64_t) 256 + threadIdx.x, (int64_t) nbx * 256);
+    } else {
+        w_to_f16_part<WT>(W, N, K, rs, wh, (int64_t) (blockIdx.x - nbx) * 256 + threadIdx.x);
     }
 }
 
@@ -1124,14 +1149,11 @@ int gemm_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const fl
     if (!ws || ws_bytes < need || ((uintptr_t) ws) % 16 != 0) {
         return set_error(MMHIP_ERR_WORKSPACE, "mul_mat gemm: workspace %zu < %zu (16-byte aligned)", ws_bytes, need);
     }
-    _Float16 *    xh = (_Float16 *) ws;
-    const int64_t n8 = M * K / 8;
-    const int64_t nb = (n8 + 255) / 256;
-    hipLaunchKernelGGL(k_x_to_f16, dim3((unsigned) (nb < 8192 ? nb : 8192)), dim3(256), 0, stream, x, ldx, K, n8, xh);
-    int rc = check_launch("mul_mat gemm: convert");
-    if (rc != MMHIP_OK) {
-        return rc;
-    }
+    _Float16 *    xh  = (_Float16 *) ws;
+    const int64_t n8  = M * K / 8;
+    const int64_t nb  = (n8 + 255) / 256;
+    const int     nbx = (int) (nb < 8192 ? nb : 8192);
+    int           rc  = MMHIP_OK;
     const GemmGlu   none{};
     const GemmMulti single{};
     GemmSplit       spl;
@@ -1147,15 +1169,38 @@ int gemm_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const fl
     }
     const uint8_t * wb  = (const uint8_t *) W;
     const void *    reg = f16_weights(W, N, K);  // a registered f16 copy: no conversion
-    if (reg) {
-        wb = (const uint8_t *) reg;
-    } else if (wh) {
+    const int64_t   nw  = (N * (K / GM_BK) * 2 + 255) / 256;  // weight-conversion workgroups
+    if (!reg && wh && nbx + nw <= 0x7fffffff) {
+        // the activations and the weights to f16 in one launch
         _Float16 * whp = (_Float16 *) ((char *) ws + xo);
-        rc             = weights_to_f16(wtype, wb, N, K, rs, whp, stream);
+        const dim3 g((unsigned) (nbx + nw));
+        switch (wtype) {
+            case TYPE_Q8_0: hipLaunchKernelGGL(k_xw_to_f16<TYPE_Q8_0>, g, dim3(256), 0, stream, x, ldx, K, n8, xh, nbx, wb, N, rs, whp); break;
+            case TYPE_Q4_K: hipLaunchKernelGGL(k_xw_to_f16<TYPE_Q4_K>, g, dim3(256), 0, stream, x, ldx, K, n8, xh, nbx, wb, N, rs, whp); break;
+            case TYPE_Q5_K: hipLaunchKernelGGL(k_xw_to_f16<TYPE_Q5_K>, g, dim3(256), 0, stream, x, ldx, K, n8, xh, nbx, wb, N, rs, whp); break;
+            default: hipLaunchKernelGGL(k_xw_to_f16<TYPE_Q6_K>, g, dim3(256), 0, stream, x, ldx, K, n8, xh, nbx, wb, N, rs, whp); break;
+        }
+        rc = check_launch("mul_mat gemm: convert");
         if (rc != MMHIP_OK) {
             return rc;
         }
         wb = (const uint8_t *) whp;
+    } else {
+        hipLaunchKernelGGL(k_x_to_f16, dim3((unsigned) nbx), dim3(256), 0, stream, x, ldx, K, n8, xh);
+        rc = check_launch("mul_mat gemm: convert");
+        if (rc != MMHIP_OK) {
+            return rc;
+        }
+        if (reg) {
+            wb = (const uint8_t *) reg;
+        } else if (wh) {
+            _Float16 * whp = (_Float16 *) ((char *) ws + xo);
+            rc             = weights_to_f16(wtype, wb, N, K, rs, whp, stream);
+            if (rc != MMHIP_OK) {
+                return rc;
+            }
+            wb = (const uint8_t *) whp;
+        }
     }
     return gemm_launch(wtype, wb, N, K, rs, xh, M, bias, res, ldr, y, ldy, glu ? *glu : none, single, spl, stream,
                        wh || reg);
