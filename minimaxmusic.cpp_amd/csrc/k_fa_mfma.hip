@@ -389,18 +389,24 @@ typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 // loads of the two younger steps stay in flight across a barrier: once the
 // short rows of a masked workgroup are done, one wave per SIMD is left to
 // cover the load latency of each step.
-template <bool MASK>
-__global__ __launch_bounds__(512, 2) void k_fa_dma(FaArgs a, const int * __restrict__ row_end,
-                                                   const int * __restrict__ zero_end, int n_qtiles,
-                                                   float * __restrict__ out) {
-    constexpr int D = 128, NQK = 8, NDB = 4, TILE = FA_BK * 256, NW = 8;
-    constexpr int KR = 4, US = 1;  // ring tiles (K and V each); unit stride of a wave
+template <bool MASK, int NW = 8, int KR = 4>
+__global__ __launch_bounds__(NW * 64, 2) void k_fa_dma(FaArgs a, const int * __restrict__ row_end,
+                                                       const int * __restrict__ zero_end, int n_qtiles,
+                                                       float * __restrict__ out) {
+    constexpr int D = 128, NQK = 8, NDB = 4, TILE = FA_BK * 256;
+    constexpr int US  = 1;         // unit stride of a wave
+    constexpr int PPW = 16 / NW;   // 1 KB pieces of a 16 KB tile each wave DMAs
+    static_assert(MASK ? (NW == 4 && KR == 2) : (NW == 8 && KR == 4), "configurations");
     extern __shared__ __attribute__((aligned(1024))) char smem[];  // K ring, then V ring
     const int  total = n_qtiles * a.Hq * a.B;
-    const int  lin   = xcd_remap((int) blockIdx.x, total);
-    const int  qt    = lin % n_qtiles;
-    const int  h     = (lin / n_qtiles) % a.Hq;
-    const int  b     = lin / (n_qtiles * a.Hq);
+    // one 128-row tile per workgroup (masked, four waves): workgroups in
+    // order of falling row ends (the longest tiles first, every XCD a share
+    // of each length), two per CU, so that a CU takes the next tile as soon
+    // as one of its two finishes
+    const int  lin   = MASK ? (int) blockIdx.x : xcd_remap((int) blockIdx.x, total);
+    const int  qt    = MASK ? n_qtiles - 1 - lin / (a.Hq * a.B) : lin % n_qtiles;
+    const int  h     = MASK ? lin % a.Hq : (lin / n_qtiles) % a.Hq;
+    const int  b     = MASK ? (lin / a.Hq) % a.B : lin / (n_qtiles * a.Hq);
     const int  hk    = h / (a.Hq / a.Hkv);
     const int  bk    = b / (a.B / a.Bk);
     const int  tid   = threadIdx.x;
@@ -411,10 +417,7 @@ __global__ __launch_bounds__(512, 2) void k_fa_dma(FaArgs a, const int * __restr
     const int   par  = 0;  // the wave's first unit
     int         my_q;
     if constexpr (MASK) {
-        const int n128 = (a.nq + 127) / 128;
-        const int half = wave >> 2;
-        const int t128 = half ? n128 - 1 - qt : qt;
-        my_q           = half && t128 <= qt ? a.nq : t128 * 128 + (wave & 3) * 32 + lq;
+        my_q = qt * 128 + wave * 32 + lq;
     } else {
         my_q = qt * 256 + wave * 32 + lq;
     }
@@ -510,27 +513,29 @@ __global__ __launch_bounds__(512, 2) void k_fa_dma(FaArgs a, const int * __restr
         }
     };
 
-    // DMA: this wave fills 1 KB pieces 2 wave and 2 wave + 1 (4 rows each) of
-    // a K and a V tile; lane -> row 4 piece + lane / 16, stored chunk lane % 16
+    // DMA: this wave fills 1 KB pieces PPW wave .. PPW wave + PPW - 1 (4 rows
+    // each) of a K and a V tile; lane -> row 4 piece + lane / 16, stored chunk
+    // lane % 16
     const char *   kbase = a.k + hk * a.knb2 + bk * a.knb3;
     const char *   vbase = a.v + hk * a.vnb2 + bk * a.vnb3;
     const uint32_t sbase = (uint32_t) (uintptr_t) (__attribute__((address_space(3))) char *) smem;
     const int      drow = lane >> 4, dpc = lane & 15;
     auto dma_k = [&](int j) {
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int piece = 2 * wave + i, r = 4 * piece + drow;
+        for (int i = 0; i < PPW; i++) {
+            const int piece = PPW * wave + i, r = 4 * piece + drow;
             const int key   = min(j * FA_BK + r, a.nkv - 1);  // rows past the end repeat the last key (masked below)
-            fa_dma16(kbase + (int64_t) key * a.knb1 + ((dpc ^ (r & 15)) << 4), sbase + (j & 3) * TILE + piece * 1024);
+            fa_dma16(kbase + (int64_t) key * a.knb1 + ((dpc ^ (r & 15)) << 4),
+                     sbase + (j & (KR - 1)) * TILE + piece * 1024);
         }
     };
     auto dma_v = [&](int j) {
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int piece = 2 * wave + i, r = 4 * piece + drow;
+        for (int i = 0; i < PPW; i++) {
+            const int piece = PPW * wave + i, r = 4 * piece + drow;
             const int key   = min(j * FA_BK + r, a.nkv - 1);
             fa_dma16(vbase + (int64_t) key * a.vnb1 + ((dpc ^ (2 * (r & 3))) << 4),
-                     sbase + (KR + (j & 3)) * TILE + piece * 1024);
+                     sbase + (KR + (j & (KR - 1))) * TILE + piece * 1024);
         }
     };
     // K operand of k-step kk: row lq of the 32-key unit, logical chunk 2 kk + hh
@@ -548,12 +553,12 @@ __global__ __launch_bounds__(512, 2) void k_fa_dma(FaArgs a, const int * __restr
         (4 * (tg >> 1) + tj) * 256 + 16 * ((2 * (tg & 1) + (tq >> 1)) ^ (2 * (tj & 1))) + 8 * (tq & 1);
     const uint32_t vb[2] = { vlane + vx, vlane - vx };
     auto qk_op = [&](int u, int kk) -> half8_t {
-        const char * kt = smem + ((u >> 1) & 3) * TILE;
+        const char * kt = smem + ((u >> 1) & (KR - 1)) * TILE;
         return *(const half8_t *) (kt + ka[kk] + (u & 1) * 8192);
     };
     // PV step i of a unit: key half t = i / 4 (16 keys), output block db = i % 4
     auto pv_op = [&](int u, int i) -> half8_t {
-        const uint32_t vt = sbase + (KR + ((u >> 1) & 3)) * TILE;
+        const uint32_t vt = sbase + (KR + ((u >> 1) & (KR - 1))) * TILE;
         const int      t = i >> 2, db = i & 3;
         half8_t        av;
 #pragma unroll
@@ -701,16 +706,16 @@ __global__ __launch_bounds__(512, 2) void k_fa_dma(FaArgs a, const int * __restr
             m_sn = m_used;
         }
     };
-    // DMA group g (g >= -2): K tile g + 4 and V tile g + 3, each 2 loads per
-    // wave when the tile exists; group -2 and -1 go out after the prologue,
-    // group j after the barrier that follows unit 2 j
-    auto group_loads = [&](int g) { return 2 * (g + 4 < n) + 2 * (g + 3 < n); };
+    // DMA group g (g >= -KR / 2): K tile g + KR and V tile g + KR - 1, each
+    // PPW loads per wave when the tile exists; the groups before 0 go out
+    // after the prologue, group j after the barrier that follows unit 2 j
+    auto group_loads = [&](int g) { return PPW * (g + KR < n) + PPW * (g + KR - 1 < n); };
     auto issue_group = [&](int g) {
-        if (g + 4 < n) {
-            dma_k(g + 4);
+        if (g + KR < n) {
+            dma_k(g + KR);
         }
-        if (g + 3 < n) {
-            dma_v(g + 3);
+        if (g + KR - 1 < n) {
+            dma_v(g + KR - 1);
         }
     };
     // after unit u: sn becomes the next softmax input (shifted if m moved
@@ -734,12 +739,17 @@ __global__ __launch_bounds__(512, 2) void k_fa_dma(FaArgs a, const int * __restr
         pp[1] = pn[1];
         if ((u & 1) == 0) {
             const int j = u >> 1;
-            switch (group_loads(j - 2) + group_loads(j - 1)) {
-                case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-                case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
-                case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
-                case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
-                default: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+            if constexpr (KR == 2) {
+                // K tile j + 1 and V tile j: group j - 1, the last one issued
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            } else {
+                switch (group_loads(j - 2) + group_loads(j - 1)) {
+                    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+                    case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
+                    case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+                    case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
+                    default: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+                }
             }
             asm volatile("s_barrier" ::: "memory");
             issue_group(j);
@@ -750,18 +760,22 @@ __global__ __launch_bounds__(512, 2) void k_fa_dma(FaArgs a, const int * __restr
     // behind the barrier; the scores of the wave's first unit (m = 0)
     const int u0 = par;
     dma_k(0);
-    if (n > 1) {
-        dma_k(1);
-    }
-    if (n > 0) {
-        dma_v(0);
+    if constexpr (KR == 4) {
+        if (n > 1) {
+            dma_k(1);
+        }
+        if (n > 0) {
+            dma_v(0);
+        }
     }
     if (mask_need(u0) && nk > 0) {
         mask_load(u0);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     asm volatile("s_barrier" ::: "memory");
-    issue_group(-2);
+    if constexpr (KR == 4) {
+        issue_group(-2);
+    }
     issue_group(-1);
     sc = zero16;
     if (nk > 0) {
@@ -832,10 +846,11 @@ __global__ __launch_bounds__(512, 2) void k_fa_dma(FaArgs a, const int * __restr
 // k_fa_dma's preconditions: 16-byte aligned Q rows (float4 loads) and K / V
 // rows (16-byte DMA), D = 128, and at least one workgroup of 256 rows per CU
 // (MMHIP_DISABLE_FA_DMA=1 takes the register-staged kernel instead)
-constexpr size_t FA_DMA_LDS = 8 * FA_BK * 256;  // K and V rings of 4 tiles
+constexpr size_t FA_DMA_LDS  = 8 * FA_BK * 256;  // K and V rings of 4 tiles
+constexpr size_t FA_DMA_LDS2 = 4 * FA_BK * 256;  // K and V rings of 2 tiles (two workgroups per CU)
 
 static int fa_dma_qtiles(const FaArgs & a) {
-    return a.mask ? ((a.nq + 127) / 128 + 1) / 2 : (a.nq + 255) / 256;
+    return a.mask ? (a.nq + 127) / 128 : (a.nq + 255) / 256;
 }
 
 static bool fa_dma_ok(const FaArgs & a, int D) {
@@ -949,11 +964,11 @@ int fa_mfma(const FaArgs & a, int D, float * out, void * ws, size_t ws_bytes, hi
         const int    nqt = fa_dma_qtiles(a);
         const size_t lds = FA_DMA_LDS;
         if (a.mask) {
-            if (!ensure_lds_limit((const void *) k_fa_dma<true>, lds)) {
+            if (!ensure_lds_limit((const void *) k_fa_dma<true, 4, 2>, FA_DMA_LDS2)) {
                 return set_error(MMHIP_ERR_HIP, "flash_attn dma: cannot raise the LDS limit");
             }
-            hipLaunchKernelGGL(k_fa_dma<true>, dim3((unsigned) (nqt * a.Hq * a.B)), dim3(512), lds, stream, a,
-                               row_end, zero_end, nqt, out);
+            hipLaunchKernelGGL((k_fa_dma<true, 4, 2>), dim3((unsigned) (nqt * a.Hq * a.B)), dim3(256), FA_DMA_LDS2,
+                               stream, a, row_end, zero_end, nqt, out);
         } else {
             if (!ensure_lds_limit((const void *) k_fa_dma<false>, lds)) {
                 return set_error(MMHIP_ERR_HIP, "flash_attn dma: cannot raise the LDS limit");
