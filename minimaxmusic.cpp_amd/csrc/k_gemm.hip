@@ -263,7 +263,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_q(const uint8_t * __restrict__
     static_assert(MB >= 1 && XI >= 1, "tile shape");
     static_assert(!WH || BK == 32, "the f16-weight ring steps 32 columns");
     static_assert(!GLU || NB % 2 == 0, "GLU tiles pair value and gate blocks in each wave");
-    static_assert(!WIDE || (WH && NW == 4 && BM == 256), "the wide tiles run on the DMA ring, four waves");
+    static_assert(!WIDE || (WH && NW == 4 && (BM == 256 || BM == 192)), "the wide tiles run on the DMA ring, four waves");
     extern __shared__ __attribute__((aligned(16))) _Float16 g_lds[];
     _Float16 * sX = g_lds;            // 2 stages
     _Float16 * sW = g_lds + 2 * TIX;  // 2 buffers
@@ -970,10 +970,23 @@ static int gemm_launch(int wtype, const uint8_t * wb, int64_t N, int64_t K, int6
                        const GemmMulti & mul, const GemmSplit & spl, hipStream_t stream, bool wh = false) {
     const int64_t tiles256 = ((N + 255) / 256) * ((M + 255) / 256);
     if (wh) {
-        // f16 weight rows (row stride K): the DMA ring on the same tile choice
+        // f16 weight rows (row stride K): the DMA ring on the same tile choice.
+        // 192-token tiles (3/4 of the work of a 256-token tile) where they
+        // take fewer rounds of the 256 CUs by that weight: the DiT's 1380
+        // tokens fill 8 of them (5.4 of 256) and its projections' grids of
+        // 144 to 384 tiles of 256 run a partly filled round
+        const int64_t nn     = (N + 255) / 256;
+        const int64_t r256   = (nn * ((M + 255) / 256) * spl.n + 255) / 256;
+        const int64_t r192   = (nn * ((M + 191) / 192) * spl.n + 255) / 256;
+        const bool    bm192  = 3 * r192 < 4 * r256;
+        auto          wide   = [&](const float * bi, const float * re, int64_t lr, float * yy, int64_t ly) {
+            return bm192 ? launch_gemm<4, 2, 32, 192, true, true>(wtype, wb, N, K, K * 2, xh, M, bi, re, lr, yy, ly, glu,
+                                                                   mul, spl, stream)
+                         : launch_gemm<4, 2, 32, 256, true, true>(wtype, wb, N, K, K * 2, xh, M, bi, re, lr, yy, ly, glu,
+                                                                   mul, spl, stream);
+        };
         if (spl.n > 1) {
-            int rc = launch_gemm<4, 2, 32, 256, true, true>(wtype, wb, N, K, K * 2, xh, M, nullptr, nullptr, 0, nullptr,
-                                                            N, glu, mul, spl, stream);
+            int rc = wide(nullptr, nullptr, 0, nullptr, N);
             if (rc != MMHIP_OK) {
                 return rc;
             }
@@ -984,8 +997,7 @@ static int gemm_launch(int wtype, const uint8_t * wb, int64_t N, int64_t K, int6
             return check_launch("mul_mat gemm: split-K reduce");
         }
         if (tiles256 >= 256 || (mul.n > 0 && tiles256 >= 128)) {
-            return launch_gemm<4, 2, 32, 256, true, true>(wtype, wb, N, K, K * 2, xh, M, bias, res, ldr, y, ldy, glu,
-                                                          mul, spl, stream);
+            return wide(bias, res, ldr, y, ldy);
         }
         return launch_gemm<4, 2, 32, 64, true>(wtype, wb, N, K, K * 2, xh, M, bias, res, ldr, y, ldy, glu, mul, spl,
                                                stream);
