@@ -1257,6 +1257,12 @@ int gemm_bf16(const void * W, int64_t N, int64_t K, int64_t rs, const float * x,
     const auto *    xb       = (const _Float16 *) ws;  // 16-bit patterns
     const int64_t   tiles256 = ((N + 255) / 256) * ((M + 255) / 256);
     if (tiles256 >= 256) {
+        // 192-token tiles where they take fewer rounds by work (gemm_launch's rule)
+        const int64_t nn = (N + 255) / 256;
+        if (3 * ((nn * ((M + 191) / 192) + 255) / 256) < 4 * ((tiles256 + 255) / 256)) {
+            return launch_gemm<4, 2, 32, 192, true, true>(TYPE_BF16, wb, N, K, rs, xb, M, nullptr, nullptr, 0, y, ldy,
+                                                          none, single, one, stream);
+        }
         return launch_gemm<4, 2, 32, 256, true, true>(TYPE_BF16, wb, N, K, rs, xb, M, nullptr, nullptr, 0, y, ldy, none,
                                                       single, one, stream);
     }

@@ -218,15 +218,17 @@ def test_mul_mat_bf16_rejects_and_backend(mm, pkg):
 
 
 @pytest.mark.parametrize("N,K,M,pad", [(2048, 2048, 1380, 0), (6144, 4096, 100, 0), (37, 544, 33, 32),
-                                       (4096, 2048, 8192, 0), (300, 1024, 17, 64), (1000, 8192, 257, 0)])
+                                       (4096, 2048, 8192, 0), (300, 1024, 17, 64), (1000, 8192, 257, 0),
+                                       (16384, 2048, 1380, 0)])
 def test_mul_mat_bf16_gemm(mm, N, K, M, pad):
     """MUL_MAT over BF16 weights above 16 tokens: the bf16 MFMA GEMM reading
     the weight rows in place (row stride K + pad elements) through the 16-bit
     DMA ring, on a bf16 copy of the activations.  ggml's BF16 arithmetic --
     activations rounded to bf16 (torch's rounding, nearest-even), exact
     products, f32 sums -- against float64 of the same bf16 operands, max-rel
-    2e-5 (f32 sums over K <= 8192).  Shapes cover both tile configurations
-    (8192 tokens: 256 x 256 tiles), ragged N and M, and padded rows; the
+    2e-5 (f32 sums over K <= 8192).  Shapes cover the three tile
+    configurations (64 x 128 tiles on small grids, 256 x 256 at 8192 tokens,
+    192 x 256 at 1380 tokens x 16384 rows), ragged N and M, and padded rows; the
     workspace is the bf16 copy and a smaller one is refused."""
     import ctypes
 
