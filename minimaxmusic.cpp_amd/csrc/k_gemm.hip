@@ -930,6 +930,10 @@ static int launch_gemm(int wtype, const uint8_t * W, int64_t N, int64_t K, int64
     if (n > 0x7fffffff) {
         return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat gemm: too many tiles");
     }
+    if (K / BK / spl.n < 1) {
+        // every K part holds at least one step (the ring's prologue loads step 0)
+        return set_error(MMHIP_ERR_UNSUPPORTED, "mul_mat gemm: K = %lld too short for %d parts", (long long) K, spl.n);
+    }
     const size_t lds = (size_t) (WH ? GM_NS : 2) * (BM + BT) * BK * sizeof(_Float16);
     auto         go  = [&](auto kern) -> int {
         if (lds > 64 * 1024 && !ensure_lds_limit((const void *) kern, lds)) {
