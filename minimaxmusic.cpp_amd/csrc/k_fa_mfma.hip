@@ -374,21 +374,21 @@ typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 
 // Masked form (MASK: the LM's causal prefill, src/qwen3-lm.h:432-436, or any
-// f16 mask), with the mask prepass's per-row ends: the workgroup pairs the
-// 128-row query tile t (waves 0-3) with tile n128 - 1 - t (waves 4-7), so that
-// under a causal mask every SIMD holds one short and one long row range; the
-// K / V tiles are staged up to the last key any row of the workgroup can
-// see, and a wave computes up to the last key its own rows can see, then only
-// takes part in the staging.  A unit past the wave's all-zero mask prefix
-// adds the mask (log2 units) to its scores, loaded while the unit before it
-// runs.  A row's running max is set on its first unit with a visible key.
+// f16 mask), with the mask prepass's per-row ends: one 128-row query tile per
+// workgroup of four waves, two workgroups per CU; the K / V tiles are staged
+// up to the last key any row of the workgroup can see, and a wave computes
+// up to the last key its own rows can see, then only takes part in the
+// staging.  A unit past the wave's all-zero mask prefix adds the mask (log2
+// units) to its scores, loaded while the unit before it runs.  A row's
+// running max is set on its first unit with a visible key.
 //
-// Both forms stage K and V through 4-tile rings (128 KB of LDS, one
+// The unmasked form stages K and V through 4-tile rings (128 KB of LDS, one
 // workgroup per CU as the registers allow anyway), each tile issued three
 // 64-key steps before its first reader and waited for by count, so the
-// loads of the two younger steps stay in flight across a barrier: once the
-// short rows of a masked workgroup are done, one wave per SIMD is left to
-// cover the load latency of each step.
+// loads of the two younger steps stay in flight across a barrier.  The
+// masked form's rings hold 2 tiles (64 KB, two workgroups per CU): the K
+// tile of the next step and the V tile of this one are waited for at each
+// step's barrier.
 template <bool MASK, int NW = 8, int KR = 4>
 __global__ __launch_bounds__(NW * 64, 2) void k_fa_dma(FaArgs a, const int * __restrict__ row_end,
                                                        const int * __restrict__ zero_end, int n_qtiles,

@@ -873,18 +873,21 @@ __global__ __launch_bounds__(256) void k_w_to_f16(const uint8_t * __restrict__ W
     w_to_f16_part<WT>(W, N, K, rs, wh, (int64_t) blockIdx.x * 256 + threadIdx.x);
 }
 
-// Both conversions of a GEMM call in one launch: workgroups [0, nbx) convert
-// the activations (grid-stride over them), the rest the weight rows, so the
-// two streams share one launch and overlap their tails.
+// Both conversions of a GEMM call in one launch: workgroups [0, nbw) convert
+// the weight rows, the rest the activations (grid-stride over them), so the
+// two streams share one launch; the dequantising weight workgroups, the
+// slower per byte, are dispatched first and run beside the activation stream
+// instead of after it.
 template <int WT>
 __global__ __launch_bounds__(256) void k_xw_to_f16(const float * __restrict__ x, int64_t ldx, int64_t K, int64_t n8,
-                                                    _Float16 * __restrict__ xh, int nbx,
+                                                    _Float16 * __restrict__ xh, int nbw,
                                                     const uint8_t * __restrict__ W, int64_t N, int64_t rs,
                                                     _Float16 * __restrict__ wh) {
-    if ((int) blockIdx.x < nbx) {
-        x_to_f16_part(x, ldx, K, n8, xh, blockIdx.x * (int64_t) 256 + threadIdx.x, (int64_t) nbx * 256);
+    if ((int) blockIdx.x < nbw) {
+        w_to_f16_part<WT>(W, N, K, rs, wh, (int64_t) blockIdx.x * 256 + threadIdx.x);
     } else {
-        w_to_f16_part<WT>(W, N, K, rs, wh, (int64_t) (blockIdx.x - nbx) * 256 + threadIdx.x);
+        const int64_t nbx = (int64_t) gridDim.x - nbw;
+        x_to_f16_part(x, ldx, K, n8, xh, (blockIdx.x - nbw) * (int64_t) 256 + threadIdx.x, nbx * 256);
     }
 }
 
@@ -1191,10 +1194,10 @@ int gemm_q(int wtype, const void * W, int64_t N, int64_t K, int64_t rs, const fl
         _Float16 * whp = (_Float16 *) ((char *) ws + xo);
         const dim3 g((unsigned) (nbx + nw));
         switch (wtype) {
-            case TYPE_Q8_0: hipLaunchKernelGGL(k_xw_to_f16<TYPE_Q8_0>, g, dim3(256), 0, stream, x, ldx, K, n8, xh, nbx, wb, N, rs, whp); break;
-            case TYPE_Q4_K: hipLaunchKernelGGL(k_xw_to_f16<TYPE_Q4_K>, g, dim3(256), 0, stream, x, ldx, K, n8, xh, nbx, wb, N, rs, whp); break;
-            case TYPE_Q5_K: hipLaunchKernelGGL(k_xw_to_f16<TYPE_Q5_K>, g, dim3(256), 0, stream, x, ldx, K, n8, xh, nbx, wb, N, rs, whp); break;
-            default: hipLaunchKernelGGL(k_xw_to_f16<TYPE_Q6_K>, g, dim3(256), 0, stream, x, ldx, K, n8, xh, nbx, wb, N, rs, whp); break;
+            case TYPE_Q8_0: hipLaunchKernelGGL(k_xw_to_f16<TYPE_Q8_0>, g, dim3(256), 0, stream, x, ldx, K, n8, xh, (int) nw, wb, N, rs, whp); break;
+            case TYPE_Q4_K: hipLaunchKernelGGL(k_xw_to_f16<TYPE_Q4_K>, g, dim3(256), 0, stream, x, ldx, K, n8, xh, (int) nw, wb, N, rs, whp); break;
+            case TYPE_Q5_K: hipLaunchKernelGGL(k_xw_to_f16<TYPE_Q5_K>, g, dim3(256), 0, stream, x, ldx, K, n8, xh, (int) nw, wb, N, rs, whp); break;
+            default: hipLaunchKernelGGL(k_xw_to_f16<TYPE_Q6_K>, g, dim3(256), 0, stream, x, ldx, K, n8, xh, (int) nw, wb, N, rs, whp); break;
         }
         rc = check_launch("mul_mat gemm: convert");
         if (rc != MMHIP_OK) {

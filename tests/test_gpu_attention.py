@@ -304,14 +304,16 @@ def test_decode_with_quantised_output(mm, orc, wt):
 @pytest.mark.parametrize("B,Bk,Hq,Hkv,nq,nkv,kind", [(1, 1, 64, 8, 1000, 1100, "random"),
                                                    (2, 2, 32, 8, 1100, 1300, "causal"),
                                                    (2, 1, 64, 64, 257, 333, "random"),
-                                                   (1, 1, 256, 32, 130, 130, "causal")])
+                                                   (1, 1, 256, 32, 130, 130, "causal"),
+                                                   (1, 1, 64, 8, 1000, 1000, "prefix")])
 def test_dma_kernel_masked(mm, orc, B, Bk, Hq, Hkv, nq, nkv, kind):
     """Masked D = 128 on >= 256 workgroups: the DMA-fed kernel with the mask
-    prepass's row ends, 128-row query tiles paired from opposite ends (an odd
-    count leaves the middle tile alone), waves that stop before the
-    workgroup's last staged key, the mask added past each wave's all-zero
-    prefix.  Random masks (-inf, biases, a fully masked row -> 0) and causal
-    masks behind a 170-key visible prefix; 48 sampled rows against fp64."""
+    prepass's row ends, one 128-row query tile per workgroup (the longest
+    first), waves that stop before the workgroup's last staged key, the mask
+    added past each wave's all-zero prefix.  Random masks (-inf, biases, a
+    fully masked row -> 0), causal masks behind a 170-key visible prefix, and
+    a 100-key prefix for every row (every workgroup stages two tiles); 48
+    sampled rows against fp64."""
     q = rnd((B, Hq, nq, 128), 111)
     k = rnd((Bk, Hkv, nkv, 128), 112, np.float16)
     v = rnd((Bk, Hkv, nkv, 128), 113, np.float16)
@@ -319,6 +321,9 @@ def test_dma_kernel_masked(mm, orc, B, Bk, Hq, Hkv, nq, nkv, kind):
     if kind == "random":
         mask = np.where(rng.random((B, 1, nq, nkv)) < 0.3, -np.inf, rng.normal(0, 1, (B, 1, nq, nkv)))
         mask[:, :, 5] = -np.inf
+    elif kind == "prefix":
+        mask = np.full((1, 1, nq, nkv), -np.inf)
+        mask[..., :100] = 0
     else:
         off = nkv - nq if nkv > nq else 0
         mask = np.full((1, 1, nq, nkv), -np.inf)
